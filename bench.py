@@ -1,0 +1,250 @@
+"""Benchmark: routed-MoE tokens/s and achieved HBM GB/s (q4, top-8, batch 1).
+
+Workload (BASELINE.json metric, first config shape, on the GPU): one decode
+token through one routed-expert layer of Qwen3.6-35B-A3B -- bf16 router
+[256][2048], softmax/top-8/renormalise, eight q4 group-64 experts
+(2048 -> 512 gate/up, SwiGLU, 512 -> 2048 down), weighted combine into the
+fp32 residual.  Steps rotate over 40 synthetic layers resident in HBM
+(40 x 453 MB = 18.1 GB, far above the 256 MB last-level cache) with a
+distinct router and input per layer, so weights stream from HBM.
+
+A step is one call of the per-layer MoE entry point (nmoe_moe_layer).
+Timed region: `--steps` back-to-back steps on the library's stream,
+bracketed by HIP events and stream synchronisation.  A second pass records
+an event pair around every launch of the dominant kernel to get its average
+duration for the roofline object.
+
+Algorithmic bytes per step (q4, K=8): 8 experts x 1,769,472 B + bf16 router
+1,048,576 B + activations 20,544 B (x bf16 4 KB, h_mid fp32 8 KB, out fp32
+8 KB, idx/w 64 B) = 15,224,896 B.
+
+cpu_baseline: the reference's CPU routines (src/math.m compiled from the
+reference sources into oracle/_ref, single-threaded, -O3) on a bounded
+sample of the same workload; the repository's C restatement ("port") when
+oracle/_ref was not built.
+
+    python bench.py [--gpus 1] [--steps 400] [--warmup 40]
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(ROOT, "nano-metal-moe-qwen36_amd")
+for _p in (ROOT, PKG):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+HBM_PEAK_GBS = 8000.0
+EXPERT_BYTES = {4: 1769472, 2: 983040}
+ROUTER_BYTES = 256 * 2048 * 2
+ACT_BYTES = 4096 + 8192 + 8192 + 64
+
+
+def step_bytes(bits: int, k: int) -> int:
+    return k * EXPERT_BYTES[bits] + ROUTER_BYTES + ACT_BYTES
+
+
+class HipEvents:
+    """hipEvent* through ctypes on the HIP runtime libnmoe_hip.so links."""
+
+    def __init__(self):
+        self.rt = C.CDLL("libamdhip64.so.7")
+        for n in ("hipEventCreate", "hipEventRecord", "hipEventSynchronize", "hipEventElapsedTime",
+                  "hipEventDestroy"):
+            getattr(self.rt, n).restype = C.c_int
+        self.rt.hipEventCreate.argtypes = [C.POINTER(C.c_void_p)]
+        self.rt.hipEventRecord.argtypes = [C.c_void_p, C.c_void_p]
+        self.rt.hipEventSynchronize.argtypes = [C.c_void_p]
+        self.rt.hipEventElapsedTime.argtypes = [C.POINTER(C.c_float), C.c_void_p, C.c_void_p]
+        self.rt.hipEventDestroy.argtypes = [C.c_void_p]
+
+    def create(self, n: int) -> list:
+        evs = []
+        for _ in range(n):
+            e = C.c_void_p()
+            assert self.rt.hipEventCreate(C.byref(e)) == 0
+            evs.append(e)
+        return evs
+
+    def record(self, ev, stream):
+        assert self.rt.hipEventRecord(ev, stream) == 0
+
+    def ms(self, a, b) -> float:
+        assert self.rt.hipEventSynchronize(b) == 0
+        out = C.c_float()
+        assert self.rt.hipEventElapsedTime(C.byref(out), a, b) == 0
+        return float(out.value)
+
+    def destroy(self, evs):
+        for e in evs:
+            self.rt.hipEventDestroy(e)
+
+
+def cpu_baseline(bits: int, k: int, seed: int, nsteps: int, nlayers: int = 4) -> dict:
+    """Times the reference's CPU decode step on `nsteps` steps over `nlayers`
+    synthetic layers (only the experts the steps route to are generated)."""
+    from oracle import binding as B
+
+    ref = B.ref_step()
+    kind = "reference" if ref is not None else "port"
+    fn = ref.orc_cpu_step_bench_ref if ref is not None else B.oracle().orc_cpu_step_bench_port
+    esz = EXPERT_BYTES[bits]
+    sigma = 0.02 if bits == 4 else 0.05
+    packs, routers, xs, hs = [], [], [], []
+    for layer in range(nlayers):
+        W = B.syn_bf16(256 * 2048, seed, layer, 16, 0.02)
+        x = B.bf16_to_f32(B.syn_bf16(2048, seed, layer, 17, 1.0))
+        h = B.bf16_to_f32(B.syn_bf16(2048, seed, layer, 18, 1.0))
+        idx, _, n = B.route(B.router_logits_bf16(W.reshape(256, 2048), x), k)
+        pack = np.zeros(256 * esz, np.uint8)
+        for e in idx[:n]:
+            pack[int(e) * esz:(int(e) + 1) * esz] = B.syn_expert(bits, seed, layer, int(e), sigma)
+        packs.append(pack), routers.append(W), xs.append(x), hs.append(h)
+    X = np.ascontiguousarray(np.stack(xs))
+    H = np.ascontiguousarray(np.stack(hs))
+    pp = (C.c_void_p * nlayers)(*[p.ctypes.data for p in packs])
+    rp = (C.c_void_p * nlayers)(*[r.ctypes.data for r in routers])
+    out = np.zeros(2048, np.float32)
+    repeats = 3
+    per_rep = max(nlayers, nsteps // repeats)
+    t0 = time.time()
+    sec = fn(pp, rp, nlayers, bits, X.ctypes.data, H.ctypes.data, nlayers, k, per_rep, repeats, out.ctypes.data)
+    wall = time.time() - t0
+    tps = 1.0 / sec
+    return {
+        "value": round(tps, 3),
+        "unit": "tokens/s",
+        "cores": 1,
+        "kind": kind,
+        "sample": (f"{repeats}x{per_rep} single-layer q{bits} top-{k} decode steps over {nlayers} synthetic layers "
+                   f"(median repeat), {wall:.1f} s of CPU work on 1 of {os.cpu_count()} host threads; "
+                   f"{sec * 1e3:.2f} ms/step, {step_bytes(bits, k) / sec / 1e9:.3f} GB/s algorithmic"),
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=400)
+    ap.add_argument("--warmup", type=int, default=40)
+    ap.add_argument("--layers", type=int, default=40)
+    ap.add_argument("--bits", type=int, default=4, choices=(4, 2))
+    ap.add_argument("--k", type=int, default=8)
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--cpu-steps", type=int, default=210)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(expert parallelism is design-only); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import nmoe_hip as nh
+
+    bits, k, NL = args.bits, args.k, args.layers
+    sigma = 0.02 if bits == 4 else 0.05
+    ctx = nh.Context(0, max_tokens=8)
+    stream = ctx.stream
+    print(f"[bench] device 0: {ctx.cus} CUs; building {NL} q{bits} layers", file=sys.stderr, flush=True)
+    for layer in range(NL):
+        ctx.synth_layer(layer, bits, args.seed, sigma)
+    routers = ctx.alloc(NL * ROUTER_BYTES, "bench.routers")
+    X = ctx.alloc(NL * 2048 * 2, "bench.x")
+    Hb = ctx.alloc(NL * 2048 * 2, "bench.hb")
+    for layer in range(NL):
+        ctx.synth_bf16(routers, 256 * 2048, args.seed, layer, 16, 0.02, offset=layer * ROUTER_BYTES)
+        ctx.synth_bf16(X, 2048, args.seed, layer, 17, 1.0, offset=layer * 4096)
+        ctx.synth_bf16(Hb, 2048, args.seed, layer, 18, 1.0, offset=layer * 4096)
+    hb = Hb.download(np.uint16, (NL, 2048))
+    H = ctx.to_device((hb.astype(np.uint32) << 16).view(np.float32), "bench.h")
+    OUT = ctx.alloc(NL * 2048 * 4, "bench.out")
+    IDX = ctx.alloc(NL * 32, "bench.idx")
+    WT = ctx.alloc(NL * 32, "bench.w")
+    rts = [ctx.router_bf16(routers.ptr + layer * ROUTER_BYTES) for layer in range(NL)]
+    ctx.sync()
+
+    def step(i):
+        layer = i % NL
+        return ctx.moe_layer(layer, rts[layer], X.ptr + layer * 4096, nh.BF16, 1, k, H.ptr + layer * 8192,
+                             OUT.ptr + layer * 8192, IDX.ptr + layer * 32, WT.ptr + layer * 32, stream=stream)
+
+    for i in range(args.warmup):
+        ctx._check(step(i))
+    ctx.sync()
+
+    ev = HipEvents()
+    e0, e1 = ev.create(2)
+    ctx.sync()
+    ev.record(e0, stream)
+    for i in range(args.steps):
+        step(i)
+    ev.record(e1, stream)
+    total_ms = ev.ms(e0, e1)
+    ctx.sync()
+    if ctx.device_status() != 0:
+        raise SystemExit(f"device status error: {ctx.last_error()}")
+    ms_per_step = total_ms / args.steps
+
+    # per-launch timing pass for the roofline object
+    n_k = min(args.steps, 200)
+    evs = ev.create(2 * n_k)
+    ctx.sync()
+    for i in range(n_k):
+        ev.record(evs[2 * i], stream)
+        step(i)
+        ev.record(evs[2 * i + 1], stream)
+    per = [ev.ms(evs[2 * i], evs[2 * i + 1]) for i in range(n_k)]
+    ev.destroy(evs + [e0, e1])
+    kern_ms = float(np.mean(per))
+
+    B = step_bytes(bits, k)
+    tps = 1e3 / ms_per_step
+    achieved = B / (kern_ms * 1e-3) / 1e9
+    result = {
+        "metric": "routed-MoE tokens/s + achieved HBM GB/s (q4, top-8, batch 1, 1 GPU)",
+        "value": round(tps, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "hbm_gbps": round(B / (ms_per_step * 1e-3) / 1e9, 1),
+        "config": {
+            "workload": f"single-layer q{bits} top-{k} batch-1 routed-MoE decode step (bf16 router, hidden 2048, "
+                        f"256 experts, FFN 512), rotating over {NL} HBM-resident layers",
+            "bits": bits, "k": k, "batch": 1, "layers_rotated": NL, "bytes_per_step": B,
+            "entry_point": "nmoe_moe_layer",
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "kernel": "whole nmoe_moe_layer step (event pair per step)",
+            "kernel_ms": round(kern_ms, 5),
+        },
+    }
+    if not args.no_cpu:
+        print("[bench] cpu baseline ...", file=sys.stderr, flush=True)
+        result["cpu_baseline"] = cpu_baseline(bits, k, args.seed, args.cpu_steps)
+    ctx.close()
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,176 @@
+/*
+ * nmoe_hip.h -- C ABI of libnmoe_hip.so: the routed-expert MoE step of
+ * Qwen3.6-35B-A3B on AMD Instinct MI355X (gfx950).
+ *
+ * Plain C, includable from C, C++ and Objective-C (the guard style of the
+ * reference's include/nmoe/backend.h:7-9,69-71).  No HIP or torch types
+ * appear in the signatures: device memory is passed as `void *` / typed
+ * pointers, streams as `void *` (a hipStream_t; NULL = the context's stream).
+ *
+ * Replaces, in the reference (file:line relative to the reference root):
+ *   - the Metal backend's device/queue/buffer registry for this path
+ *       include/nmoe/backend.h:55-67, src/backend/metal_backend.m:156-183
+ *   - the expert-pack residency (mmap + pread of packed_experts/layer_XX.bin)
+ *       src/runtime.m:2426-2465, 1588-1634; include/nmoe/expert_io.h:21-24
+ *   - the router + top-k:  metal/kernels.metal:472-513 (logits),
+ *       src/runtime.m:1498-1511 -> src/math.m:67-153 (softmax/top-k/renorm)
+ *   - the expert kernels: metal/kernels.metal:562-640 (gate/up + SwiGLU),
+ *       642-714 and 1456-1542 (down + weighted combine), 1394-1454 (combine)
+ *   - the per-layer MoE call NMOEPipelinedExpertTail, src/runtime.m:2908-2999
+ *
+ * Conventions (every entry point):
+ *   - returns 0 (NMOE_HIP_OK) or a negative NMOE_HIP_E* code; the message is
+ *     available from nmoe_hip_last_error();
+ *   - arguments are validated on the host before any launch;
+ *   - calls that launch work are asynchronous and stream-ordered and never
+ *     allocate (all scratch is sized at nmoe_hip_create);
+ *   - a context is not thread-safe and its launches must be ordered on one
+ *     stream (the persistent kernels share the context's barrier words).
+ */
+#ifndef NMOE_HIP_H
+#define NMOE_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Model constants (src/runtime.m:31-48, scripts/convert_qwen36.py:31-36). */
+#define NMOE_HIP_HIDDEN 2048
+#define NMOE_HIP_INTER 512
+#define NMOE_HIP_EXPERTS 256
+#define NMOE_HIP_GROUP 64
+#define NMOE_HIP_MAX_K 8 /* kNMOEMaxExperts, src/runtime.m:43 */
+#define NMOE_HIP_MAX_LAYERS 64
+
+/* Expert pack sizes, src/expert_io.m:90-99. */
+#define NMOE_HIP_EXPERT_SIZE_Q4 1769472u
+#define NMOE_HIP_EXPERT_SIZE_Q2 983040u
+
+/* Status codes. */
+#define NMOE_HIP_OK 0
+#define NMOE_HIP_EINVAL (-22)   /* bad argument: NULL, K outside 1..8, size, alignment */
+#define NMOE_HIP_ENOMEM (-12)   /* device allocation failed (create / upload only) */
+#define NMOE_HIP_ENODEV (-19)   /* no such device / HIP runtime error at create */
+#define NMOE_HIP_ENOENT (-2)    /* layer pack or buffer label not present */
+#define NMOE_HIP_EIO (-5)       /* file read failed / wrong file size */
+#define NMOE_HIP_EHIP (-71)     /* a HIP runtime call failed */
+#define NMOE_HIP_ETIMEDOUT (-110) /* a persistent kernel hit its bounded wait */
+
+/* Element types for activations passed in. */
+#define NMOE_HIP_F32 0
+#define NMOE_HIP_BF16 1
+
+/* Exported symbols (the library is built with -fvisibility=hidden). */
+#if defined(__GNUC__) || defined(__clang__)
+#define NMOE_HIP_API __attribute__((visibility("default")))
+#else
+#define NMOE_HIP_API
+#endif
+
+typedef struct nmoe_hip_ctx nmoe_hip_ctx;
+
+/* ---- context (replaces nmoe_backend_create/destroy, backend.h:55-56, and the
+ *      one-time buffer set-up NMOEInitExpertIOBuffers, runtime.m:1542-1584) */
+
+/* max_tokens bounds ntok for every later call; scratch for that many tokens
+ * is allocated here, once. */
+NMOE_HIP_API int nmoe_hip_create(int device, int max_tokens, nmoe_hip_ctx **out);
+NMOE_HIP_API void nmoe_hip_destroy(nmoe_hip_ctx *ctx);
+NMOE_HIP_API const char *nmoe_hip_last_error(const nmoe_hip_ctx *ctx);
+NMOE_HIP_API void *nmoe_hip_stream(nmoe_hip_ctx *ctx);
+NMOE_HIP_API int nmoe_hip_synchronize(nmoe_hip_ctx *ctx);
+/* Number of compute units of the context's device. */
+NMOE_HIP_API int nmoe_hip_device_cus(const nmoe_hip_ctx *ctx);
+/* Reads (and clears) the device-side status word that persistent kernels set
+ * when a bounded wait expires: returns 0 or NMOE_HIP_ETIMEDOUT.  Synchronous. */
+NMOE_HIP_API int nmoe_hip_check_device_status(nmoe_hip_ctx *ctx);
+
+/* ---- buffers (backend.h:64-66: register_shared_buffer / register_state_buffer
+ *      / lookup_shared_buffer).  The context owns them until destroy. */
+NMOE_HIP_API int nmoe_hip_register_state_buffer(nmoe_hip_ctx *ctx, const char *label, size_t size, void **dev_out);
+NMOE_HIP_API int nmoe_hip_register_shared_buffer(nmoe_hip_ctx *ctx, const char *label, const void *host, size_t size,
+                                    void **dev_out);
+NMOE_HIP_API void *nmoe_hip_lookup_buffer(const nmoe_hip_ctx *ctx, const char *label);
+NMOE_HIP_API int nmoe_hip_copy_to_device(nmoe_hip_ctx *ctx, void *dev, const void *host, size_t size);
+NMOE_HIP_API int nmoe_hip_copy_to_host(nmoe_hip_ctx *ctx, void *host, const void *dev, size_t size);
+
+/* ---- expert packs (expert_io.h:21-24; runtime.m:2426-2465 NMOELoadExpertLayer).
+ * A layer pack is the layer_XX.bin bytes unchanged: 256 experts of
+ * nmoe_hip_expert_size(bits) bytes each, component offsets as
+ * convert_qwen36.py:38-64.  Packs stay resident in HBM until destroy. */
+NMOE_HIP_API size_t nmoe_hip_expert_size(int bits);
+NMOE_HIP_API int nmoe_hip_upload_layer_pack(nmoe_hip_ctx *ctx, int layer, int bits, const void *host, size_t size);
+NMOE_HIP_API int nmoe_hip_load_layer_file(nmoe_hip_ctx *ctx, int layer, int bits, const char *path);
+/* Device address of a resident layer pack (NULL if absent). */
+NMOE_HIP_API const void *nmoe_hip_layer_pack(const nmoe_hip_ctx *ctx, int layer, int *bits_out);
+/* Allocates layer `layer` and fills it with the repository's synthetic
+ * generator (counter-based SplitMix64; codes uniform, scales bf16 of an
+ * Irwin-Hall(12) normal times sigma, bias = bf16(-8*scale) for q4 and
+ * bf16(-1.5*scale) for q2).  Bench/test data; no reference counterpart. */
+NMOE_HIP_API int nmoe_hip_synth_layer_pack(nmoe_hip_ctx *ctx, int layer, int bits, uint64_t seed, float sigma);
+/* Fills n bf16 values with the same generator (tag selects the stream). */
+NMOE_HIP_API int nmoe_hip_synth_bf16(nmoe_hip_ctx *ctx, uint16_t *dev, size_t n, uint64_t seed, uint32_t layer, uint32_t tag,
+                        float sigma, void *stream);
+
+/* ---- router.  Either a dense bf16 router [E][hidden] (the benchmark
+ * configs) or the reference model's q4 router (runtime.m:2357, evaluated by
+ * kernels.metal:472-513): u32 [E][hidden/8], bf16 scales/biases [E][hidden/64]. */
+#define NMOE_HIP_ROUTER_BF16 0
+#define NMOE_HIP_ROUTER_Q4 1
+typedef struct nmoe_hip_router {
+    int kind;
+    int num_experts; /* 256 */
+    const uint16_t *w_bf16;
+    const uint32_t *w_q4;
+    const uint16_t *scales;
+    const uint16_t *biases;
+} nmoe_hip_router;
+
+/* logits[ntok][E] = router . x (fp32 accumulate, fixed reduction order). */
+NMOE_HIP_API int nmoe_moe_router_logits(nmoe_hip_ctx *ctx, const nmoe_hip_router *router, const void *x, int x_dtype,
+                           int ntok, float *logits, void *stream);
+/* math.m softmax -> top-k (ties to the lower index) -> renormalise, per token
+ * (runtime.m:1498-1511).  idx/w: [ntok][8], unused slots idx 0 / w 0
+ * (kernels.metal:1767-1775).  probs (nullable): [ntok][E] softmax output. */
+NMOE_HIP_API int nmoe_moe_topk(nmoe_hip_ctx *ctx, const float *logits, int ntok, int num_experts, int k, uint32_t *idx,
+                  float *w, float *probs, void *stream);
+/* router logits + top-k.  logits (nullable) receives the logits. */
+NMOE_HIP_API int nmoe_moe_route(nmoe_hip_ctx *ctx, const nmoe_hip_router *router, const void *x, int x_dtype, int ntok, int k,
+                   uint32_t *idx, float *w, float *logits, void *stream);
+
+/* ---- routed experts with the routing given (the expert phase,
+ * runtime.m:2778-2903):
+ *   out[t] = h_mid[t] + sum_s w[t][s] * down_e(SwiGLU(gate_e x[t], up_e x[t]))
+ *            (+ sigmoid(shared_gate_raw[t]) * shared_out[t])
+ * with e = idx[t][s], the sum over slots in order (kernels.metal:1394-1423).
+ * x: [ntok][2048] fp32 or bf16; h_mid, out, shared_out: fp32 [ntok][2048];
+ * shared_gate_raw: fp32 [ntok]; shared_* both NULL or both set.  out may
+ * alias h_mid (the residual is updated in place, runtime.m:2827-2831). */
+NMOE_HIP_API int nmoe_moe_experts_q4(nmoe_hip_ctx *ctx, int layer, const void *x, int x_dtype, int ntok, int k,
+                        const uint32_t *idx, const float *w, const float *h_mid, const float *shared_out,
+                        const float *shared_gate_raw, float *out, void *stream);
+NMOE_HIP_API int nmoe_moe_experts_q2(nmoe_hip_ctx *ctx, int layer, const void *x, int x_dtype, int ntok, int k,
+                        const uint32_t *idx, const float *w, const float *h_mid, const float *shared_out,
+                        const float *shared_gate_raw, float *out, void *stream);
+
+/* ---- the whole per-layer MoE call (NMOEPipelinedExpertTail,
+ * runtime.m:2908-2999, with routing on the device and no host round trip):
+ * route x, run the selected experts of resident layer `layer`, combine into
+ * out.  idx/w/logits (nullable) receive the routing. */
+NMOE_HIP_API int nmoe_moe_layer(nmoe_hip_ctx *ctx, int layer, const nmoe_hip_router *router, const void *x, int x_dtype,
+                   int ntok, int k, const float *h_mid, const float *shared_out, const float *shared_gate_raw,
+                   float *out, uint32_t *idx, float *w, float *logits, void *stream);
+
+/* ---- bit-exact dequant probe (kernels.metal:1066-1106 nmoe_dequant_row_q4/q2,
+ * math.m:206-234): out[r][c] = q*scale + bias for `rows` rows of `in_dim`. */
+NMOE_HIP_API int nmoe_dequant_rows(nmoe_hip_ctx *ctx, int bits, const uint32_t *packed, const uint16_t *scales,
+                      const uint16_t *biases, int rows, int in_dim, float *out, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

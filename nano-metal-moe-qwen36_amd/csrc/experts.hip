@@ -1,0 +1,354 @@
+/*
+ * experts.hip -- routed-expert gate/up + SwiGLU and down + weighted combine
+ * for q4 / q2 packs resident in HBM (the multi-launch decode path).
+ *
+ * Reference: metal/kernels.metal:562-640 (nmoe_expert_gate_up_q4_batched:
+ * per expert row, SiLU(gate.x) * (up.x)), 642-714 / 1456-1542 (down and the
+ * fused weighted combine), 1394-1454 (weighted sum into the residual);
+ * q2 runs as separate dequant matvecs (kernels.metal:192-238, 303-319).
+ * Expert bases are `layer_pack + idx[slot] * expert_size`, as in the
+ * reference's all-resident variant (kernels.metal:716-856).
+ *
+ * MI355X mapping.  Every lane loads exactly 16 bytes (4 packed words) of a
+ * row per step, so a wavefront covers 1 KB:
+ *   q4 gate/up row = 256 words -> 64 lanes per row (32 columns per lane)
+ *   q2 gate/up row = 128 words -> 32 lanes per row (64 columns per lane)
+ *   q4 down row    =  64 words -> 16 lanes per row (4 rows per wavefront)
+ *   q2 down row    =  32 words ->  8 lanes per row (8 rows per wavefront)
+ * A lane's columns always sit inside one 64-column quantisation group, so
+ * its partial dot product is  scale * sum(q * x) + bias * sum(x)  with one
+ * scale/bias pair; sum(x) over the lane's columns is computed once and reused
+ * for every row.  Nibbles/crumbs are expanded with byte masks and
+ * v_cvt_f32_ubyte{0..3}; accumulation is fp32.
+ */
+#include "nmoe_hip_internal.h"
+
+template <int BITS>
+struct nmoe_q {
+    static constexpr int VPW = 32 / BITS;               /* values per word */
+    static constexpr int CPL = 4 * VPW;                 /* columns per lane (one uint4) */
+    static constexpr int LPR_G = NMOE_HIDDEN / CPL;     /* lanes per gate/up row */
+    static constexpr int LPR_D = NMOE_INTER / CPL;      /* lanes per down row */
+    static constexpr int WPR_G = NMOE_HIDDEN / VPW;     /* words per gate/up row */
+    static constexpr int WPR_D = NMOE_INTER / VPW;      /* words per down row */
+    static constexpr int GPR_G = NMOE_HIDDEN / NMOE_GROUP;
+    static constexpr int GPR_D = NMOE_INTER / NMOE_GROUP;
+};
+
+/* sum_j q_j * x_j over the 16 bytes `q` (column order of the pack). */
+template <int BITS>
+__device__ __forceinline__ float nmoe_dot16(uint4 q, const float *xs);
+
+template <>
+__device__ __forceinline__ float nmoe_dot16<4>(uint4 q, const float *xs) {
+    const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+    float a0 = 0.0f, a1 = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        uint32_t lo = w[i] & 0x0F0F0F0Fu;
+        uint32_t hi = (w[i] >> 4) & 0x0F0F0F0Fu;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            a0 = __builtin_fmaf((float)((lo >> (8 * j)) & 0xFFu), xs[8 * i + 2 * j], a0);
+            a1 = __builtin_fmaf((float)((hi >> (8 * j)) & 0xFFu), xs[8 * i + 2 * j + 1], a1);
+        }
+    }
+    return a0 + a1;
+}
+
+template <>
+__device__ __forceinline__ float nmoe_dot16<2>(uint4 q, const float *xs) {
+    const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+    float a0 = 0.0f, a1 = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+#pragma unroll
+        for (int m = 0; m < 4; m++) {
+            uint32_t p = (w[i] >> (2 * m)) & 0x03030303u;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                float v = (float)((p >> (8 * j)) & 0xFFu);
+                if (m & 1)
+                    a1 = __builtin_fmaf(v, xs[16 * i + 4 * j + m], a1);
+                else
+                    a0 = __builtin_fmaf(v, xs[16 * i + 4 * j + m], a0);
+            }
+        }
+    }
+    return a0 + a1;
+}
+
+__device__ __forceinline__ float nmoe_sigmoid_dev(float x) {
+    /* math.m:21-28 form: exp of a non-positive argument only */
+    if (x >= 0.0f) {
+        float z = __expf(-x);
+        return 1.0f / (1.0f + z);
+    }
+    float z = __expf(x);
+    return z / (1.0f + z);
+}
+
+__device__ __forceinline__ float nmoe_silu_dev(float x) { return x * nmoe_sigmoid_dev(x); }
+
+template <typename XT>
+__device__ __forceinline__ void nmoe_load_cols(const XT *x, int c0, int n, float *out);
+
+template <>
+__device__ __forceinline__ void nmoe_load_cols<float>(const float *x, int c0, int n, float *out) {
+    for (int c = 0; c < n; c += 4) {
+        float4 v = *(const float4 *)(x + c0 + c);
+        out[c] = v.x; out[c + 1] = v.y; out[c + 2] = v.z; out[c + 3] = v.w;
+    }
+}
+
+template <>
+__device__ __forceinline__ void nmoe_load_cols<uint16_t>(const uint16_t *x, int c0, int n, float *out) {
+    for (int c = 0; c < n; c += 8) {
+        uint4 v = *(const uint4 *)(x + c0 + c);
+        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            out[c + 2 * i] = __uint_as_float(w[i] << 16);
+            out[c + 2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+        }
+    }
+}
+
+/* ----------------------------------------------------------- gate/up */
+
+#define NMOE_GU_ROWS_PER_WAVE 4
+#define NMOE_GU_WAVES 4
+#define NMOE_GU_ROWS_PER_BLOCK (NMOE_GU_ROWS_PER_WAVE * NMOE_GU_WAVES)
+
+/* grid (512/16, k, ntok), 256 threads.  act[t][s][row] = SiLU(g)*u. */
+template <int BITS, typename XT>
+__global__ void __launch_bounds__(256) nmoe_gateup_kernel(const uint8_t *__restrict__ pack, const XT *__restrict__ x,
+                                                          const uint32_t *__restrict__ idx, float *__restrict__ act) {
+    using Q = nmoe_q<BITS>;
+    using L = nmoe_layout<BITS>;
+    constexpr int RPS = NMOE_WAVE / Q::LPR_G;           /* rows per wave step: 1 (q4) / 2 (q2) */
+    constexpr int STEPS = NMOE_GU_ROWS_PER_WAVE / RPS;
+    const int t = blockIdx.z, s = blockIdx.y;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int sub = lane / Q::LPR_G, l = lane % Q::LPR_G;
+    uint32_t e = idx[(size_t)t * NMOE_MAX_K + s];
+    e = e < NMOE_EXPERTS ? e : 0u; /* invalid slot: never read outside the pack */
+    const uint8_t *ex = pack + (size_t)e * L::expert_size;
+    const int row0 = blockIdx.x * NMOE_GU_ROWS_PER_BLOCK + wave * NMOE_GU_ROWS_PER_WAVE + sub;
+
+    uint4 gw[STEPS], uw[STEPS];
+    uint32_t gs[STEPS], gb[STEPS], us[STEPS], ub[STEPS];
+    const int grp = l * Q::CPL / NMOE_GROUP;
+#pragma unroll
+    for (int i = 0; i < STEPS; i++) {
+        int row = row0 + i * RPS;
+        gw[i] = ((const uint4 *)(ex + L::gate_w))[(size_t)row * (Q::WPR_G / 4) + l];
+        uw[i] = ((const uint4 *)(ex + L::up_w))[(size_t)row * (Q::WPR_G / 4) + l];
+        gs[i] = ((const uint16_t *)(ex + L::gate_s))[row * Q::GPR_G + grp];
+        gb[i] = ((const uint16_t *)(ex + L::gate_b))[row * Q::GPR_G + grp];
+        us[i] = ((const uint16_t *)(ex + L::up_s))[row * Q::GPR_G + grp];
+        ub[i] = ((const uint16_t *)(ex + L::up_b))[row * Q::GPR_G + grp];
+    }
+    float xs[Q::CPL];
+    nmoe_load_cols<XT>(x + (size_t)t * NMOE_HIDDEN, l * Q::CPL, Q::CPL, xs);
+    float xsum = 0.0f;
+#pragma unroll
+    for (int c = 0; c < Q::CPL; c++) xsum += xs[c];
+
+#pragma unroll
+    for (int i = 0; i < STEPS; i++) {
+        float g = __builtin_fmaf(nmoe_bf16f(gs[i]), nmoe_dot16<BITS>(gw[i], xs), nmoe_bf16f(gb[i]) * xsum);
+        float u = __builtin_fmaf(nmoe_bf16f(us[i]), nmoe_dot16<BITS>(uw[i], xs), nmoe_bf16f(ub[i]) * xsum);
+        g = nmoe_group_sum<Q::LPR_G>(g);
+        u = nmoe_group_sum<Q::LPR_G>(u);
+        if (l == 0) act[((size_t)t * NMOE_MAX_K + s) * NMOE_INTER + row0 + i * RPS] = nmoe_silu_dev(g) * u;
+    }
+}
+
+/* -------------------------------------------------------- down+combine */
+
+#define NMOE_DC_WAVES 4
+
+/* LDS position of act column `col` so that the LPR_D lanes of a row read
+ * consecutive 16-byte chunks (conflict-free ds_read_b128). */
+template <int BITS>
+__device__ __forceinline__ int nmoe_act_swz(int col) {
+    using Q = nmoe_q<BITS>;
+    return (((col % Q::CPL) >> 2) * Q::LPR_D + col / Q::CPL) * 4 + (col & 3);
+}
+
+/* grid (2048 / rows_per_block, ntok), 256 threads.
+ * out[t][r] = h_mid[t][r] + sum_s w[t][s] * y_s[r] (+ sigmoid(g_t) * shared[t][r]). */
+template <int BITS>
+__global__ void __launch_bounds__(256) nmoe_down_combine_kernel(
+    const uint8_t *__restrict__ pack, int k, const uint32_t *__restrict__ idx, const float *__restrict__ wts,
+    const float *__restrict__ act, const float *h_mid, const float *__restrict__ shared_out,
+    const float *__restrict__ shared_gate_raw, float *out) {
+    using Q = nmoe_q<BITS>;
+    using L = nmoe_layout<BITS>;
+    constexpr int RPW = NMOE_WAVE / Q::LPR_D;            /* rows per wavefront: 4 (q4) / 8 (q2) */
+    constexpr int RPB = RPW * NMOE_DC_WAVES;
+    __shared__ float4 act_s[NMOE_MAX_K * NMOE_INTER / 4];
+    __shared__ float asum_s[NMOE_MAX_K][Q::LPR_D];
+    const int t = blockIdx.y;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int sub = lane / Q::LPR_D, l = lane % Q::LPR_D;
+    const int row = blockIdx.x * RPB + wave * RPW + sub;
+
+    /* issue the weight loads for all slots first */
+    uint4 dw[NMOE_MAX_K];
+    uint32_t ds[NMOE_MAX_K], db[NMOE_MAX_K];
+    float wk[NMOE_MAX_K];
+    const int grp = l * Q::CPL / NMOE_GROUP;
+#pragma unroll
+    for (int s = 0; s < NMOE_MAX_K; s++) {
+        if (s < k) {
+            uint32_t e = idx[(size_t)t * NMOE_MAX_K + s];
+            /* an index outside the layer is an invalid slot: weight 0, as for
+             * a failed expert read in the reference (runtime.m:2977-2981) */
+            wk[s] = e < NMOE_EXPERTS ? wts[(size_t)t * NMOE_MAX_K + s] : 0.0f;
+            e = e < NMOE_EXPERTS ? e : 0u;
+            const uint8_t *ex = pack + (size_t)e * L::expert_size;
+            dw[s] = ((const uint4 *)(ex + L::down_w))[(size_t)row * (Q::WPR_D / 4) + l];
+            ds[s] = ((const uint16_t *)(ex + L::down_s))[row * Q::GPR_D + grp];
+            db[s] = ((const uint16_t *)(ex + L::down_b))[row * Q::GPR_D + grp];
+        }
+    }
+    /* stage this token's activations, swizzled */
+    const float4 *a4 = (const float4 *)(act + (size_t)t * NMOE_MAX_K * NMOE_INTER);
+    for (int f = threadIdx.x; f < k * (NMOE_INTER / 4); f += blockDim.x) {
+        int s = f / (NMOE_INTER / 4), col = (f % (NMOE_INTER / 4)) * 4;
+        act_s[s * (NMOE_INTER / 4) + (nmoe_act_swz<BITS>(col) >> 2)] = a4[f];
+    }
+    __syncthreads();
+    for (int p = threadIdx.x; p < k * Q::LPR_D; p += blockDim.x) {
+        int s = p / Q::LPR_D, ll = p % Q::LPR_D;
+        float a = 0.0f;
+        for (int c = 0; c < Q::CPL / 4; c++) {
+            float4 v = act_s[s * (NMOE_INTER / 4) + c * Q::LPR_D + ll];
+            a += (v.x + v.y) + (v.z + v.w);
+        }
+        asum_s[s][ll] = a;
+    }
+    __syncthreads();
+
+    float moe = 0.0f;
+#pragma unroll
+    for (int s = 0; s < NMOE_MAX_K; s++) {
+        if (s < k) {
+            float xs[Q::CPL];
+#pragma unroll
+            for (int c = 0; c < Q::CPL / 4; c++) {
+                float4 v = act_s[s * (NMOE_INTER / 4) + c * Q::LPR_D + l];
+                xs[4 * c] = v.x; xs[4 * c + 1] = v.y; xs[4 * c + 2] = v.z; xs[4 * c + 3] = v.w;
+            }
+            float y = __builtin_fmaf(nmoe_bf16f(ds[s]), nmoe_dot16<BITS>(dw[s], xs), nmoe_bf16f(db[s]) * asum_s[s][l]);
+            y = nmoe_group_sum<Q::LPR_D>(y);
+            moe += wk[s] * y;
+        }
+    }
+    if (l == 0) {
+        size_t o = (size_t)t * NMOE_HIDDEN + row;
+        float r = h_mid[o] + moe;
+        if (shared_out != NULL) r = r + nmoe_sigmoid_dev(shared_gate_raw[t]) * shared_out[o];
+        out[o] = r;
+    }
+}
+
+/* ------------------------------------------------------- entry points */
+
+int nmoe_check_x(nmoe_hip_ctx *ctx, const void *x, int x_dtype, int ntok);
+int nmoe_check_router(nmoe_hip_ctx *ctx, const nmoe_hip_router *r);
+
+static int nmoe_check_experts(nmoe_hip_ctx *ctx, int layer, int bits, const void *x, int x_dtype, int ntok, int k,
+                              const uint32_t *idx, const float *w, const float *h_mid, const float *shared_out,
+                              const float *shared_gate_raw, const float *out, const uint8_t **pack) {
+    if (ctx == NULL) return NMOE_HIP_EINVAL;
+    if (k < 1 || k > NMOE_MAX_K) return nmoe_fail(ctx, NMOE_HIP_EINVAL, "k=%d outside 1..8", k);
+    int rc = nmoe_check_x(ctx, x, x_dtype, ntok);
+    if (rc != NMOE_HIP_OK) return rc;
+    if (idx == NULL || w == NULL || h_mid == NULL || out == NULL)
+        return nmoe_fail(ctx, NMOE_HIP_EINVAL, "NULL idx/w/h_mid/out");
+    if (!nmoe_aligned(h_mid, 4) || !nmoe_aligned(out, 4) || !nmoe_aligned(idx, 4) || !nmoe_aligned(w, 4))
+        return nmoe_fail(ctx, NMOE_HIP_EINVAL, "misaligned idx/w/h_mid/out");
+    if ((shared_out == NULL) != (shared_gate_raw == NULL))
+        return nmoe_fail(ctx, NMOE_HIP_EINVAL, "shared_out and shared_gate_raw must both be set or both NULL");
+    if (layer < 0 || layer >= NMOE_HIP_MAX_LAYERS || ctx->packs[layer].dev == NULL)
+        return nmoe_fail(ctx, NMOE_HIP_ENOENT, "layer %d has no resident pack", layer);
+    if (ctx->packs[layer].bits != bits)
+        return nmoe_fail(ctx, NMOE_HIP_EINVAL, "layer %d is q%d, called as q%d", layer, ctx->packs[layer].bits, bits);
+    *pack = (const uint8_t *)ctx->packs[layer].dev;
+    return NMOE_HIP_OK;
+}
+
+template <int BITS>
+static int nmoe_launch_experts(nmoe_hip_ctx *ctx, const uint8_t *pack, const void *x, int x_dtype, int ntok, int k,
+                               const uint32_t *idx, const float *w, const float *h_mid, const float *shared_out,
+                               const float *shared_gate_raw, float *out, hipStream_t s) {
+    using Q = nmoe_q<BITS>;
+    dim3 g1(NMOE_INTER / NMOE_GU_ROWS_PER_BLOCK, k, ntok);
+    if (x_dtype == NMOE_HIP_BF16)
+        hipLaunchKernelGGL((nmoe_gateup_kernel<BITS, uint16_t>), g1, dim3(256), 0, s, pack, (const uint16_t *)x, idx,
+                           ctx->act);
+    else
+        hipLaunchKernelGGL((nmoe_gateup_kernel<BITS, float>), g1, dim3(256), 0, s, pack, (const float *)x, idx,
+                           ctx->act);
+    NMOE_HIP_TRY(ctx, hipGetLastError());
+    constexpr int RPB = (NMOE_WAVE / Q::LPR_D) * NMOE_DC_WAVES;
+    dim3 g2(NMOE_HIDDEN / RPB, ntok);
+    hipLaunchKernelGGL((nmoe_down_combine_kernel<BITS>), g2, dim3(256), 0, s, pack, k, idx, w, ctx->act, h_mid,
+                       shared_out, shared_gate_raw, out);
+    NMOE_HIP_TRY(ctx, hipGetLastError());
+    return NMOE_HIP_OK;
+}
+
+extern "C" int nmoe_moe_experts_q4(nmoe_hip_ctx *ctx, int layer, const void *x, int x_dtype, int ntok, int k,
+                                   const uint32_t *idx, const float *w, const float *h_mid, const float *shared_out,
+                                   const float *shared_gate_raw, float *out, void *stream) {
+    const uint8_t *pack = NULL;
+    int rc = nmoe_check_experts(ctx, layer, 4, x, x_dtype, ntok, k, idx, w, h_mid, shared_out, shared_gate_raw, out,
+                                &pack);
+    if (rc != NMOE_HIP_OK) return rc;
+    return nmoe_launch_experts<4>(ctx, pack, x, x_dtype, ntok, k, idx, w, h_mid, shared_out, shared_gate_raw, out,
+                                  nmoe_stream_of(ctx, stream));
+}
+
+extern "C" int nmoe_moe_experts_q2(nmoe_hip_ctx *ctx, int layer, const void *x, int x_dtype, int ntok, int k,
+                                   const uint32_t *idx, const float *w, const float *h_mid, const float *shared_out,
+                                   const float *shared_gate_raw, float *out, void *stream) {
+    const uint8_t *pack = NULL;
+    int rc = nmoe_check_experts(ctx, layer, 2, x, x_dtype, ntok, k, idx, w, h_mid, shared_out, shared_gate_raw, out,
+                                &pack);
+    if (rc != NMOE_HIP_OK) return rc;
+    return nmoe_launch_experts<2>(ctx, pack, x, x_dtype, ntok, k, idx, w, h_mid, shared_out, shared_gate_raw, out,
+                                  nmoe_stream_of(ctx, stream));
+}
+
+extern "C" int nmoe_decode_init(nmoe_hip_ctx *ctx) {
+    (void)ctx;
+    return NMOE_HIP_OK;
+}
+
+extern "C" int nmoe_moe_layer(nmoe_hip_ctx *ctx, int layer, const nmoe_hip_router *router, const void *x, int x_dtype,
+                              int ntok, int k, const float *h_mid, const float *shared_out,
+                              const float *shared_gate_raw, float *out, uint32_t *idx, float *w, float *logits,
+                              void *stream) {
+    if (ctx == NULL) return NMOE_HIP_EINVAL;
+    if (layer < 0 || layer >= NMOE_HIP_MAX_LAYERS || ctx->packs[layer].dev == NULL)
+        return nmoe_fail(ctx, NMOE_HIP_ENOENT, "layer %d has no resident pack", layer);
+    int rc = nmoe_check_router(ctx, router);
+    if (rc != NMOE_HIP_OK) return rc;
+    if (router->num_experts != NMOE_EXPERTS)
+        return nmoe_fail(ctx, NMOE_HIP_EINVAL, "a layer pack holds 256 experts; router has %d", router->num_experts);
+    rc = nmoe_check_x(ctx, x, x_dtype, ntok);
+    if (rc != NMOE_HIP_OK) return rc;
+    uint32_t *ri = idx != NULL ? idx : ctx->idx;
+    float *rw = w != NULL ? w : ctx->w;
+    rc = nmoe_moe_route(ctx, router, x, x_dtype, ntok, k, ri, rw, logits, stream);
+    if (rc != NMOE_HIP_OK) return rc;
+    if (ctx->packs[layer].bits == 4)
+        return nmoe_moe_experts_q4(ctx, layer, x, x_dtype, ntok, k, ri, rw, h_mid, shared_out, shared_gate_raw, out,
+                                   stream);
+    return nmoe_moe_experts_q2(ctx, layer, x, x_dtype, ntok, k, ri, rw, h_mid, shared_out, shared_gate_raw, out,
+                               stream);
+}

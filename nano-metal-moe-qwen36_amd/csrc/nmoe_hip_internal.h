@@ -1,0 +1,124 @@
+/*
+ * nmoe_hip_internal.h -- shared definitions of libnmoe_hip.so (not installed).
+ */
+#ifndef NMOE_HIP_INTERNAL_H
+#define NMOE_HIP_INTERNAL_H
+
+#include <hip/hip_runtime.h>
+#include <stdarg.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "nmoe_exact.h"
+#include "nmoe_hip.h"
+
+#define NMOE_WAVE 64
+#define NMOE_HIDDEN NMOE_HIP_HIDDEN
+#define NMOE_INTER NMOE_HIP_INTER
+#define NMOE_EXPERTS NMOE_HIP_EXPERTS
+#define NMOE_GROUP NMOE_HIP_GROUP
+#define NMOE_MAX_K NMOE_HIP_MAX_K
+
+/* Pack component offsets (scripts/convert_qwen36.py:38-64, runtime.m:2240-2252):
+ * gate w/s/b, up w/s/b, down w/s/b. */
+#define NMOE_Q4_OFFSETS {0u, 524288u, 557056u, 589824u, 1114112u, 1146880u, 1179648u, 1703936u, 1736704u}
+#define NMOE_Q2_OFFSETS {0u, 262144u, 294912u, 327680u, 589824u, 622592u, 655360u, 917504u, 950272u}
+
+template <int BITS>
+struct nmoe_layout;
+
+template <>
+struct nmoe_layout<4> {
+    static constexpr uint32_t expert_size = NMOE_HIP_EXPERT_SIZE_Q4;
+    static constexpr uint32_t gate_w = 0u, gate_s = 524288u, gate_b = 557056u;
+    static constexpr uint32_t up_w = 589824u, up_s = 1114112u, up_b = 1146880u;
+    static constexpr uint32_t down_w = 1179648u, down_s = 1703936u, down_b = 1736704u;
+};
+
+template <>
+struct nmoe_layout<2> {
+    static constexpr uint32_t expert_size = NMOE_HIP_EXPERT_SIZE_Q2;
+    static constexpr uint32_t gate_w = 0u, gate_s = 262144u, gate_b = 294912u;
+    static constexpr uint32_t up_w = 327680u, up_s = 589824u, up_b = 622592u;
+    static constexpr uint32_t down_w = 655360u, down_s = 917504u, down_b = 950272u;
+};
+
+/* Device scratch words used by persistent kernels.  Each counter sits on
+ * its own 128-byte line. */
+#define NMOE_SYNC_STATUS 0     /* set to 1 by a kernel whose bounded wait expired */
+#define NMOE_SYNC_BARRIER 32   /* grid barrier arrival counter */
+#define NMOE_SYNC_EXIT 64      /* exit counter (last block resets the barrier) */
+#define NMOE_SYNC_WORDS 128
+
+struct nmoe_pack_slot {
+    void *dev;
+    int bits;
+    size_t bytes;
+};
+
+struct nmoe_buf_entry {
+    char label[64];
+    void *dev;
+    size_t size;
+};
+
+struct nmoe_hip_ctx {
+    int device;
+    int num_cus;
+    int max_tokens;
+    hipStream_t stream;
+    nmoe_pack_slot packs[NMOE_HIP_MAX_LAYERS];
+    nmoe_buf_entry *bufs;
+    int nbufs;
+    int capbufs;
+    /* scratch, sized for max_tokens at create */
+    float *act;      /* [max_tokens][8][512] SwiGLU activations */
+    float *logits;   /* [max_tokens][256] */
+    uint32_t *idx;   /* [max_tokens][8] routing scratch for nmoe_moe_layer */
+    float *w;        /* [max_tokens][8] */
+    uint32_t *sync;  /* NMOE_SYNC_WORDS */
+    int fused_blocks;     /* persistent decode grid (0 = not resident-capable) */
+    char err[256];
+};
+
+int nmoe_fail(nmoe_hip_ctx *ctx, int code, const char *fmt, ...);
+int nmoe_hip_check(nmoe_hip_ctx *ctx, hipError_t e, const char *what);
+
+#define NMOE_HIP_TRY(ctx, call)                                   \
+    do {                                                          \
+        hipError_t nmoe_e_ = (call);                              \
+        if (nmoe_e_ != hipSuccess) return nmoe_hip_check((ctx), nmoe_e_, #call); \
+    } while (0)
+
+static inline hipStream_t nmoe_stream_of(nmoe_hip_ctx *ctx, void *stream) {
+    return stream != NULL ? (hipStream_t)stream : ctx->stream;
+}
+
+static inline int nmoe_aligned(const void *p, size_t a) { return ((uintptr_t)p % a) == 0; }
+
+/* ---------------------------------------------------------------- device */
+
+__device__ __forceinline__ float nmoe_bf16f(uint32_t h) { return __uint_as_float(h << 16); }
+
+__device__ __forceinline__ uint32_t nmoe_f32_to_bf16_bits(float f) {
+    uint32_t b = __float_as_uint(f);
+    return (b + 0x7FFFu + ((b >> 16) & 1u)) >> 16;
+}
+
+/* xor-butterfly sum over the 64 lanes: every lane ends with the same value,
+ * combined in the fixed order ((l ^ 32), (l ^ 16), ..., (l ^ 1)). */
+__device__ __forceinline__ float nmoe_wave_sum_butterfly(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+/* Sum over aligned groups of W lanes (W = 4..64), result in every lane. */
+template <int W>
+__device__ __forceinline__ float nmoe_group_sum(float v) {
+#pragma unroll
+    for (int off = W / 2; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+#endif

@@ -1,0 +1,242 @@
+"""GPU parity: libnmoe_hip.so's kernels, called through the C ABI, against the
+CPU oracle and the reference math.m golden vectors.
+
+Bars: routing indices, probabilities, dequantised weights and generator
+bytes bit-exact; floating-point outputs within max-abs 2e-3 and relative L2
+1e-3 (tests/conftest.py MAX_ABS / REL_L2)."""
+import numpy as np
+import pytest
+
+from conftest import assert_close
+from oracle import binding as B
+
+pytestmark = pytest.mark.gpu
+
+SIGMA = {4: 0.02, 2: 0.05}
+
+
+@pytest.fixture(scope="module")
+def nh():
+    import nmoe_hip
+    return nmoe_hip
+
+
+@pytest.fixture(scope="module")
+def ctx(nh):
+    c = nh.Context(0, max_tokens=64)
+    yield c
+    c.close()
+
+
+def host_pack(bits, seed, layer, experts):
+    """Zero-filled host layer with only `experts` generated (pages of the
+    untouched experts are never allocated)."""
+    esz = B.EXPERT_SIZE[bits]
+    pack = np.zeros(B.EXPERTS * esz, np.uint8)
+    for e in sorted(set(int(v) for v in experts)):
+        pack[e * esz:(e + 1) * esz] = B.syn_expert(bits, seed, layer, e, SIGMA[bits])
+    return pack
+
+
+def test_argument_validation(ctx, nh):
+    x = ctx.alloc(2048 * 4)
+    idx = ctx.alloc(8 * 4)
+    w = ctx.alloc(8 * 4)
+    h = ctx.alloc(2048 * 4)
+    out = ctx.alloc(2048 * 4)
+    ctx.synth_layer(3, 4, 1, 0.02)
+    for k in (0, 9, -1):
+        assert ctx.experts(4, 3, x, nh.F32, 1, k, idx, w, h, out) == nh.EINVAL
+    assert ctx.experts(4, 4, x, nh.F32, 1, 8, idx, w, h, out) == nh.ENOENT  # layer not resident
+    assert ctx.experts(2, 3, x, nh.F32, 1, 8, idx, w, h, out) == nh.EINVAL  # q4 layer called as q2
+    assert ctx.experts(4, 3, x.ptr + 4, nh.F32, 1, 8, idx, w, h, out) == nh.EINVAL  # misaligned x
+    assert ctx.experts(4, 3, x, nh.F32, 65, 8, idx, w, h, out) == nh.EINVAL  # ntok > max_tokens
+    assert ctx.experts(4, 3, None, nh.F32, 1, 8, idx, w, h, out) == nh.EINVAL
+    assert ctx.experts(4, 3, x, nh.F32, 1, 8, idx, w, h, out, shared_out=h) == nh.EINVAL
+    r = ctx.router_bf16(None)
+    assert ctx.route(r, x, nh.BF16, 1, 8, idx, w) == nh.EINVAL
+    assert ctx.topk(x, 1, 256, 9, idx, w) == nh.EINVAL
+    bad = np.zeros(100, np.uint8)
+    with pytest.raises(nh.NmoeError):
+        ctx.upload_layer(5, 4, bad)
+    ctx.sync()
+
+
+@pytest.mark.parametrize("bits", [4, 2])
+def test_device_generator_matches_oracle(ctx, bits):
+    layer = 7 if bits == 4 else 8
+    ctx.synth_layer(layer, bits, 1234, SIGMA[bits])
+    ctx.sync()
+    for e in (0, 1, 77, 255):
+        got = ctx.download_expert(layer, e, bits)
+        want = B.syn_expert(bits, 1234, layer, e, SIGMA[bits])
+        np.testing.assert_array_equal(got, want, err_msg=f"expert {e}")
+    buf = ctx.alloc(4096 * 2)
+    ctx.synth_bf16(buf, 4096, 99, 3, 17, 1.0)
+    np.testing.assert_array_equal(buf.download(np.uint16, 4096), B.syn_bf16(4096, 99, 3, 17, 1.0))
+
+
+@pytest.mark.parametrize("bits", [4, 2])
+def test_dequant_probe_bit_exact(ctx, golden, bits):
+    wg, sg, bg = golden[f"q{bits}_packed"], golden[f"q{bits}_scales"], golden[f"q{bits}_biases"]
+    rows = wg.shape[0]
+    dw, ds, db = ctx.to_device(wg), ctx.to_device(sg), ctx.to_device(bg)
+    out = ctx.alloc(rows * 2048 * 4)
+    ctx._check(ctx.dequant_rows(bits, dw, ds, db, rows, 2048, out))
+    got = out.download(np.float32, (rows, 2048))
+    np.testing.assert_array_equal(got.view(np.uint32), golden[f"q{bits}_dequant"].view(np.uint32))
+
+
+def test_topk_matches_math_m_golden(ctx, golden):
+    L = golden["route_logits"]
+    n = L.shape[0]
+    lg = ctx.to_device(L)
+    idx = ctx.alloc(n * 8 * 4)
+    w = ctx.alloc(n * 8 * 4)
+    probs = ctx.alloc(n * 256 * 4)
+    for k in range(1, 9):
+        ctx._check(ctx.topk(lg, n, 256, k, idx, w, probs))
+        gi = idx.download(np.uint32, (n, 8))
+        gw = w.download(np.float32, (n, 8))
+        gp = probs.download(np.float32, (n, 256))
+        np.testing.assert_array_equal(gp.view(np.uint32), golden["route_probs"].view(np.uint32))
+        for c in np.nonzero(golden["route_k"] == k)[0]:
+            np.testing.assert_array_equal(gi[c], golden["route_idx"][c], err_msg=f"case {c}")
+            np.testing.assert_array_equal(gw[c].view(np.uint32), golden["route_w"][c].view(np.uint32),
+                                          err_msg=f"case {c}")
+
+
+def test_topk_fewer_experts_than_k(ctx, golden):
+    lg = ctx.to_device(golden["small_logits"])
+    idx, w, probs = ctx.alloc(32), ctx.alloc(32), ctx.alloc(32)
+    ctx._check(ctx.topk(lg, 1, 5, 8, idx, w, probs))
+    np.testing.assert_array_equal(idx.download(np.uint32, 8), golden["small_idx"])
+    np.testing.assert_array_equal(w.download(np.float32, 8).view(np.uint32), golden["small_w"].view(np.uint32))
+    np.testing.assert_array_equal(probs.download(np.float32, 5).view(np.uint32),
+                                  golden["small_probs"].view(np.uint32))
+
+
+def test_topk_random_against_oracle(ctx):
+    """Many tokens, spreads from narrow to > 100 (slow exact-sum path), ties."""
+    rng = np.random.default_rng(21)
+    ntok = 64
+    L = (rng.standard_normal((ntok, 256)) * rng.choice([0.05, 1, 4, 30, 120], size=(ntok, 1))).astype(np.float32)
+    L[::5, 100:110] = L[::5, 100:101]  # exact ties
+    L[1::7, :] = np.round(L[1::7, :], 1)  # many coarse ties
+    lg = ctx.to_device(L)
+    idx, w, probs = ctx.alloc(ntok * 32), ctx.alloc(ntok * 32), ctx.alloc(ntok * 1024)
+    for k in (1, 6, 8):
+        ctx._check(ctx.topk(lg, ntok, 256, k, idx, w, probs))
+        gi, gw, gp = idx.download(np.uint32, (ntok, 8)), w.download(np.float32, (ntok, 8)), probs.download(np.float32, (ntok, 256))
+        for t in range(ntok):
+            oi, ow, on, op = B.route(L[t], k, want_probs=True)
+            np.testing.assert_array_equal(gp[t].view(np.uint32), op.view(np.uint32), err_msg=f"t={t}")
+            np.testing.assert_array_equal(gi[t], oi, err_msg=f"t={t} k={k}")
+            np.testing.assert_array_equal(gw[t].view(np.uint32), ow.view(np.uint32), err_msg=f"t={t} k={k}")
+
+
+def test_router_logits_bit_exact(ctx, nh):
+    rng = np.random.default_rng(22)
+    ntok = 5
+    W = B.syn_bf16(256 * 2048, 3, 0, 16, 0.02).reshape(256, 2048)
+    xb = B.f32_to_bf16(rng.standard_normal((ntok, 2048)).astype(np.float32))
+    xf = B.bf16_to_f32(xb) * np.float32(1.37)  # not bf16-representable: exercises the fp32 path
+    dW = ctx.to_device(W)
+    lg = ctx.alloc(ntok * 256 * 4)
+    r = ctx.router_bf16(dW)
+    for xarr, dt in ((xb, nh.BF16), (xf, nh.F32)):
+        dx = ctx.to_device(xarr)
+        ctx._check(ctx.router_logits(r, dx, dt, ntok, lg))
+        got = lg.download(np.float32, (ntok, 256))
+        xw = B.bf16_to_f32(xarr) if dt == nh.BF16 else xarr
+        for t in range(ntok):
+            want = B.router_logits_bf16(W, xw[t])
+            np.testing.assert_array_equal(got[t].view(np.uint32), want.view(np.uint32))
+    # the reference model's q4 router (kernels.metal:472-513 semantics)
+    wq = rng.integers(0, 2**32, size=(256, 256), dtype=np.uint64).astype(np.uint32)
+    sq = B.f32_to_bf16((rng.standard_normal((256, 32)) * 0.01).astype(np.float32))
+    bq = B.f32_to_bf16((-8 * B.bf16_to_f32(sq)).astype(np.float32))
+    rq = ctx.router_q4(ctx.to_device(wq), ctx.to_device(sq), ctx.to_device(bq))
+    dx = ctx.to_device(xf)
+    ctx._check(ctx.router_logits(rq, dx, nh.F32, ntok, lg))
+    got = lg.download(np.float32, (ntok, 256))
+    for t in range(ntok):
+        want = np.zeros(256, np.float32)
+        B.oracle().orc_router_logits_q4(wq.ctypes.data, sq.ctypes.data, bq.ctypes.data, xf[t].ctypes.data, 256, 2048,
+                                        want.ctypes.data)
+        np.testing.assert_array_equal(got[t].view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("bits", [4, 2])
+@pytest.mark.parametrize("ntok,k", [(1, 8), (1, 1), (3, 6), (4, 8)])
+def test_experts_against_oracle(ctx, nh, bits, ntok, k):
+    rng = np.random.default_rng(100 * bits + 10 * ntok + k)
+    seed, layer = 5, 10 + bits
+    ctx.synth_layer(layer, bits, seed, SIGMA[bits])
+    idx = np.zeros((ntok, 8), np.uint32)
+    for t in range(ntok):
+        idx[t, :k] = rng.choice(256, k, replace=False)
+    w = np.zeros((ntok, 8), np.float32)
+    w[:, :k] = rng.dirichlet(np.ones(k), size=ntok).astype(np.float32)
+    xb = B.f32_to_bf16(rng.standard_normal((ntok, 2048)).astype(np.float32))
+    x = B.bf16_to_f32(xb).reshape(ntok, 2048)
+    h = rng.standard_normal((ntok, 2048)).astype(np.float32)
+    pack = host_pack(bits, seed, layer, idx[:, :k].ravel())
+    want = B.moe_experts(pack, bits, x, k, idx, w, h)
+    d_idx, d_w, d_h, out = ctx.to_device(idx), ctx.to_device(w), ctx.to_device(h), ctx.alloc(ntok * 2048 * 4)
+    for arr, dt in ((xb, nh.BF16), (x, nh.F32)):
+        ctx._check(ctx.experts(bits, layer, ctx.to_device(arr), dt, ntok, k, d_idx, d_w, d_h, out))
+        got = out.download(np.float32, (ntok, 2048))
+        assert_close(got, want, what=f"q{bits} ntok={ntok} k={k} dt={dt}")
+    # shared-expert term, updated in place on the residual (out aliases h_mid)
+    sh = rng.standard_normal((ntok, 2048)).astype(np.float32)
+    g = rng.standard_normal(ntok).astype(np.float32)
+    want_sh = B.moe_experts(pack, bits, x, k, idx, w, h, shared_out=sh, shared_gate_raw=g)
+    d_res = ctx.to_device(h)
+    ctx._check(ctx.experts(bits, layer, ctx.to_device(x), nh.F32, ntok, k, d_idx, d_w, d_res, d_res,
+                           shared_out=ctx.to_device(sh), shared_gate_raw=ctx.to_device(g)))
+    assert_close(d_res.download(np.float32, (ntok, 2048)), want_sh, what="shared + in place")
+
+
+@pytest.mark.parametrize("name,bits,k", [("step_q4_k8", 4, 8), ("step_q2_k8", 2, 8), ("step_q2_k6", 2, 6)])
+def test_layer_matches_math_m_golden(ctx, nh, golden, name, bits, k):
+    """The whole per-layer call on the config inputs (seed 0, layer 0) against
+    the decode step computed by the reference's own math.m."""
+    seed, layer = 0, 20 + bits
+    # the generator keys on the layer number: layer 0's selected experts, held in slot `layer`
+    ctx.upload_layer(layer, bits, host_pack(bits, seed, 0, golden[f"{name}_idx"][:k]))
+    router = ctx.alloc(256 * 2048 * 2)
+    ctx.synth_bf16(router, 256 * 2048, seed, 0, 16, 0.02)
+    x = ctx.alloc(2048 * 2)
+    ctx.synth_bf16(x, 2048, seed, 0, 17, 1.0)
+    hb = ctx.alloc(2048 * 2)
+    ctx.synth_bf16(hb, 2048, seed, 0, 18, 1.0)
+    h = ctx.to_device(B.bf16_to_f32(hb.download(np.uint16, 2048)))
+    out, idx, w, lg = ctx.alloc(2048 * 4), ctx.alloc(32), ctx.alloc(32), ctx.alloc(1024)
+    ctx._check(ctx.moe_layer(layer, ctx.router_bf16(router), x, nh.BF16, 1, k, h, out, idx, w, lg))
+    np.testing.assert_array_equal(lg.download(np.float32, 256).view(np.uint32), golden[f"{name}_logits"].view(np.uint32))
+    np.testing.assert_array_equal(idx.download(np.uint32, 8), golden[f"{name}_idx"])
+    np.testing.assert_array_equal(w.download(np.float32, 8).view(np.uint32), golden[f"{name}_w"].view(np.uint32))
+    assert_close(out.download(np.float32, 2048), golden[f"{name}_out"], what=name)
+
+
+@pytest.mark.parametrize("bits", [4, 2])
+def test_layer_multi_token_against_oracle(ctx, nh, bits):
+    rng = np.random.default_rng(7 + bits)
+    seed, layer, ntok, k = 11, 30 + bits, 6, 8
+    ctx.synth_layer(layer, bits, seed, SIGMA[bits])
+    W = B.syn_bf16(256 * 2048, seed, layer, 16, 0.02).reshape(256, 2048)
+    xb = B.f32_to_bf16(rng.standard_normal((ntok, 2048)).astype(np.float32))
+    x = B.bf16_to_f32(xb).reshape(ntok, 2048)
+    h = rng.standard_normal((ntok, 2048)).astype(np.float32)
+    idx_o = np.zeros((ntok, 8), np.uint32)
+    w_o = np.zeros((ntok, 8), np.float32)
+    for t in range(ntok):
+        idx_o[t], w_o[t], _ = B.route(B.router_logits_bf16(W, x[t]), k)
+    want = B.moe_experts(host_pack(bits, seed, layer, idx_o[:, :k].ravel()), bits, x, k, idx_o, w_o, h)
+    out, idx, w = ctx.alloc(ntok * 2048 * 4), ctx.alloc(ntok * 32), ctx.alloc(ntok * 32)
+    ctx._check(ctx.moe_layer(layer, ctx.router_bf16(ctx.to_device(W)), ctx.to_device(xb), nh.BF16, ntok, k,
+                             ctx.to_device(h), out, idx, w))
+    np.testing.assert_array_equal(idx.download(np.uint32, (ntok, 8)), idx_o)
+    np.testing.assert_array_equal(w.download(np.float32, (ntok, 8)).view(np.uint32), w_o.view(np.uint32))
+    assert_close(out.download(np.float32, (ntok, 2048)), want, what=f"layer q{bits}")
