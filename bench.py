@@ -8,7 +8,8 @@ fp32 residual.  Steps rotate over 40 synthetic layers resident in HBM
 (40 x 453 MB = 18.1 GB, far above the 256 MB last-level cache) with a
 distinct router and input per layer, so weights stream from HBM.
 
-A step is one call of the per-layer MoE entry point (nmoe_moe_layer).
+A step is one call of the per-layer MoE entry point (nmoe_moe_layer), which
+for one token is a single persistent launch (nmoe_fused_decode_kernel).
 Timed region: `--steps` back-to-back steps on the library's stream,
 bracketed by HIP events and stream synchronisation.  A second pass records
 an event pair around every launch of the dominant kernel to get its average
@@ -139,7 +140,7 @@ def main():
     ap.add_argument("--bits", type=int, default=4, choices=(4, 2))
     ap.add_argument("--k", type=int, default=8)
     ap.add_argument("--seed", type=int, default=0)
-    ap.add_argument("--cpu-steps", type=int, default=210)
+    ap.add_argument("--cpu-steps", type=int, default=630)
     ap.add_argument("--no-cpu", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -235,7 +236,7 @@ def main():
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": None,
-            "kernel": "whole nmoe_moe_layer step (event pair per step)",
+            "kernel": "nmoe_fused_decode_kernel<4,true,bf16> (one launch = one step; event pair per launch)",
             "kernel_ms": round(kern_ms, 5),
         },
     }

@@ -88,6 +88,13 @@ NMOE_HIP_API int nmoe_hip_device_cus(const nmoe_hip_ctx *ctx);
  * when a bounded wait expires: returns 0 or NMOE_HIP_ETIMEDOUT.  Synchronous. */
 NMOE_HIP_API int nmoe_hip_check_device_status(nmoe_hip_ctx *ctx);
 
+/* Path options (the counterpart of the reference's experiment toggles,
+ * NMOE_FUSED_DOWN_COMBINE_Q4 / NMOE_PIPELINE etc., runtime.m:1426-1496).
+ * NMOE_HIP_OPT_FUSED_DECODE (default 1): single-token calls run as one
+ * persistent cooperative launch; 0 selects the multi-launch kernels. */
+#define NMOE_HIP_OPT_FUSED_DECODE 1
+NMOE_HIP_API int nmoe_hip_set_option(nmoe_hip_ctx *ctx, int option, int value);
+
 /* ---- buffers (backend.h:64-66: register_shared_buffer / register_state_buffer
  *      / lookup_shared_buffer).  The context owns them until destroy. */
 NMOE_HIP_API int nmoe_hip_register_state_buffer(nmoe_hip_ctx *ctx, const char *label, size_t size, void **dev_out);

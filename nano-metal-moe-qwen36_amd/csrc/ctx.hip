@@ -42,6 +42,7 @@ extern "C" int nmoe_hip_create(int device, int max_tokens, nmoe_hip_ctx **out) {
     if (ctx == NULL) return NMOE_HIP_ENOMEM;
     ctx->device = device;
     ctx->max_tokens = max_tokens;
+    ctx->use_fused = 1;
     hipDeviceProp_t prop;
     if (hipGetDeviceProperties(&prop, device) != hipSuccess || hipStreamCreate(&ctx->stream) != hipSuccess) {
         free(ctx);
@@ -86,6 +87,15 @@ extern "C" void nmoe_hip_destroy(nmoe_hip_ctx *ctx) {
     hipFree(ctx->sync);
     if (ctx->stream != NULL) hipStreamDestroy(ctx->stream);
     free(ctx);
+}
+
+extern "C" int nmoe_hip_set_option(nmoe_hip_ctx *ctx, int option, int value) {
+    if (ctx == NULL) return NMOE_HIP_EINVAL;
+    if (option == NMOE_HIP_OPT_FUSED_DECODE) {
+        ctx->use_fused = value != 0;
+        return NMOE_HIP_OK;
+    }
+    return nmoe_fail(ctx, NMOE_HIP_EINVAL, "unknown option %d", option);
 }
 
 extern "C" const char *nmoe_hip_last_error(const nmoe_hip_ctx *ctx) { return ctx != NULL ? ctx->err : "no context"; }

@@ -21,98 +21,7 @@
  * for every row.  Nibbles/crumbs are expanded with byte masks and
  * v_cvt_f32_ubyte{0..3}; accumulation is fp32.
  */
-#include "nmoe_hip_internal.h"
-
-template <int BITS>
-struct nmoe_q {
-    static constexpr int VPW = 32 / BITS;               /* values per word */
-    static constexpr int CPL = 4 * VPW;                 /* columns per lane (one uint4) */
-    static constexpr int LPR_G = NMOE_HIDDEN / CPL;     /* lanes per gate/up row */
-    static constexpr int LPR_D = NMOE_INTER / CPL;      /* lanes per down row */
-    static constexpr int WPR_G = NMOE_HIDDEN / VPW;     /* words per gate/up row */
-    static constexpr int WPR_D = NMOE_INTER / VPW;      /* words per down row */
-    static constexpr int GPR_G = NMOE_HIDDEN / NMOE_GROUP;
-    static constexpr int GPR_D = NMOE_INTER / NMOE_GROUP;
-};
-
-/* sum_j q_j * x_j over the 16 bytes `q` (column order of the pack). */
-template <int BITS>
-__device__ __forceinline__ float nmoe_dot16(uint4 q, const float *xs);
-
-template <>
-__device__ __forceinline__ float nmoe_dot16<4>(uint4 q, const float *xs) {
-    const uint32_t w[4] = {q.x, q.y, q.z, q.w};
-    float a0 = 0.0f, a1 = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        uint32_t lo = w[i] & 0x0F0F0F0Fu;
-        uint32_t hi = (w[i] >> 4) & 0x0F0F0F0Fu;
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            a0 = __builtin_fmaf((float)((lo >> (8 * j)) & 0xFFu), xs[8 * i + 2 * j], a0);
-            a1 = __builtin_fmaf((float)((hi >> (8 * j)) & 0xFFu), xs[8 * i + 2 * j + 1], a1);
-        }
-    }
-    return a0 + a1;
-}
-
-template <>
-__device__ __forceinline__ float nmoe_dot16<2>(uint4 q, const float *xs) {
-    const uint32_t w[4] = {q.x, q.y, q.z, q.w};
-    float a0 = 0.0f, a1 = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-#pragma unroll
-        for (int m = 0; m < 4; m++) {
-            uint32_t p = (w[i] >> (2 * m)) & 0x03030303u;
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                float v = (float)((p >> (8 * j)) & 0xFFu);
-                if (m & 1)
-                    a1 = __builtin_fmaf(v, xs[16 * i + 4 * j + m], a1);
-                else
-                    a0 = __builtin_fmaf(v, xs[16 * i + 4 * j + m], a0);
-            }
-        }
-    }
-    return a0 + a1;
-}
-
-__device__ __forceinline__ float nmoe_sigmoid_dev(float x) {
-    /* math.m:21-28 form: exp of a non-positive argument only */
-    if (x >= 0.0f) {
-        float z = __expf(-x);
-        return 1.0f / (1.0f + z);
-    }
-    float z = __expf(x);
-    return z / (1.0f + z);
-}
-
-__device__ __forceinline__ float nmoe_silu_dev(float x) { return x * nmoe_sigmoid_dev(x); }
-
-template <typename XT>
-__device__ __forceinline__ void nmoe_load_cols(const XT *x, int c0, int n, float *out);
-
-template <>
-__device__ __forceinline__ void nmoe_load_cols<float>(const float *x, int c0, int n, float *out) {
-    for (int c = 0; c < n; c += 4) {
-        float4 v = *(const float4 *)(x + c0 + c);
-        out[c] = v.x; out[c + 1] = v.y; out[c + 2] = v.z; out[c + 3] = v.w;
-    }
-}
-
-template <>
-__device__ __forceinline__ void nmoe_load_cols<uint16_t>(const uint16_t *x, int c0, int n, float *out) {
-    for (int c = 0; c < n; c += 8) {
-        uint4 v = *(const uint4 *)(x + c0 + c);
-        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            out[c + 2 * i] = __uint_as_float(w[i] << 16);
-            out[c + 2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
-        }
-    }
-}
+#include "nmoe_device.h"
 
 /* ----------------------------------------------------------- gate/up */
 
@@ -159,8 +68,8 @@ __global__ void __launch_bounds__(256) nmoe_gateup_kernel(const uint8_t *__restr
     for (int i = 0; i < STEPS; i++) {
         float g = __builtin_fmaf(nmoe_bf16f(gs[i]), nmoe_dot16<BITS>(gw[i], xs), nmoe_bf16f(gb[i]) * xsum);
         float u = __builtin_fmaf(nmoe_bf16f(us[i]), nmoe_dot16<BITS>(uw[i], xs), nmoe_bf16f(ub[i]) * xsum);
-        g = nmoe_group_sum<Q::LPR_G>(g);
-        u = nmoe_group_sum<Q::LPR_G>(u);
+        g = nmoe_lanes_sum<Q::LPR_G>(g);
+        u = nmoe_lanes_sum<Q::LPR_G>(u);
         if (l == 0) act[((size_t)t * NMOE_MAX_K + s) * NMOE_INTER + row0 + i * RPS] = nmoe_silu_dev(g) * u;
     }
 }
@@ -243,7 +152,7 @@ __global__ void __launch_bounds__(256) nmoe_down_combine_kernel(
                 xs[4 * c] = v.x; xs[4 * c + 1] = v.y; xs[4 * c + 2] = v.z; xs[4 * c + 3] = v.w;
             }
             float y = __builtin_fmaf(nmoe_bf16f(ds[s]), nmoe_dot16<BITS>(dw[s], xs), nmoe_bf16f(db[s]) * asum_s[s][l]);
-            y = nmoe_group_sum<Q::LPR_D>(y);
+            y = nmoe_dpp_group_sum<Q::LPR_D>(y);
             moe += wk[s] * y;
         }
     }
@@ -302,6 +211,21 @@ static int nmoe_launch_experts(nmoe_hip_ctx *ctx, const uint8_t *pack, const voi
     return NMOE_HIP_OK;
 }
 
+int nmoe_fused_decode(nmoe_hip_ctx *ctx, int bits, int route, const void *x, int x_dtype, int k,
+                      const uint16_t *router_w, const uint32_t *idx_in, const float *w_in, const float *h_mid,
+                      const float *shared_out, const float *shared_gate_raw, float *out, uint32_t *idx_out,
+                      float *w_out, float *logits, const uint8_t *pack, hipStream_t s);
+
+template <int BITS>
+static int nmoe_experts_dispatch(nmoe_hip_ctx *ctx, const uint8_t *pack, const void *x, int x_dtype, int ntok, int k,
+                                 const uint32_t *idx, const float *w, const float *h_mid, const float *shared_out,
+                                 const float *shared_gate_raw, float *out, hipStream_t s) {
+    if (ntok == 1 && ctx->fused_blocks > 0 && ctx->use_fused)
+        return nmoe_fused_decode(ctx, BITS, 0, x, x_dtype, k, NULL, idx, w, h_mid, shared_out, shared_gate_raw, out,
+                                 NULL, NULL, NULL, pack, s);
+    return nmoe_launch_experts<BITS>(ctx, pack, x, x_dtype, ntok, k, idx, w, h_mid, shared_out, shared_gate_raw, out, s);
+}
+
 extern "C" int nmoe_moe_experts_q4(nmoe_hip_ctx *ctx, int layer, const void *x, int x_dtype, int ntok, int k,
                                    const uint32_t *idx, const float *w, const float *h_mid, const float *shared_out,
                                    const float *shared_gate_raw, float *out, void *stream) {
@@ -309,8 +233,8 @@ extern "C" int nmoe_moe_experts_q4(nmoe_hip_ctx *ctx, int layer, const void *x, 
     int rc = nmoe_check_experts(ctx, layer, 4, x, x_dtype, ntok, k, idx, w, h_mid, shared_out, shared_gate_raw, out,
                                 &pack);
     if (rc != NMOE_HIP_OK) return rc;
-    return nmoe_launch_experts<4>(ctx, pack, x, x_dtype, ntok, k, idx, w, h_mid, shared_out, shared_gate_raw, out,
-                                  nmoe_stream_of(ctx, stream));
+    return nmoe_experts_dispatch<4>(ctx, pack, x, x_dtype, ntok, k, idx, w, h_mid, shared_out, shared_gate_raw, out,
+                                    nmoe_stream_of(ctx, stream));
 }
 
 extern "C" int nmoe_moe_experts_q2(nmoe_hip_ctx *ctx, int layer, const void *x, int x_dtype, int ntok, int k,
@@ -320,13 +244,8 @@ extern "C" int nmoe_moe_experts_q2(nmoe_hip_ctx *ctx, int layer, const void *x, 
     int rc = nmoe_check_experts(ctx, layer, 2, x, x_dtype, ntok, k, idx, w, h_mid, shared_out, shared_gate_raw, out,
                                 &pack);
     if (rc != NMOE_HIP_OK) return rc;
-    return nmoe_launch_experts<2>(ctx, pack, x, x_dtype, ntok, k, idx, w, h_mid, shared_out, shared_gate_raw, out,
-                                  nmoe_stream_of(ctx, stream));
-}
-
-extern "C" int nmoe_decode_init(nmoe_hip_ctx *ctx) {
-    (void)ctx;
-    return NMOE_HIP_OK;
+    return nmoe_experts_dispatch<2>(ctx, pack, x, x_dtype, ntok, k, idx, w, h_mid, shared_out, shared_gate_raw, out,
+                                    nmoe_stream_of(ctx, stream));
 }
 
 extern "C" int nmoe_moe_layer(nmoe_hip_ctx *ctx, int layer, const nmoe_hip_router *router, const void *x, int x_dtype,
@@ -342,6 +261,14 @@ extern "C" int nmoe_moe_layer(nmoe_hip_ctx *ctx, int layer, const nmoe_hip_route
         return nmoe_fail(ctx, NMOE_HIP_EINVAL, "a layer pack holds 256 experts; router has %d", router->num_experts);
     rc = nmoe_check_x(ctx, x, x_dtype, ntok);
     if (rc != NMOE_HIP_OK) return rc;
+    if (k < 1 || k > NMOE_MAX_K) return nmoe_fail(ctx, NMOE_HIP_EINVAL, "k=%d outside 1..8", k);
+    if (h_mid == NULL || out == NULL) return nmoe_fail(ctx, NMOE_HIP_EINVAL, "NULL h_mid/out");
+    if ((shared_out == NULL) != (shared_gate_raw == NULL))
+        return nmoe_fail(ctx, NMOE_HIP_EINVAL, "shared_out and shared_gate_raw must both be set or both NULL");
+    if (ntok == 1 && ctx->fused_blocks > 0 && ctx->use_fused && router->kind == NMOE_HIP_ROUTER_BF16)
+        return nmoe_fused_decode(ctx, ctx->packs[layer].bits, 1, x, x_dtype, k, router->w_bf16, NULL, NULL, h_mid,
+                                 shared_out, shared_gate_raw, out, idx, w, logits,
+                                 (const uint8_t *)ctx->packs[layer].dev, nmoe_stream_of(ctx, stream));
     uint32_t *ri = idx != NULL ? idx : ctx->idx;
     float *rw = w != NULL ? w : ctx->w;
     rc = nmoe_moe_route(ctx, router, x, x_dtype, ntok, k, ri, rw, logits, stream);

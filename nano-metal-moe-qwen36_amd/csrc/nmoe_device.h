@@ -1,0 +1,375 @@
+/*
+ * nmoe_device.h -- device building blocks shared by the decode kernels:
+ * DPP reductions, q4/q2 row dot products, the router row, bit-exact routing
+ * of one token by one wavefront, and the grid barrier of the persistent
+ * kernel.  Header-only (every .hip file is its own code object).
+ */
+#ifndef NMOE_DEVICE_H
+#define NMOE_DEVICE_H
+
+#include "nmoe_hip_internal.h"
+
+/* ---------------------------------------------------------------- DPP */
+
+/* DPP controls (gfx9): quad_perm [1,0,3,2] = lane^1, [2,3,0,1] = lane^2,
+ * row_half_mirror = 7-i within 8 lanes, row_mirror = 15-i within 16 lanes. */
+#define NMOE_DPP_XOR1 0xB1
+#define NMOE_DPP_XOR2 0x4E
+#define NMOE_DPP_HALF_MIRROR 0x141
+#define NMOE_DPP_MIRROR 0x140
+
+template <int CTRL>
+__device__ __forceinline__ uint32_t nmoe_dpp_u(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false);
+}
+
+template <int CTRL>
+__device__ __forceinline__ float nmoe_dpp_f(float v) {
+    return __uint_as_float(nmoe_dpp_u<CTRL>(__float_as_uint(v)));
+}
+
+__device__ __forceinline__ float nmoe_readlane_f(float v, int lane) {
+    return __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)__float_as_uint(v), lane));
+}
+
+/* Sum over aligned groups of W lanes (W = 4, 8, 16), every lane of a group
+ * receiving its group's sum.  The combination is the balanced pairwise tree
+ * over the group's lanes in order: (l0+l1)+(l2+l3), then quads, then octets. */
+template <int W>
+__device__ __forceinline__ float nmoe_dpp_group_sum(float v) {
+    v = v + nmoe_dpp_f<NMOE_DPP_XOR1>(v);
+    v = v + nmoe_dpp_f<NMOE_DPP_XOR2>(v);
+    if (W >= 8) v = v + nmoe_dpp_f<NMOE_DPP_HALF_MIRROR>(v);
+    if (W >= 16) v = v + nmoe_dpp_f<NMOE_DPP_MIRROR>(v);
+    return v;
+}
+
+/* Wave sum as the balanced pairwise tree over lanes 0..63 in order
+ * (rows of 16 by DPP, then (r0 + r1) + (r2 + r3)); uniform result. */
+__device__ __forceinline__ float nmoe_wave_sum_tree(float v) {
+    v = nmoe_dpp_group_sum<16>(v);
+    float r0 = nmoe_readlane_f(v, 0), r1 = nmoe_readlane_f(v, 16);
+    float r2 = nmoe_readlane_f(v, 32), r3 = nmoe_readlane_f(v, 48);
+    return (r0 + r1) + (r2 + r3);
+}
+
+/* Sum over each half wave (lanes 0-31, 32-63), same tree shape. */
+__device__ __forceinline__ float nmoe_half_sum_tree(float v) {
+    v = nmoe_dpp_group_sum<16>(v);
+    float r0 = nmoe_readlane_f(v, 0), r1 = nmoe_readlane_f(v, 16);
+    float r2 = nmoe_readlane_f(v, 32), r3 = nmoe_readlane_f(v, 48);
+    return (threadIdx.x & 32) ? (r2 + r3) : (r0 + r1);
+}
+
+/* Group sum for W in {8, 16, 32, 64} lanes (every lane of a group gets it). */
+template <int W>
+__device__ __forceinline__ float nmoe_lanes_sum(float v) {
+    if (W == 64) return nmoe_wave_sum_tree(v);
+    if (W == 32) return nmoe_half_sum_tree(v);
+    return nmoe_dpp_group_sum<W>(v);
+}
+
+__device__ __forceinline__ float nmoe_wave_max_f(float v) {
+    v = fmaxf(v, nmoe_dpp_f<NMOE_DPP_XOR1>(v));
+    v = fmaxf(v, nmoe_dpp_f<NMOE_DPP_XOR2>(v));
+    v = fmaxf(v, nmoe_dpp_f<NMOE_DPP_HALF_MIRROR>(v));
+    v = fmaxf(v, nmoe_dpp_f<NMOE_DPP_MIRROR>(v));
+    return fmaxf(fmaxf(nmoe_readlane_f(v, 0), nmoe_readlane_f(v, 16)),
+                 fmaxf(nmoe_readlane_f(v, 32), nmoe_readlane_f(v, 48)));
+}
+
+template <int CTRL>
+__device__ __forceinline__ uint64_t nmoe_dpp_u64(uint64_t v) {
+    return ((uint64_t)nmoe_dpp_u<CTRL>((uint32_t)(v >> 32)) << 32) | nmoe_dpp_u<CTRL>((uint32_t)v);
+}
+
+__device__ __forceinline__ uint64_t nmoe_readlane_u64(uint64_t v, int lane) {
+    uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, lane);
+    uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), lane);
+    return ((uint64_t)hi << 32) | lo;
+}
+
+__device__ __forceinline__ uint64_t nmoe_wave_sum_u64(uint64_t v) {
+    v += nmoe_dpp_u64<NMOE_DPP_XOR1>(v);
+    v += nmoe_dpp_u64<NMOE_DPP_XOR2>(v);
+    v += nmoe_dpp_u64<NMOE_DPP_HALF_MIRROR>(v);
+    v += nmoe_dpp_u64<NMOE_DPP_MIRROR>(v);
+    return (nmoe_readlane_u64(v, 0) + nmoe_readlane_u64(v, 16)) + (nmoe_readlane_u64(v, 32) + nmoe_readlane_u64(v, 48));
+}
+
+__device__ __forceinline__ uint64_t nmoe_max_u64(uint64_t a, uint64_t b) { return a > b ? a : b; }
+
+__device__ __forceinline__ uint64_t nmoe_wave_max_u64(uint64_t v) {
+    v = nmoe_max_u64(v, nmoe_dpp_u64<NMOE_DPP_XOR1>(v));
+    v = nmoe_max_u64(v, nmoe_dpp_u64<NMOE_DPP_XOR2>(v));
+    v = nmoe_max_u64(v, nmoe_dpp_u64<NMOE_DPP_HALF_MIRROR>(v));
+    v = nmoe_max_u64(v, nmoe_dpp_u64<NMOE_DPP_MIRROR>(v));
+    return nmoe_max_u64(nmoe_max_u64(nmoe_readlane_u64(v, 0), nmoe_readlane_u64(v, 16)),
+                        nmoe_max_u64(nmoe_readlane_u64(v, 32), nmoe_readlane_u64(v, 48)));
+}
+
+/* ------------------------------------------------------- q4 / q2 rows */
+
+template <int BITS>
+struct nmoe_q {
+    static constexpr int VPW = 32 / BITS;            /* values per word */
+    static constexpr int CPL = 4 * VPW;              /* columns per lane (one 16-byte load) */
+    static constexpr int LPR_G = NMOE_HIDDEN / CPL;  /* lanes per gate/up row: 64 / 32 */
+    static constexpr int LPR_D = NMOE_INTER / CPL;   /* lanes per down row: 16 / 8 */
+    static constexpr int WPR_G = NMOE_HIDDEN / VPW;  /* words per gate/up row */
+    static constexpr int WPR_D = NMOE_INTER / VPW;   /* words per down row */
+    static constexpr int GPR_G = NMOE_HIDDEN / NMOE_GROUP;
+    static constexpr int GPR_D = NMOE_INTER / NMOE_GROUP;
+};
+
+/* sum_j q_j * x_j over the 16 bytes `q` (column order of the pack). */
+template <int BITS>
+__device__ __forceinline__ float nmoe_dot16(uint4 q, const float *xs);
+
+template <>
+__device__ __forceinline__ float nmoe_dot16<4>(uint4 q, const float *xs) {
+    const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+    float a0 = 0.0f, a1 = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        uint32_t lo = w[i] & 0x0F0F0F0Fu;
+        uint32_t hi = (w[i] >> 4) & 0x0F0F0F0Fu;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            a0 = __builtin_fmaf((float)((lo >> (8 * j)) & 0xFFu), xs[8 * i + 2 * j], a0);
+            a1 = __builtin_fmaf((float)((hi >> (8 * j)) & 0xFFu), xs[8 * i + 2 * j + 1], a1);
+        }
+    }
+    return a0 + a1;
+}
+
+template <>
+__device__ __forceinline__ float nmoe_dot16<2>(uint4 q, const float *xs) {
+    const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+    float a0 = 0.0f, a1 = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+#pragma unroll
+        for (int m = 0; m < 4; m++) {
+            uint32_t p = (w[i] >> (2 * m)) & 0x03030303u;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                float v = (float)((p >> (8 * j)) & 0xFFu);
+                if (m & 1)
+                    a1 = __builtin_fmaf(v, xs[16 * i + 4 * j + m], a1);
+                else
+                    a0 = __builtin_fmaf(v, xs[16 * i + 4 * j + m], a0);
+            }
+        }
+    }
+    return a0 + a1;
+}
+
+__device__ __forceinline__ float nmoe_sigmoid_dev(float x) {
+    /* math.m:21-28 form: exp of a non-positive argument only */
+    if (x >= 0.0f) {
+        float z = __expf(-x);
+        return 1.0f / (1.0f + z);
+    }
+    float z = __expf(x);
+    return z / (1.0f + z);
+}
+
+__device__ __forceinline__ float nmoe_silu_dev(float x) { return x * nmoe_sigmoid_dev(x); }
+
+__device__ __forceinline__ void nmoe_unpack_bf16x8(uint4 v, float out[8]) {
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        out[2 * i] = __uint_as_float(w[i] << 16);
+        out[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+    }
+}
+
+/* n consecutive activations starting at column c0, as fp32. */
+template <typename XT>
+__device__ __forceinline__ void nmoe_load_cols(const XT *x, int c0, int n, float *out);
+
+template <>
+__device__ __forceinline__ void nmoe_load_cols<float>(const float *x, int c0, int n, float *out) {
+    for (int c = 0; c < n; c += 4) {
+        float4 v = *(const float4 *)(x + c0 + c);
+        out[c] = v.x;
+        out[c + 1] = v.y;
+        out[c + 2] = v.z;
+        out[c + 3] = v.w;
+    }
+}
+
+template <>
+__device__ __forceinline__ void nmoe_load_cols<uint16_t>(const uint16_t *x, int c0, int n, float *out) {
+    for (int c = 0; c < n; c += 8) nmoe_unpack_bf16x8(*(const uint4 *)(x + c0 + c), out + c);
+}
+
+/* ------------------------------------------------------------ router */
+
+/* Router logit of one bf16 row against x, by one wavefront: lane L owns the
+ * 16-byte chunks L, L+64, L+128, L+192 (8 columns each) and accumulates them
+ * in order with fma; the lane partials are combined by the balanced pairwise
+ * tree (nmoe_wave_sum_tree).  xs holds the lane's 32 columns of x in the
+ * same chunk order.  Uniform result. */
+__device__ __forceinline__ float nmoe_router_row_bf16(const uint4 wv[4], const float xs[32]) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        float wf[8];
+        nmoe_unpack_bf16x8(wv[j], wf);
+#pragma unroll
+        for (int i = 0; i < 8; i++) acc = __builtin_fmaf(wf[i], xs[8 * j + i], acc);
+    }
+    return nmoe_wave_sum_tree(acc);
+}
+
+/* ------------------------------------------------------------ routing */
+
+/* Key whose unsigned maximum is math.m's top-k winner: probabilities are
+ * non-negative, so their float bits order like the values; the low word is
+ * ~index so that equal probabilities rank the lower index higher. */
+__device__ __forceinline__ uint64_t nmoe_topk_key(float p, uint32_t i) {
+    return ((uint64_t)__float_as_uint(p) << 32) | (uint64_t)(0xffffffffu - i);
+}
+
+/* Routes one token with a full wavefront (math.m:67-153 bit for bit).
+ * lg: the token's logits (any memory); scratch: 256 floats of LDS for the
+ * sequential exact-sum path; tab: the exp2 table.  On return every lane
+ * holds sel_i / sel_w (slots >= n zero).  Returns n = min(k, E). */
+__device__ __forceinline__ int nmoe_wave_route(const float *lg, int num_experts, int k, float *scratch,
+                                               const uint64_t *tab, uint32_t sel_i[NMOE_MAX_K],
+                                               float sel_w[NMOE_MAX_K], float *probs) {
+    const int lane = threadIdx.x & 63;
+    float l[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        int i = lane + 64 * j;
+        l[j] = i < num_experts ? lg[i] : -__builtin_inff();
+    }
+    /* the maximum (order-free for finite logits; zeros of either sign give
+     * the same exp arguments' results) */
+    float m = nmoe_wave_max_f(fmaxf(fmaxf(l[0], l[1]), fmaxf(l[2], l[3])));
+
+    float e[4];
+    uint64_t fx = 0;
+    int ok = 1;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        int i = lane + 64 * j;
+        e[j] = i < num_experts ? nmoe_expf_glibc(l[j] - m, tab) : 0.0f;
+        uint64_t f = 0;
+        ok &= nmoe_softmax_term_fixed(e[j], &f);
+        fx += f;
+    }
+    float total;
+    if (__ballot(!ok) == 0) {
+        /* every term is a multiple of 2^-55 and the sum stays below 2^63:
+         * math.m's long double running sum was exact and equals this sum */
+        total = nmoe_u64_scaled_to_f32_rne(nmoe_wave_sum_u64(fx));
+    } else {
+        /* replay the long double running sum in index order in lane 0 */
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            int i = lane + 64 * j;
+            if (i < num_experts) scratch[i] = e[j];
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+        float t = 0.0f;
+        if (lane == 0) {
+            nmoe_x87 acc = nmoe_x87_zero();
+            for (int i = 0; i < num_experts; i++) acc = nmoe_x87_add(acc, nmoe_x87_from_float(scratch[i]));
+            t = nmoe_x87_to_float(acc);
+        }
+        total = nmoe_readlane_f(t, 0);
+        __builtin_amdgcn_wave_barrier();
+    }
+    float p[4];
+    float inv = total == 0.0f ? 0.0f : 1.0f / total;
+#pragma unroll
+    for (int j = 0; j < 4; j++) p[j] = total == 0.0f ? 1.0f / (float)num_experts : e[j] * inv;
+    if (probs != NULL) {
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            int i = lane + 64 * j;
+            if (i < num_experts) probs[i] = p[j];
+        }
+    }
+
+    int n = min(k, num_experts);
+    uint64_t key[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        uint32_t i = (uint32_t)(lane + 64 * j);
+        key[j] = i < (uint32_t)num_experts ? nmoe_topk_key(p[j], i) : 0ull;
+    }
+    float sel_v[NMOE_MAX_K];
+#pragma unroll
+    for (int s = 0; s < NMOE_MAX_K; s++) {
+        sel_i[s] = 0;
+        sel_v[s] = 0.0f;
+        if (s < n) {
+            uint64_t best = nmoe_wave_max_u64(nmoe_max_u64(nmoe_max_u64(key[0], key[1]), nmoe_max_u64(key[2], key[3])));
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                if (key[j] == best) key[j] = 0ull; /* taken */
+            sel_i[s] = 0xffffffffu - (uint32_t)best;
+            sel_v[s] = __uint_as_float((uint32_t)(best >> 32));
+        }
+    }
+    /* math.m:134-153 */
+    float sum = 0.0f;
+#pragma unroll
+    for (int s = 0; s < NMOE_MAX_K; s++)
+        if (s < n) sum += sel_v[s];
+    float rinv = sum == 0.0f ? 1.0f / (float)n : 1.0f / sum;
+#pragma unroll
+    for (int s = 0; s < NMOE_MAX_K; s++) sel_w[s] = s < n ? (sum == 0.0f ? rinv : sel_v[s] * rinv) : 0.0f;
+    return n;
+}
+
+/* ------------------------------------------------------- grid barrier */
+
+/* Bounded spin so that a grid whose blocks are not all resident still ends:
+ * the waiting block gives up, records the failure in the status word and
+ * carries on (the result is then wrong, and the host reports ETIMEDOUT). */
+#define NMOE_SPIN_LIMIT (1u << 22)
+
+/* All blocks of the grid arrive, then leave once `target` arrivals (phase
+ * number x grid size) are counted.  Release/acquire at agent scope makes the
+ * writes before the barrier visible to every block after it. */
+__device__ __forceinline__ void nmoe_grid_barrier(uint32_t *sync, uint32_t target) {
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+        __hip_atomic_fetch_add(sync + NMOE_SYNC_BARRIER, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        uint32_t spins = 0;
+        while (__hip_atomic_load(sync + NMOE_SYNC_BARRIER, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
+            __builtin_amdgcn_s_sleep(1);
+            if (++spins > NMOE_SPIN_LIMIT) {
+                __hip_atomic_store(sync + NMOE_SYNC_STATUS, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                break;
+            }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    }
+    __syncthreads();
+}
+
+/* Every block calls this once at the very end: the last block to leave
+ * resets the barrier counter for the next launch (stream order guarantees
+ * the next launch starts after this kernel has finished). */
+__device__ __forceinline__ void nmoe_grid_exit(uint32_t *sync, uint32_t nblocks) {
+    if (threadIdx.x == 0) {
+        uint32_t old = __hip_atomic_fetch_add(sync + NMOE_SYNC_EXIT, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+        if (old == nblocks - 1) {
+            __hip_atomic_store(sync + NMOE_SYNC_BARRIER, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(sync + NMOE_SYNC_EXIT, 0u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+}
+
+#endif

@@ -78,6 +78,7 @@ struct nmoe_hip_ctx {
     float *w;        /* [max_tokens][8] */
     uint32_t *sync;  /* NMOE_SYNC_WORDS */
     int fused_blocks;     /* persistent decode grid (0 = not resident-capable) */
+    int use_fused;        /* NMOE_HIP_OPT_FUSED_DECODE */
     char err[256];
 };
 
@@ -103,22 +104,6 @@ __device__ __forceinline__ float nmoe_bf16f(uint32_t h) { return __uint_as_float
 __device__ __forceinline__ uint32_t nmoe_f32_to_bf16_bits(float f) {
     uint32_t b = __float_as_uint(f);
     return (b + 0x7FFFu + ((b >> 16) & 1u)) >> 16;
-}
-
-/* xor-butterfly sum over the 64 lanes: every lane ends with the same value,
- * combined in the fixed order ((l ^ 32), (l ^ 16), ..., (l ^ 1)). */
-__device__ __forceinline__ float nmoe_wave_sum_butterfly(float v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
-    return v;
-}
-
-/* Sum over aligned groups of W lanes (W = 4..64), result in every lane. */
-template <int W>
-__device__ __forceinline__ float nmoe_group_sum(float v) {
-#pragma unroll
-    for (int off = W / 2; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
-    return v;
 }
 
 #endif

@@ -20,40 +20,19 @@
  * sequentially with an emulated 64-bit-significand adder in lane 0.
  *
  * Logits use a fixed reduction order (lane L accumulates its 16-byte chunks
- * L, L+64, ... with fma, then an xor butterfly), so identical inputs give
- * identical logits on every run.
+ * L, L+64, ... with fma; the 64 lane partials are combined by the balanced
+ * pairwise tree over lanes in order), so identical inputs give identical
+ * logits on every run, in both the standalone and the fused kernels.
  */
-#include "nmoe_hip_internal.h"
+#include "nmoe_device.h"
 
 #pragma clang fp contract(off)
 
-__constant__ uint64_t nmoe_exp2_tab[32] = NMOE_EXP2_TAB32;
+static __constant__ uint64_t nmoe_exp2_tab[32] = NMOE_EXP2_TAB32;
 
 /* ------------------------------------------------------------- logits */
 
-template <typename XT>
-__device__ __forceinline__ void nmoe_load_x8(const XT *x, int chunk, float out[8]);
-
-template <>
-__device__ __forceinline__ void nmoe_load_x8<uint16_t>(const uint16_t *x, int chunk, float out[8]) {
-    uint4 v = ((const uint4 *)x)[chunk];
-    uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        out[2 * i] = __uint_as_float(w[i] << 16);
-        out[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
-    }
-}
-
-template <>
-__device__ __forceinline__ void nmoe_load_x8<float>(const float *x, int chunk, float out[8]) {
-    float4 a = ((const float4 *)x)[2 * chunk];
-    float4 b = ((const float4 *)x)[2 * chunk + 1];
-    out[0] = a.x; out[1] = a.y; out[2] = a.z; out[3] = a.w;
-    out[4] = b.x; out[5] = b.y; out[6] = b.z; out[7] = b.w;
-}
-
-/* One wavefront computes logit e for tokens [t0, t1). */
+/* One wavefront per (row, token block): logits[t][e] for t in [t0, t1). */
 template <typename XT>
 __global__ void __launch_bounds__(64) nmoe_router_bf16_kernel(const uint16_t *__restrict__ w, const XT *__restrict__ x,
                                                               int ntok, int num_experts, int tok_per_block,
@@ -68,24 +47,17 @@ __global__ void __launch_bounds__(64) nmoe_router_bf16_kernel(const uint16_t *__
     int t1 = min(ntok, t0 + tok_per_block);
     for (int t = t0; t < t1; t++) {
         const XT *xt = x + (size_t)t * NMOE_HIDDEN;
-        float acc = 0.0f;
+        float xs[32];
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            float xv[8];
-            nmoe_load_x8<XT>(xt, lane + 64 * j, xv);
-            uint32_t ww[4] = {wv[j].x, wv[j].y, wv[j].z, wv[j].w};
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                acc = __builtin_fmaf(__uint_as_float(ww[i] << 16), xv[2 * i], acc);
-                acc = __builtin_fmaf(__uint_as_float(ww[i] & 0xffff0000u), xv[2 * i + 1], acc);
-            }
-        }
-        acc = nmoe_wave_sum_butterfly(acc);
-        if (lane == 0) logits[(size_t)t * num_experts + e] = acc;
+        for (int j = 0; j < 4; j++) nmoe_load_cols<XT>(xt, (lane + 64 * j) * 8, 8, xs + 8 * j);
+        float logit = nmoe_router_row_bf16(wv, xs);
+        if (lane == 0) logits[(size_t)t * num_experts + e] = logit;
     }
 }
 
-/* q4 router row: 256 words; lane L owns words L, L+64, L+128, L+192. */
+/* q4 router row (the reference model's router, kernels.metal:472-513):
+ * 256 words; lane L owns words L, L+64, L+128, L+192, w = fma(q, s, b),
+ * acc = fma(w, x, acc); lane partials combined by the pairwise tree. */
 template <typename XT>
 __global__ void __launch_bounds__(64) nmoe_router_q4_kernel(const uint32_t *__restrict__ w,
                                                             const uint16_t *__restrict__ sc,
@@ -111,148 +83,19 @@ __global__ void __launch_bounds__(64) nmoe_router_q4_kernel(const uint32_t *__re
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             float xv[8];
-            nmoe_load_x8<XT>(xt, lane + 64 * j, xv);
+            nmoe_load_cols<XT>(xt, (lane + 64 * j) * 8, 8, xv);
 #pragma unroll
             for (int i = 0; i < 8; i++) {
                 float q = (float)((wv[j] >> (4 * i)) & 0xFu);
                 acc = __builtin_fmaf(__builtin_fmaf(q, s[j], b[j]), xv[i], acc);
             }
         }
-        acc = nmoe_wave_sum_butterfly(acc);
+        acc = nmoe_wave_sum_tree(acc);
         if (lane == 0) logits[(size_t)t * num_experts + e] = acc;
     }
 }
 
 /* ------------------------------------------------------------ routing */
-
-__device__ __forceinline__ uint64_t nmoe_wave_sum_u64(uint64_t v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
-        uint32_t lo = __shfl_xor((uint32_t)v, off, 64);
-        uint32_t hi = __shfl_xor((uint32_t)(v >> 32), off, 64);
-        v += ((uint64_t)hi << 32) | lo;
-    }
-    return v;
-}
-
-__device__ __forceinline__ bool nmoe_better(float va, uint32_t ia, float vb, uint32_t ib) {
-    return va > vb || (va == vb && ia < ib);
-}
-
-/* Routes one token with a full wavefront.  On return every lane holds the
- * same sel_i / sel_w (slots >= n are 0).  `scratch` is 256 floats of LDS
- * (used only by the exact sequential-sum path).  Returns n = min(k, E). */
-__device__ int nmoe_wave_route(const float *__restrict__ lg, int num_experts, int k, float *scratch,
-                               uint32_t sel_i[NMOE_MAX_K], float sel_w[NMOE_MAX_K], float *__restrict__ probs) {
-    const int lane = threadIdx.x & 63;
-    float l[4];
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-        int i = lane + 64 * j;
-        l[j] = i < num_experts ? lg[i] : -__builtin_inff();
-    }
-    /* max: order-independent for finite inputs (equal zeros of either sign
-     * give identical exp arguments' results) */
-    float m = fmaxf(fmaxf(l[0], l[1]), fmaxf(l[2], l[3]));
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
-
-    float e[4];
-    uint64_t fx = 0;
-    int ok = 1;
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-        int i = lane + 64 * j;
-        e[j] = i < num_experts ? nmoe_expf_glibc(l[j] - m, nmoe_exp2_tab) : 0.0f;
-        uint64_t f = 0;
-        ok &= nmoe_softmax_term_fixed(e[j], &f);
-        fx += f;
-    }
-    float total;
-    if (__ballot(!ok) == 0) {
-        /* every term is a multiple of 2^-55 and the sum < 2^63: the x87
-         * running sum was exact, so it equals this integer sum */
-        total = nmoe_u64_scaled_to_f32_rne(nmoe_wave_sum_u64(fx));
-    } else {
-        /* replay math.m's long double running sum in index order */
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            int i = lane + 64 * j;
-            if (i < num_experts) scratch[i] = e[j];
-        }
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-        float t = 0.0f;
-        if (lane == 0) {
-            nmoe_x87 acc = nmoe_x87_zero();
-            for (int i = 0; i < num_experts; i++) acc = nmoe_x87_add(acc, nmoe_x87_from_float(scratch[i]));
-            t = nmoe_x87_to_float(acc);
-        }
-        total = __shfl(t, 0, 64);
-        __builtin_amdgcn_wave_barrier();
-    }
-    float p[4];
-    if (total == 0.0f) {
-        float u = 1.0f / (float)num_experts;
-#pragma unroll
-        for (int j = 0; j < 4; j++) p[j] = u;
-    } else {
-        float inv = 1.0f / total;
-#pragma unroll
-        for (int j = 0; j < 4; j++) p[j] = e[j] * inv;
-    }
-    if (probs != NULL) {
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            int i = lane + 64 * j;
-            if (i < num_experts) probs[i] = p[j];
-        }
-    }
-
-    int n = min(k, num_experts);
-    uint32_t taken = 0;
-    float sel_v[NMOE_MAX_K];
-#pragma unroll
-    for (int s = 0; s < NMOE_MAX_K; s++) {
-        sel_i[s] = 0;
-        sel_v[s] = 0.0f;
-    }
-#pragma unroll
-    for (int s = 0; s < NMOE_MAX_K; s++) {
-        if (s >= n) break;
-        float bv = -__builtin_inff();
-        uint32_t bi = 0xffffffffu;
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            uint32_t i = (uint32_t)(lane + 64 * j);
-            if (i < (uint32_t)num_experts && !((taken >> j) & 1u) && nmoe_better(p[j], i, bv, bi)) {
-                bv = p[j];
-                bi = i;
-            }
-        }
-#pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) {
-            float ov = __shfl_xor(bv, off, 64);
-            uint32_t oi = __shfl_xor(bi, off, 64);
-            if (nmoe_better(ov, oi, bv, bi)) {
-                bv = ov;
-                bi = oi;
-            }
-        }
-        if ((bi & 63u) == (uint32_t)lane) taken |= 1u << (bi >> 6);
-        sel_i[s] = bi;
-        sel_v[s] = bv;
-    }
-    /* math.m:134-153 */
-    float sum = 0.0f;
-#pragma unroll
-    for (int s = 0; s < NMOE_MAX_K; s++)
-        if (s < n) sum += sel_v[s];
-    float inv = sum == 0.0f ? 1.0f / (float)n : 1.0f / sum;
-#pragma unroll
-    for (int s = 0; s < NMOE_MAX_K; s++) sel_w[s] = s < n ? (sum == 0.0f ? inv : sel_v[s] * inv) : 0.0f;
-    return n;
-}
 
 __global__ void __launch_bounds__(64) nmoe_topk_kernel(const float *__restrict__ logits, int ntok, int num_experts,
                                                        int k, uint32_t *__restrict__ idx, float *__restrict__ w,
@@ -262,7 +105,7 @@ __global__ void __launch_bounds__(64) nmoe_topk_kernel(const float *__restrict__
     if (t >= ntok) return;
     uint32_t si[NMOE_MAX_K];
     float sw[NMOE_MAX_K];
-    nmoe_wave_route(logits + (size_t)t * num_experts, num_experts, k, scratch, si, sw,
+    nmoe_wave_route(logits + (size_t)t * num_experts, num_experts, k, scratch, nmoe_exp2_tab, si, sw,
                     probs != NULL ? probs + (size_t)t * num_experts : NULL);
     int lane = threadIdx.x;
     if (lane < NMOE_MAX_K) {

@@ -40,6 +40,7 @@ ENOENT = -2
 EIO = -5
 EHIP = -71
 ETIMEDOUT = -110
+OPT_FUSED_DECODE = 1
 
 # q4 / q2 component offsets (scripts/convert_qwen36.py:38-64)
 OFFSETS = {
@@ -79,6 +80,7 @@ _SIGS = {
     "nmoe_hip_synchronize": (_I, [_P]),
     "nmoe_hip_device_cus": (_I, [_P]),
     "nmoe_hip_check_device_status": (_I, [_P]),
+    "nmoe_hip_set_option": (_I, [_P, _I, _I]),
     "nmoe_hip_register_state_buffer": (_I, [_P, C.c_char_p, C.c_size_t, C.POINTER(_P)]),
     "nmoe_hip_register_shared_buffer": (_I, [_P, C.c_char_p, _P, C.c_size_t, C.POINTER(_P)]),
     "nmoe_hip_lookup_buffer": (_P, [_P, C.c_char_p]),
@@ -198,6 +200,9 @@ class Context:
 
     def sync(self):
         self._check(lib().nmoe_hip_synchronize(self.h))
+
+    def set_fused(self, on: bool):
+        self._check(lib().nmoe_hip_set_option(self.h, OPT_FUSED_DECODE, int(bool(on))))
 
     def device_status(self) -> int:
         return lib().nmoe_hip_check_device_status(self.h)

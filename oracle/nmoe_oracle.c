@@ -264,12 +264,11 @@ float orc_expf_restated(float x) {
 
 /* ------------------------------------------------------- router logits */
 
-static float orc_butterfly64(float p[64]) {
-    for (int off = 32; off >= 1; off >>= 1) {
-        float q[64];
-        for (int l = 0; l < 64; l++) q[l] = p[l] + p[l ^ off];
-        memcpy(p, q, sizeof(q));
-    }
+/* Balanced pairwise tree over the 64 lane partials in lane order:
+ * (p0+p1)+(p2+p3), ..., the combination the GPU's DPP reduction performs. */
+static float orc_tree64(float p[64]) {
+    for (int n = 64; n > 1; n >>= 1)
+        for (int i = 0; i < n / 2; i++) p[i] = p[2 * i] + p[2 * i + 1];
     return p[0];
 }
 
@@ -284,7 +283,7 @@ void orc_router_logits_bf16(const uint16_t *w, const float *x, int num_experts, 
                 for (int j = 0; j < 8; j++) acc = fmaf(orc_bf16_to_f32(row[c * 8 + j]), x[c * 8 + j], acc);
             p[l] = acc;
         }
-        out[e] = orc_butterfly64(p);
+        out[e] = orc_tree64(p);
     }
 }
 
@@ -308,7 +307,7 @@ void orc_router_logits_q4(const uint32_t *w, const uint16_t *scales, const uint1
             }
             p[l] = acc;
         }
-        out[e] = orc_butterfly64(p);
+        out[e] = orc_tree64(p);
     }
 }
 

@@ -75,8 +75,8 @@ float orc_expf_restated(float x);
 
 /* Router logits, mirroring the GPU's fixed reduction order: lane L of a
  * 64-lane wave owns the 16-byte chunks L, L+64, L+128, ... of a row and
- * accumulates them sequentially with fmaf; the 64 partials are combined with
- * an xor butterfly (offsets 32,16,8,4,2,1). */
+ * accumulates them sequentially with fmaf; the 64 partials are combined by
+ * the balanced pairwise tree over lanes in order ((p0+p1)+(p2+p3), ...). */
 void orc_router_logits_bf16(const uint16_t *w, const float *x, int num_experts, int hidden, float *out);
 void orc_router_logits_q4(const uint32_t *w, const uint16_t *scales, const uint16_t *biases, const float *x,
                           int num_experts, int hidden, float *out);

@@ -184,10 +184,14 @@ def test_experts_against_oracle(ctx, nh, bits, ntok, k):
     pack = host_pack(bits, seed, layer, idx[:, :k].ravel())
     want = B.moe_experts(pack, bits, x, k, idx, w, h)
     d_idx, d_w, d_h, out = ctx.to_device(idx), ctx.to_device(w), ctx.to_device(h), ctx.alloc(ntok * 2048 * 4)
-    for arr, dt in ((xb, nh.BF16), (x, nh.F32)):
-        ctx._check(ctx.experts(bits, layer, ctx.to_device(arr), dt, ntok, k, d_idx, d_w, d_h, out))
-        got = out.download(np.float32, (ntok, 2048))
-        assert_close(got, want, what=f"q{bits} ntok={ntok} k={k} dt={dt}")
+    for fused in (True, False):
+        ctx.set_fused(fused)
+        for arr, dt in ((xb, nh.BF16), (x, nh.F32)):
+            ctx._check(ctx.experts(bits, layer, ctx.to_device(arr), dt, ntok, k, d_idx, d_w, d_h, out))
+            got = out.download(np.float32, (ntok, 2048))
+            assert_close(got, want, what=f"q{bits} ntok={ntok} k={k} dt={dt} fused={fused}")
+    ctx.set_fused(True)
+    assert ctx.device_status() == nh.OK
     # shared-expert term, updated in place on the residual (out aliases h_mid)
     sh = rng.standard_normal((ntok, 2048)).astype(np.float32)
     g = rng.standard_normal(ntok).astype(np.float32)
@@ -212,12 +216,17 @@ def test_layer_matches_math_m_golden(ctx, nh, golden, name, bits, k):
     hb = ctx.alloc(2048 * 2)
     ctx.synth_bf16(hb, 2048, seed, 0, 18, 1.0)
     h = ctx.to_device(B.bf16_to_f32(hb.download(np.uint16, 2048)))
-    out, idx, w, lg = ctx.alloc(2048 * 4), ctx.alloc(32), ctx.alloc(32), ctx.alloc(1024)
-    ctx._check(ctx.moe_layer(layer, ctx.router_bf16(router), x, nh.BF16, 1, k, h, out, idx, w, lg))
-    np.testing.assert_array_equal(lg.download(np.float32, 256).view(np.uint32), golden[f"{name}_logits"].view(np.uint32))
-    np.testing.assert_array_equal(idx.download(np.uint32, 8), golden[f"{name}_idx"])
-    np.testing.assert_array_equal(w.download(np.float32, 8).view(np.uint32), golden[f"{name}_w"].view(np.uint32))
-    assert_close(out.download(np.float32, 2048), golden[f"{name}_out"], what=name)
+    for fused in (True, False):
+        ctx.set_fused(fused)
+        out, idx, w, lg = ctx.alloc(2048 * 4), ctx.alloc(32), ctx.alloc(32), ctx.alloc(1024)
+        ctx._check(ctx.moe_layer(layer, ctx.router_bf16(router), x, nh.BF16, 1, k, h, out, idx, w, lg))
+        np.testing.assert_array_equal(lg.download(np.float32, 256).view(np.uint32),
+                                      golden[f"{name}_logits"].view(np.uint32))
+        np.testing.assert_array_equal(idx.download(np.uint32, 8), golden[f"{name}_idx"])
+        np.testing.assert_array_equal(w.download(np.float32, 8).view(np.uint32), golden[f"{name}_w"].view(np.uint32))
+        assert_close(out.download(np.float32, 2048), golden[f"{name}_out"], what=f"{name} fused={fused}")
+    ctx.set_fused(True)
+    assert ctx.device_status() == nh.OK
 
 
 @pytest.mark.parametrize("bits", [4, 2])
@@ -240,3 +249,34 @@ def test_layer_multi_token_against_oracle(ctx, nh, bits):
     np.testing.assert_array_equal(idx.download(np.uint32, (ntok, 8)), idx_o)
     np.testing.assert_array_equal(w.download(np.float32, (ntok, 8)).view(np.uint32), w_o.view(np.uint32))
     assert_close(out.download(np.float32, (ntok, 2048)), want, what=f"layer q{bits}")
+
+
+@pytest.mark.parametrize("bits", [4, 2])
+def test_fused_repeated_launches(ctx, nh, bits):
+    """Many back-to-back persistent launches over several layers and inputs:
+    the grid barrier counters must reset between launches, and every step
+    must match the oracle (routing bit-exact)."""
+    rng = np.random.default_rng(40 + bits)
+    seed, k, nl, steps = 3, 8, 4, 64
+    layers = [40 + 4 * (bits == 2) + i for i in range(nl)]
+    for i, layer in enumerate(layers):
+        ctx.synth_layer(layer, bits, seed, SIGMA[bits])
+    W = [B.syn_bf16(256 * 2048, seed, layer, 16, 0.02).reshape(256, 2048) for layer in layers]
+    dW = [ctx.to_device(w) for w in W]
+    xb = B.f32_to_bf16(rng.standard_normal((steps, 2048)).astype(np.float32))
+    h = rng.standard_normal((steps, 2048)).astype(np.float32)
+    dx, dh = ctx.to_device(xb), ctx.to_device(h)
+    out, idx, w = ctx.alloc(steps * 8192), ctx.alloc(steps * 32), ctx.alloc(steps * 32)
+    for i in range(steps):
+        ctx._check(ctx.moe_layer(layers[i % nl], ctx.router_bf16(dW[i % nl]), dx.ptr + i * 4096, nh.BF16, 1, k,
+                                 dh.ptr + i * 8192, out.ptr + i * 8192, idx.ptr + i * 32, w.ptr + i * 32))
+    assert ctx.device_status() == nh.OK
+    go, gi, gw = out.download(np.float32, (steps, 2048)), idx.download(np.uint32, (steps, 8)), w.download(np.float32, (steps, 8))
+    x = B.bf16_to_f32(xb).reshape(steps, 2048)
+    for i in range(0, steps, 9):
+        l = i % nl
+        oi, ow, _ = B.route(B.router_logits_bf16(W[l], x[i]), k)
+        np.testing.assert_array_equal(gi[i], oi)
+        np.testing.assert_array_equal(gw[i].view(np.uint32), ow.view(np.uint32))
+        want = B.moe_experts(host_pack(bits, seed, layers[l], oi[:k]), bits, x[i:i + 1], k, oi[None], ow[None], h[i:i + 1])
+        assert_close(go[i], want[0], what=f"step {i}")
