@@ -171,6 +171,24 @@ NMOE_HIP_API int nmoe_moe_layer(nmoe_hip_ctx *ctx, int layer, const nmoe_hip_rou
                    int ntok, int k, const float *h_mid, const float *shared_out, const float *shared_gate_raw,
                    float *out, uint32_t *idx, float *w, float *logits, void *stream);
 
+/* ---- the per-layer call with the layer's input RMSNorm in front
+ * (math.m:34-65, unit weight, bit-exact), the way the reference runs the next
+ * layer's input norm right after the combine (runtime.m:2893-2900):
+ *   h_out = h_in + MoE(RMSNorm(h_in)).
+ * One token, bf16 router; h_out must not alias h_in. */
+NMOE_HIP_API int nmoe_moe_layer_rmsnorm(nmoe_hip_ctx *ctx, int layer, const nmoe_hip_router *router,
+                                        const float *h_in, float eps, int k, float *h_out, uint32_t *idx, float *w,
+                                        float *logits, void *stream);
+
+/* ---- the routed-expert stack of one decode token (the layer loop of
+ * NMOEProcessToken, runtime.m:3732-3777, restricted to the MoE tails):
+ * h_seq[l+1] = h_seq[l] + MoE_l(RMSNorm(h_seq[l])) for l < nlayers.
+ * layers[l]: resident pack of layer l; routers[l]: its bf16 router.
+ * h_seq: fp32 [nlayers+1][2048] (row 0 = input); idx_seq / w_seq: nullable
+ * [nlayers][8]. */
+NMOE_HIP_API int nmoe_moe_stack(nmoe_hip_ctx *ctx, int nlayers, const int *layers, const nmoe_hip_router *routers,
+                                int k, float eps, float *h_seq, uint32_t *idx_seq, float *w_seq, void *stream);
+
 /* ---- bit-exact dequant probe (kernels.metal:1066-1106 nmoe_dequant_row_q4/q2,
  * math.m:206-234): out[r][c] = q*scale + bias for `rows` rows of `in_dim`. */
 NMOE_HIP_API int nmoe_dequant_rows(nmoe_hip_ctx *ctx, int bits, const uint32_t *packed, const uint16_t *scales,

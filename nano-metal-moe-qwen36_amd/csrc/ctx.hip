@@ -85,6 +85,7 @@ extern "C" void nmoe_hip_destroy(nmoe_hip_ctx *ctx) {
     hipFree(ctx->idx);
     hipFree(ctx->w);
     hipFree(ctx->sync);
+    hipFree(ctx->xch);
     if (ctx->stream != NULL) hipStreamDestroy(ctx->stream);
     free(ctx);
 }

@@ -211,18 +211,19 @@ static int nmoe_launch_experts(nmoe_hip_ctx *ctx, const uint8_t *pack, const voi
     return NMOE_HIP_OK;
 }
 
-int nmoe_fused_decode(nmoe_hip_ctx *ctx, int bits, int route, const void *x, int x_dtype, int k,
-                      const uint16_t *router_w, const uint32_t *idx_in, const float *w_in, const float *h_mid,
-                      const float *shared_out, const float *shared_gate_raw, float *out, uint32_t *idx_out,
-                      float *w_out, float *logits, const uint8_t *pack, hipStream_t s);
+extern "C" int nmoe_fused_decode(nmoe_hip_ctx *ctx, int bits, int route, const void *x, int xmode, float eps, int k,
+                                 const uint16_t *router_w, const uint32_t *idx_in, const float *w_in,
+                                 const float *h_mid, const float *shared_out, const float *shared_gate_raw, float *out,
+                                 uint32_t *idx_out, float *w_out, float *logits_out, const uint8_t *pack,
+                                 hipStream_t s);
 
 template <int BITS>
 static int nmoe_experts_dispatch(nmoe_hip_ctx *ctx, const uint8_t *pack, const void *x, int x_dtype, int ntok, int k,
                                  const uint32_t *idx, const float *w, const float *h_mid, const float *shared_out,
                                  const float *shared_gate_raw, float *out, hipStream_t s) {
     if (ntok == 1 && ctx->fused_blocks > 0 && ctx->use_fused)
-        return nmoe_fused_decode(ctx, BITS, 0, x, x_dtype, k, NULL, idx, w, h_mid, shared_out, shared_gate_raw, out,
-                                 NULL, NULL, NULL, pack, s);
+        return nmoe_fused_decode(ctx, BITS, 0, x, x_dtype, 0.0f, k, NULL, idx, w, h_mid, shared_out, shared_gate_raw,
+                                 out, NULL, NULL, NULL, pack, s);
     return nmoe_launch_experts<BITS>(ctx, pack, x, x_dtype, ntok, k, idx, w, h_mid, shared_out, shared_gate_raw, out, s);
 }
 
@@ -266,8 +267,8 @@ extern "C" int nmoe_moe_layer(nmoe_hip_ctx *ctx, int layer, const nmoe_hip_route
     if ((shared_out == NULL) != (shared_gate_raw == NULL))
         return nmoe_fail(ctx, NMOE_HIP_EINVAL, "shared_out and shared_gate_raw must both be set or both NULL");
     if (ntok == 1 && ctx->fused_blocks > 0 && ctx->use_fused && router->kind == NMOE_HIP_ROUTER_BF16)
-        return nmoe_fused_decode(ctx, ctx->packs[layer].bits, 1, x, x_dtype, k, router->w_bf16, NULL, NULL, h_mid,
-                                 shared_out, shared_gate_raw, out, idx, w, logits,
+        return nmoe_fused_decode(ctx, ctx->packs[layer].bits, 1, x, x_dtype, 0.0f, k, router->w_bf16, NULL, NULL,
+                                 h_mid, shared_out, shared_gate_raw, out, idx, w, logits,
                                  (const uint8_t *)ctx->packs[layer].dev, nmoe_stream_of(ctx, stream));
     uint32_t *ri = idx != NULL ? idx : ctx->idx;
     float *rw = w != NULL ? w : ctx->w;
@@ -278,4 +279,25 @@ extern "C" int nmoe_moe_layer(nmoe_hip_ctx *ctx, int layer, const nmoe_hip_route
                                    stream);
     return nmoe_moe_experts_q2(ctx, layer, x, x_dtype, ntok, k, ri, rw, h_mid, shared_out, shared_gate_raw, out,
                                stream);
+}
+
+extern "C" int nmoe_moe_layer_rmsnorm(nmoe_hip_ctx *ctx, int layer, const nmoe_hip_router *router,
+                                      const float *h_in, float eps, int k, float *h_out, uint32_t *idx, float *w,
+                                      float *logits, void *stream) {
+    if (ctx == NULL) return NMOE_HIP_EINVAL;
+    if (layer < 0 || layer >= NMOE_HIP_MAX_LAYERS || ctx->packs[layer].dev == NULL)
+        return nmoe_fail(ctx, NMOE_HIP_ENOENT, "layer %d has no resident pack", layer);
+    int rc = nmoe_check_router(ctx, router);
+    if (rc != NMOE_HIP_OK) return rc;
+    if (router->kind != NMOE_HIP_ROUTER_BF16 || router->num_experts != NMOE_EXPERTS)
+        return nmoe_fail(ctx, NMOE_HIP_EINVAL, "nmoe_moe_layer_rmsnorm needs a bf16 router of 256 experts");
+    if (k < 1 || k > NMOE_MAX_K) return nmoe_fail(ctx, NMOE_HIP_EINVAL, "k=%d outside 1..8", k);
+    if (h_in == NULL || h_out == NULL || !nmoe_aligned(h_in, 16) || !nmoe_aligned(h_out, 4))
+        return nmoe_fail(ctx, NMOE_HIP_EINVAL, "h_in (16-byte aligned) and h_out are required");
+    if (h_in == h_out) return nmoe_fail(ctx, NMOE_HIP_EINVAL, "h_out must not alias h_in");
+    if (ctx->fused_blocks == 0)
+        return nmoe_fail(ctx, NMOE_HIP_EINVAL, "the device cannot hold the 256-block fused grid");
+    return nmoe_fused_decode(ctx, ctx->packs[layer].bits, 1, h_in, 2 /* XNORM */, eps, k, router->w_bf16, NULL, NULL,
+                             h_in, NULL, NULL, h_out, idx, w, logits, (const uint8_t *)ctx->packs[layer].dev,
+                             nmoe_stream_of(ctx, stream));
 }

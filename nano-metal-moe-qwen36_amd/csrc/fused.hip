@@ -1,33 +1,41 @@
 /*
- * fused.hip -- the whole batch-1 routed-MoE step in one persistent launch.
+ * fused.hip -- the whole batch-1 routed-MoE step in one launch.
  *
  * Reference: the per-layer MoE tail NMOEPipelinedExpertTail
- * (src/runtime.m:2908-2999) runs router logits on the GPU
+ * (src/runtime.m:2908-2999) computes router logits on the GPU
  * (kernels.metal:472-513), routes on the host (runtime.m:1498-1511, math.m),
  * preads the K selected experts, then runs gate/up + SwiGLU
- * (kernels.metal:562-640) and down + weighted combine (kernels.metal:
- * 1456-1542) -- three host/device crossings per layer.  Here the layer pack
- * is resident in HBM and the step is one cooperative kernel of 256 blocks x
- * 4 wavefronts with two grid barriers:
+ * (kernels.metal:562-640), down + weighted combine (kernels.metal:1456-1542)
+ * and the next layer's input RMSNorm (runtime.m:2893-2900) -- three
+ * host/device crossings per layer.  Here the layer pack is resident in HBM
+ * and the step is one launch of 256 blocks x 4 wavefronts.
  *
- *   R  router: wave 0 of block b computes logit b (1 MB bf16 router read
- *      once across the grid), writes it to global scratch.      -- barrier 1
- *   T  every block routes the token itself from the 256 logits (bit-exact
- *      math.m softmax / top-k / renormalise in one wavefront), so no second
- *      barrier is needed to publish the routing.
- *   P  every wavefront issues all of its weight loads at once: its gate/up
- *      rows (K x 512 rows spread over the grid's 1024 wavefronts) AND the
- *      down rows it will need after the next barrier (block b owns output
- *      rows 8b..8b+7 of all K experts), so the down stream overlaps the
- *      gate/up stream: ~14 MB in flight in one wave of requests.
- *   G  gate/up dot products + SwiGLU -> act[K][512] in global scratch.
- *                                                             -- barrier 2
- *   D  down dot products from the prefetched registers against act, then
- *      out = h_mid + sum_s w_s y_s (+ sigmoid(g) shared), slot order.
+ * Blocks form 8 groups of 32 (group g = block % 8, j = block / 8); group g
+ * streams expert slot g, so its barriers involve 32 blocks only (a counter
+ * shared by all 256 blocks serialises 256 same-address atomics, ~3.7 us on
+ * MI355X; 32 arrivals cost ~0.8 us).
  *
- * Without routing (routing given), R and T are skipped and there is one
- * barrier.  The grid is launched cooperatively, so all 256 blocks are
- * co-resident; every wait is bounded (nmoe_grid_barrier).
+ *   N  (stack variant) every block derives x = RMSNorm(h) itself, bit-exact
+ *      with math.m:34-65.
+ *   R  group g computes all 256 logits (block j: rows 8j..8j+7; the router
+ *      is re-read by the 8 groups, mostly from the last-level cache) and
+ *      exchanges them inside the group.                    -- group barrier
+ *   T  every block routes the token (bit-exact math.m softmax / top-k /
+ *      renormalise in one wavefront).
+ *   P  block j of group g issues all weight loads of slot g at once: gate/up
+ *      rows 16j..16j+15 and down rows 64j..64j+63 (~55 KB per block, the
+ *      whole 14 MB of expert weights in flight across the grid).
+ *   G  gate/up dot products + SwiGLU -> act[g][512].        -- group barrier
+ *   D  y_g = down_g . act[g] for rows 64j..64j+63 -> ypart[g].
+ *   C  per 64-row chunk, a counter counts the K slots; the block that
+ *      arrives last combines out = h_mid + sum_s w_s y_s (+ sigmoid(g) *
+ *      shared) in slot order, deterministic, with no global barrier.
+ *
+ * Exchanged values use device-coherent (sc1) loads/stores and the counters
+ * device-scope atomics.  Group counters grow by exactly 64 per launch (two
+ * barriers x 32 blocks; a launch without routing adds its first 32 without
+ * waiting), so a block derives this launch's targets from the counter value
+ * it reads at start and nothing needs resetting.  Every wait is bounded.
  */
 #include "nmoe_device.h"
 
@@ -36,69 +44,128 @@
 static __constant__ uint64_t nmoe_fused_exp2_tab[32] = NMOE_EXP2_TAB32;
 
 #define NMOE_FUSED_BLOCKS 256
-#define NMOE_FUSED_WAVES 4
-#define NMOE_FUSED_MAXS 4 /* weight-load steps per wavefront and phase */
-#define NMOE_FUSED_OUT_ROWS (NMOE_HIDDEN / NMOE_FUSED_BLOCKS) /* 8 output rows per block */
+#define NMOE_FUSED_GROUPS 8
+#define NMOE_FUSED_GROUP_BLOCKS (NMOE_FUSED_BLOCKS / NMOE_FUSED_GROUPS) /* 32 */
+#define NMOE_FUSED_CHUNK (NMOE_HIDDEN / NMOE_FUSED_GROUP_BLOCKS)         /* 64 output rows per block */
+#define NMOE_FUSED_GU_ROWS (NMOE_INTER / NMOE_FUSED_GROUP_BLOCKS)        /* 16 gate/up rows per block */
+
+/* sync word layout (uint32 words, counters on separate 128-byte lines) */
+#define NMOE_SYNC_GROUP(g) (32 + 32 * (g))
+#define NMOE_SYNC_CHUNK(c) (32 * (NMOE_FUSED_GROUPS + 1) + 32 * (c))
+
+/* exchange scratch layout (floats) */
+#define NMOE_XCH_LOGITS 0
+#define NMOE_XCH_ACT (NMOE_FUSED_GROUPS * NMOE_EXPERTS)
+#define NMOE_XCH_YPART (NMOE_XCH_ACT + NMOE_FUSED_GROUPS * NMOE_INTER)
+
+/* x sources: XF32 / XBF16 = activations given; XNORM = x is RMSNorm(h). */
+#define NMOE_XF32 0
+#define NMOE_XBF16 1
+#define NMOE_XNORM 2
 
 struct nmoe_fused_args {
     const uint8_t *pack;
-    const uint16_t *router_w; /* bf16 [256][2048] (ROUTE) */
-    const void *x;            /* [2048] fp32 or bf16 */
+    const uint16_t *router_w; /* bf16 [256][2048] (routing) */
+    const void *x;            /* [2048]: fp32 x, bf16 x, or fp32 h (XNORM) */
+    float eps;                /* XNORM */
     int k;
-    const uint32_t *idx_in; /* [8] (!ROUTE) */
-    const float *w_in;      /* [8] (!ROUTE) */
-    const float *h_mid;
+    const uint32_t *idx_in; /* [8] (routing given) */
+    const float *w_in;
+    const float *h_mid; /* residual in */
     const float *shared_out;
     const float *shared_gate_raw;
-    float *out;
-    uint32_t *idx_out; /* nullable (ROUTE) */
-    float *w_out;      /* nullable (ROUTE) */
-    float *logits;     /* [256] global scratch / output (ROUTE) */
-    float *act;        /* [8][512] global scratch */
+    float *out; /* residual out (may alias h_mid unless XNORM) */
+    uint32_t *idx_out;
+    float *w_out;
+    float *logits_out;
+    float *xch;
     uint32_t *sync;
 };
 
-template <int BITS, bool ROUTE, typename XT>
+/* The lane's n activations at columns c0.. (fp32, bf16, or normalised h).
+ * Normalised: math.m:63 computes (input / rms) * 1.0f.  With rinv the double
+ * reciprocal of rms, (float)(h * rinv) is that correctly rounded quotient:
+ * its error before the final rounding is below 2^-51 relative, while a
+ * quotient of two floats never lies within 2^-49 of a float rounding
+ * midpoint (nor exactly on one). */
+template <int XMODE>
+__device__ __forceinline__ void nmoe_x_cols(const void *x, int c0, int n, double rinv, float *out) {
+    if (XMODE == NMOE_XBF16) {
+        nmoe_load_cols<uint16_t>((const uint16_t *)x, c0, n, out);
+    } else {
+        nmoe_load_cols<float>((const float *)x, c0, n, out);
+        if (XMODE == NMOE_XNORM)
+            for (int i = 0; i < n; i++) out[i] = (float)((double)out[i] * rinv);
+    }
+}
+
+template <int BITS, bool ROUTE, int XMODE>
 __global__ void __launch_bounds__(256) nmoe_fused_decode_kernel(nmoe_fused_args a) {
     using Q = nmoe_q<BITS>;
     using L = nmoe_layout<BITS>;
-    constexpr int RPS = NMOE_WAVE / Q::LPR_G; /* gate/up rows per wave step: 1 (q4) / 2 (q2) */
+    constexpr int RPS = NMOE_WAVE / Q::LPR_G;   /* gate/up rows per wave step: 1 (q4) / 2 (q2) */
+    constexpr int GSTEPS = 4 / RPS;             /* 4 gate/up rows per wavefront */
     constexpr int RPW_D = NMOE_WAVE / Q::LPR_D; /* down rows per wave step: 4 (q4) / 8 (q2) */
-    constexpr int DSTEPS_PER_EXPERT = NMOE_FUSED_OUT_ROWS / RPW_D; /* 2 (q4) / 1 (q2) */
-    __shared__ float route_scratch[NMOE_EXPERTS];
+    constexpr int DSTEPS = 16 / RPW_D;          /* 16 down rows per wavefront */
+    __shared__ uint64_t s_tab[32];
+    __shared__ float s_lg[NMOE_EXPERTS];
+    __shared__ float s_scratch[NMOE_EXPERTS];
+    __shared__ float s_act[NMOE_INTER];
+    __shared__ float s_y[NMOE_FUSED_CHUNK];
     __shared__ uint32_t s_idx[NMOE_MAX_K];
     __shared__ float s_w[NMOE_MAX_K];
-    __shared__ float s_y[NMOE_MAX_K][NMOE_FUSED_OUT_ROWS];
+    __shared__ double s_dd[8];
+    __shared__ float s_f[2];
+    __shared__ float s_h[XMODE == NMOE_XNORM ? NMOE_HIDDEN : 1];
 
-    const int nb = gridDim.x;
-    const int b = blockIdx.x;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int g = blockIdx.x % NMOE_FUSED_GROUPS, j = blockIdx.x / NMOE_FUSED_GROUPS;
     const int k = a.k;
-    const XT *x = (const XT *)a.x;
-    uint32_t phase_target = 0;
+    uint32_t *gcnt = a.sync + NMOE_SYNC_GROUP(g);
+    uint32_t *status = a.sync + NMOE_SYNC_STATUS;
+    float *xlg = a.xch + NMOE_XCH_LOGITS + g * NMOE_EXPERTS;
+
+    uint32_t base = 0;
+    if (tid == 0) base = nmoe_ld_u32_dev(gcnt) & ~63u;
+    if (tid < 32) s_tab[tid] = nmoe_fused_exp2_tab[tid];
+    /* residual rows of this block's chunk, needed if it ends up combining */
+    float hm = 0.0f, sh = 0.0f;
+    if (tid < NMOE_FUSED_CHUNK) {
+        hm = a.h_mid[j * NMOE_FUSED_CHUNK + tid];
+        if (a.shared_out != NULL) sh = a.shared_out[j * NMOE_FUSED_CHUNK + tid];
+    }
+    double rinv = 1.0;
+    if (XMODE == NMOE_XNORM) rinv = 1.0 / (double)nmoe_block_rms_exact((const float *)a.x, a.eps, s_h, s_dd, s_f);
 
     if (ROUTE) {
-        /* ---- R: router rows, one per block (wave 0) */
-        if (wave == 0) {
-            for (int e = b; e < NMOE_EXPERTS; e += nb) {
-                const uint4 *row = (const uint4 *)(a.router_w + (size_t)e * NMOE_HIDDEN);
-                uint4 wv[4];
-                float xs[32];
+        /* ---- R: rows 8j + 2*wave + {0, 1} of the router, in group g */
+        const int e0 = NMOE_FUSED_GROUP_BLOCKS / 4 * j + 2 * wave; /* 8j + 2*wave */
+        uint4 wv[2][4];
 #pragma unroll
-                for (int j = 0; j < 4; j++) wv[j] = row[lane + 64 * j];
+        for (int r = 0; r < 2; r++) {
+            const uint4 *row = (const uint4 *)(a.router_w + (size_t)(e0 + r) * NMOE_HIDDEN);
 #pragma unroll
-                for (int j = 0; j < 4; j++) nmoe_load_cols<XT>(x, (lane + 64 * j) * 8, 8, xs + 8 * j);
-                float logit = nmoe_router_row_bf16(wv, xs);
-                if (lane == 0) a.logits[e] = logit;
-            }
+            for (int q = 0; q < 4; q++) wv[r][q] = row[lane + 64 * q];
         }
-        phase_target += (uint32_t)nb;
-        nmoe_grid_barrier(a.sync, phase_target);
-        /* ---- T: route the token in every block */
+        float xs[32];
+#pragma unroll
+        for (int q = 0; q < 4; q++) nmoe_x_cols<XMODE>(a.x, (lane + 64 * q) * 8, 8, rinv, xs + 8 * q);
+#pragma unroll
+        for (int r = 0; r < 2; r++) {
+            float logit = nmoe_router_row_bf16(wv[r], xs);
+            if (lane == 0) nmoe_st_dev(xlg + e0 + r, logit);
+        }
+        nmoe_group_barrier(gcnt, base + NMOE_FUSED_GROUP_BLOCKS, status);
+        /* ---- T: route in every block */
         if (wave == 0) {
+#pragma unroll
+            for (int q = 0; q < 4; q++) s_lg[lane + 64 * q] = nmoe_ld_dev(xlg + lane + 64 * q);
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
             uint32_t si[NMOE_MAX_K];
             float sw[NMOE_MAX_K];
-            nmoe_wave_route(a.logits, NMOE_EXPERTS, k, route_scratch, nmoe_fused_exp2_tab, si, sw, NULL);
+            nmoe_wave_route(s_lg, NMOE_EXPERTS, k, s_scratch, s_tab, si, sw, NULL);
             if (lane < NMOE_MAX_K) {
                 uint32_t vi = 0;
                 float vw = 0.0f;
@@ -110,37 +177,40 @@ __global__ void __launch_bounds__(256) nmoe_fused_decode_kernel(nmoe_fused_args 
                     }
                 s_idx[lane] = vi;
                 s_w[lane] = vw;
-                if (b == 0 && a.idx_out != NULL) a.idx_out[lane] = vi;
-                if (b == 0 && a.w_out != NULL) a.w_out[lane] = vw;
+                if (blockIdx.x == 0 && a.idx_out != NULL) a.idx_out[lane] = vi;
+                if (blockIdx.x == 0 && a.w_out != NULL) a.w_out[lane] = vw;
             }
+            if (blockIdx.x == 0 && a.logits_out != NULL)
+#pragma unroll
+                for (int q = 0; q < 4; q++) a.logits_out[lane + 64 * q] = s_lg[lane + 64 * q];
         }
     } else {
-        if (threadIdx.x < NMOE_MAX_K) {
-            uint32_t e = threadIdx.x < (unsigned)k ? a.idx_in[threadIdx.x] : 0u;
-            float wv = threadIdx.x < (unsigned)k ? a.w_in[threadIdx.x] : 0.0f;
-            /* an index outside the layer is an invalid slot: weight 0
-             * (failed expert reads get weight 0, runtime.m:2977-2981) */
-            s_w[threadIdx.x] = e < NMOE_EXPERTS ? wv : 0.0f;
-            s_idx[threadIdx.x] = e < NMOE_EXPERTS ? e : 0u;
+        if (tid < NMOE_MAX_K) {
+            uint32_t e = tid < k ? a.idx_in[tid] : 0u;
+            float wv = tid < k ? a.w_in[tid] : 0.0f;
+            /* an index outside the layer is an invalid slot: weight 0, as
+             * for a failed expert read (runtime.m:2977-2981) */
+            s_w[tid] = e < NMOE_EXPERTS ? wv : 0.0f;
+            s_idx[tid] = e < NMOE_EXPERTS ? e : 0u;
         }
+        if (tid == 0) nmoe_add_u32_dev(gcnt, 1u); /* keep 64 arrivals per launch */
     }
     __syncthreads();
 
-    /* ---- P: issue every weight load of this wavefront */
-    const int nw = nb * NMOE_FUSED_WAVES;
-    const int gw = b * NMOE_FUSED_WAVES + wave;
-    const int g_units = k * (NMOE_INTER / RPS);
-    const int gsub = lane / Q::LPR_G, gl = lane % Q::LPR_G;
-    const int ggrp = gl * Q::CPL / NMOE_GROUP;
-    uint4 gwv[NMOE_FUSED_MAXS], uwv[NMOE_FUSED_MAXS];
-    uint32_t gsb[NMOE_FUSED_MAXS], usb[NMOE_FUSED_MAXS]; /* scale | bias << 16 */
+    const bool active = g < k; /* group g streams expert slot g */
+    const uint8_t *ex = a.pack + (size_t)s_idx[active ? g : 0] * L::expert_size;
+
+    /* ---- P: issue all weight loads of this wavefront */
+    const int gsub = lane / Q::LPR_G, gl = lane % Q::LPR_G, ggrp = gl * Q::CPL / NMOE_GROUP;
+    const int dsub = lane / Q::LPR_D, dl = lane % Q::LPR_D, dgrp = dl * Q::CPL / NMOE_GROUP;
+    const int grow0 = j * NMOE_FUSED_GU_ROWS + 4 * wave + gsub;
+    const int drow0 = j * NMOE_FUSED_CHUNK + 16 * wave + dsub;
+    uint4 gwv[GSTEPS], uwv[GSTEPS], dwv[DSTEPS];
+    uint32_t gsb[GSTEPS], usb[GSTEPS], dsb[DSTEPS]; /* scale | bias << 16 */
+    if (active) {
 #pragma unroll
-    for (int i = 0; i < NMOE_FUSED_MAXS; i++) {
-        int u = gw + nw * i;
-        if (u < g_units) {
-            int s = u / (NMOE_INTER / RPS);
-            int row = (u % (NMOE_INTER / RPS)) * RPS + gsub;
-            const uint8_t *ex = a.pack + (size_t)s_idx[s] * L::expert_size;
+        for (int i = 0; i < GSTEPS; i++) {
+            int row = grow0 + i * RPS;
             gwv[i] = ((const uint4 *)(ex + L::gate_w))[(size_t)row * (Q::WPR_G / 4) + gl];
             uwv[i] = ((const uint4 *)(ex + L::up_w))[(size_t)row * (Q::WPR_G / 4) + gl];
             const uint16_t *gs = (const uint16_t *)(ex + L::gate_s) + row * Q::GPR_G + ggrp;
@@ -148,128 +218,137 @@ __global__ void __launch_bounds__(256) nmoe_fused_decode_kernel(nmoe_fused_args 
             gsb[i] = (uint32_t)gs[0] | ((uint32_t)gs[NMOE_INTER * Q::GPR_G] << 16);
             usb[i] = (uint32_t)us[0] | ((uint32_t)us[NMOE_INTER * Q::GPR_G] << 16);
         }
-    }
-    const int d_units = k * DSTEPS_PER_EXPERT;
-    const int dsub = lane / Q::LPR_D, dl = lane % Q::LPR_D;
-    const int dgrp = dl * Q::CPL / NMOE_GROUP;
-    uint4 dwv[NMOE_FUSED_MAXS];
-    uint32_t dsb[NMOE_FUSED_MAXS];
 #pragma unroll
-    for (int i = 0; i < NMOE_FUSED_MAXS; i++) {
-        int v = wave + NMOE_FUSED_WAVES * i;
-        if (v < d_units) {
-            int s = v / DSTEPS_PER_EXPERT;
-            int row = b * NMOE_FUSED_OUT_ROWS + (v % DSTEPS_PER_EXPERT) * RPW_D + dsub;
-            const uint8_t *ex = a.pack + (size_t)s_idx[s] * L::expert_size;
+        for (int i = 0; i < DSTEPS; i++) {
+            int row = drow0 + i * RPW_D;
             dwv[i] = ((const uint4 *)(ex + L::down_w))[(size_t)row * (Q::WPR_D / 4) + dl];
             const uint16_t *ds = (const uint16_t *)(ex + L::down_s) + row * Q::GPR_D + dgrp;
             dsb[i] = (uint32_t)ds[0] | ((uint32_t)ds[NMOE_HIDDEN * Q::GPR_D] << 16);
         }
-    }
-
-    /* ---- G: gate/up + SwiGLU */
-    {
+        /* ---- G: gate/up + SwiGLU -> act[g] */
         float xs[Q::CPL];
-        nmoe_load_cols<XT>(x, gl * Q::CPL, Q::CPL, xs);
+        nmoe_x_cols<XMODE>(a.x, gl * Q::CPL, Q::CPL, rinv, xs);
         float xsum = 0.0f;
 #pragma unroll
         for (int c = 0; c < Q::CPL; c++) xsum += xs[c];
+        float *xact = a.xch + NMOE_XCH_ACT + g * NMOE_INTER;
 #pragma unroll
-        for (int i = 0; i < NMOE_FUSED_MAXS; i++) {
-            int u = gw + nw * i;
-            if (u < g_units) { /* uniform across the wavefront */
-                int s = u / (NMOE_INTER / RPS);
-                int row = (u % (NMOE_INTER / RPS)) * RPS + gsub;
-                float g = __builtin_fmaf(nmoe_bf16f(gsb[i] & 0xffffu), nmoe_dot16<BITS>(gwv[i], xs),
-                                         nmoe_bf16f(gsb[i] >> 16) * xsum);
-                float up = __builtin_fmaf(nmoe_bf16f(usb[i] & 0xffffu), nmoe_dot16<BITS>(uwv[i], xs),
-                                          nmoe_bf16f(usb[i] >> 16) * xsum);
-                g = nmoe_lanes_sum<Q::LPR_G>(g);
-                up = nmoe_lanes_sum<Q::LPR_G>(up);
-                if (gl == 0) a.act[s * NMOE_INTER + row] = nmoe_silu_dev(g) * up;
-            }
+        for (int i = 0; i < GSTEPS; i++) {
+            float gv = __builtin_fmaf(nmoe_bf16f(gsb[i] & 0xffffu), nmoe_dot16<BITS>(gwv[i], xs),
+                                      nmoe_bf16f(gsb[i] >> 16) * xsum);
+            float uv = __builtin_fmaf(nmoe_bf16f(usb[i] & 0xffffu), nmoe_dot16<BITS>(uwv[i], xs),
+                                      nmoe_bf16f(usb[i] >> 16) * xsum);
+            gv = nmoe_lanes_sum<Q::LPR_G>(gv);
+            uv = nmoe_lanes_sum<Q::LPR_G>(uv);
+            if (gl == 0) nmoe_st_dev(xact + grow0 + i * RPS, nmoe_silu_dev(gv) * uv);
         }
     }
-    phase_target += (uint32_t)nb;
-    nmoe_grid_barrier(a.sync, phase_target);
+    if (active) {
+        nmoe_group_barrier(gcnt, base + 2 * NMOE_FUSED_GROUP_BLOCKS, status);
+    } else {
+        if (tid == 0) nmoe_add_u32_dev(gcnt, 1u);
+        return;
+    }
 
-    /* ---- D: down + combine */
+    /* ---- D: y_g for rows 64j..64j+63 */
+    const float *xact = a.xch + NMOE_XCH_ACT + g * NMOE_INTER;
+    s_act[tid] = nmoe_ld_dev(xact + tid);
+    s_act[tid + 256] = nmoe_ld_dev(xact + tid + 256);
+    __syncthreads();
 #pragma unroll
-    for (int i = 0; i < NMOE_FUSED_MAXS; i++) {
-        int v = wave + NMOE_FUSED_WAVES * i;
-        if (v < d_units) {
-            int s = v / DSTEPS_PER_EXPERT;
-            int rloc = (v % DSTEPS_PER_EXPERT) * RPW_D + dsub;
-            float as[Q::CPL];
-            const float4 *a4 = (const float4 *)(a.act + s * NMOE_INTER + dl * Q::CPL);
+    for (int i = 0; i < DSTEPS; i++) {
+        float as[Q::CPL];
 #pragma unroll
-            for (int c = 0; c < Q::CPL / 4; c++) {
-                float4 t = a4[c];
-                as[4 * c] = t.x;
-                as[4 * c + 1] = t.y;
-                as[4 * c + 2] = t.z;
-                as[4 * c + 3] = t.w;
-            }
-            float asum = 0.0f;
-#pragma unroll
-            for (int c = 0; c < Q::CPL; c++) asum += as[c];
-            float y = __builtin_fmaf(nmoe_bf16f(dsb[i] & 0xffffu), nmoe_dot16<BITS>(dwv[i], as),
-                                     nmoe_bf16f(dsb[i] >> 16) * asum);
-            y = nmoe_dpp_group_sum<Q::LPR_D>(y);
-            if (dl == 0) s_y[s][rloc] = y;
+        for (int c = 0; c < Q::CPL / 4; c++) {
+            float4 t = ((const float4 *)(s_act + dl * Q::CPL))[c];
+            as[4 * c] = t.x;
+            as[4 * c + 1] = t.y;
+            as[4 * c + 2] = t.z;
+            as[4 * c + 3] = t.w;
         }
+        float asum = 0.0f;
+#pragma unroll
+        for (int c = 0; c < Q::CPL; c++) asum += as[c];
+        float y = __builtin_fmaf(nmoe_bf16f(dsb[i] & 0xffffu), nmoe_dot16<BITS>(dwv[i], as),
+                                 nmoe_bf16f(dsb[i] >> 16) * asum);
+        y = nmoe_dpp_group_sum<Q::LPR_D>(y);
+        if (dl == 0) s_y[16 * wave + dsub + i * RPW_D] = y;
     }
     __syncthreads();
-    if (threadIdx.x < NMOE_FUSED_OUT_ROWS) {
-        int row = b * NMOE_FUSED_OUT_ROWS + threadIdx.x;
+    float *ypart = a.xch + NMOE_XCH_YPART;
+    if (tid < NMOE_FUSED_CHUNK) nmoe_st_dev(ypart + g * NMOE_HIDDEN + j * NMOE_FUSED_CHUNK + tid, s_y[tid]);
+
+    /* ---- C: the last of the K slots to finish chunk j combines it */
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    uint32_t *ccnt = a.sync + NMOE_SYNC_CHUNK(j);
+    if (tid == 0) {
+        uint32_t old = nmoe_add_u32_dev(ccnt, 1u);
+        int last = old == (uint32_t)(k - 1);
+        if (last) __hip_atomic_store(ccnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_f[1] = last ? 1.0f : 0.0f;
+    }
+    __syncthreads();
+    if (s_f[1] != 0.0f && tid < NMOE_FUSED_CHUNK) {
+        int row = j * NMOE_FUSED_CHUNK + tid;
+        float ys[NMOE_MAX_K];
+#pragma unroll
+        for (int s = 0; s < NMOE_MAX_K; s++) ys[s] = s < k ? nmoe_ld_dev(ypart + s * NMOE_HIDDEN + row) : 0.0f;
         float moe = 0.0f;
-        for (int s = 0; s < k; s++) moe += s_w[s] * s_y[s][threadIdx.x];
-        float r = a.h_mid[row] + moe;
-        if (a.shared_out != NULL) r = r + nmoe_sigmoid_dev(a.shared_gate_raw[0]) * a.shared_out[row];
+#pragma unroll
+        for (int s = 0; s < NMOE_MAX_K; s++)
+            if (s < k) moe += s_w[s] * ys[s];
+        float r = hm + moe;
+        if (a.shared_out != NULL) r = r + nmoe_sigmoid_dev(a.shared_gate_raw[0]) * sh;
         a.out[row] = r;
     }
-    nmoe_grid_exit(a.sync, (uint32_t)nb);
 }
 
 /* ----------------------------------------------------------- launching */
 
-template <int BITS, bool ROUTE, typename XT>
+template <int BITS, bool ROUTE, int XMODE>
 static hipError_t nmoe_fused_launch(const nmoe_fused_args &args, hipStream_t s) {
-    nmoe_fused_args a = args;
-    void *kargs[] = {&a};
-    return hipLaunchCooperativeKernel((const void *)nmoe_fused_decode_kernel<BITS, ROUTE, XT>,
-                                      dim3(NMOE_FUSED_BLOCKS), dim3(256), kargs, 0, s);
+    hipLaunchKernelGGL((nmoe_fused_decode_kernel<BITS, ROUTE, XMODE>), dim3(NMOE_FUSED_BLOCKS), dim3(256), 0, s, args);
+    return hipGetLastError();
 }
 
-template <int BITS, bool ROUTE, typename XT>
+template <int BITS, bool ROUTE, int XMODE>
 static int nmoe_fused_fits(int num_cus) {
     int per_cu = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, nmoe_fused_decode_kernel<BITS, ROUTE, XT>, 256, 0) !=
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, nmoe_fused_decode_kernel<BITS, ROUTE, XMODE>, 256, 0) !=
         hipSuccess)
         return 0;
-    return per_cu * num_cus >= NMOE_FUSED_BLOCKS;
+    return per_cu >= 1 && per_cu * num_cus >= NMOE_FUSED_BLOCKS;
 }
 
+/* The fused path needs all 256 blocks resident at once (its group barriers
+ * wait on each other); decided here from the occupancy of every variant. */
 extern "C" int nmoe_decode_init(nmoe_hip_ctx *ctx) {
-    int coop = 0;
-    if (hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, ctx->device) != hipSuccess) coop = 0;
-    int ok = coop && nmoe_fused_fits<4, true, uint16_t>(ctx->num_cus) && nmoe_fused_fits<4, true, float>(ctx->num_cus) &&
-             nmoe_fused_fits<2, true, uint16_t>(ctx->num_cus) && nmoe_fused_fits<2, true, float>(ctx->num_cus) &&
-             nmoe_fused_fits<4, false, uint16_t>(ctx->num_cus) && nmoe_fused_fits<4, false, float>(ctx->num_cus) &&
-             nmoe_fused_fits<2, false, uint16_t>(ctx->num_cus) && nmoe_fused_fits<2, false, float>(ctx->num_cus);
+    int n = ctx->num_cus;
+    int ok = nmoe_fused_fits<4, true, NMOE_XBF16>(n) && nmoe_fused_fits<4, true, NMOE_XF32>(n) &&
+             nmoe_fused_fits<4, true, NMOE_XNORM>(n) && nmoe_fused_fits<2, true, NMOE_XBF16>(n) &&
+             nmoe_fused_fits<2, true, NMOE_XF32>(n) && nmoe_fused_fits<2, true, NMOE_XNORM>(n) &&
+             nmoe_fused_fits<4, false, NMOE_XBF16>(n) && nmoe_fused_fits<4, false, NMOE_XF32>(n) &&
+             nmoe_fused_fits<2, false, NMOE_XBF16>(n) && nmoe_fused_fits<2, false, NMOE_XF32>(n);
     ctx->fused_blocks = ok ? NMOE_FUSED_BLOCKS : 0;
+    size_t need = (size_t)(NMOE_XCH_YPART + NMOE_FUSED_GROUPS * NMOE_HIDDEN) * sizeof(float);
+    if (hipMalloc((void **)&ctx->xch, need) != hipSuccess) return NMOE_HIP_ENOMEM;
+    if (hipMemset(ctx->xch, 0, need) != hipSuccess) return NMOE_HIP_EHIP;
     return NMOE_HIP_OK;
 }
 
-/* One token; routing computed (route != 0) or given (idx_in / w_in). */
-int nmoe_fused_decode(nmoe_hip_ctx *ctx, int bits, int route, const void *x, int x_dtype, int k,
-                      const uint16_t *router_w, const uint32_t *idx_in, const float *w_in, const float *h_mid,
-                      const float *shared_out, const float *shared_gate_raw, float *out, uint32_t *idx_out,
-                      float *w_out, float *logits, const uint8_t *pack, hipStream_t s) {
+/* One token.  route != 0: routing computed from router_w; else given by
+ * idx_in / w_in.  xmode: NMOE_XF32 / NMOE_XBF16 / NMOE_XNORM. */
+extern "C" int nmoe_fused_decode(nmoe_hip_ctx *ctx, int bits, int route, const void *x, int xmode, float eps, int k,
+                                 const uint16_t *router_w, const uint32_t *idx_in, const float *w_in,
+                                 const float *h_mid, const float *shared_out, const float *shared_gate_raw, float *out,
+                                 uint32_t *idx_out, float *w_out, float *logits_out, const uint8_t *pack,
+                                 hipStream_t s) {
     nmoe_fused_args a;
     a.pack = pack;
     a.router_w = router_w;
     a.x = x;
+    a.eps = eps;
     a.k = k;
     a.idx_in = idx_in;
     a.w_in = w_in;
@@ -279,22 +358,29 @@ int nmoe_fused_decode(nmoe_hip_ctx *ctx, int bits, int route, const void *x, int
     a.out = out;
     a.idx_out = idx_out;
     a.w_out = w_out;
-    a.logits = logits != NULL ? logits : ctx->logits;
-    a.act = ctx->act;
+    a.logits_out = logits_out;
+    a.xch = ctx->xch;
     a.sync = ctx->sync;
-    bool bf = x_dtype == NMOE_HIP_BF16;
-    hipError_t e;
+    hipError_t e = hipErrorInvalidValue;
     if (bits == 4) {
-        if (route)
-            e = bf ? nmoe_fused_launch<4, true, uint16_t>(a, s) : nmoe_fused_launch<4, true, float>(a, s);
-        else
-            e = bf ? nmoe_fused_launch<4, false, uint16_t>(a, s) : nmoe_fused_launch<4, false, float>(a, s);
+        if (route) {
+            if (xmode == NMOE_XBF16) e = nmoe_fused_launch<4, true, NMOE_XBF16>(a, s);
+            else if (xmode == NMOE_XF32) e = nmoe_fused_launch<4, true, NMOE_XF32>(a, s);
+            else e = nmoe_fused_launch<4, true, NMOE_XNORM>(a, s);
+        } else {
+            e = xmode == NMOE_XBF16 ? nmoe_fused_launch<4, false, NMOE_XBF16>(a, s)
+                                    : nmoe_fused_launch<4, false, NMOE_XF32>(a, s);
+        }
     } else {
-        if (route)
-            e = bf ? nmoe_fused_launch<2, true, uint16_t>(a, s) : nmoe_fused_launch<2, true, float>(a, s);
-        else
-            e = bf ? nmoe_fused_launch<2, false, uint16_t>(a, s) : nmoe_fused_launch<2, false, float>(a, s);
+        if (route) {
+            if (xmode == NMOE_XBF16) e = nmoe_fused_launch<2, true, NMOE_XBF16>(a, s);
+            else if (xmode == NMOE_XF32) e = nmoe_fused_launch<2, true, NMOE_XF32>(a, s);
+            else e = nmoe_fused_launch<2, true, NMOE_XNORM>(a, s);
+        } else {
+            e = xmode == NMOE_XBF16 ? nmoe_fused_launch<2, false, NMOE_XBF16>(a, s)
+                                    : nmoe_fused_launch<2, false, NMOE_XF32>(a, s);
+        }
     }
-    if (e != hipSuccess) return nmoe_hip_check(ctx, e, "hipLaunchCooperativeKernel(fused decode)");
+    if (e != hipSuccess) return nmoe_hip_check(ctx, e, "fused decode launch");
     return NMOE_HIP_OK;
 }

@@ -78,6 +78,16 @@ __device__ __forceinline__ float nmoe_wave_max_f(float v) {
                  fmaxf(nmoe_readlane_f(v, 32), nmoe_readlane_f(v, 48)));
 }
 
+__device__ __forceinline__ uint32_t nmoe_wave_max_u32(uint32_t v) {
+    v = max(v, nmoe_dpp_u<NMOE_DPP_XOR1>(v));
+    v = max(v, nmoe_dpp_u<NMOE_DPP_XOR2>(v));
+    v = max(v, nmoe_dpp_u<NMOE_DPP_HALF_MIRROR>(v));
+    v = max(v, nmoe_dpp_u<NMOE_DPP_MIRROR>(v));
+    uint32_t r0 = (uint32_t)__builtin_amdgcn_readlane((int)v, 0), r1 = (uint32_t)__builtin_amdgcn_readlane((int)v, 16);
+    uint32_t r2 = (uint32_t)__builtin_amdgcn_readlane((int)v, 32), r3 = (uint32_t)__builtin_amdgcn_readlane((int)v, 48);
+    return max(max(r0, r1), max(r2, r3));
+}
+
 template <int CTRL>
 __device__ __forceinline__ uint64_t nmoe_dpp_u64(uint64_t v) {
     return ((uint64_t)nmoe_dpp_u<CTRL>((uint32_t)(v >> 32)) << 32) | nmoe_dpp_u<CTRL>((uint32_t)v);
@@ -95,17 +105,6 @@ __device__ __forceinline__ uint64_t nmoe_wave_sum_u64(uint64_t v) {
     v += nmoe_dpp_u64<NMOE_DPP_HALF_MIRROR>(v);
     v += nmoe_dpp_u64<NMOE_DPP_MIRROR>(v);
     return (nmoe_readlane_u64(v, 0) + nmoe_readlane_u64(v, 16)) + (nmoe_readlane_u64(v, 32) + nmoe_readlane_u64(v, 48));
-}
-
-__device__ __forceinline__ uint64_t nmoe_max_u64(uint64_t a, uint64_t b) { return a > b ? a : b; }
-
-__device__ __forceinline__ uint64_t nmoe_wave_max_u64(uint64_t v) {
-    v = nmoe_max_u64(v, nmoe_dpp_u64<NMOE_DPP_XOR1>(v));
-    v = nmoe_max_u64(v, nmoe_dpp_u64<NMOE_DPP_XOR2>(v));
-    v = nmoe_max_u64(v, nmoe_dpp_u64<NMOE_DPP_HALF_MIRROR>(v));
-    v = nmoe_max_u64(v, nmoe_dpp_u64<NMOE_DPP_MIRROR>(v));
-    return nmoe_max_u64(nmoe_max_u64(nmoe_readlane_u64(v, 0), nmoe_readlane_u64(v, 16)),
-                        nmoe_max_u64(nmoe_readlane_u64(v, 32), nmoe_readlane_u64(v, 48)));
 }
 
 /* ------------------------------------------------------- q4 / q2 rows */
@@ -227,16 +226,9 @@ __device__ __forceinline__ float nmoe_router_row_bf16(const uint4 wv[4], const f
 
 /* ------------------------------------------------------------ routing */
 
-/* Key whose unsigned maximum is math.m's top-k winner: probabilities are
- * non-negative, so their float bits order like the values; the low word is
- * ~index so that equal probabilities rank the lower index higher. */
-__device__ __forceinline__ uint64_t nmoe_topk_key(float p, uint32_t i) {
-    return ((uint64_t)__float_as_uint(p) << 32) | (uint64_t)(0xffffffffu - i);
-}
-
 /* Routes one token with a full wavefront (math.m:67-153 bit for bit).
  * lg: the token's logits (any memory); scratch: 256 floats of LDS for the
- * sequential exact-sum path; tab: the exp2 table.  On return every lane
+ * sequential exact-sum path; tab: the exp2 table (LDS or constant memory).  On return every lane
  * holds sel_i / sel_w (slots >= n zero).  Returns n = min(k, E). */
 __device__ __forceinline__ int nmoe_wave_route(const float *lg, int num_experts, int k, float *scratch,
                                                const uint64_t *tab, uint32_t sel_i[NMOE_MAX_K],
@@ -299,12 +291,17 @@ __device__ __forceinline__ int nmoe_wave_route(const float *lg, int num_experts,
         }
     }
 
+    /* top-k (math.m:95-132): per round, the wave maximum of the 32-bit keys
+     * p_bits + 1 (probabilities are >= 0, so their bits order like the
+     * values; 0 marks a taken entry), then the lowest index holding that
+     * maximum from the compare masks -- index = lane + 64 j, so the lowest
+     * j with a hit, then its lowest lane. */
     int n = min(k, num_experts);
-    uint64_t key[4];
+    uint32_t key[4];
 #pragma unroll
     for (int j = 0; j < 4; j++) {
-        uint32_t i = (uint32_t)(lane + 64 * j);
-        key[j] = i < (uint32_t)num_experts ? nmoe_topk_key(p[j], i) : 0ull;
+        int i = lane + 64 * j;
+        key[j] = i < num_experts ? __float_as_uint(p[j]) + 1u : 0u;
     }
     float sel_v[NMOE_MAX_K];
 #pragma unroll
@@ -312,12 +309,17 @@ __device__ __forceinline__ int nmoe_wave_route(const float *lg, int num_experts,
         sel_i[s] = 0;
         sel_v[s] = 0.0f;
         if (s < n) {
-            uint64_t best = nmoe_wave_max_u64(nmoe_max_u64(nmoe_max_u64(key[0], key[1]), nmoe_max_u64(key[2], key[3])));
+            uint32_t best = nmoe_wave_max_u32(max(max(key[0], key[1]), max(key[2], key[3])));
+            uint64_t m0 = __ballot(key[0] == best), m1 = __ballot(key[1] == best);
+            uint64_t m2 = __ballot(key[2] == best), m3 = __ballot(key[3] == best);
+            uint32_t win = m0 ? (uint32_t)__builtin_ctzll(m0)
+                              : m1 ? 64u + (uint32_t)__builtin_ctzll(m1)
+                                   : m2 ? 128u + (uint32_t)__builtin_ctzll(m2) : 192u + (uint32_t)__builtin_ctzll(m3);
 #pragma unroll
             for (int j = 0; j < 4; j++)
-                if (key[j] == best) key[j] = 0ull; /* taken */
-            sel_i[s] = 0xffffffffu - (uint32_t)best;
-            sel_v[s] = __uint_as_float((uint32_t)(best >> 32));
+                if ((uint32_t)(lane + 64 * j) == win) key[j] = 0u; /* taken */
+            sel_i[s] = win;
+            sel_v[s] = __uint_as_float(best - 1u);
         }
     }
     /* math.m:134-153 */
@@ -331,45 +333,150 @@ __device__ __forceinline__ int nmoe_wave_route(const float *lg, int num_experts,
     return n;
 }
 
-/* ------------------------------------------------------- grid barrier */
+/* --------------------------------------------- exchange across blocks */
+
+/* Device-coherent loads/stores of values exchanged between blocks of one
+ * launch: agent-scope relaxed atomics (global_load/store ... sc1), so no
+ * L2-wide writeback or invalidate is needed; ordering comes from s_waitcnt
+ * before the counter update that publishes them. */
+__device__ __forceinline__ void nmoe_st_dev(float *p, float v) {
+    __hip_atomic_store((uint32_t *)p, __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float nmoe_ld_dev(const float *p) {
+    return __uint_as_float(__hip_atomic_load((uint32_t *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+}
+__device__ __forceinline__ uint32_t nmoe_ld_u32_dev(uint32_t *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t nmoe_add_u32_dev(uint32_t *p, uint32_t v) {
+    return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
 /* Bounded spin so that a grid whose blocks are not all resident still ends:
  * the waiting block gives up, records the failure in the status word and
  * carries on (the result is then wrong, and the host reports ETIMEDOUT). */
 #define NMOE_SPIN_LIMIT (1u << 22)
 
-/* All blocks of the grid arrive, then leave once `target` arrivals (phase
- * number x grid size) are counted.  Release/acquire at agent scope makes the
- * writes before the barrier visible to every block after it. */
-__device__ __forceinline__ void nmoe_grid_barrier(uint32_t *sync, uint32_t target) {
+/* Barrier of the blocks sharing counter `cnt`: every block adds 1 and leaves
+ * once the counter reaches `target` (wrap-around safe).  Stores issued before
+ * the barrier with nmoe_st_dev are visible to nmoe_ld_dev after it. */
+__device__ __forceinline__ void nmoe_group_barrier(uint32_t *cnt, uint32_t target, uint32_t *status) {
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (threadIdx.x == 0) {
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-        __hip_atomic_fetch_add(sync + NMOE_SYNC_BARRIER, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        nmoe_add_u32_dev(cnt, 1u);
         uint32_t spins = 0;
-        while (__hip_atomic_load(sync + NMOE_SYNC_BARRIER, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
+        while ((int32_t)(nmoe_ld_u32_dev(cnt) - target) < 0) {
             __builtin_amdgcn_s_sleep(1);
             if (++spins > NMOE_SPIN_LIMIT) {
-                __hip_atomic_store(sync + NMOE_SYNC_STATUS, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 break;
             }
         }
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     }
     __syncthreads();
 }
 
-/* Every block calls this once at the very end: the last block to leave
- * resets the barrier counter for the next launch (stream order guarantees
- * the next launch starts after this kernel has finished). */
-__device__ __forceinline__ void nmoe_grid_exit(uint32_t *sync, uint32_t nblocks) {
-    if (threadIdx.x == 0) {
-        uint32_t old = __hip_atomic_fetch_add(sync + NMOE_SYNC_EXIT, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-        if (old == nblocks - 1) {
-            __hip_atomic_store(sync + NMOE_SYNC_BARRIER, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(sync + NMOE_SYNC_EXIT, 0u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
-        }
+/* ------------------------------------------------------------ RMSNorm */
+
+__device__ __forceinline__ void nmoe_two_sum(double a, double b, double &s, double &e) {
+    s = a + b;
+    double bb = s - a;
+    e = (a - (s - bb)) + (b - bb);
+}
+
+template <int CTRL>
+__device__ __forceinline__ double nmoe_dpp_d(double v) {
+    uint64_t u = __builtin_bit_cast(uint64_t, v);
+    u = ((uint64_t)nmoe_dpp_u<CTRL>((uint32_t)(u >> 32)) << 32) | nmoe_dpp_u<CTRL>((uint32_t)u);
+    return __builtin_bit_cast(double, u);
+}
+
+__device__ __forceinline__ double nmoe_readlane_d(double v, int lane) {
+    uint64_t u = __builtin_bit_cast(uint64_t, v);
+    uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)u, lane);
+    uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(u >> 32), lane);
+    return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+}
+
+__device__ __forceinline__ void nmoe_dd_add(double &s, double &c, double s2, double c2) {
+    double e;
+    nmoe_two_sum(s, s2, s, e);
+    c = c + c2 + e;
+}
+
+/* rms of math.m:34-65 (unit weight) over the 2048 fp32 values h, by a whole
+ * 256-thread block; uniform result.  math.m sums the squares in an x87
+ * `long double` (64-bit significand) running sum, so its mean square differs
+ * from the exact one by less than 2^-53 relative.  The block computes the
+ * exact mean square as a double-double; if no float rounding midpoint lies
+ * within 2^-51 of it, rounding it to float gives math.m's value.  Otherwise
+ * (a near-tie, or tiny values) lane 0 replays the x87 running sum in index
+ * order.  lds_h: 2048 floats of LDS, lds_dd: 8 doubles, lds_f: 1 float. */
+__device__ float nmoe_block_rms_exact(const float *h, float eps, float *lds_h, double *lds_dd, float *lds_f) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const float4 *h4 = (const float4 *)h;
+    float4 v0 = h4[2 * tid], v1 = h4[2 * tid + 1];
+    float vv[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+    double s = 0.0, c = 0.0;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        double q = (double)vv[i] * (double)vv[i]; /* exact: 48 significant bits */
+        double e;
+        nmoe_two_sum(s, q, s, e);
+        c += e;
     }
+    nmoe_dd_add(s, c, nmoe_dpp_d<NMOE_DPP_XOR1>(s), nmoe_dpp_d<NMOE_DPP_XOR1>(c));
+    nmoe_dd_add(s, c, nmoe_dpp_d<NMOE_DPP_XOR2>(s), nmoe_dpp_d<NMOE_DPP_XOR2>(c));
+    nmoe_dd_add(s, c, nmoe_dpp_d<NMOE_DPP_HALF_MIRROR>(s), nmoe_dpp_d<NMOE_DPP_HALF_MIRROR>(c));
+    nmoe_dd_add(s, c, nmoe_dpp_d<NMOE_DPP_MIRROR>(s), nmoe_dpp_d<NMOE_DPP_MIRROR>(c));
+    if (lane == 0) {
+        double ws = nmoe_readlane_d(s, 0), wc = nmoe_readlane_d(c, 0);
+        nmoe_dd_add(ws, wc, nmoe_readlane_d(s, 16), nmoe_readlane_d(c, 16));
+        nmoe_dd_add(ws, wc, nmoe_readlane_d(s, 32), nmoe_readlane_d(c, 32));
+        nmoe_dd_add(ws, wc, nmoe_readlane_d(s, 48), nmoe_readlane_d(c, 48));
+        lds_dd[2 * wave] = ws;
+        lds_dd[2 * wave + 1] = wc;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        double S = lds_dd[0], Cc = lds_dd[1];
+        for (int w = 1; w < 4; w++) nmoe_dd_add(S, Cc, lds_dd[2 * w], lds_dd[2 * w + 1]);
+        double hi, lo;
+        nmoe_two_sum(S, Cc, hi, lo);
+        hi *= 1.0 / 2048.0; /* exact */
+        lo *= 1.0 / 2048.0;
+        float f = (float)hi;
+        uint32_t fb = __float_as_uint(f);
+        int fast = 0;
+        if (hi == 0.0 && lo == 0.0) {
+            fast = 1;
+        } else if (fb >= 0x00800000u && fb < 0x7f000000u) {
+            double up = ((double)f + (double)__uint_as_float(fb + 1u)) * 0.5;
+            double dn = ((double)f + (double)__uint_as_float(fb - 1u)) * 0.5;
+            double margin = hi * 0x1p-51;
+            fast = ((up - hi) - lo) > margin && ((hi - dn) + lo) > margin;
+        }
+        lds_f[0] = fast ? f : -1.0f;
+    }
+    __syncthreads();
+    float mean = lds_f[0];
+    if (mean < 0.0f) {
+        /* near a rounding midpoint: replay the x87 running sum */
+#pragma unroll
+        for (int i = 0; i < 8; i++) lds_h[8 * tid + i] = vv[i];
+        __syncthreads();
+        if (tid == 0) {
+            nmoe_x87 acc = nmoe_x87_zero();
+            for (int i = 0; i < NMOE_HIDDEN; i++) acc = nmoe_x87_add(acc, nmoe_x87_square(lds_h[i]));
+            acc.e -= 11; /* / 2048, exact */
+            lds_f[0] = nmoe_x87_to_float(acc);
+        }
+        __syncthreads();
+        mean = lds_f[0];
+    }
+    float rms = __fsqrt_rn(mean + eps);
+    return rms == 0.0f ? 1.0f : rms;
 }
 
 #endif

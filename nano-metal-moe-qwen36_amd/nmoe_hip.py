@@ -99,6 +99,8 @@ _SIGS = {
     "nmoe_moe_experts_q2": (_I, [_P, _I, _P, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P]),
     "nmoe_moe_layer": (_I, [_P, _I, C.POINTER(Router), _P, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P]),
     "nmoe_dequant_rows": (_I, [_P, _I, _P, _P, _P, _I, _I, _P, _P]),
+    "nmoe_moe_layer_rmsnorm": (_I, [_P, _I, C.POINTER(Router), _P, C.c_float, _I, _P, _P, _P, _P, _P]),
+    "nmoe_moe_stack": (_I, [_P, _I, C.POINTER(_I), C.POINTER(Router), _I, C.c_float, _P, _P, _P, _P]),
 }
 
 
@@ -272,6 +274,17 @@ class Context:
         return lib().nmoe_moe_layer(self.h, layer, C.byref(router), _ptr(x), x_dtype, ntok, k, _ptr(h_mid),
                                     _ptr(shared_out), _ptr(shared_gate_raw), _ptr(out), _ptr(idx), _ptr(w),
                                     _ptr(logits), stream)
+
+    def moe_layer_rmsnorm(self, layer: int, router: Router, h_in, eps: float, k: int, h_out, idx=None, w=None,
+                          logits=None, stream=None) -> int:
+        return lib().nmoe_moe_layer_rmsnorm(self.h, layer, C.byref(router), _ptr(h_in), eps, k, _ptr(h_out),
+                                            _ptr(idx), _ptr(w), _ptr(logits), stream)
+
+    def moe_stack(self, layers, routers, k: int, eps: float, h_seq, idx_seq=None, w_seq=None, stream=None) -> int:
+        n = len(layers)
+        la = (C.c_int * n)(*layers)
+        ra = (Router * n)(*routers)
+        return lib().nmoe_moe_stack(self.h, n, la, ra, k, eps, _ptr(h_seq), _ptr(idx_seq), _ptr(w_seq), stream)
 
     def dequant_rows(self, bits: int, packed, scales, biases, rows: int, in_dim: int, out, stream=None) -> int:
         return lib().nmoe_dequant_rows(self.h, bits, _ptr(packed), _ptr(scales), _ptr(biases), rows, in_dim,

@@ -52,6 +52,7 @@ _ORACLE_SIGS = {
     "orc_moe_step_bf16router": (_I, [_P, _I, _P, _P, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P]),
     "orc_moe_experts": (_I, [_P, _I, _P, _I, _I, _P, _P, _P, _P, _P, _P, _P]),
     "orc_dispatch": (None, [_P, _I, _I, _I, _I, _P, _P]),
+    "orc_moe_layer_rmsnorm": (_I, [_P, _I, _P, _P, _F, _I, _P, _P, _P, _P]),
     "orc_syn_mix64": (_U64, [_U64]),
     "orc_syn_stream": (_U64, [_U64, _U32, _U32, _U32]),
     "orc_syn_rand64": (_U64, [_U64, _U64]),

@@ -393,6 +393,20 @@ int orc_moe_step_bf16router(const uint8_t *layer_pack, int bits, const uint16_t 
     return orc_moe_experts(layer_pack, bits, x, ntok, k, idx, w, h_mid, shared_out, shared_gate_raw, out, act);
 }
 
+int orc_moe_layer_rmsnorm(const uint8_t *layer_pack, int bits, const uint16_t *router_w, const float *h_in, float eps,
+                          int k, float *h_out, uint32_t *idx8, float *w8, float *x_out) {
+    float x[ORC_HIDDEN], lg[ORC_EXPERTS];
+    uint32_t idx[ORC_MAX_K];
+    float w[ORC_MAX_K];
+    orc_rms_norm(h_in, NULL, x, ORC_HIDDEN, eps, 0);
+    if (x_out != NULL) memcpy(x_out, x, sizeof(x));
+    orc_router_logits_bf16(router_w, x, ORC_EXPERTS, ORC_HIDDEN, lg);
+    if (orc_route(lg, ORC_EXPERTS, k, idx, w, NULL) < 0) return -1;
+    if (idx8 != NULL) memcpy(idx8, idx, sizeof(idx));
+    if (w8 != NULL) memcpy(w8, w, sizeof(w));
+    return orc_moe_experts(layer_pack, bits, x, 1, k, idx, w, h_in, NULL, NULL, h_out, NULL);
+}
+
 /* ------------------------------------------------------------ dispatch */
 
 void orc_dispatch(const uint32_t *idx, int ntok, int k, int stride, int num_experts, uint32_t *perm,

@@ -105,6 +105,11 @@ int orc_moe_step_bf16router(const uint8_t *layer_pack, int bits, const uint16_t 
                             const float *shared_gate_raw, float *out, uint32_t *idx, float *w, float *logits,
                             float *act);
 
+/* One token through one layer with its input RMSNorm (math.m:34-65, unit
+ * weight): x = RMSNorm(h_in); h_out = h_in + MoE(x).  idx/w/x_out nullable. */
+int orc_moe_layer_rmsnorm(const uint8_t *layer_pack, int bits, const uint16_t *router_w, const float *h_in, float eps,
+                          int k, float *h_out, uint32_t *idx8, float *w8, float *x_out);
+
 /* Experts only (routing given): idx/w [ntok][8]. */
 int orc_moe_experts(const uint8_t *layer_pack, int bits, const float *x, int ntok, int k, const uint32_t *idx,
                     const float *w, const float *h_mid, const float *shared_out, const float *shared_gate_raw,

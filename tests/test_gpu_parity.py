@@ -280,3 +280,90 @@ def test_fused_repeated_launches(ctx, nh, bits):
         np.testing.assert_array_equal(gw[i].view(np.uint32), ow.view(np.uint32))
         want = B.moe_experts(host_pack(bits, seed, layers[l], oi[:k]), bits, x[i:i + 1], k, oi[None], ow[None], h[i:i + 1])
         assert_close(go[i], want[0], what=f"step {i}")
+
+
+def _oracle_layer_rmsnorm(pack, bits, W, h_in, k, eps=1e-6):
+    h_out = np.zeros(2048, np.float32)
+    idx = np.zeros(8, np.uint32)
+    w = np.zeros(8, np.float32)
+    x = np.zeros(2048, np.float32)
+    rc = B.oracle().orc_moe_layer_rmsnorm(pack.ctypes.data, bits, np.ascontiguousarray(W).ctypes.data,
+                                          np.ascontiguousarray(h_in, np.float32).ctypes.data, eps, k,
+                                          h_out.ctypes.data, idx.ctypes.data, w.ctypes.data, x.ctypes.data)
+    assert rc == 0
+    return h_out, idx, w, x
+
+
+@pytest.mark.parametrize("bits", [4, 2])
+def test_stack_teacher_forced(ctx, nh, bits):
+    """The routed-expert stack of one token: every layer's routing bit-exact
+    and its output within tolerance, each layer checked on the GPU's own input
+    (RMSNorm in front of every layer, math.m:34-65)."""
+    seed, k, nl = 17, 8, 6
+    layers = [50 + 6 * (bits == 2) + i for i in range(nl)]
+    for layer in layers:
+        ctx.synth_layer(layer, bits, seed, SIGMA[bits])
+    W = [B.syn_bf16(256 * 2048, seed, layer, 16, 0.02).reshape(256, 2048) for layer in layers]
+    dW = [ctx.to_device(w) for w in W]
+    h0 = B.bf16_to_f32(B.syn_bf16(2048, seed, 99, 18, 1.0))
+    hs = ctx.alloc((nl + 1) * 8192)
+    hs.upload(h0)
+    idx_s, w_s = ctx.alloc(nl * 32), ctx.alloc(nl * 32)
+    ctx._check(ctx.moe_stack(layers, [ctx.router_bf16(d) for d in dW], k, 1e-6, hs, idx_s, w_s))
+    assert ctx.device_status() == nh.OK
+    H = hs.download(np.float32, (nl + 1, 2048))
+    I, Wt = idx_s.download(np.uint32, (nl, 8)), w_s.download(np.float32, (nl, 8))
+    np.testing.assert_array_equal(H[0], h0)
+    for l in range(nl):
+        x = np.zeros(2048, np.float32)
+        B.oracle().orc_rms_norm(H[l].ctypes.data, None, x.ctypes.data, 2048, 1e-6, 0)
+        oi, ow, _ = B.route(B.router_logits_bf16(W[l], x), k)
+        pack = host_pack(bits, seed, layers[l], oi[:k])
+        h_out, oi2, ow2, _ = _oracle_layer_rmsnorm(pack, bits, W[l], H[l], k)
+        np.testing.assert_array_equal(oi2, oi)
+        np.testing.assert_array_equal(I[l], oi, err_msg=f"layer {l}")
+        np.testing.assert_array_equal(Wt[l].view(np.uint32), ow.view(np.uint32), err_msg=f"layer {l}")
+        assert_close(H[l + 1], h_out, what=f"layer {l}")
+
+
+def test_rmsnorm_midpoint_takes_exact_path(ctx, nh):
+    """h_i = 1 + 2^-12 for all i: the mean square 1 + 2^-11 + 2^-24 is exactly
+    a float rounding midpoint, which the double-double fast test rejects, so
+    the sequential x87 replay must produce math.m's float."""
+    bits, seed, k, layer = 4, 23, 8, 60
+    ctx.synth_layer(layer, bits, seed, SIGMA[bits])
+    W = B.syn_bf16(256 * 2048, seed, layer, 16, 0.02).reshape(256, 2048)
+    dW = ctx.to_device(W)
+    for h in (np.full(2048, 1 + 2 ** -12, np.float32),
+              np.concatenate([np.full(2047, 1 + 2 ** -12), [1.5]]).astype(np.float32)):
+        x = np.zeros(2048, np.float32)
+        B.oracle().orc_rms_norm(h.ctypes.data, None, x.ctypes.data, 2048, 1e-6, 0)
+        oi, ow, _ = B.route(B.router_logits_bf16(W, x), k)
+        dh, dout, di, dw, dl = ctx.to_device(h), ctx.alloc(8192), ctx.alloc(32), ctx.alloc(32), ctx.alloc(1024)
+        ctx._check(ctx.moe_layer_rmsnorm(layer, ctx.router_bf16(dW), dh, 1e-6, k, dout, di, dw, dl))
+        np.testing.assert_array_equal(dl.download(np.float32, 256).view(np.uint32),
+                                      B.router_logits_bf16(W, x).view(np.uint32))
+        np.testing.assert_array_equal(di.download(np.uint32, 8), oi)
+        h_out, _, _, _ = _oracle_layer_rmsnorm(host_pack(bits, seed, layer, oi[:k]), bits, W, h, k)
+        assert_close(dout.download(np.float32, 2048), h_out, what="midpoint rms")
+
+
+def test_fused_wide_logit_spread(ctx, nh):
+    """Logits spread over ~100 (x scaled by 40): many softmax terms fall below
+    2^-32, so the fused kernel replays the long double sum sequentially."""
+    rng = np.random.default_rng(77)
+    bits, seed, k, layer = 4, 31, 8, 61
+    ctx.synth_layer(layer, bits, seed, SIGMA[bits])
+    W = B.syn_bf16(256 * 2048, seed, layer, 16, 0.02).reshape(256, 2048)
+    x = (rng.standard_normal(2048) * 40).astype(np.float32)
+    h = rng.standard_normal(2048).astype(np.float32)
+    lg = B.router_logits_bf16(W, x)
+    assert (np.exp(lg.astype(np.float64) - lg.max()) < 2.0 ** -32).any()
+    oi, ow, _ = B.route(lg, k)
+    want = B.moe_experts(host_pack(bits, seed, layer, oi[:k]), bits, x[None], k, oi[None], ow[None], h[None])[0]
+    out, di, dw = ctx.alloc(8192), ctx.alloc(32), ctx.alloc(32)
+    ctx._check(ctx.moe_layer(layer, ctx.router_bf16(ctx.to_device(W)), ctx.to_device(x), nh.F32, 1, k,
+                             ctx.to_device(h), out, di, dw))
+    np.testing.assert_array_equal(di.download(np.uint32, 8), oi)
+    np.testing.assert_array_equal(dw.download(np.float32, 8).view(np.uint32), ow.view(np.uint32))
+    assert_close(out.download(np.float32, 2048), want, what="wide spread")
