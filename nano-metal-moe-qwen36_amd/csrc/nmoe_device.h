@@ -355,7 +355,7 @@ __device__ __forceinline__ uint32_t nmoe_add_u32_dev(uint32_t *p, uint32_t v) {
 /* Bounded spin so that a grid whose blocks are not all resident still ends:
  * the waiting block gives up, records the failure in the status word and
  * carries on (the result is then wrong, and the host reports ETIMEDOUT). */
-#define NMOE_SPIN_LIMIT (1u << 22)
+#define NMOE_SPIN_LIMIT (1u << 20)
 
 /* Barrier of the blocks sharing counter `cnt`: every block adds 1 and leaves
  * once the counter reaches `target` (wrap-around safe).  Stores issued before
