@@ -430,11 +430,13 @@ __device__ float nmoe_block_rms_exact(const float *h, float eps, float *lds_h, d
     nmoe_dd_add(s, c, nmoe_dpp_d<NMOE_DPP_XOR2>(s), nmoe_dpp_d<NMOE_DPP_XOR2>(c));
     nmoe_dd_add(s, c, nmoe_dpp_d<NMOE_DPP_HALF_MIRROR>(s), nmoe_dpp_d<NMOE_DPP_HALF_MIRROR>(c));
     nmoe_dd_add(s, c, nmoe_dpp_d<NMOE_DPP_MIRROR>(s), nmoe_dpp_d<NMOE_DPP_MIRROR>(c));
+    /* cross-row combination with every lane active (reading other lanes
+     * from inside a lane-divergent branch would read undefined values) */
+    double ws = nmoe_readlane_d(s, 0), wc = nmoe_readlane_d(c, 0);
+    nmoe_dd_add(ws, wc, nmoe_readlane_d(s, 16), nmoe_readlane_d(c, 16));
+    nmoe_dd_add(ws, wc, nmoe_readlane_d(s, 32), nmoe_readlane_d(c, 32));
+    nmoe_dd_add(ws, wc, nmoe_readlane_d(s, 48), nmoe_readlane_d(c, 48));
     if (lane == 0) {
-        double ws = nmoe_readlane_d(s, 0), wc = nmoe_readlane_d(c, 0);
-        nmoe_dd_add(ws, wc, nmoe_readlane_d(s, 16), nmoe_readlane_d(c, 16));
-        nmoe_dd_add(ws, wc, nmoe_readlane_d(s, 32), nmoe_readlane_d(c, 32));
-        nmoe_dd_add(ws, wc, nmoe_readlane_d(s, 48), nmoe_readlane_d(c, 48));
         lds_dd[2 * wave] = ws;
         lds_dd[2 * wave + 1] = wc;
     }
