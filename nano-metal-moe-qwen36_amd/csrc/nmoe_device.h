@@ -477,7 +477,7 @@ __device__ float nmoe_block_rms_exact(const float *h, float eps, float *lds_h, d
         __syncthreads();
         mean = lds_f[0];
     }
-    float rms = __fsqrt_rn(mean + eps);
+    float rms = nmoe_sqrtf_rn(mean + eps); /* sqrtf((float)mean + eps) */
     return rms == 0.0f ? 1.0f : rms;
 }
 

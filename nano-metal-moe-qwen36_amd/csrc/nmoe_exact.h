@@ -275,4 +275,21 @@ NMOE_HD int nmoe_softmax_term_fixed(float e, uint64_t *out) {
     return 1;
 }
 
+/* Correctly rounded single-precision square root of v >= 0 (normal range),
+ * as sqrtf: an estimate r from double precision, then the exact test against
+ * the squares of the neighbouring rounding midpoints (a midpoint has 25
+ * significant bits, so its square is exact in double; v never equals one,
+ * having only 24). */
+NMOE_HD float nmoe_sqrtf_rn(float v) {
+    if (!(v > 0.0f)) return v == 0.0f ? v : nmoe_bits_flt(0x7fc00000u);
+    double vd = (double)v;
+    float r = (float)sqrt(vd);
+    uint32_t rb = nmoe_flt_bits(r);
+    double up = ((double)r + (double)nmoe_bits_flt(rb + 1u)) * 0.5;
+    if (vd > up * up) return nmoe_bits_flt(rb + 1u);
+    double dn = ((double)r + (double)nmoe_bits_flt(rb - 1u)) * 0.5;
+    if (vd < dn * dn) return nmoe_bits_flt(rb - 1u);
+    return r;
+}
+
 #endif

@@ -53,3 +53,5 @@ float h_native_mean_sq(const float *v, int n) {
 }
 
 float h_u64e_to_f32(uint64_t m, int e) { return nmoe_u64e_to_f32_rne(m, e); }
+
+float h_sqrtf(float v) { return nmoe_sqrtf_rn(v); }

@@ -34,6 +34,7 @@ def h(tmp_path_factory):
     lib.h_x87_mean_sq.restype, lib.h_x87_mean_sq.argtypes = ctypes.c_float, [P, ctypes.c_int, ctypes.c_int]
     lib.h_fixed_sum.restype, lib.h_fixed_sum.argtypes = ctypes.c_int, [P, ctypes.c_int, P]
     lib.h_u64e_to_f32.restype, lib.h_u64e_to_f32.argtypes = ctypes.c_float, [ctypes.c_uint64, ctypes.c_int]
+    lib.h_sqrtf.restype, lib.h_sqrtf.argtypes = ctypes.c_float, [ctypes.c_float]
     return lib
 
 
@@ -113,3 +114,17 @@ def test_u64_to_float_rounding(h):
             assert abs(Fraction(float(got)) - exact) <= abs(Fraction(float(hi)) - exact)
         else:
             assert np.float32(got) == want
+
+
+def test_sqrtf_correctly_rounded(h):
+    """nmoe_sqrtf_rn == libm sqrtf (IEEE correctly rounded) on a sweep of
+    positive normal floats, including the neighbours of exact squares."""
+    LIBM.sqrtf.restype, LIBM.sqrtf.argtypes = ctypes.c_float, [ctypes.c_float]
+    bits = np.arange(0x00800000, 0x7f800000, 7919, dtype=np.uint64).astype(np.uint32)
+    vals = list(bits.view(np.float32))
+    for r in (1.0, 1.5, 3.0, 1.0031055, 7.25):
+        sq = np.float32(np.float32(r) * np.float32(r))
+        vals += [sq, np.nextafter(sq, np.float32(0)), np.nextafter(sq, np.float32(np.inf))]
+    for v in vals:
+        a, b = h.h_sqrtf(float(v)), LIBM.sqrtf(float(v))
+        assert np.float32(a).view(np.uint32) == np.float32(b).view(np.uint32), float(v)
