@@ -366,4 +366,6 @@ def test_fused_wide_logit_spread(ctx, nh):
                              ctx.to_device(h), out, di, dw))
     np.testing.assert_array_equal(di.download(np.uint32, 8), oi)
     np.testing.assert_array_equal(dw.download(np.float32, 8).view(np.uint32), ow.view(np.uint32))
-    assert_close(out.download(np.float32, 2048), want, what="wide spread")
+    # x is scaled by 40, so outputs reach ~1e5: the absolute bound scales with them
+    scale = max(1.0, float(np.abs(want).max()) / 10.0)
+    assert_close(out.download(np.float32, 2048), want, max_abs=2e-3 * scale, what="wide spread")
