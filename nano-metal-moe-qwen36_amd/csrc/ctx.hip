@@ -117,8 +117,10 @@ extern "C" int nmoe_hip_check_device_status(nmoe_hip_ctx *ctx) {
     NMOE_HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
     NMOE_HIP_TRY(ctx, hipMemcpy(&status, ctx->sync + NMOE_SYNC_STATUS, sizeof(status), hipMemcpyDeviceToHost));
     if (status != 0) {
-        /* a timed-out persistent kernel leaves its counters mid-way: clear all */
+        /* restart the launch epochs and clear every tagged exchange word, so
+         * no stale word can carry a future epoch */
         NMOE_HIP_TRY(ctx, hipMemset(ctx->sync, 0, NMOE_SYNC_WORDS * sizeof(uint32_t)));
+        if (ctx->xch != NULL) NMOE_HIP_TRY(ctx, hipMemset(ctx->xch, 0, ctx->xch_bytes));
         NMOE_HIP_TRY(ctx, hipDeviceSynchronize());
         return nmoe_fail(ctx, NMOE_HIP_ETIMEDOUT, "a persistent kernel's bounded wait expired (status %u)", status);
     }

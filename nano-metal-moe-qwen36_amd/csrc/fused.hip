@@ -11,31 +11,31 @@
  * and the step is one launch of 256 blocks x 4 wavefronts.
  *
  * Blocks form 8 groups of 32 (group g = block % 8, j = block / 8); group g
- * streams expert slot g, so its barriers involve 32 blocks only (a counter
- * shared by all 256 blocks serialises 256 same-address atomics, ~3.7 us on
- * MI355X; 32 arrivals cost ~0.8 us).
+ * streams expert slot g.
  *
  *   N  (stack variant) every block derives x = RMSNorm(h) itself, bit-exact
  *      with math.m:34-65.
  *   R  group g computes all 256 logits (block j: rows 8j..8j+7; the router
- *      is re-read by the 8 groups, mostly from the last-level cache) and
- *      exchanges them inside the group.                    -- group barrier
- *   T  every block routes the token (bit-exact math.m softmax / top-k /
- *      renormalise in one wavefront).
+ *      is re-read by the 8 groups, mostly from the last-level cache).
+ *   T  every block waits for its group's 256 logits and routes the token
+ *      (bit-exact math.m softmax / top-k / renormalise in one wavefront).
  *   P  block j of group g issues all weight loads of slot g at once: gate/up
  *      rows 16j..16j+15 and down rows 64j..64j+63 (~55 KB per block, the
  *      whole 14 MB of expert weights in flight across the grid).
- *   G  gate/up dot products + SwiGLU -> act[g][512].        -- group barrier
- *   D  y_g = down_g . act[g] for rows 64j..64j+63 -> ypart[g].
- *   C  per 64-row chunk, a counter counts the K slots; the block that
- *      arrives last combines out = h_mid + sum_s w_s y_s (+ sigmoid(g) *
- *      shared) in slot order, deterministic, with no global barrier.
+ *   G  gate/up dot products + SwiGLU -> act[g][512].
+ *   D  block j waits for act[g], computes y_g = down_g . act[g] for rows
+ *      64j..64j+63 -> ypart[g].
+ *   C  block j of group 0 waits for the K partials of its rows and combines
+ *      out = h_mid + sum_s w_s y_s (+ sigmoid(g) * shared) in slot order.
  *
- * Exchanged values use device-coherent (sc1) loads/stores and the counters
- * device-scope atomics.  Group counters grow by exactly 64 per launch (two
- * barriers x 32 blocks; a launch without routing adds its first 32 without
- * waiting), so a block derives this launch's targets from the counter value
- * it reads at start and nothing needs resetting.  Every wait is bounded.
+ * Values cross blocks as 64-bit (epoch, value) words written and read with
+ * one device-coherent (sc1) access each; a consumer polls the words it needs
+ * until all carry this launch's epoch.  That merges "wait" and "fetch" into
+ * one memory round trip: no barrier counter, no same-address atomics, no
+ * L2-wide cache maintenance.  The epoch is the launch count, kept per block
+ * (each block increments its own word once per launch, so all agree).  A
+ * group's barrier-free hand-offs also mean idle groups (K < 8) simply exit.
+ * Every wait is bounded.
  */
 #include "nmoe_device.h"
 
@@ -49,14 +49,14 @@ static __constant__ uint64_t nmoe_fused_exp2_tab[32] = NMOE_EXP2_TAB32;
 #define NMOE_FUSED_CHUNK (NMOE_HIDDEN / NMOE_FUSED_GROUP_BLOCKS)         /* 64 output rows per block */
 #define NMOE_FUSED_GU_ROWS (NMOE_INTER / NMOE_FUSED_GROUP_BLOCKS)        /* 16 gate/up rows per block */
 
-/* sync word layout (uint32 words, counters on separate 128-byte lines) */
-#define NMOE_SYNC_GROUP(g) (32 + 32 * (g))
-#define NMOE_SYNC_CHUNK(c) (32 * (NMOE_FUSED_GROUPS + 1) + 32 * (c))
+/* sync words: per-block launch epochs, 64 bytes apart */
+#define NMOE_SYNC_EPOCH(b) (64 + 16 * (b))
 
-/* exchange scratch layout (floats) */
+/* exchange scratch layout (64-bit tagged words) */
 #define NMOE_XCH_LOGITS 0
 #define NMOE_XCH_ACT (NMOE_FUSED_GROUPS * NMOE_EXPERTS)
 #define NMOE_XCH_YPART (NMOE_XCH_ACT + NMOE_FUSED_GROUPS * NMOE_INTER)
+#define NMOE_XCH_WORDS (NMOE_XCH_YPART + NMOE_FUSED_GROUPS * NMOE_HIDDEN)
 
 /* x sources: XF32 / XBF16 = activations given; XNORM = x is RMSNorm(h). */
 #define NMOE_XF32 0
@@ -78,9 +78,31 @@ struct nmoe_fused_args {
     uint32_t *idx_out;
     float *w_out;
     float *logits_out;
-    float *xch;
+    uint64_t *xch;
     uint32_t *sync;
 };
+
+/* Polls n tagged words until all carry `epoch` (bounded); returns the
+ * values.  Each lane polls its own words. */
+template <int N>
+__device__ __forceinline__ void nmoe_poll(const uint64_t *const p[N], uint32_t epoch, float v[N], uint32_t *status) {
+    uint32_t spins = 0;
+    for (;;) {
+        bool ready = true;
+#pragma unroll
+        for (int i = 0; i < N; i++) {
+            uint64_t w = nmoe_ld_tagged(p[i]);
+            ready = ready && nmoe_tag_is(w, epoch);
+            v[i] = nmoe_tag_val(w);
+        }
+        if (ready) return;
+        __builtin_amdgcn_s_sleep(1);
+        if (++spins > NMOE_SPIN_LIMIT) {
+            __hip_atomic_store(status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            return;
+        }
+    }
+}
 
 /* The lane's n activations at columns c0.. (fp32, bf16, or normalised h).
  * Normalised: math.m:63 computes (input / rms) * 1.0f.  With rinv the double
@@ -115,27 +137,35 @@ __global__ void __launch_bounds__(256) nmoe_fused_decode_kernel(nmoe_fused_args 
     __shared__ uint32_t s_idx[NMOE_MAX_K];
     __shared__ float s_w[NMOE_MAX_K];
     __shared__ double s_dd[8];
-    __shared__ float s_f[2];
+    __shared__ float s_f[1];
+    __shared__ uint32_t s_epoch;
     __shared__ float s_h[XMODE == NMOE_XNORM ? NMOE_HIDDEN : 1];
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int g = blockIdx.x % NMOE_FUSED_GROUPS, j = blockIdx.x / NMOE_FUSED_GROUPS;
     const int k = a.k;
-    uint32_t *gcnt = a.sync + NMOE_SYNC_GROUP(g);
     uint32_t *status = a.sync + NMOE_SYNC_STATUS;
-    float *xlg = a.xch + NMOE_XCH_LOGITS + g * NMOE_EXPERTS;
+    uint64_t *xlg = a.xch + NMOE_XCH_LOGITS + g * NMOE_EXPERTS;
+    uint64_t *xact = a.xch + NMOE_XCH_ACT + g * NMOE_INTER;
+    uint64_t *ypart = a.xch + NMOE_XCH_YPART;
 
-    uint32_t base = 0;
-    if (tid == 0) base = nmoe_ld_u32_dev(gcnt) & ~63u;
+    if (tid == 0) {
+        uint32_t *ep = a.sync + NMOE_SYNC_EPOCH(blockIdx.x);
+        uint32_t e = nmoe_ld_u32_dev(ep) + 1u;
+        __hip_atomic_store(ep, e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_epoch = e;
+    }
     if (tid < 32) s_tab[tid] = nmoe_fused_exp2_tab[tid];
-    /* residual rows of this block's chunk, needed if it ends up combining */
+    /* residual rows of this block's chunk (used by the combining blocks) */
     float hm = 0.0f, sh = 0.0f;
-    if (tid < NMOE_FUSED_CHUNK) {
+    if (g == 0 && tid < NMOE_FUSED_CHUNK) {
         hm = a.h_mid[j * NMOE_FUSED_CHUNK + tid];
         if (a.shared_out != NULL) sh = a.shared_out[j * NMOE_FUSED_CHUNK + tid];
     }
     double rinv = 1.0;
     if (XMODE == NMOE_XNORM) rinv = 1.0 / (double)nmoe_block_rms_exact((const float *)a.x, a.eps, s_h, s_dd, s_f);
+    __syncthreads();
+    const uint32_t epoch = s_epoch;
 
     if (ROUTE) {
         /* ---- R: rows 8j + 2*wave + {0, 1} of the router, in group g */
@@ -153,13 +183,15 @@ __global__ void __launch_bounds__(256) nmoe_fused_decode_kernel(nmoe_fused_args 
 #pragma unroll
         for (int r = 0; r < 2; r++) {
             float logit = nmoe_router_row_bf16(wv[r], xs);
-            if (lane == 0) nmoe_st_dev(xlg + e0 + r, logit);
+            if (lane == 0) nmoe_st_tagged(xlg + e0 + r, epoch, logit);
         }
-        nmoe_group_barrier(gcnt, base + NMOE_FUSED_GROUP_BLOCKS, status);
-        /* ---- T: route in every block */
+        /* ---- T: wait for the group's 256 logits, route in every block */
         if (wave == 0) {
+            const uint64_t *pl[4] = {xlg + lane, xlg + lane + 64, xlg + lane + 128, xlg + lane + 192};
+            float lv[4];
+            nmoe_poll<4>(pl, epoch, lv, status);
 #pragma unroll
-            for (int q = 0; q < 4; q++) s_lg[lane + 64 * q] = nmoe_ld_dev(xlg + lane + 64 * q);
+            for (int q = 0; q < 4; q++) s_lg[lane + 64 * q] = lv[q];
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
             __builtin_amdgcn_wave_barrier();
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
@@ -193,12 +225,10 @@ __global__ void __launch_bounds__(256) nmoe_fused_decode_kernel(nmoe_fused_args 
             s_w[tid] = e < NMOE_EXPERTS ? wv : 0.0f;
             s_idx[tid] = e < NMOE_EXPERTS ? e : 0u;
         }
-        if (tid == 0) nmoe_add_u32_dev(gcnt, 1u); /* keep 64 arrivals per launch */
     }
     __syncthreads();
-
-    const bool active = g < k; /* group g streams expert slot g */
-    const uint8_t *ex = a.pack + (size_t)s_idx[active ? g : 0] * L::expert_size;
+    if (g >= k) return; /* group g streams expert slot g */
+    const uint8_t *ex = a.pack + (size_t)s_idx[g] * L::expert_size;
 
     /* ---- P: issue all weight loads of this wavefront */
     const int gsub = lane / Q::LPR_G, gl = lane % Q::LPR_G, ggrp = gl * Q::CPL / NMOE_GROUP;
@@ -207,31 +237,30 @@ __global__ void __launch_bounds__(256) nmoe_fused_decode_kernel(nmoe_fused_args 
     const int drow0 = j * NMOE_FUSED_CHUNK + 16 * wave + dsub;
     uint4 gwv[GSTEPS], uwv[GSTEPS], dwv[DSTEPS];
     uint32_t gsb[GSTEPS], usb[GSTEPS], dsb[DSTEPS]; /* scale | bias << 16 */
-    if (active) {
 #pragma unroll
-        for (int i = 0; i < GSTEPS; i++) {
-            int row = grow0 + i * RPS;
-            gwv[i] = ((const uint4 *)(ex + L::gate_w))[(size_t)row * (Q::WPR_G / 4) + gl];
-            uwv[i] = ((const uint4 *)(ex + L::up_w))[(size_t)row * (Q::WPR_G / 4) + gl];
-            const uint16_t *gs = (const uint16_t *)(ex + L::gate_s) + row * Q::GPR_G + ggrp;
-            const uint16_t *us = (const uint16_t *)(ex + L::up_s) + row * Q::GPR_G + ggrp;
-            gsb[i] = (uint32_t)gs[0] | ((uint32_t)gs[NMOE_INTER * Q::GPR_G] << 16);
-            usb[i] = (uint32_t)us[0] | ((uint32_t)us[NMOE_INTER * Q::GPR_G] << 16);
-        }
+    for (int i = 0; i < GSTEPS; i++) {
+        int row = grow0 + i * RPS;
+        gwv[i] = ((const uint4 *)(ex + L::gate_w))[(size_t)row * (Q::WPR_G / 4) + gl];
+        uwv[i] = ((const uint4 *)(ex + L::up_w))[(size_t)row * (Q::WPR_G / 4) + gl];
+        const uint16_t *gs = (const uint16_t *)(ex + L::gate_s) + row * Q::GPR_G + ggrp;
+        const uint16_t *us = (const uint16_t *)(ex + L::up_s) + row * Q::GPR_G + ggrp;
+        gsb[i] = (uint32_t)gs[0] | ((uint32_t)gs[NMOE_INTER * Q::GPR_G] << 16);
+        usb[i] = (uint32_t)us[0] | ((uint32_t)us[NMOE_INTER * Q::GPR_G] << 16);
+    }
 #pragma unroll
-        for (int i = 0; i < DSTEPS; i++) {
-            int row = drow0 + i * RPW_D;
-            dwv[i] = ((const uint4 *)(ex + L::down_w))[(size_t)row * (Q::WPR_D / 4) + dl];
-            const uint16_t *ds = (const uint16_t *)(ex + L::down_s) + row * Q::GPR_D + dgrp;
-            dsb[i] = (uint32_t)ds[0] | ((uint32_t)ds[NMOE_HIDDEN * Q::GPR_D] << 16);
-        }
-        /* ---- G: gate/up + SwiGLU -> act[g] */
+    for (int i = 0; i < DSTEPS; i++) {
+        int row = drow0 + i * RPW_D;
+        dwv[i] = ((const uint4 *)(ex + L::down_w))[(size_t)row * (Q::WPR_D / 4) + dl];
+        const uint16_t *ds = (const uint16_t *)(ex + L::down_s) + row * Q::GPR_D + dgrp;
+        dsb[i] = (uint32_t)ds[0] | ((uint32_t)ds[NMOE_HIDDEN * Q::GPR_D] << 16);
+    }
+    /* ---- G: gate/up + SwiGLU -> act[g] */
+    {
         float xs[Q::CPL];
         nmoe_x_cols<XMODE>(a.x, gl * Q::CPL, Q::CPL, rinv, xs);
         float xsum = 0.0f;
 #pragma unroll
         for (int c = 0; c < Q::CPL; c++) xsum += xs[c];
-        float *xact = a.xch + NMOE_XCH_ACT + g * NMOE_INTER;
 #pragma unroll
         for (int i = 0; i < GSTEPS; i++) {
             float gv = __builtin_fmaf(nmoe_bf16f(gsb[i] & 0xffffu), nmoe_dot16<BITS>(gwv[i], xs),
@@ -240,20 +269,18 @@ __global__ void __launch_bounds__(256) nmoe_fused_decode_kernel(nmoe_fused_args 
                                       nmoe_bf16f(usb[i] >> 16) * xsum);
             gv = nmoe_lanes_sum<Q::LPR_G>(gv);
             uv = nmoe_lanes_sum<Q::LPR_G>(uv);
-            if (gl == 0) nmoe_st_dev(xact + grow0 + i * RPS, nmoe_silu_dev(gv) * uv);
+            if (gl == 0) nmoe_st_tagged(xact + grow0 + i * RPS, epoch, nmoe_silu_dev(gv) * uv);
         }
     }
-    if (active) {
-        nmoe_group_barrier(gcnt, base + 2 * NMOE_FUSED_GROUP_BLOCKS, status);
-    } else {
-        if (tid == 0) nmoe_add_u32_dev(gcnt, 1u);
-        return;
-    }
 
-    /* ---- D: y_g for rows 64j..64j+63 */
-    const float *xact = a.xch + NMOE_XCH_ACT + g * NMOE_INTER;
-    s_act[tid] = nmoe_ld_dev(xact + tid);
-    s_act[tid + 256] = nmoe_ld_dev(xact + tid + 256);
+    /* ---- D: wait for act[g], then y_g for rows 64j..64j+63 */
+    {
+        const uint64_t *pa[2] = {xact + tid, xact + tid + 256};
+        float av[2];
+        nmoe_poll<2>(pa, epoch, av, status);
+        s_act[tid] = av[0];
+        s_act[tid + 256] = av[1];
+    }
     __syncthreads();
 #pragma unroll
     for (int i = 0; i < DSTEPS; i++) {
@@ -275,25 +302,36 @@ __global__ void __launch_bounds__(256) nmoe_fused_decode_kernel(nmoe_fused_args 
         if (dl == 0) s_y[16 * wave + dsub + i * RPW_D] = y;
     }
     __syncthreads();
-    float *ypart = a.xch + NMOE_XCH_YPART;
-    if (tid < NMOE_FUSED_CHUNK) nmoe_st_dev(ypart + g * NMOE_HIDDEN + j * NMOE_FUSED_CHUNK + tid, s_y[tid]);
-
-    /* ---- C: the last of the K slots to finish chunk j combines it */
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    uint32_t *ccnt = a.sync + NMOE_SYNC_CHUNK(j);
-    if (tid == 0) {
-        uint32_t old = nmoe_add_u32_dev(ccnt, 1u);
-        int last = old == (uint32_t)(k - 1);
-        if (last) __hip_atomic_store(ccnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        s_f[1] = last ? 1.0f : 0.0f;
+    const int row = j * NMOE_FUSED_CHUNK + tid;
+    if (g != 0) {
+        if (tid < NMOE_FUSED_CHUNK) nmoe_st_tagged(ypart + g * NMOE_HIDDEN + row, epoch, s_y[tid]);
+        return;
     }
-    __syncthreads();
-    if (s_f[1] != 0.0f && tid < NMOE_FUSED_CHUNK) {
-        int row = j * NMOE_FUSED_CHUNK + tid;
+
+    /* ---- C: block j of group 0 combines rows 64j..64j+63 over the K slots */
+    if (tid < NMOE_FUSED_CHUNK) {
+        /* one polling round loads all K-1 partials at once */
         float ys[NMOE_MAX_K];
+        ys[0] = s_y[tid];
+        uint32_t spins = 0;
+        for (;;) {
+            bool ready = true;
 #pragma unroll
-        for (int s = 0; s < NMOE_MAX_K; s++) ys[s] = s < k ? nmoe_ld_dev(ypart + s * NMOE_HIDDEN + row) : 0.0f;
+            for (int s = 1; s < NMOE_MAX_K; s++) {
+                ys[s] = 0.0f;
+                if (s < k) {
+                    uint64_t w = nmoe_ld_tagged(ypart + s * NMOE_HIDDEN + row);
+                    ready = ready && nmoe_tag_is(w, epoch);
+                    ys[s] = nmoe_tag_val(w);
+                }
+            }
+            if (ready) break;
+            __builtin_amdgcn_s_sleep(1);
+            if (++spins > NMOE_SPIN_LIMIT) {
+                __hip_atomic_store(status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                break;
+            }
+        }
         float moe = 0.0f;
 #pragma unroll
         for (int s = 0; s < NMOE_MAX_K; s++)
@@ -331,9 +369,9 @@ extern "C" int nmoe_decode_init(nmoe_hip_ctx *ctx) {
              nmoe_fused_fits<4, false, NMOE_XBF16>(n) && nmoe_fused_fits<4, false, NMOE_XF32>(n) &&
              nmoe_fused_fits<2, false, NMOE_XBF16>(n) && nmoe_fused_fits<2, false, NMOE_XF32>(n);
     ctx->fused_blocks = ok ? NMOE_FUSED_BLOCKS : 0;
-    size_t need = (size_t)(NMOE_XCH_YPART + NMOE_FUSED_GROUPS * NMOE_HIDDEN) * sizeof(float);
-    if (hipMalloc((void **)&ctx->xch, need) != hipSuccess) return NMOE_HIP_ENOMEM;
-    if (hipMemset(ctx->xch, 0, need) != hipSuccess) return NMOE_HIP_EHIP;
+    ctx->xch_bytes = (size_t)NMOE_XCH_WORDS * sizeof(uint64_t);
+    if (hipMalloc((void **)&ctx->xch, ctx->xch_bytes) != hipSuccess) return NMOE_HIP_ENOMEM;
+    if (hipMemset(ctx->xch, 0, ctx->xch_bytes) != hipSuccess) return NMOE_HIP_EHIP;
     return NMOE_HIP_OK;
 }
 

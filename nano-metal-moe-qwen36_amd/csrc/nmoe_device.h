@@ -352,6 +352,19 @@ __device__ __forceinline__ uint32_t nmoe_add_u32_dev(uint32_t *p, uint32_t v) {
     return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+/* Values exchanged between the blocks of one launch travel as 64-bit words
+ * (launch epoch << 32 | float bits), written and read whole with one
+ * device-coherent access: a consumer polls the data itself until every word
+ * carries the current epoch, so no separate counter round trip is needed. */
+__device__ __forceinline__ void nmoe_st_tagged(uint64_t *p, uint32_t epoch, float v) {
+    __hip_atomic_store(p, ((uint64_t)epoch << 32) | __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t nmoe_ld_tagged(const uint64_t *p) {
+    return __hip_atomic_load((uint64_t *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ bool nmoe_tag_is(uint64_t w, uint32_t epoch) { return (uint32_t)(w >> 32) == epoch; }
+__device__ __forceinline__ float nmoe_tag_val(uint64_t w) { return __uint_as_float((uint32_t)w); }
+
 /* Bounded spin so that a grid whose blocks are not all resident still ends:
  * the waiting block gives up, records the failure in the status word and
  * carries on (the result is then wrong, and the host reports ETIMEDOUT). */

@@ -46,7 +46,7 @@ struct nmoe_layout<2> {
 /* Device scratch words used by persistent kernels.  Each counter sits on
  * its own 128-byte line. */
 #define NMOE_SYNC_STATUS 0     /* set to 1 by a kernel whose bounded wait expired */
-#define NMOE_SYNC_WORDS 2048   /* status + group and chunk counters of the fused kernel */
+#define NMOE_SYNC_WORDS 8192   /* status + per-block launch epochs of the fused kernel */
 
 struct nmoe_pack_slot {
     void *dev;
@@ -75,7 +75,8 @@ struct nmoe_hip_ctx {
     uint32_t *idx;   /* [max_tokens][8] routing scratch for nmoe_moe_layer */
     float *w;        /* [max_tokens][8] */
     uint32_t *sync;  /* NMOE_SYNC_WORDS */
-    float *xch;      /* fused kernel's cross-block exchange (logits, act, partial y) */
+    uint64_t *xch;   /* fused kernel's cross-block exchange (tagged logits, act, partial y) */
+    size_t xch_bytes;
     int fused_blocks;     /* persistent decode grid (0 = not resident-capable) */
     int use_fused;        /* NMOE_HIP_OPT_FUSED_DECODE */
     char err[256];
