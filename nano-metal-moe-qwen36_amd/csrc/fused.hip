@@ -121,6 +121,16 @@ __device__ __forceinline__ void nmoe_x_cols(const void *x, int c0, int n, double
     }
 }
 
+/* LDS slot of act element e.  Lane dl of a down row reads float4 chunks
+ * dl*N .. dl*N+N-1 (N = CPL/4); chunk c of lane dl is stored at position
+ * (c + dl + dl/8) mod N of its lane's span, so the lanes of one LDS pass
+ * (8 or 16 consecutive dl, one chunk each) hit distinct banks. */
+template <int N>
+__device__ __forceinline__ int nmoe_act_slot(int e) {
+    const int f = e >> 2, dl = f / N, c = f % N;
+    return 4 * (dl * N + ((c + dl + (dl >> 3)) & (N - 1))) + (e & 3);
+}
+
 template <int BITS, bool ROUTE, int XMODE>
 __global__ void __launch_bounds__(256) nmoe_fused_decode_kernel(nmoe_fused_args a) {
     using Q = nmoe_q<BITS>;
@@ -149,18 +159,34 @@ __global__ void __launch_bounds__(256) nmoe_fused_decode_kernel(nmoe_fused_args 
     uint64_t *xact = a.xch + NMOE_XCH_ACT + g * NMOE_INTER;
     uint64_t *ypart = a.xch + NMOE_XCH_YPART;
 
-    if (tid == 0) {
-        uint32_t *ep = a.sync + NMOE_SYNC_EPOCH(blockIdx.x);
-        uint32_t e = nmoe_ld_u32_dev(ep) + 1u;
-        __hip_atomic_store(ep, e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        s_epoch = e;
+    /* Independent loads go out first and unconditionally (loads retire in
+     * order, so a later wait on one of them must not cover the big ones):
+     * the launch epoch, the exp2 table entry, the residual row this thread
+     * may combine; then this block's router rows and their x columns. */
+    uint32_t *ep = a.sync + NMOE_SYNC_EPOCH(blockIdx.x);
+    const uint32_t ep_old = nmoe_ld_u32_dev(ep);
+    const uint64_t tab_v = nmoe_fused_exp2_tab[tid & 31];
+    const int crow = j * NMOE_FUSED_CHUNK + (tid & (NMOE_FUSED_CHUNK - 1));
+    const float hm = a.h_mid[crow];
+    const float sh = a.shared_out != NULL ? a.shared_out[crow] : 0.0f;
+    const int e0 = NMOE_FUSED_GROUP_BLOCKS / 4 * j + 2 * wave; /* router rows 8j + 2*wave + {0,1} */
+    uint4 wv[2][4];
+    float xs_r[32];
+    if (ROUTE) {
+#pragma unroll
+        for (int r = 0; r < 2; r++) {
+            const uint4 *row = (const uint4 *)(a.router_w + (size_t)(e0 + r) * NMOE_HIDDEN);
+#pragma unroll
+            for (int q = 0; q < 4; q++) wv[r][q] = row[lane + 64 * q];
+        }
+        if (XMODE != NMOE_XNORM)
+#pragma unroll
+            for (int q = 0; q < 4; q++) nmoe_x_cols<XMODE>(a.x, (lane + 64 * q) * 8, 8, 1.0, xs_r + 8 * q);
     }
-    if (tid < 32) s_tab[tid] = nmoe_fused_exp2_tab[tid];
-    /* residual rows of this block's chunk (used by the combining blocks) */
-    float hm = 0.0f, sh = 0.0f;
-    if (g == 0 && tid < NMOE_FUSED_CHUNK) {
-        hm = a.h_mid[j * NMOE_FUSED_CHUNK + tid];
-        if (a.shared_out != NULL) sh = a.shared_out[j * NMOE_FUSED_CHUNK + tid];
+    if (tid < 32) s_tab[tid] = tab_v;
+    if (tid == 0) {
+        __hip_atomic_store(ep, ep_old + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_epoch = ep_old + 1u;
     }
     double rinv = 1.0;
     if (XMODE == NMOE_XNORM) rinv = 1.0 / (double)nmoe_block_rms_exact((const float *)a.x, a.eps, s_h, s_dd, s_f);
@@ -168,21 +194,13 @@ __global__ void __launch_bounds__(256) nmoe_fused_decode_kernel(nmoe_fused_args 
     const uint32_t epoch = s_epoch;
 
     if (ROUTE) {
-        /* ---- R: rows 8j + 2*wave + {0, 1} of the router, in group g */
-        const int e0 = NMOE_FUSED_GROUP_BLOCKS / 4 * j + 2 * wave; /* 8j + 2*wave */
-        uint4 wv[2][4];
+        /* ---- R: two router rows per wavefront, in group g */
+        if (XMODE == NMOE_XNORM)
+#pragma unroll
+            for (int q = 0; q < 4; q++) nmoe_x_cols<XMODE>(a.x, (lane + 64 * q) * 8, 8, rinv, xs_r + 8 * q);
 #pragma unroll
         for (int r = 0; r < 2; r++) {
-            const uint4 *row = (const uint4 *)(a.router_w + (size_t)(e0 + r) * NMOE_HIDDEN);
-#pragma unroll
-            for (int q = 0; q < 4; q++) wv[r][q] = row[lane + 64 * q];
-        }
-        float xs[32];
-#pragma unroll
-        for (int q = 0; q < 4; q++) nmoe_x_cols<XMODE>(a.x, (lane + 64 * q) * 8, 8, rinv, xs + 8 * q);
-#pragma unroll
-        for (int r = 0; r < 2; r++) {
-            float logit = nmoe_router_row_bf16(wv[r], xs);
+            float logit = nmoe_router_row_bf16(wv[r], xs_r);
             if (lane == 0) nmoe_st_tagged(xlg + e0 + r, epoch, logit);
         }
         /* ---- T: wait for the group's 256 logits, route in every block */
@@ -235,6 +253,9 @@ __global__ void __launch_bounds__(256) nmoe_fused_decode_kernel(nmoe_fused_args 
     const int dsub = lane / Q::LPR_D, dl = lane % Q::LPR_D, dgrp = dl * Q::CPL / NMOE_GROUP;
     const int grow0 = j * NMOE_FUSED_GU_ROWS + 4 * wave + gsub;
     const int drow0 = j * NMOE_FUSED_CHUNK + 16 * wave + dsub;
+    /* x first: loads retire in order, so G can start while down rows stream */
+    float xs[Q::CPL];
+    nmoe_x_cols<XMODE>(a.x, gl * Q::CPL, Q::CPL, rinv, xs);
     uint4 gwv[GSTEPS], uwv[GSTEPS], dwv[DSTEPS];
     uint32_t gsb[GSTEPS], usb[GSTEPS], dsb[DSTEPS]; /* scale | bias << 16 */
 #pragma unroll
@@ -254,10 +275,10 @@ __global__ void __launch_bounds__(256) nmoe_fused_decode_kernel(nmoe_fused_args 
         const uint16_t *ds = (const uint16_t *)(ex + L::down_s) + row * Q::GPR_D + dgrp;
         dsb[i] = (uint32_t)ds[0] | ((uint32_t)ds[NMOE_HIDDEN * Q::GPR_D] << 16);
     }
+    /* keep every weight load above in one burst: no compute hoisted into it */
+    __builtin_amdgcn_sched_barrier(0);
     /* ---- G: gate/up + SwiGLU -> act[g] */
     {
-        float xs[Q::CPL];
-        nmoe_x_cols<XMODE>(a.x, gl * Q::CPL, Q::CPL, rinv, xs);
         float xsum = 0.0f;
 #pragma unroll
         for (int c = 0; c < Q::CPL; c++) xsum += xs[c];
@@ -278,24 +299,25 @@ __global__ void __launch_bounds__(256) nmoe_fused_decode_kernel(nmoe_fused_args 
         const uint64_t *pa[2] = {xact + tid, xact + tid + 256};
         float av[2];
         nmoe_poll<2>(pa, epoch, av, status);
-        s_act[tid] = av[0];
-        s_act[tid + 256] = av[1];
+        s_act[nmoe_act_slot<Q::CPL / 4>(tid)] = av[0];
+        s_act[nmoe_act_slot<Q::CPL / 4>(tid + 256)] = av[1];
     }
     __syncthreads();
+    /* this lane's CPL act columns, read once (conflict-free: swizzled) */
+    float as[Q::CPL];
+#pragma unroll
+    for (int c = 0; c < Q::CPL / 4; c++) {
+        float4 t = ((const float4 *)s_act)[nmoe_act_slot<Q::CPL / 4>(4 * (dl * (Q::CPL / 4) + c)) / 4];
+        as[4 * c] = t.x;
+        as[4 * c + 1] = t.y;
+        as[4 * c + 2] = t.z;
+        as[4 * c + 3] = t.w;
+    }
+    float asum = 0.0f;
+#pragma unroll
+    for (int c = 0; c < Q::CPL; c++) asum += as[c];
 #pragma unroll
     for (int i = 0; i < DSTEPS; i++) {
-        float as[Q::CPL];
-#pragma unroll
-        for (int c = 0; c < Q::CPL / 4; c++) {
-            float4 t = ((const float4 *)(s_act + dl * Q::CPL))[c];
-            as[4 * c] = t.x;
-            as[4 * c + 1] = t.y;
-            as[4 * c + 2] = t.z;
-            as[4 * c + 3] = t.w;
-        }
-        float asum = 0.0f;
-#pragma unroll
-        for (int c = 0; c < Q::CPL; c++) asum += as[c];
         float y = __builtin_fmaf(nmoe_bf16f(dsb[i] & 0xffffu), nmoe_dot16<BITS>(dwv[i], as),
                                  nmoe_bf16f(dsb[i] >> 16) * asum);
         y = nmoe_dpp_group_sum<Q::LPR_D>(y);
