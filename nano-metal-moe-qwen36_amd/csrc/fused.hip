@@ -15,10 +15,10 @@
  *
  *   N  (stack variant) every block derives x = RMSNorm(h) itself, bit-exact
  *      with math.m:34-65.
- *   R  group g computes all 256 logits (block j: rows 8j..8j+7; the router
- *      is re-read by the 8 groups, mostly from the last-level cache).
- *   T  every block waits for its group's 256 logits and routes the token
- *      (bit-exact math.m softmax / top-k / renormalise in one wavefront).
+ *   R  block b computes router row b in its first wavefront: the 1 MB
+ *      router is read once per step (one 4 KB row per block).
+ *   T  every block waits for all 256 logits and routes the token (bit-exact
+ *      math.m softmax / top-k / renormalise in one wavefront).
  *   P  block j of group g issues all weight loads of slot g at once: gate/up
  *      rows 16j..16j+15 and down rows 64j..64j+63 (~55 KB per block, the
  *      whole 14 MB of expert weights in flight across the grid).
@@ -54,7 +54,7 @@ static __constant__ uint64_t nmoe_fused_exp2_tab[32] = NMOE_EXP2_TAB32;
 
 /* exchange scratch layout (64-bit tagged words) */
 #define NMOE_XCH_LOGITS 0
-#define NMOE_XCH_ACT (NMOE_FUSED_GROUPS * NMOE_EXPERTS)
+#define NMOE_XCH_ACT NMOE_EXPERTS
 #define NMOE_XCH_YPART (NMOE_XCH_ACT + NMOE_FUSED_GROUPS * NMOE_INTER)
 #define NMOE_XCH_WORDS (NMOE_XCH_YPART + NMOE_FUSED_GROUPS * NMOE_HIDDEN)
 
@@ -86,16 +86,22 @@ struct nmoe_fused_args {
  * values.  Each lane polls its own words. */
 template <int N>
 __device__ __forceinline__ void nmoe_poll(const uint64_t *const p[N], uint32_t epoch, float v[N], uint32_t *status) {
-    uint32_t spins = 0;
+    /* a word, once seen with this epoch, is not loaded again: after the
+     * first round only the stragglers' words are re-polled, which keeps the
+     * polling traffic off the memory channels the late writers need */
+    uint32_t need = (1u << N) - 1u, spins = 0;
     for (;;) {
-        bool ready = true;
+        uint64_t w[N];
 #pragma unroll
-        for (int i = 0; i < N; i++) {
-            uint64_t w = nmoe_ld_tagged(p[i]);
-            ready = ready && nmoe_tag_is(w, epoch);
-            v[i] = nmoe_tag_val(w);
-        }
-        if (ready) return;
+        for (int i = 0; i < N; i++) /* all loads of a round in flight together */
+            if (need & (1u << i)) w[i] = nmoe_ld_tagged(p[i]);
+#pragma unroll
+        for (int i = 0; i < N; i++)
+            if ((need & (1u << i)) && nmoe_tag_is(w[i], epoch)) {
+                v[i] = nmoe_tag_val(w[i]);
+                need &= ~(1u << i);
+            }
+        if (need == 0) return;
         __builtin_amdgcn_s_sleep(1);
         if (++spins > NMOE_SPIN_LIMIT) {
             __hip_atomic_store(status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -155,30 +161,26 @@ __global__ void __launch_bounds__(256) nmoe_fused_decode_kernel(nmoe_fused_args 
     const int g = blockIdx.x % NMOE_FUSED_GROUPS, j = blockIdx.x / NMOE_FUSED_GROUPS;
     const int k = a.k;
     uint32_t *status = a.sync + NMOE_SYNC_STATUS;
-    uint64_t *xlg = a.xch + NMOE_XCH_LOGITS + g * NMOE_EXPERTS;
+    uint64_t *xlg = a.xch + NMOE_XCH_LOGITS;
     uint64_t *xact = a.xch + NMOE_XCH_ACT + g * NMOE_INTER;
     uint64_t *ypart = a.xch + NMOE_XCH_YPART;
 
     /* Independent loads go out first and unconditionally (loads retire in
      * order, so a later wait on one of them must not cover the big ones):
      * the launch epoch, the exp2 table entry, the residual row this thread
-     * may combine; then this block's router rows and their x columns. */
+     * may combine; then this block's router row and its x columns. */
     uint32_t *ep = a.sync + NMOE_SYNC_EPOCH(blockIdx.x);
     const uint32_t ep_old = nmoe_ld_u32_dev(ep);
     const uint64_t tab_v = nmoe_fused_exp2_tab[tid & 31];
     const int crow = j * NMOE_FUSED_CHUNK + (tid & (NMOE_FUSED_CHUNK - 1));
     const float hm = a.h_mid[crow];
     const float sh = a.shared_out != NULL ? a.shared_out[crow] : 0.0f;
-    const int e0 = NMOE_FUSED_GROUP_BLOCKS / 4 * j + 2 * wave; /* router rows 8j + 2*wave + {0,1} */
-    uint4 wv[2][4];
+    uint4 wv[4];
     float xs_r[32];
-    if (ROUTE) {
+    if (ROUTE && wave == 0) {
+        const uint4 *row = (const uint4 *)(a.router_w + (size_t)blockIdx.x * NMOE_HIDDEN);
 #pragma unroll
-        for (int r = 0; r < 2; r++) {
-            const uint4 *row = (const uint4 *)(a.router_w + (size_t)(e0 + r) * NMOE_HIDDEN);
-#pragma unroll
-            for (int q = 0; q < 4; q++) wv[r][q] = row[lane + 64 * q];
-        }
+        for (int q = 0; q < 4; q++) wv[q] = row[lane + 64 * q];
         if (XMODE != NMOE_XNORM)
 #pragma unroll
             for (int q = 0; q < 4; q++) nmoe_x_cols<XMODE>(a.x, (lane + 64 * q) * 8, 8, 1.0, xs_r + 8 * q);
@@ -194,17 +196,14 @@ __global__ void __launch_bounds__(256) nmoe_fused_decode_kernel(nmoe_fused_args 
     const uint32_t epoch = s_epoch;
 
     if (ROUTE) {
-        /* ---- R: two router rows per wavefront, in group g */
-        if (XMODE == NMOE_XNORM)
-#pragma unroll
-            for (int q = 0; q < 4; q++) nmoe_x_cols<XMODE>(a.x, (lane + 64 * q) * 8, 8, rinv, xs_r + 8 * q);
-#pragma unroll
-        for (int r = 0; r < 2; r++) {
-            float logit = nmoe_router_row_bf16(wv[r], xs_r);
-            if (lane == 0) nmoe_st_tagged(xlg + e0 + r, epoch, logit);
-        }
-        /* ---- T: wait for the group's 256 logits, route in every block */
+        /* ---- R + T in the first wavefront: router row blockIdx.x, then wait
+         * for all 256 logits and route */
         if (wave == 0) {
+            if (XMODE == NMOE_XNORM)
+#pragma unroll
+                for (int q = 0; q < 4; q++) nmoe_x_cols<XMODE>(a.x, (lane + 64 * q) * 8, 8, rinv, xs_r + 8 * q);
+            float logit = nmoe_router_row_bf16(wv, xs_r);
+            if (lane == 0) nmoe_st_tagged(xlg + blockIdx.x, epoch, logit);
             const uint64_t *pl[4] = {xlg + lane, xlg + lane + 64, xlg + lane + 128, xlg + lane + 192};
             float lv[4];
             nmoe_poll<4>(pl, epoch, lv, status);
@@ -335,19 +334,24 @@ __global__ void __launch_bounds__(256) nmoe_fused_decode_kernel(nmoe_fused_args 
         /* one polling round loads all K-1 partials at once */
         float ys[NMOE_MAX_K];
         ys[0] = s_y[tid];
-        uint32_t spins = 0;
-        for (;;) {
-            bool ready = true;
+        uint32_t need = 0, spins = 0;
 #pragma unroll
-            for (int s = 1; s < NMOE_MAX_K; s++) {
-                ys[s] = 0.0f;
-                if (s < k) {
-                    uint64_t w = nmoe_ld_tagged(ypart + s * NMOE_HIDDEN + row);
-                    ready = ready && nmoe_tag_is(w, epoch);
-                    ys[s] = nmoe_tag_val(w);
+        for (int s = 1; s < NMOE_MAX_K; s++) {
+            ys[s] = 0.0f;
+            if (s < k) need |= 1u << s;
+        }
+        for (;;) {
+            uint64_t w[NMOE_MAX_K];
+#pragma unroll
+            for (int s = 1; s < NMOE_MAX_K; s++)
+                if (need & (1u << s)) w[s] = nmoe_ld_tagged(ypart + s * NMOE_HIDDEN + row);
+#pragma unroll
+            for (int s = 1; s < NMOE_MAX_K; s++)
+                if ((need & (1u << s)) && nmoe_tag_is(w[s], epoch)) {
+                    ys[s] = nmoe_tag_val(w[s]);
+                    need &= ~(1u << s);
                 }
-            }
-            if (ready) break;
+            if (need == 0) break;
             __builtin_amdgcn_s_sleep(1);
             if (++spins > NMOE_SPIN_LIMIT) {
                 __hip_atomic_store(status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
