@@ -91,8 +91,14 @@ NMOE_HIP_API int nmoe_hip_check_device_status(nmoe_hip_ctx *ctx);
 /* Path options (the counterpart of the reference's experiment toggles,
  * NMOE_FUSED_DOWN_COMBINE_Q4 / NMOE_PIPELINE etc., runtime.m:1426-1496).
  * NMOE_HIP_OPT_FUSED_DECODE (default 1): single-token calls run as one
- * persistent cooperative launch; 0 selects the multi-launch kernels. */
+ * persistent launch; 0 selects the multi-launch kernels.
+ * NMOE_HIP_OPT_XCD_LOCAL (default 1 where the device deals the blocks of a
+ * launch round-robin over its 8 accelerator dies, checked at create): the
+ * fused launch exchanges values that stay within a group of blocks on one
+ * die through that die's L2; 0 sends them through device-coherent memory
+ * like the rest. */
 #define NMOE_HIP_OPT_FUSED_DECODE 1
+#define NMOE_HIP_OPT_XCD_LOCAL 2
 NMOE_HIP_API int nmoe_hip_set_option(nmoe_hip_ctx *ctx, int option, int value);
 
 /* ---- buffers (backend.h:64-66: register_shared_buffer / register_state_buffer

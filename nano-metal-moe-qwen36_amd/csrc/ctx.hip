@@ -96,6 +96,12 @@ extern "C" int nmoe_hip_set_option(nmoe_hip_ctx *ctx, int option, int value) {
         ctx->use_fused = value != 0;
         return NMOE_HIP_OK;
     }
+    if (option == NMOE_HIP_OPT_XCD_LOCAL) {
+        if (value != 0 && !ctx->xcd_placed)
+            return nmoe_fail(ctx, NMOE_HIP_EINVAL, "this device does not deal a launch's blocks round-robin over 8 dies");
+        ctx->use_xcd_local = value != 0;
+        return NMOE_HIP_OK;
+    }
     return nmoe_fail(ctx, NMOE_HIP_EINVAL, "unknown option %d", option);
 }
 
@@ -117,10 +123,20 @@ extern "C" int nmoe_hip_check_device_status(nmoe_hip_ctx *ctx) {
     NMOE_HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
     NMOE_HIP_TRY(ctx, hipMemcpy(&status, ctx->sync + NMOE_SYNC_STATUS, sizeof(status), hipMemcpyDeviceToHost));
     if (status != 0) {
-        /* restart the launch epochs and clear every tagged exchange word, so
-         * no stale word can carry a future epoch */
-        NMOE_HIP_TRY(ctx, hipMemset(ctx->sync, 0, NMOE_SYNC_WORDS * sizeof(uint32_t)));
-        if (ctx->xch != NULL) NMOE_HIP_TRY(ctx, hipMemset(ctx->xch, 0, ctx->xch_bytes));
+        /* An aborted launch leaves the blocks' epochs unequal and combine
+         * counters part-counted.  Every epoch moves past the largest one
+         * (exchange words only ever carry past epochs, so none can match a
+         * future one -- including copies still held in a die's L2), and the
+         * counters and the status restart from 0. */
+        static uint32_t words[NMOE_SYNC_WORDS];
+        NMOE_HIP_TRY(ctx, hipMemcpy(words, ctx->sync, sizeof(words), hipMemcpyDeviceToHost));
+        uint32_t top = 0;
+        for (int b = 0; b < NMOE_SYNC_BLOCKS; b++)
+            if (words[NMOE_SYNC_EPOCH(b)] > top) top = words[NMOE_SYNC_EPOCH(b)];
+        for (int b = 0; b < NMOE_SYNC_BLOCKS; b++) words[NMOE_SYNC_EPOCH(b)] = top + 1u;
+        for (int c = 0; c < NMOE_SYNC_BLOCKS / 8; c++) words[NMOE_SYNC_COMBINE(c)] = 0u;
+        words[NMOE_SYNC_STATUS] = 0u;
+        NMOE_HIP_TRY(ctx, hipMemcpy(ctx->sync, words, sizeof(words), hipMemcpyHostToDevice));
         NMOE_HIP_TRY(ctx, hipDeviceSynchronize());
         return nmoe_fail(ctx, NMOE_HIP_ETIMEDOUT, "a persistent kernel's bounded wait expired (status %u)", status);
     }

@@ -8,7 +8,8 @@
  * (kernels.metal:562-640), down + weighted combine (kernels.metal:1456-1542)
  * and the next layer's input RMSNorm (runtime.m:2893-2900) -- three
  * host/device crossings per layer.  Here the layer pack is resident in HBM
- * and the step is one launch of 256 blocks x 4 wavefronts.
+ * and the step is one launch of 256 blocks x 5 wavefronts (4 workers that
+ * stream and multiply expert rows, 1 control wavefront that routes).
  *
  * Blocks form 8 groups of 32 (group g = block % 8, j = block / 8); group g
  * streams expert slot g.
@@ -25,17 +26,24 @@
  *   G  gate/up dot products + SwiGLU -> act[g][512].
  *   D  block j waits for act[g], computes y_g = down_g . act[g] for rows
  *      64j..64j+63 -> ypart[g].
- *   C  block j of group 0 waits for the K partials of its rows and combines
+ *   C  the last of the K blocks j to count in on chunk j's counter combines
  *      out = h_mid + sum_s w_s y_s (+ sigmoid(g) * shared) in slot order.
  *
- * Values cross blocks as 64-bit (epoch, value) words written and read with
- * one device-coherent (sc1) access each; a consumer polls the words it needs
- * until all carry this launch's epoch.  That merges "wait" and "fetch" into
- * one memory round trip: no barrier counter, no same-address atomics, no
+ * Routing runs in a control wavefront per block: the candidates (the k
+ * largest logits) are handed to the workers one selection round at a time,
+ * so group s starts streaming expert s while later rounds and the exact
+ * softmax / top-k still run; the exact result confirms each group's expert
+ * (or re-points it, on probability ties) before act is published.
+ *
+ * Values a block waits for cross blocks as 64-bit (epoch, value) words
+ * written and read with one device-coherent (sc1) access each; a consumer
+ * polls the words it needs until all carry this launch's epoch.  That merges
+ * "wait" and "fetch" into one memory round trip: no barrier counter and no
  * L2-wide cache maintenance.  The epoch is the launch count, kept per block
- * (each block increments its own word once per launch, so all agree).  A
- * group's barrier-free hand-offs also mean idle groups (K < 8) simply exit.
- * Every wait is bounded.
+ * (each block increments its own word once per launch, so all agree).  The
+ * combine needs no waiting at all: the K partials of a chunk meet at an
+ * arrival counter, and only the last arrival reads the others.  Idle
+ * groups (K < 8) exit after their router row.  Every wait is bounded.
  */
 #include "nmoe_device.h"
 
@@ -48,9 +56,9 @@ static __constant__ uint64_t nmoe_fused_exp2_tab[32] = NMOE_EXP2_TAB32;
 #define NMOE_FUSED_GROUP_BLOCKS (NMOE_FUSED_BLOCKS / NMOE_FUSED_GROUPS) /* 32 */
 #define NMOE_FUSED_CHUNK (NMOE_HIDDEN / NMOE_FUSED_GROUP_BLOCKS)         /* 64 output rows per block */
 #define NMOE_FUSED_GU_ROWS (NMOE_INTER / NMOE_FUSED_GROUP_BLOCKS)        /* 16 gate/up rows per block */
+#define NMOE_FUSED_THREADS 320 /* 4 worker wavefronts + the control wavefront */
+#define NMOE_FUSED_CTRL 4
 
-/* sync words: per-block launch epochs, 64 bytes apart */
-#define NMOE_SYNC_EPOCH(b) (64 + 16 * (b))
 
 /* exchange scratch layout (64-bit tagged words) */
 /* Words that many blocks poll sit 64 bytes apart (SP words): polling a
@@ -61,7 +69,7 @@ static __constant__ uint64_t nmoe_fused_exp2_tab[32] = NMOE_EXP2_TAB32;
 #define NMOE_XCH_LOGITS 0
 #define NMOE_XCH_ACT (NMOE_XCH_SP * NMOE_EXPERTS)
 #define NMOE_XCH_YPART (NMOE_XCH_ACT + NMOE_XCH_SP * NMOE_FUSED_GROUPS * NMOE_INTER)
-#define NMOE_XCH_WORDS (NMOE_XCH_YPART + NMOE_FUSED_GROUPS * NMOE_HIDDEN)
+#define NMOE_XCH_WORDS (NMOE_XCH_YPART + NMOE_FUSED_GROUPS * NMOE_HIDDEN / 2) /* partials: fp32 */
 
 /* x sources: XF32 / XBF16 = activations given; XNORM = x is RMSNorm(h). */
 #define NMOE_XF32 0
@@ -85,12 +93,35 @@ struct nmoe_fused_args {
     float *logits_out;
     uint64_t *xch;
     uint32_t *sync;
+    int xcd_local; /* act travels through the die's L2 (a group's blocks share a die) */
 };
+
+/* Die-local exchange: words written and read only by blocks of one
+ * accelerator die meet in that die's L2.  The store is a plain one (the
+ * vector L1 writes through to L2, and the line stays there); the load is a
+ * system-scope one (sc0 sc1), which bypasses the L1 and is served by the
+ * L2.  Round trip about 0.55 us instead of 0.85 us through device-coherent
+ * memory, and no traffic on the fabric the expert rows stream over. */
+__device__ __forceinline__ void nmoe_st_tagged_die(uint64_t *p, uint32_t epoch, float v) {
+    const uint64_t w = ((uint64_t)epoch << 32) | __float_as_uint(v);
+    asm volatile("global_store_dwordx2 %0, %1, off" ::"v"(p), "v"(w) : "memory");
+}
+__device__ __forceinline__ uint64_t nmoe_ld_tagged_die(const uint64_t *p) {
+    return __hip_atomic_load((uint64_t *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
+/* Accelerator die (XCC) the calling wave runs on. */
+__device__ __forceinline__ uint32_t nmoe_xcc_id() {
+    uint32_t v;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID, 0, 4)" : "=s"(v));
+    return v;
+}
 
 /* Polls n tagged words until all carry `epoch` (bounded); returns the
  * values.  Each lane polls its own words. */
 template <int N>
-__device__ __forceinline__ void nmoe_poll(const uint64_t *const p[N], uint32_t epoch, float v[N], uint32_t *status) {
+__device__ __forceinline__ void nmoe_poll(const uint64_t *const p[N], uint32_t epoch, float v[N], uint32_t *status,
+                                          bool die_local = false) {
     /* a word, once seen with this epoch, is not loaded again: after the
      * first round only the stragglers' words are re-polled, which keeps the
      * polling traffic off the memory channels the late writers need */
@@ -99,7 +130,7 @@ __device__ __forceinline__ void nmoe_poll(const uint64_t *const p[N], uint32_t e
         uint64_t w[N];
 #pragma unroll
         for (int i = 0; i < N; i++) /* all loads of a round in flight together */
-            if (need & (1u << i)) w[i] = nmoe_ld_tagged(p[i]);
+            if (need & (1u << i)) w[i] = die_local ? nmoe_ld_tagged_die(p[i]) : nmoe_ld_tagged(p[i]);
 #pragma unroll
         for (int i = 0; i < N; i++)
             if ((need & (1u << i)) && nmoe_tag_is(w[i], epoch)) {
@@ -107,6 +138,19 @@ __device__ __forceinline__ void nmoe_poll(const uint64_t *const p[N], uint32_t e
                 need &= ~(1u << i);
             }
         if (need == 0) return;
+        __builtin_amdgcn_s_sleep(1);
+        if (++spins > NMOE_SPIN_LIMIT) {
+            __hip_atomic_store(status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            return;
+        }
+    }
+}
+
+/* Waits (bounded) until the LDS word *w exceeds v: a hand-off from another
+ * wavefront of the block that needs no block-wide barrier. */
+__device__ __forceinline__ void nmoe_lds_wait_above(uint32_t *w, uint32_t v, uint32_t *status) {
+    uint32_t spins = 0;
+    while (__hip_atomic_load(w, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) <= v) {
         __builtin_amdgcn_s_sleep(1);
         if (++spins > NMOE_SPIN_LIMIT) {
             __hip_atomic_store(status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -143,37 +187,41 @@ __device__ __forceinline__ int nmoe_act_slot(int e) {
 }
 
 template <int BITS, bool ROUTE, int XMODE>
-__global__ void __launch_bounds__(256) nmoe_fused_decode_kernel(nmoe_fused_args a) {
+__global__ void __launch_bounds__(NMOE_FUSED_THREADS) nmoe_fused_decode_kernel(nmoe_fused_args a) {
     using Q = nmoe_q<BITS>;
     using L = nmoe_layout<BITS>;
     constexpr int RPS = NMOE_WAVE / Q::LPR_G;   /* gate/up rows per wave step: 1 (q4) / 2 (q2) */
-    constexpr int GSTEPS = 4 / RPS;             /* 4 gate/up rows per wavefront */
+    constexpr int GSTEPS = 4 / RPS;             /* 4 gate/up rows per worker wavefront */
     constexpr int RPW_D = NMOE_WAVE / Q::LPR_D; /* down rows per wave step: 4 (q4) / 8 (q2) */
-    constexpr int DSTEPS = 16 / RPW_D;          /* 16 down rows per wavefront */
+    constexpr int DSTEPS = 16 / RPW_D;          /* 16 down rows per worker wavefront */
     __shared__ uint64_t s_tab[32];
-    __shared__ float s_lg[NMOE_EXPERTS];
     __shared__ float s_scratch[NMOE_EXPERTS];
     __shared__ float s_act[NMOE_INTER];
     __shared__ float s_y[NMOE_FUSED_CHUNK];
-    __shared__ uint32_t s_idx[NMOE_MAX_K];
+    __shared__ uint32_t s_t[4 * NMOE_MAX_K];
+    __shared__ uint32_t s_cand[NMOE_MAX_K];  /* expert group g starts loading */
+    __shared__ uint32_t s_gx[NMOE_MAX_K];    /* expert group g streams */
+    __shared__ uint32_t s_slotg[NMOE_MAX_K]; /* group streaming slot s */
     __shared__ float s_w[NMOE_MAX_K];
     __shared__ double s_dd[8];
     __shared__ float s_f[1];
     __shared__ uint32_t s_epoch;
+    __shared__ uint32_t s_ncand, s_confirm; /* control -> workers hand-offs */
     __shared__ float s_h[XMODE == NMOE_XNORM ? NMOE_HIDDEN : 1];
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const bool ctrl = wave == NMOE_FUSED_CTRL;
     const int g = blockIdx.x % NMOE_FUSED_GROUPS, j = blockIdx.x / NMOE_FUSED_GROUPS;
     const int k = a.k;
     uint32_t *status = a.sync + NMOE_SYNC_STATUS;
     uint64_t *xlg = a.xch + NMOE_XCH_LOGITS;
     uint64_t *xact = a.xch + NMOE_XCH_ACT + NMOE_XCH_SP * g * NMOE_INTER;
-    uint64_t *ypart = a.xch + NMOE_XCH_YPART;
+    float *ypart = (float *)(a.xch + NMOE_XCH_YPART);
 
     /* Independent loads go out first and unconditionally (loads retire in
      * order, so a later wait on one of them must not cover the big ones):
      * the launch epoch, the exp2 table entry, the residual row this thread
-     * may combine; then this block's router row and its x columns. */
+     * may combine; then the control wavefront's router row and x columns. */
     uint32_t *ep = a.sync + NMOE_SYNC_EPOCH(blockIdx.x);
     const uint32_t ep_old = nmoe_ld_u32_dev(ep);
     const uint64_t tab_v = nmoe_fused_exp2_tab[tid & 31];
@@ -181,8 +229,9 @@ __global__ void __launch_bounds__(256) nmoe_fused_decode_kernel(nmoe_fused_args 
     const float hm = a.h_mid[crow];
     const float sh = a.shared_out != NULL ? a.shared_out[crow] : 0.0f;
     uint4 wv[4];
-    float xs_r[32];
-    if (ROUTE && wave == 0) {
+    float xs_r[32], lv[4];
+    uint32_t cand[NMOE_MAX_K];
+    if (ROUTE && ctrl) {
         const uint4 *row = (const uint4 *)(a.router_w + (size_t)blockIdx.x * NMOE_HIDDEN);
 #pragma unroll
         for (int q = 0; q < 4; q++) wv[q] = row[lane + 64 * q];
@@ -194,183 +243,289 @@ __global__ void __launch_bounds__(256) nmoe_fused_decode_kernel(nmoe_fused_args 
     if (tid == 0) {
         __hip_atomic_store(ep, ep_old + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         s_epoch = ep_old + 1u;
+        s_ncand = 0u;
+        s_confirm = 0u;
     }
     double rinv = 1.0;
     if (XMODE == NMOE_XNORM) rinv = 1.0 / (double)nmoe_block_rms_exact((const float *)a.x, a.eps, s_h, s_dd, s_f);
     __syncthreads();
     const uint32_t epoch = s_epoch;
 
-    if (ROUTE) {
-        /* ---- R + T in the first wavefront: router row blockIdx.x, then wait
-         * for all 256 logits and route */
-        if (wave == 0) {
-            if (XMODE == NMOE_XNORM)
+    if (ROUTE && ctrl) {
+        /* the control wavefront shares a SIMD with a worker: its routing is
+         * on the critical path, the worker's multiply-adds mostly are not */
+        __builtin_amdgcn_s_setprio(2);
+        /* ---- R (control wavefront): router row blockIdx.x */
+        if (XMODE == NMOE_XNORM)
 #pragma unroll
-                for (int q = 0; q < 4; q++) nmoe_x_cols<XMODE>(a.x, (lane + 64 * q) * 8, 8, rinv, xs_r + 8 * q);
-            float logit = nmoe_router_row_bf16(wv, xs_r);
-            if (lane == 0) nmoe_st_tagged(xlg + NMOE_XCH_SP * blockIdx.x, epoch, logit);
+            for (int q = 0; q < 4; q++) nmoe_x_cols<XMODE>(a.x, (lane + 64 * q) * 8, 8, rinv, xs_r + 8 * q);
+        float logit = nmoe_router_row_bf16(wv, xs_r);
+        if (lane == 0) nmoe_st_tagged(xlg + NMOE_XCH_SP * blockIdx.x, epoch, logit);
+        if (g < k) {
+            /* ---- T: wait for all 256 logits; the candidates are the k
+             * largest logits, published one per selection round so that
+             * group s starts streaming its expert as soon as candidate s is
+             * known.  Their probabilities are the k largest too, up to
+             * ties, which the exact routing below settles. */
             const uint64_t *pl[4] = {xlg + NMOE_XCH_SP * lane, xlg + NMOE_XCH_SP * (lane + 64),
                                      xlg + NMOE_XCH_SP * (lane + 128), xlg + NMOE_XCH_SP * (lane + 192)};
-            float lv[4];
             nmoe_poll<4>(pl, epoch, lv, status);
+            uint32_t key[4], ck[NMOE_MAX_K];
 #pragma unroll
-            for (int q = 0; q < 4; q++) s_lg[lane + 64 * q] = lv[q];
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+            for (int q = 0; q < 4; q++) key[q] = nmoe_fkey(lv[q]);
+            nmoe_wave_top_keys(key, k, cand, ck, [&](int s, uint32_t e) {
+                if (lane == 0) {
+                    s_cand[s] = e;
+                    __hip_atomic_store(&s_ncand, (uint32_t)(s + 1), __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+                }
+            });
+            bool taken[4];
+#pragma unroll
+            for (int q = 0; q < 4; q++) taken[q] = key[q] == 0u; /* fkeys are never 0 */
+
+            /* ---- exact routing (under the expert loads), then the expert of
+             * each group: a candidate outside the exact selection (only
+             * possible on probability ties) hands its group to a selected
+             * expert no group holds yet */
             uint32_t si[NMOE_MAX_K];
             float sw[NMOE_MAX_K];
-            nmoe_wave_route(s_lg, NMOE_EXPERTS, k, s_scratch, s_tab, si, sw, NULL);
-            if (lane < NMOE_MAX_K) {
-                uint32_t vi = 0;
-                float vw = 0.0f;
+            nmoe_wave_route_cand(lv, k, taken, s_scratch, s_t, s_tab, si, sw);
+            uint32_t ct = 0, et = 0;
+            float wt = 0.0f;
+            bool c_in_e = false, e_in_c = false;
+#pragma unroll
+            for (int s = 0; s < NMOE_MAX_K; s++) {
+                if (s == lane) {
+                    ct = cand[s];
+                    et = si[s];
+                    wt = sw[s];
+                }
+            }
+#pragma unroll
+            for (int s = 0; s < NMOE_MAX_K; s++) {
+                if (s < k) {
+                    c_in_e = c_in_e || ct == si[s];
+                    e_in_c = e_in_c || et == cand[s];
+                }
+            }
+            const uint64_t fm = __ballot(lane < k && !c_in_e); /* groups to re-point */
+            const uint64_t mm = __ballot(lane < k && !e_in_c); /* slots no group holds */
+            uint32_t xg = ct;
+            if (fm != 0) {
+                const int fr = (int)__builtin_popcountll(fm & ((1ull << lane) - 1ull));
 #pragma unroll
                 for (int s = 0; s < NMOE_MAX_K; s++)
-                    if (s == lane) {
-                        vi = si[s];
-                        vw = sw[s];
-                    }
-                s_idx[lane] = vi;
-                s_w[lane] = vw;
-                if (blockIdx.x == 0 && a.idx_out != NULL) a.idx_out[lane] = vi;
-                if (blockIdx.x == 0 && a.w_out != NULL) a.w_out[lane] = vw;
+                    if (((mm >> s) & 1) && (int)__builtin_popcountll(mm & ((1ull << s) - 1ull)) == fr &&
+                        ((fm >> lane) & 1))
+                        xg = si[s];
             }
-            if (blockIdx.x == 0 && a.logits_out != NULL)
+            uint32_t sg = 0;
 #pragma unroll
-                for (int q = 0; q < 4; q++) a.logits_out[lane + 64 * q] = s_lg[lane + 64 * q];
-        }
-    } else {
-        if (tid < NMOE_MAX_K) {
-            uint32_t e = tid < k ? a.idx_in[tid] : 0u;
-            float wv = tid < k ? a.w_in[tid] : 0.0f;
-            /* an index outside the layer is an invalid slot: weight 0, as
-             * for a failed expert read (runtime.m:2977-2981) */
-            s_w[tid] = e < NMOE_EXPERTS ? wv : 0.0f;
-            s_idx[tid] = e < NMOE_EXPERTS ? e : 0u;
+            for (int q = 0; q < NMOE_MAX_K; q++)
+                if (q < k && (uint32_t)__builtin_amdgcn_readlane((int)xg, q) == et) sg = (uint32_t)q;
+            if (lane < NMOE_MAX_K) {
+                s_gx[lane] = xg;
+                s_slotg[lane] = sg;
+                s_w[lane] = wt;
+                s_t[lane] = et; /* written out at the end */
+            }
+            if (lane == 0) __hip_atomic_store(&s_confirm, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
         }
     }
-    __syncthreads();
-    if (g >= k) return; /* group g streams expert slot g */
-    const uint8_t *ex = a.pack + (size_t)s_idx[g] * L::expert_size;
+    if (!ROUTE) {
+        if (tid < NMOE_MAX_K) {
+            uint32_t e = tid < k ? a.idx_in[tid] : 0u;
+            float wv_in = tid < k ? a.w_in[tid] : 0.0f;
+            /* an index outside the layer is an invalid slot: weight 0, as
+             * for a failed expert read (runtime.m:2977-2981) */
+            s_w[tid] = e < NMOE_EXPERTS ? wv_in : 0.0f;
+            s_cand[tid] = e < NMOE_EXPERTS ? e : 0u;
+            s_gx[tid] = e < NMOE_EXPERTS ? e : 0u;
+            s_slotg[tid] = tid;
+        }
+        __syncthreads();
+    }
+    if (g >= k) return; /* group g streams one expert */
 
-    /* ---- P: issue all weight loads of this wavefront */
+    /* ---- P (workers): issue all weight loads of this wavefront */
     const int gsub = lane / Q::LPR_G, gl = lane % Q::LPR_G, ggrp = gl * Q::CPL / NMOE_GROUP;
     const int dsub = lane / Q::LPR_D, dl = lane % Q::LPR_D, dgrp = dl * Q::CPL / NMOE_GROUP;
     const int grow0 = j * NMOE_FUSED_GU_ROWS + 4 * wave + gsub;
     const int drow0 = j * NMOE_FUSED_CHUNK + 16 * wave + dsub;
-    /* x first: loads retire in order, so G can start while down rows stream */
-    float xs[Q::CPL];
-    nmoe_x_cols<XMODE>(a.x, gl * Q::CPL, Q::CPL, rinv, xs);
+    /* the burst holds raw loads only: unpacking x or combining a scale with
+     * its bias inside it would make the wave wait for those loads before
+     * issuing the rest */
+    constexpr int XV = XMODE == NMOE_XBF16 ? Q::CPL / 8 : Q::CPL / 4; /* 16-byte x chunks per lane */
+    uint4 xr[XV];
     uint4 gwv[GSTEPS], uwv[GSTEPS], dwv[DSTEPS];
-    uint32_t gsb[GSTEPS], usb[GSTEPS], dsb[DSTEPS]; /* scale | bias << 16 */
+    uint32_t gsc[GSTEPS], gbi[GSTEPS], usc[GSTEPS], ubi[GSTEPS], dsc[DSTEPS], dbi[DSTEPS];
+    auto load_expert = [&](uint32_t e) {
+        const uint8_t *ex = a.pack + (size_t)e * L::expert_size;
 #pragma unroll
-    for (int i = 0; i < GSTEPS; i++) {
-        int row = grow0 + i * RPS;
-        gwv[i] = ((const uint4 *)(ex + L::gate_w))[(size_t)row * (Q::WPR_G / 4) + gl];
-        uwv[i] = ((const uint4 *)(ex + L::up_w))[(size_t)row * (Q::WPR_G / 4) + gl];
-        const uint16_t *gs = (const uint16_t *)(ex + L::gate_s) + row * Q::GPR_G + ggrp;
-        const uint16_t *us = (const uint16_t *)(ex + L::up_s) + row * Q::GPR_G + ggrp;
-        gsb[i] = (uint32_t)gs[0] | ((uint32_t)gs[NMOE_INTER * Q::GPR_G] << 16);
-        usb[i] = (uint32_t)us[0] | ((uint32_t)us[NMOE_INTER * Q::GPR_G] << 16);
-    }
+        for (int i = 0; i < GSTEPS; i++) {
+            int row = grow0 + i * RPS;
+            gwv[i] = ((const uint4 *)(ex + L::gate_w))[(size_t)row * (Q::WPR_G / 4) + gl];
+            uwv[i] = ((const uint4 *)(ex + L::up_w))[(size_t)row * (Q::WPR_G / 4) + gl];
+            const uint16_t *gs = (const uint16_t *)(ex + L::gate_s) + row * Q::GPR_G + ggrp;
+            const uint16_t *us = (const uint16_t *)(ex + L::up_s) + row * Q::GPR_G + ggrp;
+            gsc[i] = gs[0];
+            gbi[i] = gs[NMOE_INTER * Q::GPR_G];
+            usc[i] = us[0];
+            ubi[i] = us[NMOE_INTER * Q::GPR_G];
+        }
+        __builtin_amdgcn_sched_barrier(0); /* gate/up rows ahead of the down rows */
 #pragma unroll
-    for (int i = 0; i < DSTEPS; i++) {
-        int row = drow0 + i * RPW_D;
-        dwv[i] = ((const uint4 *)(ex + L::down_w))[(size_t)row * (Q::WPR_D / 4) + dl];
-        const uint16_t *ds = (const uint16_t *)(ex + L::down_s) + row * Q::GPR_D + dgrp;
-        dsb[i] = (uint32_t)ds[0] | ((uint32_t)ds[NMOE_HIDDEN * Q::GPR_D] << 16);
+        for (int i = 0; i < DSTEPS; i++) {
+            int row = drow0 + i * RPW_D;
+            dwv[i] = ((const uint4 *)(ex + L::down_w))[(size_t)row * (Q::WPR_D / 4) + dl];
+            const uint16_t *ds = (const uint16_t *)(ex + L::down_s) + row * Q::GPR_D + dgrp;
+            dsc[i] = ds[0];
+            dbi[i] = ds[NMOE_HIDDEN * Q::GPR_D];
+        }
+    };
+    uint32_t cand_g = 0;
+    if (!ctrl) {
+        /* x first: loads retire in order, so G can start while down rows stream */
+        const uint4 *xp = (const uint4 *)a.x + gl * XV;
+#pragma unroll
+        for (int c = 0; c < XV; c++) xr[c] = xp[c];
+        if (ROUTE) /* candidate g published by the control wavefront */
+            nmoe_lds_wait_above(&s_ncand, (uint32_t)g, status);
+        cand_g = s_cand[g];
+        __builtin_amdgcn_sched_barrier(0);
+        load_expert(cand_g);
+        /* keep every weight load above in one burst: no compute hoisted into it */
+        __builtin_amdgcn_sched_barrier(0);
     }
-    /* keep every weight load above in one burst: no compute hoisted into it */
-    __builtin_amdgcn_sched_barrier(0);
-    /* ---- G: gate/up + SwiGLU -> act[g] */
-    {
+    float xs[Q::CPL];
+#pragma unroll
+    for (int c = 0; c < XV; c++) {
+        if (XMODE == NMOE_XBF16) {
+            nmoe_unpack_bf16x8(xr[c], xs + 8 * c);
+        } else {
+            xs[4 * c] = __uint_as_float(xr[c].x);
+            xs[4 * c + 1] = __uint_as_float(xr[c].y);
+            xs[4 * c + 2] = __uint_as_float(xr[c].z);
+            xs[4 * c + 3] = __uint_as_float(xr[c].w);
+        }
+    }
+    if (XMODE == NMOE_XNORM)
+#pragma unroll
+        for (int c = 0; c < Q::CPL; c++) xs[c] = (float)((double)xs[c] * rinv);
+
+    /* ---- G (workers): gate/up + SwiGLU -> act[g], published once the
+     * control wavefront has confirmed the expert */
+    float actv[GSTEPS];
+    auto gate_up = [&]() {
         float xsum = 0.0f;
 #pragma unroll
         for (int c = 0; c < Q::CPL; c++) xsum += xs[c];
 #pragma unroll
         for (int i = 0; i < GSTEPS; i++) {
-            float gv = __builtin_fmaf(nmoe_bf16f(gsb[i] & 0xffffu), nmoe_dot16<BITS>(gwv[i], xs),
-                                      nmoe_bf16f(gsb[i] >> 16) * xsum);
-            float uv = __builtin_fmaf(nmoe_bf16f(usb[i] & 0xffffu), nmoe_dot16<BITS>(uwv[i], xs),
-                                      nmoe_bf16f(usb[i] >> 16) * xsum);
+            float gv = __builtin_fmaf(nmoe_bf16f(gsc[i]), nmoe_dot16<BITS>(gwv[i], xs), nmoe_bf16f(gbi[i]) * xsum);
+            float uv = __builtin_fmaf(nmoe_bf16f(usc[i]), nmoe_dot16<BITS>(uwv[i], xs), nmoe_bf16f(ubi[i]) * xsum);
             gv = nmoe_lanes_sum<Q::LPR_G>(gv);
             uv = nmoe_lanes_sum<Q::LPR_G>(uv);
-            if (gl == 0) nmoe_st_tagged(xact + NMOE_XCH_SP * (grow0 + i * RPS), epoch, nmoe_silu_dev(gv) * uv);
+            actv[i] = nmoe_silu_dev(gv) * uv;
+        }
+    };
+    if (!ctrl) {
+        gate_up();
+        if (ROUTE) {
+            nmoe_lds_wait_above(&s_confirm, 0u, status);
+            const uint32_t xg = s_gx[g];
+            if (xg != cand_g) { /* probability tie at the boundary: redo with the selected expert */
+                load_expert(xg);
+                gate_up();
+            }
+        }
+        if (gl == 0) {
+#pragma unroll
+            for (int i = 0; i < GSTEPS; i++) {
+                if (a.xcd_local)
+                    nmoe_st_tagged_die(xact + NMOE_XCH_SP * (grow0 + i * RPS), epoch, actv[i]);
+                else
+                    nmoe_st_tagged(xact + NMOE_XCH_SP * (grow0 + i * RPS), epoch, actv[i]);
+            }
         }
     }
 
-    /* ---- D: wait for act[g], then y_g for rows 64j..64j+63 */
-    {
+    /* ---- D (workers): wait for act[g], then y_g for rows 64j..64j+63 */
+    if (!ctrl) {
         const uint64_t *pa[2] = {xact + NMOE_XCH_SP * tid, xact + NMOE_XCH_SP * (tid + 256)};
         float av[2];
-        nmoe_poll<2>(pa, epoch, av, status);
+        nmoe_poll<2>(pa, epoch, av, status, a.xcd_local != 0);
         s_act[nmoe_act_slot<Q::CPL / 4>(tid)] = av[0];
         s_act[nmoe_act_slot<Q::CPL / 4>(tid + 256)] = av[1];
     }
     __syncthreads();
-    /* this lane's CPL act columns, read once (conflict-free: swizzled) */
-    float as[Q::CPL];
+    if (!ctrl) {
+        /* this lane's CPL act columns, read once (conflict-free: swizzled) */
+        float as[Q::CPL];
 #pragma unroll
-    for (int c = 0; c < Q::CPL / 4; c++) {
-        float4 t = ((const float4 *)s_act)[nmoe_act_slot<Q::CPL / 4>(4 * (dl * (Q::CPL / 4) + c)) / 4];
-        as[4 * c] = t.x;
-        as[4 * c + 1] = t.y;
-        as[4 * c + 2] = t.z;
-        as[4 * c + 3] = t.w;
-    }
-    float asum = 0.0f;
+        for (int c = 0; c < Q::CPL / 4; c++) {
+            float4 t = ((const float4 *)s_act)[nmoe_act_slot<Q::CPL / 4>(4 * (dl * (Q::CPL / 4) + c)) / 4];
+            as[4 * c] = t.x;
+            as[4 * c + 1] = t.y;
+            as[4 * c + 2] = t.z;
+            as[4 * c + 3] = t.w;
+        }
+        float asum = 0.0f;
 #pragma unroll
-    for (int c = 0; c < Q::CPL; c++) asum += as[c];
+        for (int c = 0; c < Q::CPL; c++) asum += as[c];
 #pragma unroll
-    for (int i = 0; i < DSTEPS; i++) {
-        float y = __builtin_fmaf(nmoe_bf16f(dsb[i] & 0xffffu), nmoe_dot16<BITS>(dwv[i], as),
-                                 nmoe_bf16f(dsb[i] >> 16) * asum);
-        y = nmoe_dpp_group_sum<Q::LPR_D>(y);
-        if (dl == 0) s_y[16 * wave + dsub + i * RPW_D] = y;
+        for (int i = 0; i < DSTEPS; i++) {
+            float y = __builtin_fmaf(nmoe_bf16f(dsc[i]), nmoe_dot16<BITS>(dwv[i], as), nmoe_bf16f(dbi[i]) * asum);
+            y = nmoe_dpp_group_sum<Q::LPR_D>(y);
+            if (dl == 0) s_y[16 * wave + dsub + i * RPW_D] = y;
+        }
     }
     __syncthreads();
+    /* ---- C: the last of the K groups to finish rows 64j..64j+63 combines
+     * them (out = h_mid + sum_s w_s y_s in slot order): each block j
+     * publishes its partial, then counts itself in on chunk j's counter;
+     * the block that completes the count reads the other partials.  Nobody
+     * waits, and the counter is left at 0 for the next launch. */
     const int row = j * NMOE_FUSED_CHUNK + tid;
-    if (g != 0) {
-        if (tid < NMOE_FUSED_CHUNK) nmoe_st_tagged(ypart + g * NMOE_HIDDEN + row, epoch, s_y[tid]);
-        return;
-    }
-
-    /* ---- C: block j of group 0 combines rows 64j..64j+63 over the K slots */
     if (tid < NMOE_FUSED_CHUNK) {
-        /* one polling round loads all K-1 partials at once */
-        float ys[NMOE_MAX_K];
-        ys[0] = s_y[tid];
-        uint32_t need = 0, spins = 0;
+        nmoe_st_dev(ypart + g * NMOE_HIDDEN + row, s_y[tid]);
+        __builtin_amdgcn_s_waitcnt(0); /* the partials are visible before the count */
+        uint32_t old = 0;
+        uint32_t *cnt = a.sync + NMOE_SYNC_COMBINE(j);
+        if (tid == 0) old = nmoe_add_u32_dev(cnt, 1u);
+        old = (uint32_t)__builtin_amdgcn_readfirstlane((int)old);
+        if (old == (uint32_t)k - 1u) {
+            float ys[NMOE_MAX_K];
 #pragma unroll
-        for (int s = 1; s < NMOE_MAX_K; s++) {
-            ys[s] = 0.0f;
-            if (s < k) need |= 1u << s;
-        }
-        for (;;) {
-            uint64_t w[NMOE_MAX_K];
+            for (int q = 0; q < NMOE_MAX_K; q++)
+                ys[q] = q == g ? s_y[tid] : (q < k ? nmoe_ld_dev(ypart + q * NMOE_HIDDEN + row) : 0.0f);
+            /* slot order: slot s is streamed by group s_slotg[s] */
+            float moe = 0.0f;
 #pragma unroll
-            for (int s = 1; s < NMOE_MAX_K; s++)
-                if (need & (1u << s)) w[s] = nmoe_ld_tagged(ypart + s * NMOE_HIDDEN + row);
+            for (int s = 0; s < NMOE_MAX_K; s++) {
+                if (s < k) {
+                    const uint32_t sg = s_slotg[s];
+                    float y = ys[0];
 #pragma unroll
-            for (int s = 1; s < NMOE_MAX_K; s++)
-                if ((need & (1u << s)) && nmoe_tag_is(w[s], epoch)) {
-                    ys[s] = nmoe_tag_val(w[s]);
-                    need &= ~(1u << s);
+                    for (int q = 1; q < NMOE_MAX_K; q++)
+                        if (sg == (uint32_t)q) y = ys[q];
+                    moe += s_w[s] * y;
                 }
-            if (need == 0) break;
-            __builtin_amdgcn_s_sleep(1);
-            if (++spins > NMOE_SPIN_LIMIT) {
-                __hip_atomic_store(status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                break;
             }
+            float r = hm + moe;
+            if (a.shared_out != NULL) r = r + nmoe_sigmoid_dev(a.shared_gate_raw[0]) * sh;
+            a.out[row] = r;
+            if (tid == 0) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
-        float moe = 0.0f;
+    }
+    if (ROUTE && blockIdx.x == 0 && ctrl) {
+        if (lane < NMOE_MAX_K) {
+            if (a.idx_out != NULL) a.idx_out[lane] = s_t[lane];
+            if (a.w_out != NULL) a.w_out[lane] = s_w[lane];
+        }
+        if (a.logits_out != NULL)
 #pragma unroll
-        for (int s = 0; s < NMOE_MAX_K; s++)
-            if (s < k) moe += s_w[s] * ys[s];
-        float r = hm + moe;
-        if (a.shared_out != NULL) r = r + nmoe_sigmoid_dev(a.shared_gate_raw[0]) * sh;
-        a.out[row] = r;
+            for (int q = 0; q < 4; q++) a.logits_out[lane + 64 * q] = lv[q];
     }
 }
 
@@ -378,17 +533,48 @@ __global__ void __launch_bounds__(256) nmoe_fused_decode_kernel(nmoe_fused_args 
 
 template <int BITS, bool ROUTE, int XMODE>
 static hipError_t nmoe_fused_launch(const nmoe_fused_args &args, hipStream_t s) {
-    hipLaunchKernelGGL((nmoe_fused_decode_kernel<BITS, ROUTE, XMODE>), dim3(NMOE_FUSED_BLOCKS), dim3(256), 0, s, args);
+    hipLaunchKernelGGL((nmoe_fused_decode_kernel<BITS, ROUTE, XMODE>), dim3(NMOE_FUSED_BLOCKS), dim3(NMOE_FUSED_THREADS), 0, s, args);
     return hipGetLastError();
 }
 
 template <int BITS, bool ROUTE, int XMODE>
 static int nmoe_fused_fits(int num_cus) {
     int per_cu = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, nmoe_fused_decode_kernel<BITS, ROUTE, XMODE>, 256, 0) !=
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, nmoe_fused_decode_kernel<BITS, ROUTE, XMODE>, NMOE_FUSED_THREADS, 0) !=
         hipSuccess)
         return 0;
     return per_cu >= 1 && per_cu * num_cus >= NMOE_FUSED_BLOCKS;
+}
+
+/* Which die each block runs on. */
+__global__ void nmoe_xcc_probe_kernel(uint32_t *out) {
+    if (threadIdx.x == 0) out[blockIdx.x] = nmoe_xcc_id();
+}
+
+/* *placed = 1 when the blocks of a 256-block grid go round-robin over the
+ * 8 dies -- block b on die (b + c) % 8, c fixed within a launch (the
+ * dispatcher continues its rotation from the previous launch, so c varies
+ * between launches).  The blocks of a group (b % 8 equal) then share a die
+ * and its L2, which the die-local exchange relies on.  Checked over launches
+ * with different rotations (a 1-block launch in between shifts c). */
+static int nmoe_check_xcd_placement(int *placed) {
+    uint32_t *d = NULL, h[NMOE_FUSED_BLOCKS];
+    *placed = 0;
+    if (hipMalloc((void **)&d, sizeof(h)) != hipSuccess) return NMOE_HIP_ENOMEM;
+    int ok = 1;
+    for (int rep = 0; rep < 4 && ok; rep++) {
+        hipLaunchKernelGGL(nmoe_xcc_probe_kernel, dim3(NMOE_FUSED_BLOCKS), dim3(NMOE_FUSED_THREADS), 0, 0, d);
+        if (hipGetLastError() != hipSuccess || hipMemcpy(h, d, sizeof(h), hipMemcpyDeviceToHost) != hipSuccess) {
+            (void)hipFree(d);
+            return NMOE_HIP_EHIP;
+        }
+        const uint32_t c = h[0] % NMOE_FUSED_GROUPS;
+        for (int b = 0; b < NMOE_FUSED_BLOCKS; b++) ok = ok && h[b] == (uint32_t)(b + c) % NMOE_FUSED_GROUPS;
+        hipLaunchKernelGGL(nmoe_xcc_probe_kernel, dim3(1 + rep), dim3(64), 0, 0, d); /* shift the rotation */
+    }
+    (void)hipFree(d);
+    *placed = ok;
+    return NMOE_HIP_OK;
 }
 
 /* The fused path needs all 256 blocks resident at once (its group barriers
@@ -401,6 +587,12 @@ extern "C" int nmoe_decode_init(nmoe_hip_ctx *ctx) {
              nmoe_fused_fits<4, false, NMOE_XBF16>(n) && nmoe_fused_fits<4, false, NMOE_XF32>(n) &&
              nmoe_fused_fits<2, false, NMOE_XBF16>(n) && nmoe_fused_fits<2, false, NMOE_XF32>(n);
     ctx->fused_blocks = ok ? NMOE_FUSED_BLOCKS : 0;
+    ctx->xcd_placed = 0;
+    if (ok) {
+        int r = nmoe_check_xcd_placement(&ctx->xcd_placed);
+        if (r != NMOE_HIP_OK) return r;
+    }
+    ctx->use_xcd_local = ctx->xcd_placed;
     ctx->xch_bytes = (size_t)NMOE_XCH_WORDS * sizeof(uint64_t);
     if (hipMalloc((void **)&ctx->xch, ctx->xch_bytes) != hipSuccess) return NMOE_HIP_ENOMEM;
     if (hipMemset(ctx->xch, 0, ctx->xch_bytes) != hipSuccess) return NMOE_HIP_EHIP;
@@ -431,6 +623,7 @@ extern "C" int nmoe_fused_decode(nmoe_hip_ctx *ctx, int bits, int route, const v
     a.logits_out = logits_out;
     a.xch = ctx->xch;
     a.sync = ctx->sync;
+    a.xcd_local = ctx->use_xcd_local;
     hipError_t e = hipErrorInvalidValue;
     if (bits == 4) {
         if (route) {

@@ -78,6 +78,15 @@ __device__ __forceinline__ float nmoe_wave_max_f(float v) {
                  fmaxf(nmoe_readlane_f(v, 32), nmoe_readlane_f(v, 48)));
 }
 
+__device__ __forceinline__ float nmoe_wave_min_f(float v) {
+    v = fminf(v, nmoe_dpp_f<NMOE_DPP_XOR1>(v));
+    v = fminf(v, nmoe_dpp_f<NMOE_DPP_XOR2>(v));
+    v = fminf(v, nmoe_dpp_f<NMOE_DPP_HALF_MIRROR>(v));
+    v = fminf(v, nmoe_dpp_f<NMOE_DPP_MIRROR>(v));
+    return fminf(fminf(nmoe_readlane_f(v, 0), nmoe_readlane_f(v, 16)),
+                 fminf(nmoe_readlane_f(v, 32), nmoe_readlane_f(v, 48)));
+}
+
 __device__ __forceinline__ uint32_t nmoe_wave_max_u32(uint32_t v) {
     v = max(v, nmoe_dpp_u<NMOE_DPP_XOR1>(v));
     v = max(v, nmoe_dpp_u<NMOE_DPP_XOR2>(v));
@@ -226,20 +235,16 @@ __device__ __forceinline__ float nmoe_router_row_bf16(const uint4 wv[4], const f
 
 /* ------------------------------------------------------------ routing */
 
-/* Routes one token with a full wavefront (math.m:67-153 bit for bit).
- * lg: the token's logits (any memory); scratch: 256 floats of LDS for the
- * sequential exact-sum path; tab: the exp2 table (LDS or constant memory).  On return every lane
- * holds sel_i / sel_w (slots >= n zero).  Returns n = min(k, E). */
-__device__ __forceinline__ int nmoe_wave_route(const float *lg, int num_experts, int k, float *scratch,
-                                               const uint64_t *tab, uint32_t sel_i[NMOE_MAX_K],
-                                               float sel_w[NMOE_MAX_K], float *probs) {
+/* Softmax probabilities of one token (math.m:67-93 bit for bit), entry
+ * lane + 64 j in p[j] (0 for entries >= num_experts).  l: the lane's four
+ * logits; scratch: 256 floats of LDS for the sequential exact-sum path;
+ * tab: the exp2 table. */
+__device__ __forceinline__ void nmoe_wave_softmax(const float l_in[4], int num_experts, float *scratch,
+                                                  const uint64_t *tab, float p[4]) {
     const int lane = threadIdx.x & 63;
     float l[4];
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-        int i = lane + 64 * j;
-        l[j] = i < num_experts ? lg[i] : -__builtin_inff();
-    }
+    for (int j = 0; j < 4; j++) l[j] = lane + 64 * j < num_experts ? l_in[j] : -__builtin_inff();
     /* the maximum (order-free for finite logits; zeros of either sign give
      * the same exp arguments' results) */
     float m = nmoe_wave_max_f(fmaxf(fmaxf(l[0], l[1]), fmaxf(l[2], l[3])));
@@ -279,50 +284,59 @@ __device__ __forceinline__ int nmoe_wave_route(const float *lg, int num_experts,
         total = nmoe_readlane_f(t, 0);
         __builtin_amdgcn_wave_barrier();
     }
-    float p[4];
     float inv = total == 0.0f ? 0.0f : 1.0f / total;
 #pragma unroll
-    for (int j = 0; j < 4; j++) p[j] = total == 0.0f ? 1.0f / (float)num_experts : e[j] * inv;
-    if (probs != NULL) {
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            int i = lane + 64 * j;
-            if (i < num_experts) probs[i] = p[j];
-        }
-    }
+    for (int j = 0; j < 4; j++)
+        p[j] = lane + 64 * j < num_experts ? (total == 0.0f ? 1.0f / (float)num_experts : e[j] * inv) : 0.0f;
+}
 
-    /* top-k (math.m:95-132): per round, the wave maximum of the 32-bit keys
-     * p_bits + 1 (probabilities are >= 0, so their bits order like the
-     * values; 0 marks a taken entry), then the lowest index holding that
-     * maximum from the compare masks -- index = lane + 64 j, so the lowest
-     * j with a hit, then its lowest lane. */
-    int n = min(k, num_experts);
-    uint32_t key[4];
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-        int i = lane + 64 * j;
-        key[j] = i < num_experts ? __float_as_uint(p[j]) + 1u : 0u;
-    }
-    float sel_v[NMOE_MAX_K];
+/* Order-preserving key of a float: a > b <=> key(a) > key(b) (-0 < +0);
+ * never 0, so 0 can mark an absent or taken entry. */
+__device__ __forceinline__ uint32_t nmoe_fkey(float f) {
+    uint32_t u = __float_as_uint(f);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+/* The n (<= NMOE_MAX_K) largest of the wavefront's 256 keys (key[j] of
+ * lane L belongs to entry L + 64 j; 0 = absent), in decreasing key order,
+ * ties to the lower entry -- the selection rule of math.m:95-132.  Per
+ * round: the wave maximum, then the lowest entry holding it from the
+ * compare masks (lowest j with a hit, then its lowest lane).  Consumes key;
+ * uniform results, slots >= n zero; hook(s, entry) runs after round s. */
+struct nmoe_no_round_hook {
+    __device__ void operator()(int, uint32_t) const {}
+};
+
+template <typename Hook = nmoe_no_round_hook>
+__device__ __forceinline__ void nmoe_wave_top_keys(uint32_t key[4], int n, uint32_t sel[NMOE_MAX_K],
+                                                   uint32_t selkey[NMOE_MAX_K], Hook hook = Hook()) {
+    const int lane = threadIdx.x & 63;
 #pragma unroll
     for (int s = 0; s < NMOE_MAX_K; s++) {
-        sel_i[s] = 0;
-        sel_v[s] = 0.0f;
+        sel[s] = 0;
+        selkey[s] = 0;
         if (s < n) {
-            uint32_t best = nmoe_wave_max_u32(max(max(key[0], key[1]), max(key[2], key[3])));
-            uint64_t m0 = __ballot(key[0] == best), m1 = __ballot(key[1] == best);
-            uint64_t m2 = __ballot(key[2] == best), m3 = __ballot(key[3] == best);
-            uint32_t win = m0 ? (uint32_t)__builtin_ctzll(m0)
-                              : m1 ? 64u + (uint32_t)__builtin_ctzll(m1)
-                                   : m2 ? 128u + (uint32_t)__builtin_ctzll(m2) : 192u + (uint32_t)__builtin_ctzll(m3);
+            const uint32_t best = nmoe_wave_max_u32(max(max(key[0], key[1]), max(key[2], key[3])));
+            const uint64_t m0 = __ballot(key[0] == best), m1 = __ballot(key[1] == best);
+            const uint64_t m2 = __ballot(key[2] == best), m3 = __ballot(key[3] == best);
+            /* branch-free: find-first-set of each mask (0 = none) */
+            const int f0 = __ffsll((unsigned long long)m0), f1 = __ffsll((unsigned long long)m1);
+            const int f2 = __ffsll((unsigned long long)m2), f3 = __ffsll((unsigned long long)m3);
+            const uint32_t win = f0 ? f0 - 1 : f1 ? 63 + f1 : f2 ? 127 + f2 : 191 + f3;
+            const bool here = (uint32_t)lane == (win & 63u);
 #pragma unroll
             for (int j = 0; j < 4; j++)
-                if ((uint32_t)(lane + 64 * j) == win) key[j] = 0u; /* taken */
-            sel_i[s] = win;
-            sel_v[s] = __uint_as_float(best - 1u);
+                if (here && (win >> 6) == (uint32_t)j) key[j] = 0u; /* taken */
+            sel[s] = win;
+            selkey[s] = best;
+            hook(s, win); /* e.g. publish each selection as soon as it is made */
         }
     }
-    /* math.m:134-153 */
+}
+
+/* math.m:134-153: weights = selected probabilities / their sum, summed in
+ * slot order (1/n each when the sum is 0). */
+__device__ __forceinline__ void nmoe_renormalize(const float sel_v[NMOE_MAX_K], int n, float sel_w[NMOE_MAX_K]) {
     float sum = 0.0f;
 #pragma unroll
     for (int s = 0; s < NMOE_MAX_K; s++)
@@ -330,7 +344,125 @@ __device__ __forceinline__ int nmoe_wave_route(const float *lg, int num_experts,
     float rinv = sum == 0.0f ? 1.0f / (float)n : 1.0f / sum;
 #pragma unroll
     for (int s = 0; s < NMOE_MAX_K; s++) sel_w[s] = s < n ? (sum == 0.0f ? rinv : sel_v[s] * rinv) : 0.0f;
+}
+
+/* Routes one token with a full wavefront (math.m:67-153 bit for bit).
+ * lg: the token's logits (any memory); scratch: 256 floats of LDS for the
+ * sequential exact-sum path; tab: the exp2 table (LDS or constant memory).
+ * On return every lane holds sel_i / sel_w (slots >= n zero); probs, if not
+ * NULL, receives the probabilities.  Returns n = min(k, E). */
+__device__ __forceinline__ int nmoe_wave_route(const float *lg, int num_experts, int k, float *scratch,
+                                               const uint64_t *tab, uint32_t sel_i[NMOE_MAX_K],
+                                               float sel_w[NMOE_MAX_K], float *probs) {
+    const int lane = threadIdx.x & 63;
+    float l[4], p[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) l[j] = lane + 64 * j < num_experts ? lg[lane + 64 * j] : 0.0f;
+    nmoe_wave_softmax(l, num_experts, scratch, tab, p);
+    if (probs != NULL) {
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            if (lane + 64 * j < num_experts) probs[lane + 64 * j] = p[j];
+    }
+    /* probabilities are >= 0, so their bits order like the values; +1 keeps
+     * 0 free for absent entries */
+    const int n = min(k, num_experts);
+    uint32_t key[4], selkey[NMOE_MAX_K];
+#pragma unroll
+    for (int j = 0; j < 4; j++) key[j] = lane + 64 * j < num_experts ? __float_as_uint(p[j]) + 1u : 0u;
+    nmoe_wave_top_keys(key, n, sel_i, selkey);
+    float sel_v[NMOE_MAX_K];
+#pragma unroll
+    for (int s = 0; s < NMOE_MAX_K; s++) sel_v[s] = s < n ? __uint_as_float(selkey[s] - 1u) : 0.0f;
+    nmoe_renormalize(sel_v, n, sel_w);
     return n;
+}
+
+/* Exact routing of one token of 256 experts given the candidates: the n
+ * entries with the largest logits, marked by taken[j] (lane L, entry
+ * L + 64 j).  Same result as nmoe_wave_route, but the slow part -- softmax --
+ * can run while work that only needs the candidate set proceeds.  With p8
+ * the smallest candidate probability, every entry has p <= p8 or is a
+ * candidate whenever A = #{p > p8} < n (always, as exp is monotone; checked,
+ * not assumed): the selection is then the A entries with p > p8 plus the
+ * lowest-index entries with p == p8, put in (p desc, index asc) order by
+ * rank counting.  A >= n falls back to the full top-k on p.
+ * s_t: 4 x NMOE_MAX_K words of LDS, private to the wave. */
+__device__ __forceinline__ void nmoe_wave_route_cand(const float l[4], int n, const bool taken[4], float *scratch,
+                                                     uint32_t *s_t, const uint64_t *tab, uint32_t sel_i[NMOE_MAX_K],
+                                                     float sel_w[NMOE_MAX_K]) {
+    const int lane = threadIdx.x & 63;
+    float p[4];
+    nmoe_wave_softmax(l, NMOE_EXPERTS, scratch, tab, p);
+    float pc = __builtin_inff();
+#pragma unroll
+    for (int j = 0; j < 4; j++) pc = taken[j] ? fminf(pc, p[j]) : pc;
+    const float p8 = nmoe_wave_min_f(pc);
+    uint64_t gt[4], eq[4];
+    int above = 0;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        gt[j] = __ballot(p[j] > p8);
+        eq[j] = __ballot(p[j] == p8);
+        above += __builtin_popcountll(gt[j]);
+    }
+    float sel_v[NMOE_MAX_K];
+    if (above < n) {
+        /* members: p > p8, and the first n - above entries with p == p8;
+         * member t (index order) goes to s_t[t] (entry) / s_t[8 + t] (p) */
+        const int take = n - above;
+        int before = 0, pos_base = 0;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const bool e_j = (eq[j] >> lane) & 1, g_j = (gt[j] >> lane) & 1;
+            const int eq_rank = before + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(eq[j] >> 32),
+                                                                        __builtin_amdgcn_mbcnt_lo((uint32_t)eq[j], 0u));
+            const bool mine = g_j || (e_j && eq_rank < take);
+            before += __builtin_popcountll(eq[j]);
+            const uint64_t mm = __ballot(mine);
+            const int pos = pos_base + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mm >> 32),
+                                                                      __builtin_amdgcn_mbcnt_lo((uint32_t)mm, 0u));
+            if (mine) {
+                s_t[pos] = (uint32_t)(lane + 64 * j);
+                s_t[NMOE_MAX_K + pos] = __float_as_uint(p[j]);
+            }
+            pos_base += __builtin_popcountll(mm);
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+        /* lane t < n: member t; its slot = members ahead of it in
+         * (p desc, index asc) order */
+        const uint32_t my_i = s_t[lane & (NMOE_MAX_K - 1)];
+        const float my_p = __uint_as_float(s_t[NMOE_MAX_K + (lane & (NMOE_MAX_K - 1))]);
+        int rank = 0;
+#pragma unroll
+        for (int u = 0; u < NMOE_MAX_K; u++) {
+            const float pu = nmoe_readlane_f(my_p, u);
+            rank += (u < n && (pu > my_p || (pu == my_p && u < lane))) ? 1 : 0;
+        }
+        if (lane < n) {
+            s_t[2 * NMOE_MAX_K + rank] = my_i;
+            s_t[3 * NMOE_MAX_K + rank] = __float_as_uint(my_p);
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+#pragma unroll
+        for (int s = 0; s < NMOE_MAX_K; s++) {
+            const uint32_t ii = s_t[2 * NMOE_MAX_K + s], pp = s_t[3 * NMOE_MAX_K + s];
+            sel_i[s] = s < n ? ii : 0u;
+            sel_v[s] = s < n ? __uint_as_float(pp) : 0.0f;
+        }
+    } else {
+        uint32_t key[4], selkey[NMOE_MAX_K];
+#pragma unroll
+        for (int j = 0; j < 4; j++) key[j] = __float_as_uint(p[j]) + 1u;
+        nmoe_wave_top_keys(key, n, sel_i, selkey);
+#pragma unroll
+        for (int s = 0; s < NMOE_MAX_K; s++) sel_v[s] = s < n ? __uint_as_float(selkey[s] - 1u) : 0.0f;
+    }
+    nmoe_renormalize(sel_v, n, sel_w);
 }
 
 /* --------------------------------------------- exchange across blocks */
@@ -419,7 +551,8 @@ __device__ __forceinline__ void nmoe_dd_add(double &s, double &c, double s2, dou
 }
 
 /* rms of math.m:34-65 (unit weight) over the 2048 fp32 values h, by a whole
- * 256-thread block; uniform result.  math.m sums the squares in an x87
+ * block of 256 or more threads (threads 0..255 hold the data, the rest
+ * only take part in the barriers); uniform result.  math.m sums the squares in an x87
  * `long double` (64-bit significand) running sum, so its mean square differs
  * from the exact one by less than 2^-53 relative.  The block computes the
  * exact mean square as a double-double; if no float rounding midpoint lies
@@ -429,7 +562,12 @@ __device__ __forceinline__ void nmoe_dd_add(double &s, double &c, double s2, dou
 __device__ float nmoe_block_rms_exact(const float *h, float eps, float *lds_h, double *lds_dd, float *lds_f) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const float4 *h4 = (const float4 *)h;
-    float4 v0 = h4[2 * tid], v1 = h4[2 * tid + 1];
+    const bool holds = tid < NMOE_HIDDEN / 8;
+    float4 v0 = make_float4(0.0f, 0.0f, 0.0f, 0.0f), v1 = v0;
+    if (holds) {
+        v0 = h4[2 * tid];
+        v1 = h4[2 * tid + 1];
+    }
     float vv[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
     double s = 0.0, c = 0.0;
 #pragma unroll
@@ -449,7 +587,7 @@ __device__ float nmoe_block_rms_exact(const float *h, float eps, float *lds_h, d
     nmoe_dd_add(ws, wc, nmoe_readlane_d(s, 16), nmoe_readlane_d(c, 16));
     nmoe_dd_add(ws, wc, nmoe_readlane_d(s, 32), nmoe_readlane_d(c, 32));
     nmoe_dd_add(ws, wc, nmoe_readlane_d(s, 48), nmoe_readlane_d(c, 48));
-    if (lane == 0) {
+    if (lane == 0 && holds) {
         lds_dd[2 * wave] = ws;
         lds_dd[2 * wave + 1] = wc;
     }
@@ -479,7 +617,8 @@ __device__ float nmoe_block_rms_exact(const float *h, float eps, float *lds_h, d
     if (mean < 0.0f) {
         /* near a rounding midpoint: replay the x87 running sum */
 #pragma unroll
-        for (int i = 0; i < 8; i++) lds_h[8 * tid + i] = vv[i];
+        for (int i = 0; i < 8; i++)
+            if (holds) lds_h[8 * tid + i] = vv[i];
         __syncthreads();
         if (tid == 0) {
             nmoe_x87 acc = nmoe_x87_zero();

@@ -47,6 +47,9 @@ struct nmoe_layout<2> {
  * its own 128-byte line. */
 #define NMOE_SYNC_STATUS 0     /* set to 1 by a kernel whose bounded wait expired */
 #define NMOE_SYNC_WORDS 8192   /* status + per-block launch epochs of the fused kernel */
+#define NMOE_SYNC_EPOCH(b) (64 + 16 * (b))     /* per-block launch epochs, 64 bytes apart */
+#define NMOE_SYNC_COMBINE(j) (4352 + 16 * (j)) /* per-chunk arrival counters of the combine */
+#define NMOE_SYNC_BLOCKS 256
 
 struct nmoe_pack_slot {
     void *dev;
@@ -79,6 +82,8 @@ struct nmoe_hip_ctx {
     size_t xch_bytes;
     int fused_blocks;     /* persistent decode grid (0 = not resident-capable) */
     int use_fused;        /* NMOE_HIP_OPT_FUSED_DECODE */
+    int xcd_placed;       /* blocks dealt round-robin over 8 dies (checked at create) */
+    int use_xcd_local;    /* NMOE_HIP_OPT_XCD_LOCAL */
     char err[256];
 };
 

@@ -41,6 +41,7 @@ EIO = -5
 EHIP = -71
 ETIMEDOUT = -110
 OPT_FUSED_DECODE = 1
+OPT_XCD_LOCAL = 2
 
 # q4 / q2 component offsets (scripts/convert_qwen36.py:38-64)
 OFFSETS = {
@@ -205,6 +206,11 @@ class Context:
 
     def set_fused(self, on: bool):
         self._check(lib().nmoe_hip_set_option(self.h, OPT_FUSED_DECODE, int(bool(on))))
+
+    def set_xcd_local(self, on: bool):
+        """Die-local exchange in the fused launch (raises where the device
+        does not deal a launch's blocks round-robin over 8 dies)."""
+        self._check(lib().nmoe_hip_set_option(self.h, OPT_XCD_LOCAL, int(bool(on))))
 
     def device_status(self) -> int:
         return lib().nmoe_hip_check_device_status(self.h)

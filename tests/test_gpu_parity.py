@@ -369,3 +369,81 @@ def test_fused_wide_logit_spread(ctx, nh):
     # x is scaled by 40, so outputs reach ~1e5: the absolute bound scales with them
     scale = max(1.0, float(np.abs(want).max()) / 10.0)
     assert_close(out.download(np.float32, 2048), want, max_abs=2e-3 * scale, what="wide spread")
+
+
+def _tie_router(k):
+    """Router rows and x whose logits put a probability tie on the top-k
+    boundary between two entries with different logits: k-1 experts at logit
+    2^-10, expert 200 at 2^-11 and expert 3 at 2^-11 - 2^-30 (everything else
+    -1).  exp() of the two boundary arguments rounds to the same float, so
+    the k largest logits hold 200 while math.m's top-k takes 3 (lower index
+    among equal probabilities)."""
+    W = np.zeros((256, 2048), np.float32)
+    W[:, 0] = -1.0
+    top = [50 + 10 * i for i in range(k - 1)]
+    W[top, 0] = 2.0 ** -10
+    W[200, 0] = 2.0 ** -11
+    W[3, 0] = 2.0 ** -11
+    W[3, 1] = -(2.0 ** -10)
+    x = np.zeros(2048, np.float32)
+    x[0], x[1] = 1.0, 2.0 ** -20
+    Wb = B.f32_to_bf16(W.ravel()).reshape(256, 2048)
+    return Wb, x, top
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("bits,k", [(4, 8), (2, 6)])
+def test_fused_probability_tie_at_boundary(ctx, nh, bits, k):
+    """The fused kernel starts streaming the k largest logits' experts before
+    the softmax; a probability tie across the boundary must still give
+    math.m's selection, slot order and weights, with the right expert's
+    weights in the combine."""
+    seed, layer = 41, 62
+    Wb, x, top = _tie_router(k)
+    lg = B.router_logits_bf16(Wb, x)
+    assert lg[200] > lg[3]
+    oi, ow, _ = B.route(lg, k)
+    assert 3 in oi[:k] and 200 not in oi[:k]  # the construction holds
+    assert sorted(np.argsort(-lg, kind="stable")[:k].tolist()) == sorted(top + [200])
+    ctx.synth_layer(layer, bits, seed, SIGMA[bits])
+    rng = np.random.default_rng(5)
+    h = rng.standard_normal(2048).astype(np.float32)
+    want = B.moe_experts(host_pack(bits, seed, layer, oi[:k]), bits, x[None], k, oi[None], ow[None], h[None])[0]
+    out, di, dw = ctx.alloc(8192), ctx.alloc(32), ctx.alloc(32)
+    ctx._check(ctx.moe_layer(layer, ctx.router_bf16(ctx.to_device(Wb)), ctx.to_device(x), nh.F32, 1, k,
+                             ctx.to_device(h), out, di, dw))
+    np.testing.assert_array_equal(di.download(np.uint32, 8)[:k], oi[:k])
+    np.testing.assert_array_equal(dw.download(np.float32, 8)[:k].view(np.uint32), ow[:k].view(np.uint32))
+    assert_close(out.download(np.float32, 2048), want, what="tie at boundary")
+
+
+@pytest.mark.gpu
+def test_xcd_placement_and_die_local_exchange(ctx, nh):
+    """MI355X deals a launch's blocks round-robin over its 8 dies (checked at
+    create), so the die-local exchange is available; with it on or off the
+    fused step gives identical results, equal to the oracle's routing."""
+    bits, seed, k, layer = 4, 52, 8, 63
+    ctx.set_xcd_local(True)  # raises where the placement check failed
+    ctx.synth_layer(layer, bits, seed, SIGMA[bits])
+    rng = np.random.default_rng(9)
+    W = B.syn_bf16(256 * 2048, seed, layer, 16, 0.02).reshape(256, 2048)
+    x = rng.standard_normal(2048).astype(np.float32)
+    h = rng.standard_normal(2048).astype(np.float32)
+    oi, ow, _ = B.route(B.router_logits_bf16(W, x), k)
+    want = B.moe_experts(host_pack(bits, seed, layer, oi[:k]), bits, x[None], k, oi[None], ow[None], h[None])[0]
+    rt, xd, hd = ctx.router_bf16(ctx.to_device(W)), ctx.to_device(x), ctx.to_device(h)
+    outs = []
+    try:
+        for on in (True, False, True):
+            ctx.set_xcd_local(on)
+            out, di, dw = ctx.alloc(8192), ctx.alloc(32), ctx.alloc(32)
+            for _ in range(3):
+                ctx._check(ctx.moe_layer(layer, rt, xd, nh.F32, 1, k, hd, out, di, dw))
+            assert ctx.device_status() == 0
+            np.testing.assert_array_equal(di.download(np.uint32, 8), oi)
+            outs.append(out.download(np.float32, 2048))
+    finally:
+        ctx.set_xcd_local(True)
+    np.testing.assert_array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+    np.testing.assert_array_equal(outs[0].view(np.uint32), outs[2].view(np.uint32))
+    assert_close(outs[0], want, what="die-local exchange")
