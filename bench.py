@@ -11,9 +11,13 @@ distinct router and input per layer, so weights stream from HBM.
 A step is one call of the per-layer MoE entry point (nmoe_moe_layer), which
 for one token is a single persistent launch (nmoe_fused_decode_kernel).
 Timed region: `--steps` back-to-back steps on the library's stream,
-bracketed by HIP events and stream synchronisation.  A second pass records
-an event pair around every launch of the dominant kernel to get its average
-duration for the roofline object.
+bracketed by HIP events recorded on that stream and stream synchronisation.
+One step is one launch of the dominant kernel, so its average launch
+duration for the roofline object is the timed region / steps (this includes
+the dispatch gap between back-to-back launches; rocprofv3's kernel-only
+average is in profiles/).  `traffic` (HBM bytes per launch) comes from the
+rocprofv3 FETCH_SIZE / WRITE_SIZE runs summarised in
+profiles/fused_decode_q4_k8.md (copy-calibrated), for the q4 top-8 workload.
 
 Algorithmic bytes per step (q4, K=8): 8 experts x 1,769,472 B + bf16 router
 1,048,576 B + activations 20,544 B (x bf16 4 KB, h_mid fp32 8 KB, out fp32
@@ -84,9 +88,31 @@ class HipEvents:
         assert self.rt.hipEventElapsedTime(C.byref(out), a, b) == 0
         return float(out.value)
 
+    def copy_d2d(self, dst, src, nbytes, stream):
+        """hipMemcpyAsync device-to-device (a blit kernel: the known-size
+        copy that HBM byte counters are calibrated against)."""
+        f = self.rt.hipMemcpyAsync
+        f.restype = C.c_int
+        f.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int, C.c_void_p]
+        assert f(dst, src, nbytes, 3, stream) == 0  # hipMemcpyDeviceToDevice
+
     def destroy(self, evs):
         for e in evs:
             self.rt.hipEventDestroy(e)
+
+
+def profiled_traffic(bits: int, k: int):
+    """HBM bytes per launch from the committed rocprofv3 counter summary of
+    this workload (None for a workload without one)."""
+    path = os.path.join(ROOT, "profiles", f"fused_decode_q{bits}_k{k}.md")
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch = "):
+                    return int(line.split("=")[1])
+    except OSError:
+        pass
+    return None
 
 
 def cpu_baseline(bits: int, k: int, seed: int, nsteps: int, nlayers: int = 4) -> dict:
@@ -142,6 +168,8 @@ def main():
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--cpu-steps", type=int, default=630)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-calib", type=int, default=0, metavar="MIB",
+                    help="only run 5 device-to-device copies of MIB MiB (counter calibration) and exit")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -149,6 +177,18 @@ def main():
         sys.exit(2)
 
     import nmoe_hip as nh
+
+    if args.copy_calib:
+        ctx = nh.Context(0, max_tokens=1)
+        n = args.copy_calib << 20
+        src, dst = ctx.alloc(n, "calib.src"), ctx.alloc(n, "calib.dst")
+        ev = HipEvents()
+        for _ in range(5):
+            ev.copy_d2d(dst.ptr, src.ptr, n, ctx.stream)
+        ctx.sync()
+        print(json.dumps({"copy_calib_bytes": n, "copies": 5}), flush=True)
+        ctx.close()
+        return
 
     bits, k, NL = args.bits, args.k, args.layers
     sigma = 0.02 if bits == 4 else 0.05
@@ -194,17 +234,8 @@ def main():
         raise SystemExit(f"device status error: {ctx.last_error()}")
     ms_per_step = total_ms / args.steps
 
-    # per-launch timing pass for the roofline object
-    n_k = min(args.steps, 200)
-    evs = ev.create(2 * n_k)
-    ctx.sync()
-    for i in range(n_k):
-        ev.record(evs[2 * i], stream)
-        step(i)
-        ev.record(evs[2 * i + 1], stream)
-    per = [ev.ms(evs[2 * i], evs[2 * i + 1]) for i in range(n_k)]
-    ev.destroy(evs + [e0, e1])
-    kern_ms = float(np.mean(per))
+    ev.destroy([e0, e1])
+    kern_ms = ms_per_step  # one launch per step
 
     B = step_bytes(bits, k)
     tps = 1e3 / ms_per_step
@@ -235,8 +266,8 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
-            "kernel": "nmoe_fused_decode_kernel<4,true,bf16> (one launch = one step; event pair per launch)",
+            "traffic": profiled_traffic(bits, k),
+            "kernel": f"nmoe_fused_decode_kernel<{bits},true,bf16> (one launch per step)",
             "kernel_ms": round(kern_ms, 5),
         },
     }
