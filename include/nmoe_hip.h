@@ -99,6 +99,11 @@ NMOE_HIP_API int nmoe_hip_check_device_status(nmoe_hip_ctx *ctx);
  * like the rest. */
 #define NMOE_HIP_OPT_FUSED_DECODE 1
 #define NMOE_HIP_OPT_XCD_LOCAL 2
+/* NMOE_HIP_OPT_GROUPED_MIN_TOKENS (default 8): calls with at least this many
+ * tokens run the experts as grouped GEMMs on the matrix cores (dispatch
+ * permutation, then each expert's weights read once for all its tokens);
+ * fewer tokens run the per-token kernels. */
+#define NMOE_HIP_OPT_GROUPED_MIN_TOKENS 3
 NMOE_HIP_API int nmoe_hip_set_option(nmoe_hip_ctx *ctx, int option, int value);
 
 /* ---- buffers (backend.h:64-66: register_shared_buffer / register_state_buffer
@@ -168,6 +173,16 @@ NMOE_HIP_API int nmoe_moe_experts_q4(nmoe_hip_ctx *ctx, int layer, const void *x
 NMOE_HIP_API int nmoe_moe_experts_q2(nmoe_hip_ctx *ctx, int layer, const void *x, int x_dtype, int ntok, int k,
                         const uint32_t *idx, const float *w, const float *h_mid, const float *shared_out,
                         const float *shared_gate_raw, float *out, void *stream);
+
+/* ---- dispatch permutation for batched tokens (no reference counterpart:
+ * the reference runs its MoE tail once per token, runtime.m:3816).  The
+ * entries q = t*k + s of idx [ntok][8] (slots s < k) sorted stably by
+ * expert -- ties by t, then s: perm [ntok*k] lists the entries of expert 0,
+ * then expert 1, ...; offsets [257]: expert e owns perm[offsets[e] ..
+ * offsets[e+1]).  Entries whose index is >= 256 are left out (offsets[256]
+ * counts the rest). */
+NMOE_HIP_API int nmoe_moe_dispatch(nmoe_hip_ctx *ctx, const uint32_t *idx, int ntok, int k, uint32_t *perm,
+                                   uint32_t *offsets, void *stream);
 
 /* ---- the whole per-layer MoE call (NMOEPipelinedExpertTail,
  * runtime.m:2908-2999, with routing on the device and no host round trip):

@@ -68,6 +68,11 @@ extern "C" int nmoe_hip_create(int device, int max_tokens, nmoe_hip_ctx **out) {
         nmoe_hip_destroy(ctx);
         return NMOE_HIP_ENODEV;
     }
+    extern int nmoe_grouped_init(nmoe_hip_ctx *);
+    if (nmoe_grouped_init(ctx) != NMOE_HIP_OK) {
+        nmoe_hip_destroy(ctx);
+        return NMOE_HIP_ENOMEM;
+    }
     *out = ctx;
     return NMOE_HIP_OK;
 }
@@ -86,6 +91,8 @@ extern "C" void nmoe_hip_destroy(nmoe_hip_ctx *ctx) {
     hipFree(ctx->w);
     hipFree(ctx->sync);
     hipFree(ctx->xch);
+    extern void nmoe_grouped_free(nmoe_hip_ctx *);
+    nmoe_grouped_free(ctx);
     if (ctx->stream != NULL) hipStreamDestroy(ctx->stream);
     free(ctx);
 }
@@ -94,6 +101,11 @@ extern "C" int nmoe_hip_set_option(nmoe_hip_ctx *ctx, int option, int value) {
     if (ctx == NULL) return NMOE_HIP_EINVAL;
     if (option == NMOE_HIP_OPT_FUSED_DECODE) {
         ctx->use_fused = value != 0;
+        return NMOE_HIP_OK;
+    }
+    if (option == NMOE_HIP_OPT_GROUPED_MIN_TOKENS) {
+        if (value < 1) return nmoe_fail(ctx, NMOE_HIP_EINVAL, "grouped path minimum %d < 1", value);
+        ctx->grouped_min_tokens = value;
         return NMOE_HIP_OK;
     }
     if (option == NMOE_HIP_OPT_XCD_LOCAL) {

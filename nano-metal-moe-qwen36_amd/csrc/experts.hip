@@ -190,6 +190,25 @@ static int nmoe_check_experts(nmoe_hip_ctx *ctx, int layer, int bits, const void
     return NMOE_HIP_OK;
 }
 
+extern "C" int nmoe_grouped_experts(nmoe_hip_ctx *ctx, int bits, const uint8_t *pack, const void *x, int x_dtype,
+                                    int ntok, int k, const uint32_t *idx, const float *w, const float *h_mid,
+                                    const float *shared_out, const float *shared_gate_raw, float *out,
+                                    hipStream_t s);
+extern "C" int nmoe_grouped_dispatch(nmoe_hip_ctx *ctx, const uint32_t *idx, int ntok, int k, uint32_t *perm,
+                                     uint32_t *offsets, hipStream_t s);
+
+extern "C" int nmoe_moe_dispatch(nmoe_hip_ctx *ctx, const uint32_t *idx, int ntok, int k, uint32_t *perm,
+                                 uint32_t *offsets, void *stream) {
+    if (ctx == NULL) return NMOE_HIP_EINVAL;
+    if (k < 1 || k > NMOE_MAX_K) return nmoe_fail(ctx, NMOE_HIP_EINVAL, "k=%d outside 1..8", k);
+    if (ntok < 1 || ntok > ctx->max_tokens)
+        return nmoe_fail(ctx, NMOE_HIP_EINVAL, "ntok=%d outside 1..%d", ntok, ctx->max_tokens);
+    if (idx == NULL || perm == NULL || offsets == NULL) return nmoe_fail(ctx, NMOE_HIP_EINVAL, "NULL idx/perm/offsets");
+    if (!nmoe_aligned(idx, 4) || !nmoe_aligned(perm, 4) || !nmoe_aligned(offsets, 4))
+        return nmoe_fail(ctx, NMOE_HIP_EINVAL, "misaligned idx/perm/offsets");
+    return nmoe_grouped_dispatch(ctx, idx, ntok, k, perm, offsets, nmoe_stream_of(ctx, stream));
+}
+
 template <int BITS>
 static int nmoe_launch_experts(nmoe_hip_ctx *ctx, const uint8_t *pack, const void *x, int x_dtype, int ntok, int k,
                                const uint32_t *idx, const float *w, const float *h_mid, const float *shared_out,
@@ -224,6 +243,9 @@ static int nmoe_experts_dispatch(nmoe_hip_ctx *ctx, const uint8_t *pack, const v
     if (ntok == 1 && ctx->fused_blocks > 0 && ctx->use_fused)
         return nmoe_fused_decode(ctx, BITS, 0, x, x_dtype, 0.0f, k, NULL, idx, w, h_mid, shared_out, shared_gate_raw,
                                  out, NULL, NULL, NULL, pack, s);
+    if (ntok >= ctx->grouped_min_tokens)
+        return nmoe_grouped_experts(ctx, BITS, pack, x, x_dtype, ntok, k, idx, w, h_mid, shared_out, shared_gate_raw,
+                                    out, s);
     return nmoe_launch_experts<BITS>(ctx, pack, x, x_dtype, ntok, k, idx, w, h_mid, shared_out, shared_gate_raw, out, s);
 }
 

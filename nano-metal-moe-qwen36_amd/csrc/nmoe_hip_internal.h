@@ -84,6 +84,16 @@ struct nmoe_hip_ctx {
     int use_fused;        /* NMOE_HIP_OPT_FUSED_DECODE */
     int xcd_placed;       /* blocks dealt round-robin over 8 dies (checked at create) */
     int use_xcd_local;    /* NMOE_HIP_OPT_XCD_LOCAL */
+    /* grouped (matrix-core) path for many tokens, sized for max_tokens */
+    int grouped_min_tokens; /* NMOE_HIP_OPT_GROUPED_MIN_TOKENS */
+    uint32_t *g_counts;     /* [16][257] per-block expert histograms */
+    uint32_t *g_perm;       /* [T*8] entries grouped by expert */
+    uint32_t *g_offsets;    /* [257] */
+    uint16_t *g_xhi, *g_xlo; /* [T][2048] x in operand order (bf16 hi / lo) */
+    float *g_xs;            /* [T][32] group sums of x */
+    uint16_t *g_ahi, *g_alo; /* [T*8][512] act (bf16 hi / lo), by permuted row */
+    float *g_as;            /* [T*8][8] group sums of act */
+    float *g_y;             /* [T*8][2048] per-entry expert outputs */
     char err[256];
 };
 

@@ -42,6 +42,7 @@ EHIP = -71
 ETIMEDOUT = -110
 OPT_FUSED_DECODE = 1
 OPT_XCD_LOCAL = 2
+OPT_GROUPED_MIN_TOKENS = 3
 
 # q4 / q2 component offsets (scripts/convert_qwen36.py:38-64)
 OFFSETS = {
@@ -102,6 +103,7 @@ _SIGS = {
     "nmoe_dequant_rows": (_I, [_P, _I, _P, _P, _P, _I, _I, _P, _P]),
     "nmoe_moe_layer_rmsnorm": (_I, [_P, _I, C.POINTER(Router), _P, C.c_float, _I, _P, _P, _P, _P, _P]),
     "nmoe_moe_stack": (_I, [_P, _I, C.POINTER(_I), C.POINTER(Router), _I, C.c_float, _P, _P, _P, _P]),
+    "nmoe_moe_dispatch": (_I, [_P, _P, _I, _I, _P, _P, _P]),
 }
 
 
@@ -206,6 +208,13 @@ class Context:
 
     def set_fused(self, on: bool):
         self._check(lib().nmoe_hip_set_option(self.h, OPT_FUSED_DECODE, int(bool(on))))
+
+    def set_grouped_min_tokens(self, n: int):
+        """Calls with at least n tokens run the grouped (matrix-core) path."""
+        self._check(lib().nmoe_hip_set_option(self.h, OPT_GROUPED_MIN_TOKENS, int(n)))
+
+    def dispatch(self, idx, ntok: int, k: int, perm, offsets, stream=None) -> int:
+        return lib().nmoe_moe_dispatch(self.h, _ptr(idx), ntok, k, _ptr(perm), _ptr(offsets), stream)
 
     def set_xcd_local(self, on: bool):
         """Die-local exchange in the fused launch (raises where the device

@@ -447,3 +447,130 @@ def test_xcd_placement_and_die_local_exchange(ctx, nh):
     np.testing.assert_array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
     np.testing.assert_array_equal(outs[0].view(np.uint32), outs[2].view(np.uint32))
     assert_close(outs[0], want, what="die-local exchange")
+
+
+# ---------------------------------------------------------------- grouped path
+
+def zipf_idx(rng, ntok, k, alpha=1.1):
+    """Per token, k distinct experts drawn without replacement with
+    p_e ~ rank_e^-alpha over a seeded permutation (Gumbel-top-k)."""
+    order = rng.permutation(256)
+    logp = np.empty(256)
+    logp[order] = -alpha * np.log(np.arange(1, 257))
+    g = logp[None, :] + rng.gumbel(size=(ntok, 256))
+    idx = np.zeros((ntok, 8), np.uint32)
+    idx[:, :k] = np.argsort(-g, axis=1, kind="stable")[:, :k]
+    return idx
+
+
+@pytest.fixture(scope="module")
+def big(nh):
+    c = nh.Context(0, max_tokens=2048)
+    yield c
+    c.close()
+
+
+@pytest.mark.parametrize("ntok,k,kind", [(1, 8, "uniform"), (64, 8, "zipf"), (2048, 8, "uniform"), (33, 6, "zipf"),
+                                         (100, 3, "uniform"), (64, 8, "invalid")])
+def test_dispatch_matches_oracle(big, ntok, k, kind):
+    """a14: the stable counting sort of (t, s) entries by expert is bit-exact
+    with the oracle's (numpy's stable argsort); entries outside the layer
+    are left out."""
+    rng = np.random.default_rng(ntok * 10 + k)
+    if kind == "zipf":
+        idx = zipf_idx(rng, ntok, k)
+    else:
+        idx = np.zeros((ntok, 8), np.uint32)
+        idx[:, :k] = rng.integers(0, 256, size=(ntok, k))
+    if kind == "invalid":
+        idx[rng.integers(0, ntok, 20), rng.integers(0, k, 20)] = 300 + rng.integers(0, 50, 20)
+    flat = idx[:, :k].reshape(-1)
+    valid = flat < 256
+    perm = big.alloc(ntok * k * 4)
+    offs = big.alloc(257 * 4)
+    big._check(big.dispatch(big.to_device(idx), ntok, k, perm, offs))
+    got_p = perm.download(np.uint32, ntok * k)
+    got_o = offs.download(np.uint32, 257)
+    if kind != "invalid":
+        want_p, want_o = B.dispatch(idx, ntok, k, 8)
+    else:
+        keys = np.where(valid, flat, 256)
+        want_p = np.argsort(keys, kind="stable")[:valid.sum()].astype(np.uint32)
+        want_o = np.concatenate([[0], np.cumsum(np.bincount(flat[valid], minlength=256))]).astype(np.uint32)
+    np.testing.assert_array_equal(got_o, want_o)
+    np.testing.assert_array_equal(got_p[:int(want_o[256])], want_p)
+
+
+@pytest.mark.parametrize("bits", [4, 2])
+@pytest.mark.parametrize("ntok,k,xkind,ikind", [(8, 8, "bf16", "uniform"), (64, 8, "bf16", "zipf"),
+                                               (64, 6, "f32", "zipf"), (40, 8, "f32", "uniform")])
+def test_grouped_experts_against_oracle(big, nh, bits, ntok, k, xkind, ikind):
+    """a15: the grouped matrix-core path (dispatch, gate/up + SwiGLU, down,
+    slot-order combine) against the oracle, and against the per-token
+    kernels, with shared-expert term and an invalid slot."""
+    rng = np.random.default_rng(1000 * bits + ntok + k)
+    seed, layer = 21, 40 + bits
+    big.synth_layer(layer, bits, seed, SIGMA[bits])
+    idx = zipf_idx(rng, ntok, k) if ikind == "zipf" else np.zeros((ntok, 8), np.uint32)
+    if ikind == "uniform":
+        for t in range(ntok):
+            idx[t, :k] = rng.choice(256, k, replace=False)
+    w = np.zeros((ntok, 8), np.float32)
+    w[:, :k] = rng.dirichlet(np.ones(k), size=ntok).astype(np.float32)
+    idx[3, 1] = 999  # invalid slot: weight 0 (runtime.m:2977-2981)
+    w_eff = w.copy()
+    w_eff[3, 1] = 0.0
+    idx_eff = idx.copy()
+    idx_eff[3, 1] = idx[3, 0]
+    xf = rng.standard_normal((ntok, 2048)).astype(np.float32)
+    if xkind == "bf16":
+        xb = B.f32_to_bf16(xf)
+        x, xdev, dt = B.bf16_to_f32(xb).reshape(ntok, 2048), xb, nh.BF16
+    else:
+        x, xdev, dt = xf, xf, nh.F32
+    h = rng.standard_normal((ntok, 2048)).astype(np.float32)
+    sh = rng.standard_normal((ntok, 2048)).astype(np.float32)
+    gr = rng.standard_normal(ntok).astype(np.float32)
+    pack = host_pack(bits, seed, layer, idx_eff[:, :k].ravel())
+    want = B.moe_experts(pack, bits, x, k, idx_eff, w_eff, h, sh, gr)
+    d = [big.to_device(a) for a in (xdev, idx, w, h, sh, gr)]
+    outs = {}
+    for path, nmin in (("grouped", 1), ("per-token", 1 << 20)):
+        big.set_grouped_min_tokens(nmin)
+        out = big.alloc(ntok * 2048 * 4)
+        big._check(big.experts(bits, layer, d[0], dt, ntok, k, d[1], d[2], d[3], out, d[4], d[5]))
+        outs[path] = out.download(np.float32, (ntok, 2048))
+    big.set_grouped_min_tokens(8)
+    assert big.device_status() == nh.OK
+    for path, got in outs.items():
+        assert_close(got, want, what=f"{path} q{bits} ntok={ntok} k={k} x={xkind}")
+
+
+@pytest.mark.parametrize("bits", [4, 2])
+def test_prefill_2048_sampled(big, nh, bits):
+    """C5 shape: 2048 tokens, uniform-random logits -> device top-8 ->
+    grouped experts; routing bit-exact for every token, outputs checked
+    against the oracle on a sample of 48 tokens."""
+    rng = np.random.default_rng(2048 + bits)
+    seed, layer, ntok, k = 33, 50 + bits, 2048, 8
+    big.synth_layer(layer, bits, seed, SIGMA[bits])
+    logits = rng.random((ntok, 256), dtype=np.float32)
+    xb = B.f32_to_bf16(rng.standard_normal((ntok, 2048)).astype(np.float32))
+    x = B.bf16_to_f32(xb).reshape(ntok, 2048)
+    h = rng.standard_normal((ntok, 2048)).astype(np.float32)
+    d_lg, d_x, d_h = big.to_device(logits), big.to_device(xb), big.to_device(h)
+    d_idx, d_w, out = big.alloc(ntok * 32), big.alloc(ntok * 32), big.alloc(ntok * 2048 * 4)
+    big._check(big.topk(d_lg, ntok, 256, k, d_idx, d_w))
+    big._check(big.experts(bits, layer, d_x, nh.BF16, ntok, k, d_idx, d_w, d_h, out))
+    idx = d_idx.download(np.uint32, (ntok, 8))
+    w = d_w.download(np.float32, (ntok, 8))
+    sample = rng.choice(ntok, 48, replace=False)
+    for t in sample[:8]:
+        oi, ow, _ = B.route(logits[t], k)
+        np.testing.assert_array_equal(idx[t], oi)
+        np.testing.assert_array_equal(w[t].view(np.uint32), ow.view(np.uint32))
+    got = out.download(np.float32, (ntok, 2048))[sample]
+    pack = host_pack(bits, seed, layer, idx[sample, :k].ravel())
+    want = B.moe_experts(pack, bits, x[sample], k, idx[sample], w[sample], h[sample])
+    assert big.device_status() == nh.OK
+    assert_close(got, want, what=f"prefill q{bits}")
