@@ -233,138 +233,245 @@ __global__ void __launch_bounds__(256) nmoe_grouped_xprep_kernel(const XT *x, ui
 
 /* ------------------------------------------------------------ gate/up */
 
-/* Expert blockIdx.x, gate/up rows 64 * blockIdx.y .. +63: act rows of all the
- * expert's entries.  Wave w owns rows 16w..16w+15 of the tile for gate and
- * up alike, so a lane holds gate and up of the same (entry, row). */
+/* A rows of one 64-deep group go through LDS (each block stages the x or
+ * act of its 64 expert rows once per group, double-buffered, for its four
+ * wavefronts); a row is 64 bf16 = 8 uint4, padded to 9 so the 16 rows an
+ * MFMA operand read touches fall on different banks. */
+#define NMOE_APAD 9
+
+/* stage loaders (plain functions: arrays passed by reference stay in
+ * registers) */
+template <int XPL>
+__device__ __forceinline__ void nmoe_gu_load_a(uint4 (&ra)[2][XPL], const uint16_t *xhi, const uint16_t *xlo,
+                                               const uint32_t (&ta)[2], int g, int ach) {
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        ra[i][0] = ((const uint4 *)(xhi + (size_t)ta[i] * NMOE_HIDDEN + 64 * g))[ach];
+        if (XPL == 2) ra[i][XPL - 1] = ((const uint4 *)(xlo + (size_t)ta[i] * NMOE_HIDDEN + 64 * g))[ach];
+    }
+}
+
+template <int XPL, int NI>
+__device__ __forceinline__ void nmoe_store_a(uint4 (&sa)[XPL][NMOE_MCHUNK][NMOE_APAD], const uint4 (&ra)[NI][XPL],
+                                             int arow0, int ach) {
+#pragma unroll
+    for (int i = 0; i < NI; i++)
+#pragma unroll
+        for (int pl = 0; pl < XPL; pl++) sa[pl][arow0 + 32 * i][ach] = ra[i][pl];
+}
+
+template <int BITS>
+__device__ __forceinline__ void nmoe_gu_load_b(uint32_t (&rb)[2][2][2], const uint32_t *const (&wrow)[2][2], int g,
+                                               int kb) {
+#pragma unroll
+    for (int mat = 0; mat < 2; mat++)
+#pragma unroll
+        for (int nb2 = 0; nb2 < 2; nb2++) {
+            if (BITS == 4) {
+                const uint2 v = *(const uint2 *)(wrow[mat][nb2] + 8 * g + 2 * kb);
+                rb[mat][nb2][0] = v.x;
+                rb[mat][nb2][1] = v.y;
+            } else {
+                rb[mat][nb2][0] = wrow[mat][nb2][4 * g + kb];
+                rb[mat][nb2][1] = 0;
+            }
+        }
+}
+
+__device__ __forceinline__ void nmoe_dn_load_a(uint4 (&ra)[4], const uint16_t *ahi, const uint16_t *alo, uint32_t p0,
+                                               uint32_t m0, uint32_t n, int g, int tid) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int u = tid + 256 * i, pl = u >> 9, row = (u >> 3) & 63, ch = u & 7;
+        const uint32_t m = min(m0 + row, n - 1);
+        ra[i] = ((const uint4 *)((pl == 0 ? ahi : alo) + (size_t)(p0 + m) * NMOE_INTER + 64 * g))[ch];
+    }
+}
+
+__device__ __forceinline__ void nmoe_dn_store_a(uint4 (&sa)[2][NMOE_MCHUNK][NMOE_APAD], const uint4 (&ra)[4], int tid) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int u = tid + 256 * i, pl = u >> 9, row = (u >> 3) & 63, ch = u & 7;
+        sa[pl][row][ch] = ra[i];
+    }
+}
+
+template <int BITS>
+__device__ __forceinline__ void nmoe_dn_load_b(uint32_t (&rb)[4][2], const uint32_t *const (&wrow)[4], int g, int kb) {
+#pragma unroll
+    for (int nb4 = 0; nb4 < 4; nb4++) {
+        if (BITS == 4) {
+            const uint2 v = *(const uint2 *)(wrow[nb4] + 8 * g + 2 * kb);
+            rb[nb4][0] = v.x;
+            rb[nb4][1] = v.y;
+        } else {
+            rb[nb4][0] = wrow[nb4][4 * g + kb];
+            rb[nb4][1] = 0;
+        }
+    }
+}
+
+/* Expert blockIdx.x, gate/up rows 128 * blockIdx.y .. +127 (both
+ * matrices): act rows of all the expert's entries.  Wave w owns gate and up
+ * rows 32w..32w+31 of the tile as two 16-row MFMA column blocks each, over
+ * four 16-row blocks of entries: a lane holds gate and up of the same
+ * (entry, row). */
 template <int BITS, int XPL>
-__global__ void __launch_bounds__(256) nmoe_grouped_gateup_kernel(const uint8_t *pack, const uint16_t *xhi,
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) nmoe_grouped_gateup_kernel(const uint8_t *pack, const uint16_t *xhi,
                                                                    const uint16_t *xlo, const float *xs,
                                                                    const uint32_t *perm, const uint32_t *offsets,
                                                                    int k, uint16_t *ahi, uint16_t *alo, float *as) {
     using Q = nmoe_q<BITS>;
     using L = nmoe_layout<BITS>;
     constexpr int G = NMOE_HIDDEN / NMOE_GROUP; /* 32 groups */
-    __shared__ float s_sc[2][NMOE_GU_TILE][G];  /* scale */
-    __shared__ float s_cc[2][NMOE_GU_TILE][G];  /* bias - 128 scale */
+    constexpr int NT = 2 * NMOE_GU_TILE;        /* 128 rows per matrix per block */
+    __shared__ uint16_t s_sb[4][NT][G];         /* gate s, gate b, up s, up b */
+    __shared__ uint4 s_a[2][XPL][NMOE_MCHUNK][NMOE_APAD];
+    __shared__ uint32_t s_tok[NMOE_MCHUNK];
     __shared__ float s_as[4][NMOE_MCHUNK];
     const int e = blockIdx.x, nt = blockIdx.y;
     const uint32_t p0 = offsets[e], n = offsets[e + 1] - p0;
     if (n == 0) return;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, col = lane & 15, kb = lane >> 4;
     const uint8_t *ex = pack + (size_t)e * L::expert_size;
-    for (int i = tid; i < 2 * NMOE_GU_TILE * G; i += 256) {
-        const int mat = i / (NMOE_GU_TILE * G), rr = (i / G) % NMOE_GU_TILE, g = i % G;
-        const size_t so = mat == 0 ? L::gate_s : L::up_s;
-        const size_t sb = mat == 0 ? L::gate_b : L::up_b;
-        const int row = nt * NMOE_GU_TILE + rr;
-        const float s = nmoe_bf16f(((const uint16_t *)(ex + so))[row * G + g]);
-        const float b = nmoe_bf16f(((const uint16_t *)(ex + sb))[row * G + g]);
-        s_sc[mat][rr][g] = s;
-        s_cc[mat][rr][g] = b - 128.0f * s; /* exact: both have 8 significant bits */
+    for (int i = tid; i < 4 * NT * G / 8; i += 256) {
+        const int arr = i / (NT * G / 8), j = i % (NT * G / 8);
+        const uint32_t so = arr == 0 ? L::gate_s : arr == 1 ? L::gate_b : arr == 2 ? L::up_s : L::up_b;
+        ((uint4 *)&s_sb[arr][0][0])[j] = ((const uint4 *)(ex + so + (size_t)nt * NT * G * 2))[j];
     }
-    __syncthreads();
-    const int rt = wave * 16 + col;           /* row within the tile */
-    const int r = nt * NMOE_GU_TILE + rt;      /* gate/up row */
-    const uint32_t *gw = (const uint32_t *)(ex + L::gate_w) + (size_t)r * Q::WPR_G;
-    const uint32_t *uw = (const uint32_t *)(ex + L::up_w) + (size_t)r * Q::WPR_G;
+    const int rt0 = 32 * wave + col; /* tile row of column block nb2: rt0 + 16 nb2 */
+    const uint32_t *wrow[2][2];
+#pragma unroll
+    for (int mat = 0; mat < 2; mat++)
+#pragma unroll
+        for (int nb2 = 0; nb2 < 2; nb2++)
+            wrow[mat][nb2] = (const uint32_t *)(ex + (mat == 0 ? L::gate_w : L::up_w)) +
+                             (size_t)(nt * NT + rt0 + 16 * nb2) * Q::WPR_G;
+    /* A loader: uint4 u = tid + 256 i -> row u / 8, chunk u % 8 */
+    const int arow0 = tid >> 3, ach = tid & 7;
 
     for (uint32_t m0 = 0; m0 < n; m0 += NMOE_MCHUNK) {
-        /* A rows: entry m0 + 16 mb + col; output rows: 16 mb + 4 kb + i */
-        const uint16_t *xa[4], *xla[4];
-        const float *xsa[4];
-#pragma unroll
-        for (int mb = 0; mb < 4; mb++) {
-            const uint32_t m = m0 + 16 * mb + col;
-            const uint32_t t = m < n ? perm[p0 + m] / (uint32_t)k : perm[p0] / (uint32_t)k;
-            xa[mb] = xhi + (size_t)t * NMOE_HIDDEN + 16 * kb;
-            xla[mb] = XPL == 2 ? xlo + (size_t)t * NMOE_HIDDEN + 16 * kb : NULL;
-            xsa[mb] = xs + (size_t)t * G;
-        }
+        if (tid < NMOE_MCHUNK) s_tok[tid] = perm[p0 + min(m0 + tid, n - 1)] / (uint32_t)k;
+        __syncthreads();
         const int nb = (int)min((n - m0 + 15) / 16, 4u);
-        nmoe_f32x4 acc[2][4];
-        /* sum_g (b_g - 128 s_g) xs_g on the fp32 cores: A lane = (entry col, group 4tq + kb),
-         * B lane = (row col, group 4tq + kb) */
+        const uint32_t ta[2] = {s_tok[arow0], s_tok[arow0 + 32]};
+        uint4 ra[2][XPL];
+        uint32_t rb[2][2][2];
+        nmoe_gu_load_a<XPL>(ra, xhi, xlo, ta, 0, ach);
+        nmoe_gu_load_b<BITS>(rb, wrow, 0, kb);
+        /* sum_g (b_g - 128 s_g) xs_g on the fp32 cores: A lane = (entry col,
+         * group 4tq + kb), B lane = (row col, group 4tq + kb) */
+        nmoe_f32x4 acc[2][2][4];
 #pragma unroll
         for (int mb = 0; mb < 4; mb++) {
-            acc[0][mb] = nmoe_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-            acc[1][mb] = nmoe_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-            if (mb < nb) {
+            const float *xsr = xs + (size_t)s_tok[16 * mb + col] * G;
 #pragma unroll
-                for (int tq = 0; tq < G / 4; tq++) {
-                    const float a = xsa[mb][4 * tq + kb];
-                    acc[0][mb] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, s_cc[0][rt][4 * tq + kb], acc[0][mb], 0, 0, 0);
-                    acc[1][mb] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, s_cc[1][rt][4 * tq + kb], acc[1][mb], 0, 0, 0);
+            for (int mat = 0; mat < 2; mat++)
+#pragma unroll
+                for (int nb2 = 0; nb2 < 2; nb2++) {
+                    acc[mat][nb2][mb] = nmoe_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+                    if (mb < nb) {
+                        const int rr = rt0 + 16 * nb2;
+#pragma unroll
+                        for (int tq = 0; tq < G / 4; tq++) {
+                            const int gg = 4 * tq + kb;
+                            const float sc = nmoe_bf16f(s_sb[2 * mat][rr][gg]);
+                            const float c = nmoe_bf16f(s_sb[2 * mat + 1][rr][gg]) - 128.0f * sc;
+                            acc[mat][nb2][mb] =
+                                __builtin_amdgcn_mfma_f32_16x16x4f32(xsr[gg], c, acc[mat][nb2][mb], 0, 0, 0);
+                        }
+                    }
                 }
-            }
         }
+        nmoe_store_a<XPL, 2>(s_a[0], ra, arow0, ach);
+#pragma unroll 1
         for (int g = 0; g < G; g++) {
-            uint32_t g0, g1 = 0, u0, u1 = 0;
-            if (BITS == 4) {
-                const uint2 gv = *(const uint2 *)(gw + 8 * g + 2 * kb);
-                const uint2 uv = *(const uint2 *)(uw + 8 * g + 2 * kb);
-                g0 = gv.x, g1 = gv.y, u0 = uv.x, u1 = uv.y;
-            } else {
-                g0 = gw[4 * g + kb];
-                u0 = uw[4 * g + kb];
+            __syncthreads(); /* stage g visible; stage g+1's buffer no longer read */
+            uint32_t cb[2][2][2];
+#pragma unroll
+            for (int mat = 0; mat < 2; mat++)
+#pragma unroll
+                for (int nb2 = 0; nb2 < 2; nb2++) cb[mat][nb2][0] = rb[mat][nb2][0], cb[mat][nb2][1] = rb[mat][nb2][1];
+            if (g + 1 < G) {
+                nmoe_gu_load_a<XPL>(ra, xhi, xlo, ta, g + 1, ach);
+                nmoe_gu_load_b<BITS>(rb, wrow, g + 1, kb);
             }
-            uint4 bg0, bg1, bu0, bu1;
-            nmoe_codes_bf16<BITS>(g0, g1, bg0, bg1);
-            nmoe_codes_bf16<BITS>(u0, u1, bu0, bu1);
-            /* the lane's column is the same row for every group: its scales */
-            const float sg = s_sc[0][rt][g], su = s_sc[1][rt][g];
+            uint4 bq[2][2][2];
+            float sg[2][2];
+#pragma unroll
+            for (int mat = 0; mat < 2; mat++)
+#pragma unroll
+                for (int nb2 = 0; nb2 < 2; nb2++) {
+                    nmoe_codes_bf16<BITS>(cb[mat][nb2][0], cb[mat][nb2][1], bq[mat][nb2][0], bq[mat][nb2][1]);
+                    sg[mat][nb2] = nmoe_bf16f(s_sb[2 * mat][rt0 + 16 * nb2][g]);
+                }
+            const int buf = g & 1;
 #pragma unroll
             for (int mb = 0; mb < 4; mb++) {
                 if (mb < nb) {
-                    const uint4 *pa = (const uint4 *)(xa[mb] + 64 * g);
-                    const uint4 a0 = pa[0], a1 = pa[1];
-                    nmoe_f32x4 pg = nmoe_mfma16(a0, bg0, nmoe_f32x4{0.0f, 0.0f, 0.0f, 0.0f});
-                    pg = nmoe_mfma16(a1, bg1, pg);
-                    nmoe_f32x4 pu = nmoe_mfma16(a0, bu0, nmoe_f32x4{0.0f, 0.0f, 0.0f, 0.0f});
-                    pu = nmoe_mfma16(a1, bu1, pu);
-                    if (XPL == 2) {
-                        const uint4 *pl = (const uint4 *)(xla[mb] + 64 * g);
-                        const uint4 l0 = pl[0], l1 = pl[1];
-                        pg = nmoe_mfma16(l0, bg0, pg);
-                        pg = nmoe_mfma16(l1, bg1, pg);
-                        pu = nmoe_mfma16(l0, bu0, pu);
-                        pu = nmoe_mfma16(l1, bu1, pu);
+                    uint4 a[XPL][2];
+#pragma unroll
+                    for (int pl = 0; pl < XPL; pl++) {
+                        a[pl][0] = s_a[buf][pl][16 * mb + col][2 * kb];
+                        a[pl][1] = s_a[buf][pl][16 * mb + col][2 * kb + 1];
                     }
 #pragma unroll
-                    for (int i = 0; i < 4; i++) {
-                        acc[0][mb][i] = __builtin_fmaf(sg, pg[i], acc[0][mb][i]);
-                        acc[1][mb][i] = __builtin_fmaf(su, pu[i], acc[1][mb][i]);
-                    }
+                    for (int mat = 0; mat < 2; mat++)
+#pragma unroll
+                        for (int nb2 = 0; nb2 < 2; nb2++) {
+                            nmoe_f32x4 pp = nmoe_mfma16(a[0][0], bq[mat][nb2][0], nmoe_f32x4{0.0f, 0.0f, 0.0f, 0.0f});
+                            pp = nmoe_mfma16(a[0][1], bq[mat][nb2][1], pp);
+                            if (XPL == 2) {
+                                pp = nmoe_mfma16(a[XPL - 1][0], bq[mat][nb2][0], pp);
+                                pp = nmoe_mfma16(a[XPL - 1][1], bq[mat][nb2][1], pp);
+                            }
+#pragma unroll
+                            for (int i = 0; i < 4; i++)
+                                acc[mat][nb2][mb][i] = __builtin_fmaf(sg[mat][nb2], pp[i], acc[mat][nb2][mb][i]);
+                        }
                 }
             }
+            if (g + 1 < G) nmoe_store_a<XPL, 2>(s_a[(g + 1) & 1], ra, arow0, ach);
         }
         /* epilogue: act = SiLU(gate) * up as hi + lo bf16, in the down
-         * kernel's operand order; group sums of act rows over this tile */
-        const int span = (nt * NMOE_GU_TILE + wave * 16) / 16;
-        const int slot = nmoe_kperm_inv<BITS>(col);
+         * kernel's operand order; group sums of act rows (a down group is
+         * 64 act columns = waves 0-1 or 2-3 of this tile) */
 #pragma unroll
-        for (int mb = 0; mb < 4; mb++) {
+        for (int nb2 = 0; nb2 < 2; nb2++) {
+            const int r = nt * NT + rt0 + 16 * nb2; /* act column */
+            const int span = r >> 4;
+            const int slot = nmoe_kperm_inv<BITS>(r & 15);
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const uint32_t m = m0 + 16 * mb + 4 * kb + i;
-                const float a = nmoe_silu_dev(acc[0][mb][i]) * acc[1][mb][i];
-                const uint32_t h = nmoe_bf16_rne(a);
-                const uint32_t l = nmoe_bf16_rne(a - nmoe_bf16f(h));
-                float part = nmoe_bf16f(h) + nmoe_bf16f(l);
-                if (mb < nb && m < n) {
-                    const size_t o = (size_t)(p0 + m) * NMOE_INTER + 16 * span + slot;
-                    ahi[o] = (uint16_t)h;
-                    alo[o] = (uint16_t)l;
+            for (int mb = 0; mb < 4; mb++) {
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const uint32_t m = m0 + 16 * mb + 4 * kb + i;
+                    const float av = nmoe_silu_dev(acc[0][nb2][mb][i]) * acc[1][nb2][mb][i];
+                    const uint32_t h = nmoe_bf16_rne(av);
+                    const uint32_t l = nmoe_bf16_rne(av - nmoe_bf16f(h));
+                    float part = nmoe_bf16f(h) + nmoe_bf16f(l);
+                    if (mb < nb && m < n) {
+                        const size_t o = (size_t)(p0 + m) * NMOE_INTER + 16 * span + slot;
+                        ahi[o] = (uint16_t)h;
+                        alo[o] = (uint16_t)l;
+                    }
+                    part = nmoe_dpp_group_sum<16>(part); /* the 16 rows of this column block */
+                    if (col == 0) {
+                        if (nb2 == 0)
+                            s_as[wave][16 * mb + 4 * kb + i] = part;
+                        else
+                            s_as[wave][16 * mb + 4 * kb + i] += part;
+                    }
                 }
-                part = nmoe_dpp_group_sum<16>(part); /* the 16 rows of this wave */
-                if (col == 0) s_as[wave][16 * mb + 4 * kb + i] = part;
             }
         }
         __syncthreads();
-        if (tid < NMOE_MCHUNK) {
-            const uint32_t m = m0 + tid;
+        if (tid < 2 * NMOE_MCHUNK) {
+            const int half = tid >> 6, row = tid & 63;
+            const uint32_t m = m0 + row;
             if (m < n)
-                as[(size_t)(p0 + m) * (NMOE_INTER / NMOE_GROUP) + nt] =
-                    (s_as[0][tid] + s_as[1][tid]) + (s_as[2][tid] + s_as[3][tid]);
+                as[(size_t)(p0 + m) * (NMOE_INTER / NMOE_GROUP) + 2 * nt + half] =
+                    s_as[2 * half][row] + s_as[2 * half + 1][row];
         }
         __syncthreads();
     }
@@ -372,86 +479,114 @@ __global__ void __launch_bounds__(256) nmoe_grouped_gateup_kernel(const uint8_t 
 
 /* ------------------------------------------------------------ down */
 
-/* Expert blockIdx.x, down rows 64 * blockIdx.y .. +63: y[q][row] for all the
- * expert's entries q. */
+#define NMOE_DN_ROWS 256 /* down rows per block: 64 per wave */
+
+/* Expert blockIdx.x, down rows 256 * blockIdx.y .. +255: y[q][row] for all
+ * the expert's entries q.  Wave w owns rows 64w..64w+63 of the tile as four
+ * 16-row column blocks. */
 template <int BITS>
-__global__ void __launch_bounds__(256) nmoe_grouped_down_kernel(const uint8_t *pack, const uint16_t *ahi,
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) nmoe_grouped_down_kernel(const uint8_t *pack, const uint16_t *ahi,
                                                                  const uint16_t *alo, const float *as,
                                                                  const uint32_t *perm, const uint32_t *offsets,
                                                                  float *y) {
     using Q = nmoe_q<BITS>;
     using L = nmoe_layout<BITS>;
     constexpr int G = NMOE_INTER / NMOE_GROUP; /* 8 groups */
+    __shared__ uint16_t s_sb[2][NMOE_DN_ROWS][G];
+    __shared__ uint4 s_a[2][2][NMOE_MCHUNK][NMOE_APAD];
     const int e = blockIdx.x, nt = blockIdx.y;
     const uint32_t p0 = offsets[e], n = offsets[e + 1] - p0;
     if (n == 0) return;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, col = lane & 15, kb = lane >> 4;
     const uint8_t *ex = pack + (size_t)e * L::expert_size;
-    const int r = nt * NMOE_DN_TILE + wave * 16 + col;
-    const uint32_t *dw = (const uint32_t *)(ex + L::down_w) + (size_t)r * Q::WPR_D;
-    float sc[G], cc[G];
-#pragma unroll
-    for (int g = 0; g < G; g++) {
-        sc[g] = nmoe_bf16f(((const uint16_t *)(ex + L::down_s))[r * G + g]);
-        cc[g] = nmoe_bf16f(((const uint16_t *)(ex + L::down_b))[r * G + g]) - 128.0f * sc[g];
+    for (int i = tid; i < 2 * NMOE_DN_ROWS * G / 8; i += 256) {
+        const int arr = i / (NMOE_DN_ROWS * G / 8), j = i % (NMOE_DN_ROWS * G / 8);
+        ((uint4 *)&s_sb[arr][0][0])[j] =
+            ((const uint4 *)(ex + (arr == 0 ? L::down_s : L::down_b) + (size_t)nt * NMOE_DN_ROWS * G * 2))[j];
     }
+    const int rt0 = 64 * wave + col;
+    const uint32_t *wrow[4];
+#pragma unroll
+    for (int nb4 = 0; nb4 < 4; nb4++)
+        wrow[nb4] = (const uint32_t *)(ex + L::down_w) + (size_t)(nt * NMOE_DN_ROWS + rt0 + 16 * nb4) * Q::WPR_D;
+    __syncthreads();
+    /* A loader: 2 planes x 64 rows x 8 uint4 = 1024 uint4: u = tid + 256 i ->
+     * plane u / 512, row (u / 8) % 64, chunk u % 8 */
     for (uint32_t m0 = 0; m0 < n; m0 += NMOE_MCHUNK) {
         const int nb = (int)min((n - m0 + 15) / 16, 4u);
-        const uint16_t *ah[4], *al[4];
-        const float *asa[4];
+        uint4 ra[4];
+        uint32_t rb[4][2];
+        nmoe_dn_load_a(ra, ahi, alo, p0, m0, n, 0, tid);
+        nmoe_dn_load_b<BITS>(rb, wrow, 0, kb);
+        nmoe_f32x4 acc[4][4];
 #pragma unroll
         for (int mb = 0; mb < 4; mb++) {
-            const uint32_t m = min(m0 + 16 * mb + col, n - 1);
-            ah[mb] = ahi + (size_t)(p0 + m) * NMOE_INTER + 16 * kb;
-            al[mb] = alo + (size_t)(p0 + m) * NMOE_INTER + 16 * kb;
-            asa[mb] = as + (size_t)(p0 + m) * G;
-        }
-        nmoe_f32x4 acc[4];
+            const float *asr = as + (size_t)(p0 + min(m0 + 16 * mb + col, n - 1)) * G;
 #pragma unroll
-        for (int mb = 0; mb < 4; mb++) {
-            acc[mb] = nmoe_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-            if (mb < nb) {
+            for (int nb4 = 0; nb4 < 4; nb4++) {
+                acc[nb4][mb] = nmoe_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+                if (mb < nb) {
+                    const int rr = rt0 + 16 * nb4;
 #pragma unroll
-                for (int tq = 0; tq < G / 4; tq++) {
-                    const float c = tq == 0 ? (kb == 0 ? cc[0] : kb == 1 ? cc[1] : kb == 2 ? cc[2] : cc[3])
-                                            : (kb == 0 ? cc[4] : kb == 1 ? cc[5] : kb == 2 ? cc[6] : cc[7]);
-                    acc[mb] = __builtin_amdgcn_mfma_f32_16x16x4f32(asa[mb][4 * tq + kb], c, acc[mb], 0, 0, 0);
+                    for (int tq = 0; tq < G / 4; tq++) {
+                        const int gg = 4 * tq + kb;
+                        const float sc = nmoe_bf16f(s_sb[0][rr][gg]);
+                        const float c = nmoe_bf16f(s_sb[1][rr][gg]) - 128.0f * sc;
+                        acc[nb4][mb] = __builtin_amdgcn_mfma_f32_16x16x4f32(asr[gg], c, acc[nb4][mb], 0, 0, 0);
+                    }
                 }
             }
         }
-#pragma unroll
+        nmoe_dn_store_a(s_a[0], ra, tid);
+#pragma unroll 1
         for (int g = 0; g < G; g++) {
-            uint32_t w0, w1 = 0;
-            if (BITS == 4) {
-                const uint2 v = *(const uint2 *)(dw + 8 * g + 2 * kb);
-                w0 = v.x, w1 = v.y;
-            } else {
-                w0 = dw[4 * g + kb];
+            __syncthreads();
+            uint32_t cb[4][2];
+#pragma unroll
+            for (int nb4 = 0; nb4 < 4; nb4++) cb[nb4][0] = rb[nb4][0], cb[nb4][1] = rb[nb4][1];
+            if (g + 1 < G) {
+                nmoe_dn_load_a(ra, ahi, alo, p0, m0, n, g + 1, tid);
+                nmoe_dn_load_b<BITS>(rb, wrow, g + 1, kb);
             }
-            uint4 b0, b1;
-            nmoe_codes_bf16<BITS>(w0, w1, b0, b1);
+            uint4 bq[4][2];
+            float sg[4];
+#pragma unroll
+            for (int nb4 = 0; nb4 < 4; nb4++) {
+                nmoe_codes_bf16<BITS>(cb[nb4][0], cb[nb4][1], bq[nb4][0], bq[nb4][1]);
+                sg[nb4] = nmoe_bf16f(s_sb[0][rt0 + 16 * nb4][g]);
+            }
+            const int buf = g & 1;
 #pragma unroll
             for (int mb = 0; mb < 4; mb++) {
                 if (mb < nb) {
-                    const uint4 *ph = (const uint4 *)(ah[mb] + 64 * g);
-                    const uint4 *pl = (const uint4 *)(al[mb] + 64 * g);
-                    nmoe_f32x4 p = nmoe_mfma16(ph[0], b0, nmoe_f32x4{0.0f, 0.0f, 0.0f, 0.0f});
-                    p = nmoe_mfma16(ph[1], b1, p);
-                    p = nmoe_mfma16(pl[0], b0, p);
-                    p = nmoe_mfma16(pl[1], b1, p);
+                    const uint4 h0 = s_a[buf][0][16 * mb + col][2 * kb], h1 = s_a[buf][0][16 * mb + col][2 * kb + 1];
+                    const uint4 l0 = s_a[buf][1][16 * mb + col][2 * kb], l1 = s_a[buf][1][16 * mb + col][2 * kb + 1];
 #pragma unroll
-                    for (int i = 0; i < 4; i++) acc[mb][i] = __builtin_fmaf(sc[g], p[i], acc[mb][i]);
+                    for (int nb4 = 0; nb4 < 4; nb4++) {
+                        nmoe_f32x4 pp = nmoe_mfma16(h0, bq[nb4][0], nmoe_f32x4{0.0f, 0.0f, 0.0f, 0.0f});
+                        pp = nmoe_mfma16(h1, bq[nb4][1], pp);
+                        pp = nmoe_mfma16(l0, bq[nb4][0], pp);
+                        pp = nmoe_mfma16(l1, bq[nb4][1], pp);
+#pragma unroll
+                        for (int i = 0; i < 4; i++) acc[nb4][mb][i] = __builtin_fmaf(sg[nb4], pp[i], acc[nb4][mb][i]);
+                    }
+                }
+            }
+            if (g + 1 < G) nmoe_dn_store_a(s_a[(g + 1) & 1], ra, tid);
+        }
+#pragma unroll
+        for (int nb4 = 0; nb4 < 4; nb4++) {
+            const int r = nt * NMOE_DN_ROWS + rt0 + 16 * nb4;
+#pragma unroll
+            for (int mb = 0; mb < 4; mb++) {
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const uint32_t m = m0 + 16 * mb + 4 * kb + i;
+                    if (mb < nb && m < n) y[(size_t)perm[p0 + m] * NMOE_HIDDEN + r] = acc[nb4][mb][i];
                 }
             }
         }
-#pragma unroll
-        for (int mb = 0; mb < 4; mb++) {
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const uint32_t m = m0 + 16 * mb + 4 * kb + i;
-                if (mb < nb && m < n) y[(size_t)perm[p0 + m] * NMOE_HIDDEN + r] = acc[mb][i];
-            }
-        }
+        __syncthreads(); /* the stage buffers are reused by the next chunk */
     }
 }
 
@@ -525,7 +660,7 @@ static int nmoe_grouped_run(nmoe_hip_ctx *ctx, const uint8_t *pack, const void *
     else
         hipLaunchKernelGGL((nmoe_grouped_xprep_kernel<BITS, float>), dim3(ntok), dim3(256), 0, s, (const float *)x,
                            ctx->g_xhi, ctx->g_xlo, ctx->g_xs);
-    const dim3 ggu(NMOE_EXPERTS, NMOE_INTER / NMOE_GU_TILE), gdn(NMOE_EXPERTS, NMOE_HIDDEN / NMOE_DN_TILE);
+    const dim3 ggu(NMOE_EXPERTS, NMOE_INTER / (2 * NMOE_GU_TILE)), gdn(NMOE_EXPERTS, NMOE_HIDDEN / NMOE_DN_ROWS);
     if (bf)
         hipLaunchKernelGGL((nmoe_grouped_gateup_kernel<BITS, 1>), ggu, dim3(256), 0, s, pack,
                            (const uint16_t *)ctx->g_xhi, (const uint16_t *)ctx->g_xlo, (const float *)ctx->g_xs,
