@@ -233,82 +233,92 @@ __global__ void __launch_bounds__(256) nmoe_grouped_xprep_kernel(const XT *x, ui
 
 /* ------------------------------------------------------------ gate/up */
 
-/* A rows of one 64-deep group go through LDS (each block stages the x or
- * act of its 64 expert rows once per group, double-buffered, for its four
- * wavefronts); a row is 64 bf16 = 8 uint4, padded to 9 so the 16 rows an
- * MFMA operand read touches fall on different banks. */
-#define NMOE_APAD 9
+/* A rows of one 64-deep group reach LDS by direct global->LDS loads
+ * (global_load_lds_dwordx4: lane l of a wavefront writes bytes 16l..16l+15
+ * of the instruction's 1 KB), into a ring of NMOE_NS stages, so a group's
+ * rows are requested NMOE_NS - 1 groups before they are multiplied.  A
+ * stage row is 64 bf16 = 8 chunks of 16 bytes; chunk c of row r sits at
+ * slot c ^ (r & 7), so the 16 rows one MFMA operand read touches spread
+ * over the banks.  The codes of the weight rows go through a register ring
+ * of the same depth. */
+#define NMOE_NS 4
 
-/* stage loaders (plain functions: arrays passed by reference stay in
- * registers) */
-template <int XPL>
-__device__ __forceinline__ void nmoe_gu_load_a(uint4 (&ra)[2][XPL], const uint16_t *xhi, const uint16_t *xlo,
-                                               const uint32_t (&ta)[2], int g, int ach) {
-#pragma unroll
-    for (int i = 0; i < 2; i++) {
-        ra[i][0] = ((const uint4 *)(xhi + (size_t)ta[i] * NMOE_HIDDEN + 64 * g))[ach];
-        if (XPL == 2) ra[i][XPL - 1] = ((const uint4 *)(xlo + (size_t)ta[i] * NMOE_HIDDEN + 64 * g))[ach];
-    }
+typedef __attribute__((address_space(3))) void nmoe_lds_void;
+
+/* One ring stage: the activation rows of a group (PL planes of 64 rows x
+ * 64 bf16) and the codes of the tile's weight rows for that group.  Each
+ * stage is a __shared__ variable of its own: the compiler then tells the
+ * stages' direct loads apart and a read of one stage does not wait for
+ * the loads still in flight into the others. */
+template <int PL, int CW>
+struct nmoe_stage {
+    uint4 a[PL][NMOE_MCHUNK * 8];
+    uint32_t b[CW];
+};
+
+/* Issue the direct loads of one stage: `nins` 1-KB instructions per
+ * wavefront; instruction j of plane pl covers stage rows 8j..8j+7. */
+__device__ __forceinline__ void nmoe_stage_rows(uint4 *stage, const uint16_t *src_row0, const uint16_t *src_row1,
+                                                int j0, int lane) {
+    /* rows 8 j0 + (lane >> 3) and 8 (j0 + 1) + (lane >> 3): source row
+     * pointers already include the group's column offset */
+    const int slot = lane & 7;
+    const int r0 = 8 * j0 + (lane >> 3), r1 = r0 + 8;
+    const int c0 = slot ^ (r0 & 7), c1 = slot ^ (r1 & 7);
+    __builtin_amdgcn_global_load_lds((const void *)(src_row0 + 8 * c0), (nmoe_lds_void *)(stage + 64 * j0), 16, 0, 0);
+    __builtin_amdgcn_global_load_lds((const void *)(src_row1 + 8 * c1), (nmoe_lds_void *)(stage + 64 * (j0 + 1)), 16, 0, 0);
 }
 
-template <int XPL, int NI>
-__device__ __forceinline__ void nmoe_store_a(uint4 (&sa)[XPL][NMOE_MCHUNK][NMOE_APAD], const uint4 (&ra)[NI][XPL],
-                                             int arow0, int ach) {
-#pragma unroll
-    for (int i = 0; i < NI; i++)
-#pragma unroll
-        for (int pl = 0; pl < XPL; pl++) sa[pl][arow0 + 32 * i][ach] = ra[i][pl];
+/* MFMA A operand (two slices) of stage row r, lane k-block kb. */
+__device__ __forceinline__ void nmoe_stage_operand(const uint4 *stage, int r, int kb, uint4 &a0, uint4 &a1) {
+    a0 = stage[8 * r + ((2 * kb) ^ (r & 7))];
+    a1 = stage[8 * r + ((2 * kb + 1) ^ (r & 7))];
 }
 
+/* Direct loads of one group's codes of `rows` weight rows (starting at
+ * global row pointer base + row * wpr words, group g) into a stage of
+ * [rows][wpg] words; wpg = 8 (q4) or 4 (q2) words = 32 / 16 bytes per row.
+ * Instruction j of this wavefront covers 1 KB of the stage. */
 template <int BITS>
-__device__ __forceinline__ void nmoe_gu_load_b(uint32_t (&rb)[2][2][2], const uint32_t *const (&wrow)[2][2], int g,
-                                               int kb) {
-#pragma unroll
-    for (int mat = 0; mat < 2; mat++)
-#pragma unroll
-        for (int nb2 = 0; nb2 < 2; nb2++) {
-            if (BITS == 4) {
-                const uint2 v = *(const uint2 *)(wrow[mat][nb2] + 8 * g + 2 * kb);
-                rb[mat][nb2][0] = v.x;
-                rb[mat][nb2][1] = v.y;
-            } else {
-                rb[mat][nb2][0] = wrow[mat][nb2][4 * g + kb];
-                rb[mat][nb2][1] = 0;
-            }
-        }
+__device__ __forceinline__ void nmoe_stage_codes(uint32_t *stage, const uint32_t *base, int wpr, int g, int j,
+                                                 int lane) {
+    constexpr int WPG = BITS == 4 ? 8 : 4;
+    const int byte = 1024 * j + 16 * lane;
+    const int row = byte / (4 * WPG), w = (byte % (4 * WPG)) / 4;
+    __builtin_amdgcn_global_load_lds((const void *)(base + (size_t)row * wpr + WPG * g + w),
+                                     (nmoe_lds_void *)(stage + 256 * j), 16, 0, 0);
 }
 
-__device__ __forceinline__ void nmoe_dn_load_a(uint4 (&ra)[4], const uint16_t *ahi, const uint16_t *alo, uint32_t p0,
-                                               uint32_t m0, uint32_t n, int g, int tid) {
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const int u = tid + 256 * i, pl = u >> 9, row = (u >> 3) & 63, ch = u & 7;
-        const uint32_t m = min(m0 + row, n - 1);
-        ra[i] = ((const uint4 *)((pl == 0 ? ahi : alo) + (size_t)(p0 + m) * NMOE_INTER + 64 * g))[ch];
-    }
-}
-
-__device__ __forceinline__ void nmoe_dn_store_a(uint4 (&sa)[2][NMOE_MCHUNK][NMOE_APAD], const uint4 (&ra)[4], int tid) {
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const int u = tid + 256 * i, pl = u >> 9, row = (u >> 3) & 63, ch = u & 7;
-        sa[pl][row][ch] = ra[i];
-    }
-}
-
+/* The lane's code words of stage row r: q4 words 2kb, 2kb+1; q2 word kb. */
 template <int BITS>
-__device__ __forceinline__ void nmoe_dn_load_b(uint32_t (&rb)[4][2], const uint32_t *const (&wrow)[4], int g, int kb) {
-#pragma unroll
-    for (int nb4 = 0; nb4 < 4; nb4++) {
-        if (BITS == 4) {
-            const uint2 v = *(const uint2 *)(wrow[nb4] + 8 * g + 2 * kb);
-            rb[nb4][0] = v.x;
-            rb[nb4][1] = v.y;
-        } else {
-            rb[nb4][0] = wrow[nb4][4 * g + kb];
-            rb[nb4][1] = 0;
-        }
+__device__ __forceinline__ void nmoe_stage_code_words(const uint32_t *stage, int r, int kb, uint32_t &w0,
+                                                      uint32_t &w1) {
+    if (BITS == 4) {
+        const uint2 v = *(const uint2 *)(stage + 8 * r + 2 * kb);
+        w0 = v.x;
+        w1 = v.y;
+    } else {
+        w0 = stage[4 * r + kb];
+        w1 = 0;
     }
+}
+
+/* Ring barrier: this wavefront's loads of the stage about to be used are
+ * complete (vmcnt <= N: only later stages still in flight) and its LDS
+ * accesses are done (lgkmcnt 0), then all wavefronts meet.  A bare
+ * s_barrier: the usual __syncthreads() fence would wait for every load in
+ * flight, the later stages included. */
+template <int N>
+__device__ __forceinline__ void nmoe_ring_barrier() {
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4));
+    asm volatile("s_barrier" ::: "memory");
+}
+
+template <int N>
+__device__ __forceinline__ void nmoe_wait_vm() {
+    /* s_waitcnt vmcnt(N) (gfx9 encoding: vmcnt[3:0] | vmcnt[5:4] << 14,
+     * expcnt and lgkmcnt left at their maxima) */
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
 /* Expert blockIdx.x, gate/up rows 128 * blockIdx.y .. +127 (both
@@ -317,16 +327,21 @@ __device__ __forceinline__ void nmoe_dn_load_b(uint32_t (&rb)[4][2], const uint3
  * four 16-row blocks of entries: a lane holds gate and up of the same
  * (entry, row). */
 template <int BITS, int XPL>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) nmoe_grouped_gateup_kernel(const uint8_t *pack, const uint16_t *xhi,
-                                                                   const uint16_t *xlo, const float *xs,
-                                                                   const uint32_t *perm, const uint32_t *offsets,
-                                                                   int k, uint16_t *ahi, uint16_t *alo, float *as) {
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+nmoe_grouped_gateup_kernel(const uint8_t *pack, const uint16_t *xhi, const uint16_t *xlo, const float *xs,
+                           const uint32_t *perm, const uint32_t *offsets, int k, uint16_t *ahi, uint16_t *alo,
+                           float *as) {
     using Q = nmoe_q<BITS>;
     using L = nmoe_layout<BITS>;
     constexpr int G = NMOE_HIDDEN / NMOE_GROUP; /* 32 groups */
     constexpr int NT = 2 * NMOE_GU_TILE;        /* 128 rows per matrix per block */
+    constexpr int WPG = BITS == 4 ? 8 : 4;      /* code words per row per group */
+    constexpr int BI = 2 * NT * WPG * 4 / 1024 / 4; /* code instructions per wavefront per stage: 2 (q4) / 1 (q2) */
+    constexpr int LPG = 2 * XPL + BI;           /* loads per group per wavefront */
     __shared__ uint16_t s_sb[4][NT][G];         /* gate s, gate b, up s, up b */
-    __shared__ uint4 s_a[2][XPL][NMOE_MCHUNK][NMOE_APAD];
+    typedef nmoe_stage<XPL, 2 * NT * WPG> Stage;
+    __shared__ Stage s_st0, s_st1, s_st2, s_st3;
+    auto stage = [&](int st) -> Stage & { return st == 0 ? s_st0 : st == 1 ? s_st1 : st == 2 ? s_st2 : s_st3; };
     __shared__ uint32_t s_tok[NMOE_MCHUNK];
     __shared__ float s_as[4][NMOE_MCHUNK];
     const int e = blockIdx.x, nt = blockIdx.y;
@@ -340,81 +355,102 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))
         ((uint4 *)&s_sb[arr][0][0])[j] = ((const uint4 *)(ex + so + (size_t)nt * NT * G * 2))[j];
     }
     const int rt0 = 32 * wave + col; /* tile row of column block nb2: rt0 + 16 nb2 */
-    const uint32_t *wrow[2][2];
-#pragma unroll
-    for (int mat = 0; mat < 2; mat++)
-#pragma unroll
-        for (int nb2 = 0; nb2 < 2; nb2++)
-            wrow[mat][nb2] = (const uint32_t *)(ex + (mat == 0 ? L::gate_w : L::up_w)) +
-                             (size_t)(nt * NT + rt0 + 16 * nb2) * Q::WPR_G;
-    /* A loader: uint4 u = tid + 256 i -> row u / 8, chunk u % 8 */
-    const int arow0 = tid >> 3, ach = tid & 7;
+    const uint32_t *wbase[2] = {(const uint32_t *)(ex + L::gate_w) + (size_t)nt * NT * Q::WPR_G,
+                                (const uint32_t *)(ex + L::up_w) + (size_t)nt * NT * Q::WPR_G};
 
     for (uint32_t m0 = 0; m0 < n; m0 += NMOE_MCHUNK) {
         if (tid < NMOE_MCHUNK) s_tok[tid] = perm[p0 + min(m0 + tid, n - 1)] / (uint32_t)k;
         __syncthreads();
         const int nb = (int)min((n - m0 + 15) / 16, 4u);
-        const uint32_t ta[2] = {s_tok[arow0], s_tok[arow0 + 32]};
-        uint4 ra[2][XPL];
-        uint32_t rb[2][2][2];
-        nmoe_gu_load_a<XPL>(ra, xhi, xlo, ta, 0, ach);
-        nmoe_gu_load_b<BITS>(rb, wrow, 0, kb);
+        /* this lane's two stage rows (instructions 2w, 2w+1) */
+        const uint16_t *srow[XPL][2];
+#pragma unroll
+        for (int jj = 0; jj < 2; jj++) {
+            const uint32_t t = s_tok[8 * (2 * wave + jj) + (lane >> 3)];
+            srow[0][jj] = xhi + (size_t)t * NMOE_HIDDEN;
+            if (XPL == 2) srow[XPL - 1][jj] = xlo + (size_t)t * NMOE_HIDDEN;
+        }
+        auto issue = [&](int g, int st) {
+#pragma unroll
+            for (int pl = 0; pl < XPL; pl++)
+                nmoe_stage_rows(stage(st).a[pl], srow[pl][0] + 64 * g, srow[pl][1] + 64 * g, 2 * wave, lane);
+            /* codes: 2 matrices x NT rows x WPG words = 8 (q4) / 4 (q2) KB */
+#pragma unroll
+            for (int i = 0; i < BI; i++) {
+                const int j = BI * wave + i;                 /* 0 .. 4 BI - 1 */
+                const int mat = j / (2 * BI), jm = j % (2 * BI); /* instruction within the matrix */
+                nmoe_stage_codes<BITS>(stage(st).b + mat * NT * WPG, wbase[mat], Q::WPR_G, g, jm, lane);
+            }
+        };
         /* sum_g (b_g - 128 s_g) xs_g on the fp32 cores: A lane = (entry col,
          * group 4tq + kb), B lane = (row col, group 4tq + kb) */
         nmoe_f32x4 acc[2][2][4];
+        {
+            /* all operand loads first (one memory round trip), then the MFMAs */
+            float xv[4][G / 4];
 #pragma unroll
-        for (int mb = 0; mb < 4; mb++) {
-            const float *xsr = xs + (size_t)s_tok[16 * mb + col] * G;
+            for (int mb = 0; mb < 4; mb++) {
+                const float *xsr = xs + (size_t)s_tok[16 * mb + col] * G;
+#pragma unroll
+                for (int tq = 0; tq < G / 4; tq++) xv[mb][tq] = xsr[4 * tq + kb];
+            }
 #pragma unroll
             for (int mat = 0; mat < 2; mat++)
 #pragma unroll
                 for (int nb2 = 0; nb2 < 2; nb2++) {
-                    acc[mat][nb2][mb] = nmoe_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-                    if (mb < nb) {
-                        const int rr = rt0 + 16 * nb2;
+                    const int rr = rt0 + 16 * nb2;
+                    float cv[G / 4];
 #pragma unroll
-                        for (int tq = 0; tq < G / 4; tq++) {
-                            const int gg = 4 * tq + kb;
-                            const float sc = nmoe_bf16f(s_sb[2 * mat][rr][gg]);
-                            const float c = nmoe_bf16f(s_sb[2 * mat + 1][rr][gg]) - 128.0f * sc;
-                            acc[mat][nb2][mb] =
-                                __builtin_amdgcn_mfma_f32_16x16x4f32(xsr[gg], c, acc[mat][nb2][mb], 0, 0, 0);
-                        }
+                    for (int tq = 0; tq < G / 4; tq++) {
+                        const float sc = nmoe_bf16f(s_sb[2 * mat][rr][4 * tq + kb]);
+                        cv[tq] = nmoe_bf16f(s_sb[2 * mat + 1][rr][4 * tq + kb]) - 128.0f * sc;
+                    }
+#pragma unroll
+                    for (int mb = 0; mb < 4; mb++) {
+                        acc[mat][nb2][mb] = nmoe_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+                        if (mb < nb)
+#pragma unroll
+                            for (int tq = 0; tq < G / 4; tq++)
+                                acc[mat][nb2][mb] =
+                                    __builtin_amdgcn_mfma_f32_16x16x4f32(xv[mb][tq], cv[tq], acc[mat][nb2][mb], 0, 0, 0);
                     }
                 }
         }
-        nmoe_store_a<XPL, 2>(s_a[0], ra, arow0, ach);
-#pragma unroll 1
-        for (int g = 0; g < G; g++) {
-            __syncthreads(); /* stage g visible; stage g+1's buffer no longer read */
-            uint32_t cb[2][2][2];
+        /* keep every operand load above out of the vmcnt ring below */
+        nmoe_wait_vm<0>();
 #pragma unroll
-            for (int mat = 0; mat < 2; mat++)
-#pragma unroll
-                for (int nb2 = 0; nb2 < 2; nb2++) cb[mat][nb2][0] = rb[mat][nb2][0], cb[mat][nb2][1] = rb[mat][nb2][1];
-            if (g + 1 < G) {
-                nmoe_gu_load_a<XPL>(ra, xhi, xlo, ta, g + 1, ach);
-                nmoe_gu_load_b<BITS>(rb, wrow, g + 1, kb);
-            }
+        for (int st = 0; st < NMOE_NS - 1; st++) issue(st, st);
+        auto step = [&](int g, const int st) {
+            /* group g's stage: groups g+1, g+2 may still be in flight */
+            if (g + 2 < G)
+                nmoe_ring_barrier<2 * LPG>();
+            else if (g + 1 < G)
+                nmoe_ring_barrier<LPG>();
+            else
+                nmoe_ring_barrier<0>();
+            if (g + NMOE_NS - 1 < G) issue(g + NMOE_NS - 1, (st + NMOE_NS - 1) % NMOE_NS);
             uint4 bq[2][2][2];
             float sg[2][2];
 #pragma unroll
             for (int mat = 0; mat < 2; mat++)
 #pragma unroll
                 for (int nb2 = 0; nb2 < 2; nb2++) {
-                    nmoe_codes_bf16<BITS>(cb[mat][nb2][0], cb[mat][nb2][1], bq[mat][nb2][0], bq[mat][nb2][1]);
+                    uint32_t w0, w1;
+                    /* kept apart: a read merged across the two matrices
+                     * loses the stage it belongs to, and then waits for
+                     * every stage's loads */
+                    if (mat == 1 && nb2 == 0) asm volatile("" ::: "memory");
+                    nmoe_stage_code_words<BITS>(stage(st).b + mat * NT * WPG, rt0 + 16 * nb2, kb, w0, w1);
+                    nmoe_codes_bf16<BITS>(w0, w1, bq[mat][nb2][0], bq[mat][nb2][1]);
                     sg[mat][nb2] = nmoe_bf16f(s_sb[2 * mat][rt0 + 16 * nb2][g]);
                 }
-            const int buf = g & 1;
 #pragma unroll
             for (int mb = 0; mb < 4; mb++) {
                 if (mb < nb) {
                     uint4 a[XPL][2];
 #pragma unroll
-                    for (int pl = 0; pl < XPL; pl++) {
-                        a[pl][0] = s_a[buf][pl][16 * mb + col][2 * kb];
-                        a[pl][1] = s_a[buf][pl][16 * mb + col][2 * kb + 1];
-                    }
+                    for (int pl = 0; pl < XPL; pl++)
+                        nmoe_stage_operand(stage(st).a[pl], 16 * mb + col, kb, a[pl][0], a[pl][1]);
 #pragma unroll
                     for (int mat = 0; mat < 2; mat++)
 #pragma unroll
@@ -431,7 +467,13 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))
                         }
                 }
             }
-            if (g + 1 < G) nmoe_store_a<XPL, 2>(s_a[(g + 1) & 1], ra, arow0, ach);
+        };
+#pragma unroll 1
+        for (int g = 0; g < G; g += NMOE_NS) {
+            step(g, 0);
+            step(g + 1, 1);
+            step(g + 2, 2);
+            step(g + 3, 3);
         }
         /* epilogue: act = SiLU(gate) * up as hi + lo bf16, in the down
          * kernel's operand order; group sums of act rows (a down group is
@@ -485,15 +527,20 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))
  * the expert's entries q.  Wave w owns rows 64w..64w+63 of the tile as four
  * 16-row column blocks. */
 template <int BITS>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) nmoe_grouped_down_kernel(const uint8_t *pack, const uint16_t *ahi,
-                                                                 const uint16_t *alo, const float *as,
-                                                                 const uint32_t *perm, const uint32_t *offsets,
-                                                                 float *y) {
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+nmoe_grouped_down_kernel(const uint8_t *pack, const uint16_t *ahi, const uint16_t *alo, const float *as,
+                         const uint32_t *perm, const uint32_t *offsets, float *y) {
     using Q = nmoe_q<BITS>;
     using L = nmoe_layout<BITS>;
     constexpr int G = NMOE_INTER / NMOE_GROUP; /* 8 groups */
+    constexpr int WPG = BITS == 4 ? 8 : 4;
+    constexpr int BI = NMOE_DN_ROWS * WPG * 4 / 1024 / 4; /* code instructions per wavefront per stage: 2 / 1 */
+    constexpr int LPG = 4 + BI;                /* loads per group per wavefront: 2 planes x 2 + codes */
     __shared__ uint16_t s_sb[2][NMOE_DN_ROWS][G];
-    __shared__ uint4 s_a[2][2][NMOE_MCHUNK][NMOE_APAD];
+    typedef nmoe_stage<2, NMOE_DN_ROWS * WPG> Stage;
+    __shared__ Stage s_st0, s_st1, s_st2, s_st3;
+    __shared__ uint32_t s_q[NMOE_MCHUNK]; /* the chunk's output slots */
+    auto stage = [&](int st) -> Stage & { return st == 0 ? s_st0 : st == 1 ? s_st1 : st == 2 ? s_st2 : s_st3; };
     const int e = blockIdx.x, nt = blockIdx.y;
     const uint32_t p0 = offsets[e], n = offsets[e + 1] - p0;
     if (n == 0) return;
@@ -505,62 +552,80 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))
             ((const uint4 *)(ex + (arr == 0 ? L::down_s : L::down_b) + (size_t)nt * NMOE_DN_ROWS * G * 2))[j];
     }
     const int rt0 = 64 * wave + col;
-    const uint32_t *wrow[4];
-#pragma unroll
-    for (int nb4 = 0; nb4 < 4; nb4++)
-        wrow[nb4] = (const uint32_t *)(ex + L::down_w) + (size_t)(nt * NMOE_DN_ROWS + rt0 + 16 * nb4) * Q::WPR_D;
+    const uint32_t *wbase = (const uint32_t *)(ex + L::down_w) + (size_t)nt * NMOE_DN_ROWS * Q::WPR_D;
     __syncthreads();
-    /* A loader: 2 planes x 64 rows x 8 uint4 = 1024 uint4: u = tid + 256 i ->
-     * plane u / 512, row (u / 8) % 64, chunk u % 8 */
     for (uint32_t m0 = 0; m0 < n; m0 += NMOE_MCHUNK) {
         const int nb = (int)min((n - m0 + 15) / 16, 4u);
-        uint4 ra[4];
-        uint32_t rb[4][2];
-        nmoe_dn_load_a(ra, ahi, alo, p0, m0, n, 0, tid);
-        nmoe_dn_load_b<BITS>(rb, wrow, 0, kb);
-        nmoe_f32x4 acc[4][4];
+        if (tid < NMOE_MCHUNK) s_q[tid] = perm[p0 + min(m0 + tid, n - 1)]; /* visible after the first ring barrier */
+        /* this lane's two stage rows: act rows p0 + m0 + 8 (2w + jj) + lane / 8 */
+        const uint16_t *srow[2][2];
 #pragma unroll
-        for (int mb = 0; mb < 4; mb++) {
-            const float *asr = as + (size_t)(p0 + min(m0 + 16 * mb + col, n - 1)) * G;
+        for (int jj = 0; jj < 2; jj++) {
+            const uint32_t m = min(m0 + 8 * (2 * wave + jj) + (lane >> 3), n - 1);
+            srow[0][jj] = ahi + (size_t)(p0 + m) * NMOE_INTER;
+            srow[1][jj] = alo + (size_t)(p0 + m) * NMOE_INTER;
+        }
+        auto issue = [&](int g, int st) {
+#pragma unroll
+            for (int pl = 0; pl < 2; pl++)
+                nmoe_stage_rows(stage(st).a[pl], srow[pl][0] + 64 * g, srow[pl][1] + 64 * g, 2 * wave, lane);
+#pragma unroll
+            for (int i = 0; i < BI; i++) nmoe_stage_codes<BITS>(stage(st).b, wbase, Q::WPR_D, g, BI * wave + i, lane);
+        };
+        nmoe_f32x4 acc[4][4];
+        {
+            float av[4][G / 4];
+#pragma unroll
+            for (int mb = 0; mb < 4; mb++) {
+                const float *asr = as + (size_t)(p0 + min(m0 + 16 * mb + col, n - 1)) * G;
+#pragma unroll
+                for (int tq = 0; tq < G / 4; tq++) av[mb][tq] = asr[4 * tq + kb];
+            }
 #pragma unroll
             for (int nb4 = 0; nb4 < 4; nb4++) {
-                acc[nb4][mb] = nmoe_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-                if (mb < nb) {
-                    const int rr = rt0 + 16 * nb4;
+                const int rr = rt0 + 16 * nb4;
+                float cv[G / 4];
 #pragma unroll
-                    for (int tq = 0; tq < G / 4; tq++) {
-                        const int gg = 4 * tq + kb;
-                        const float sc = nmoe_bf16f(s_sb[0][rr][gg]);
-                        const float c = nmoe_bf16f(s_sb[1][rr][gg]) - 128.0f * sc;
-                        acc[nb4][mb] = __builtin_amdgcn_mfma_f32_16x16x4f32(asr[gg], c, acc[nb4][mb], 0, 0, 0);
-                    }
+                for (int tq = 0; tq < G / 4; tq++) {
+                    const float sc = nmoe_bf16f(s_sb[0][rr][4 * tq + kb]);
+                    cv[tq] = nmoe_bf16f(s_sb[1][rr][4 * tq + kb]) - 128.0f * sc;
+                }
+#pragma unroll
+                for (int mb = 0; mb < 4; mb++) {
+                    acc[nb4][mb] = nmoe_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+                    if (mb < nb)
+#pragma unroll
+                        for (int tq = 0; tq < G / 4; tq++)
+                            acc[nb4][mb] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[mb][tq], cv[tq], acc[nb4][mb], 0, 0, 0);
                 }
             }
         }
-        nmoe_dn_store_a(s_a[0], ra, tid);
-#pragma unroll 1
-        for (int g = 0; g < G; g++) {
-            __syncthreads();
-            uint32_t cb[4][2];
+        nmoe_wait_vm<0>();
 #pragma unroll
-            for (int nb4 = 0; nb4 < 4; nb4++) cb[nb4][0] = rb[nb4][0], cb[nb4][1] = rb[nb4][1];
-            if (g + 1 < G) {
-                nmoe_dn_load_a(ra, ahi, alo, p0, m0, n, g + 1, tid);
-                nmoe_dn_load_b<BITS>(rb, wrow, g + 1, kb);
-            }
+        for (int st = 0; st < NMOE_NS - 1; st++) issue(st, st);
+        auto step = [&](int g, const int st) {
+            if (g + 2 < G)
+                nmoe_ring_barrier<2 * LPG>();
+            else if (g + 1 < G)
+                nmoe_ring_barrier<LPG>();
+            else
+                nmoe_ring_barrier<0>();
+            if (g + NMOE_NS - 1 < G) issue(g + NMOE_NS - 1, (st + NMOE_NS - 1) % NMOE_NS);
             uint4 bq[4][2];
             float sg[4];
 #pragma unroll
             for (int nb4 = 0; nb4 < 4; nb4++) {
-                nmoe_codes_bf16<BITS>(cb[nb4][0], cb[nb4][1], bq[nb4][0], bq[nb4][1]);
+                uint32_t w0, w1;
+                nmoe_stage_code_words<BITS>(stage(st).b, rt0 + 16 * nb4, kb, w0, w1);
+                nmoe_codes_bf16<BITS>(w0, w1, bq[nb4][0], bq[nb4][1]);
                 sg[nb4] = nmoe_bf16f(s_sb[0][rt0 + 16 * nb4][g]);
             }
-            const int buf = g & 1;
 #pragma unroll
             for (int mb = 0; mb < 4; mb++) {
                 if (mb < nb) {
-                    const uint4 h0 = s_a[buf][0][16 * mb + col][2 * kb], h1 = s_a[buf][0][16 * mb + col][2 * kb + 1];
-                    const uint4 l0 = s_a[buf][1][16 * mb + col][2 * kb], l1 = s_a[buf][1][16 * mb + col][2 * kb + 1];
+                    uint4 h0, h1, l0, l1;
+                    nmoe_stage_operand(stage(st).a[0], 16 * mb + col, kb, h0, h1);
+                    nmoe_stage_operand(stage(st).a[1], 16 * mb + col, kb, l0, l1);
 #pragma unroll
                     for (int nb4 = 0; nb4 < 4; nb4++) {
                         nmoe_f32x4 pp = nmoe_mfma16(h0, bq[nb4][0], nmoe_f32x4{0.0f, 0.0f, 0.0f, 0.0f});
@@ -572,8 +637,15 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))
                     }
                 }
             }
-            if (g + 1 < G) nmoe_dn_store_a(s_a[(g + 1) & 1], ra, tid);
-        }
+        };
+        step(0, 0);
+        step(1, 1);
+        step(2, 2);
+        step(3, 3);
+        step(4, 0);
+        step(5, 1);
+        step(6, 2);
+        step(7, 3);
 #pragma unroll
         for (int nb4 = 0; nb4 < 4; nb4++) {
             const int r = nt * NMOE_DN_ROWS + rt0 + 16 * nb4;
@@ -582,11 +654,11 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
                     const uint32_t m = m0 + 16 * mb + 4 * kb + i;
-                    if (mb < nb && m < n) y[(size_t)perm[p0 + m] * NMOE_HIDDEN + r] = acc[nb4][mb][i];
+                    if (mb < nb && m < n) y[(size_t)s_q[m - m0] * NMOE_HIDDEN + r] = acc[nb4][mb][i];
                 }
             }
         }
-        __syncthreads(); /* the stage buffers are reused by the next chunk */
+        __syncthreads(); /* the stage ring is reused by the next chunk */
     }
 }
 
