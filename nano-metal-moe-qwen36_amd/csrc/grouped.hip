@@ -49,8 +49,6 @@ typedef __attribute__((ext_vector_type(8))) __bf16 nmoe_bf16x8;
 typedef __attribute__((ext_vector_type(4))) float nmoe_f32x4;
 
 #define NMOE_DISPATCH_BLOCKS 16
-#define NMOE_GU_TILE 64   /* gate/up rows per block (one down-K group) */
-#define NMOE_DN_TILE 64   /* down rows per block */
 #define NMOE_MCHUNK 64    /* expert rows per pass (four 16-row MFMA blocks) */
 
 /* k offset (within a lane's 16-k span) of operand element `slot`
@@ -73,24 +71,28 @@ __device__ __forceinline__ int nmoe_kperm_inv(int off) {
  * q4: words w0 (k 0..7), w1 (k 8..15); q2: word w0 (k 0..15). */
 template <int BITS>
 __device__ __forceinline__ void nmoe_codes_bf16(uint32_t w0, uint32_t w1, uint4 &b0, uint4 &b1) {
+    /* 0x43004300 in a VGPR: (x & mask) | c is then one v_and_or_b32 with
+     * the mask in an SGPR (a VOP3 of gfx9 takes no literal) */
+    uint32_t c;
+    asm("v_mov_b32 %0, 0x43004300" : "=v"(c));
     if (BITS == 4) {
-        b0.x = (w0 & 0x000F000Fu) | 0x43004300u;
-        b0.y = ((w0 >> 4) & 0x000F000Fu) | 0x43004300u;
-        b0.z = ((w0 >> 8) & 0x000F000Fu) | 0x43004300u;
-        b0.w = ((w0 >> 12) & 0x000F000Fu) | 0x43004300u;
-        b1.x = (w1 & 0x000F000Fu) | 0x43004300u;
-        b1.y = ((w1 >> 4) & 0x000F000Fu) | 0x43004300u;
-        b1.z = ((w1 >> 8) & 0x000F000Fu) | 0x43004300u;
-        b1.w = ((w1 >> 12) & 0x000F000Fu) | 0x43004300u;
+        b0.x = (w0 & 0x000F000Fu) | c;
+        b0.y = ((w0 >> 4) & 0x000F000Fu) | c;
+        b0.z = ((w0 >> 8) & 0x000F000Fu) | c;
+        b0.w = ((w0 >> 12) & 0x000F000Fu) | c;
+        b1.x = (w1 & 0x000F000Fu) | c;
+        b1.y = ((w1 >> 4) & 0x000F000Fu) | c;
+        b1.z = ((w1 >> 8) & 0x000F000Fu) | c;
+        b1.w = ((w1 >> 12) & 0x000F000Fu) | c;
     } else {
-        b0.x = (w0 & 0x00030003u) | 0x43004300u;
-        b0.y = ((w0 >> 2) & 0x00030003u) | 0x43004300u;
-        b0.z = ((w0 >> 4) & 0x00030003u) | 0x43004300u;
-        b0.w = ((w0 >> 6) & 0x00030003u) | 0x43004300u;
-        b1.x = ((w0 >> 8) & 0x00030003u) | 0x43004300u;
-        b1.y = ((w0 >> 10) & 0x00030003u) | 0x43004300u;
-        b1.z = ((w0 >> 12) & 0x00030003u) | 0x43004300u;
-        b1.w = ((w0 >> 14) & 0x00030003u) | 0x43004300u;
+        b0.x = (w0 & 0x00030003u) | c;
+        b0.y = ((w0 >> 2) & 0x00030003u) | c;
+        b0.z = ((w0 >> 4) & 0x00030003u) | c;
+        b0.w = ((w0 >> 6) & 0x00030003u) | c;
+        b1.x = ((w0 >> 8) & 0x00030003u) | c;
+        b1.y = ((w0 >> 10) & 0x00030003u) | c;
+        b1.z = ((w0 >> 12) & 0x00030003u) | c;
+        b1.w = ((w0 >> 14) & 0x00030003u) | c;
     }
 }
 
@@ -231,62 +233,74 @@ __global__ void __launch_bounds__(256) nmoe_grouped_xprep_kernel(const XT *x, ui
     if ((tid & 7) == 0) xs[(size_t)t * (NMOE_HIDDEN / NMOE_GROUP) + (tid >> 3)] = sum;
 }
 
-/* ------------------------------------------------------------ gate/up */
+/* ------------------------------------------------------------ stage ring */
 
-/* A rows of one 64-deep group reach LDS by direct global->LDS loads
+/* Both GEMMs stream one 64-deep K group per step through a ring of
+ * NMOE_NS LDS stages, filled by direct global->LDS loads
  * (global_load_lds_dwordx4: lane l of a wavefront writes bytes 16l..16l+15
- * of the instruction's 1 KB), into a ring of NMOE_NS stages, so a group's
- * rows are requested NMOE_NS - 1 groups before they are multiplied.  A
- * stage row is 64 bf16 = 8 chunks of 16 bytes; chunk c of row r sits at
- * slot c ^ (r & 7), so the 16 rows one MFMA operand read touches spread
- * over the banks.  The codes of the weight rows go through a register ring
- * of the same depth. */
+ * of the instruction's 1 KB), so a group is requested NMOE_NS - 1 steps
+ * before it is multiplied.  A stage holds
+ *   - the A rows of the group: PL planes of 64 rows x 64 bf16 (128 B); the
+ *     16-byte chunk c of row r sits at slot c ^ ((r >> 1) & 7), so the 16
+ *     rows of one ds_read_b128 pass cover all 64 banks;
+ *   - the codes of the tile's weight rows for the group: rows of 32 B (q4,
+ *     whose two 16-byte halves swap on rows with bit 3 set, making the
+ *     ds_read_b64 of 16 rows x 2 lanes conflict-free) or 16 B (q2).
+ * Each stage is a __shared__ variable of its own: the compiler then tells
+ * the stages' direct loads apart and a read of one stage does not wait for
+ * the loads still in flight into the others. */
 #define NMOE_NS 4
 
 typedef __attribute__((address_space(3))) void nmoe_lds_void;
 
-/* One ring stage: the activation rows of a group (PL planes of 64 rows x
- * 64 bf16) and the codes of the tile's weight rows for that group.  Each
- * stage is a __shared__ variable of its own: the compiler then tells the
- * stages' direct loads apart and a read of one stage does not wait for
- * the loads still in flight into the others. */
 template <int PL, int CW>
 struct nmoe_stage {
     uint4 a[PL][NMOE_MCHUNK * 8];
     uint32_t b[CW];
 };
 
-/* Issue the direct loads of one stage: `nins` 1-KB instructions per
- * wavefront; instruction j of plane pl covers stage rows 8j..8j+7. */
-__device__ __forceinline__ void nmoe_stage_rows(uint4 *stage, const uint16_t *src_row0, const uint16_t *src_row1,
-                                                int j0, int lane) {
-    /* rows 8 j0 + (lane >> 3) and 8 (j0 + 1) + (lane >> 3): source row
-     * pointers already include the group's column offset */
-    const int slot = lane & 7;
-    const int r0 = 8 * j0 + (lane >> 3), r1 = r0 + 8;
-    const int c0 = slot ^ (r0 & 7), c1 = slot ^ (r1 & 7);
-    __builtin_amdgcn_global_load_lds((const void *)(src_row0 + 8 * c0), (nmoe_lds_void *)(stage + 64 * j0), 16, 0, 0);
-    __builtin_amdgcn_global_load_lds((const void *)(src_row1 + 8 * c1), (nmoe_lds_void *)(stage + 64 * (j0 + 1)), 16, 0, 0);
+/* Instruction j (rows 8j..8j+7) of one A plane: src_row is this lane's row
+ * (8j + lane / 8) pointer at the group's first column. */
+__device__ __forceinline__ void nmoe_stage_rows(uint4 *plane, const uint16_t *src_row, int j, int lane) {
+    const int r = 8 * j + (lane >> 3);
+    const int c = (lane & 7) ^ ((r >> 1) & 7);
+    __builtin_amdgcn_global_load_lds((const void *)(src_row + 8 * c), (nmoe_lds_void *)(plane + 64 * j), 16, 0, 0);
 }
 
-/* MFMA A operand (two slices) of stage row r, lane k-block kb. */
-__device__ __forceinline__ void nmoe_stage_operand(const uint4 *stage, int r, int kb, uint4 &a0, uint4 &a1) {
-    a0 = stage[8 * r + ((2 * kb) ^ (r & 7))];
-    a1 = stage[8 * r + ((2 * kb + 1) ^ (r & 7))];
+/* MFMA A operand (the lane's two 8-element chunks 2kb, 2kb+1) of row r. */
+__device__ __forceinline__ void nmoe_stage_operand(const uint4 *plane, int r, int kb, uint4 &a0, uint4 &a1) {
+    const int h = (r >> 1) & 7;
+    a0 = plane[8 * r + ((2 * kb) ^ h)];
+    a1 = plane[8 * r + ((2 * kb + 1) ^ h)];
 }
 
-/* Direct loads of one group's codes of `rows` weight rows (starting at
- * global row pointer base + row * wpr words, group g) into a stage of
- * [rows][wpg] words; wpg = 8 (q4) or 4 (q2) words = 32 / 16 bytes per row.
- * Instruction j of this wavefront covers 1 KB of the stage. */
+/* Code instructions per wavefront and stage: one 1-KB instruction (16 B a
+ * lane) for q4; two 256-byte instructions (4 B a lane) for q2, whose
+ * stage is half the size, so every wavefront issues the same number of
+ * loads and the ring waits are compile-time constants. */
+template <int BITS>
+struct nmoe_code_ins {
+    static constexpr int PER_WAVE = BITS == 4 ? 1 : 2;
+    static constexpr int BYTES = BITS == 4 ? 1024 : 256;
+};
+
+/* Instruction j of the codes of one group g: stage rows are weight rows
+ * base + row * wpr words. */
 template <int BITS>
 __device__ __forceinline__ void nmoe_stage_codes(uint32_t *stage, const uint32_t *base, int wpr, int g, int j,
                                                  int lane) {
-    constexpr int WPG = BITS == 4 ? 8 : 4;
-    const int byte = 1024 * j + 16 * lane;
-    const int row = byte / (4 * WPG), w = (byte % (4 * WPG)) / 4;
-    __builtin_amdgcn_global_load_lds((const void *)(base + (size_t)row * wpr + WPG * g + w),
-                                     (nmoe_lds_void *)(stage + 256 * j), 16, 0, 0);
+    if (BITS == 4) {
+        /* rows 32j + lane / 2, half lane % 2 (swapped on rows with bit 3 set) */
+        const int row = 32 * j + (lane >> 1);
+        const int half = (lane & 1) ^ ((row >> 3) & 1);
+        __builtin_amdgcn_global_load_lds((const void *)(base + (size_t)row * wpr + 8 * g + 4 * half),
+                                         (nmoe_lds_void *)(stage + 256 * j), 16, 0, 0);
+    } else {
+        /* rows 16j + lane / 4, word lane % 4 */
+        const int row = 16 * j + (lane >> 2);
+        __builtin_amdgcn_global_load_lds((const void *)(base + (size_t)row * wpr + 4 * g + (lane & 3)),
+                                         (nmoe_lds_void *)(stage + 64 * j), 4, 0, 0);
+    }
 }
 
 /* The lane's code words of stage row r: q4 words 2kb, 2kb+1; q2 word kb. */
@@ -294,7 +308,10 @@ template <int BITS>
 __device__ __forceinline__ void nmoe_stage_code_words(const uint32_t *stage, int r, int kb, uint32_t &w0,
                                                       uint32_t &w1) {
     if (BITS == 4) {
-        const uint2 v = *(const uint2 *)(stage + 8 * r + 2 * kb);
+        /* written as an index XOR: the compiler then still knows which
+         * stage the read belongs to */
+        const uint2 *rowp = (const uint2 *)(stage + 8 * r);
+        const uint2 v = rowp[kb ^ (2 * ((r >> 3) & 1))];
         w0 = v.x;
         w1 = v.y;
     } else {
@@ -314,6 +331,39 @@ __device__ __forceinline__ void nmoe_ring_barrier() {
     asm volatile("s_barrier" ::: "memory");
 }
 
+/* The barrier before group g of G, for a wavefront that issues L loads per
+ * group: groups g+1 and g+2 may still be in flight. */
+template <int L, int G>
+__device__ __forceinline__ void nmoe_ring_step_barrier(int g) {
+    if (g + 2 < G)
+        nmoe_ring_barrier<2 * L>();
+    else if (g + 1 < G)
+        nmoe_ring_barrier<L>();
+    else
+        nmoe_ring_barrier<0>();
+}
+
+/* Runs step(g, stage, issue_ahead) over the G groups: the loop body issues
+ * group g + NS - 1 unconditionally (a load issued under a runtime condition
+ * makes the compiler wait for every stage), the last NS - 1 steps issue
+ * nothing. */
+template <int G, typename Step>
+__device__ __forceinline__ void nmoe_ring_run(Step step) {
+    static_assert(G % NMOE_NS == 0, "whole ring turns");
+    constexpr int MAIN = G - NMOE_NS; /* steps in the loop */
+#pragma unroll 1
+    for (int g = 0; g < MAIN; g += NMOE_NS) {
+        step(g, 0, true);
+        step(g + 1, 1, true);
+        step(g + 2, 2, true);
+        step(g + 3, 3, true);
+    }
+    step(MAIN, 0, true);
+    step(MAIN + 1, 1, false);
+    step(MAIN + 2, 2, false);
+    step(MAIN + 3, 3, false);
+}
+
 template <int N>
 __device__ __forceinline__ void nmoe_wait_vm() {
     /* s_waitcnt vmcnt(N) (gfx9 encoding: vmcnt[3:0] | vmcnt[5:4] << 14,
@@ -321,72 +371,75 @@ __device__ __forceinline__ void nmoe_wait_vm() {
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-/* Expert blockIdx.x, gate/up rows 128 * blockIdx.y .. +127 (both
- * matrices): act rows of all the expert's entries.  Wave w owns gate and up
- * rows 32w..32w+31 of the tile as two 16-row MFMA column blocks each, over
- * four 16-row blocks of entries: a lane holds gate and up of the same
- * (entry, row). */
+/* ------------------------------------------------------------ gate/up */
+
+#define NMOE_GU_ROWS 128 /* gate rows (and up rows) per block: 16 per wavefront */
+
+/* Expert blockIdx.x, gate and up rows 128 * blockIdx.y .. +127 (one pair of
+ * down-K groups): act rows of all the expert's entries, 64 entries per
+ * pass.  Eight wavefronts, two per SIMD; wavefront w owns gate and up rows
+ * 16w..16w+15 of the tile as one MFMA column block each, over four 16-entry
+ * row blocks, so a lane holds gate and up of the same (entry, row).
+ *
+ * y = sum_g s_g P_g + sum_g (b_g - 128 s_g) xs_g with P_g the MFMA product
+ * of the group's A rows and the codes as bf16(128 + q); the second sum runs
+ * first, on the fp32 matrix cores. */
 template <int BITS, int XPL>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+__global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 nmoe_grouped_gateup_kernel(const uint8_t *pack, const uint16_t *xhi, const uint16_t *xlo, const float *xs,
                            const uint32_t *perm, const uint32_t *offsets, int k, uint16_t *ahi, uint16_t *alo,
                            float *as) {
     using Q = nmoe_q<BITS>;
     using L = nmoe_layout<BITS>;
     constexpr int G = NMOE_HIDDEN / NMOE_GROUP; /* 32 groups */
-    constexpr int NT = 2 * NMOE_GU_TILE;        /* 128 rows per matrix per block */
-    constexpr int WPG = BITS == 4 ? 8 : 4;      /* code words per row per group */
-    constexpr int BI = 2 * NT * WPG * 4 / 1024 / 4; /* code instructions per wavefront per stage: 2 (q4) / 1 (q2) */
-    constexpr int LPG = 2 * XPL + BI;           /* loads per group per wavefront */
+    constexpr int NT = NMOE_GU_ROWS;
+    constexpr int WPG = BITS == 4 ? 8 : 4;
+    using CI = nmoe_code_ins<BITS>;
+    constexpr int CPM = NT * WPG * 4 / CI::BYTES; /* code instructions per matrix: 4 (q4) / 8 (q2) */
     __shared__ uint16_t s_sb[4][NT][G];         /* gate s, gate b, up s, up b */
     typedef nmoe_stage<XPL, 2 * NT * WPG> Stage;
     __shared__ Stage s_st0, s_st1, s_st2, s_st3;
     auto stage = [&](int st) -> Stage & { return st == 0 ? s_st0 : st == 1 ? s_st1 : st == 2 ? s_st2 : s_st3; };
     __shared__ uint32_t s_tok[NMOE_MCHUNK];
-    __shared__ float s_as[4][NMOE_MCHUNK];
+    __shared__ float s_as[8][NMOE_MCHUNK];
     const int e = blockIdx.x, nt = blockIdx.y;
     const uint32_t p0 = offsets[e], n = offsets[e + 1] - p0;
     if (n == 0) return;
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, col = lane & 15, kb = lane >> 4;
+    const int tid = threadIdx.x, lane = tid & 63, col = lane & 15, kb = lane >> 4;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint8_t *ex = pack + (size_t)e * L::expert_size;
-    for (int i = tid; i < 4 * NT * G / 8; i += 256) {
+    for (int i = tid; i < 4 * NT * G / 8; i += 512) {
         const int arr = i / (NT * G / 8), j = i % (NT * G / 8);
         const uint32_t so = arr == 0 ? L::gate_s : arr == 1 ? L::gate_b : arr == 2 ? L::up_s : L::up_b;
         ((uint4 *)&s_sb[arr][0][0])[j] = ((const uint4 *)(ex + so + (size_t)nt * NT * G * 2))[j];
     }
-    const int rt0 = 32 * wave + col; /* tile row of column block nb2: rt0 + 16 nb2 */
-    const uint32_t *wbase[2] = {(const uint32_t *)(ex + L::gate_w) + (size_t)nt * NT * Q::WPR_G,
-                                (const uint32_t *)(ex + L::up_w) + (size_t)nt * NT * Q::WPR_G};
+    const int rt = 16 * wave + col; /* this lane's tile row */
+    /* this wavefront's code instructions CI::PER_WAVE * wave + i all fall in
+     * matrix cmat (gate for wavefronts 0-3, up for 4-7) */
+    const int cmat = wave >> 2;
+    const uint32_t *cbase = (const uint32_t *)(ex + (cmat == 0 ? L::gate_w : L::up_w)) + (size_t)nt * NT * Q::WPR_G;
 
     for (uint32_t m0 = 0; m0 < n; m0 += NMOE_MCHUNK) {
         if (tid < NMOE_MCHUNK) s_tok[tid] = perm[p0 + min(m0 + tid, n - 1)] / (uint32_t)k;
         __syncthreads();
         const int nb = (int)min((n - m0 + 15) / 16, 4u);
-        /* this lane's two stage rows (instructions 2w, 2w+1) */
-        const uint16_t *srow[XPL][2];
-#pragma unroll
-        for (int jj = 0; jj < 2; jj++) {
-            const uint32_t t = s_tok[8 * (2 * wave + jj) + (lane >> 3)];
-            srow[0][jj] = xhi + (size_t)t * NMOE_HIDDEN;
-            if (XPL == 2) srow[XPL - 1][jj] = xlo + (size_t)t * NMOE_HIDDEN;
-        }
+        /* this lane's A row for instruction `wave`: entry 8 wave + lane / 8 */
+        const uint32_t tsrc = s_tok[8 * wave + (lane >> 3)];
+        const uint16_t *srow[XPL];
+        srow[0] = xhi + (size_t)tsrc * NMOE_HIDDEN;
+        if (XPL == 2) srow[XPL - 1] = xlo + (size_t)tsrc * NMOE_HIDDEN;
         auto issue = [&](int g, int st) {
 #pragma unroll
-            for (int pl = 0; pl < XPL; pl++)
-                nmoe_stage_rows(stage(st).a[pl], srow[pl][0] + 64 * g, srow[pl][1] + 64 * g, 2 * wave, lane);
-            /* codes: 2 matrices x NT rows x WPG words = 8 (q4) / 4 (q2) KB */
+            for (int pl = 0; pl < XPL; pl++) nmoe_stage_rows(stage(st).a[pl], srow[pl] + 64 * g, wave, lane);
 #pragma unroll
-            for (int i = 0; i < BI; i++) {
-                const int j = BI * wave + i;                 /* 0 .. 4 BI - 1 */
-                const int mat = j / (2 * BI), jm = j % (2 * BI); /* instruction within the matrix */
-                nmoe_stage_codes<BITS>(stage(st).b + mat * NT * WPG, wbase[mat], Q::WPR_G, g, jm, lane);
-            }
+            for (int i = 0; i < CI::PER_WAVE; i++)
+                nmoe_stage_codes<BITS>(stage(st).b + cmat * NT * WPG, cbase, Q::WPR_G, g,
+                                       (CI::PER_WAVE * wave + i) % CPM, lane);
         };
-        /* sum_g (b_g - 128 s_g) xs_g on the fp32 cores: A lane = (entry col,
-         * group 4tq + kb), B lane = (row col, group 4tq + kb) */
-        nmoe_f32x4 acc[2][2][4];
+        nmoe_f32x4 acc[2][4];
         {
-            /* all operand loads first (one memory round trip), then the MFMAs */
+            /* all operand loads first (one memory round trip), then the MFMAs:
+             * A lane = (entry col, group 4tq + kb), B lane = (row col, group 4tq + kb) */
             float xv[4][G / 4];
 #pragma unroll
             for (int mb = 0; mb < 4; mb++) {
@@ -395,55 +448,42 @@ nmoe_grouped_gateup_kernel(const uint8_t *pack, const uint16_t *xhi, const uint1
                 for (int tq = 0; tq < G / 4; tq++) xv[mb][tq] = xsr[4 * tq + kb];
             }
 #pragma unroll
-            for (int mat = 0; mat < 2; mat++)
+            for (int mat = 0; mat < 2; mat++) {
+                float cv[G / 4];
 #pragma unroll
-                for (int nb2 = 0; nb2 < 2; nb2++) {
-                    const int rr = rt0 + 16 * nb2;
-                    float cv[G / 4];
-#pragma unroll
-                    for (int tq = 0; tq < G / 4; tq++) {
-                        const float sc = nmoe_bf16f(s_sb[2 * mat][rr][4 * tq + kb]);
-                        cv[tq] = nmoe_bf16f(s_sb[2 * mat + 1][rr][4 * tq + kb]) - 128.0f * sc;
-                    }
-#pragma unroll
-                    for (int mb = 0; mb < 4; mb++) {
-                        acc[mat][nb2][mb] = nmoe_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-                        if (mb < nb)
-#pragma unroll
-                            for (int tq = 0; tq < G / 4; tq++)
-                                acc[mat][nb2][mb] =
-                                    __builtin_amdgcn_mfma_f32_16x16x4f32(xv[mb][tq], cv[tq], acc[mat][nb2][mb], 0, 0, 0);
-                    }
+                for (int tq = 0; tq < G / 4; tq++) {
+                    const float sc = nmoe_bf16f(s_sb[2 * mat][rt][4 * tq + kb]);
+                    cv[tq] = nmoe_bf16f(s_sb[2 * mat + 1][rt][4 * tq + kb]) - 128.0f * sc;
                 }
+#pragma unroll
+                for (int mb = 0; mb < 4; mb++) {
+                    acc[mat][mb] = nmoe_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+                    if (mb < nb)
+#pragma unroll
+                        for (int tq = 0; tq < G / 4; tq++)
+                            acc[mat][mb] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[mb][tq], cv[tq], acc[mat][mb], 0, 0, 0);
+                }
+            }
         }
         /* keep every operand load above out of the vmcnt ring below */
         nmoe_wait_vm<0>();
 #pragma unroll
         for (int st = 0; st < NMOE_NS - 1; st++) issue(st, st);
-        auto step = [&](int g, const int st) {
-            /* group g's stage: groups g+1, g+2 may still be in flight */
-            if (g + 2 < G)
-                nmoe_ring_barrier<2 * LPG>();
-            else if (g + 1 < G)
-                nmoe_ring_barrier<LPG>();
-            else
-                nmoe_ring_barrier<0>();
-            if (g + NMOE_NS - 1 < G) issue(g + NMOE_NS - 1, (st + NMOE_NS - 1) % NMOE_NS);
-            uint4 bq[2][2][2];
-            float sg[2][2];
+        auto step = [&](int g, const int st, const bool ahead) {
+            nmoe_ring_step_barrier<XPL + CI::PER_WAVE, G>(g);
+            if (ahead) issue(g + NMOE_NS - 1, (st + NMOE_NS - 1) % NMOE_NS);
+            uint4 bq[2][2];
+            float sg[2];
 #pragma unroll
-            for (int mat = 0; mat < 2; mat++)
-#pragma unroll
-                for (int nb2 = 0; nb2 < 2; nb2++) {
-                    uint32_t w0, w1;
-                    /* kept apart: a read merged across the two matrices
-                     * loses the stage it belongs to, and then waits for
-                     * every stage's loads */
-                    if (mat == 1 && nb2 == 0) asm volatile("" ::: "memory");
-                    nmoe_stage_code_words<BITS>(stage(st).b + mat * NT * WPG, rt0 + 16 * nb2, kb, w0, w1);
-                    nmoe_codes_bf16<BITS>(w0, w1, bq[mat][nb2][0], bq[mat][nb2][1]);
-                    sg[mat][nb2] = nmoe_bf16f(s_sb[2 * mat][rt0 + 16 * nb2][g]);
-                }
+            for (int mat = 0; mat < 2; mat++) {
+                uint32_t w0, w1;
+                /* kept apart: a read merged across the two matrices loses
+                 * the stage it belongs to, and then waits for every stage */
+                if (mat == 1) asm volatile("" ::: "memory");
+                nmoe_stage_code_words<BITS>(stage(st).b + mat * NT * WPG, rt, kb, w0, w1);
+                nmoe_codes_bf16<BITS>(w0, w1, bq[mat][0], bq[mat][1]);
+                sg[mat] = nmoe_bf16f(s_sb[2 * mat][rt][g]);
+            }
 #pragma unroll
             for (int mb = 0; mb < 4; mb++) {
                 if (mb < nb) {
@@ -452,35 +492,25 @@ nmoe_grouped_gateup_kernel(const uint8_t *pack, const uint16_t *xhi, const uint1
                     for (int pl = 0; pl < XPL; pl++)
                         nmoe_stage_operand(stage(st).a[pl], 16 * mb + col, kb, a[pl][0], a[pl][1]);
 #pragma unroll
-                    for (int mat = 0; mat < 2; mat++)
-#pragma unroll
-                        for (int nb2 = 0; nb2 < 2; nb2++) {
-                            nmoe_f32x4 pp = nmoe_mfma16(a[0][0], bq[mat][nb2][0], nmoe_f32x4{0.0f, 0.0f, 0.0f, 0.0f});
-                            pp = nmoe_mfma16(a[0][1], bq[mat][nb2][1], pp);
-                            if (XPL == 2) {
-                                pp = nmoe_mfma16(a[XPL - 1][0], bq[mat][nb2][0], pp);
-                                pp = nmoe_mfma16(a[XPL - 1][1], bq[mat][nb2][1], pp);
-                            }
-#pragma unroll
-                            for (int i = 0; i < 4; i++)
-                                acc[mat][nb2][mb][i] = __builtin_fmaf(sg[mat][nb2], pp[i], acc[mat][nb2][mb][i]);
+                    for (int mat = 0; mat < 2; mat++) {
+                        nmoe_f32x4 pp = nmoe_mfma16(a[0][0], bq[mat][0], nmoe_f32x4{0.0f, 0.0f, 0.0f, 0.0f});
+                        pp = nmoe_mfma16(a[0][1], bq[mat][1], pp);
+                        if (XPL == 2) {
+                            pp = nmoe_mfma16(a[XPL - 1][0], bq[mat][0], pp);
+                            pp = nmoe_mfma16(a[XPL - 1][1], bq[mat][1], pp);
                         }
+#pragma unroll
+                        for (int i = 0; i < 4; i++) acc[mat][mb][i] = __builtin_fmaf(sg[mat], pp[i], acc[mat][mb][i]);
+                    }
                 }
             }
         };
-#pragma unroll 1
-        for (int g = 0; g < G; g += NMOE_NS) {
-            step(g, 0);
-            step(g + 1, 1);
-            step(g + 2, 2);
-            step(g + 3, 3);
-        }
+        nmoe_ring_run<G>(step);
         /* epilogue: act = SiLU(gate) * up as hi + lo bf16, in the down
          * kernel's operand order; group sums of act rows (a down group is
-         * 64 act columns = waves 0-1 or 2-3 of this tile) */
-#pragma unroll
-        for (int nb2 = 0; nb2 < 2; nb2++) {
-            const int r = nt * NT + rt0 + 16 * nb2; /* act column */
+         * 64 act columns = wavefronts 0-3 or 4-7 of this tile) */
+        {
+            const int r = nt * NT + rt; /* act column */
             const int span = r >> 4;
             const int slot = nmoe_kperm_inv<BITS>(r & 15);
 #pragma unroll
@@ -488,7 +518,7 @@ nmoe_grouped_gateup_kernel(const uint8_t *pack, const uint16_t *xhi, const uint1
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
                     const uint32_t m = m0 + 16 * mb + 4 * kb + i;
-                    const float av = nmoe_silu_dev(acc[0][nb2][mb][i]) * acc[1][nb2][mb][i];
+                    const float av = nmoe_silu_dev(acc[0][mb][i]) * acc[1][mb][i];
                     const uint32_t h = nmoe_bf16_rne(av);
                     const uint32_t l = nmoe_bf16_rne(av - nmoe_bf16f(h));
                     float part = nmoe_bf16f(h) + nmoe_bf16f(l);
@@ -498,12 +528,7 @@ nmoe_grouped_gateup_kernel(const uint8_t *pack, const uint16_t *xhi, const uint1
                         alo[o] = (uint16_t)l;
                     }
                     part = nmoe_dpp_group_sum<16>(part); /* the 16 rows of this column block */
-                    if (col == 0) {
-                        if (nb2 == 0)
-                            s_as[wave][16 * mb + 4 * kb + i] = part;
-                        else
-                            s_as[wave][16 * mb + 4 * kb + i] += part;
-                    }
+                    if (col == 0) s_as[wave][16 * mb + 4 * kb + i] = part;
                 }
             }
         }
@@ -513,7 +538,7 @@ nmoe_grouped_gateup_kernel(const uint8_t *pack, const uint16_t *xhi, const uint1
             const uint32_t m = m0 + row;
             if (m < n)
                 as[(size_t)(p0 + m) * (NMOE_INTER / NMOE_GROUP) + 2 * nt + half] =
-                    s_as[2 * half][row] + s_as[2 * half + 1][row];
+                    (s_as[4 * half][row] + s_as[4 * half + 1][row]) + (s_as[4 * half + 2][row] + s_as[4 * half + 3][row]);
         }
         __syncthreads();
     }
@@ -521,58 +546,54 @@ nmoe_grouped_gateup_kernel(const uint8_t *pack, const uint16_t *xhi, const uint1
 
 /* ------------------------------------------------------------ down */
 
-#define NMOE_DN_ROWS 256 /* down rows per block: 64 per wave */
+#define NMOE_DN_ROWS 256 /* down rows per block: 32 per wavefront */
 
 /* Expert blockIdx.x, down rows 256 * blockIdx.y .. +255: y[q][row] for all
- * the expert's entries q.  Wave w owns rows 64w..64w+63 of the tile as four
- * 16-row column blocks. */
+ * the expert's entries q.  Eight wavefronts; wavefront w owns rows
+ * 32w..32w+31 of the tile as two 16-row column blocks.  act enters as hi
+ * and lo bf16 planes. */
 template <int BITS>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+__global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 nmoe_grouped_down_kernel(const uint8_t *pack, const uint16_t *ahi, const uint16_t *alo, const float *as,
                          const uint32_t *perm, const uint32_t *offsets, float *y) {
     using Q = nmoe_q<BITS>;
     using L = nmoe_layout<BITS>;
     constexpr int G = NMOE_INTER / NMOE_GROUP; /* 8 groups */
     constexpr int WPG = BITS == 4 ? 8 : 4;
-    constexpr int BI = NMOE_DN_ROWS * WPG * 4 / 1024 / 4; /* code instructions per wavefront per stage: 2 / 1 */
-    constexpr int LPG = 4 + BI;                /* loads per group per wavefront: 2 planes x 2 + codes */
+    using CI = nmoe_code_ins<BITS>;
     __shared__ uint16_t s_sb[2][NMOE_DN_ROWS][G];
     typedef nmoe_stage<2, NMOE_DN_ROWS * WPG> Stage;
     __shared__ Stage s_st0, s_st1, s_st2, s_st3;
-    __shared__ uint32_t s_q[NMOE_MCHUNK]; /* the chunk's output slots */
     auto stage = [&](int st) -> Stage & { return st == 0 ? s_st0 : st == 1 ? s_st1 : st == 2 ? s_st2 : s_st3; };
+    __shared__ uint32_t s_q[NMOE_MCHUNK]; /* the chunk's output slots */
     const int e = blockIdx.x, nt = blockIdx.y;
     const uint32_t p0 = offsets[e], n = offsets[e + 1] - p0;
     if (n == 0) return;
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, col = lane & 15, kb = lane >> 4;
+    const int tid = threadIdx.x, lane = tid & 63, col = lane & 15, kb = lane >> 4;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint8_t *ex = pack + (size_t)e * L::expert_size;
-    for (int i = tid; i < 2 * NMOE_DN_ROWS * G / 8; i += 256) {
+    for (int i = tid; i < 2 * NMOE_DN_ROWS * G / 8; i += 512) {
         const int arr = i / (NMOE_DN_ROWS * G / 8), j = i % (NMOE_DN_ROWS * G / 8);
         ((uint4 *)&s_sb[arr][0][0])[j] =
             ((const uint4 *)(ex + (arr == 0 ? L::down_s : L::down_b) + (size_t)nt * NMOE_DN_ROWS * G * 2))[j];
     }
-    const int rt0 = 64 * wave + col;
-    const uint32_t *wbase = (const uint32_t *)(ex + L::down_w) + (size_t)nt * NMOE_DN_ROWS * Q::WPR_D;
+    const int rt0 = 32 * wave + col; /* tile row of column block nb: rt0 + 16 nb */
+    const uint32_t *cbase = (const uint32_t *)(ex + L::down_w) + (size_t)nt * NMOE_DN_ROWS * Q::WPR_D;
     __syncthreads();
     for (uint32_t m0 = 0; m0 < n; m0 += NMOE_MCHUNK) {
         const int nb = (int)min((n - m0 + 15) / 16, 4u);
         if (tid < NMOE_MCHUNK) s_q[tid] = perm[p0 + min(m0 + tid, n - 1)]; /* visible after the first ring barrier */
-        /* this lane's two stage rows: act rows p0 + m0 + 8 (2w + jj) + lane / 8 */
-        const uint16_t *srow[2][2];
-#pragma unroll
-        for (int jj = 0; jj < 2; jj++) {
-            const uint32_t m = min(m0 + 8 * (2 * wave + jj) + (lane >> 3), n - 1);
-            srow[0][jj] = ahi + (size_t)(p0 + m) * NMOE_INTER;
-            srow[1][jj] = alo + (size_t)(p0 + m) * NMOE_INTER;
-        }
+        /* this lane's A row for instruction `wave`: act row p0 + m0 + 8 wave + lane / 8 */
+        const uint32_t msrc = min(m0 + 8 * wave + (lane >> 3), n - 1);
+        const uint16_t *srow[2] = {ahi + (size_t)(p0 + msrc) * NMOE_INTER, alo + (size_t)(p0 + msrc) * NMOE_INTER};
         auto issue = [&](int g, int st) {
 #pragma unroll
-            for (int pl = 0; pl < 2; pl++)
-                nmoe_stage_rows(stage(st).a[pl], srow[pl][0] + 64 * g, srow[pl][1] + 64 * g, 2 * wave, lane);
+            for (int pl = 0; pl < 2; pl++) nmoe_stage_rows(stage(st).a[pl], srow[pl] + 64 * g, wave, lane);
 #pragma unroll
-            for (int i = 0; i < BI; i++) nmoe_stage_codes<BITS>(stage(st).b, wbase, Q::WPR_D, g, BI * wave + i, lane);
+            for (int i = 0; i < CI::PER_WAVE; i++)
+                nmoe_stage_codes<BITS>(stage(st).b, cbase, Q::WPR_D, g, CI::PER_WAVE * wave + i, lane);
         };
-        nmoe_f32x4 acc[4][4];
+        nmoe_f32x4 acc[2][4];
         {
             float av[4][G / 4];
 #pragma unroll
@@ -582,8 +603,8 @@ nmoe_grouped_down_kernel(const uint8_t *pack, const uint16_t *ahi, const uint16_
                 for (int tq = 0; tq < G / 4; tq++) av[mb][tq] = asr[4 * tq + kb];
             }
 #pragma unroll
-            for (int nb4 = 0; nb4 < 4; nb4++) {
-                const int rr = rt0 + 16 * nb4;
+            for (int nb2 = 0; nb2 < 2; nb2++) {
+                const int rr = rt0 + 16 * nb2;
                 float cv[G / 4];
 #pragma unroll
                 for (int tq = 0; tq < G / 4; tq++) {
@@ -592,33 +613,28 @@ nmoe_grouped_down_kernel(const uint8_t *pack, const uint16_t *ahi, const uint16_
                 }
 #pragma unroll
                 for (int mb = 0; mb < 4; mb++) {
-                    acc[nb4][mb] = nmoe_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+                    acc[nb2][mb] = nmoe_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
                     if (mb < nb)
 #pragma unroll
                         for (int tq = 0; tq < G / 4; tq++)
-                            acc[nb4][mb] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[mb][tq], cv[tq], acc[nb4][mb], 0, 0, 0);
+                            acc[nb2][mb] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[mb][tq], cv[tq], acc[nb2][mb], 0, 0, 0);
                 }
             }
         }
         nmoe_wait_vm<0>();
 #pragma unroll
         for (int st = 0; st < NMOE_NS - 1; st++) issue(st, st);
-        auto step = [&](int g, const int st) {
-            if (g + 2 < G)
-                nmoe_ring_barrier<2 * LPG>();
-            else if (g + 1 < G)
-                nmoe_ring_barrier<LPG>();
-            else
-                nmoe_ring_barrier<0>();
-            if (g + NMOE_NS - 1 < G) issue(g + NMOE_NS - 1, (st + NMOE_NS - 1) % NMOE_NS);
-            uint4 bq[4][2];
-            float sg[4];
+        auto step = [&](int g, const int st, const bool ahead) {
+            nmoe_ring_step_barrier<2 + CI::PER_WAVE, G>(g);
+            if (ahead) issue(g + NMOE_NS - 1, (st + NMOE_NS - 1) % NMOE_NS);
+            uint4 bq[2][2];
+            float sg[2];
 #pragma unroll
-            for (int nb4 = 0; nb4 < 4; nb4++) {
+            for (int nb2 = 0; nb2 < 2; nb2++) {
                 uint32_t w0, w1;
-                nmoe_stage_code_words<BITS>(stage(st).b, rt0 + 16 * nb4, kb, w0, w1);
-                nmoe_codes_bf16<BITS>(w0, w1, bq[nb4][0], bq[nb4][1]);
-                sg[nb4] = nmoe_bf16f(s_sb[0][rt0 + 16 * nb4][g]);
+                nmoe_stage_code_words<BITS>(stage(st).b, rt0 + 16 * nb2, kb, w0, w1);
+                nmoe_codes_bf16<BITS>(w0, w1, bq[nb2][0], bq[nb2][1]);
+                sg[nb2] = nmoe_bf16f(s_sb[0][rt0 + 16 * nb2][g]);
             }
 #pragma unroll
             for (int mb = 0; mb < 4; mb++) {
@@ -627,38 +643,31 @@ nmoe_grouped_down_kernel(const uint8_t *pack, const uint16_t *ahi, const uint16_
                     nmoe_stage_operand(stage(st).a[0], 16 * mb + col, kb, h0, h1);
                     nmoe_stage_operand(stage(st).a[1], 16 * mb + col, kb, l0, l1);
 #pragma unroll
-                    for (int nb4 = 0; nb4 < 4; nb4++) {
-                        nmoe_f32x4 pp = nmoe_mfma16(h0, bq[nb4][0], nmoe_f32x4{0.0f, 0.0f, 0.0f, 0.0f});
-                        pp = nmoe_mfma16(h1, bq[nb4][1], pp);
-                        pp = nmoe_mfma16(l0, bq[nb4][0], pp);
-                        pp = nmoe_mfma16(l1, bq[nb4][1], pp);
+                    for (int nb2 = 0; nb2 < 2; nb2++) {
+                        nmoe_f32x4 pp = nmoe_mfma16(h0, bq[nb2][0], nmoe_f32x4{0.0f, 0.0f, 0.0f, 0.0f});
+                        pp = nmoe_mfma16(h1, bq[nb2][1], pp);
+                        pp = nmoe_mfma16(l0, bq[nb2][0], pp);
+                        pp = nmoe_mfma16(l1, bq[nb2][1], pp);
 #pragma unroll
-                        for (int i = 0; i < 4; i++) acc[nb4][mb][i] = __builtin_fmaf(sg[nb4], pp[i], acc[nb4][mb][i]);
+                        for (int i = 0; i < 4; i++) acc[nb2][mb][i] = __builtin_fmaf(sg[nb2], pp[i], acc[nb2][mb][i]);
                     }
                 }
             }
         };
-        step(0, 0);
-        step(1, 1);
-        step(2, 2);
-        step(3, 3);
-        step(4, 0);
-        step(5, 1);
-        step(6, 2);
-        step(7, 3);
+        nmoe_ring_run<G>(step);
 #pragma unroll
-        for (int nb4 = 0; nb4 < 4; nb4++) {
-            const int r = nt * NMOE_DN_ROWS + rt0 + 16 * nb4;
+        for (int nb2 = 0; nb2 < 2; nb2++) {
+            const int r = nt * NMOE_DN_ROWS + rt0 + 16 * nb2;
 #pragma unroll
             for (int mb = 0; mb < 4; mb++) {
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
                     const uint32_t m = m0 + 16 * mb + 4 * kb + i;
-                    if (mb < nb && m < n) y[(size_t)s_q[m - m0] * NMOE_HIDDEN + r] = acc[nb4][mb][i];
+                    if (mb < nb && m < n) y[(size_t)s_q[m - m0] * NMOE_HIDDEN + r] = acc[nb2][mb][i];
                 }
             }
         }
-        __syncthreads(); /* the stage ring is reused by the next chunk */
+        __syncthreads(); /* the stage ring and s_q are reused by the next chunk */
     }
 }
 
@@ -732,18 +741,18 @@ static int nmoe_grouped_run(nmoe_hip_ctx *ctx, const uint8_t *pack, const void *
     else
         hipLaunchKernelGGL((nmoe_grouped_xprep_kernel<BITS, float>), dim3(ntok), dim3(256), 0, s, (const float *)x,
                            ctx->g_xhi, ctx->g_xlo, ctx->g_xs);
-    const dim3 ggu(NMOE_EXPERTS, NMOE_INTER / (2 * NMOE_GU_TILE)), gdn(NMOE_EXPERTS, NMOE_HIDDEN / NMOE_DN_ROWS);
+    const dim3 ggu(NMOE_EXPERTS, NMOE_INTER / NMOE_GU_ROWS), gdn(NMOE_EXPERTS, NMOE_HIDDEN / NMOE_DN_ROWS);
     if (bf)
-        hipLaunchKernelGGL((nmoe_grouped_gateup_kernel<BITS, 1>), ggu, dim3(256), 0, s, pack,
+        hipLaunchKernelGGL((nmoe_grouped_gateup_kernel<BITS, 1>), ggu, dim3(512), 0, s, pack,
                            (const uint16_t *)ctx->g_xhi, (const uint16_t *)ctx->g_xlo, (const float *)ctx->g_xs,
                            (const uint32_t *)ctx->g_perm, (const uint32_t *)ctx->g_offsets, k, ctx->g_ahi,
                            ctx->g_alo, ctx->g_as);
     else
-        hipLaunchKernelGGL((nmoe_grouped_gateup_kernel<BITS, 2>), ggu, dim3(256), 0, s, pack,
+        hipLaunchKernelGGL((nmoe_grouped_gateup_kernel<BITS, 2>), ggu, dim3(512), 0, s, pack,
                            (const uint16_t *)ctx->g_xhi, (const uint16_t *)ctx->g_xlo, (const float *)ctx->g_xs,
                            (const uint32_t *)ctx->g_perm, (const uint32_t *)ctx->g_offsets, k, ctx->g_ahi,
                            ctx->g_alo, ctx->g_as);
-    hipLaunchKernelGGL((nmoe_grouped_down_kernel<BITS>), gdn, dim3(256), 0, s, pack, (const uint16_t *)ctx->g_ahi,
+    hipLaunchKernelGGL((nmoe_grouped_down_kernel<BITS>), gdn, dim3(512), 0, s, pack, (const uint16_t *)ctx->g_ahi,
                        (const uint16_t *)ctx->g_alo, (const float *)ctx->g_as, (const uint32_t *)ctx->g_perm,
                        (const uint32_t *)ctx->g_offsets, ctx->g_y);
     hipLaunchKernelGGL(nmoe_grouped_combine_kernel, dim3(NMOE_HIDDEN / 256, ntok), dim3(256), 0, s,
