@@ -243,9 +243,10 @@ __global__ void __launch_bounds__(256) nmoe_grouped_xprep_kernel(const XT *x, ui
  *   - the A rows of the group: PL planes of 64 rows x 64 bf16 (128 B); the
  *     16-byte chunk c of row r sits at slot c ^ ((r >> 1) & 7), so the 16
  *     rows of one ds_read_b128 pass cover all 64 banks;
- *   - the codes of the tile's weight rows for the group: rows of 32 B (q4,
- *     whose two 16-byte halves swap on rows with bit 3 set, making the
- *     ds_read_b64 of 16 rows x 2 lanes conflict-free) or 16 B (q2).
+ *   - the codes of the tile's weight rows for the group: q4 as rows of
+ *     32 B whose two 16-byte halves swap on rows with bit 3 set (two lanes
+ *     fetch a row's 32 bytes; the swap spreads the ds_read_b64 of 16 rows
+ *     over more banks), q2 as rows of 16 B.
  * Each stage is a __shared__ variable of its own: the compiler then tells
  * the stages' direct loads apart and a read of one stage does not wait for
  * the loads still in flight into the others. */
@@ -274,26 +275,34 @@ __device__ __forceinline__ void nmoe_stage_operand(const uint4 *plane, int r, in
     a1 = plane[8 * r + ((2 * kb + 1) ^ h)];
 }
 
-/* Code instructions per wavefront and stage: one 1-KB instruction (16 B a
- * lane) for q4; two 256-byte instructions (4 B a lane) for q2, whose
- * stage is half the size, so every wavefront issues the same number of
- * loads and the ring waits are compile-time constants. */
-template <int BITS>
-struct nmoe_code_ins {
-    static constexpr int PER_WAVE = BITS == 4 ? 1 : 2;
-    static constexpr int BYTES = BITS == 4 ? 1024 : 256;
+/* The direct loads of one stage's codes (NR weight rows of 32 B (q4) or
+ * 16 B (q2)) over the eight wavefronts of a block: 1-KB instructions (16 B
+ * a lane) where each wavefront has at least 1 KB to load, else 256-byte
+ * ones (4 B a lane).  Every wavefront issues the same number, so the ring
+ * waits are compile-time constants. */
+template <int BITS, int NR>
+struct nmoe_code_plan {
+    static constexpr int BYTES = NR * (BITS == 4 ? 32 : 16);
+    static constexpr bool WIDE = BYTES / 8 >= 1024;
+    static constexpr int INS_BYTES = WIDE ? 1024 : 256;
+    static constexpr int PER_WAVE = BYTES / 8 / INS_BYTES;
+    static_assert(PER_WAVE >= 1 && PER_WAVE * INS_BYTES * 8 == BYTES, "codes split evenly over 8 wavefronts");
+    static_assert(WIDE || BITS == 2, "q4 stages are at least 8 KB");
 };
 
-/* Instruction j of the codes of one group g: stage rows are weight rows
- * base + row * wpr words. */
-template <int BITS>
+/* Instruction j of the codes of group g for one matrix of NR rows (global
+ * rows base + row * wpr words), in the stage layout above. */
+template <int BITS, int NR, bool WIDE>
 __device__ __forceinline__ void nmoe_stage_codes(uint32_t *stage, const uint32_t *base, int wpr, int g, int j,
                                                  int lane) {
     if (BITS == 4) {
-        /* rows 32j + lane / 2, half lane % 2 (swapped on rows with bit 3 set) */
-        const int row = 32 * j + (lane >> 1);
-        const int half = (lane & 1) ^ ((row >> 3) & 1);
+        /* rows 32j + lane / 2, half (lane % 2) ^ row bit 3 */
+        const int row = 32 * j + (lane >> 1), half = (lane & 1) ^ ((row >> 3) & 1);
         __builtin_amdgcn_global_load_lds((const void *)(base + (size_t)row * wpr + 8 * g + 4 * half),
+                                         (nmoe_lds_void *)(stage + 256 * j), 16, 0, 0);
+    } else if (WIDE) {
+        const int row = 64 * j + lane;
+        __builtin_amdgcn_global_load_lds((const void *)(base + (size_t)row * wpr + 4 * g),
                                          (nmoe_lds_void *)(stage + 256 * j), 16, 0, 0);
     } else {
         /* rows 16j + lane / 4, word lane % 4 */
@@ -303,13 +312,12 @@ __device__ __forceinline__ void nmoe_stage_codes(uint32_t *stage, const uint32_t
     }
 }
 
-/* The lane's code words of stage row r: q4 words 2kb, 2kb+1; q2 word kb. */
-template <int BITS>
+/* The lane's code words of stage row r (of NR): q4 words 2kb, 2kb+1; q2
+ * word kb. */
+template <int BITS, int NR>
 __device__ __forceinline__ void nmoe_stage_code_words(const uint32_t *stage, int r, int kb, uint32_t &w0,
                                                       uint32_t &w1) {
     if (BITS == 4) {
-        /* written as an index XOR: the compiler then still knows which
-         * stage the read belongs to */
         const uint2 *rowp = (const uint2 *)(stage + 8 * r);
         const uint2 v = rowp[kb ^ (2 * ((r >> 3) & 1))];
         w0 = v.x;
@@ -364,6 +372,13 @@ __device__ __forceinline__ void nmoe_ring_run(Step step) {
     step(MAIN + 3, 3, false);
 }
 
+/* Workgroup barrier over LDS only: waits for this wavefront's LDS accesses
+ * (lgkmcnt 0) but not for its global stores, which __syncthreads() would. */
+__device__ __forceinline__ void nmoe_lds_barrier() {
+    __builtin_amdgcn_s_waitcnt(0xC07F); /* vmcnt 63, expcnt 7, lgkmcnt 0 */
+    asm volatile("s_barrier" ::: "memory");
+}
+
 template <int N>
 __device__ __forceinline__ void nmoe_wait_vm() {
     /* s_waitcnt vmcnt(N) (gfx9 encoding: vmcnt[3:0] | vmcnt[5:4] << 14,
@@ -371,15 +386,35 @@ __device__ __forceinline__ void nmoe_wait_vm() {
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
+/* Block b of a 1-D grid of NMOE_EXPERTS * ntiles blocks -> (expert, tile).
+ * Blocks b, b+8, b+16, ... land on the same die (blocks are dealt to the
+ * eight dies in turn), so the tiles of one expert run side by side on one
+ * die and share its activation rows in that die's L2. */
+__device__ __forceinline__ void nmoe_die_tile(int b, int ntiles, int &e, int &nt) {
+    e = 8 * (b / (8 * ntiles)) + (b & 7);
+    nt = (b >> 3) % ntiles;
+}
+
+/* SiLU for the grouped path (outputs are checked to a tolerance there):
+ * the exp of a non-positive argument as in math.m:21-28, the reciprocal by
+ * v_rcp_f32 instead of a full division. */
+__device__ __forceinline__ float nmoe_silu_fast(float x) {
+    const float z = __expf(-fabsf(x));
+    const float r = __builtin_amdgcn_rcpf(1.0f + z);
+    return x * (x >= 0.0f ? r : z * r);
+}
+
 /* ------------------------------------------------------------ gate/up */
 
-#define NMOE_GU_ROWS 128 /* gate rows (and up rows) per block: 16 per wavefront */
+/* Gate (and up) rows per block: 256 for bf16 x (one A plane), 128 for fp32
+ * x (hi + lo planes), so a stage fits four times in LDS. */
+__host__ __device__ constexpr int nmoe_gu_rows(int xpl) { return xpl == 1 ? 256 : 128; }
 
-/* Expert blockIdx.x, gate and up rows 128 * blockIdx.y .. +127 (one pair of
- * down-K groups): act rows of all the expert's entries, 64 entries per
- * pass.  Eight wavefronts, two per SIMD; wavefront w owns gate and up rows
- * 16w..16w+15 of the tile as one MFMA column block each, over four 16-entry
- * row blocks, so a lane holds gate and up of the same (entry, row).
+/* Expert e, gate and up rows NT * nt .. +NT-1: act rows of all the
+ * expert's entries, 64 entries per pass.  Eight wavefronts, two per SIMD;
+ * wavefront w owns gate and up rows (NT/8)w .. +NT/8-1 of the tile as NB
+ * 16-row MFMA column blocks each, over four 16-entry row blocks, so a lane
+ * holds gate and up of the same (entry, row).
  *
  * y = sum_g s_g P_g + sum_g (b_g - 128 s_g) xs_g with P_g the MFMA product
  * of the group's A rows and the codes as bf16(128 + q); the second sum runs
@@ -392,36 +427,36 @@ nmoe_grouped_gateup_kernel(const uint8_t *pack, const uint16_t *xhi, const uint1
     using Q = nmoe_q<BITS>;
     using L = nmoe_layout<BITS>;
     constexpr int G = NMOE_HIDDEN / NMOE_GROUP; /* 32 groups */
-    constexpr int NT = NMOE_GU_ROWS;
+    static_assert(G == 32, "the correction's operand layout assumes 8 groups per lane");
+    constexpr int NT = nmoe_gu_rows(XPL);
+    constexpr int NB = NT / 128;                /* column blocks per wavefront and matrix */
     constexpr int WPG = BITS == 4 ? 8 : 4;
-    using CI = nmoe_code_ins<BITS>;
-    constexpr int CPM = NT * WPG * 4 / CI::BYTES; /* code instructions per matrix: 4 (q4) / 8 (q2) */
-    __shared__ uint16_t s_sb[4][NT][G];         /* gate s, gate b, up s, up b */
+    using CP = nmoe_code_plan<BITS, 2 * NT>;
+    constexpr int CPM = CP::BYTES / 2 / CP::INS_BYTES; /* code instructions per matrix */
+    __shared__ uint16_t s_s[2][NT][G];          /* gate and up scales of the tile */
     typedef nmoe_stage<XPL, 2 * NT * WPG> Stage;
     __shared__ Stage s_st0, s_st1, s_st2, s_st3;
     auto stage = [&](int st) -> Stage & { return st == 0 ? s_st0 : st == 1 ? s_st1 : st == 2 ? s_st2 : s_st3; };
     __shared__ uint32_t s_tok[NMOE_MCHUNK];
     __shared__ float s_as[8][NMOE_MCHUNK];
-    const int e = blockIdx.x, nt = blockIdx.y;
+    int e, nt;
+    nmoe_die_tile(blockIdx.x, NMOE_INTER / NT, e, nt);
     const uint32_t p0 = offsets[e], n = offsets[e + 1] - p0;
     if (n == 0) return;
     const int tid = threadIdx.x, lane = tid & 63, col = lane & 15, kb = lane >> 4;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint8_t *ex = pack + (size_t)e * L::expert_size;
-    for (int i = tid; i < 4 * NT * G / 8; i += 512) {
-        const int arr = i / (NT * G / 8), j = i % (NT * G / 8);
-        const uint32_t so = arr == 0 ? L::gate_s : arr == 1 ? L::gate_b : arr == 2 ? L::up_s : L::up_b;
-        ((uint4 *)&s_sb[arr][0][0])[j] = ((const uint4 *)(ex + so + (size_t)nt * NT * G * 2))[j];
-    }
-    const int rt = 16 * wave + col; /* this lane's tile row */
-    /* this wavefront's code instructions CI::PER_WAVE * wave + i all fall in
+    const int rt0 = (NT / 8) * wave + col; /* tile row of column block nb: rt0 + 16 nb */
+    /* this wavefront's code instructions CP::PER_WAVE * wave + i all fall in
      * matrix cmat (gate for wavefronts 0-3, up for 4-7) */
     const int cmat = wave >> 2;
     const uint32_t *cbase = (const uint32_t *)(ex + (cmat == 0 ? L::gate_w : L::up_w)) + (size_t)nt * NT * Q::WPR_G;
+    const uint16_t *bias[2] = {(const uint16_t *)(ex + L::gate_b) + (size_t)nt * NT * G,
+                               (const uint16_t *)(ex + L::up_b) + (size_t)nt * NT * G};
 
     for (uint32_t m0 = 0; m0 < n; m0 += NMOE_MCHUNK) {
         if (tid < NMOE_MCHUNK) s_tok[tid] = perm[p0 + min(m0 + tid, n - 1)] / (uint32_t)k;
-        __syncthreads();
+        nmoe_lds_barrier();
         const int nb = (int)min((n - m0 + 15) / 16, 4u);
         /* this lane's A row for instruction `wave`: entry 8 wave + lane / 8 */
         const uint32_t tsrc = s_tok[8 * wave + (lane >> 3)];
@@ -432,58 +467,89 @@ nmoe_grouped_gateup_kernel(const uint8_t *pack, const uint16_t *xhi, const uint1
 #pragma unroll
             for (int pl = 0; pl < XPL; pl++) nmoe_stage_rows(stage(st).a[pl], srow[pl] + 64 * g, wave, lane);
 #pragma unroll
-            for (int i = 0; i < CI::PER_WAVE; i++)
-                nmoe_stage_codes<BITS>(stage(st).b + cmat * NT * WPG, cbase, Q::WPR_G, g,
-                                       (CI::PER_WAVE * wave + i) % CPM, lane);
+            for (int i = 0; i < CP::PER_WAVE; i++)
+                nmoe_stage_codes<BITS, NT, CP::WIDE>(stage(st).b + cmat * NT * WPG, cbase, Q::WPR_G, g,
+                                                     (CP::PER_WAVE * wave + i) % CPM, lane);
         };
-        nmoe_f32x4 acc[2][4];
+        /* the first stages go out before the correction's loads, so their
+         * latency overlaps it */
+#pragma unroll
+        for (int st = 0; st < NMOE_NS - 1; st++) issue(st, st);
+        nmoe_f32x4 acc[2][NB][4];
         {
+            /* the tile's scales (first pass only) */
+            if (m0 == 0) {
+                constexpr int PER = 2 * NT * G / 8 / 512;
+                uint4 v[PER];
+#pragma unroll
+                for (int q = 0; q < PER; q++) {
+                    const int i = tid + 512 * q, mat = i / (NT * G / 8), j = i % (NT * G / 8);
+                    v[q] = ((const uint4 *)(ex + (mat == 0 ? L::gate_s : L::up_s) + (size_t)nt * NT * G * 2))[j];
+                }
+#pragma unroll
+                for (int q = 0; q < PER; q++) ((uint4 *)&s_s[0][0][0])[tid + 512 * q] = v[q];
+            }
             /* all operand loads first (one memory round trip), then the MFMAs:
-             * A lane = (entry col, group 4tq + kb), B lane = (row col, group 4tq + kb) */
+             * A lane = (entry col, groups 8kb + tq), B lane = (row col, groups
+             * 8kb + tq): a lane's eight groups are contiguous (two 16-byte
+             * loads of xs, one of the biases) */
+            float4 xv4[4][2];
+            uint4 bv[2][NB];
+#pragma unroll
+            for (int mb = 0; mb < 4; mb++) {
+                const float4 *xsr = (const float4 *)(xs + (size_t)s_tok[16 * mb + col] * G + 8 * kb);
+                xv4[mb][0] = xsr[0];
+                xv4[mb][1] = xsr[1];
+            }
+#pragma unroll
+            for (int mat = 0; mat < 2; mat++)
+#pragma unroll
+                for (int b2 = 0; b2 < NB; b2++)
+                    bv[mat][b2] = *(const uint4 *)(bias[mat] + (rt0 + 16 * b2) * G + 8 * kb);
+            __syncthreads(); /* the scales */
             float xv[4][G / 4];
 #pragma unroll
             for (int mb = 0; mb < 4; mb++) {
-                const float *xsr = xs + (size_t)s_tok[16 * mb + col] * G;
-#pragma unroll
-                for (int tq = 0; tq < G / 4; tq++) xv[mb][tq] = xsr[4 * tq + kb];
+                xv[mb][0] = xv4[mb][0].x, xv[mb][1] = xv4[mb][0].y, xv[mb][2] = xv4[mb][0].z, xv[mb][3] = xv4[mb][0].w;
+                xv[mb][4] = xv4[mb][1].x, xv[mb][5] = xv4[mb][1].y, xv[mb][6] = xv4[mb][1].z, xv[mb][7] = xv4[mb][1].w;
             }
 #pragma unroll
-            for (int mat = 0; mat < 2; mat++) {
-                float cv[G / 4];
+            for (int mat = 0; mat < 2; mat++)
 #pragma unroll
-                for (int tq = 0; tq < G / 4; tq++) {
-                    const float sc = nmoe_bf16f(s_sb[2 * mat][rt][4 * tq + kb]);
-                    cv[tq] = nmoe_bf16f(s_sb[2 * mat + 1][rt][4 * tq + kb]) - 128.0f * sc;
+                for (int b2 = 0; b2 < NB; b2++) {
+                    float cv[G / 4], bf[8], sf[8];
+                    nmoe_unpack_bf16x8(bv[mat][b2], bf);
+                    nmoe_unpack_bf16x8(*(const uint4 *)&s_s[mat][rt0 + 16 * b2][8 * kb], sf);
+#pragma unroll
+                    for (int tq = 0; tq < G / 4; tq++) cv[tq] = bf[tq] - 128.0f * sf[tq];
+#pragma unroll
+                    for (int mb = 0; mb < 4; mb++) {
+                        acc[mat][b2][mb] = nmoe_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+                        if (mb < nb)
+#pragma unroll
+                            for (int tq = 0; tq < G / 4; tq++)
+                                acc[mat][b2][mb] =
+                                    __builtin_amdgcn_mfma_f32_16x16x4f32(xv[mb][tq], cv[tq], acc[mat][b2][mb], 0, 0, 0);
+                    }
                 }
-#pragma unroll
-                for (int mb = 0; mb < 4; mb++) {
-                    acc[mat][mb] = nmoe_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-                    if (mb < nb)
-#pragma unroll
-                        for (int tq = 0; tq < G / 4; tq++)
-                            acc[mat][mb] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[mb][tq], cv[tq], acc[mat][mb], 0, 0, 0);
-                }
-            }
         }
-        /* keep every operand load above out of the vmcnt ring below */
-        nmoe_wait_vm<0>();
-#pragma unroll
-        for (int st = 0; st < NMOE_NS - 1; st++) issue(st, st);
         auto step = [&](int g, const int st, const bool ahead) {
-            nmoe_ring_step_barrier<XPL + CI::PER_WAVE, G>(g);
+            nmoe_ring_step_barrier<XPL + CP::PER_WAVE, G>(g);
             if (ahead) issue(g + NMOE_NS - 1, (st + NMOE_NS - 1) % NMOE_NS);
-            uint4 bq[2][2];
-            float sg[2];
+            uint4 bq[2][NB][2];
+            float sg[2][NB];
 #pragma unroll
-            for (int mat = 0; mat < 2; mat++) {
-                uint32_t w0, w1;
-                /* kept apart: a read merged across the two matrices loses
-                 * the stage it belongs to, and then waits for every stage */
-                if (mat == 1) asm volatile("" ::: "memory");
-                nmoe_stage_code_words<BITS>(stage(st).b + mat * NT * WPG, rt, kb, w0, w1);
-                nmoe_codes_bf16<BITS>(w0, w1, bq[mat][0], bq[mat][1]);
-                sg[mat] = nmoe_bf16f(s_sb[2 * mat][rt][g]);
-            }
+            for (int mat = 0; mat < 2; mat++)
+#pragma unroll
+                for (int b2 = 0; b2 < NB; b2++) {
+                    uint32_t w0, w1;
+                    /* kept apart: a read merged across the two matrices loses
+                     * the stage it belongs to, and then waits for every stage */
+                    if (mat == 1 && b2 == 0) asm volatile("" ::: "memory");
+                    nmoe_stage_code_words<BITS, NT>(stage(st).b + mat * NT * WPG, rt0 + 16 * b2, kb, w0, w1);
+                    nmoe_codes_bf16<BITS>(w0, w1, bq[mat][b2][0], bq[mat][b2][1]);
+                    sg[mat][b2] = nmoe_bf16f(s_s[mat][rt0 + 16 * b2][g]);
+                }
 #pragma unroll
             for (int mb = 0; mb < 4; mb++) {
                 if (mb < nb) {
@@ -492,66 +558,79 @@ nmoe_grouped_gateup_kernel(const uint8_t *pack, const uint16_t *xhi, const uint1
                     for (int pl = 0; pl < XPL; pl++)
                         nmoe_stage_operand(stage(st).a[pl], 16 * mb + col, kb, a[pl][0], a[pl][1]);
 #pragma unroll
-                    for (int mat = 0; mat < 2; mat++) {
-                        nmoe_f32x4 pp = nmoe_mfma16(a[0][0], bq[mat][0], nmoe_f32x4{0.0f, 0.0f, 0.0f, 0.0f});
-                        pp = nmoe_mfma16(a[0][1], bq[mat][1], pp);
-                        if (XPL == 2) {
-                            pp = nmoe_mfma16(a[XPL - 1][0], bq[mat][0], pp);
-                            pp = nmoe_mfma16(a[XPL - 1][1], bq[mat][1], pp);
-                        }
+                    for (int mat = 0; mat < 2; mat++)
 #pragma unroll
-                        for (int i = 0; i < 4; i++) acc[mat][mb][i] = __builtin_fmaf(sg[mat], pp[i], acc[mat][mb][i]);
-                    }
+                        for (int b2 = 0; b2 < NB; b2++) {
+                            nmoe_f32x4 pp = nmoe_mfma16(a[0][0], bq[mat][b2][0], nmoe_f32x4{0.0f, 0.0f, 0.0f, 0.0f});
+                            pp = nmoe_mfma16(a[0][1], bq[mat][b2][1], pp);
+                            if (XPL == 2) {
+                                pp = nmoe_mfma16(a[XPL - 1][0], bq[mat][b2][0], pp);
+                                pp = nmoe_mfma16(a[XPL - 1][1], bq[mat][b2][1], pp);
+                            }
+#pragma unroll
+                            for (int i = 0; i < 4; i++)
+                                acc[mat][b2][mb][i] = __builtin_fmaf(sg[mat][b2], pp[i], acc[mat][b2][mb][i]);
+                        }
                 }
             }
         };
         nmoe_ring_run<G>(step);
         /* epilogue: act = SiLU(gate) * up as hi + lo bf16, in the down
-         * kernel's operand order; group sums of act rows (a down group is
-         * 64 act columns = wavefronts 0-3 or 4-7 of this tile) */
-        {
-            const int r = nt * NT + rt; /* act column */
+         * kernel's operand order; group sums of act rows (a down group is 64
+         * act columns = 512 / NT wavefronts of this tile) */
+        float part_sum[4][4] = {};
+#pragma unroll
+        for (int b2 = 0; b2 < NB; b2++) {
+            const int r = nt * NT + rt0 + 16 * b2; /* act column */
             const int span = r >> 4;
             const int slot = nmoe_kperm_inv<BITS>(r & 15);
 #pragma unroll
             for (int mb = 0; mb < 4; mb++) {
+                if (mb >= nb) continue;
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
                     const uint32_t m = m0 + 16 * mb + 4 * kb + i;
-                    const float av = nmoe_silu_dev(acc[0][mb][i]) * acc[1][mb][i];
+                    const float av = nmoe_silu_fast(acc[0][b2][mb][i]) * acc[1][b2][mb][i];
                     const uint32_t h = nmoe_bf16_rne(av);
                     const uint32_t l = nmoe_bf16_rne(av - nmoe_bf16f(h));
                     float part = nmoe_bf16f(h) + nmoe_bf16f(l);
-                    if (mb < nb && m < n) {
+                    if (m < n) {
                         const size_t o = (size_t)(p0 + m) * NMOE_INTER + 16 * span + slot;
                         ahi[o] = (uint16_t)h;
                         alo[o] = (uint16_t)l;
                     }
                     part = nmoe_dpp_group_sum<16>(part); /* the 16 rows of this column block */
-                    if (col == 0) s_as[wave][16 * mb + 4 * kb + i] = part;
+                    part_sum[mb][i] = b2 == 0 ? part : part_sum[mb][i] + part;
                 }
             }
         }
-        __syncthreads();
-        if (tid < 2 * NMOE_MCHUNK) {
-            const int half = tid >> 6, row = tid & 63;
+        if (col == 0)
+#pragma unroll
+            for (int mb = 0; mb < 4; mb++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) s_as[wave][16 * mb + 4 * kb + i] = part_sum[mb][i];
+        nmoe_lds_barrier();
+        constexpr int DG = NT / 64;   /* down groups per tile */
+        constexpr int WPD = 8 / DG;   /* wavefronts per down group */
+        if (tid < DG * NMOE_MCHUNK) {
+            const int dg = tid / NMOE_MCHUNK, row = tid % NMOE_MCHUNK;
             const uint32_t m = m0 + row;
-            if (m < n)
-                as[(size_t)(p0 + m) * (NMOE_INTER / NMOE_GROUP) + 2 * nt + half] =
-                    (s_as[4 * half][row] + s_as[4 * half + 1][row]) + (s_as[4 * half + 2][row] + s_as[4 * half + 3][row]);
+            float t = s_as[WPD * dg][row];
+#pragma unroll
+            for (int q = 1; q < WPD; q++) t = t + s_as[WPD * dg + q][row];
+            if (m < n) as[(size_t)(p0 + m) * (NMOE_INTER / NMOE_GROUP) + DG * nt + dg] = t;
         }
-        __syncthreads();
+        nmoe_lds_barrier(); /* s_tok, s_as and the stages are reused by the next pass */
     }
 }
 
 /* ------------------------------------------------------------ down */
 
-#define NMOE_DN_ROWS 256 /* down rows per block: 32 per wavefront */
+#define NMOE_DN_ROWS 512 /* down rows per block: 64 per wavefront */
 
-/* Expert blockIdx.x, down rows 256 * blockIdx.y .. +255: y[q][row] for all
- * the expert's entries q.  Eight wavefronts; wavefront w owns rows
- * 32w..32w+31 of the tile as two 16-row column blocks.  act enters as hi
- * and lo bf16 planes. */
+/* Expert e, down rows 512 * nt .. +511: y[q][row] for all the expert's
+ * entries q.  Eight wavefronts; wavefront w owns rows 64w..64w+63 of the
+ * tile as four 16-row column blocks.  act enters as hi and lo bf16 planes. */
 template <int BITS>
 __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 nmoe_grouped_down_kernel(const uint8_t *pack, const uint16_t *ahi, const uint16_t *alo, const float *as,
@@ -559,30 +638,29 @@ nmoe_grouped_down_kernel(const uint8_t *pack, const uint16_t *ahi, const uint16_
     using Q = nmoe_q<BITS>;
     using L = nmoe_layout<BITS>;
     constexpr int G = NMOE_INTER / NMOE_GROUP; /* 8 groups */
+    static_assert(G == 8, "the correction's operand layout assumes 2 groups per lane");
+    constexpr int NT = NMOE_DN_ROWS;
+    constexpr int NB = NT / 128;
     constexpr int WPG = BITS == 4 ? 8 : 4;
-    using CI = nmoe_code_ins<BITS>;
-    __shared__ uint16_t s_sb[2][NMOE_DN_ROWS][G];
-    typedef nmoe_stage<2, NMOE_DN_ROWS * WPG> Stage;
+    using CP = nmoe_code_plan<BITS, NT>;
+    __shared__ uint16_t s_s[NT][G]; /* scales of the tile */
+    typedef nmoe_stage<2, NT * WPG> Stage;
     __shared__ Stage s_st0, s_st1, s_st2, s_st3;
     auto stage = [&](int st) -> Stage & { return st == 0 ? s_st0 : st == 1 ? s_st1 : st == 2 ? s_st2 : s_st3; };
     __shared__ uint32_t s_q[NMOE_MCHUNK]; /* the chunk's output slots */
-    const int e = blockIdx.x, nt = blockIdx.y;
+    int e, nt;
+    nmoe_die_tile(blockIdx.x, NMOE_HIDDEN / NT, e, nt);
     const uint32_t p0 = offsets[e], n = offsets[e + 1] - p0;
     if (n == 0) return;
     const int tid = threadIdx.x, lane = tid & 63, col = lane & 15, kb = lane >> 4;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint8_t *ex = pack + (size_t)e * L::expert_size;
-    for (int i = tid; i < 2 * NMOE_DN_ROWS * G / 8; i += 512) {
-        const int arr = i / (NMOE_DN_ROWS * G / 8), j = i % (NMOE_DN_ROWS * G / 8);
-        ((uint4 *)&s_sb[arr][0][0])[j] =
-            ((const uint4 *)(ex + (arr == 0 ? L::down_s : L::down_b) + (size_t)nt * NMOE_DN_ROWS * G * 2))[j];
-    }
-    const int rt0 = 32 * wave + col; /* tile row of column block nb: rt0 + 16 nb */
-    const uint32_t *cbase = (const uint32_t *)(ex + L::down_w) + (size_t)nt * NMOE_DN_ROWS * Q::WPR_D;
-    __syncthreads();
+    const int rt0 = (NT / 8) * wave + col; /* tile row of column block nb: rt0 + 16 nb */
+    const uint32_t *cbase = (const uint32_t *)(ex + L::down_w) + (size_t)nt * NT * Q::WPR_D;
+    const uint16_t *bias = (const uint16_t *)(ex + L::down_b) + (size_t)nt * NT * G;
     for (uint32_t m0 = 0; m0 < n; m0 += NMOE_MCHUNK) {
         const int nb = (int)min((n - m0 + 15) / 16, 4u);
-        if (tid < NMOE_MCHUNK) s_q[tid] = perm[p0 + min(m0 + tid, n - 1)]; /* visible after the first ring barrier */
+        if (tid < NMOE_MCHUNK) s_q[tid] = perm[p0 + min(m0 + tid, n - 1)]; /* visible after the barrier below */
         /* this lane's A row for instruction `wave`: act row p0 + m0 + 8 wave + lane / 8 */
         const uint32_t msrc = min(m0 + 8 * wave + (lane >> 3), n - 1);
         const uint16_t *srow[2] = {ahi + (size_t)(p0 + msrc) * NMOE_INTER, alo + (size_t)(p0 + msrc) * NMOE_INTER};
@@ -590,51 +668,59 @@ nmoe_grouped_down_kernel(const uint8_t *pack, const uint16_t *ahi, const uint16_
 #pragma unroll
             for (int pl = 0; pl < 2; pl++) nmoe_stage_rows(stage(st).a[pl], srow[pl] + 64 * g, wave, lane);
 #pragma unroll
-            for (int i = 0; i < CI::PER_WAVE; i++)
-                nmoe_stage_codes<BITS>(stage(st).b, cbase, Q::WPR_D, g, CI::PER_WAVE * wave + i, lane);
+            for (int i = 0; i < CP::PER_WAVE; i++)
+                nmoe_stage_codes<BITS, NT, CP::WIDE>(stage(st).b, cbase, Q::WPR_D, g, CP::PER_WAVE * wave + i, lane);
         };
-        nmoe_f32x4 acc[2][4];
+        /* the first stages go out before the correction's loads */
+#pragma unroll
+        for (int st = 0; st < NMOE_NS - 1; st++) issue(st, st);
+        nmoe_f32x4 acc[NB][4];
         {
-            float av[4][G / 4];
+            if (m0 == 0) {
+                constexpr int PER = NT * G / 8 / 512;
+                uint4 v[PER];
 #pragma unroll
-            for (int mb = 0; mb < 4; mb++) {
-                const float *asr = as + (size_t)(p0 + min(m0 + 16 * mb + col, n - 1)) * G;
+                for (int q = 0; q < PER; q++) v[q] = ((const uint4 *)(ex + L::down_s + (size_t)nt * NT * G * 2))[tid + 512 * q];
 #pragma unroll
-                for (int tq = 0; tq < G / 4; tq++) av[mb][tq] = asr[4 * tq + kb];
+                for (int q = 0; q < PER; q++) ((uint4 *)&s_s[0][0])[tid + 512 * q] = v[q];
             }
+            /* A lane = (entry col, groups 2kb + tq), B lane = (row col, groups 2kb + tq) */
+            float2 av[4];
+            uint32_t bv[NB];
 #pragma unroll
-            for (int nb2 = 0; nb2 < 2; nb2++) {
-                const int rr = rt0 + 16 * nb2;
+            for (int mb = 0; mb < 4; mb++)
+                av[mb] = *(const float2 *)(as + (size_t)(p0 + min(m0 + 16 * mb + col, n - 1)) * G + 2 * kb);
+#pragma unroll
+            for (int b2 = 0; b2 < NB; b2++) bv[b2] = *(const uint32_t *)(bias + (rt0 + 16 * b2) * G + 2 * kb);
+            __syncthreads(); /* the scales and s_q */
+#pragma unroll
+            for (int b2 = 0; b2 < NB; b2++) {
                 float cv[G / 4];
-#pragma unroll
-                for (int tq = 0; tq < G / 4; tq++) {
-                    const float sc = nmoe_bf16f(s_sb[0][rr][4 * tq + kb]);
-                    cv[tq] = nmoe_bf16f(s_sb[1][rr][4 * tq + kb]) - 128.0f * sc;
-                }
+                const uint32_t sw = *(const uint32_t *)&s_s[rt0 + 16 * b2][2 * kb];
+                cv[0] = __uint_as_float(bv[b2] << 16) - 128.0f * __uint_as_float(sw << 16);
+                cv[1] = __uint_as_float(bv[b2] & 0xffff0000u) - 128.0f * __uint_as_float(sw & 0xffff0000u);
 #pragma unroll
                 for (int mb = 0; mb < 4; mb++) {
-                    acc[nb2][mb] = nmoe_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+                    acc[b2][mb] = nmoe_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
                     if (mb < nb)
 #pragma unroll
                         for (int tq = 0; tq < G / 4; tq++)
-                            acc[nb2][mb] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[mb][tq], cv[tq], acc[nb2][mb], 0, 0, 0);
+                            acc[b2][mb] = __builtin_amdgcn_mfma_f32_16x16x4f32(tq == 0 ? av[mb].x : av[mb].y, cv[tq],
+                                                                               acc[b2][mb], 0, 0, 0);
                 }
             }
         }
-        nmoe_wait_vm<0>();
-#pragma unroll
-        for (int st = 0; st < NMOE_NS - 1; st++) issue(st, st);
         auto step = [&](int g, const int st, const bool ahead) {
-            nmoe_ring_step_barrier<2 + CI::PER_WAVE, G>(g);
+            nmoe_ring_step_barrier<2 + CP::PER_WAVE, G>(g);
             if (ahead) issue(g + NMOE_NS - 1, (st + NMOE_NS - 1) % NMOE_NS);
-            uint4 bq[2][2];
-            float sg[2];
+            uint4 bq[NB][2];
+            float sg[NB];
 #pragma unroll
-            for (int nb2 = 0; nb2 < 2; nb2++) {
+            for (int b2 = 0; b2 < NB; b2++) {
                 uint32_t w0, w1;
-                nmoe_stage_code_words<BITS>(stage(st).b, rt0 + 16 * nb2, kb, w0, w1);
-                nmoe_codes_bf16<BITS>(w0, w1, bq[nb2][0], bq[nb2][1]);
-                sg[nb2] = nmoe_bf16f(s_sb[0][rt0 + 16 * nb2][g]);
+                nmoe_stage_code_words<BITS, NT>(stage(st).b, rt0 + 16 * b2, kb, w0, w1);
+                nmoe_codes_bf16<BITS>(w0, w1, bq[b2][0], bq[b2][1]);
+                sg[b2] = nmoe_bf16f(s_s[rt0 + 16 * b2][g]);
             }
 #pragma unroll
             for (int mb = 0; mb < 4; mb++) {
@@ -643,31 +729,31 @@ nmoe_grouped_down_kernel(const uint8_t *pack, const uint16_t *ahi, const uint16_
                     nmoe_stage_operand(stage(st).a[0], 16 * mb + col, kb, h0, h1);
                     nmoe_stage_operand(stage(st).a[1], 16 * mb + col, kb, l0, l1);
 #pragma unroll
-                    for (int nb2 = 0; nb2 < 2; nb2++) {
-                        nmoe_f32x4 pp = nmoe_mfma16(h0, bq[nb2][0], nmoe_f32x4{0.0f, 0.0f, 0.0f, 0.0f});
-                        pp = nmoe_mfma16(h1, bq[nb2][1], pp);
-                        pp = nmoe_mfma16(l0, bq[nb2][0], pp);
-                        pp = nmoe_mfma16(l1, bq[nb2][1], pp);
+                    for (int b2 = 0; b2 < NB; b2++) {
+                        nmoe_f32x4 pp = nmoe_mfma16(h0, bq[b2][0], nmoe_f32x4{0.0f, 0.0f, 0.0f, 0.0f});
+                        pp = nmoe_mfma16(h1, bq[b2][1], pp);
+                        pp = nmoe_mfma16(l0, bq[b2][0], pp);
+                        pp = nmoe_mfma16(l1, bq[b2][1], pp);
 #pragma unroll
-                        for (int i = 0; i < 4; i++) acc[nb2][mb][i] = __builtin_fmaf(sg[nb2], pp[i], acc[nb2][mb][i]);
+                        for (int i = 0; i < 4; i++) acc[b2][mb][i] = __builtin_fmaf(sg[b2], pp[i], acc[b2][mb][i]);
                     }
                 }
             }
         };
         nmoe_ring_run<G>(step);
 #pragma unroll
-        for (int nb2 = 0; nb2 < 2; nb2++) {
-            const int r = nt * NMOE_DN_ROWS + rt0 + 16 * nb2;
+        for (int b2 = 0; b2 < NB; b2++) {
+            const int r = nt * NT + rt0 + 16 * b2;
 #pragma unroll
             for (int mb = 0; mb < 4; mb++) {
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
                     const uint32_t m = m0 + 16 * mb + 4 * kb + i;
-                    if (mb < nb && m < n) y[(size_t)s_q[m - m0] * NMOE_HIDDEN + r] = acc[nb2][mb][i];
+                    if (mb < nb && m < n) y[(size_t)s_q[m - m0] * NMOE_HIDDEN + r] = acc[b2][mb][i];
                 }
             }
         }
-        __syncthreads(); /* the stage ring and s_q are reused by the next chunk */
+        nmoe_lds_barrier(); /* the stages and s_q are reused by the next pass */
     }
 }
 
@@ -741,7 +827,7 @@ static int nmoe_grouped_run(nmoe_hip_ctx *ctx, const uint8_t *pack, const void *
     else
         hipLaunchKernelGGL((nmoe_grouped_xprep_kernel<BITS, float>), dim3(ntok), dim3(256), 0, s, (const float *)x,
                            ctx->g_xhi, ctx->g_xlo, ctx->g_xs);
-    const dim3 ggu(NMOE_EXPERTS, NMOE_INTER / NMOE_GU_ROWS), gdn(NMOE_EXPERTS, NMOE_HIDDEN / NMOE_DN_ROWS);
+    const dim3 ggu(NMOE_EXPERTS * (NMOE_INTER / nmoe_gu_rows(bf ? 1 : 2))), gdn(NMOE_EXPERTS * (NMOE_HIDDEN / NMOE_DN_ROWS));
     if (bf)
         hipLaunchKernelGGL((nmoe_grouped_gateup_kernel<BITS, 1>), ggu, dim3(512), 0, s, pack,
                            (const uint16_t *)ctx->g_xhi, (const uint16_t *)ctx->g_xlo, (const float *)ctx->g_xs,
