@@ -160,6 +160,67 @@ def cpu_baseline(bits: int, k: int, seed: int, nsteps: int, nlayers: int = 4) ->
 MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 (no sparsity)
 
 
+def bench_stack(args, nh):
+    """C3: the routed-expert stack of one decode token through 40 resident
+    layers, h_{l+1} = h_l + MoE_l(RMSNorm(h_l)) (unit weight, eps 1e-6), one
+    fused launch per layer (nmoe_moe_stack); a step is one token's 40 layers,
+    over 128 distinct synthetic tokens.  tokens/s = 1 / (time for 40 layers)."""
+    bits, k, NL = args.bits, args.k, 40
+    ntok = 128
+    sigma = 0.02 if bits == 4 else 0.05
+    ctx = nh.Context(0, max_tokens=8)
+    stream = ctx.stream
+    print(f"[bench] c3: {NL}-layer stack, q{bits} top-{k}, {ntok} tokens", file=sys.stderr, flush=True)
+    for layer in range(NL):
+        ctx.synth_layer(layer, bits, args.seed, sigma)
+    routers = ctx.alloc(NL * ROUTER_BYTES, "bench.routers")
+    for layer in range(NL):
+        ctx.synth_bf16(routers, 256 * 2048, args.seed, layer, 16, 0.02, offset=layer * ROUTER_BYTES)
+    H0 = ctx.alloc(ntok * 2048 * 2, "bench.h0")
+    ctx.synth_bf16(H0, ntok * 2048, args.seed, 99, 18, 1.0)
+    h0 = (H0.download(np.uint16, (ntok, 2048)).astype(np.uint32) << 16).view(np.float32)
+    HS = ctx.alloc(ntok * (NL + 1) * 2048 * 4, "bench.hseq")
+    row = (NL + 1) * 2048 * 4
+    for t in range(ntok):
+        HS.upload(h0[t], offset=t * row)
+    rts = [ctx.router_bf16(routers.ptr + layer * ROUTER_BYTES) for layer in range(NL)]
+    layers = list(range(NL))
+    ctx.sync()
+
+    def step(i):
+        return ctx.moe_stack(layers, rts, k, 1e-6, HS.ptr + (i % ntok) * row, stream=stream)
+
+    warm = min(args.warmup, 8)
+    for i in range(warm):
+        ctx._check(step(i))
+    ctx.sync()
+    steps = args.steps if args.steps != 400 else ntok
+    ev = HipEvents()
+    e0, e1 = ev.create(2)
+    ev.record(e0, stream)
+    for i in range(steps):
+        step(i)
+    ev.record(e1, stream)
+    ms = ev.ms(e0, e1) / steps
+    ctx.sync()
+    if ctx.device_status() != 0:
+        raise SystemExit(f"device status error: {ctx.last_error()}")
+    ev.destroy([e0, e1])
+    B = NL * step_bytes(bits, k)
+    result = {
+        "metric": f"routed-MoE stack tokens/s (c3: {NL} layers, q{bits}, top-{k}, batch 1, 1 GPU)",
+        "value": round(1e3 / ms, 1), "unit": "tokens/s", "n_gpus": 1, "steps": steps, "warmup": warm,
+        "ms_per_step": round(ms, 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32", "data": "synthetic",
+        "config": {"workload": "c3", "layers": NL, "tokens": ntok, "bits": bits, "k": k, "bytes_per_token": B,
+                   "entry_point": "nmoe_moe_stack (one nmoe_moe_layer_rmsnorm launch per layer)"},
+        "hbm_gbps": round(B / (ms * 1e-3) / 1e9, 1),
+        "us_per_layer": round(ms * 1e3 / NL, 2),
+    }
+    ctx.close()
+    print(json.dumps(result), flush=True)
+
+
 def bench_grouped(args, nh):
     """C4 (64 tokens, Zipf-skewed logits = ln p_e + Gumbel, p_e ~ rank^-1.1)
     or C5 (2048 tokens, uniform U(0,1) logits): a step is device top-k on
@@ -259,9 +320,10 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-calib", type=int, default=0, metavar="MIB",
                     help="only run 5 device-to-device copies of MIB MiB (counter calibration) and exit")
-    ap.add_argument("--workload", default="c1", choices=("c1", "c4", "c5"),
-                    help="c1: the headline single-layer decode step (default); c4: batched decode, 64 tokens, "
-                         "Zipf-skewed routing; c5: 2048-token prefill (grouped matrix-core path)")
+    ap.add_argument("--workload", default="c1", choices=("c1", "c3", "c4", "c5"),
+                    help="c1: the headline single-layer decode step (default); c3: 40-layer routed-expert stack of "
+                         "one decode token, 128 tokens; c4: batched decode, 64 tokens, Zipf-skewed routing; "
+                         "c5: 2048-token prefill (grouped matrix-core path)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -282,6 +344,8 @@ def main():
         ctx.close()
         return
 
+    if args.workload == "c3":
+        return bench_stack(args, nh)
     if args.workload != "c1":
         return bench_grouped(args, nh)
 
