@@ -184,6 +184,37 @@ NMOE_HIP_API int nmoe_moe_experts_q2(nmoe_hip_ctx *ctx, int layer, const void *x
 NMOE_HIP_API int nmoe_moe_dispatch(nmoe_hip_ctx *ctx, const uint32_t *idx, int ntok, int k, uint32_t *perm,
                                    uint32_t *offsets, void *stream);
 
+/* ---- the shared expert (metal/kernels.metal:421-469 and 510-513: rows 0-511
+ * and 768 of nmoe_route_shared_q4; :1520-1537: the shared down of
+ * nmoe_expert_down_combine_q4; tensors mlp.shared_expert.{gate,up,down}_proj
+ * and mlp.shared_expert_gate, src/runtime.m:2360-2369):
+ *   act[t]             = SiLU(Wg . x[t]) * (Wu . x[t])   Wg, Wu: q4 [512][2048]
+ *   shared_out[t]      = Wd . act[t]                     Wd: q4 [2048][512]
+ *   shared_gate_raw[t] = Ws . x[t]                       Ws: q4 [1][2048]
+ * A q4 tensor is the model's own quantised tensor, unchanged: w u32
+ * [rows][cols/8] (column 8w+v in nibble v), scales and biases bf16
+ * [rows][cols/64], weight = q*scale + bias.  The outputs are the
+ * shared_out / shared_gate_raw inputs of the expert and layer calls, whose
+ * combine adds sigmoid(shared_gate_raw) * shared_out (kernels.metal:1539-1541).
+ * x: [ntok][2048] fp32 or bf16; shared_out fp32 [ntok][2048];
+ * shared_gate_raw fp32 [ntok]. */
+typedef struct nmoe_hip_qtensor {
+    const uint32_t *w;
+    const uint16_t *scales;
+    const uint16_t *biases;
+} nmoe_hip_qtensor;
+
+typedef struct nmoe_hip_shared_expert {
+    nmoe_hip_qtensor gate;  /* [512][2048] */
+    nmoe_hip_qtensor up;    /* [512][2048] */
+    nmoe_hip_qtensor down;  /* [2048][512] */
+    nmoe_hip_qtensor score; /* [1][2048] */
+} nmoe_hip_shared_expert;
+
+NMOE_HIP_API int nmoe_moe_shared_expert(nmoe_hip_ctx *ctx, const nmoe_hip_shared_expert *se, const void *x,
+                                        int x_dtype, int ntok, float *shared_out, float *shared_gate_raw,
+                                        void *stream);
+
 /* ---- the whole per-layer MoE call (NMOEPipelinedExpertTail,
  * runtime.m:2908-2999, with routing on the device and no host round trip):
  * route x, run the selected experts of resident layer `layer`, combine into

@@ -57,6 +57,7 @@ extern "C" int nmoe_hip_create(int device, int max_tokens, nmoe_hip_ctx **out) {
         hipMalloc((void **)&ctx->logits, bytes_logits) != hipSuccess ||
         hipMalloc((void **)&ctx->idx, bytes_idx) != hipSuccess ||
         hipMalloc((void **)&ctx->w, bytes_idx) != hipSuccess ||
+        hipMalloc((void **)&ctx->s_act, mt * NMOE_INTER * sizeof(float)) != hipSuccess ||
         hipMalloc((void **)&ctx->sync, NMOE_SYNC_WORDS * sizeof(uint32_t)) != hipSuccess ||
         hipMemset(ctx->sync, 0, NMOE_SYNC_WORDS * sizeof(uint32_t)) != hipSuccess ||
         hipDeviceSynchronize() != hipSuccess) {
@@ -89,6 +90,7 @@ extern "C" void nmoe_hip_destroy(nmoe_hip_ctx *ctx) {
     hipFree(ctx->logits);
     hipFree(ctx->idx);
     hipFree(ctx->w);
+    hipFree(ctx->s_act);
     hipFree(ctx->sync);
     hipFree(ctx->xch);
     extern void nmoe_grouped_free(nmoe_hip_ctx *);

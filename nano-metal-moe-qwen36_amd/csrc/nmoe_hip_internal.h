@@ -94,6 +94,7 @@ struct nmoe_hip_ctx {
     uint16_t *g_ahi, *g_alo; /* [T*8][512] act (bf16 hi / lo), by permuted row */
     float *g_as;            /* [T*8][8] group sums of act */
     float *g_y;             /* [T*8][2048] per-entry expert outputs */
+    float *s_act;           /* [T][512] shared-expert activations */
     char err[256];
 };
 

@@ -70,6 +70,16 @@ class Router(C.Structure):
     ]
 
 
+class QTensor(C.Structure):
+    """nmoe_hip_qtensor: a q4 tensor as stored (w u32, scales/biases bf16)."""
+    _fields_ = [("w", C.c_void_p), ("scales", C.c_void_p), ("biases", C.c_void_p)]
+
+
+class SharedExpert(C.Structure):
+    """nmoe_hip_shared_expert: gate/up [512][2048], down [2048][512], score [1][2048]."""
+    _fields_ = [("gate", QTensor), ("up", QTensor), ("down", QTensor), ("score", QTensor)]
+
+
 _lib = None
 
 _P = C.c_void_p
@@ -104,6 +114,7 @@ _SIGS = {
     "nmoe_moe_layer_rmsnorm": (_I, [_P, _I, C.POINTER(Router), _P, C.c_float, _I, _P, _P, _P, _P, _P]),
     "nmoe_moe_stack": (_I, [_P, _I, C.POINTER(_I), C.POINTER(Router), _I, C.c_float, _P, _P, _P, _P]),
     "nmoe_moe_dispatch": (_I, [_P, _P, _I, _I, _P, _P, _P]),
+    "nmoe_moe_shared_expert": (_I, [_P, C.POINTER(SharedExpert), _P, _I, _I, _P, _P, _P]),
 }
 
 
@@ -300,6 +311,17 @@ class Context:
         la = (C.c_int * n)(*layers)
         ra = (Router * n)(*routers)
         return lib().nmoe_moe_stack(self.h, n, la, ra, k, eps, _ptr(h_seq), _ptr(idx_seq), _ptr(w_seq), stream)
+
+    @staticmethod
+    def shared_expert_desc(gate, up, down, score) -> SharedExpert:
+        """Each argument: (w, scales, biases) device buffers or pointers."""
+        q = lambda t: QTensor(_ptr(t[0]), _ptr(t[1]), _ptr(t[2]))
+        return SharedExpert(q(gate), q(up), q(down), q(score))
+
+    def shared_expert(self, se: SharedExpert, x, x_dtype: int, ntok: int, shared_out, shared_gate_raw,
+                      stream=None) -> int:
+        return lib().nmoe_moe_shared_expert(self.h, C.byref(se), _ptr(x), x_dtype, ntok, _ptr(shared_out),
+                                            _ptr(shared_gate_raw), stream)
 
     def dequant_rows(self, bits: int, packed, scales, biases, rows: int, in_dim: int, out, stream=None) -> int:
         return lib().nmoe_dequant_rows(self.h, bits, _ptr(packed), _ptr(scales), _ptr(biases), rows, in_dim,

@@ -48,6 +48,7 @@ _ORACLE_SIGS = {
     "orc_expert_offsets": (None, [_I, _P]),
     "orc_expert_gate_up": (None, [_P, _I, _P, _P]),
     "orc_expert_down": (None, [_P, _I, _P, _P]),
+    "orc_shared_expert": (None, [_P] * 15),
     "orc_combine": (None, [_P, _P, _P, _I, _P, _P, _P, _I]),
     "orc_moe_step_bf16router": (_I, [_P, _I, _P, _P, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P]),
     "orc_moe_experts": (_I, [_P, _I, _P, _I, _I, _P, _P, _P, _P, _P, _P, _P]),
@@ -178,6 +179,32 @@ def moe_experts(pack: np.ndarray, bits: int, x: np.ndarray, k: int, idx: np.ndar
                                   p(shared_out), p(shared_gate_raw), out.ctypes.data, p(act))
     assert rc == 0
     return (out, act) if want_act else out
+
+
+def syn_shared_expert(seed: int, sigma: float = 0.02):
+    """Synthetic q4 shared-expert tensors: gate/up [512][2048] and down
+    [2048][512] are carved out of a generated routed-expert pack (the same
+    shapes), score [1][2048] is row 0 of another pack's gate.  Returns
+    {name: (w u32, scales u16, biases u16)}."""
+    off = [0, 524288, 557056, 589824, 1114112, 1146880, 1179648, 1703936, 1736704, EXPERT_SIZE[4]]
+    pk = syn_expert(4, seed, 61, 7, sigma)
+    pk2 = syn_expert(4, seed, 61, 8, sigma)
+    t = lambda b, i: (b[off[i]:off[i + 1]].view(np.uint32), b[off[i + 1]:off[i + 2]].view(np.uint16),
+                      b[off[i + 2]:off[i + 3]].view(np.uint16))
+    g2 = t(pk2, 0)
+    return {"gate": t(pk, 0), "up": t(pk, 3), "down": t(pk, 6),
+            "score": (g2[0][:256].copy(), g2[1][:32].copy(), g2[2][:32].copy())}
+
+
+def shared_expert(se: dict, x: np.ndarray):
+    """orc_shared_expert per token: (shared_out [ntok][2048], shared_gate_raw [ntok])."""
+    x = np.ascontiguousarray(np.atleast_2d(x), np.float32)
+    out = np.zeros((x.shape[0], HIDDEN), np.float32)
+    g = np.zeros(x.shape[0], np.float32)
+    args = [p(np.ascontiguousarray(a)) for n in ("gate", "up", "down", "score") for a in se[n]]
+    for t in range(x.shape[0]):
+        oracle().orc_shared_expert(*args, x[t].ctypes.data, out[t].ctypes.data, g[t:].ctypes.data)
+    return out, g
 
 
 def dispatch(idx: np.ndarray, ntok: int, k: int, stride: int, num_experts: int = EXPERTS):

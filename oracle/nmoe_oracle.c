@@ -341,6 +341,21 @@ void orc_expert_down(const uint8_t *expert, int bits, const float *act512, float
                        (const uint16_t *)(expert + off[8]), act512, y2048, ORC_HIDDEN, ORC_INTER, bits);
 }
 
+/* The shared expert of one token: metal/kernels.metal:421-469 (rows 0-511:
+ * SiLU(gate.x) * (up.x)), 510-513 (row 768: the gate score) and 1520-1537
+ * (the shared down), each matvec in math.m:236-274 form (q4). */
+void orc_shared_expert(const uint32_t *gw, const uint16_t *gs, const uint16_t *gb, const uint32_t *uw,
+                       const uint16_t *us, const uint16_t *ub, const uint32_t *dw, const uint16_t *ds,
+                       const uint16_t *db, const uint32_t *sw, const uint16_t *ss, const uint16_t *sb, const float *x,
+                       float *shared_out, float *shared_gate_raw) {
+    float gate[ORC_INTER], up[ORC_INTER], act[ORC_INTER];
+    orc_dequant_matvec(gw, gs, gb, x, gate, ORC_INTER, ORC_HIDDEN, 4);
+    orc_dequant_matvec(uw, us, ub, x, up, ORC_INTER, ORC_HIDDEN, 4);
+    orc_swiglu(gate, up, act, ORC_INTER);
+    orc_dequant_matvec(dw, ds, db, act, shared_out, ORC_HIDDEN, ORC_INTER, 4);
+    orc_dequant_matvec(sw, ss, sb, x, shared_gate_raw, 1, ORC_HIDDEN, 4);
+}
+
 /* kernels.metal:1394-1423 (and the fused tail at 1539-1541). */
 void orc_combine(const float *h_mid, const float *y, const float *w, int k, const float *shared_out,
                  const float *shared_gate_raw, float *out, int hidden) {

@@ -94,6 +94,10 @@ void orc_expert_down(const uint8_t *expert, int bits, const float *act512, float
 /* Weighted combine, kernels.metal:1394-1423 / 1539-1541:
  * out = h_mid + sum_k w_k*y_k + sigmoid(g)*shared, moe summed in slot order.
  * shared_out / shared_gate_raw are nullable (then the term is absent). */
+void orc_shared_expert(const uint32_t *gw, const uint16_t *gs, const uint16_t *gb, const uint32_t *uw,
+                       const uint16_t *us, const uint16_t *ub, const uint32_t *dw, const uint16_t *ds,
+                       const uint16_t *db, const uint32_t *sw, const uint16_t *ss, const uint16_t *sb, const float *x,
+                       float *shared_out, float *shared_gate_raw);
 void orc_combine(const float *h_mid, const float *y, const float *w, int k, const float *shared_out,
                  const float *shared_gate_raw, float *out, int hidden);
 

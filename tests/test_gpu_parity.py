@@ -574,3 +574,48 @@ def test_prefill_2048_sampled(big, nh, bits):
     want = B.moe_experts(pack, bits, x[sample], k, idx[sample], w[sample], h[sample])
     assert big.device_status() == nh.OK
     assert_close(got, want, what=f"prefill q{bits}")
+
+
+@pytest.mark.parametrize("xdt,ntok", [("f32", 1), ("bf16", 1), ("f32", 5), ("bf16", 6)])
+def test_shared_expert_against_oracle(ctx, nh, xdt, ntok):
+    """nmoe_moe_shared_expert (kernels.metal:421-469, 510-513, 1520-1537)
+    against the oracle: shared_out and the gate score within tolerance."""
+    se = B.syn_shared_expert(11)
+    dev = {n: tuple(ctx.to_device(np.ascontiguousarray(a)) for a in se[n]) for n in se}
+    desc = nh.Context.shared_expert_desc(dev["gate"], dev["up"], dev["down"], dev["score"])
+    rng = np.random.default_rng(ntok)
+    x = rng.standard_normal((ntok, 2048)).astype(np.float32)
+    if xdt == "bf16":
+        xb = B.f32_to_bf16(x)
+        x, dx, dt = B.bf16_to_f32(xb), ctx.to_device(xb), nh.BF16
+    else:
+        dx, dt = ctx.to_device(x), nh.F32
+    so, gr = ctx.alloc(ntok * 8192), ctx.alloc(ntok * 4)
+    ctx._check(ctx.shared_expert(desc, dx, dt, ntok, so, gr))
+    want_so, want_g = B.shared_expert(se, x)
+    assert_close(so.download(np.float32, (ntok, 2048)), want_so, what="shared_out")
+    assert_close(gr.download(np.float32, ntok), want_g, what="shared_gate_raw")
+
+
+def test_shared_expert_then_layer(ctx, nh):
+    """The reference's whole layer tail: the shared expert's outputs feed the
+    routed combine, out = h_mid + sum_s w_s y_s + sigmoid(g) * shared_out."""
+    seed, bits, k, layer, ntok = 23, 4, 8, 44, 2
+    ctx.synth_layer(layer, bits, seed, SIGMA[bits])
+    se = B.syn_shared_expert(12)
+    dev = {n: tuple(ctx.to_device(np.ascontiguousarray(a)) for a in se[n]) for n in se}
+    desc = nh.Context.shared_expert_desc(dev["gate"], dev["up"], dev["down"], dev["score"])
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((ntok, 2048)).astype(np.float32)
+    h = rng.standard_normal((ntok, 2048)).astype(np.float32)
+    idx = np.array([[3, 9, 27, 81, 100, 200, 250, 7], [5, 6, 7, 8, 9, 10, 11, 12]], np.uint32)
+    w = np.full((ntok, 8), 0.125, np.float32)
+    dx, dh = ctx.to_device(x), ctx.to_device(h)
+    so, gr, out = ctx.alloc(ntok * 8192), ctx.alloc(ntok * 4), ctx.alloc(ntok * 8192)
+    ctx._check(ctx.shared_expert(desc, dx, nh.F32, ntok, so, gr))
+    ctx._check(ctx.experts(bits, layer, dx, nh.F32, ntok, k, ctx.to_device(idx), ctx.to_device(w), dh, out,
+                           shared_out=so, shared_gate_raw=gr))
+    want_so, want_g = B.shared_expert(se, x)
+    pack = host_pack(bits, seed, layer, idx.ravel())
+    want = B.moe_experts(pack, bits, x, k, idx, w, h, shared_out=want_so, shared_gate_raw=want_g)
+    assert_close(out.download(np.float32, (ntok, 2048)), want, what="layer with the shared expert")

@@ -145,6 +145,35 @@ def test_expert_and_combine_against_float64():
         np.testing.assert_allclose(y, D @ act.astype(np.float64), rtol=1e-4, atol=1e-4)
 
 
+def test_shared_expert_against_float64_and_one_hot():
+    """The shared expert (gate/up -> SwiGLU -> down, plus the score row)
+    against float64 dense algebra on the dequantised tensors, and the score
+    row with one-hot x equal to that row's dequantised column exactly."""
+    se = B.syn_shared_expert(5)
+
+    def dense(t, rows, cols):
+        w, s, b = t
+        q = ((w.reshape(rows, cols // 8)[:, :, None] >> (np.arange(8, dtype=np.uint32) * 4)) & 15).reshape(rows, cols)
+        return q * np.repeat(B.bf16_to_f32(s.reshape(rows, cols // 64)), 64, 1).astype(np.float64) + \
+            np.repeat(B.bf16_to_f32(b.reshape(rows, cols // 64)), 64, 1)
+
+    G, U, D, S = dense(se["gate"], 512, 2048), dense(se["up"], 512, 2048), dense(se["down"], 2048, 512), \
+        dense(se["score"], 1, 2048)
+    rng = np.random.default_rng(6)
+    x = rng.standard_normal((2, 2048)).astype(np.float32)
+    out, g = B.shared_expert(se, x)
+    for t in range(2):
+        gg, uu = G @ x[t], U @ x[t]
+        act = gg / (1 + np.exp(-gg)) * uu
+        np.testing.assert_allclose(out[t], D @ act, rtol=1e-4, atol=2e-4)
+        np.testing.assert_allclose(g[t], (S @ x[t])[0], rtol=1e-4, atol=1e-4)
+    for j in (0, 777, 2047):
+        e = np.zeros(2048, np.float32)
+        e[j] = 1.0
+        _, gj = B.shared_expert(se, e)
+        assert gj[0] == np.float32(S[0, j])
+
+
 def test_combine_formula():
     rng = np.random.default_rng(6)
     h = rng.standard_normal(2048).astype(np.float32)
