@@ -122,6 +122,23 @@ NMOE_HIP_API int nmoe_hip_copy_to_host(nmoe_hip_ctx *ctx, void *host, const void
 NMOE_HIP_API size_t nmoe_hip_expert_size(int bits);
 NMOE_HIP_API int nmoe_hip_upload_layer_pack(nmoe_hip_ctx *ctx, int layer, int bits, const void *host, size_t size);
 NMOE_HIP_API int nmoe_hip_load_layer_file(nmoe_hip_ctx *ctx, int layer, int bits, const char *path);
+
+/* Validates an expert directory's layout.json against the fixed pack layout.
+ * Accepts the converter's schema {expert_size, num_layers, num_experts,
+ * components[{name, offset, size}]} (scripts/convert_qwen36.py:341-360) and
+ * the richer one src/expert_io.m:230-320 reads (bits/quant, per-component
+ * dtype/shape/logical_shape).  bits comes from bits/quant, else from
+ * expert_size; num_layers is 0 when absent.  No context needed; err
+ * (nullable) receives the reason.  EINVAL on a mismatch, ENOENT when the file
+ * cannot be opened. */
+NMOE_HIP_API int nmoe_hip_validate_layout(const char *layout_json_path, int *bits, int *num_layers, char *err,
+                                          size_t err_len);
+/* Validates dir/layout.json, then makes dir/layer_00.bin .. layer_{n-1}.bin
+ * resident as layers 0..n-1 (each with nmoe_hip_load_layer_file's size
+ * check); n = nlayers if > 0, else num_layers of the file.  bits_out and
+ * layers_out (nullable) receive the quantisation and the layers loaded. */
+NMOE_HIP_API int nmoe_hip_load_expert_dir(nmoe_hip_ctx *ctx, const char *dir, int nlayers, int *bits_out,
+                                          int *layers_out);
 /* Device address of a resident layer pack (NULL if absent). */
 NMOE_HIP_API const void *nmoe_hip_layer_pack(const nmoe_hip_ctx *ctx, int layer, int *bits_out);
 /* Allocates layer `layer` and fills it with the repository's synthetic

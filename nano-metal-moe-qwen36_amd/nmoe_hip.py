@@ -115,6 +115,8 @@ _SIGS = {
     "nmoe_moe_stack": (_I, [_P, _I, C.POINTER(_I), C.POINTER(Router), _I, C.c_float, _P, _P, _P, _P]),
     "nmoe_moe_dispatch": (_I, [_P, _P, _I, _I, _P, _P, _P]),
     "nmoe_moe_shared_expert": (_I, [_P, C.POINTER(SharedExpert), _P, _I, _I, _P, _P, _P]),
+    "nmoe_hip_validate_layout": (_I, [C.c_char_p, C.POINTER(_I), C.POINTER(_I), C.c_char_p, C.c_size_t]),
+    "nmoe_hip_load_expert_dir": (_I, [_P, C.c_char_p, _I, C.POINTER(_I), C.POINTER(_I)]),
 }
 
 
@@ -312,6 +314,12 @@ class Context:
         ra = (Router * n)(*routers)
         return lib().nmoe_moe_stack(self.h, n, la, ra, k, eps, _ptr(h_seq), _ptr(idx_seq), _ptr(w_seq), stream)
 
+    def load_expert_dir(self, path: str, nlayers: int = 0):
+        """Validates path/layout.json and makes its layer files resident; returns (bits, layers)."""
+        b, n = C.c_int(0), C.c_int(0)
+        self._check(lib().nmoe_hip_load_expert_dir(self.h, path.encode(), nlayers, C.byref(b), C.byref(n)))
+        return b.value, n.value
+
     @staticmethod
     def shared_expert_desc(gate, up, down, score) -> SharedExpert:
         """Each argument: (w, scales, biases) device buffers or pointers."""
@@ -326,3 +334,11 @@ class Context:
     def dequant_rows(self, bits: int, packed, scales, biases, rows: int, in_dim: int, out, stream=None) -> int:
         return lib().nmoe_dequant_rows(self.h, bits, _ptr(packed), _ptr(scales), _ptr(biases), rows, in_dim,
                                        _ptr(out), stream)
+
+
+def validate_layout(path: str):
+    """nmoe_hip_validate_layout: (status, bits, num_layers, message)."""
+    b, n = C.c_int(0), C.c_int(0)
+    err = C.create_string_buffer(256)
+    rc = lib().nmoe_hip_validate_layout(path.encode(), C.byref(b), C.byref(n), err, 256)
+    return rc, b.value, n.value, err.value.decode()

@@ -619,3 +619,29 @@ def test_shared_expert_then_layer(ctx, nh):
     pack = host_pack(bits, seed, layer, idx.ravel())
     want = B.moe_experts(pack, bits, x, k, idx, w, h, shared_out=want_so, shared_gate_raw=want_g)
     assert_close(out.download(np.float32, (ntok, 2048)), want, what="layer with the shared expert")
+
+
+def test_load_expert_dir(nh, tmp_path):
+    """nmoe_hip_load_expert_dir: layout.json validated (the converter's
+    schema), layer_00.bin made resident byte for byte; a truncated layer file
+    is refused with the reference's size check (runtime.m:2444-2451)."""
+    import shutil
+    import os
+    d = tmp_path / "packed_experts_2bit"
+    d.mkdir()
+    shutil.copy(os.path.join(os.path.dirname(__file__), "golden", "layout_q2.json"), d / "layout.json")
+    pack = B.syn_layer(2, 31, 0, SIGMA[2])
+    pack.tofile(d / "layer_00.bin")
+    c = nh.Context(0, max_tokens=1)
+    try:
+        assert c.load_expert_dir(str(d), nlayers=1) == (2, 1)
+        for e in (0, 129, 255):
+            np.testing.assert_array_equal(c.download_expert(0, e, 2), B.syn_expert(2, 31, 0, e, SIGMA[2]))
+        with open(d / "layer_00.bin", "r+b") as f:
+            f.truncate(pack.nbytes - 1)
+        with pytest.raises(nh.NmoeError):
+            c.load_expert_dir(str(d), nlayers=1)
+        with pytest.raises(nh.NmoeError):  # layout.json says 40 layers; only layer_00.bin exists
+            c.load_expert_dir(str(d))
+    finally:
+        c.close()
