@@ -50,11 +50,12 @@ for _p in (ROOT, PKG):
 HBM_PEAK_GBS = 8000.0
 EXPERT_BYTES = {4: 1769472, 2: 983040}
 ROUTER_BYTES = 256 * 2048 * 2
+ROUTER_Q4_BYTES = 256 * 256 * 4 + 2 * 256 * 32 * 2  # the model's q4 router: codes + scales + biases
 ACT_BYTES = 4096 + 8192 + 8192 + 64
 
 
-def step_bytes(bits: int, k: int) -> int:
-    return k * EXPERT_BYTES[bits] + ROUTER_BYTES + ACT_BYTES
+def step_bytes(bits: int, k: int, router: str = "bf16") -> int:
+    return k * EXPERT_BYTES[bits] + (ROUTER_BYTES if router == "bf16" else ROUTER_Q4_BYTES) + ACT_BYTES
 
 
 class HipEvents:
@@ -160,6 +161,31 @@ def cpu_baseline(bits: int, k: int, seed: int, nsteps: int, nlayers: int = 4) ->
 MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 (no sparsity)
 
 
+def synth_routers(ctx, buf, NL: int, args) -> list:
+    """One synthetic router per layer in `buf` (NL * ROUTER_BYTES): dense bf16
+    N(0, 0.02) [256][2048], or the model's q4 form (codes uniform 0..15,
+    scale bf16(N(0, 0.002)), bias bf16(-8 scale), all from the repository's
+    seeded generators) packed into the same slot."""
+    rts = []
+    for layer in range(NL):
+        base = buf.ptr + layer * ROUTER_BYTES
+        if args.router == "bf16":
+            ctx.synth_bf16(buf, 256 * 2048, args.seed, layer, 16, 0.02, offset=layer * ROUTER_BYTES)
+            rts.append(ctx.router_bf16(base))
+        else:
+            rng = np.random.default_rng(args.seed * 1000 + layer)
+            wq = rng.integers(0, 2**32, size=256 * 256, dtype=np.uint64).astype(np.uint32)
+            sc = (rng.standard_normal(256 * 32) * 0.002).astype(np.float32)
+            s16 = ((sc.view(np.uint32).astype(np.uint64) + 0x7FFF + ((sc.view(np.uint32) >> 16) & 1)) >> 16).astype(np.uint16)
+            bi = (-8.0 * (s16.astype(np.uint32) << 16).view(np.float32)).astype(np.float32)
+            b16 = ((bi.view(np.uint32).astype(np.uint64) + 0x7FFF + ((bi.view(np.uint32) >> 16) & 1)) >> 16).astype(np.uint16)
+            buf.upload(wq, offset=layer * ROUTER_BYTES)
+            buf.upload(s16, offset=layer * ROUTER_BYTES + wq.nbytes)
+            buf.upload(b16, offset=layer * ROUTER_BYTES + wq.nbytes + s16.nbytes)
+            rts.append(ctx.router_q4(base, base + wq.nbytes, base + wq.nbytes + s16.nbytes))
+    return rts
+
+
 def bench_stack(args, nh):
     """C3: the routed-expert stack of one decode token through 40 resident
     layers, h_{l+1} = h_l + MoE_l(RMSNorm(h_l)) (unit weight, eps 1e-6), one
@@ -174,8 +200,7 @@ def bench_stack(args, nh):
     for layer in range(NL):
         ctx.synth_layer(layer, bits, args.seed, sigma)
     routers = ctx.alloc(NL * ROUTER_BYTES, "bench.routers")
-    for layer in range(NL):
-        ctx.synth_bf16(routers, 256 * 2048, args.seed, layer, 16, 0.02, offset=layer * ROUTER_BYTES)
+    rts = synth_routers(ctx, routers, NL, args)
     H0 = ctx.alloc(ntok * 2048 * 2, "bench.h0")
     ctx.synth_bf16(H0, ntok * 2048, args.seed, 99, 18, 1.0)
     h0 = (H0.download(np.uint16, (ntok, 2048)).astype(np.uint32) << 16).view(np.float32)
@@ -183,7 +208,6 @@ def bench_stack(args, nh):
     row = (NL + 1) * 2048 * 4
     for t in range(ntok):
         HS.upload(h0[t], offset=t * row)
-    rts = [ctx.router_bf16(routers.ptr + layer * ROUTER_BYTES) for layer in range(NL)]
     layers = list(range(NL))
     ctx.sync()
 
@@ -206,13 +230,14 @@ def bench_stack(args, nh):
     if ctx.device_status() != 0:
         raise SystemExit(f"device status error: {ctx.last_error()}")
     ev.destroy([e0, e1])
-    B = NL * step_bytes(bits, k)
+    B = NL * step_bytes(bits, k, args.router)
     result = {
         "metric": f"routed-MoE stack tokens/s (c3: {NL} layers, q{bits}, top-{k}, batch 1, 1 GPU)",
         "value": round(1e3 / ms, 1), "unit": "tokens/s", "n_gpus": 1, "steps": steps, "warmup": warm,
         "ms_per_step": round(ms, 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "f32", "data": "synthetic",
         "config": {"workload": "c3", "layers": NL, "tokens": ntok, "bits": bits, "k": k, "bytes_per_token": B,
+                   "router": args.router,
                    "entry_point": "nmoe_moe_stack (one nmoe_moe_layer_rmsnorm launch per layer)"},
         "hbm_gbps": round(B / (ms * 1e-3) / 1e9, 1),
         "us_per_layer": round(ms * 1e3 / NL, 2),
@@ -320,6 +345,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-calib", type=int, default=0, metavar="MIB",
                     help="only run 5 device-to-device copies of MIB MiB (counter calibration) and exit")
+    ap.add_argument("--router", default="bf16", choices=("bf16", "q4"),
+                    help="c1/c3: the benchmark configs' dense bf16 router (default) or the model's q4 router")
     ap.add_argument("--workload", default="c1", choices=("c1", "c3", "c4", "c5"),
                     help="c1: the headline single-layer decode step (default); c3: 40-layer routed-expert stack of "
                          "one decode token, 128 tokens; c4: batched decode, 64 tokens, Zipf-skewed routing; "
@@ -357,10 +384,10 @@ def main():
     for layer in range(NL):
         ctx.synth_layer(layer, bits, args.seed, sigma)
     routers = ctx.alloc(NL * ROUTER_BYTES, "bench.routers")
+    rts = synth_routers(ctx, routers, NL, args)
     X = ctx.alloc(NL * 2048 * 2, "bench.x")
     Hb = ctx.alloc(NL * 2048 * 2, "bench.hb")
     for layer in range(NL):
-        ctx.synth_bf16(routers, 256 * 2048, args.seed, layer, 16, 0.02, offset=layer * ROUTER_BYTES)
         ctx.synth_bf16(X, 2048, args.seed, layer, 17, 1.0, offset=layer * 4096)
         ctx.synth_bf16(Hb, 2048, args.seed, layer, 18, 1.0, offset=layer * 4096)
     hb = Hb.download(np.uint16, (NL, 2048))
@@ -368,7 +395,6 @@ def main():
     OUT = ctx.alloc(NL * 2048 * 4, "bench.out")
     IDX = ctx.alloc(NL * 32, "bench.idx")
     WT = ctx.alloc(NL * 32, "bench.w")
-    rts = [ctx.router_bf16(routers.ptr + layer * ROUTER_BYTES) for layer in range(NL)]
     ctx.sync()
 
     def step(i):
@@ -396,7 +422,7 @@ def main():
     ev.destroy([e0, e1])
     kern_ms = ms_per_step  # one launch per step
 
-    B = step_bytes(bits, k)
+    B = step_bytes(bits, k, args.router)
     tps = 1e3 / ms_per_step
     achieved = B / (kern_ms * 1e-3) / 1e9
     result = {
@@ -414,9 +440,9 @@ def main():
         "data": "synthetic",
         "hbm_gbps": round(B / (ms_per_step * 1e-3) / 1e9, 1),
         "config": {
-            "workload": f"single-layer q{bits} top-{k} batch-1 routed-MoE decode step (bf16 router, hidden 2048, "
+            "workload": f"single-layer q{bits} top-{k} batch-1 routed-MoE decode step ({args.router} router, hidden 2048, "
                         f"256 experts, FFN 512), rotating over {NL} HBM-resident layers",
-            "bits": bits, "k": k, "batch": 1, "layers_rotated": NL, "bytes_per_step": B,
+            "bits": bits, "k": k, "batch": 1, "layers_rotated": NL, "bytes_per_step": B, "router": args.router,
             "entry_point": "nmoe_moe_layer",
         },
         "roofline": {
@@ -425,7 +451,7 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": profiled_traffic(bits, k),
+            "traffic": profiled_traffic(bits, k) if args.router == "bf16" else None,
             "kernel": f"nmoe_fused_decode_kernel<{bits},true,bf16> (one launch per step)",
             "kernel_ms": round(kern_ms, 5),
         },

@@ -244,7 +244,7 @@ NMOE_HIP_API int nmoe_moe_layer(nmoe_hip_ctx *ctx, int layer, const nmoe_hip_rou
  * (math.m:34-65, unit weight, bit-exact), the way the reference runs the next
  * layer's input norm right after the combine (runtime.m:2893-2900):
  *   h_out = h_in + MoE(RMSNorm(h_in)).
- * One token, bf16 router; h_out must not alias h_in. */
+ * One token, bf16 or q4 router; h_out must not alias h_in. */
 NMOE_HIP_API int nmoe_moe_layer_rmsnorm(nmoe_hip_ctx *ctx, int layer, const nmoe_hip_router *router,
                                         const float *h_in, float eps, int k, float *h_out, uint32_t *idx, float *w,
                                         float *logits, void *stream);
@@ -252,7 +252,7 @@ NMOE_HIP_API int nmoe_moe_layer_rmsnorm(nmoe_hip_ctx *ctx, int layer, const nmoe
 /* ---- the routed-expert stack of one decode token (the layer loop of
  * NMOEProcessToken, runtime.m:3732-3777, restricted to the MoE tails):
  * h_seq[l+1] = h_seq[l] + MoE_l(RMSNorm(h_seq[l])) for l < nlayers.
- * layers[l]: resident pack of layer l; routers[l]: its bf16 router.
+ * layers[l]: resident pack of layer l; routers[l]: its router (bf16 or q4).
  * h_seq: fp32 [nlayers+1][2048] (row 0 = input); idx_seq / w_seq: nullable
  * [nlayers][8]. */
 NMOE_HIP_API int nmoe_moe_stack(nmoe_hip_ctx *ctx, int nlayers, const int *layers, const nmoe_hip_router *routers,

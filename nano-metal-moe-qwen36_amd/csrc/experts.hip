@@ -231,7 +231,7 @@ static int nmoe_launch_experts(nmoe_hip_ctx *ctx, const uint8_t *pack, const voi
 }
 
 extern "C" int nmoe_fused_decode(nmoe_hip_ctx *ctx, int bits, int route, const void *x, int xmode, float eps, int k,
-                                 const uint16_t *router_w, const uint32_t *idx_in, const float *w_in,
+                                 const nmoe_hip_router *router, const uint32_t *idx_in, const float *w_in,
                                  const float *h_mid, const float *shared_out, const float *shared_gate_raw, float *out,
                                  uint32_t *idx_out, float *w_out, float *logits_out, const uint8_t *pack,
                                  hipStream_t s);
@@ -288,8 +288,8 @@ extern "C" int nmoe_moe_layer(nmoe_hip_ctx *ctx, int layer, const nmoe_hip_route
     if (h_mid == NULL || out == NULL) return nmoe_fail(ctx, NMOE_HIP_EINVAL, "NULL h_mid/out");
     if ((shared_out == NULL) != (shared_gate_raw == NULL))
         return nmoe_fail(ctx, NMOE_HIP_EINVAL, "shared_out and shared_gate_raw must both be set or both NULL");
-    if (ntok == 1 && ctx->fused_blocks > 0 && ctx->use_fused && router->kind == NMOE_HIP_ROUTER_BF16)
-        return nmoe_fused_decode(ctx, ctx->packs[layer].bits, 1, x, x_dtype, 0.0f, k, router->w_bf16, NULL, NULL,
+    if (ntok == 1 && ctx->fused_blocks > 0 && ctx->use_fused)
+        return nmoe_fused_decode(ctx, ctx->packs[layer].bits, 1, x, x_dtype, 0.0f, k, router, NULL, NULL,
                                  h_mid, shared_out, shared_gate_raw, out, idx, w, logits,
                                  (const uint8_t *)ctx->packs[layer].dev, nmoe_stream_of(ctx, stream));
     uint32_t *ri = idx != NULL ? idx : ctx->idx;
@@ -311,15 +311,15 @@ extern "C" int nmoe_moe_layer_rmsnorm(nmoe_hip_ctx *ctx, int layer, const nmoe_h
         return nmoe_fail(ctx, NMOE_HIP_ENOENT, "layer %d has no resident pack", layer);
     int rc = nmoe_check_router(ctx, router);
     if (rc != NMOE_HIP_OK) return rc;
-    if (router->kind != NMOE_HIP_ROUTER_BF16 || router->num_experts != NMOE_EXPERTS)
-        return nmoe_fail(ctx, NMOE_HIP_EINVAL, "nmoe_moe_layer_rmsnorm needs a bf16 router of 256 experts");
+    if (router->num_experts != NMOE_EXPERTS)
+        return nmoe_fail(ctx, NMOE_HIP_EINVAL, "nmoe_moe_layer_rmsnorm needs a router of 256 experts");
     if (k < 1 || k > NMOE_MAX_K) return nmoe_fail(ctx, NMOE_HIP_EINVAL, "k=%d outside 1..8", k);
     if (h_in == NULL || h_out == NULL || !nmoe_aligned(h_in, 16) || !nmoe_aligned(h_out, 4))
         return nmoe_fail(ctx, NMOE_HIP_EINVAL, "h_in (16-byte aligned) and h_out are required");
     if (h_in == h_out) return nmoe_fail(ctx, NMOE_HIP_EINVAL, "h_out must not alias h_in");
     if (ctx->fused_blocks == 0)
         return nmoe_fail(ctx, NMOE_HIP_EINVAL, "the device cannot hold the 256-block fused grid");
-    return nmoe_fused_decode(ctx, ctx->packs[layer].bits, 1, h_in, 2 /* XNORM */, eps, k, router->w_bf16, NULL, NULL,
+    return nmoe_fused_decode(ctx, ctx->packs[layer].bits, 1, h_in, 2 /* XNORM */, eps, k, router, NULL, NULL,
                              h_in, NULL, NULL, h_out, idx, w, logits, (const uint8_t *)ctx->packs[layer].dev,
                              nmoe_stream_of(ctx, stream));
 }

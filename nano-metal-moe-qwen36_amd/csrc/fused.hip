@@ -76,9 +76,17 @@ static __constant__ uint64_t nmoe_fused_exp2_tab[32] = NMOE_EXP2_TAB32;
 #define NMOE_XBF16 1
 #define NMOE_XNORM 2
 
+/* ROUTE: routing given (idx_in / w_in), or computed from a bf16 or a q4 router */
+#define NMOE_ROUTE_GIVEN 0
+#define NMOE_ROUTE_BF16 1
+#define NMOE_ROUTE_Q4 2
+
 struct nmoe_fused_args {
     const uint8_t *pack;
-    const uint16_t *router_w; /* bf16 [256][2048] (routing) */
+    const uint16_t *router_w; /* bf16 [256][2048] (routing), or NULL with router_q4 */
+    const uint32_t *router_q4; /* q4 [256][256] words, scales/biases bf16 [256][32] (routing) */
+    const uint16_t *router_s;
+    const uint16_t *router_b;
     const void *x;            /* [2048]: fp32 x, bf16 x, or fp32 h (XNORM) */
     float eps;                /* XNORM */
     int k;
@@ -186,7 +194,7 @@ __device__ __forceinline__ int nmoe_act_slot(int e) {
     return 4 * (dl * N + ((c + dl + (dl >> 3)) & (N - 1))) + (e & 3);
 }
 
-template <int BITS, bool ROUTE, int XMODE>
+template <int BITS, int ROUTE, int XMODE>
 __global__ void __launch_bounds__(NMOE_FUSED_THREADS) nmoe_fused_decode_kernel(nmoe_fused_args a) {
     using Q = nmoe_q<BITS>;
     using L = nmoe_layout<BITS>;
@@ -229,12 +237,27 @@ __global__ void __launch_bounds__(NMOE_FUSED_THREADS) nmoe_fused_decode_kernel(n
     const float hm = a.h_mid[crow];
     const float sh = a.shared_out != NULL ? a.shared_out[crow] : 0.0f;
     uint4 wv[4];
+    uint32_t wq[4];
+    uint16_t rsr[4], rbr[4];
     float xs_r[32], lv[4];
     uint32_t cand[NMOE_MAX_K];
     if (ROUTE && ctrl) {
-        const uint4 *row = (const uint4 *)(a.router_w + (size_t)blockIdx.x * NMOE_HIDDEN);
+        if (ROUTE == NMOE_ROUTE_Q4) {
+            /* q4 router row: words lane + 64q (columns 8 word .. +7) and their
+             * groups' scale and bias, kept raw until the dot product */
+            const uint32_t *rowq = a.router_q4 + (size_t)blockIdx.x * (NMOE_HIDDEN / 8);
+            const size_t g0 = (size_t)blockIdx.x * (NMOE_HIDDEN / NMOE_GROUP);
 #pragma unroll
-        for (int q = 0; q < 4; q++) wv[q] = row[lane + 64 * q];
+            for (int q = 0; q < 4; q++) {
+                wq[q] = rowq[lane + 64 * q];
+                rsr[q] = a.router_s[g0 + (lane + 64 * q) / 8];
+                rbr[q] = a.router_b[g0 + (lane + 64 * q) / 8];
+            }
+        } else {
+            const uint4 *row = (const uint4 *)(a.router_w + (size_t)blockIdx.x * NMOE_HIDDEN);
+#pragma unroll
+            for (int q = 0; q < 4; q++) wv[q] = row[lane + 64 * q];
+        }
         if (XMODE != NMOE_XNORM)
 #pragma unroll
             for (int q = 0; q < 4; q++) nmoe_x_cols<XMODE>(a.x, (lane + 64 * q) * 8, 8, 1.0, xs_r + 8 * q);
@@ -259,7 +282,8 @@ __global__ void __launch_bounds__(NMOE_FUSED_THREADS) nmoe_fused_decode_kernel(n
         if (XMODE == NMOE_XNORM)
 #pragma unroll
             for (int q = 0; q < 4; q++) nmoe_x_cols<XMODE>(a.x, (lane + 64 * q) * 8, 8, rinv, xs_r + 8 * q);
-        float logit = nmoe_router_row_bf16(wv, xs_r);
+        const float logit =
+            ROUTE == NMOE_ROUTE_Q4 ? nmoe_router_row_q4(wq, rsr, rbr, xs_r) : nmoe_router_row_bf16(wv, xs_r);
         if (lane == 0) nmoe_st_tagged(xlg + NMOE_XCH_SP * blockIdx.x, epoch, logit);
         if (g < k) {
             /* ---- T: wait for all 256 logits; the candidates are the k
@@ -531,13 +555,13 @@ __global__ void __launch_bounds__(NMOE_FUSED_THREADS) nmoe_fused_decode_kernel(n
 
 /* ----------------------------------------------------------- launching */
 
-template <int BITS, bool ROUTE, int XMODE>
+template <int BITS, int ROUTE, int XMODE>
 static hipError_t nmoe_fused_launch(const nmoe_fused_args &args, hipStream_t s) {
     hipLaunchKernelGGL((nmoe_fused_decode_kernel<BITS, ROUTE, XMODE>), dim3(NMOE_FUSED_BLOCKS), dim3(NMOE_FUSED_THREADS), 0, s, args);
     return hipGetLastError();
 }
 
-template <int BITS, bool ROUTE, int XMODE>
+template <int BITS, int ROUTE, int XMODE>
 static int nmoe_fused_fits(int num_cus) {
     int per_cu = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, nmoe_fused_decode_kernel<BITS, ROUTE, XMODE>, NMOE_FUSED_THREADS, 0) !=
@@ -581,11 +605,17 @@ static int nmoe_check_xcd_placement(int *placed) {
  * wait on each other); decided here from the occupancy of every variant. */
 extern "C" int nmoe_decode_init(nmoe_hip_ctx *ctx) {
     int n = ctx->num_cus;
-    int ok = nmoe_fused_fits<4, true, NMOE_XBF16>(n) && nmoe_fused_fits<4, true, NMOE_XF32>(n) &&
-             nmoe_fused_fits<4, true, NMOE_XNORM>(n) && nmoe_fused_fits<2, true, NMOE_XBF16>(n) &&
-             nmoe_fused_fits<2, true, NMOE_XF32>(n) && nmoe_fused_fits<2, true, NMOE_XNORM>(n) &&
-             nmoe_fused_fits<4, false, NMOE_XBF16>(n) && nmoe_fused_fits<4, false, NMOE_XF32>(n) &&
-             nmoe_fused_fits<2, false, NMOE_XBF16>(n) && nmoe_fused_fits<2, false, NMOE_XF32>(n);
+    int ok = 1;
+#define NMOE_FITS_ALL(B, R) \
+    ok = ok && nmoe_fused_fits<B, R, NMOE_XBF16>(n) && nmoe_fused_fits<B, R, NMOE_XF32>(n) && \
+         (R == NMOE_ROUTE_GIVEN || nmoe_fused_fits<B, R, NMOE_XNORM>(n))
+    NMOE_FITS_ALL(4, NMOE_ROUTE_BF16);
+    NMOE_FITS_ALL(4, NMOE_ROUTE_Q4);
+    NMOE_FITS_ALL(4, NMOE_ROUTE_GIVEN);
+    NMOE_FITS_ALL(2, NMOE_ROUTE_BF16);
+    NMOE_FITS_ALL(2, NMOE_ROUTE_Q4);
+    NMOE_FITS_ALL(2, NMOE_ROUTE_GIVEN);
+#undef NMOE_FITS_ALL
     ctx->fused_blocks = ok ? NMOE_FUSED_BLOCKS : 0;
     ctx->xcd_placed = 0;
     if (ok) {
@@ -599,16 +629,28 @@ extern "C" int nmoe_decode_init(nmoe_hip_ctx *ctx) {
     return NMOE_HIP_OK;
 }
 
-/* One token.  route != 0: routing computed from router_w; else given by
+template <int BITS, int ROUTE>
+static hipError_t nmoe_fused_launch_x(int xmode, const nmoe_fused_args &a, hipStream_t s) {
+    if (xmode == NMOE_XBF16) return nmoe_fused_launch<BITS, ROUTE, NMOE_XBF16>(a, s);
+    if (xmode == NMOE_XF32) return nmoe_fused_launch<BITS, ROUTE, NMOE_XF32>(a, s);
+    if constexpr (ROUTE != NMOE_ROUTE_GIVEN) return nmoe_fused_launch<BITS, ROUTE, NMOE_XNORM>(a, s);
+    return hipErrorInvalidValue;
+}
+
+/* One token.  route != 0: routing computed from `router` (bf16 or q4); else given by
  * idx_in / w_in.  xmode: NMOE_XF32 / NMOE_XBF16 / NMOE_XNORM. */
 extern "C" int nmoe_fused_decode(nmoe_hip_ctx *ctx, int bits, int route, const void *x, int xmode, float eps, int k,
-                                 const uint16_t *router_w, const uint32_t *idx_in, const float *w_in,
+                                 const nmoe_hip_router *router, const uint32_t *idx_in, const float *w_in,
                                  const float *h_mid, const float *shared_out, const float *shared_gate_raw, float *out,
                                  uint32_t *idx_out, float *w_out, float *logits_out, const uint8_t *pack,
                                  hipStream_t s) {
     nmoe_fused_args a;
     a.pack = pack;
-    a.router_w = router_w;
+    const bool q4r = router != NULL && router->kind == NMOE_HIP_ROUTER_Q4;
+    a.router_w = router != NULL && !q4r ? router->w_bf16 : NULL;
+    a.router_q4 = q4r ? router->w_q4 : NULL;
+    a.router_s = q4r ? router->scales : NULL;
+    a.router_b = q4r ? router->biases : NULL;
     a.x = x;
     a.eps = eps;
     a.k = k;
@@ -625,25 +667,15 @@ extern "C" int nmoe_fused_decode(nmoe_hip_ctx *ctx, int bits, int route, const v
     a.sync = ctx->sync;
     a.xcd_local = ctx->use_xcd_local;
     hipError_t e = hipErrorInvalidValue;
-    if (bits == 4) {
-        if (route) {
-            if (xmode == NMOE_XBF16) e = nmoe_fused_launch<4, true, NMOE_XBF16>(a, s);
-            else if (xmode == NMOE_XF32) e = nmoe_fused_launch<4, true, NMOE_XF32>(a, s);
-            else e = nmoe_fused_launch<4, true, NMOE_XNORM>(a, s);
-        } else {
-            e = xmode == NMOE_XBF16 ? nmoe_fused_launch<4, false, NMOE_XBF16>(a, s)
-                                    : nmoe_fused_launch<4, false, NMOE_XF32>(a, s);
-        }
-    } else {
-        if (route) {
-            if (xmode == NMOE_XBF16) e = nmoe_fused_launch<2, true, NMOE_XBF16>(a, s);
-            else if (xmode == NMOE_XF32) e = nmoe_fused_launch<2, true, NMOE_XF32>(a, s);
-            else e = nmoe_fused_launch<2, true, NMOE_XNORM>(a, s);
-        } else {
-            e = xmode == NMOE_XBF16 ? nmoe_fused_launch<2, false, NMOE_XBF16>(a, s)
-                                    : nmoe_fused_launch<2, false, NMOE_XF32>(a, s);
-        }
-    }
+    const int r = !route ? NMOE_ROUTE_GIVEN : q4r ? NMOE_ROUTE_Q4 : NMOE_ROUTE_BF16;
+    if (bits == 4)
+        e = r == NMOE_ROUTE_Q4     ? nmoe_fused_launch_x<4, NMOE_ROUTE_Q4>(xmode, a, s)
+            : r == NMOE_ROUTE_BF16 ? nmoe_fused_launch_x<4, NMOE_ROUTE_BF16>(xmode, a, s)
+                                   : nmoe_fused_launch_x<4, NMOE_ROUTE_GIVEN>(xmode, a, s);
+    else
+        e = r == NMOE_ROUTE_Q4     ? nmoe_fused_launch_x<2, NMOE_ROUTE_Q4>(xmode, a, s)
+            : r == NMOE_ROUTE_BF16 ? nmoe_fused_launch_x<2, NMOE_ROUTE_BF16>(xmode, a, s)
+                                   : nmoe_fused_launch_x<2, NMOE_ROUTE_GIVEN>(xmode, a, s);
     if (e != hipSuccess) return nmoe_hip_check(ctx, e, "fused decode launch");
     return NMOE_HIP_OK;
 }

@@ -233,6 +233,25 @@ __device__ __forceinline__ float nmoe_router_row_bf16(const uint4 wv[4], const f
     return nmoe_wave_sum_tree(acc);
 }
 
+/* Router logit of one q4 row (the model's router, metal/kernels.metal:472-513
+ * semantics) by one wavefront: lane L owns the words L, L+64, L+128, L+192
+ * (columns 8 word .. +7) and their groups' raw bf16 scale and bias;
+ * w = fma(q, s, b), acc = fma(w, x, acc) in column order, lanes combined by
+ * the pairwise tree -- the order of the multi-launch q4 router kernel, so both
+ * paths give the same logits. */
+__device__ __forceinline__ float nmoe_router_row_q4(const uint32_t wq[4], const uint16_t s[4], const uint16_t b[4],
+                                                    const float xs[32]) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const float sf = nmoe_bf16f(s[j]), bf = nmoe_bf16f(b[j]);
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+            acc = __builtin_fmaf(__builtin_fmaf((float)((wq[j] >> (4 * i)) & 0xFu), sf, bf), xs[8 * j + i], acc);
+    }
+    return nmoe_wave_sum_tree(acc);
+}
+
 /* ------------------------------------------------------------ routing */
 
 /* Softmax probabilities of one token (math.m:67-93 bit for bit), entry

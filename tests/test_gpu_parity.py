@@ -645,3 +645,36 @@ def test_load_expert_dir(nh, tmp_path):
             c.load_expert_dir(str(d))
     finally:
         c.close()
+
+
+@pytest.mark.parametrize("bits", [4, 2])
+def test_fused_layer_with_q4_router(ctx, nh, bits):
+    """One token through nmoe_moe_layer with the model's q4 router: the fused
+    launch (router row per block, kernels.metal:472-513 semantics) routes
+    bit-exactly like the oracle and like the multi-launch kernels, and its
+    output is within tolerance."""
+    rng = np.random.default_rng(40 + bits)
+    seed, k, layer = 41, 8, 30 + bits
+    ctx.synth_layer(layer, bits, seed, SIGMA[bits])
+    wq = rng.integers(0, 2**32, size=(256, 256), dtype=np.uint64).astype(np.uint32)
+    sq = B.f32_to_bf16((rng.standard_normal((256, 32)) * 0.01).astype(np.float32))
+    bq = B.f32_to_bf16((-8 * B.bf16_to_f32(sq)).astype(np.float32))
+    rq = ctx.router_q4(ctx.to_device(wq), ctx.to_device(sq), ctx.to_device(bq))
+    x = rng.standard_normal(2048).astype(np.float32)
+    h = rng.standard_normal(2048).astype(np.float32)
+    dx, dh = ctx.to_device(x), ctx.to_device(h)
+    lg_want = np.zeros(256, np.float32)
+    B.oracle().orc_router_logits_q4(wq.ctypes.data, sq.ctypes.data, bq.ctypes.data, x.ctypes.data, 256, 2048,
+                                    lg_want.ctypes.data)
+    oi, ow, _ = B.route(lg_want, k)
+    want = B.moe_experts(host_pack(bits, seed, layer, oi[:k]), bits, x[None], k, oi[None], ow[None], h[None])[0]
+    for fused in (True, False):
+        ctx.set_fused(fused)
+        out, idx, w, lg = ctx.alloc(8192), ctx.alloc(32), ctx.alloc(32), ctx.alloc(1024)
+        ctx._check(ctx.moe_layer(layer, rq, dx, nh.F32, 1, k, dh, out, idx, w, lg))
+        assert ctx.device_status() == nh.OK
+        np.testing.assert_array_equal(lg.download(np.float32, 256).view(np.uint32), lg_want.view(np.uint32))
+        np.testing.assert_array_equal(idx.download(np.uint32, 8), oi, err_msg=f"fused={fused}")
+        np.testing.assert_array_equal(w.download(np.float32, 8).view(np.uint32), ow.view(np.uint32))
+        assert_close(out.download(np.float32, 2048), want, what=f"q4 router fused={fused}")
+    ctx.set_fused(True)
