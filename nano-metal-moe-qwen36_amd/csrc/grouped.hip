@@ -762,10 +762,11 @@ nmoe_grouped_down_kernel(const uint8_t *pack, const uint16_t *ahi, const uint16_
 /* out[t] = h_mid[t] + sum_{s<k} w[t][s] y[t*k+s] in slot order
  * (kernels.metal:1394-1423) (+ sigmoid(g) * shared_out); a slot whose index
  * is outside the layer contributes nothing (runtime.m:2977-2981). */
-__global__ void __launch_bounds__(256) nmoe_grouped_combine_kernel(const float *y, const uint32_t *idx,
-                                                                    const float *w, int k, const float *h_mid,
-                                                                    const float *shared_out,
-                                                                    const float *shared_gate_raw, float *out) {
+/* The same for rows not 16-byte aligned: one row per thread. */
+__global__ void __launch_bounds__(256) nmoe_grouped_combine_rows_kernel(const float *y, const uint32_t *idx,
+                                                                         const float *w, int k, const float *h_mid,
+                                                                         const float *shared_out,
+                                                                         const float *shared_gate_raw, float *out) {
     const int t = blockIdx.y, r = blockIdx.x * 256 + threadIdx.x;
     float moe = 0.0f;
     for (int s = 0; s < k; s++) {
@@ -775,6 +776,38 @@ __global__ void __launch_bounds__(256) nmoe_grouped_combine_kernel(const float *
     float o = h_mid[(size_t)t * NMOE_HIDDEN + r] + moe;
     if (shared_out != NULL) o = o + nmoe_sigmoid_dev(shared_gate_raw[t]) * shared_out[(size_t)t * NMOE_HIDDEN + r];
     out[(size_t)t * NMOE_HIDDEN + r] = o;
+}
+
+__global__ void __launch_bounds__(256) nmoe_grouped_combine_kernel(const float *y, const uint32_t *idx,
+                                                                    const float *w, int k, const float *h_mid,
+                                                                    const float *shared_out,
+                                                                    const float *shared_gate_raw, float *out) {
+    /* four consecutive rows per thread; all k partial rows are loaded before
+     * the sum (an invalid slot's row was never written: its value is
+     * dropped by the select, never multiplied into the sum) */
+    const int t = blockIdx.y, r = 4 * (blockIdx.x * 256 + threadIdx.x);
+    float4 yv[NMOE_MAX_K];
+#pragma unroll
+    for (int s = 0; s < NMOE_MAX_K; s++)
+        if (s < k) yv[s] = *(const float4 *)(y + ((size_t)t * k + s) * NMOE_HIDDEN + r);
+    const float4 h = *(const float4 *)(h_mid + (size_t)t * NMOE_HIDDEN + r);
+    float m[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int s = 0; s < NMOE_MAX_K; s++) {
+        if (s >= k) break;
+        const bool valid = idx[(size_t)t * NMOE_MAX_K + s] < NMOE_EXPERTS;
+        const float ws = w[(size_t)t * NMOE_MAX_K + s];
+        const float v[4] = {yv[s].x, yv[s].y, yv[s].z, yv[s].w};
+#pragma unroll
+        for (int i = 0; i < 4; i++) m[i] = valid ? m[i] + ws * v[i] : m[i];
+    }
+    float o[4] = {h.x + m[0], h.y + m[1], h.z + m[2], h.w + m[3]};
+    if (shared_out != NULL) {
+        const float g = nmoe_sigmoid_dev(shared_gate_raw[t]);
+        const float4 sh = *(const float4 *)(shared_out + (size_t)t * NMOE_HIDDEN + r);
+        o[0] = o[0] + g * sh.x, o[1] = o[1] + g * sh.y, o[2] = o[2] + g * sh.z, o[3] = o[3] + g * sh.w;
+    }
+    *(float4 *)(out + (size_t)t * NMOE_HIDDEN + r) = make_float4(o[0], o[1], o[2], o[3]);
 }
 
 /* ------------------------------------------------------------ host */
@@ -841,8 +874,12 @@ static int nmoe_grouped_run(nmoe_hip_ctx *ctx, const uint8_t *pack, const void *
     hipLaunchKernelGGL((nmoe_grouped_down_kernel<BITS>), gdn, dim3(512), 0, s, pack, (const uint16_t *)ctx->g_ahi,
                        (const uint16_t *)ctx->g_alo, (const float *)ctx->g_as, (const uint32_t *)ctx->g_perm,
                        (const uint32_t *)ctx->g_offsets, ctx->g_y);
-    hipLaunchKernelGGL(nmoe_grouped_combine_kernel, dim3(NMOE_HIDDEN / 256, ntok), dim3(256), 0, s,
-                       (const float *)ctx->g_y, idx, w, k, h_mid, shared_out, shared_gate_raw, out);
+    if (nmoe_aligned(h_mid, 16) && nmoe_aligned(out, 16) && (shared_out == NULL || nmoe_aligned(shared_out, 16)))
+        hipLaunchKernelGGL(nmoe_grouped_combine_kernel, dim3(NMOE_HIDDEN / 1024, ntok), dim3(256), 0, s,
+                           (const float *)ctx->g_y, idx, w, k, h_mid, shared_out, shared_gate_raw, out);
+    else
+        hipLaunchKernelGGL(nmoe_grouped_combine_rows_kernel, dim3(NMOE_HIDDEN / 256, ntok), dim3(256), 0, s,
+                           (const float *)ctx->g_y, idx, w, k, h_mid, shared_out, shared_gate_raw, out);
     const hipError_t e = hipGetLastError();
     return e == hipSuccess ? NMOE_HIP_OK : nmoe_hip_check(ctx, e, "grouped expert launch");
 }
