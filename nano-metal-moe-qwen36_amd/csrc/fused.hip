@@ -8,7 +8,7 @@
  * (kernels.metal:562-640), down + weighted combine (kernels.metal:1456-1542)
  * and the next layer's input RMSNorm (runtime.m:2893-2900) -- three
  * host/device crossings per layer.  Here the layer pack is resident in HBM
- * and the step is one launch of 256 blocks x 5 wavefronts (4 workers that
+ * and the step is one launch of 256 blocks x 9 wavefronts (8 workers that
  * stream and multiply expert rows, 1 control wavefront that routes).
  *
  * Blocks form 8 groups of 32 (group g = block % 8, j = block / 8); group g
@@ -26,8 +26,9 @@
  *   G  gate/up dot products + SwiGLU -> act[g][512].
  *   D  block j waits for act[g], computes y_g = down_g . act[g] for rows
  *      64j..64j+63 -> ypart[g].
- *   C  the last of the K blocks j to count in on chunk j's counter combines
- *      out = h_mid + sum_s w_s y_s (+ sigmoid(g) * shared) in slot order.
+ *   C  block j of group j % K polls the other groups' partials of rows
+ *      64j..64j+63 and combines out = h_mid + sum_s w_s y_s
+ *      (+ sigmoid(g) * shared) in slot order.
  *
  * Routing runs in a control wavefront per block: the candidates (the k
  * largest logits) are handed to the workers one selection round at a time,
@@ -41,9 +42,8 @@
  * "wait" and "fetch" into one memory round trip: no barrier counter and no
  * L2-wide cache maintenance.  The epoch is the launch count, kept per block
  * (each block increments its own word once per launch, so all agree).  The
- * combine needs no waiting at all: the K partials of a chunk meet at an
- * arrival counter, and only the last arrival reads the others.  Idle
- * groups (K < 8) exit after their router row.  Every wait is bounded.
+ * combine of a chunk polls the chunk's K-1 other partials in one block.
+ * Idle groups (K < 8) exit after their router row.  Every wait is bounded.
  */
 #include "nmoe_device.h"
 
@@ -56,8 +56,10 @@ static __constant__ uint64_t nmoe_fused_exp2_tab[32] = NMOE_EXP2_TAB32;
 #define NMOE_FUSED_GROUP_BLOCKS (NMOE_FUSED_BLOCKS / NMOE_FUSED_GROUPS) /* 32 */
 #define NMOE_FUSED_CHUNK (NMOE_HIDDEN / NMOE_FUSED_GROUP_BLOCKS)         /* 64 output rows per block */
 #define NMOE_FUSED_GU_ROWS (NMOE_INTER / NMOE_FUSED_GROUP_BLOCKS)        /* 16 gate/up rows per block */
-#define NMOE_FUSED_THREADS 320 /* 4 worker wavefronts + the control wavefront */
-#define NMOE_FUSED_CTRL 4
+#define NMOE_FUSED_WORKERS 8 /* worker wavefronts per block, plus two control wavefronts */
+#define NMOE_FUSED_THREADS (64 * (NMOE_FUSED_WORKERS + 2))
+#define NMOE_FUSED_CTRL NMOE_FUSED_WORKERS        /* router row, candidate selection */
+#define NMOE_FUSED_EXACT (NMOE_FUSED_WORKERS + 1) /* exact routing, group assignment */
 
 
 /* exchange scratch layout (64-bit tagged words) */
@@ -69,7 +71,7 @@ static __constant__ uint64_t nmoe_fused_exp2_tab[32] = NMOE_EXP2_TAB32;
 #define NMOE_XCH_LOGITS 0
 #define NMOE_XCH_ACT (NMOE_XCH_SP * NMOE_EXPERTS)
 #define NMOE_XCH_YPART (NMOE_XCH_ACT + NMOE_XCH_SP * NMOE_FUSED_GROUPS * NMOE_INTER)
-#define NMOE_XCH_WORDS (NMOE_XCH_YPART + NMOE_FUSED_GROUPS * NMOE_HIDDEN / 2) /* partials: fp32 */
+#define NMOE_XCH_WORDS (NMOE_XCH_YPART + NMOE_FUSED_GROUPS * NMOE_HIDDEN) /* tagged partials, polled by one block */
 
 /* x sources: XF32 / XBF16 = activations given; XNORM = x is RMSNorm(h). */
 #define NMOE_XF32 0
@@ -129,11 +131,13 @@ __device__ __forceinline__ uint32_t nmoe_xcc_id() {
  * values.  Each lane polls its own words. */
 template <int N>
 __device__ __forceinline__ void nmoe_poll(const uint64_t *const p[N], uint32_t epoch, float v[N], uint32_t *status,
-                                          bool die_local = false) {
+                                          bool die_local = false, uint32_t need = (1u << N) - 1u) {
     /* a word, once seen with this epoch, is not loaded again: after the
      * first round only the stragglers' words are re-polled, which keeps the
-     * polling traffic off the memory channels the late writers need */
-    uint32_t need = (1u << N) - 1u, spins = 0;
+     * polling traffic off the memory channels the late writers need.  need:
+     * the words to wait for (the others are left untouched) */
+    uint32_t spins = 0;
+    if (need == 0) return;
     for (;;) {
         uint64_t w[N];
 #pragma unroll
@@ -199,11 +203,13 @@ __global__ void __launch_bounds__(NMOE_FUSED_THREADS) nmoe_fused_decode_kernel(n
     using Q = nmoe_q<BITS>;
     using L = nmoe_layout<BITS>;
     constexpr int RPS = NMOE_WAVE / Q::LPR_G;   /* gate/up rows per wave step: 1 (q4) / 2 (q2) */
-    constexpr int GSTEPS = 4 / RPS;             /* 4 gate/up rows per worker wavefront */
+    constexpr int GSTEPS = NMOE_FUSED_GU_ROWS / NMOE_FUSED_WORKERS / RPS; /* gate/up rows per worker, in steps */
     constexpr int RPW_D = NMOE_WAVE / Q::LPR_D; /* down rows per wave step: 4 (q4) / 8 (q2) */
-    constexpr int DSTEPS = 16 / RPW_D;          /* 16 down rows per worker wavefront */
+    constexpr int DSTEPS = NMOE_FUSED_CHUNK / NMOE_FUSED_WORKERS / RPW_D; /* down rows per worker, in steps */
+    static_assert(GSTEPS >= 1 && DSTEPS >= 1, "rows split evenly over the worker wavefronts");
     __shared__ uint64_t s_tab[32];
     __shared__ float s_scratch[NMOE_EXPERTS];
+    __shared__ float s_lg[NMOE_EXPERTS]; /* the token's logits, candidate -> exact wavefront */
     __shared__ float s_act[NMOE_INTER];
     __shared__ float s_y[NMOE_FUSED_CHUNK];
     __shared__ uint32_t s_t[4 * NMOE_MAX_K];
@@ -214,17 +220,18 @@ __global__ void __launch_bounds__(NMOE_FUSED_THREADS) nmoe_fused_decode_kernel(n
     __shared__ double s_dd[8];
     __shared__ float s_f[1];
     __shared__ uint32_t s_epoch;
-    __shared__ uint32_t s_ncand, s_confirm; /* control -> workers hand-offs */
+    __shared__ uint32_t s_ncand, s_confirm, s_lgok; /* control -> workers / control -> control hand-offs */
     __shared__ float s_h[XMODE == NMOE_XNORM ? NMOE_HIDDEN : 1];
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const bool ctrl = wave == NMOE_FUSED_CTRL;
+    const bool ctrl = wave >= NMOE_FUSED_CTRL; /* either control wavefront */
+    const bool cwave = wave == NMOE_FUSED_CTRL;
     const int g = blockIdx.x % NMOE_FUSED_GROUPS, j = blockIdx.x / NMOE_FUSED_GROUPS;
     const int k = a.k;
     uint32_t *status = a.sync + NMOE_SYNC_STATUS;
     uint64_t *xlg = a.xch + NMOE_XCH_LOGITS;
     uint64_t *xact = a.xch + NMOE_XCH_ACT + NMOE_XCH_SP * g * NMOE_INTER;
-    float *ypart = (float *)(a.xch + NMOE_XCH_YPART);
+    uint64_t *ypart = a.xch + NMOE_XCH_YPART;
 
     /* Independent loads go out first and unconditionally (loads retire in
      * order, so a later wait on one of them must not cover the big ones):
@@ -240,8 +247,7 @@ __global__ void __launch_bounds__(NMOE_FUSED_THREADS) nmoe_fused_decode_kernel(n
     uint32_t wq[4];
     uint16_t rsr[4], rbr[4];
     float xs_r[32], lv[4];
-    uint32_t cand[NMOE_MAX_K];
-    if (ROUTE && ctrl) {
+    if (ROUTE && cwave) {
         if (ROUTE == NMOE_ROUTE_Q4) {
             /* q4 router row: words lane + 64q (columns 8 word .. +7) and their
              * groups' scale and bias, kept raw until the dot product */
@@ -268,17 +274,18 @@ __global__ void __launch_bounds__(NMOE_FUSED_THREADS) nmoe_fused_decode_kernel(n
         s_epoch = ep_old + 1u;
         s_ncand = 0u;
         s_confirm = 0u;
+        s_lgok = 0u;
     }
     double rinv = 1.0;
     if (XMODE == NMOE_XNORM) rinv = 1.0 / (double)nmoe_block_rms_exact((const float *)a.x, a.eps, s_h, s_dd, s_f);
     __syncthreads();
     const uint32_t epoch = s_epoch;
 
-    if (ROUTE && ctrl) {
-        /* the control wavefront shares a SIMD with a worker: its routing is
-         * on the critical path, the worker's multiply-adds mostly are not */
+    if (ROUTE && cwave) {
+        /* the control wavefronts share SIMDs with workers: their routing is
+         * on the critical path, the workers' multiply-adds mostly are not */
         __builtin_amdgcn_s_setprio(2);
-        /* ---- R (control wavefront): router row blockIdx.x */
+        /* ---- R (candidate wavefront): router row blockIdx.x */
         if (XMODE == NMOE_XNORM)
 #pragma unroll
             for (int q = 0; q < 4; q++) nmoe_x_cols<XMODE>(a.x, (lane + 64 * q) * 8, 8, rinv, xs_r + 8 * q);
@@ -286,15 +293,19 @@ __global__ void __launch_bounds__(NMOE_FUSED_THREADS) nmoe_fused_decode_kernel(n
             ROUTE == NMOE_ROUTE_Q4 ? nmoe_router_row_q4(wq, rsr, rbr, xs_r) : nmoe_router_row_bf16(wv, xs_r);
         if (lane == 0) nmoe_st_tagged(xlg + NMOE_XCH_SP * blockIdx.x, epoch, logit);
         if (g < k) {
-            /* ---- T: wait for all 256 logits; the candidates are the k
-             * largest logits, published one per selection round so that
-             * group s starts streaming its expert as soon as candidate s is
-             * known.  Their probabilities are the k largest too, up to
-             * ties, which the exact routing below settles. */
+            /* ---- T: wait for all 256 logits and hand them to the exact
+             * wavefront; the candidates are the k largest logits, published
+             * one per selection round so that group s starts streaming its
+             * expert as soon as candidate s is known.  Their probabilities
+             * are the k largest too, up to ties, which the exact routing
+             * settles. */
             const uint64_t *pl[4] = {xlg + NMOE_XCH_SP * lane, xlg + NMOE_XCH_SP * (lane + 64),
                                      xlg + NMOE_XCH_SP * (lane + 128), xlg + NMOE_XCH_SP * (lane + 192)};
             nmoe_poll<4>(pl, epoch, lv, status);
-            uint32_t key[4], ck[NMOE_MAX_K];
+#pragma unroll
+            for (int q = 0; q < 4; q++) s_lg[lane + 64 * q] = lv[q];
+            if (lane == 0) __hip_atomic_store(&s_lgok, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+            uint32_t key[4], cand[NMOE_MAX_K], ck[NMOE_MAX_K];
 #pragma unroll
             for (int q = 0; q < 4; q++) key[q] = nmoe_fkey(lv[q]);
             nmoe_wave_top_keys(key, k, cand, ck, [&](int s, uint32_t e) {
@@ -303,58 +314,61 @@ __global__ void __launch_bounds__(NMOE_FUSED_THREADS) nmoe_fused_decode_kernel(n
                     __hip_atomic_store(&s_ncand, (uint32_t)(s + 1), __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
                 }
             });
-            bool taken[4];
-#pragma unroll
-            for (int q = 0; q < 4; q++) taken[q] = key[q] == 0u; /* fkeys are never 0 */
-
-            /* ---- exact routing (under the expert loads), then the expert of
-             * each group: a candidate outside the exact selection (only
-             * possible on probability ties) hands its group to a selected
-             * expert no group holds yet */
-            uint32_t si[NMOE_MAX_K];
-            float sw[NMOE_MAX_K];
-            nmoe_wave_route_cand(lv, k, taken, s_scratch, s_t, s_tab, si, sw);
-            uint32_t ct = 0, et = 0;
-            float wt = 0.0f;
-            bool c_in_e = false, e_in_c = false;
-#pragma unroll
-            for (int s = 0; s < NMOE_MAX_K; s++) {
-                if (s == lane) {
-                    ct = cand[s];
-                    et = si[s];
-                    wt = sw[s];
-                }
-            }
-#pragma unroll
-            for (int s = 0; s < NMOE_MAX_K; s++) {
-                if (s < k) {
-                    c_in_e = c_in_e || ct == si[s];
-                    e_in_c = e_in_c || et == cand[s];
-                }
-            }
-            const uint64_t fm = __ballot(lane < k && !c_in_e); /* groups to re-point */
-            const uint64_t mm = __ballot(lane < k && !e_in_c); /* slots no group holds */
-            uint32_t xg = ct;
-            if (fm != 0) {
-                const int fr = (int)__builtin_popcountll(fm & ((1ull << lane) - 1ull));
-#pragma unroll
-                for (int s = 0; s < NMOE_MAX_K; s++)
-                    if (((mm >> s) & 1) && (int)__builtin_popcountll(mm & ((1ull << s) - 1ull)) == fr &&
-                        ((fm >> lane) & 1))
-                        xg = si[s];
-            }
-            uint32_t sg = 0;
-#pragma unroll
-            for (int q = 0; q < NMOE_MAX_K; q++)
-                if (q < k && (uint32_t)__builtin_amdgcn_readlane((int)xg, q) == et) sg = (uint32_t)q;
-            if (lane < NMOE_MAX_K) {
-                s_gx[lane] = xg;
-                s_slotg[lane] = sg;
-                s_w[lane] = wt;
-                s_t[lane] = et; /* written out at the end */
-            }
-            if (lane == 0) __hip_atomic_store(&s_confirm, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
         }
+    }
+    if (ROUTE && wave == NMOE_FUSED_EXACT && g < k) {
+        /* ---- exact routing (math.m softmax / top-k / renormalise), from
+         * the moment the logits are in, alongside the candidate rounds and
+         * the expert loads; then the expert of each group: a candidate
+         * outside the exact selection (only possible on probability ties)
+         * hands its group to a selected expert no group holds yet */
+        __builtin_amdgcn_s_setprio(2);
+        nmoe_lds_wait_above(&s_lgok, 0u, status);
+        uint32_t si[NMOE_MAX_K], cand[NMOE_MAX_K];
+        float sw[NMOE_MAX_K];
+        nmoe_wave_route(s_lg, NMOE_EXPERTS, k, s_scratch, s_tab, si, sw, NULL);
+        nmoe_lds_wait_above(&s_ncand, (uint32_t)(k - 1), status);
+#pragma unroll
+        for (int s = 0; s < NMOE_MAX_K; s++) cand[s] = s < k ? s_cand[s] : 0u;
+        uint32_t ct = 0, et = 0;
+        float wt = 0.0f;
+        bool c_in_e = false, e_in_c = false;
+#pragma unroll
+        for (int s = 0; s < NMOE_MAX_K; s++) {
+            if (s == lane) {
+                ct = cand[s];
+                et = si[s];
+                wt = sw[s];
+            }
+        }
+#pragma unroll
+        for (int s = 0; s < NMOE_MAX_K; s++) {
+            if (s < k) {
+                c_in_e = c_in_e || ct == si[s];
+                e_in_c = e_in_c || et == cand[s];
+            }
+        }
+        const uint64_t fm = __ballot(lane < k && !c_in_e); /* groups to re-point */
+        const uint64_t mm = __ballot(lane < k && !e_in_c); /* slots no group holds */
+        uint32_t xg = ct;
+        if (fm != 0) {
+            const int fr = (int)__builtin_popcountll(fm & ((1ull << lane) - 1ull));
+#pragma unroll
+            for (int s = 0; s < NMOE_MAX_K; s++)
+                if (((mm >> s) & 1) && (int)__builtin_popcountll(mm & ((1ull << s) - 1ull)) == fr && ((fm >> lane) & 1))
+                    xg = si[s];
+        }
+        uint32_t sg = 0;
+#pragma unroll
+        for (int q = 0; q < NMOE_MAX_K; q++)
+            if (q < k && (uint32_t)__builtin_amdgcn_readlane((int)xg, q) == et) sg = (uint32_t)q;
+        if (lane < NMOE_MAX_K) {
+            s_gx[lane] = xg;
+            s_slotg[lane] = sg;
+            s_w[lane] = wt;
+            s_t[lane] = et; /* written out at the end */
+        }
+        if (lane == 0) __hip_atomic_store(&s_confirm, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
     }
     if (!ROUTE) {
         if (tid < NMOE_MAX_K) {
@@ -374,8 +388,8 @@ __global__ void __launch_bounds__(NMOE_FUSED_THREADS) nmoe_fused_decode_kernel(n
     /* ---- P (workers): issue all weight loads of this wavefront */
     const int gsub = lane / Q::LPR_G, gl = lane % Q::LPR_G, ggrp = gl * Q::CPL / NMOE_GROUP;
     const int dsub = lane / Q::LPR_D, dl = lane % Q::LPR_D, dgrp = dl * Q::CPL / NMOE_GROUP;
-    const int grow0 = j * NMOE_FUSED_GU_ROWS + 4 * wave + gsub;
-    const int drow0 = j * NMOE_FUSED_CHUNK + 16 * wave + dsub;
+    const int grow0 = j * NMOE_FUSED_GU_ROWS + (NMOE_FUSED_GU_ROWS / NMOE_FUSED_WORKERS) * wave + gsub;
+    const int drow0 = j * NMOE_FUSED_CHUNK + (NMOE_FUSED_CHUNK / NMOE_FUSED_WORKERS) * wave + dsub;
     /* the burst holds raw loads only: unpacking x or combining a scale with
      * its bias inside it would make the wave wait for those loads before
      * issuing the rest */
@@ -476,11 +490,14 @@ __global__ void __launch_bounds__(NMOE_FUSED_THREADS) nmoe_fused_decode_kernel(n
 
     /* ---- D (workers): wait for act[g], then y_g for rows 64j..64j+63 */
     if (!ctrl) {
-        const uint64_t *pa[2] = {xact + NMOE_XCH_SP * tid, xact + NMOE_XCH_SP * (tid + 256)};
-        float av[2];
-        nmoe_poll<2>(pa, epoch, av, status, a.xcd_local != 0);
-        s_act[nmoe_act_slot<Q::CPL / 4>(tid)] = av[0];
-        s_act[nmoe_act_slot<Q::CPL / 4>(tid + 256)] = av[1];
+        constexpr int APT = NMOE_INTER / (64 * NMOE_FUSED_WORKERS); /* act words per worker thread */
+        const uint64_t *pa[APT];
+        float av[APT];
+#pragma unroll
+        for (int q = 0; q < APT; q++) pa[q] = xact + NMOE_XCH_SP * (tid + 64 * NMOE_FUSED_WORKERS * q);
+        nmoe_poll<APT>(pa, epoch, av, status, a.xcd_local != 0);
+#pragma unroll
+        for (int q = 0; q < APT; q++) s_act[nmoe_act_slot<Q::CPL / 4>(tid + 64 * NMOE_FUSED_WORKERS * q)] = av[q];
     }
     __syncthreads();
     if (!ctrl) {
@@ -501,28 +518,27 @@ __global__ void __launch_bounds__(NMOE_FUSED_THREADS) nmoe_fused_decode_kernel(n
         for (int i = 0; i < DSTEPS; i++) {
             float y = __builtin_fmaf(nmoe_bf16f(dsc[i]), nmoe_dot16<BITS>(dwv[i], as), nmoe_bf16f(dbi[i]) * asum);
             y = nmoe_dpp_group_sum<Q::LPR_D>(y);
-            if (dl == 0) s_y[16 * wave + dsub + i * RPW_D] = y;
+            if (dl == 0) s_y[(NMOE_FUSED_CHUNK / NMOE_FUSED_WORKERS) * wave + dsub + i * RPW_D] = y;
         }
     }
     __syncthreads();
-    /* ---- C: the last of the K groups to finish rows 64j..64j+63 combines
-     * them (out = h_mid + sum_s w_s y_s in slot order): each block j
-     * publishes its partial, then counts itself in on chunk j's counter;
-     * the block that completes the count reads the other partials.  Nobody
-     * waits, and the counter is left at 0 for the next launch. */
+    /* ---- C: group j % K combines rows 64j..64j+63 (out = h_mid + sum_s
+     * w_s y_s in slot order); the other groups publish their partials as
+     * tagged words and are done.  The combiner polls the K-1 partials of its
+     * chunk: one round trip after the last one is written. */
     const int row = j * NMOE_FUSED_CHUNK + tid;
     if (tid < NMOE_FUSED_CHUNK) {
-        nmoe_st_dev(ypart + g * NMOE_HIDDEN + row, s_y[tid]);
-        __builtin_amdgcn_s_waitcnt(0); /* the partials are visible before the count */
-        uint32_t old = 0;
-        uint32_t *cnt = a.sync + NMOE_SYNC_COMBINE(j);
-        if (tid == 0) old = nmoe_add_u32_dev(cnt, 1u);
-        old = (uint32_t)__builtin_amdgcn_readfirstlane((int)old);
-        if (old == (uint32_t)k - 1u) {
+        if (g != j % k) {
+            nmoe_st_tagged(ypart + g * NMOE_HIDDEN + row, epoch, s_y[tid]);
+        } else {
+            const uint64_t *pp[NMOE_MAX_K];
             float ys[NMOE_MAX_K];
 #pragma unroll
-            for (int q = 0; q < NMOE_MAX_K; q++)
-                ys[q] = q == g ? s_y[tid] : (q < k ? nmoe_ld_dev(ypart + q * NMOE_HIDDEN + row) : 0.0f);
+            for (int q = 0; q < NMOE_MAX_K; q++) {
+                pp[q] = ypart + q * NMOE_HIDDEN + row;
+                ys[q] = s_y[tid];
+            }
+            nmoe_poll<NMOE_MAX_K>(pp, epoch, ys, status, false, ((1u << k) - 1u) & ~(1u << g));
             /* slot order: slot s is streamed by group s_slotg[s] */
             float moe = 0.0f;
 #pragma unroll
@@ -539,10 +555,9 @@ __global__ void __launch_bounds__(NMOE_FUSED_THREADS) nmoe_fused_decode_kernel(n
             float r = hm + moe;
             if (a.shared_out != NULL) r = r + nmoe_sigmoid_dev(a.shared_gate_raw[0]) * sh;
             a.out[row] = r;
-            if (tid == 0) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     }
-    if (ROUTE && blockIdx.x == 0 && ctrl) {
+    if (ROUTE && blockIdx.x == 0 && cwave) {
         if (lane < NMOE_MAX_K) {
             if (a.idx_out != NULL) a.idx_out[lane] = s_t[lane];
             if (a.w_out != NULL) a.w_out[lane] = s_w[lane];

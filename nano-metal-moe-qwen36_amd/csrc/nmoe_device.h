@@ -397,93 +397,6 @@ __device__ __forceinline__ int nmoe_wave_route(const float *lg, int num_experts,
     return n;
 }
 
-/* Exact routing of one token of 256 experts given the candidates: the n
- * entries with the largest logits, marked by taken[j] (lane L, entry
- * L + 64 j).  Same result as nmoe_wave_route, but the slow part -- softmax --
- * can run while work that only needs the candidate set proceeds.  With p8
- * the smallest candidate probability, every entry has p <= p8 or is a
- * candidate whenever A = #{p > p8} < n (always, as exp is monotone; checked,
- * not assumed): the selection is then the A entries with p > p8 plus the
- * lowest-index entries with p == p8, put in (p desc, index asc) order by
- * rank counting.  A >= n falls back to the full top-k on p.
- * s_t: 4 x NMOE_MAX_K words of LDS, private to the wave. */
-__device__ __forceinline__ void nmoe_wave_route_cand(const float l[4], int n, const bool taken[4], float *scratch,
-                                                     uint32_t *s_t, const uint64_t *tab, uint32_t sel_i[NMOE_MAX_K],
-                                                     float sel_w[NMOE_MAX_K]) {
-    const int lane = threadIdx.x & 63;
-    float p[4];
-    nmoe_wave_softmax(l, NMOE_EXPERTS, scratch, tab, p);
-    float pc = __builtin_inff();
-#pragma unroll
-    for (int j = 0; j < 4; j++) pc = taken[j] ? fminf(pc, p[j]) : pc;
-    const float p8 = nmoe_wave_min_f(pc);
-    uint64_t gt[4], eq[4];
-    int above = 0;
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-        gt[j] = __ballot(p[j] > p8);
-        eq[j] = __ballot(p[j] == p8);
-        above += __builtin_popcountll(gt[j]);
-    }
-    float sel_v[NMOE_MAX_K];
-    if (above < n) {
-        /* members: p > p8, and the first n - above entries with p == p8;
-         * member t (index order) goes to s_t[t] (entry) / s_t[8 + t] (p) */
-        const int take = n - above;
-        int before = 0, pos_base = 0;
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const bool e_j = (eq[j] >> lane) & 1, g_j = (gt[j] >> lane) & 1;
-            const int eq_rank = before + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(eq[j] >> 32),
-                                                                        __builtin_amdgcn_mbcnt_lo((uint32_t)eq[j], 0u));
-            const bool mine = g_j || (e_j && eq_rank < take);
-            before += __builtin_popcountll(eq[j]);
-            const uint64_t mm = __ballot(mine);
-            const int pos = pos_base + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mm >> 32),
-                                                                      __builtin_amdgcn_mbcnt_lo((uint32_t)mm, 0u));
-            if (mine) {
-                s_t[pos] = (uint32_t)(lane + 64 * j);
-                s_t[NMOE_MAX_K + pos] = __float_as_uint(p[j]);
-            }
-            pos_base += __builtin_popcountll(mm);
-        }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-        /* lane t < n: member t; its slot = members ahead of it in
-         * (p desc, index asc) order */
-        const uint32_t my_i = s_t[lane & (NMOE_MAX_K - 1)];
-        const float my_p = __uint_as_float(s_t[NMOE_MAX_K + (lane & (NMOE_MAX_K - 1))]);
-        int rank = 0;
-#pragma unroll
-        for (int u = 0; u < NMOE_MAX_K; u++) {
-            const float pu = nmoe_readlane_f(my_p, u);
-            rank += (u < n && (pu > my_p || (pu == my_p && u < lane))) ? 1 : 0;
-        }
-        if (lane < n) {
-            s_t[2 * NMOE_MAX_K + rank] = my_i;
-            s_t[3 * NMOE_MAX_K + rank] = __float_as_uint(my_p);
-        }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-#pragma unroll
-        for (int s = 0; s < NMOE_MAX_K; s++) {
-            const uint32_t ii = s_t[2 * NMOE_MAX_K + s], pp = s_t[3 * NMOE_MAX_K + s];
-            sel_i[s] = s < n ? ii : 0u;
-            sel_v[s] = s < n ? __uint_as_float(pp) : 0.0f;
-        }
-    } else {
-        uint32_t key[4], selkey[NMOE_MAX_K];
-#pragma unroll
-        for (int j = 0; j < 4; j++) key[j] = __float_as_uint(p[j]) + 1u;
-        nmoe_wave_top_keys(key, n, sel_i, selkey);
-#pragma unroll
-        for (int s = 0; s < NMOE_MAX_K; s++) sel_v[s] = s < n ? __uint_as_float(selkey[s] - 1u) : 0.0f;
-    }
-    nmoe_renormalize(sel_v, n, sel_w);
-}
-
 /* --------------------------------------------- exchange across blocks */
 
 /* Device-coherent loads/stores of values exchanged between blocks of one
