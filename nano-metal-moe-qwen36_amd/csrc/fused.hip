@@ -221,7 +221,7 @@ __global__ void __launch_bounds__(NMOE_FUSED_THREADS) nmoe_fused_decode_kernel(n
     __shared__ float s_f[1];
     __shared__ uint32_t s_epoch;
     __shared__ uint32_t s_ncand, s_confirm, s_lgok; /* control -> workers / control -> control hand-offs */
-    __shared__ float s_h[XMODE == NMOE_XNORM ? NMOE_HIDDEN : 1];
+    __shared__ __align__(16) float s_h[XMODE == NMOE_XNORM ? NMOE_HIDDEN : 4];
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const bool ctrl = wave >= NMOE_FUSED_CTRL; /* either control wavefront */
@@ -276,8 +276,21 @@ __global__ void __launch_bounds__(NMOE_FUSED_THREADS) nmoe_fused_decode_kernel(n
         s_confirm = 0u;
         s_lgok = 0u;
     }
-    double rinv = 1.0;
-    if (XMODE == NMOE_XNORM) rinv = 1.0 / (double)nmoe_block_rms_exact((const float *)a.x, a.eps, s_h, s_dd, s_f);
+    if (XMODE == NMOE_XNORM) {
+        /* x = h / rms once per block, into LDS in the workers' swizzled
+         * chunk order (as the act): the workers then hold no raw h and do
+         * no double arithmetic of their own */
+        const double rinv = 1.0 / (double)nmoe_block_rms_exact((const float *)a.x, a.eps, s_h, s_dd, s_f);
+        if (tid < NMOE_HIDDEN / 8) {
+#pragma unroll
+            for (int q = 0; q < 2; q++) {
+                const int c0 = 8 * tid + 4 * q;
+                float4 v;
+                nmoe_x_cols<NMOE_XNORM>(a.x, c0, 4, rinv, &v.x);
+                ((float4 *)s_h)[nmoe_act_slot<Q::CPL / 4>(c0) / 4] = v;
+            }
+        }
+    }
     __syncthreads();
     const uint32_t epoch = s_epoch;
 
@@ -288,7 +301,9 @@ __global__ void __launch_bounds__(NMOE_FUSED_THREADS) nmoe_fused_decode_kernel(n
         /* ---- R (candidate wavefront): router row blockIdx.x */
         if (XMODE == NMOE_XNORM)
 #pragma unroll
-            for (int q = 0; q < 4; q++) nmoe_x_cols<XMODE>(a.x, (lane + 64 * q) * 8, 8, rinv, xs_r + 8 * q);
+            for (int c = 0; c < 8; c++)
+                *(float4 *)(xs_r + 4 * c) =
+                    ((const float4 *)s_h)[nmoe_act_slot<Q::CPL / 4>(8 * lane + 512 * (c >> 1) + 4 * (c & 1)) / 4];
         const float logit =
             ROUTE == NMOE_ROUTE_Q4 ? nmoe_router_row_q4(wq, rsr, rbr, xs_r) : nmoe_router_row_bf16(wv, xs_r);
         if (lane == 0) nmoe_st_tagged(xlg + NMOE_XCH_SP * blockIdx.x, epoch, logit);
@@ -425,8 +440,9 @@ __global__ void __launch_bounds__(NMOE_FUSED_THREADS) nmoe_fused_decode_kernel(n
     if (!ctrl) {
         /* x first: loads retire in order, so G can start while down rows stream */
         const uint4 *xp = (const uint4 *)a.x + gl * XV;
+        if (XMODE != NMOE_XNORM)
 #pragma unroll
-        for (int c = 0; c < XV; c++) xr[c] = xp[c];
+            for (int c = 0; c < XV; c++) xr[c] = xp[c];
         if (ROUTE) /* candidate g published by the control wavefront */
             nmoe_lds_wait_above(&s_ncand, (uint32_t)g, status);
         cand_g = s_cand[g];
@@ -438,7 +454,9 @@ __global__ void __launch_bounds__(NMOE_FUSED_THREADS) nmoe_fused_decode_kernel(n
     float xs[Q::CPL];
 #pragma unroll
     for (int c = 0; c < XV; c++) {
-        if (XMODE == NMOE_XBF16) {
+        if (XMODE == NMOE_XNORM) {
+            *(float4 *)(xs + 4 * c) = ((const float4 *)s_h)[nmoe_act_slot<Q::CPL / 4>(4 * (gl * XV + c)) / 4];
+        } else if (XMODE == NMOE_XBF16) {
             nmoe_unpack_bf16x8(xr[c], xs + 8 * c);
         } else {
             xs[4 * c] = __uint_as_float(xr[c].x);
@@ -447,9 +465,6 @@ __global__ void __launch_bounds__(NMOE_FUSED_THREADS) nmoe_fused_decode_kernel(n
             xs[4 * c + 3] = __uint_as_float(xr[c].w);
         }
     }
-    if (XMODE == NMOE_XNORM)
-#pragma unroll
-        for (int c = 0; c < Q::CPL; c++) xs[c] = (float)((double)xs[c] * rinv);
 
     /* ---- G (workers): gate/up + SwiGLU -> act[g], published once the
      * control wavefront has confirmed the expert */
