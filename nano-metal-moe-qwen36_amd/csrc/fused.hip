@@ -68,6 +68,10 @@ static __constant__ uint64_t nmoe_fused_exp2_tab[32] = NMOE_EXP2_TAB32;
  * lines (measured: the last of 256 packed words is seen ~2.6 us after it is
  * written by 256 polling blocks, ~1.2 us when the words are 64 B apart). */
 #define NMOE_XCH_SP 8
+/* The act words of a group are polled by the group's own 32 blocks on one
+ * die and sit densely packed: 16 rows of one writer block share one
+ * 128-byte line, so a poll round is 32 line reads per block. */
+#define NMOE_XCH_ASP 1
 #define NMOE_XCH_LOGITS 0
 #define NMOE_XCH_ACT (NMOE_XCH_SP * NMOE_EXPERTS)
 #define NMOE_XCH_YPART (NMOE_XCH_ACT + NMOE_XCH_SP * NMOE_FUSED_GROUPS * NMOE_INTER)
@@ -158,6 +162,48 @@ __device__ __forceinline__ void nmoe_poll(const uint64_t *const p[N], uint32_t e
     }
 }
 
+/* nmoe_poll with two rounds in flight: loads return in order, so while one
+ * round's words are checked the next round is already on its way, and a
+ * word that lands just after a round was issued is seen about one round
+ * trip later instead of two.  All N words are loaded each round (they
+ * must be valid addresses); only those in `need` are waited for. */
+template <int N>
+__device__ __forceinline__ void nmoe_poll2(const uint64_t *const p[N], uint32_t epoch, float v[N], uint32_t *status,
+                                           uint32_t need) {
+    if (need == 0) return;
+    uint32_t spins = 0;
+    uint64_t wa[N], wb[N];
+    auto issue = [&](uint64_t(&w)[N]) { /* every word, so each round is N loads and the wait is vmcnt(N) */
+#pragma unroll
+        for (int i = 0; i < N; i++) w[i] = nmoe_ld_tagged(p[i]);
+    };
+    auto check = [&](const uint64_t(&w)[N]) {
+#pragma unroll
+        for (int i = 0; i < N; i++)
+            if ((need & (1u << i)) && nmoe_tag_is(w[i], epoch)) {
+                v[i] = nmoe_tag_val(w[i]);
+                need &= ~(1u << i);
+            }
+    };
+    issue(wa);
+    for (;;) { /* the barriers keep each round's loads ahead of the previous round's check */
+        __builtin_amdgcn_s_sleep(4);
+        issue(wb);
+        __builtin_amdgcn_sched_barrier(0);
+        check(wa);
+        if (need == 0) return;
+        __builtin_amdgcn_s_sleep(4);
+        issue(wa);
+        __builtin_amdgcn_sched_barrier(0);
+        check(wb);
+        if (need == 0) return;
+        if (++spins > NMOE_SPIN_LIMIT / 2) {
+            __hip_atomic_store(status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            return;
+        }
+    }
+}
+
 /* Waits (bounded) until the LDS word *w exceeds v: a hand-off from another
  * wavefront of the block that needs no block-wide barrier. */
 __device__ __forceinline__ void nmoe_lds_wait_above(uint32_t *w, uint32_t v, uint32_t *status) {
@@ -213,7 +259,7 @@ __global__ void __launch_bounds__(NMOE_FUSED_THREADS) nmoe_fused_decode_kernel(n
     __shared__ float s_act[NMOE_INTER];
     __shared__ float s_y[NMOE_FUSED_CHUNK];
     __shared__ uint32_t s_t[4 * NMOE_MAX_K];
-    __shared__ uint32_t s_cand[NMOE_MAX_K];  /* expert group g starts loading */
+    __shared__ uint32_t s_cand[NMOE_MAX_K];  /* expert group g starts loading (entry + 1; 0 = not yet) */
     __shared__ uint32_t s_gx[NMOE_MAX_K];    /* expert group g streams */
     __shared__ uint32_t s_slotg[NMOE_MAX_K]; /* group streaming slot s */
     __shared__ float s_w[NMOE_MAX_K];
@@ -230,7 +276,7 @@ __global__ void __launch_bounds__(NMOE_FUSED_THREADS) nmoe_fused_decode_kernel(n
     const int k = a.k;
     uint32_t *status = a.sync + NMOE_SYNC_STATUS;
     uint64_t *xlg = a.xch + NMOE_XCH_LOGITS;
-    uint64_t *xact = a.xch + NMOE_XCH_ACT + NMOE_XCH_SP * g * NMOE_INTER;
+    uint64_t *xact = a.xch + NMOE_XCH_ACT + NMOE_XCH_ASP * g * NMOE_INTER;
     uint64_t *ypart = a.xch + NMOE_XCH_YPART;
 
     /* Independent loads go out first and unconditionally (loads retire in
@@ -243,6 +289,7 @@ __global__ void __launch_bounds__(NMOE_FUSED_THREADS) nmoe_fused_decode_kernel(n
     const int crow = j * NMOE_FUSED_CHUNK + (tid & (NMOE_FUSED_CHUNK - 1));
     const float hm = a.h_mid[crow];
     const float sh = a.shared_out != NULL ? a.shared_out[crow] : 0.0f;
+    const float sgr = a.shared_out != NULL ? a.shared_gate_raw[0] : 0.0f;
     uint4 wv[4];
     uint32_t wq[4];
     uint16_t rsr[4], rbr[4];
@@ -269,6 +316,7 @@ __global__ void __launch_bounds__(NMOE_FUSED_THREADS) nmoe_fused_decode_kernel(n
             for (int q = 0; q < 4; q++) nmoe_x_cols<XMODE>(a.x, (lane + 64 * q) * 8, 8, 1.0, xs_r + 8 * q);
     }
     if (tid < 32) s_tab[tid] = tab_v;
+    if (tid < NMOE_MAX_K) s_cand[tid] = 0u;
     if (tid == 0) {
         __hip_atomic_store(ep, ep_old + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         s_epoch = ep_old + 1u;
@@ -320,68 +368,157 @@ __global__ void __launch_bounds__(NMOE_FUSED_THREADS) nmoe_fused_decode_kernel(n
 #pragma unroll
             for (int q = 0; q < 4; q++) s_lg[lane + 64 * q] = lv[q];
             if (lane == 0) __hip_atomic_store(&s_lgok, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
-            uint32_t key[4], cand[NMOE_MAX_K], ck[NMOE_MAX_K];
+            /* one wave maximum per round: the key's top 24 bits with the
+             * complemented entry below make every key distinct and name
+             * its entry (logits that agree in those bits go lowest entry
+             * first; the exact routing corrects that where it matters).
+             * Each lane keeps its four keys sorted, so a round reduces one
+             * value and the winning lane shifts its next key up. */
+            uint32_t key[4];
 #pragma unroll
-            for (int q = 0; q < 4; q++) key[q] = nmoe_fkey(lv[q]);
-            nmoe_wave_top_keys(key, k, cand, ck, [&](int s, uint32_t e) {
-                if (lane == 0) {
-                    s_cand[s] = e;
-                    __hip_atomic_store(&s_ncand, (uint32_t)(s + 1), __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+            for (int q = 0; q < 4; q++) key[q] = (nmoe_fkey(lv[q]) & 0xffffff00u) | (uint32_t)(255 - lane - 64 * q);
+            {
+                const uint32_t a0 = max(key[0], key[1]), b0 = min(key[0], key[1]);
+                const uint32_t a1 = max(key[2], key[3]), b1 = min(key[2], key[3]);
+                const uint32_t x = min(a0, a1), y = max(b0, b1);
+                key[0] = max(a0, a1);
+                key[1] = max(x, y);
+                key[2] = min(x, y);
+                key[3] = min(b0, b1);
+            }
+#pragma unroll
+            for (int s = 0; s < NMOE_MAX_K; s++) {
+                if (s < k) {
+                    const uint32_t best = nmoe_wave_max_u32(key[0]);
+                    if (lane == 0)
+                        __hip_atomic_store(&s_cand[s], 256u - (best & 255u), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+                    if (key[0] == best) {
+                        key[0] = key[1];
+                        key[1] = key[2];
+                        key[2] = key[3];
+                        key[3] = 0u;
+                    }
                 }
-            });
+            }
+            if (lane == 0) __hip_atomic_store(&s_ncand, (uint32_t)k, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
         }
     }
     if (ROUTE && wave == NMOE_FUSED_EXACT && g < k) {
         /* ---- exact routing (math.m softmax / top-k / renormalise), from
          * the moment the logits are in, alongside the candidate rounds and
-         * the expert loads; then the expert of each group: a candidate
-         * outside the exact selection (only possible on probability ties)
-         * hands its group to a selected expert no group holds yet */
+         * the expert loads; then the expert of each group. */
         __builtin_amdgcn_s_setprio(2);
         nmoe_lds_wait_above(&s_lgok, 0u, status);
-        uint32_t si[NMOE_MAX_K], cand[NMOE_MAX_K];
-        float sw[NMOE_MAX_K];
-        nmoe_wave_route(s_lg, NMOE_EXPERTS, k, s_scratch, s_tab, si, sw, NULL);
+        float l[4], p[4];
+#pragma unroll
+        for (int q = 0; q < 4; q++) l[q] = s_lg[lane + 64 * q];
+        nmoe_wave_softmax(l, NMOE_EXPERTS, s_scratch, s_tab, p);
+#pragma unroll
+        for (int q = 0; q < 4; q++) s_scratch[lane + 64 * q] = p[q];
         nmoe_lds_wait_above(&s_ncand, (uint32_t)(k - 1), status);
+        /* lane s < k: group s's candidate and its probability.  With p8 the
+         * smallest of these, math.m's top-k is {p > p8} plus the lowest
+         * entries with p == p8, since p8 is at most the k-th largest
+         * probability and equal to it once fewer than k exceed it; when
+         * every p > p8 and every p == p8 belongs to a candidate, the top-k
+         * is the candidate set, each group keeps its expert and only the
+         * slot order (probability, ties to the lower entry) is left. */
+        const bool mine = lane < k;
+        const uint32_t c = mine ? s_cand[lane] - 1u : 0u;
+        const uint32_t pcb = mine ? __float_as_uint(s_scratch[c]) : 0xffffffffu; /* p >= 0: bits order like values */
+        uint32_t p8 = 0xffffffffu;
 #pragma unroll
-        for (int s = 0; s < NMOE_MAX_K; s++) cand[s] = s < k ? s_cand[s] : 0u;
-        uint32_t ct = 0, et = 0;
-        float wt = 0.0f;
-        bool c_in_e = false, e_in_c = false;
+        for (int t = 0; t < NMOE_MAX_K; t++)
+            if (t < k) p8 = min(p8, (uint32_t)__builtin_amdgcn_readlane((int)pcb, t));
+        int ngt = 0, neq = 0;
 #pragma unroll
-        for (int s = 0; s < NMOE_MAX_K; s++) {
-            if (s == lane) {
-                ct = cand[s];
-                et = si[s];
-                wt = sw[s];
+        for (int q = 0; q < 4; q++) {
+            ngt += __popcll(__ballot(__float_as_uint(p[q]) > p8));
+            neq += __popcll(__ballot(__float_as_uint(p[q]) == p8));
+        }
+        const int cgt = __popcll(__ballot(mine && pcb > p8)), ceq = __popcll(__ballot(mine && pcb == p8));
+        if (ngt == cgt && neq == ceq) {
+            int slot = 0;
+#pragma unroll
+            for (int t = 0; t < NMOE_MAX_K; t++) {
+                if (t < k) {
+                    const uint32_t pt = (uint32_t)__builtin_amdgcn_readlane((int)pcb, t);
+                    const uint32_t ct = (uint32_t)__builtin_amdgcn_readlane((int)c, t);
+                    slot += (pt > pcb || (pt == pcb && ct < c)) ? 1 : 0;
+                }
             }
-        }
-#pragma unroll
-        for (int s = 0; s < NMOE_MAX_K; s++) {
-            if (s < k) {
-                c_in_e = c_in_e || ct == si[s];
-                e_in_c = e_in_c || et == cand[s];
+            if (mine) {
+                s_gx[lane] = c;
+                s_slotg[slot] = (uint32_t)lane;
+                s_t[slot] = c;
+                s_t[NMOE_MAX_K + slot] = pcb;
+            } else if (lane < NMOE_MAX_K) {
+                s_t[lane] = 0u; /* unused slots: entry 0, weight 0 */
             }
-        }
-        const uint64_t fm = __ballot(lane < k && !c_in_e); /* groups to re-point */
-        const uint64_t mm = __ballot(lane < k && !e_in_c); /* slots no group holds */
-        uint32_t xg = ct;
-        if (fm != 0) {
-            const int fr = (int)__builtin_popcountll(fm & ((1ull << lane) - 1ull));
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+            /* math.m:134-153 in slot order */
+            const float pq = mine ? __uint_as_float(s_t[NMOE_MAX_K + lane]) : 0.0f;
+            float sum = 0.0f;
 #pragma unroll
-            for (int s = 0; s < NMOE_MAX_K; s++)
-                if (((mm >> s) & 1) && (int)__builtin_popcountll(mm & ((1ull << s) - 1ull)) == fr && ((fm >> lane) & 1))
-                    xg = si[s];
-        }
-        uint32_t sg = 0;
+            for (int q = 0; q < NMOE_MAX_K; q++)
+                if (q < k) sum += __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)__float_as_uint(pq), q));
+            const float rinv = sum == 0.0f ? 1.0f / (float)k : 1.0f / sum;
+            if (lane < NMOE_MAX_K) s_w[lane] = mine ? (sum == 0.0f ? rinv : pq * rinv) : 0.0f;
+        } else {
+            /* ties at the boundary (or candidates cut short by their 24-bit
+             * keys): the full selection; a candidate outside it hands its
+             * group to a selected expert no group holds yet */
+            uint32_t si[NMOE_MAX_K], cand[NMOE_MAX_K], key[4], selkey[NMOE_MAX_K];
+            float sw[NMOE_MAX_K], sel_v[NMOE_MAX_K];
 #pragma unroll
-        for (int q = 0; q < NMOE_MAX_K; q++)
-            if (q < k && (uint32_t)__builtin_amdgcn_readlane((int)xg, q) == et) sg = (uint32_t)q;
-        if (lane < NMOE_MAX_K) {
-            s_gx[lane] = xg;
-            s_slotg[lane] = sg;
-            s_w[lane] = wt;
-            s_t[lane] = et; /* written out at the end */
+            for (int q = 0; q < 4; q++) key[q] = __float_as_uint(p[q]) + 1u;
+            nmoe_wave_top_keys(key, k, si, selkey);
+#pragma unroll
+            for (int q = 0; q < NMOE_MAX_K; q++) sel_v[q] = q < k ? __uint_as_float(selkey[q] - 1u) : 0.0f;
+            nmoe_renormalize(sel_v, k, sw);
+#pragma unroll
+            for (int q = 0; q < NMOE_MAX_K; q++) cand[q] = (uint32_t)__builtin_amdgcn_readlane((int)c, q);
+            uint32_t ct = 0, et = 0;
+            float wt = 0.0f;
+            bool c_in_e = false, e_in_c = false;
+#pragma unroll
+            for (int q = 0; q < NMOE_MAX_K; q++) {
+                if (q == lane) {
+                    ct = cand[q];
+                    et = si[q];
+                    wt = sw[q];
+                }
+            }
+#pragma unroll
+            for (int q = 0; q < NMOE_MAX_K; q++) {
+                if (q < k) {
+                    c_in_e = c_in_e || ct == si[q];
+                    e_in_c = e_in_c || et == cand[q];
+                }
+            }
+            const uint64_t fm = __ballot(lane < k && !c_in_e); /* groups to re-point */
+            const uint64_t mm = __ballot(lane < k && !e_in_c); /* slots no group holds */
+            uint32_t xg = ct;
+            if (fm != 0) {
+                const int fr = (int)__builtin_popcountll(fm & ((1ull << lane) - 1ull));
+#pragma unroll
+                for (int q = 0; q < NMOE_MAX_K; q++)
+                    if (((mm >> q) & 1) && (int)__builtin_popcountll(mm & ((1ull << q) - 1ull)) == fr &&
+                        ((fm >> lane) & 1))
+                        xg = si[q];
+            }
+            uint32_t sg = 0;
+#pragma unroll
+            for (int q = 0; q < NMOE_MAX_K; q++)
+                if (q < k && (uint32_t)__builtin_amdgcn_readlane((int)xg, q) == et) sg = (uint32_t)q;
+            if (lane < NMOE_MAX_K) {
+                s_gx[lane] = xg;
+                s_slotg[lane] = sg;
+                s_w[lane] = wt;
+                s_t[lane] = et; /* written out at the end */
+            }
         }
         if (lane == 0) __hip_atomic_store(&s_confirm, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
     }
@@ -392,7 +529,7 @@ __global__ void __launch_bounds__(NMOE_FUSED_THREADS) nmoe_fused_decode_kernel(n
             /* an index outside the layer is an invalid slot: weight 0, as
              * for a failed expert read (runtime.m:2977-2981) */
             s_w[tid] = e < NMOE_EXPERTS ? wv_in : 0.0f;
-            s_cand[tid] = e < NMOE_EXPERTS ? e : 0u;
+            s_cand[tid] = e < NMOE_EXPERTS ? e + 1u : 1u;
             s_gx[tid] = e < NMOE_EXPERTS ? e : 0u;
             s_slotg[tid] = tid;
         }
@@ -444,8 +581,8 @@ __global__ void __launch_bounds__(NMOE_FUSED_THREADS) nmoe_fused_decode_kernel(n
 #pragma unroll
             for (int c = 0; c < XV; c++) xr[c] = xp[c];
         if (ROUTE) /* candidate g published by the control wavefront */
-            nmoe_lds_wait_above(&s_ncand, (uint32_t)g, status);
-        cand_g = s_cand[g];
+            nmoe_lds_wait_above(&s_cand[g], 0u, status);
+        cand_g = s_cand[g] - 1u;
         __builtin_amdgcn_sched_barrier(0);
         load_expert(cand_g);
         /* keep every weight load above in one burst: no compute hoisted into it */
@@ -496,9 +633,9 @@ __global__ void __launch_bounds__(NMOE_FUSED_THREADS) nmoe_fused_decode_kernel(n
 #pragma unroll
             for (int i = 0; i < GSTEPS; i++) {
                 if (a.xcd_local)
-                    nmoe_st_tagged_die(xact + NMOE_XCH_SP * (grow0 + i * RPS), epoch, actv[i]);
+                    nmoe_st_tagged_die(xact + NMOE_XCH_ASP * (grow0 + i * RPS), epoch, actv[i]);
                 else
-                    nmoe_st_tagged(xact + NMOE_XCH_SP * (grow0 + i * RPS), epoch, actv[i]);
+                    nmoe_st_tagged(xact + NMOE_XCH_ASP * (grow0 + i * RPS), epoch, actv[i]);
             }
         }
     }
@@ -509,7 +646,7 @@ __global__ void __launch_bounds__(NMOE_FUSED_THREADS) nmoe_fused_decode_kernel(n
         const uint64_t *pa[APT];
         float av[APT];
 #pragma unroll
-        for (int q = 0; q < APT; q++) pa[q] = xact + NMOE_XCH_SP * (tid + 64 * NMOE_FUSED_WORKERS * q);
+        for (int q = 0; q < APT; q++) pa[q] = xact + NMOE_XCH_ASP * (tid + 64 * NMOE_FUSED_WORKERS * q);
         nmoe_poll<APT>(pa, epoch, av, status, a.xcd_local != 0);
 #pragma unroll
         for (int q = 0; q < APT; q++) s_act[nmoe_act_slot<Q::CPL / 4>(tid + 64 * NMOE_FUSED_WORKERS * q)] = av[q];
@@ -553,22 +690,40 @@ __global__ void __launch_bounds__(NMOE_FUSED_THREADS) nmoe_fused_decode_kernel(n
                 pp[q] = ypart + q * NMOE_HIDDEN + row;
                 ys[q] = s_y[tid];
             }
-            nmoe_poll<NMOE_MAX_K>(pp, epoch, ys, status, false, ((1u << k) - 1u) & ~(1u << g));
-            /* slot order: slot s is streamed by group s_slotg[s] */
-            float moe = 0.0f;
+            /* everything but the partials before the wait: slot s's weight
+             * and the group that streams it (usually group s), the shared
+             * expert's gate */
+            float wsl[NMOE_MAX_K];
+            uint32_t sgl[NMOE_MAX_K];
+            bool ident = true;
 #pragma unroll
             for (int s = 0; s < NMOE_MAX_K; s++) {
-                if (s < k) {
-                    const uint32_t sg = s_slotg[s];
-                    float y = ys[0];
+                wsl[s] = s < k ? s_w[s] : 0.0f;
+                sgl[s] = s < k ? s_slotg[s] : (uint32_t)s;
+                ident = ident && sgl[s] == (uint32_t)s;
+            }
+            const float gsig = a.shared_out != NULL ? nmoe_sigmoid_dev(sgr) : 0.0f;
+            nmoe_poll2<NMOE_MAX_K>(pp, epoch, ys, status, ((1u << k) - 1u) & ~(1u << g));
+            /* slot order: slot s is streamed by group sgl[s] */
+            float moe = 0.0f;
+            if (ident) {
 #pragma unroll
-                    for (int q = 1; q < NMOE_MAX_K; q++)
-                        if (sg == (uint32_t)q) y = ys[q];
-                    moe += s_w[s] * y;
+                for (int s = 0; s < NMOE_MAX_K; s++)
+                    if (s < k) moe += wsl[s] * ys[s];
+            } else {
+#pragma unroll
+                for (int s = 0; s < NMOE_MAX_K; s++) {
+                    if (s < k) {
+                        float y = ys[0];
+#pragma unroll
+                        for (int q = 1; q < NMOE_MAX_K; q++)
+                            if (sgl[s] == (uint32_t)q) y = ys[q];
+                        moe += wsl[s] * y;
+                    }
                 }
             }
             float r = hm + moe;
-            if (a.shared_out != NULL) r = r + nmoe_sigmoid_dev(a.shared_gate_raw[0]) * sh;
+            if (a.shared_out != NULL) r = r + gsig * sh;
             a.out[row] = r;
         }
     }
