@@ -640,6 +640,14 @@ __global__ void __launch_bounds__(NMOE_FUSED_THREADS) nmoe_fused_decode_kernel(n
         }
     }
 
+    /* q4: the down codes as floats while the act is in flight, so that D is
+     * multiply-adds only (q2 has no registers to spare for this) */
+    constexpr bool DPRE = BITS == 4;
+    float dwf[DPRE ? DSTEPS : 1][DPRE ? Q::CPL : 1];
+    if (DPRE && !ctrl)
+#pragma unroll
+        for (int i = 0; i < DSTEPS; i++) nmoe_unpack_q4(dwv[i], dwf[i]);
+
     /* ---- D (workers): wait for act[g], then y_g for rows 64j..64j+63 */
     if (!ctrl) {
         constexpr int APT = NMOE_INTER / (64 * NMOE_FUSED_WORKERS); /* act words per worker thread */
@@ -668,7 +676,8 @@ __global__ void __launch_bounds__(NMOE_FUSED_THREADS) nmoe_fused_decode_kernel(n
         for (int c = 0; c < Q::CPL; c++) asum += as[c];
 #pragma unroll
         for (int i = 0; i < DSTEPS; i++) {
-            float y = __builtin_fmaf(nmoe_bf16f(dsc[i]), nmoe_dot16<BITS>(dwv[i], as), nmoe_bf16f(dbi[i]) * asum);
+            const float dot = DPRE ? nmoe_dot_f4(dwf[i], as) : nmoe_dot16<BITS>(dwv[i], as);
+            float y = __builtin_fmaf(nmoe_bf16f(dsc[i]), dot, nmoe_bf16f(dbi[i]) * asum);
             y = nmoe_dpp_group_sum<Q::LPR_D>(y);
             if (dl == 0) s_y[(NMOE_FUSED_CHUNK / NMOE_FUSED_WORKERS) * wave + dsub + i * RPW_D] = y;
         }

@@ -151,6 +151,34 @@ __device__ __forceinline__ float nmoe_dot16<4>(uint4 q, const float *xs) {
     return a0 + a1;
 }
 
+/* The 32 q4 codes of `q` as floats, in the element order nmoe_dot16<4>
+ * uses, and the same dot product over such floats: nmoe_dot_f4(w, xs) with
+ * nmoe_unpack_q4(q, w) equals nmoe_dot16<4>(q, xs) bit for bit. */
+__device__ __forceinline__ void nmoe_unpack_q4(uint4 q, float *w) {
+    const uint32_t u[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const uint32_t lo = u[i] & 0x0F0F0F0Fu, hi = (u[i] >> 4) & 0x0F0F0F0Fu;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            w[8 * i + 2 * j] = (float)((lo >> (8 * j)) & 0xFFu);
+            w[8 * i + 2 * j + 1] = (float)((hi >> (8 * j)) & 0xFFu);
+        }
+    }
+}
+__device__ __forceinline__ float nmoe_dot_f4(const float *w, const float *xs) {
+    float a0 = 0.0f, a1 = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            a0 = __builtin_fmaf(w[8 * i + 2 * j], xs[8 * i + 2 * j], a0);
+            a1 = __builtin_fmaf(w[8 * i + 2 * j + 1], xs[8 * i + 2 * j + 1], a1);
+        }
+    }
+    return a0 + a1;
+}
+
 template <>
 __device__ __forceinline__ float nmoe_dot16<2>(uint4 q, const float *xs) {
     const uint32_t w[4] = {q.x, q.y, q.z, q.w};
