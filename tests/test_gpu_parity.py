@@ -417,6 +417,52 @@ def test_fused_probability_tie_at_boundary(ctx, nh, bits, k):
     assert_close(out.download(np.float32, 2048), want, what="tie at boundary")
 
 
+def _near_tie_router(k):
+    """Router rows and x whose logits put two entries a few ulps apart on the
+    top-k boundary, the higher one at the higher index: k-1 experts at logit
+    1, expert 3 at 0.5 and expert 200 at 0.5 + 2^-22 (everything else -1).
+    The two agree in their top 24 key bits, so a selection on those bits
+    prefers the lower entry 3, while their probabilities differ and math.m's
+    top-k takes 200."""
+    W = np.zeros((256, 2048), np.float32)
+    W[:, 0] = -1.0
+    top = [50 + 10 * i for i in range(k - 1)]
+    W[top, 0] = 1.0
+    W[3, 0] = 0.5
+    W[200, 0] = 0.5
+    W[200, 1] = 0.25
+    x = np.zeros(2048, np.float32)
+    x[0], x[1] = 1.0, 2.0 ** -20
+    Wb = B.f32_to_bf16(W.ravel()).reshape(256, 2048)
+    return Wb, x, top
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("bits,k", [(4, 8), (2, 6)])
+def test_fused_near_tie_candidate_corrected(ctx, nh, bits, k):
+    """The fused kernel's early candidates compare logits on their top 24
+    key bits; when that picks the wrong one of two near-equal boundary
+    logits, the exact routing must re-point the group to math.m's expert,
+    with math.m's slot order, weights and output."""
+    seed, layer = 43, 61
+    Wb, x, top = _near_tie_router(k)
+    lg = B.router_logits_bf16(Wb, x)
+    key = lambda f: int(np.float32(f).view(np.uint32)) | 0x80000000  # positive logits
+    assert lg[200] > lg[3] and key(lg[200]) >> 8 == key(lg[3]) >> 8  # the construction holds
+    oi, ow, _ = B.route(lg, k)
+    assert 200 in oi[:k] and 3 not in oi[:k]
+    ctx.synth_layer(layer, bits, seed, SIGMA[bits])
+    rng = np.random.default_rng(6)
+    h = rng.standard_normal(2048).astype(np.float32)
+    want = B.moe_experts(host_pack(bits, seed, layer, oi[:k]), bits, x[None], k, oi[None], ow[None], h[None])[0]
+    out, di, dw = ctx.alloc(8192), ctx.alloc(32), ctx.alloc(32)
+    ctx._check(ctx.moe_layer(layer, ctx.router_bf16(ctx.to_device(Wb)), ctx.to_device(x), nh.F32, 1, k,
+                             ctx.to_device(h), out, di, dw))
+    np.testing.assert_array_equal(di.download(np.uint32, 8)[:k], oi[:k])
+    np.testing.assert_array_equal(dw.download(np.float32, 8)[:k].view(np.uint32), ow[:k].view(np.uint32))
+    assert_close(out.download(np.float32, 2048), want, what="near tie at boundary")
+
+
 @pytest.mark.gpu
 def test_xcd_placement_and_die_local_exchange(ctx, nh):
     """MI355X deals a launch's blocks round-robin over its 8 dies (checked at
