@@ -260,12 +260,26 @@ struct nmoe_stage {
     uint32_t b[CW];
 };
 
-/* Instruction j (rows 8j..8j+7) of one A plane: src_row is this lane's row
- * (8j + lane / 8) pointer at the group's first column. */
-__device__ __forceinline__ void nmoe_stage_rows(uint4 *plane, const uint16_t *src_row, int j, int lane) {
+/* A direct load into LDS from a wavefront-uniform base plus a 32-bit
+ * per-lane byte offset: the compiler can address it as a scalar base and a
+ * vector offset, so the stages' per-group addresses cost no vector
+ * registers (the group moves the scalar base). */
+template <int SZ>
+__device__ __forceinline__ void nmoe_dma(const void *ubase, uint32_t off, void *lds) {
+    const void *src = (const void *)((const char *)ubase + off);
+    if constexpr (SZ == 16)
+        __builtin_amdgcn_global_load_lds(src, (nmoe_lds_void *)lds, 16, 0, 0);
+    else
+        __builtin_amdgcn_global_load_lds(src, (nmoe_lds_void *)lds, 4, 0, 0);
+}
+
+/* Instruction j (rows 8j..8j+7) of one A plane: ubase is the plane at the
+ * group's first column (uniform), row_off this lane's row (8j + lane / 8)
+ * in bytes. */
+__device__ __forceinline__ void nmoe_stage_rows(uint4 *plane, const uint16_t *ubase, uint32_t row_off, int j, int lane) {
     const int r = 8 * j + (lane >> 3);
     const int c = (lane & 7) ^ ((r >> 1) & 7);
-    __builtin_amdgcn_global_load_lds((const void *)(src_row + 8 * c), (nmoe_lds_void *)(plane + 64 * j), 16, 0, 0);
+    nmoe_dma<16>(ubase, row_off + 16u * (uint32_t)c, plane + 64 * j);
 }
 
 /* MFMA A operand (the lane's two 8-element chunks 2kb, 2kb+1) of row r. */
@@ -290,25 +304,26 @@ struct nmoe_code_plan {
     static_assert(WIDE || BITS == 2, "q4 stages are at least 8 KB");
 };
 
-/* Instruction j of the codes of group g for one matrix of NR rows (global
- * rows base + row * wpr words), in the stage layout above. */
+/* Words of group g from a row's first word: 8 (q4) or 4 (q2). */
+template <int BITS>
+__host__ __device__ constexpr int nmoe_gwords() { return BITS == 4 ? 8 : 4; }
+
+/* Instruction j of one group's codes for one matrix of NR rows, in the
+ * stage layout above: gbase is the matrix's first row at the group's first
+ * word (uniform), rows wpr words apart. */
 template <int BITS, int NR, bool WIDE>
-__device__ __forceinline__ void nmoe_stage_codes(uint32_t *stage, const uint32_t *base, int wpr, int g, int j,
-                                                 int lane) {
+__device__ __forceinline__ void nmoe_stage_codes(uint32_t *stage, const uint32_t *gbase, int wpr, int j, int lane) {
     if (BITS == 4) {
         /* rows 32j + lane / 2, half (lane % 2) ^ row bit 3 */
         const int row = 32 * j + (lane >> 1), half = (lane & 1) ^ ((row >> 3) & 1);
-        __builtin_amdgcn_global_load_lds((const void *)(base + (size_t)row * wpr + 8 * g + 4 * half),
-                                         (nmoe_lds_void *)(stage + 256 * j), 16, 0, 0);
+        nmoe_dma<16>(gbase, 4u * (uint32_t)(row * wpr + 4 * half), stage + 256 * j);
     } else if (WIDE) {
         const int row = 64 * j + lane;
-        __builtin_amdgcn_global_load_lds((const void *)(base + (size_t)row * wpr + 4 * g),
-                                         (nmoe_lds_void *)(stage + 256 * j), 16, 0, 0);
+        nmoe_dma<16>(gbase, 4u * (uint32_t)(row * wpr), stage + 256 * j);
     } else {
         /* rows 16j + lane / 4, word lane % 4 */
         const int row = 16 * j + (lane >> 2);
-        __builtin_amdgcn_global_load_lds((const void *)(base + (size_t)row * wpr + 4 * g + (lane & 3)),
-                                         (nmoe_lds_void *)(stage + 64 * j), 4, 0, 0);
+        nmoe_dma<4>(gbase, 4u * (uint32_t)(row * wpr + (lane & 3)), stage + 64 * j);
     }
 }
 
@@ -339,37 +354,50 @@ __device__ __forceinline__ void nmoe_ring_barrier() {
     asm volatile("s_barrier" ::: "memory");
 }
 
-/* The barrier before group g of G, for a wavefront that issues L loads per
- * group: groups g+1 and g+2 may still be in flight. */
-template <int L, int G>
+/* The barrier before group g of G in a ring of NS stages, for a wavefront
+ * that issues L loads per group: groups g+1 .. g+NS-2 (those that exist)
+ * may still be in flight.  (K: the groups allowed in flight, tried from
+ * NS-2 down.) */
+template <int L, int G, int NS, int K = NS - 2>
 __device__ __forceinline__ void nmoe_ring_step_barrier(int g) {
-    if (g + 2 < G)
-        nmoe_ring_barrier<2 * L>();
-    else if (g + 1 < G)
-        nmoe_ring_barrier<L>();
-    else
+    if constexpr (K == 0) {
         nmoe_ring_barrier<0>();
+    } else {
+        if (g + K < G)
+            nmoe_ring_barrier<K * L>();
+        else
+            nmoe_ring_step_barrier<L, G, NS, K - 1>(g);
+    }
 }
 
-/* Runs step(g, stage, issue_ahead) over the G groups: the loop body issues
- * group g + NS - 1 unconditionally (a load issued under a runtime condition
- * makes the compiler wait for every stage), the last NS - 1 steps issue
- * nothing. */
-template <int G, typename Step>
-__device__ __forceinline__ void nmoe_ring_run(Step step) {
-    static_assert(G % NMOE_NS == 0, "whole ring turns");
-    constexpr int MAIN = G - NMOE_NS; /* steps in the loop */
-#pragma unroll 1
-    for (int g = 0; g < MAIN; g += NMOE_NS) {
-        step(g, 0, true);
-        step(g + 1, 1, true);
-        step(g + 2, 2, true);
-        step(g + 3, 3, true);
+template <int I, int NS, typename Step>
+__device__ __forceinline__ void nmoe_ring_turn(Step &step, int g) {
+    if constexpr (I < NS) {
+        step(g + I, I, true);
+        nmoe_ring_turn<I + 1, NS>(step, g);
     }
-    step(MAIN, 0, true);
-    step(MAIN + 1, 1, false);
-    step(MAIN + 2, 2, false);
-    step(MAIN + 3, 3, false);
+}
+
+template <int G0, int G, int NS, int ISSUE, typename Step>
+__device__ __forceinline__ void nmoe_ring_tail(Step &step) {
+    if constexpr (G0 < G) {
+        step(G0, G0 % NS, G0 < ISSUE);
+        nmoe_ring_tail<G0 + 1, G, NS, ISSUE>(step);
+    }
+}
+
+/* Runs step(g, stage, issue_ahead) over the G groups with NS stages: step g
+ * issues group g + NS - 1 while it exists.  The loop's steps all issue,
+ * unconditionally (a load issued under a runtime condition makes the
+ * compiler wait for every stage); the remaining steps are unrolled with
+ * their stage and issue flag known at compile time. */
+template <int G, int NS, typename Step>
+__device__ __forceinline__ void nmoe_ring_run(Step step) {
+    constexpr int ISSUE = G - NS + 1;          /* steps that issue a later group */
+    constexpr int MAIN = (ISSUE / NS) * NS;    /* steps in the loop, whole ring turns */
+#pragma unroll 1
+    for (int g = 0; g < MAIN; g += NS) nmoe_ring_turn<0, NS>(step, g);
+    nmoe_ring_tail<MAIN, G, NS, ISSUE>(step);
 }
 
 /* Workgroup barrier over LDS only: waits for this wavefront's LDS accesses
@@ -434,6 +462,7 @@ nmoe_grouped_gateup_kernel(const uint8_t *pack, const uint16_t *xhi, const uint1
     using CP = nmoe_code_plan<BITS, 2 * NT>;
     constexpr int CPM = CP::BYTES / 2 / CP::INS_BYTES; /* code instructions per matrix */
     __shared__ uint16_t s_s[2][NT][G];          /* gate and up scales of the tile */
+    constexpr int NS = NMOE_NS; /* (five stages measured no faster) */
     typedef nmoe_stage<XPL, 2 * NT * WPG> Stage;
     __shared__ Stage s_st0, s_st1, s_st2, s_st3;
     auto stage = [&](int st) -> Stage & { return st == 0 ? s_st0 : st == 1 ? s_st1 : st == 2 ? s_st2 : s_st3; };
@@ -460,39 +489,36 @@ nmoe_grouped_gateup_kernel(const uint8_t *pack, const uint16_t *xhi, const uint1
         const int nb = (int)min((n - m0 + 15) / 16, 4u);
         /* this lane's A row for instruction `wave`: entry 8 wave + lane / 8 */
         const uint32_t tsrc = s_tok[8 * wave + (lane >> 3)];
-        const uint16_t *srow[XPL];
-        srow[0] = xhi + (size_t)tsrc * NMOE_HIDDEN;
-        if (XPL == 2) srow[XPL - 1] = xlo + (size_t)tsrc * NMOE_HIDDEN;
+        const uint16_t *xpl[2] = {xhi, xlo};
+        const uint32_t row_off = tsrc * (uint32_t)(NMOE_HIDDEN * 2);
         auto issue = [&](int g, int st) {
 #pragma unroll
-            for (int pl = 0; pl < XPL; pl++) nmoe_stage_rows(stage(st).a[pl], srow[pl] + 64 * g, wave, lane);
+            for (int pl = 0; pl < XPL; pl++) nmoe_stage_rows(stage(st).a[pl], xpl[pl] + 64 * g, row_off, wave, lane);
 #pragma unroll
             for (int i = 0; i < CP::PER_WAVE; i++)
-                nmoe_stage_codes<BITS, NT, CP::WIDE>(stage(st).b + cmat * NT * WPG, cbase, Q::WPR_G, g,
-                                                     (CP::PER_WAVE * wave + i) % CPM, lane);
+                nmoe_stage_codes<BITS, NT, CP::WIDE>(stage(st).b + cmat * NT * WPG, cbase + nmoe_gwords<BITS>() * g,
+                                                     Q::WPR_G, (CP::PER_WAVE * wave + i) % CPM, lane);
         };
-        /* the first stages go out before the correction's loads, so their
-         * latency overlaps it */
-#pragma unroll
-        for (int st = 0; st < NMOE_NS - 1; st++) issue(st, st);
         nmoe_f32x4 acc[2][NB][4];
         {
-            /* the tile's scales (first pass only) */
-            if (m0 == 0) {
-                constexpr int PER = 2 * NT * G / 8 / 512;
-                uint4 v[PER];
+            /* The correction's operands go out first and the first ring
+             * stages right after them: loads retire in order, so the small
+             * loads then return without waiting for the stages, and the
+             * correction's MFMAs run while the stages stream in.
+             * The tile's scales (first pass only); A lane = (entry col,
+             * groups 8kb + tq), B lane = (row col, groups 8kb + tq): a lane's
+             * eight groups are contiguous (two 16-byte loads of xs, one of
+             * the biases). */
+            constexpr int PER = 2 * NT * G / 8 / 512;
+            /* scales straight into LDS, every pass (later passes hit L2):
+             * wavefront w's q-th 1 KB at uint4 512q + 64w */
 #pragma unroll
-                for (int q = 0; q < PER; q++) {
-                    const int i = tid + 512 * q, mat = i / (NT * G / 8), j = i % (NT * G / 8);
-                    v[q] = ((const uint4 *)(ex + (mat == 0 ? L::gate_s : L::up_s) + (size_t)nt * NT * G * 2))[j];
-                }
-#pragma unroll
-                for (int q = 0; q < PER; q++) ((uint4 *)&s_s[0][0][0])[tid + 512 * q] = v[q];
+            for (int q = 0; q < PER; q++) {
+                const int i = tid + 512 * q, mat = i / (NT * G / 8), j = i % (NT * G / 8);
+                const uint4 *src = (const uint4 *)(ex + (mat == 0 ? L::gate_s : L::up_s) + (size_t)nt * NT * G * 2) + j;
+                __builtin_amdgcn_global_load_lds((const void *)src,
+                                                 (nmoe_lds_void *)((uint4 *)&s_s[0][0][0] + 512 * q + 64 * wave), 16, 0, 0);
             }
-            /* all operand loads first (one memory round trip), then the MFMAs:
-             * A lane = (entry col, groups 8kb + tq), B lane = (row col, groups
-             * 8kb + tq): a lane's eight groups are contiguous (two 16-byte
-             * loads of xs, one of the biases) */
             float4 xv4[4][2];
             uint4 bv[2][NB];
 #pragma unroll
@@ -506,36 +532,48 @@ nmoe_grouped_gateup_kernel(const uint8_t *pack, const uint16_t *xhi, const uint1
 #pragma unroll
                 for (int b2 = 0; b2 < NB; b2++)
                     bv[mat][b2] = *(const uint4 *)(bias[mat] + (rt0 + 16 * b2) * G + 8 * kb);
-            __syncthreads(); /* the scales */
+#pragma unroll
+            for (int st = 0; st < NS - 1; st++) issue(st, st);
+            /* scales, xs and biases have landed once only the stages' loads
+             * are in flight; then every wavefront's scales are in LDS */
+            nmoe_wait_vm<(NS - 1) * (XPL + CP::PER_WAVE)>();
+            nmoe_lds_barrier();
             float xv[4][G / 4];
 #pragma unroll
             for (int mb = 0; mb < 4; mb++) {
                 xv[mb][0] = xv4[mb][0].x, xv[mb][1] = xv4[mb][0].y, xv[mb][2] = xv4[mb][0].z, xv[mb][3] = xv4[mb][0].w;
                 xv[mb][4] = xv4[mb][1].x, xv[mb][5] = xv4[mb][1].y, xv[mb][6] = xv4[mb][1].z, xv[mb][7] = xv4[mb][1].w;
             }
+            float cv[2][NB][G / 4];
 #pragma unroll
             for (int mat = 0; mat < 2; mat++)
 #pragma unroll
                 for (int b2 = 0; b2 < NB; b2++) {
-                    float cv[G / 4], bf[8], sf[8];
+                    float bf[8], sf[8];
                     nmoe_unpack_bf16x8(bv[mat][b2], bf);
                     nmoe_unpack_bf16x8(*(const uint4 *)&s_s[mat][rt0 + 16 * b2][8 * kb], sf);
 #pragma unroll
-                    for (int tq = 0; tq < G / 4; tq++) cv[tq] = bf[tq] - 128.0f * sf[tq];
+                    for (int tq = 0; tq < G / 4; tq++) cv[mat][b2][tq] = bf[tq] - 128.0f * sf[tq];
 #pragma unroll
-                    for (int mb = 0; mb < 4; mb++) {
-                        acc[mat][b2][mb] = nmoe_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-                        if (mb < nb)
-#pragma unroll
-                            for (int tq = 0; tq < G / 4; tq++)
-                                acc[mat][b2][mb] =
-                                    __builtin_amdgcn_mfma_f32_16x16x4f32(xv[mb][tq], cv[tq], acc[mat][b2][mb], 0, 0, 0);
-                    }
+                    for (int mb = 0; mb < 4; mb++) acc[mat][b2][mb] = nmoe_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
                 }
+            /* group-slice outermost: the 4 NB 4 accumulator chains interleave,
+             * so each MFMA's latency hides behind the others' */
+#pragma unroll
+            for (int tq = 0; tq < G / 4; tq++)
+#pragma unroll
+                for (int mb = 0; mb < 4; mb++)
+                    if (mb < nb)
+#pragma unroll
+                        for (int mat = 0; mat < 2; mat++)
+#pragma unroll
+                            for (int b2 = 0; b2 < NB; b2++)
+                                acc[mat][b2][mb] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[mb][tq], cv[mat][b2][tq],
+                                                                                        acc[mat][b2][mb], 0, 0, 0);
         }
         auto step = [&](int g, const int st, const bool ahead) {
-            nmoe_ring_step_barrier<XPL + CP::PER_WAVE, G>(g);
-            if (ahead) issue(g + NMOE_NS - 1, (st + NMOE_NS - 1) % NMOE_NS);
+            nmoe_ring_step_barrier<XPL + CP::PER_WAVE, G, NS>(g);
+            if (ahead) issue(g + NS - 1, (st + NS - 1) % NS);
             uint4 bq[2][NB][2];
             float sg[2][NB];
 #pragma unroll
@@ -574,7 +612,7 @@ nmoe_grouped_gateup_kernel(const uint8_t *pack, const uint16_t *xhi, const uint1
                 }
             }
         };
-        nmoe_ring_run<G>(step);
+        nmoe_ring_run<G, NS>(step);
         /* epilogue: act = SiLU(gate) * up as hi + lo bf16, in the down
          * kernel's operand order; group sums of act rows (a down group is 64
          * act columns = 512 / NT wavefronts of this tile) */
@@ -660,31 +698,35 @@ nmoe_grouped_down_kernel(const uint8_t *pack, const uint16_t *ahi, const uint16_
     const uint16_t *bias = (const uint16_t *)(ex + L::down_b) + (size_t)nt * NT * G;
     for (uint32_t m0 = 0; m0 < n; m0 += NMOE_MCHUNK) {
         const int nb = (int)min((n - m0 + 15) / 16, 4u);
-        if (tid < NMOE_MCHUNK) s_q[tid] = perm[p0 + min(m0 + tid, n - 1)]; /* visible after the barrier below */
+        /* the chunk's output slots, stored to LDS after the stages are issued
+         * (so that this load's wait does not hold them back) and visible
+         * after the barrier below */
+        const uint32_t qv = tid < NMOE_MCHUNK ? perm[p0 + min(m0 + tid, n - 1)] : 0u;
         /* this lane's A row for instruction `wave`: act row p0 + m0 + 8 wave + lane / 8 */
         const uint32_t msrc = min(m0 + 8 * wave + (lane >> 3), n - 1);
-        const uint16_t *srow[2] = {ahi + (size_t)(p0 + msrc) * NMOE_INTER, alo + (size_t)(p0 + msrc) * NMOE_INTER};
+        const uint16_t *apl[2] = {ahi, alo};
+        const uint32_t row_off = (p0 + msrc) * (uint32_t)(NMOE_INTER * 2);
         auto issue = [&](int g, int st) {
 #pragma unroll
-            for (int pl = 0; pl < 2; pl++) nmoe_stage_rows(stage(st).a[pl], srow[pl] + 64 * g, wave, lane);
+            for (int pl = 0; pl < 2; pl++) nmoe_stage_rows(stage(st).a[pl], apl[pl] + 64 * g, row_off, wave, lane);
 #pragma unroll
             for (int i = 0; i < CP::PER_WAVE; i++)
-                nmoe_stage_codes<BITS, NT, CP::WIDE>(stage(st).b, cbase, Q::WPR_D, g, CP::PER_WAVE * wave + i, lane);
+                nmoe_stage_codes<BITS, NT, CP::WIDE>(stage(st).b, cbase + nmoe_gwords<BITS>() * g, Q::WPR_D,
+                                                     CP::PER_WAVE * wave + i, lane);
         };
-        /* the first stages go out before the correction's loads */
-#pragma unroll
-        for (int st = 0; st < NMOE_NS - 1; st++) issue(st, st);
         nmoe_f32x4 acc[NB][4];
         {
-            if (m0 == 0) {
-                constexpr int PER = NT * G / 8 / 512;
-                uint4 v[PER];
+            /* as in the gate/up kernel: the correction's operands (scales
+             * straight into LDS, every pass), then the first ring stages,
+             * then a wait that leaves only the stages in flight.
+             * A lane = (entry col, groups 2kb + tq), B lane = (row col,
+             * groups 2kb + tq) */
+            constexpr int PER = NT * G / 8 / 512;
 #pragma unroll
-                for (int q = 0; q < PER; q++) v[q] = ((const uint4 *)(ex + L::down_s + (size_t)nt * NT * G * 2))[tid + 512 * q];
-#pragma unroll
-                for (int q = 0; q < PER; q++) ((uint4 *)&s_s[0][0])[tid + 512 * q] = v[q];
-            }
-            /* A lane = (entry col, groups 2kb + tq), B lane = (row col, groups 2kb + tq) */
+            for (int q = 0; q < PER; q++)
+                __builtin_amdgcn_global_load_lds(
+                    (const void *)((const uint4 *)(ex + L::down_s + (size_t)nt * NT * G * 2) + tid + 512 * q),
+                    (nmoe_lds_void *)((uint4 *)&s_s[0][0] + 512 * q + 64 * wave), 16, 0, 0);
             float2 av[4];
             uint32_t bv[NB];
 #pragma unroll
@@ -692,26 +734,32 @@ nmoe_grouped_down_kernel(const uint8_t *pack, const uint16_t *ahi, const uint16_
                 av[mb] = *(const float2 *)(as + (size_t)(p0 + min(m0 + 16 * mb + col, n - 1)) * G + 2 * kb);
 #pragma unroll
             for (int b2 = 0; b2 < NB; b2++) bv[b2] = *(const uint32_t *)(bias + (rt0 + 16 * b2) * G + 2 * kb);
-            __syncthreads(); /* the scales and s_q */
+#pragma unroll
+            for (int st = 0; st < NMOE_NS - 1; st++) issue(st, st);
+            nmoe_wait_vm<(NMOE_NS - 1) * (2 + CP::PER_WAVE)>();
+            if (tid < NMOE_MCHUNK) s_q[tid] = qv;
+            nmoe_lds_barrier(); /* the scales and s_q */
+            float cv[NB][G / 4];
 #pragma unroll
             for (int b2 = 0; b2 < NB; b2++) {
-                float cv[G / 4];
                 const uint32_t sw = *(const uint32_t *)&s_s[rt0 + 16 * b2][2 * kb];
-                cv[0] = __uint_as_float(bv[b2] << 16) - 128.0f * __uint_as_float(sw << 16);
-                cv[1] = __uint_as_float(bv[b2] & 0xffff0000u) - 128.0f * __uint_as_float(sw & 0xffff0000u);
+                cv[b2][0] = __uint_as_float(bv[b2] << 16) - 128.0f * __uint_as_float(sw << 16);
+                cv[b2][1] = __uint_as_float(bv[b2] & 0xffff0000u) - 128.0f * __uint_as_float(sw & 0xffff0000u);
 #pragma unroll
-                for (int mb = 0; mb < 4; mb++) {
-                    acc[b2][mb] = nmoe_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+                for (int mb = 0; mb < 4; mb++) acc[b2][mb] = nmoe_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            }
+#pragma unroll
+            for (int tq = 0; tq < G / 4; tq++)
+#pragma unroll
+                for (int mb = 0; mb < 4; mb++)
                     if (mb < nb)
 #pragma unroll
-                        for (int tq = 0; tq < G / 4; tq++)
-                            acc[b2][mb] = __builtin_amdgcn_mfma_f32_16x16x4f32(tq == 0 ? av[mb].x : av[mb].y, cv[tq],
-                                                                               acc[b2][mb], 0, 0, 0);
-                }
-            }
+                        for (int b2 = 0; b2 < NB; b2++)
+                            acc[b2][mb] = __builtin_amdgcn_mfma_f32_16x16x4f32(tq == 0 ? av[mb].x : av[mb].y,
+                                                                               cv[b2][tq], acc[b2][mb], 0, 0, 0);
         }
         auto step = [&](int g, const int st, const bool ahead) {
-            nmoe_ring_step_barrier<2 + CP::PER_WAVE, G>(g);
+            nmoe_ring_step_barrier<2 + CP::PER_WAVE, G, NMOE_NS>(g);
             if (ahead) issue(g + NMOE_NS - 1, (st + NMOE_NS - 1) % NMOE_NS);
             uint4 bq[NB][2];
             float sg[NB];
@@ -740,7 +788,7 @@ nmoe_grouped_down_kernel(const uint8_t *pack, const uint16_t *ahi, const uint16_
                 }
             }
         };
-        nmoe_ring_run<G>(step);
+        nmoe_ring_run<G, NMOE_NS>(step);
 #pragma unroll
         for (int b2 = 0; b2 < NB; b2++) {
             const int r = nt * NT + rt0 + 16 * b2;
