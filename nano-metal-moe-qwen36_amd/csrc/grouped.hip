@@ -461,7 +461,11 @@ nmoe_grouped_gateup_kernel(const uint8_t *pack, const uint16_t *xhi, const uint1
     constexpr int WPG = BITS == 4 ? 8 : 4;
     using CP = nmoe_code_plan<BITS, 2 * NT>;
     constexpr int CPM = CP::BYTES / 2 / CP::INS_BYTES; /* code instructions per matrix */
-    __shared__ uint16_t s_s[2][NT][G];          /* gate and up scales of the tile */
+    /* gate and up scales of the tile, chunk-major: 16-byte chunk q (groups
+     * 8q..8q+7) of row r at [mat][q][r], so a ring step's 16 rows of one
+     * group sit 16 bytes apart (distinct banks; row-major rows 64 bytes
+     * apart put four rows on each bank) */
+    __shared__ uint16_t s_s[2][G / 8][NT][8];
     constexpr int NS = NMOE_NS; /* (five stages measured no faster) */
     typedef nmoe_stage<XPL, 2 * NT * WPG> Stage;
     __shared__ Stage s_st0, s_st1, s_st2, s_st3;
@@ -514,10 +518,14 @@ nmoe_grouped_gateup_kernel(const uint8_t *pack, const uint16_t *xhi, const uint1
              * wavefront w's q-th 1 KB at uint4 512q + 64w */
 #pragma unroll
             for (int q = 0; q < PER; q++) {
+                /* LDS chunk i = (mat, chunk, row) <- global chunk row * G/8 + chunk of the matrix */
                 const int i = tid + 512 * q, mat = i / (NT * G / 8), j = i % (NT * G / 8);
-                const uint4 *src = (const uint4 *)(ex + (mat == 0 ? L::gate_s : L::up_s) + (size_t)nt * NT * G * 2) + j;
+                const int ch = j / NT, row = j % NT;
+                const uint4 *src =
+                    (const uint4 *)(ex + (mat == 0 ? L::gate_s : L::up_s) + (size_t)nt * NT * G * 2) + row * (G / 8) + ch;
                 __builtin_amdgcn_global_load_lds((const void *)src,
-                                                 (nmoe_lds_void *)((uint4 *)&s_s[0][0][0] + 512 * q + 64 * wave), 16, 0, 0);
+                                                 (nmoe_lds_void *)((uint4 *)&s_s[0][0][0][0] + 512 * q + 64 * wave), 16, 0,
+                                                 0);
             }
             float4 xv4[4][2];
             uint4 bv[2][NB];
@@ -551,7 +559,7 @@ nmoe_grouped_gateup_kernel(const uint8_t *pack, const uint16_t *xhi, const uint1
                 for (int b2 = 0; b2 < NB; b2++) {
                     float bf[8], sf[8];
                     nmoe_unpack_bf16x8(bv[mat][b2], bf);
-                    nmoe_unpack_bf16x8(*(const uint4 *)&s_s[mat][rt0 + 16 * b2][8 * kb], sf);
+                    nmoe_unpack_bf16x8(*(const uint4 *)&s_s[mat][kb][rt0 + 16 * b2][0], sf);
 #pragma unroll
                     for (int tq = 0; tq < G / 4; tq++) cv[mat][b2][tq] = bf[tq] - 128.0f * sf[tq];
 #pragma unroll
@@ -586,7 +594,7 @@ nmoe_grouped_gateup_kernel(const uint8_t *pack, const uint16_t *xhi, const uint1
                     if (mat == 1 && b2 == 0) asm volatile("" ::: "memory");
                     nmoe_stage_code_words<BITS, NT>(stage(st).b + mat * NT * WPG, rt0 + 16 * b2, kb, w0, w1);
                     nmoe_codes_bf16<BITS>(w0, w1, bq[mat][b2][0], bq[mat][b2][1]);
-                    sg[mat][b2] = nmoe_bf16f(s_s[mat][rt0 + 16 * b2][g]);
+                    sg[mat][b2] = nmoe_bf16f(s_s[mat][g >> 3][rt0 + 16 * b2][g & 7]);
                 }
 #pragma unroll
             for (int mb = 0; mb < 4; mb++) {
