@@ -124,6 +124,14 @@ __device__ __forceinline__ uint64_t nmoe_ld_tagged_die(const uint64_t *p) {
     return __hip_atomic_load((uint64_t *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
+/* A 16-byte load marked non-temporal (the expert weights are read once per
+ * step). */
+typedef unsigned int nmoe_u32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 nmoe_ld_nt4(const uint4 *p) {
+    const nmoe_u32x4 v = __builtin_nontemporal_load((const nmoe_u32x4 *)p);
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
 /* Accelerator die (XCC) the calling wave runs on. */
 __device__ __forceinline__ uint32_t nmoe_xcc_id() {
     uint32_t v;
@@ -554,23 +562,23 @@ __global__ void __launch_bounds__(NMOE_FUSED_THREADS) nmoe_fused_decode_kernel(n
 #pragma unroll
         for (int i = 0; i < GSTEPS; i++) {
             int row = grow0 + i * RPS;
-            gwv[i] = ((const uint4 *)(ex + L::gate_w))[(size_t)row * (Q::WPR_G / 4) + gl];
-            uwv[i] = ((const uint4 *)(ex + L::up_w))[(size_t)row * (Q::WPR_G / 4) + gl];
+            gwv[i] = nmoe_ld_nt4(&((const uint4 *)(ex + L::gate_w))[(size_t)row * (Q::WPR_G / 4) + gl]);
+            uwv[i] = nmoe_ld_nt4(&((const uint4 *)(ex + L::up_w))[(size_t)row * (Q::WPR_G / 4) + gl]);
             const uint16_t *gs = (const uint16_t *)(ex + L::gate_s) + row * Q::GPR_G + ggrp;
             const uint16_t *us = (const uint16_t *)(ex + L::up_s) + row * Q::GPR_G + ggrp;
-            gsc[i] = gs[0];
-            gbi[i] = gs[NMOE_INTER * Q::GPR_G];
-            usc[i] = us[0];
-            ubi[i] = us[NMOE_INTER * Q::GPR_G];
+            gsc[i] = __builtin_nontemporal_load(gs);
+            gbi[i] = __builtin_nontemporal_load(gs + NMOE_INTER * Q::GPR_G);
+            usc[i] = __builtin_nontemporal_load(us);
+            ubi[i] = __builtin_nontemporal_load(us + NMOE_INTER * Q::GPR_G);
         }
         __builtin_amdgcn_sched_barrier(0); /* gate/up rows ahead of the down rows */
 #pragma unroll
         for (int i = 0; i < DSTEPS; i++) {
             int row = drow0 + i * RPW_D;
-            dwv[i] = ((const uint4 *)(ex + L::down_w))[(size_t)row * (Q::WPR_D / 4) + dl];
+            dwv[i] = nmoe_ld_nt4(&((const uint4 *)(ex + L::down_w))[(size_t)row * (Q::WPR_D / 4) + dl]);
             const uint16_t *ds = (const uint16_t *)(ex + L::down_s) + row * Q::GPR_D + dgrp;
-            dsc[i] = ds[0];
-            dbi[i] = ds[NMOE_HIDDEN * Q::GPR_D];
+            dsc[i] = __builtin_nontemporal_load(ds);
+            dbi[i] = __builtin_nontemporal_load(ds + NMOE_HIDDEN * Q::GPR_D);
         }
     };
     uint32_t cand_g = 0;
