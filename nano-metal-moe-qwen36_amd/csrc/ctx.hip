@@ -137,20 +137,24 @@ extern "C" int nmoe_hip_check_device_status(nmoe_hip_ctx *ctx) {
     NMOE_HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
     NMOE_HIP_TRY(ctx, hipMemcpy(&status, ctx->sync + NMOE_SYNC_STATUS, sizeof(status), hipMemcpyDeviceToHost));
     if (status != 0) {
-        /* An aborted launch leaves the blocks' epochs unequal and combine
-         * counters part-counted.  Every epoch moves past the largest one
-         * (exchange words only ever carry past epochs, so none can match a
-         * future one -- including copies still held in a die's L2), and the
-         * counters and the status restart from 0. */
-        static uint32_t words[NMOE_SYNC_WORDS];
-        NMOE_HIP_TRY(ctx, hipMemcpy(words, ctx->sync, sizeof(words), hipMemcpyDeviceToHost));
-        uint32_t top = 0;
-        for (int b = 0; b < NMOE_SYNC_BLOCKS; b++)
-            if (words[NMOE_SYNC_EPOCH(b)] > top) top = words[NMOE_SYNC_EPOCH(b)];
-        for (int b = 0; b < NMOE_SYNC_BLOCKS; b++) words[NMOE_SYNC_EPOCH(b)] = top + 1u;
-        for (int c = 0; c < NMOE_SYNC_BLOCKS / 8; c++) words[NMOE_SYNC_COMBINE(c)] = 0u;
-        words[NMOE_SYNC_STATUS] = 0u;
-        NMOE_HIP_TRY(ctx, hipMemcpy(ctx->sync, words, sizeof(words), hipMemcpyHostToDevice));
+        /* An aborted launch leaves the blocks' epochs unequal.  Every epoch
+         * moves past the largest one (exchange words only ever carry past
+         * epochs, so none can match a future one -- including copies still
+         * held in a die's L2), and the status restarts from 0.  (A host
+         * copy of the words; this is the error path.) */
+        uint32_t *words = (uint32_t *)malloc(NMOE_SYNC_WORDS * sizeof(uint32_t));
+        if (words == NULL) return nmoe_fail(ctx, NMOE_HIP_ENOMEM, "host copy of the sync words");
+        hipError_t e = hipMemcpy(words, ctx->sync, NMOE_SYNC_WORDS * sizeof(uint32_t), hipMemcpyDeviceToHost);
+        if (e == hipSuccess) {
+            uint32_t top = 0;
+            for (int b = 0; b < NMOE_SYNC_BLOCKS; b++)
+                if (words[NMOE_SYNC_EPOCH(b)] > top) top = words[NMOE_SYNC_EPOCH(b)];
+            for (int b = 0; b < NMOE_SYNC_BLOCKS; b++) words[NMOE_SYNC_EPOCH(b)] = top + 1u;
+            words[NMOE_SYNC_STATUS] = 0u;
+            e = hipMemcpy(ctx->sync, words, NMOE_SYNC_WORDS * sizeof(uint32_t), hipMemcpyHostToDevice);
+        }
+        free(words);
+        NMOE_HIP_TRY(ctx, e);
         NMOE_HIP_TRY(ctx, hipDeviceSynchronize());
         return nmoe_fail(ctx, NMOE_HIP_ETIMEDOUT, "a persistent kernel's bounded wait expired (status %u)", status);
     }

@@ -8,18 +8,19 @@
  * (kernels.metal:562-640), down + weighted combine (kernels.metal:1456-1542)
  * and the next layer's input RMSNorm (runtime.m:2893-2900) -- three
  * host/device crossings per layer.  Here the layer pack is resident in HBM
- * and the step is one launch of 256 blocks x 9 wavefronts (8 workers that
- * stream and multiply expert rows, 1 control wavefront that routes).
+ * and the step is one launch of 256 blocks x 10 wavefronts (8 workers that
+ * stream and multiply expert rows, 2 control wavefronts that route).
  *
  * Blocks form 8 groups of 32 (group g = block % 8, j = block / 8); group g
  * streams expert slot g.
  *
  *   N  (stack variant) every block derives x = RMSNorm(h) itself, bit-exact
  *      with math.m:34-65.
- *   R  block b computes router row b in its first wavefront: the 1 MB
+ *   R  block b computes router row b in its candidate wavefront: the 1 MB
  *      router is read once per step (one 4 KB row per block).
- *   T  every block waits for all 256 logits and routes the token (bit-exact
- *      math.m softmax / top-k / renormalise in one wavefront).
+ *   T  every block waits for all 256 logits and routes the token: the
+ *      candidate wavefront selects the k largest logits, the exact
+ *      wavefront runs math.m's softmax / top-k / renormalise bit for bit.
  *   P  block j of group g issues all weight loads of slot g at once: gate/up
  *      rows 16j..16j+15 and down rows 64j..64j+63 (~55 KB per block, the
  *      whole 14 MB of expert weights in flight across the grid).
@@ -30,11 +31,12 @@
  *      64j..64j+63 and combines out = h_mid + sum_s w_s y_s
  *      (+ sigmoid(g) * shared) in slot order.
  *
- * Routing runs in a control wavefront per block: the candidates (the k
- * largest logits) are handed to the workers one selection round at a time,
- * so group s starts streaming expert s while later rounds and the exact
- * softmax / top-k still run; the exact result confirms each group's expert
- * (or re-points it, on probability ties) before act is published.
+ * The candidates (the k largest logits) are handed to the workers one
+ * selection round at a time, so group s starts streaming expert s while
+ * later rounds and the exact softmax still run; the exact result confirms
+ * each group's expert (or re-points it, on probability ties) before act is
+ * published.  The expert weights are loaded non-temporally: read once per
+ * step, they would otherwise evict the routers from the memory-side cache.
  *
  * Values a block waits for cross blocks as 64-bit (epoch, value) words
  * written and read with one device-coherent (sc1) access each; a consumer
@@ -772,6 +774,15 @@ static int nmoe_fused_fits(int num_cus) {
     return per_cu >= 1 && per_cu * num_cus >= NMOE_FUSED_BLOCKS;
 }
 
+/* Every x form the launcher may use with this router kind (the RMSNorm
+ * form needs the kernel to route). */
+template <int BITS, int ROUTE>
+static int nmoe_fused_fits_all(int num_cus) {
+    int ok = nmoe_fused_fits<BITS, ROUTE, NMOE_XBF16>(num_cus) && nmoe_fused_fits<BITS, ROUTE, NMOE_XF32>(num_cus);
+    if constexpr (ROUTE != NMOE_ROUTE_GIVEN) ok = ok && nmoe_fused_fits<BITS, ROUTE, NMOE_XNORM>(num_cus);
+    return ok;
+}
+
 /* Which die each block runs on. */
 __global__ void nmoe_xcc_probe_kernel(uint32_t *out) {
     if (threadIdx.x == 0) out[blockIdx.x] = nmoe_xcc_id();
@@ -803,14 +814,14 @@ static int nmoe_check_xcd_placement(int *placed) {
     return NMOE_HIP_OK;
 }
 
-/* The fused path needs all 256 blocks resident at once (its group barriers
- * wait on each other); decided here from the occupancy of every variant. */
+/* The fused path needs all 256 blocks resident at once (its blocks wait for
+ * each other's exchange words); decided here from the occupancy of every
+ * variant. */
 extern "C" int nmoe_decode_init(nmoe_hip_ctx *ctx) {
     int n = ctx->num_cus;
     int ok = 1;
 #define NMOE_FITS_ALL(B, R) \
-    ok = ok && nmoe_fused_fits<B, R, NMOE_XBF16>(n) && nmoe_fused_fits<B, R, NMOE_XF32>(n) && \
-         (R == NMOE_ROUTE_GIVEN || nmoe_fused_fits<B, R, NMOE_XNORM>(n))
+    ok = ok && nmoe_fused_fits_all<B, R>(n)
     NMOE_FITS_ALL(4, NMOE_ROUTE_BF16);
     NMOE_FITS_ALL(4, NMOE_ROUTE_Q4);
     NMOE_FITS_ALL(4, NMOE_ROUTE_GIVEN);
