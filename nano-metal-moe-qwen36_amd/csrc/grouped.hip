@@ -116,10 +116,9 @@ __device__ __forceinline__ uint32_t nmoe_entry_expert(const uint32_t *idx, int q
 }
 
 /* D1: counts[b][257] = expert histogram of entry slice b. */
-__global__ void __launch_bounds__(256) nmoe_dispatch_count_kernel(const uint32_t *idx, int ntok, int k,
-                                                                   uint32_t *counts) {
+__device__ __forceinline__ void nmoe_dispatch_count(const uint32_t *idx, int ntok, int k, uint32_t *counts, int b) {
     __shared__ uint32_t h[NMOE_EXPERTS + 1];
-    const int tid = threadIdx.x, b = blockIdx.x, n = ntok * k;
+    const int tid = threadIdx.x, n = ntok * k;
     const int per = (n + NMOE_DISPATCH_BLOCKS - 1) / NMOE_DISPATCH_BLOCKS;
     for (int i = tid; i <= NMOE_EXPERTS; i += 256) h[i] = 0;
     __syncthreads();
@@ -133,13 +132,12 @@ __global__ void __launch_bounds__(256) nmoe_dispatch_count_kernel(const uint32_t
  * chunks of 256 entries in order; within a chunk the rank of an entry is
  * its rank among the equal-expert lanes of its wavefront (a 9-bit
  * multi-split by ballots) plus the counts of the earlier wavefronts. */
-__global__ void __launch_bounds__(256) nmoe_dispatch_scatter_kernel(const uint32_t *idx, int ntok, int k,
-                                                                     const uint32_t *counts, uint32_t *perm,
-                                                                     uint32_t *offsets) {
+__device__ __forceinline__ void nmoe_dispatch_scatter(const uint32_t *idx, int ntok, int k, const uint32_t *counts,
+                                                      uint32_t *perm, uint32_t *offsets, int b) {
     __shared__ uint32_t s_base[NMOE_EXPERTS];
     __shared__ uint32_t s_scan[256];
     __shared__ uint32_t s_wc[4][NMOE_EXPERTS + 1];
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, b = blockIdx.x, n = ntok * k;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, n = ntok * k;
     const int per = (n + NMOE_DISPATCH_BLOCKS - 1) / NMOE_DISPATCH_BLOCKS;
     /* thread e: total of expert e and its count in the slices before b */
     uint32_t total = 0, before = 0;
@@ -197,9 +195,8 @@ __global__ void __launch_bounds__(256) nmoe_dispatch_scatter_kernel(const uint32
  * lo plane x - hi when x is fp32), xs[t][g] = sum of the 64 values of group
  * g (hi + lo, in a fixed order). */
 template <int BITS, typename XT>
-__global__ void __launch_bounds__(256) nmoe_grouped_xprep_kernel(const XT *x, uint16_t *xhi, uint16_t *xlo,
-                                                                  float *xs) {
-    const int t = blockIdx.x, tid = threadIdx.x; /* 8 elements per thread: half a span */
+__device__ __forceinline__ void nmoe_grouped_xprep(const XT *x, uint16_t *xhi, uint16_t *xlo, float *xs, int t) {
+    const int tid = threadIdx.x; /* 8 elements per thread: half a span */
     const int span = tid >> 1, half = tid & 1;
     float v[8];
 #pragma unroll
@@ -231,6 +228,42 @@ __global__ void __launch_bounds__(256) nmoe_grouped_xprep_kernel(const XT *x, ui
     sum = sum + nmoe_dpp_f<NMOE_DPP_XOR2>(sum);
     sum = sum + nmoe_dpp_f<NMOE_DPP_HALF_MIRROR>(sum);
     if ((tid & 7) == 0) xs[(size_t)t * (NMOE_HIDDEN / NMOE_GROUP) + (tid >> 3)] = sum;
+}
+
+/* One launch for the grouped path's preparation: blocks 0..15 run the
+ * dispatch (D1, then D2 once every slice's histogram is in), the blocks
+ * after them prepare one token's x each (none when x is NULL).  The 16
+ * dispatch blocks are the grid's first, so they are resident together;
+ * they meet at a counter in the sync words that only ever grows by 16 per
+ * launch (bounded wait; an expired wait sets the status word). */
+template <int BITS, typename XT>
+__global__ void __launch_bounds__(256) nmoe_grouped_prep_kernel(const uint32_t *idx, int ntok, int k, uint32_t *counts,
+                                                                uint32_t *perm, uint32_t *offsets, uint32_t *sync,
+                                                                const XT *x, uint16_t *xhi, uint16_t *xlo, float *xs) {
+    const int b = blockIdx.x;
+    if (b >= NMOE_DISPATCH_BLOCKS) {
+        nmoe_grouped_xprep<BITS, XT>(x, xhi, xlo, xs, b - NMOE_DISPATCH_BLOCKS);
+        return;
+    }
+    nmoe_dispatch_count(idx, ntok, k, counts, b);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent"); /* this slice's histogram, to the other blocks */
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint32_t *cnt = sync + NMOE_SYNC_DISPATCH;
+        const uint32_t old = nmoe_add_u32_dev(cnt, 1u);
+        const uint32_t target = (old / NMOE_DISPATCH_BLOCKS + 1u) * NMOE_DISPATCH_BLOCKS;
+        uint32_t spins = 0;
+        while ((int32_t)(nmoe_ld_u32_dev(cnt) - target) < 0) {
+            __builtin_amdgcn_s_sleep(1);
+            if (++spins > NMOE_SPIN_LIMIT) {
+                __hip_atomic_store(sync + NMOE_SYNC_STATUS, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                break;
+            }
+        }
+    }
+    __syncthreads();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent"); /* the other slices' histograms */
+    nmoe_dispatch_scatter(idx, ntok, k, counts, perm, offsets, b);
 }
 
 /* ------------------------------------------------------------ stage ring */
@@ -895,10 +928,9 @@ extern "C" void nmoe_grouped_free(nmoe_hip_ctx *ctx) {
 /* D1 + D2 into perm / offsets (any device buffers of T*k and 257 words). */
 extern "C" int nmoe_grouped_dispatch(nmoe_hip_ctx *ctx, const uint32_t *idx, int ntok, int k, uint32_t *perm,
                                      uint32_t *offsets, hipStream_t s) {
-    hipLaunchKernelGGL(nmoe_dispatch_count_kernel, dim3(NMOE_DISPATCH_BLOCKS), dim3(256), 0, s, idx, ntok, k,
-                       ctx->g_counts);
-    hipLaunchKernelGGL(nmoe_dispatch_scatter_kernel, dim3(NMOE_DISPATCH_BLOCKS), dim3(256), 0, s, idx, ntok, k,
-                       (const uint32_t *)ctx->g_counts, perm, offsets);
+    hipLaunchKernelGGL((nmoe_grouped_prep_kernel<4, uint16_t>), dim3(NMOE_DISPATCH_BLOCKS), dim3(256), 0, s, idx, ntok,
+                       k, ctx->g_counts, perm, offsets, ctx->sync, (const uint16_t *)NULL, (uint16_t *)NULL,
+                       (uint16_t *)NULL, (float *)NULL);
     const hipError_t e = hipGetLastError();
     return e == hipSuccess ? NMOE_HIP_OK : nmoe_hip_check(ctx, e, "dispatch launch");
 }
@@ -907,15 +939,16 @@ template <int BITS>
 static int nmoe_grouped_run(nmoe_hip_ctx *ctx, const uint8_t *pack, const void *x, int x_dtype, int ntok, int k,
                             const uint32_t *idx, const float *w, const float *h_mid, const float *shared_out,
                             const float *shared_gate_raw, float *out, hipStream_t s) {
-    int rc = nmoe_grouped_dispatch(ctx, idx, ntok, k, ctx->g_perm, ctx->g_offsets, s);
-    if (rc != NMOE_HIP_OK) return rc;
     const bool bf = x_dtype == NMOE_HIP_BF16;
+    const dim3 gprep(NMOE_DISPATCH_BLOCKS + ntok);
     if (bf)
-        hipLaunchKernelGGL((nmoe_grouped_xprep_kernel<BITS, uint16_t>), dim3(ntok), dim3(256), 0, s,
-                           (const uint16_t *)x, ctx->g_xhi, (uint16_t *)NULL, ctx->g_xs);
+        hipLaunchKernelGGL((nmoe_grouped_prep_kernel<BITS, uint16_t>), gprep, dim3(256), 0, s, idx, ntok, k,
+                           ctx->g_counts, ctx->g_perm, ctx->g_offsets, ctx->sync, (const uint16_t *)x, ctx->g_xhi,
+                           (uint16_t *)NULL, ctx->g_xs);
     else
-        hipLaunchKernelGGL((nmoe_grouped_xprep_kernel<BITS, float>), dim3(ntok), dim3(256), 0, s, (const float *)x,
-                           ctx->g_xhi, ctx->g_xlo, ctx->g_xs);
+        hipLaunchKernelGGL((nmoe_grouped_prep_kernel<BITS, float>), gprep, dim3(256), 0, s, idx, ntok, k,
+                           ctx->g_counts, ctx->g_perm, ctx->g_offsets, ctx->sync, (const float *)x, ctx->g_xhi,
+                           ctx->g_xlo, ctx->g_xs);
     const dim3 ggu(NMOE_EXPERTS * (NMOE_INTER / nmoe_gu_rows(bf ? 1 : 2))), gdn(NMOE_EXPERTS * (NMOE_HIDDEN / NMOE_DN_ROWS));
     if (bf)
         hipLaunchKernelGGL((nmoe_grouped_gateup_kernel<BITS, 1>), ggu, dim3(512), 0, s, pack,

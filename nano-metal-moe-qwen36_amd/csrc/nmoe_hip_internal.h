@@ -48,6 +48,7 @@ struct nmoe_layout<2> {
 #define NMOE_SYNC_STATUS 0     /* set to 1 by a kernel whose bounded wait expired */
 #define NMOE_SYNC_WORDS 8192   /* status + per-block launch epochs of the fused kernel */
 #define NMOE_SYNC_EPOCH(b) (64 + 16 * (b))     /* per-block launch epochs, 64 bytes apart */
+#define NMOE_SYNC_DISPATCH 4352                /* arrival counter of the dispatch blocks */
 #define NMOE_SYNC_BLOCKS 256
 
 struct nmoe_pack_slot {
