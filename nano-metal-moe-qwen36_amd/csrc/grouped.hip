@@ -49,7 +49,11 @@ typedef __attribute__((ext_vector_type(8))) __bf16 nmoe_bf16x8;
 typedef __attribute__((ext_vector_type(4))) float nmoe_f32x4;
 
 #define NMOE_DISPATCH_BLOCKS 16
-#define NMOE_MCHUNK 64    /* expert rows per pass (four 16-row MFMA blocks) */
+#define NMOE_MCHUNK 64 /* expert rows (entries) per pass: four 16-row MFMA blocks */
+/* Wavefronts per gate/up and down block: 8 (one block a CU) or 4 (two). */
+#ifndef NMOE_GROUPED_NW
+#define NMOE_GROUPED_NW 4
+#endif
 
 /* k offset (within a lane's 16-k span) of operand element `slot`
  * (slot = 8 * slice + 2 * dword + half). */
@@ -268,12 +272,12 @@ __global__ void __launch_bounds__(256) nmoe_grouped_prep_kernel(const uint32_t *
 
 /* ------------------------------------------------------------ stage ring */
 
-/* Both GEMMs stream one 64-deep K group per step through a ring of
- * NMOE_NS LDS stages, filled by direct global->LDS loads
- * (global_load_lds_dwordx4: lane l of a wavefront writes bytes 16l..16l+15
- * of the instruction's 1 KB), so a group is requested NMOE_NS - 1 steps
- * before it is multiplied.  A stage holds
- *   - the A rows of the group: PL planes of 64 rows x 64 bf16 (128 B); the
+/* Both GEMMs stream one 64-deep K group per step through a ring of NS LDS
+ * stages (four where they fit the block's LDS share, else three), filled by
+ * direct global->LDS loads (global_load_lds_dwordx4: lane l of a wavefront
+ * writes bytes 16l..16l+15 of the instruction's 1 KB), so a group is
+ * requested NS - 1 steps before it is multiplied.  A stage holds
+ *   - the A rows of the group: PL planes of 64 or 128 rows x 64 bf16 (128 B); the
  *     16-byte chunk c of row r sits at slot c ^ ((r >> 1) & 7), so the 16
  *     rows of one ds_read_b128 pass cover all 64 banks;
  *   - the codes of the tile's weight rows for the group: q4 as rows of
@@ -283,13 +287,11 @@ __global__ void __launch_bounds__(256) nmoe_grouped_prep_kernel(const uint32_t *
  * Each stage is a __shared__ variable of its own: the compiler then tells
  * the stages' direct loads apart and a read of one stage does not wait for
  * the loads still in flight into the others. */
-#define NMOE_NS 4
-
 typedef __attribute__((address_space(3))) void nmoe_lds_void;
 
-template <int PL, int CW>
+template <int PL, int R, int CW>
 struct nmoe_stage {
-    uint4 a[PL][NMOE_MCHUNK * 8];
+    uint4 a[PL][R * 8];
     uint32_t b[CW];
 };
 
@@ -323,18 +325,18 @@ __device__ __forceinline__ void nmoe_stage_operand(const uint4 *plane, int r, in
 }
 
 /* The direct loads of one stage's codes (NR weight rows of 32 B (q4) or
- * 16 B (q2)) over the eight wavefronts of a block: 1-KB instructions (16 B
- * a lane) where each wavefront has at least 1 KB to load, else 256-byte
- * ones (4 B a lane).  Every wavefront issues the same number, so the ring
- * waits are compile-time constants. */
-template <int BITS, int NR>
+ * 16 B (q2)) over the NW wavefronts of a block: 1-KB instructions (16 B a
+ * lane) where each wavefront has at least 1 KB to load, else 256-byte ones
+ * (4 B a lane).  Every wavefront issues the same number, so the ring waits
+ * are compile-time constants. */
+template <int BITS, int NR, int NW>
 struct nmoe_code_plan {
     static constexpr int BYTES = NR * (BITS == 4 ? 32 : 16);
-    static constexpr bool WIDE = BYTES / 8 >= 1024;
+    static constexpr bool WIDE = BYTES / NW >= 1024;
     static constexpr int INS_BYTES = WIDE ? 1024 : 256;
-    static constexpr int PER_WAVE = BYTES / 8 / INS_BYTES;
-    static_assert(PER_WAVE >= 1 && PER_WAVE * INS_BYTES * 8 == BYTES, "codes split evenly over 8 wavefronts");
-    static_assert(WIDE || BITS == 2, "q4 stages are at least 8 KB");
+    static constexpr int PER_WAVE = BYTES / NW / INS_BYTES;
+    static_assert(PER_WAVE >= 1 && PER_WAVE * INS_BYTES * NW == BYTES, "codes split evenly over the wavefronts");
+    static_assert(WIDE || BITS == 2, "a q4 wavefront loads at least 1 KB of codes");
 };
 
 /* Words of group g from a row's first word: 8 (q4) or 4 (q2). */
@@ -467,21 +469,36 @@ __device__ __forceinline__ float nmoe_silu_fast(float x) {
 
 /* ------------------------------------------------------------ gate/up */
 
-/* Gate (and up) rows per block: 256 for bf16 x (one A plane), 128 for fp32
- * x (hi + lo planes), so a stage fits four times in LDS. */
-__host__ __device__ constexpr int nmoe_gu_rows(int xpl) { return xpl == 1 ? 256 : 128; }
+/* Gate (and up) rows per block of NW wavefronts: 32 a wavefront for bf16 x
+ * (one A plane), 16 for fp32 x (hi + lo planes). */
+__host__ __device__ constexpr int nmoe_gu_rows(int xpl, int nw) { return nw * 32 / xpl; }
+
+/* LDS bytes of a gate/up block with ns stages: the stages (A rows, codes),
+ * the scales, s_tok and s_as. */
+__host__ __device__ constexpr int nmoe_gu_lds(int bits, int xpl, int nw, int ns) {
+    return ns * (xpl * NMOE_MCHUNK * 128 + 2 * nmoe_gu_rows(xpl, nw) * (bits == 4 ? 32 : 16)) +
+           2 * nmoe_gu_rows(xpl, nw) * 64 + 4 * NMOE_MCHUNK * (1 + nw);
+}
+/* Stages: four where they fit the block's share of the CU's 160 KB (the
+ * whole of it for eight wavefronts, half for four), else three. */
+__host__ __device__ constexpr int nmoe_gu_stages(int bits, int xpl, int nw) {
+    return nmoe_gu_lds(bits, xpl, nw, 4) <= (nw == 8 ? 160 : 80) * 1024 - 512 ? 4 : 3;
+}
+
 
 /* Expert e, gate and up rows NT * nt .. +NT-1: act rows of all the
- * expert's entries, 64 entries per pass.  Eight wavefronts, two per SIMD;
- * wavefront w owns gate and up rows (NT/8)w .. +NT/8-1 of the tile as NB
- * 16-row MFMA column blocks each, over four 16-entry row blocks, so a lane
- * holds gate and up of the same (entry, row).
+ * expert's entries, 64 entries per pass.  NW wavefronts (eight: one block a
+ * CU; four: two blocks a CU, whose set-up and epilogue then overlap the
+ * other's ring), two per SIMD either way; wavefront w owns gate and up rows
+ * (NT/NW)w .. +NT/NW-1 of the tile as NB 16-row MFMA column blocks each,
+ * over the pass's (up to four) 16-entry row blocks, so a lane holds gate and
+ * up of the same (entry, row).
  *
  * y = sum_g s_g P_g + sum_g (b_g - 128 s_g) xs_g with P_g the MFMA product
  * of the group's A rows and the codes as bf16(128 + q); the second sum runs
  * first, on the fp32 matrix cores. */
-template <int BITS, int XPL>
-__global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
+template <int BITS, int XPL, int NW>
+__global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
 nmoe_grouped_gateup_kernel(const uint8_t *pack, const uint16_t *xhi, const uint16_t *xlo, const float *xs,
                            const uint32_t *perm, const uint32_t *offsets, int k, uint16_t *ahi, uint16_t *alo,
                            float *as) {
@@ -489,22 +506,30 @@ nmoe_grouped_gateup_kernel(const uint8_t *pack, const uint16_t *xhi, const uint1
     using L = nmoe_layout<BITS>;
     constexpr int G = NMOE_HIDDEN / NMOE_GROUP; /* 32 groups */
     static_assert(G == 32, "the correction's operand layout assumes 8 groups per lane");
-    constexpr int NT = nmoe_gu_rows(XPL);
-    constexpr int NB = NT / 128;                /* column blocks per wavefront and matrix */
+    static_assert(NW == 8 || NW == 4, "eight or four wavefronts");
+    constexpr int NT = nmoe_gu_rows(XPL, NW);
+    constexpr int NB = NT / (16 * NW);          /* column blocks per wavefront and matrix */
+    constexpr int MB = 4;                       /* row blocks per full pass */
+    constexpr int MCH = NMOE_MCHUNK;            /* entries per pass */
+    constexpr int AI = 8 / NW;                  /* A instructions per plane and wavefront */
+    constexpr int NTH = 64 * NW;
     constexpr int WPG = BITS == 4 ? 8 : 4;
-    using CP = nmoe_code_plan<BITS, 2 * NT>;
+    using CP = nmoe_code_plan<BITS, 2 * NT, NW>;
     constexpr int CPM = CP::BYTES / 2 / CP::INS_BYTES; /* code instructions per matrix */
     /* gate and up scales of the tile, chunk-major: 16-byte chunk q (groups
      * 8q..8q+7) of row r at [mat][q][r], so a ring step's 16 rows of one
      * group sit 16 bytes apart (distinct banks; row-major rows 64 bytes
      * apart put four rows on each bank) */
     __shared__ uint16_t s_s[2][G / 8][NT][8];
-    constexpr int NS = NMOE_NS; /* (five stages measured no faster) */
-    typedef nmoe_stage<XPL, 2 * NT * WPG> Stage;
+    constexpr int NS = nmoe_gu_stages(BITS, XPL, NW); /* (five measured no faster than four) */
+    typedef nmoe_stage<XPL, MCH, 2 * NT * WPG> Stage;
     __shared__ Stage s_st0, s_st1, s_st2, s_st3;
-    auto stage = [&](int st) -> Stage & { return st == 0 ? s_st0 : st == 1 ? s_st1 : st == 2 ? s_st2 : s_st3; };
-    __shared__ uint32_t s_tok[NMOE_MCHUNK];
-    __shared__ float s_as[8][NMOE_MCHUNK];
+    auto stage = [&](int st) -> Stage & {
+        if constexpr (NS == 3) return st == 0 ? s_st0 : st == 1 ? s_st1 : s_st2;
+        else return st == 0 ? s_st0 : st == 1 ? s_st1 : st == 2 ? s_st2 : s_st3;
+    };
+    __shared__ uint32_t s_tok[MCH];
+    __shared__ float s_as[NW][MCH];
     int e, nt;
     nmoe_die_tile(blockIdx.x, NMOE_INTER / NT, e, nt);
     const uint32_t p0 = offsets[e], n = offsets[e + 1] - p0;
@@ -512,99 +537,106 @@ nmoe_grouped_gateup_kernel(const uint8_t *pack, const uint16_t *xhi, const uint1
     const int tid = threadIdx.x, lane = tid & 63, col = lane & 15, kb = lane >> 4;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint8_t *ex = pack + (size_t)e * L::expert_size;
-    const int rt0 = (NT / 8) * wave + col; /* tile row of column block nb: rt0 + 16 nb */
+    const int rt0 = (NT / NW) * wave + col; /* tile row of column block nb: rt0 + 16 nb */
     /* this wavefront's code instructions CP::PER_WAVE * wave + i all fall in
-     * matrix cmat (gate for wavefronts 0-3, up for 4-7) */
-    const int cmat = wave >> 2;
+     * matrix cmat (gate for the first half of the wavefronts, up for the
+     * second) */
+    const int cmat = wave / (NW / 2);
     const uint32_t *cbase = (const uint32_t *)(ex + (cmat == 0 ? L::gate_w : L::up_w)) + (size_t)nt * NT * Q::WPR_G;
     const uint16_t *bias[2] = {(const uint16_t *)(ex + L::gate_b) + (size_t)nt * NT * G,
                                (const uint16_t *)(ex + L::up_b) + (size_t)nt * NT * G};
 
-    for (uint32_t m0 = 0; m0 < n; m0 += NMOE_MCHUNK) {
-        if (tid < NMOE_MCHUNK) s_tok[tid] = perm[p0 + min(m0 + tid, n - 1)] / (uint32_t)k;
+    for (uint32_t m0 = 0; m0 < n; m0 += MCH) {
+        if (tid < MCH) s_tok[tid] = perm[p0 + min(m0 + tid, n - 1)] / (uint32_t)k;
         nmoe_lds_barrier();
-        const int nb = (int)min((n - m0 + 15) / 16, 4u);
-        /* this lane's A row for instruction `wave`: entry 8 wave + lane / 8 */
-        const uint32_t tsrc = s_tok[8 * wave + (lane >> 3)];
+        /* this lane's A row for instruction wave + NW i: entry 8 (wave + NW i) + lane / 8 */
+        uint32_t row_off[AI];
+#pragma unroll
+        for (int i = 0; i < AI; i++)
+            row_off[i] = s_tok[8 * (wave + NW * i) + (lane >> 3)] * (uint32_t)(NMOE_HIDDEN * 2);
         const uint16_t *xpl[2] = {xhi, xlo};
-        const uint32_t row_off = tsrc * (uint32_t)(NMOE_HIDDEN * 2);
         auto issue = [&](int g, int st) {
 #pragma unroll
-            for (int pl = 0; pl < XPL; pl++) nmoe_stage_rows(stage(st).a[pl], xpl[pl] + 64 * g, row_off, wave, lane);
+            for (int pl = 0; pl < XPL; pl++)
+#pragma unroll
+                for (int i = 0; i < AI; i++)
+                    nmoe_stage_rows(stage(st).a[pl], xpl[pl] + 64 * g, row_off[i], wave + NW * i, lane);
 #pragma unroll
             for (int i = 0; i < CP::PER_WAVE; i++)
                 nmoe_stage_codes<BITS, NT, CP::WIDE>(stage(st).b + cmat * NT * WPG, cbase + nmoe_gwords<BITS>() * g,
                                                      Q::WPR_G, (CP::PER_WAVE * wave + i) % CPM, lane);
         };
-        nmoe_f32x4 acc[2][NB][4];
+        const int nb = (int)min((n - m0 + 15) / 16, (uint32_t)MB);
+        nmoe_f32x4 acc[2][NB][MB];
         {
-            /* The correction's operands go out first and the first ring
-             * stages right after them: loads retire in order, so the small
-             * loads then return without waiting for the stages, and the
-             * correction's MFMAs run while the stages stream in.
-             * The tile's scales (first pass only); A lane = (entry col,
-             * groups 8kb + tq), B lane = (row col, groups 8kb + tq): a lane's
-             * eight groups are contiguous (two 16-byte loads of xs, one of
-             * the biases). */
-            constexpr int PER = 2 * NT * G / 8 / 512;
-            /* scales straight into LDS, every pass (later passes hit L2):
-             * wavefront w's q-th 1 KB at uint4 512q + 64w */
+                /* The correction's operands go out first and the first ring
+                 * stages right after them: loads retire in order, so the
+                 * small loads then return without waiting for the stages,
+                 * and the correction's MFMAs run while the stages stream in.
+                 * A lane = (entry col, groups 8kb + tq), B lane = (row col,
+                 * groups 8kb + tq): a lane's eight groups are contiguous (two
+                 * 16-byte loads of xs, one of the biases). */
+                constexpr int PER = 2 * NT * G / 8 / NTH;
+                static_assert(PER * NTH == 2 * NT * G / 8, "scale chunks split evenly over the threads");
+                /* the tile's scales straight into LDS, every pass (later
+                 * passes hit L2): wavefront w's q-th 1 KB at uint4 NTH q + 64w */
 #pragma unroll
-            for (int q = 0; q < PER; q++) {
-                /* LDS chunk i = (mat, chunk, row) <- global chunk row * G/8 + chunk of the matrix */
-                const int i = tid + 512 * q, mat = i / (NT * G / 8), j = i % (NT * G / 8);
-                const int ch = j / NT, row = j % NT;
-                const uint4 *src =
-                    (const uint4 *)(ex + (mat == 0 ? L::gate_s : L::up_s) + (size_t)nt * NT * G * 2) + row * (G / 8) + ch;
-                __builtin_amdgcn_global_load_lds((const void *)src,
-                                                 (nmoe_lds_void *)((uint4 *)&s_s[0][0][0][0] + 512 * q + 64 * wave), 16, 0,
-                                                 0);
-            }
-            float4 xv4[4][2];
-            uint4 bv[2][NB];
-#pragma unroll
-            for (int mb = 0; mb < 4; mb++) {
-                const float4 *xsr = (const float4 *)(xs + (size_t)s_tok[16 * mb + col] * G + 8 * kb);
-                xv4[mb][0] = xsr[0];
-                xv4[mb][1] = xsr[1];
-            }
-#pragma unroll
-            for (int mat = 0; mat < 2; mat++)
-#pragma unroll
-                for (int b2 = 0; b2 < NB; b2++)
-                    bv[mat][b2] = *(const uint4 *)(bias[mat] + (rt0 + 16 * b2) * G + 8 * kb);
-#pragma unroll
-            for (int st = 0; st < NS - 1; st++) issue(st, st);
-            /* scales, xs and biases have landed once only the stages' loads
-             * are in flight; then every wavefront's scales are in LDS */
-            nmoe_wait_vm<(NS - 1) * (XPL + CP::PER_WAVE)>();
-            nmoe_lds_barrier();
-            float xv[4][G / 4];
-#pragma unroll
-            for (int mb = 0; mb < 4; mb++) {
-                xv[mb][0] = xv4[mb][0].x, xv[mb][1] = xv4[mb][0].y, xv[mb][2] = xv4[mb][0].z, xv[mb][3] = xv4[mb][0].w;
-                xv[mb][4] = xv4[mb][1].x, xv[mb][5] = xv4[mb][1].y, xv[mb][6] = xv4[mb][1].z, xv[mb][7] = xv4[mb][1].w;
-            }
-            float cv[2][NB][G / 4];
-#pragma unroll
-            for (int mat = 0; mat < 2; mat++)
-#pragma unroll
-                for (int b2 = 0; b2 < NB; b2++) {
-                    float bf[8], sf[8];
-                    nmoe_unpack_bf16x8(bv[mat][b2], bf);
-                    nmoe_unpack_bf16x8(*(const uint4 *)&s_s[mat][kb][rt0 + 16 * b2][0], sf);
-#pragma unroll
-                    for (int tq = 0; tq < G / 4; tq++) cv[mat][b2][tq] = bf[tq] - 128.0f * sf[tq];
-#pragma unroll
-                    for (int mb = 0; mb < 4; mb++) acc[mat][b2][mb] = nmoe_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+                for (int q = 0; q < PER; q++) {
+                    /* LDS chunk i = (mat, chunk, row) <- global chunk row * G/8 + chunk of the matrix */
+                    const int i = tid + NTH * q, mat = i / (NT * G / 8), j = i % (NT * G / 8);
+                    const int ch = j / NT, row = j % NT;
+                    const uint4 *src = (const uint4 *)(ex + (mat == 0 ? L::gate_s : L::up_s) + (size_t)nt * NT * G * 2) +
+                                       row * (G / 8) + ch;
+                    __builtin_amdgcn_global_load_lds(
+                        (const void *)src, (nmoe_lds_void *)((uint4 *)&s_s[0][0][0][0] + NTH * q + 64 * wave), 16, 0, 0);
                 }
-            /* group-slice outermost: the 4 NB 4 accumulator chains interleave,
-             * so each MFMA's latency hides behind the others' */
+                float4 xv4[MB][2];
+                uint4 bv[2][NB];
 #pragma unroll
-            for (int tq = 0; tq < G / 4; tq++)
+                for (int mb = 0; mb < MB; mb++) {
+                    const float4 *xsr = (const float4 *)(xs + (size_t)s_tok[16 * mb + col] * G + 8 * kb);
+                    xv4[mb][0] = xsr[0];
+                    xv4[mb][1] = xsr[1];
+                }
 #pragma unroll
-                for (int mb = 0; mb < 4; mb++)
-                    if (mb < nb)
+                for (int mat = 0; mat < 2; mat++)
+#pragma unroll
+                    for (int b2 = 0; b2 < NB; b2++)
+                        bv[mat][b2] = *(const uint4 *)(bias[mat] + (rt0 + 16 * b2) * G + 8 * kb);
+#pragma unroll
+                for (int st = 0; st < NS - 1; st++) issue(st, st);
+                /* scales, xs and biases have landed once only the stages'
+                 * loads are in flight; then every wavefront's scales are in
+                 * LDS */
+                nmoe_wait_vm<(NS - 1) * (XPL * AI + CP::PER_WAVE)>();
+                nmoe_lds_barrier();
+                float xv[MB][G / 4];
+#pragma unroll
+                for (int mb = 0; mb < MB; mb++) {
+                    xv[mb][0] = xv4[mb][0].x, xv[mb][1] = xv4[mb][0].y, xv[mb][2] = xv4[mb][0].z;
+                    xv[mb][3] = xv4[mb][0].w, xv[mb][4] = xv4[mb][1].x, xv[mb][5] = xv4[mb][1].y;
+                    xv[mb][6] = xv4[mb][1].z, xv[mb][7] = xv4[mb][1].w;
+                }
+                float cv[2][NB][G / 4];
+#pragma unroll
+                for (int mat = 0; mat < 2; mat++)
+#pragma unroll
+                    for (int b2 = 0; b2 < NB; b2++) {
+                        float bf[8], sf[8];
+                        nmoe_unpack_bf16x8(bv[mat][b2], bf);
+                        nmoe_unpack_bf16x8(*(const uint4 *)&s_s[mat][kb][rt0 + 16 * b2][0], sf);
+#pragma unroll
+                        for (int tq = 0; tq < G / 4; tq++) cv[mat][b2][tq] = bf[tq] - 128.0f * sf[tq];
+#pragma unroll
+                        for (int mb = 0; mb < MB; mb++) acc[mat][b2][mb] = nmoe_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+                    }
+                /* group-slice outermost: the 2 NB MB accumulator chains
+                 * interleave, so each MFMA's latency hides behind the others' */
+#pragma unroll
+                for (int tq = 0; tq < G / 4; tq++)
+#pragma unroll
+                    for (int mb = 0; mb < MB; mb++)
+                        if (mb < nb)
 #pragma unroll
                         for (int mat = 0; mat < 2; mat++)
 #pragma unroll
@@ -613,7 +645,7 @@ nmoe_grouped_gateup_kernel(const uint8_t *pack, const uint16_t *xhi, const uint1
                                                                                         acc[mat][b2][mb], 0, 0, 0);
         }
         auto step = [&](int g, const int st, const bool ahead) {
-            nmoe_ring_step_barrier<XPL + CP::PER_WAVE, G, NS>(g);
+            nmoe_ring_step_barrier<XPL * AI + CP::PER_WAVE, G, NS>(g);
             if (ahead) issue(g + NS - 1, (st + NS - 1) % NS);
             uint4 bq[2][NB][2];
             float sg[2][NB];
@@ -630,7 +662,7 @@ nmoe_grouped_gateup_kernel(const uint8_t *pack, const uint16_t *xhi, const uint1
                     sg[mat][b2] = nmoe_bf16f(s_s[mat][g >> 3][rt0 + 16 * b2][g & 7]);
                 }
 #pragma unroll
-            for (int mb = 0; mb < 4; mb++) {
+            for (int mb = 0; mb < MB; mb++) {
                 if (mb < nb) {
                     uint4 a[XPL][2];
 #pragma unroll
@@ -654,45 +686,47 @@ nmoe_grouped_gateup_kernel(const uint8_t *pack, const uint16_t *xhi, const uint1
             }
         };
         nmoe_ring_run<G, NS>(step);
-        /* epilogue: act = SiLU(gate) * up as hi + lo bf16, in the down
-         * kernel's operand order; group sums of act rows (a down group is 64
-         * act columns = 512 / NT wavefronts of this tile) */
-        float part_sum[4][4] = {};
+        {
+            /* epilogue: act = SiLU(gate) * up as hi + lo bf16, in the down
+             * kernel's operand order; group sums of act rows (a down group
+             * is 64 act columns, WPD wavefronts of this tile) */
+            float part_sum[MB][4] = {};
 #pragma unroll
-        for (int b2 = 0; b2 < NB; b2++) {
-            const int r = nt * NT + rt0 + 16 * b2; /* act column */
-            const int span = r >> 4;
-            const int slot = nmoe_kperm_inv<BITS>(r & 15);
+            for (int b2 = 0; b2 < NB; b2++) {
+                const int r = nt * NT + rt0 + 16 * b2; /* act column */
+                const int span = r >> 4;
+                const int slot = nmoe_kperm_inv<BITS>(r & 15);
 #pragma unroll
-            for (int mb = 0; mb < 4; mb++) {
-                if (mb >= nb) continue;
+                for (int mb = 0; mb < MB; mb++) {
+                    if (mb >= nb) continue;
 #pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const uint32_t m = m0 + 16 * mb + 4 * kb + i;
-                    const float av = nmoe_silu_fast(acc[0][b2][mb][i]) * acc[1][b2][mb][i];
-                    const uint32_t h = nmoe_bf16_rne(av);
-                    const uint32_t l = nmoe_bf16_rne(av - nmoe_bf16f(h));
-                    float part = nmoe_bf16f(h) + nmoe_bf16f(l);
-                    if (m < n) {
-                        const size_t o = (size_t)(p0 + m) * NMOE_INTER + 16 * span + slot;
-                        ahi[o] = (uint16_t)h;
-                        alo[o] = (uint16_t)l;
+                    for (int i = 0; i < 4; i++) {
+                        const uint32_t m = m0 + 16 * mb + 4 * kb + i;
+                        const float av = nmoe_silu_fast(acc[0][b2][mb][i]) * acc[1][b2][mb][i];
+                        const uint32_t h = nmoe_bf16_rne(av);
+                        const uint32_t l = nmoe_bf16_rne(av - nmoe_bf16f(h));
+                        float part = nmoe_bf16f(h) + nmoe_bf16f(l);
+                        if (m < n) {
+                            const size_t o = (size_t)(p0 + m) * NMOE_INTER + 16 * span + slot;
+                            ahi[o] = (uint16_t)h;
+                            alo[o] = (uint16_t)l;
+                        }
+                        part = nmoe_dpp_group_sum<16>(part); /* the 16 rows of this column block */
+                        part_sum[mb][i] = b2 == 0 ? part : part_sum[mb][i] + part;
                     }
-                    part = nmoe_dpp_group_sum<16>(part); /* the 16 rows of this column block */
-                    part_sum[mb][i] = b2 == 0 ? part : part_sum[mb][i] + part;
                 }
             }
+            if (col == 0)
+#pragma unroll
+                for (int mb = 0; mb < MB; mb++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++) s_as[wave][16 * mb + 4 * kb + i] = part_sum[mb][i];
         }
-        if (col == 0)
-#pragma unroll
-            for (int mb = 0; mb < 4; mb++)
-#pragma unroll
-                for (int i = 0; i < 4; i++) s_as[wave][16 * mb + 4 * kb + i] = part_sum[mb][i];
         nmoe_lds_barrier();
-        constexpr int DG = NT / 64;   /* down groups per tile */
-        constexpr int WPD = 8 / DG;   /* wavefronts per down group */
-        if (tid < DG * NMOE_MCHUNK) {
-            const int dg = tid / NMOE_MCHUNK, row = tid % NMOE_MCHUNK;
+        constexpr int DG = NT / 64;  /* down groups per tile */
+        constexpr int WPD = NW / DG; /* wavefronts per down group */
+        if (tid < DG * MCH) {
+            const int dg = tid / MCH, row = tid % MCH;
             const uint32_t m = m0 + row;
             float t = s_as[WPD * dg][row];
 #pragma unroll
@@ -705,28 +739,48 @@ nmoe_grouped_gateup_kernel(const uint8_t *pack, const uint16_t *xhi, const uint1
 
 /* ------------------------------------------------------------ down */
 
-#define NMOE_DN_ROWS 512 /* down rows per block: 64 per wavefront */
+/* Down rows per block of NW wavefronts: 64 a wavefront. */
+__host__ __device__ constexpr int nmoe_dn_rows(int nw) { return nw * 64; }
 
-/* Expert e, down rows 512 * nt .. +511: y[q][row] for all the expert's
- * entries q.  Eight wavefronts; wavefront w owns rows 64w..64w+63 of the
- * tile as four 16-row column blocks.  act enters as hi and lo bf16 planes. */
-template <int BITS>
-__global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
+/* LDS bytes of a down block with ns stages: the stages (act hi and lo rows,
+ * codes), the scales and s_q. */
+__host__ __device__ constexpr int nmoe_dn_lds(int bits, int nw, int ns) {
+    return ns * (2 * NMOE_MCHUNK * 128 + nmoe_dn_rows(nw) * (bits == 4 ? 32 : 16)) + nmoe_dn_rows(nw) * 16 +
+           4 * NMOE_MCHUNK;
+}
+__host__ __device__ constexpr int nmoe_dn_stages(int bits, int nw) {
+    return nmoe_dn_lds(bits, nw, 4) <= (nw == 8 ? 160 : 80) * 1024 - 512 ? 4 : 3;
+}
+
+/* Expert e, down rows NT * nt .. +NT-1: y[q][row] for all the expert's
+ * entries q, 64 per pass.  NW wavefronts (as in the gate/up kernel);
+ * wavefront w owns rows (NT/NW)w .. +NT/NW-1 of the tile as NB 16-row
+ * column blocks.  act enters as hi and lo bf16 planes. */
+template <int BITS, int NW>
+__global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
 nmoe_grouped_down_kernel(const uint8_t *pack, const uint16_t *ahi, const uint16_t *alo, const float *as,
                          const uint32_t *perm, const uint32_t *offsets, float *y) {
     using Q = nmoe_q<BITS>;
     using L = nmoe_layout<BITS>;
     constexpr int G = NMOE_INTER / NMOE_GROUP; /* 8 groups */
     static_assert(G == 8, "the correction's operand layout assumes 2 groups per lane");
-    constexpr int NT = NMOE_DN_ROWS;
-    constexpr int NB = NT / 128;
+    static_assert(NW == 8 || NW == 4, "eight or four wavefronts");
+    constexpr int NT = nmoe_dn_rows(NW);
+    constexpr int NB = NT / (16 * NW);
+    constexpr int MB = 4;           /* row blocks per full pass */
+    constexpr int MCH = NMOE_MCHUNK; /* entries per pass */
+    constexpr int AI = 8 / NW;      /* A instructions per plane and wavefront */
+    constexpr int NS = nmoe_dn_stages(BITS, NW);
     constexpr int WPG = BITS == 4 ? 8 : 4;
-    using CP = nmoe_code_plan<BITS, NT>;
+    using CP = nmoe_code_plan<BITS, NT, NW>;
     __shared__ uint16_t s_s[NT][G]; /* scales of the tile */
-    typedef nmoe_stage<2, NT * WPG> Stage;
+    typedef nmoe_stage<2, MCH, NT * WPG> Stage;
     __shared__ Stage s_st0, s_st1, s_st2, s_st3;
-    auto stage = [&](int st) -> Stage & { return st == 0 ? s_st0 : st == 1 ? s_st1 : st == 2 ? s_st2 : s_st3; };
-    __shared__ uint32_t s_q[NMOE_MCHUNK]; /* the chunk's output slots */
+    auto stage = [&](int st) -> Stage & {
+        if constexpr (NS == 3) return st == 0 ? s_st0 : st == 1 ? s_st1 : s_st2;
+        else return st == 0 ? s_st0 : st == 1 ? s_st1 : st == 2 ? s_st2 : s_st3;
+    };
+    __shared__ uint32_t s_q[MCH]; /* the chunk's output slots */
     int e, nt;
     nmoe_die_tile(blockIdx.x, NMOE_HIDDEN / NT, e, nt);
     const uint32_t p0 = offsets[e], n = offsets[e + 1] - p0;
@@ -734,74 +788,78 @@ nmoe_grouped_down_kernel(const uint8_t *pack, const uint16_t *ahi, const uint16_
     const int tid = threadIdx.x, lane = tid & 63, col = lane & 15, kb = lane >> 4;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint8_t *ex = pack + (size_t)e * L::expert_size;
-    const int rt0 = (NT / 8) * wave + col; /* tile row of column block nb: rt0 + 16 nb */
+    const int rt0 = (NT / NW) * wave + col; /* tile row of column block nb: rt0 + 16 nb */
     const uint32_t *cbase = (const uint32_t *)(ex + L::down_w) + (size_t)nt * NT * Q::WPR_D;
     const uint16_t *bias = (const uint16_t *)(ex + L::down_b) + (size_t)nt * NT * G;
-    for (uint32_t m0 = 0; m0 < n; m0 += NMOE_MCHUNK) {
-        const int nb = (int)min((n - m0 + 15) / 16, 4u);
+    for (uint32_t m0 = 0; m0 < n; m0 += MCH) {
         /* the chunk's output slots, stored to LDS after the stages are issued
          * (so that this load's wait does not hold them back) and visible
          * after the barrier below */
-        const uint32_t qv = tid < NMOE_MCHUNK ? perm[p0 + min(m0 + tid, n - 1)] : 0u;
-        /* this lane's A row for instruction `wave`: act row p0 + m0 + 8 wave + lane / 8 */
-        const uint32_t msrc = min(m0 + 8 * wave + (lane >> 3), n - 1);
+        const uint32_t qv = tid < MCH ? perm[p0 + min(m0 + tid, n - 1)] : 0u;
+        /* this lane's A row for instruction wave + NW i: act row p0 + m0 + 8 (wave + NW i) + lane / 8 */
+        uint32_t row_off[AI];
+#pragma unroll
+        for (int i = 0; i < AI; i++)
+            row_off[i] = (p0 + min(m0 + 8 * (wave + NW * i) + (lane >> 3), n - 1)) * (uint32_t)(NMOE_INTER * 2);
         const uint16_t *apl[2] = {ahi, alo};
-        const uint32_t row_off = (p0 + msrc) * (uint32_t)(NMOE_INTER * 2);
         auto issue = [&](int g, int st) {
 #pragma unroll
-            for (int pl = 0; pl < 2; pl++) nmoe_stage_rows(stage(st).a[pl], apl[pl] + 64 * g, row_off, wave, lane);
+            for (int pl = 0; pl < 2; pl++)
+#pragma unroll
+                for (int i = 0; i < AI; i++)
+                    nmoe_stage_rows(stage(st).a[pl], apl[pl] + 64 * g, row_off[i], wave + NW * i, lane);
 #pragma unroll
             for (int i = 0; i < CP::PER_WAVE; i++)
                 nmoe_stage_codes<BITS, NT, CP::WIDE>(stage(st).b, cbase + nmoe_gwords<BITS>() * g, Q::WPR_D,
                                                      CP::PER_WAVE * wave + i, lane);
         };
-        nmoe_f32x4 acc[NB][4];
+        const int nb = (int)min((n - m0 + 15) / 16, (uint32_t)MB);
+        nmoe_f32x4 acc[NB][MB];
         {
-            /* as in the gate/up kernel: the correction's operands (scales
-             * straight into LDS, every pass), then the first ring stages,
-             * then a wait that leaves only the stages in flight.
-             * A lane = (entry col, groups 2kb + tq), B lane = (row col,
-             * groups 2kb + tq) */
-            constexpr int PER = NT * G / 8 / 512;
-#pragma unroll
-            for (int q = 0; q < PER; q++)
+                /* as in the gate/up kernel: the correction's operands
+                 * (scales straight into LDS, one 16-byte chunk a thread,
+                 * every pass), then the first ring stages, then a wait that
+                 * leaves only the stages in flight.
+                 * A lane = (entry col, groups 2kb + tq), B lane = (row col,
+                 * groups 2kb + tq) */
+                static_assert(NT * G / 8 == 64 * NW, "one scale chunk per thread");
                 __builtin_amdgcn_global_load_lds(
-                    (const void *)((const uint4 *)(ex + L::down_s + (size_t)nt * NT * G * 2) + tid + 512 * q),
-                    (nmoe_lds_void *)((uint4 *)&s_s[0][0] + 512 * q + 64 * wave), 16, 0, 0);
-            float2 av[4];
-            uint32_t bv[NB];
+                    (const void *)((const uint4 *)(ex + L::down_s + (size_t)nt * NT * G * 2) + tid),
+                    (nmoe_lds_void *)((uint4 *)&s_s[0][0] + 64 * wave), 16, 0, 0);
+                float2 av[MB];
+                uint32_t bv[NB];
 #pragma unroll
-            for (int mb = 0; mb < 4; mb++)
-                av[mb] = *(const float2 *)(as + (size_t)(p0 + min(m0 + 16 * mb + col, n - 1)) * G + 2 * kb);
+                for (int mb = 0; mb < MB; mb++)
+                    av[mb] = *(const float2 *)(as + (size_t)(p0 + min(m0 + 16 * mb + col, n - 1)) * G + 2 * kb);
 #pragma unroll
-            for (int b2 = 0; b2 < NB; b2++) bv[b2] = *(const uint32_t *)(bias + (rt0 + 16 * b2) * G + 2 * kb);
+                for (int b2 = 0; b2 < NB; b2++) bv[b2] = *(const uint32_t *)(bias + (rt0 + 16 * b2) * G + 2 * kb);
 #pragma unroll
-            for (int st = 0; st < NMOE_NS - 1; st++) issue(st, st);
-            nmoe_wait_vm<(NMOE_NS - 1) * (2 + CP::PER_WAVE)>();
-            if (tid < NMOE_MCHUNK) s_q[tid] = qv;
-            nmoe_lds_barrier(); /* the scales and s_q */
-            float cv[NB][G / 4];
+                for (int st = 0; st < NS - 1; st++) issue(st, st);
+                nmoe_wait_vm<(NS - 1) * (2 * AI + CP::PER_WAVE)>();
+                if (tid < MCH) s_q[tid] = qv;
+                nmoe_lds_barrier(); /* the scales and s_q */
+                float cv[NB][G / 4];
 #pragma unroll
-            for (int b2 = 0; b2 < NB; b2++) {
-                const uint32_t sw = *(const uint32_t *)&s_s[rt0 + 16 * b2][2 * kb];
-                cv[b2][0] = __uint_as_float(bv[b2] << 16) - 128.0f * __uint_as_float(sw << 16);
-                cv[b2][1] = __uint_as_float(bv[b2] & 0xffff0000u) - 128.0f * __uint_as_float(sw & 0xffff0000u);
+                for (int b2 = 0; b2 < NB; b2++) {
+                    const uint32_t sw = *(const uint32_t *)&s_s[rt0 + 16 * b2][2 * kb];
+                    cv[b2][0] = __uint_as_float(bv[b2] << 16) - 128.0f * __uint_as_float(sw << 16);
+                    cv[b2][1] = __uint_as_float(bv[b2] & 0xffff0000u) - 128.0f * __uint_as_float(sw & 0xffff0000u);
 #pragma unroll
-                for (int mb = 0; mb < 4; mb++) acc[b2][mb] = nmoe_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-            }
+                    for (int mb = 0; mb < MB; mb++) acc[b2][mb] = nmoe_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+                }
 #pragma unroll
-            for (int tq = 0; tq < G / 4; tq++)
+                for (int tq = 0; tq < G / 4; tq++)
 #pragma unroll
-                for (int mb = 0; mb < 4; mb++)
-                    if (mb < nb)
+                    for (int mb = 0; mb < MB; mb++)
+                        if (mb < nb)
 #pragma unroll
                         for (int b2 = 0; b2 < NB; b2++)
                             acc[b2][mb] = __builtin_amdgcn_mfma_f32_16x16x4f32(tq == 0 ? av[mb].x : av[mb].y,
                                                                                cv[b2][tq], acc[b2][mb], 0, 0, 0);
         }
         auto step = [&](int g, const int st, const bool ahead) {
-            nmoe_ring_step_barrier<2 + CP::PER_WAVE, G, NMOE_NS>(g);
-            if (ahead) issue(g + NMOE_NS - 1, (st + NMOE_NS - 1) % NMOE_NS);
+            nmoe_ring_step_barrier<2 * AI + CP::PER_WAVE, G, NS>(g);
+            if (ahead) issue(g + NS - 1, (st + NS - 1) % NS);
             uint4 bq[NB][2];
             float sg[NB];
 #pragma unroll
@@ -812,7 +870,7 @@ nmoe_grouped_down_kernel(const uint8_t *pack, const uint16_t *ahi, const uint16_
                 sg[b2] = nmoe_bf16f(s_s[rt0 + 16 * b2][g]);
             }
 #pragma unroll
-            for (int mb = 0; mb < 4; mb++) {
+            for (int mb = 0; mb < MB; mb++) {
                 if (mb < nb) {
                     uint4 h0, h1, l0, l1;
                     nmoe_stage_operand(stage(st).a[0], 16 * mb + col, kb, h0, h1);
@@ -829,12 +887,12 @@ nmoe_grouped_down_kernel(const uint8_t *pack, const uint16_t *ahi, const uint16_
                 }
             }
         };
-        nmoe_ring_run<G, NMOE_NS>(step);
+        nmoe_ring_run<G, NS>(step);
 #pragma unroll
         for (int b2 = 0; b2 < NB; b2++) {
             const int r = nt * NT + rt0 + 16 * b2;
 #pragma unroll
-            for (int mb = 0; mb < 4; mb++) {
+            for (int mb = 0; mb < MB; mb++) {
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
                     const uint32_t m = m0 + 16 * mb + 4 * kb + i;
@@ -949,20 +1007,23 @@ static int nmoe_grouped_run(nmoe_hip_ctx *ctx, const uint8_t *pack, const void *
         hipLaunchKernelGGL((nmoe_grouped_prep_kernel<BITS, float>), gprep, dim3(256), 0, s, idx, ntok, k,
                            ctx->g_counts, ctx->g_perm, ctx->g_offsets, ctx->sync, (const float *)x, ctx->g_xhi,
                            ctx->g_xlo, ctx->g_xs);
-    const dim3 ggu(NMOE_EXPERTS * (NMOE_INTER / nmoe_gu_rows(bf ? 1 : 2))), gdn(NMOE_EXPERTS * (NMOE_HIDDEN / NMOE_DN_ROWS));
+    constexpr int NW = NMOE_GROUPED_NW;
+    const dim3 blk(64 * NW);
+    const dim3 ggu(NMOE_EXPERTS * (NMOE_INTER / nmoe_gu_rows(bf ? 1 : 2, NW))),
+        gdn(NMOE_EXPERTS * (NMOE_HIDDEN / nmoe_dn_rows(NW)));
+    const uint16_t *xhi = (const uint16_t *)ctx->g_xhi, *xlo = (const uint16_t *)ctx->g_xlo;
+    const uint32_t *perm = (const uint32_t *)ctx->g_perm, *offsets = (const uint32_t *)ctx->g_offsets;
+    const uint16_t *ahi = (const uint16_t *)ctx->g_ahi, *alo = (const uint16_t *)ctx->g_alo;
+    const float *xs = (const float *)ctx->g_xs, *as = (const float *)ctx->g_as;
+    /* gate/up, then down */
     if (bf)
-        hipLaunchKernelGGL((nmoe_grouped_gateup_kernel<BITS, 1>), ggu, dim3(512), 0, s, pack,
-                           (const uint16_t *)ctx->g_xhi, (const uint16_t *)ctx->g_xlo, (const float *)ctx->g_xs,
-                           (const uint32_t *)ctx->g_perm, (const uint32_t *)ctx->g_offsets, k, ctx->g_ahi,
-                           ctx->g_alo, ctx->g_as);
+        hipLaunchKernelGGL((nmoe_grouped_gateup_kernel<BITS, 1, NW>), ggu, blk, 0, s, pack, xhi, xlo, xs, perm, offsets, k,
+                           ctx->g_ahi, ctx->g_alo, ctx->g_as);
     else
-        hipLaunchKernelGGL((nmoe_grouped_gateup_kernel<BITS, 2>), ggu, dim3(512), 0, s, pack,
-                           (const uint16_t *)ctx->g_xhi, (const uint16_t *)ctx->g_xlo, (const float *)ctx->g_xs,
-                           (const uint32_t *)ctx->g_perm, (const uint32_t *)ctx->g_offsets, k, ctx->g_ahi,
-                           ctx->g_alo, ctx->g_as);
-    hipLaunchKernelGGL((nmoe_grouped_down_kernel<BITS>), gdn, dim3(512), 0, s, pack, (const uint16_t *)ctx->g_ahi,
-                       (const uint16_t *)ctx->g_alo, (const float *)ctx->g_as, (const uint32_t *)ctx->g_perm,
-                       (const uint32_t *)ctx->g_offsets, ctx->g_y);
+        hipLaunchKernelGGL((nmoe_grouped_gateup_kernel<BITS, 2, NW>), ggu, blk, 0, s, pack, xhi, xlo, xs, perm, offsets, k,
+                           ctx->g_ahi, ctx->g_alo, ctx->g_as);
+    hipLaunchKernelGGL((nmoe_grouped_down_kernel<BITS, NW>), gdn, blk, 0, s, pack, ahi, alo, as, perm, offsets,
+                       ctx->g_y);
     if (nmoe_aligned(h_mid, 16) && nmoe_aligned(out, 16) && (shared_out == NULL || nmoe_aligned(shared_out, 16)))
         hipLaunchKernelGGL(nmoe_grouped_combine_kernel, dim3(NMOE_HIDDEN / 1024, ntok), dim3(256), 0, s,
                            (const float *)ctx->g_y, idx, w, k, h_mid, shared_out, shared_gate_raw, out);

@@ -622,6 +622,43 @@ def test_prefill_2048_sampled(big, nh, bits):
     assert_close(got, want, what=f"prefill q{bits}")
 
 
+@pytest.mark.parametrize("bits", [4, 2])
+@pytest.mark.parametrize("xkind", ["bf16", "f32"])
+def test_grouped_zipf_1200_sampled(big, nh, bits, xkind):
+    """1200 tokens x 8 entries with Zipf routing: several hundred entries on
+    the hottest experts (many 64-entry passes, every row-block count in the
+    last one) and a handful on the tail; outputs on 40 sampled tokens (token
+    3 with an invalid slot among them) against the oracle."""
+    rng = np.random.default_rng(128 + 10 * bits + (xkind == "f32"))
+    seed, layer, ntok, k = 37, 56 + bits, 1200, 8
+    big.synth_layer(layer, bits, seed, SIGMA[bits])
+    idx = zipf_idx(rng, ntok, k)
+    counts = np.bincount(idx[:, :k].ravel(), minlength=256)
+    assert counts.max() > 256
+    w = rng.dirichlet(np.ones(k), size=ntok).astype(np.float32)
+    idx[3, 1] = 999
+    w_eff = w.copy()
+    w_eff[3, 1] = 0.0
+    idx_eff = idx.copy()
+    idx_eff[3, 1] = idx[3, 0]
+    xf = rng.standard_normal((ntok, 2048)).astype(np.float32)
+    if xkind == "bf16":
+        xb = B.f32_to_bf16(xf)
+        x, xdev, dt = B.bf16_to_f32(xb).reshape(ntok, 2048), xb, nh.BF16
+    else:
+        x, xdev, dt = xf, xf, nh.F32
+    h = rng.standard_normal((ntok, 2048)).astype(np.float32)
+    d = [big.to_device(a) for a in (xdev, idx, w, h)]
+    out = big.alloc(ntok * 2048 * 4)
+    big._check(big.experts(bits, layer, d[0], dt, ntok, k, d[1], d[2], d[3], out))
+    assert big.device_status() == nh.OK
+    sample = np.concatenate([[3], rng.choice(np.arange(4, ntok), 39, replace=False)])
+    got = out.download(np.float32, (ntok, 2048))[sample]
+    pack = host_pack(bits, seed, layer, idx_eff[sample, :k].ravel())
+    want = B.moe_experts(pack, bits, x[sample], k, idx_eff[sample], w_eff[sample], h[sample])
+    assert_close(got, want, what=f"zipf 1200 q{bits} x={xkind}")
+
+
 @pytest.mark.parametrize("xdt,ntok", [("f32", 1), ("bf16", 1), ("f32", 5), ("bf16", 6)])
 def test_shared_expert_against_oracle(ctx, nh, xdt, ntok):
     """nmoe_moe_shared_expert (kernels.metal:421-469, 510-513, 1520-1537)
