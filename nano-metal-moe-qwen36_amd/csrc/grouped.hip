@@ -500,8 +500,8 @@ __host__ __device__ constexpr int nmoe_gu_stages(int bits, int xpl, int nw) {
 template <int BITS, int XPL, int NW>
 __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
 nmoe_grouped_gateup_kernel(const uint8_t *pack, const uint16_t *xhi, const uint16_t *xlo, const float *xs,
-                           const uint32_t *perm, const uint32_t *offsets, int k, uint16_t *ahi, uint16_t *alo,
-                           float *as) {
+                           const uint32_t *perm, const uint32_t *offsets, int k, int lanes, uint16_t *ahi,
+                           uint16_t *alo, float *as) {
     using Q = nmoe_q<BITS>;
     using L = nmoe_layout<BITS>;
     constexpr int G = NMOE_HIDDEN / NMOE_GROUP; /* 32 groups */
@@ -530,10 +530,13 @@ nmoe_grouped_gateup_kernel(const uint8_t *pack, const uint16_t *xhi, const uint1
     };
     __shared__ uint32_t s_tok[MCH];
     __shared__ float s_as[NW][MCH];
+    /* pass lane pl of `lanes`: passes pl, pl + lanes, ... of tile (e, nt) */
+    constexpr int NTILE = NMOE_INTER / NT;
+    const int pl = blockIdx.x / (NMOE_EXPERTS * NTILE);
     int e, nt;
-    nmoe_die_tile(blockIdx.x, NMOE_INTER / NT, e, nt);
+    nmoe_die_tile(blockIdx.x % (NMOE_EXPERTS * NTILE), NTILE, e, nt);
     const uint32_t p0 = offsets[e], n = offsets[e + 1] - p0;
-    if (n == 0) return;
+    if (n <= (uint32_t)(pl * MCH)) return;
     const int tid = threadIdx.x, lane = tid & 63, col = lane & 15, kb = lane >> 4;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint8_t *ex = pack + (size_t)e * L::expert_size;
@@ -546,7 +549,7 @@ nmoe_grouped_gateup_kernel(const uint8_t *pack, const uint16_t *xhi, const uint1
     const uint16_t *bias[2] = {(const uint16_t *)(ex + L::gate_b) + (size_t)nt * NT * G,
                                (const uint16_t *)(ex + L::up_b) + (size_t)nt * NT * G};
 
-    for (uint32_t m0 = 0; m0 < n; m0 += MCH) {
+    for (uint32_t m0 = pl * MCH; m0 < n; m0 += lanes * MCH) {
         if (tid < MCH) s_tok[tid] = perm[p0 + min(m0 + tid, n - 1)] / (uint32_t)k;
         nmoe_lds_barrier();
         /* this lane's A row for instruction wave + NW i: entry 8 (wave + NW i) + lane / 8 */
@@ -759,7 +762,7 @@ __host__ __device__ constexpr int nmoe_dn_stages(int bits, int nw) {
 template <int BITS, int NW>
 __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
 nmoe_grouped_down_kernel(const uint8_t *pack, const uint16_t *ahi, const uint16_t *alo, const float *as,
-                         const uint32_t *perm, const uint32_t *offsets, float *y) {
+                         const uint32_t *perm, const uint32_t *offsets, int lanes, float *y) {
     using Q = nmoe_q<BITS>;
     using L = nmoe_layout<BITS>;
     constexpr int G = NMOE_INTER / NMOE_GROUP; /* 8 groups */
@@ -781,17 +784,19 @@ nmoe_grouped_down_kernel(const uint8_t *pack, const uint16_t *ahi, const uint16_
         else return st == 0 ? s_st0 : st == 1 ? s_st1 : st == 2 ? s_st2 : s_st3;
     };
     __shared__ uint32_t s_q[MCH]; /* the chunk's output slots */
+    constexpr int NTILE = NMOE_HIDDEN / NT;
+    const int pl = blockIdx.x / (NMOE_EXPERTS * NTILE); /* pass lane, as in the gate/up kernel */
     int e, nt;
-    nmoe_die_tile(blockIdx.x, NMOE_HIDDEN / NT, e, nt);
+    nmoe_die_tile(blockIdx.x % (NMOE_EXPERTS * NTILE), NTILE, e, nt);
     const uint32_t p0 = offsets[e], n = offsets[e + 1] - p0;
-    if (n == 0) return;
+    if (n <= (uint32_t)(pl * MCH)) return;
     const int tid = threadIdx.x, lane = tid & 63, col = lane & 15, kb = lane >> 4;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint8_t *ex = pack + (size_t)e * L::expert_size;
     const int rt0 = (NT / NW) * wave + col; /* tile row of column block nb: rt0 + 16 nb */
     const uint32_t *cbase = (const uint32_t *)(ex + L::down_w) + (size_t)nt * NT * Q::WPR_D;
     const uint16_t *bias = (const uint16_t *)(ex + L::down_b) + (size_t)nt * NT * G;
-    for (uint32_t m0 = 0; m0 < n; m0 += MCH) {
+    for (uint32_t m0 = pl * MCH; m0 < n; m0 += lanes * MCH) {
         /* the chunk's output slots, stored to LDS after the stages are issued
          * (so that this load's wait does not hold them back) and visible
          * after the barrier below */
@@ -1009,8 +1014,12 @@ static int nmoe_grouped_run(nmoe_hip_ctx *ctx, const uint8_t *pack, const void *
                            ctx->g_xlo, ctx->g_xs);
     constexpr int NW = NMOE_GROUPED_NW;
     const dim3 blk(64 * NW);
-    const dim3 ggu(NMOE_EXPERTS * (NMOE_INTER / nmoe_gu_rows(bf ? 1 : 2, NW))),
-        gdn(NMOE_EXPERTS * (NMOE_HIDDEN / nmoe_dn_rows(NW)));
+    /* two pass lanes once an expert averages more than half a pass: the
+     * passes of a large expert's tile then run in blocks of their own, side
+     * by side (on the same die, so the second reads the codes from L2) */
+    const int lanes = (long)ntok * k > (long)NMOE_EXPERTS * NMOE_MCHUNK / 2 ? 2 : 1;
+    const dim3 ggu(lanes * NMOE_EXPERTS * (NMOE_INTER / nmoe_gu_rows(bf ? 1 : 2, NW))),
+        gdn(lanes * NMOE_EXPERTS * (NMOE_HIDDEN / nmoe_dn_rows(NW)));
     const uint16_t *xhi = (const uint16_t *)ctx->g_xhi, *xlo = (const uint16_t *)ctx->g_xlo;
     const uint32_t *perm = (const uint32_t *)ctx->g_perm, *offsets = (const uint32_t *)ctx->g_offsets;
     const uint16_t *ahi = (const uint16_t *)ctx->g_ahi, *alo = (const uint16_t *)ctx->g_alo;
@@ -1018,11 +1027,11 @@ static int nmoe_grouped_run(nmoe_hip_ctx *ctx, const uint8_t *pack, const void *
     /* gate/up, then down */
     if (bf)
         hipLaunchKernelGGL((nmoe_grouped_gateup_kernel<BITS, 1, NW>), ggu, blk, 0, s, pack, xhi, xlo, xs, perm, offsets, k,
-                           ctx->g_ahi, ctx->g_alo, ctx->g_as);
+                           lanes, ctx->g_ahi, ctx->g_alo, ctx->g_as);
     else
         hipLaunchKernelGGL((nmoe_grouped_gateup_kernel<BITS, 2, NW>), ggu, blk, 0, s, pack, xhi, xlo, xs, perm, offsets, k,
-                           ctx->g_ahi, ctx->g_alo, ctx->g_as);
-    hipLaunchKernelGGL((nmoe_grouped_down_kernel<BITS, NW>), gdn, blk, 0, s, pack, ahi, alo, as, perm, offsets,
+                           lanes, ctx->g_ahi, ctx->g_alo, ctx->g_as);
+    hipLaunchKernelGGL((nmoe_grouped_down_kernel<BITS, NW>), gdn, blk, 0, s, pack, ahi, alo, as, perm, offsets, lanes,
                        ctx->g_y);
     if (nmoe_aligned(h_mid, 16) && nmoe_aligned(out, 16) && (shared_out == NULL || nmoe_aligned(shared_out, 16)))
         hipLaunchKernelGGL(nmoe_grouped_combine_kernel, dim3(NMOE_HIDDEN / 1024, ntok), dim3(256), 0, s,
