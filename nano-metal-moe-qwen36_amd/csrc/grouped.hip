@@ -48,7 +48,16 @@
 typedef __attribute__((ext_vector_type(8))) __bf16 nmoe_bf16x8;
 typedef __attribute__((ext_vector_type(4))) float nmoe_f32x4;
 
-#define NMOE_DISPATCH_BLOCKS 16
+/* Dispatch blocks: one up to 1,024 entries (its histogram never leaves
+ * LDS), else a power of two up to 64 so that a slice is one 256-entry chunk
+ * while the entries fit (16,384 of them). */
+#define NMOE_DISPATCH_MAX 64
+__host__ __device__ constexpr int nmoe_dispatch_blocks(int n) {
+    if (n <= 1024) return 1;
+    int nd = 8;
+    while (nd < NMOE_DISPATCH_MAX && nd * 256 < n) nd *= 2;
+    return nd;
+}
 #define NMOE_MCHUNK 64 /* expert rows (entries) per pass: four 16-row MFMA blocks */
 /* Wavefronts per gate/up and down block: 8 (one block a CU) or 4 (two). */
 #ifndef NMOE_GROUPED_NW
@@ -119,50 +128,84 @@ __device__ __forceinline__ uint32_t nmoe_entry_expert(const uint32_t *idx, int q
     return e < NMOE_EXPERTS ? e : (uint32_t)NMOE_EXPERTS; /* 256: left out */
 }
 
-/* D1: counts[b][257] = expert histogram of entry slice b. */
-__device__ __forceinline__ void nmoe_dispatch_count(const uint32_t *idx, int ntok, int k, uint32_t *counts, int b) {
-    __shared__ uint32_t h[NMOE_EXPERTS + 1];
+#define NMOE_DISPATCH_PRE 4 /* chunks of a slice whose entries are read up front */
+
+/* This thread's entries of the first NMOE_DISPATCH_PRE chunks of slice b
+ * (256 past the slice's end), all loads in flight together; read once for
+ * both phases. */
+__device__ __forceinline__ void nmoe_dispatch_entries(const uint32_t *idx, int ntok, int k, int b, int nd,
+                                                      uint32_t *ev) {
+    const int n = ntok * k, per = (n + nd - 1) / nd, q1 = min(n, (b + 1) * per);
+#pragma unroll
+    for (int j = 0; j < NMOE_DISPATCH_PRE; j++) {
+        const int q = b * per + 256 * j + (int)threadIdx.x;
+        ev[j] = q < q1 ? nmoe_entry_expert(idx, q, k) : (uint32_t)NMOE_EXPERTS;
+    }
+}
+
+/* D1: h = expert histogram of entry slice b of nd (in LDS). */
+__device__ __forceinline__ void nmoe_dispatch_count(const uint32_t *idx, int ntok, int k, uint32_t *h, int b, int nd,
+                                                    const uint32_t *ev) {
     const int tid = threadIdx.x, n = ntok * k;
-    const int per = (n + NMOE_DISPATCH_BLOCKS - 1) / NMOE_DISPATCH_BLOCKS;
+    const int per = (n + nd - 1) / nd;
     for (int i = tid; i <= NMOE_EXPERTS; i += 256) h[i] = 0;
     __syncthreads();
     const int q1 = min(n, (b + 1) * per);
-    for (int q = b * per + tid; q < q1; q += 256) atomicAdd(&h[nmoe_entry_expert(idx, q, k)], 1u);
+#pragma unroll
+    for (int j = 0; j < NMOE_DISPATCH_PRE; j++)
+        if (b * per + 256 * j + tid < q1) atomicAdd(&h[ev[j]], 1u);
+    for (int q = b * per + 256 * NMOE_DISPATCH_PRE + tid; q < q1; q += 256)
+        atomicAdd(&h[nmoe_entry_expert(idx, q, k)], 1u);
     __syncthreads();
-    for (int i = tid; i <= NMOE_EXPERTS; i += 256) counts[b * (NMOE_EXPERTS + 1) + i] = h[i];
 }
 
-/* D2: offsets (block 0 writes them) and the stable permutation of slice b:
+/* D2: offsets (block 0 writes them) and the stable permutation of slice b
+ * (the slices' histograms from counts, or from h when there is one slice):
  * chunks of 256 entries in order; within a chunk the rank of an entry is
  * its rank among the equal-expert lanes of its wavefront (a 9-bit
  * multi-split by ballots) plus the counts of the earlier wavefronts. */
-__device__ __forceinline__ void nmoe_dispatch_scatter(const uint32_t *idx, int ntok, int k, const uint32_t *counts,
-                                                      uint32_t *perm, uint32_t *offsets, int b) {
+__device__ __forceinline__ void nmoe_dispatch_scatter(const uint32_t *idx, int ntok, int k, uint32_t *counts,
+                                                      const uint32_t *h, uint32_t *perm, uint32_t *offsets, int b,
+                                                      int nd, const uint32_t *ev) {
     __shared__ uint32_t s_base[NMOE_EXPERTS];
-    __shared__ uint32_t s_scan[256];
+    __shared__ uint32_t s_scan[4]; /* the wavefronts' totals */
     __shared__ uint32_t s_wc[4][NMOE_EXPERTS + 1];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, n = ntok * k;
-    const int per = (n + NMOE_DISPATCH_BLOCKS - 1) / NMOE_DISPATCH_BLOCKS;
-    /* thread e: total of expert e and its count in the slices before b */
+    const int per = (n + nd - 1) / nd;
+    /* thread e: total of expert e and its count in the slices before b.  All
+     * NMOE_DISPATCH_MAX slices are loaded at once (the buffer holds that
+     * many; those at nd and above are masked), so the loads are in flight
+     * together rather than one latency each. */
     uint32_t total = 0, before = 0;
-    for (int bb = 0; bb < NMOE_DISPATCH_BLOCKS; bb++) {
-        const uint32_t c = counts[bb * (NMOE_EXPERTS + 1) + tid];
-        total += c;
-        before += bb < b ? c : 0u;
+    if (nd == 1) {
+        total = h[tid];
+    } else {
+        uint32_t cs[NMOE_DISPATCH_MAX];
+#pragma unroll
+        for (int bb = 0; bb < NMOE_DISPATCH_MAX; bb++) cs[bb] = nmoe_ld_u32_dev(&counts[bb * (NMOE_EXPERTS + 1) + tid]);
+#pragma unroll
+        for (int bb = 0; bb < NMOE_DISPATCH_MAX; bb++) {
+            const uint32_t c = bb < nd ? cs[bb] : 0u;
+            total += c;
+            before += bb < b ? c : 0u;
+        }
     }
-    /* exclusive scan of total over the 256 experts (Hillis-Steele in LDS) */
-    s_scan[tid] = total;
+    /* exclusive scan of total over the 256 experts: an inclusive scan within
+     * each wavefront (six shuffles), then the earlier wavefronts' totals */
+    uint32_t inc = total;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const uint32_t v = (uint32_t)__shfl_up((int)inc, d, 64);
+        inc += lane >= d ? v : 0u;
+    }
+    if (lane == 63) s_scan[wave] = inc;
     __syncthreads();
-    for (int d = 1; d < 256; d <<= 1) {
-        const uint32_t v = tid >= d ? s_scan[tid - d] : 0u;
-        __syncthreads();
-        s_scan[tid] += v;
-        __syncthreads();
-    }
-    const uint32_t off = s_scan[tid] - total;
+    uint32_t prior = 0;
+    for (int w = 0; w < wave; w++) prior += s_scan[w];
+    const uint32_t off = prior + inc - total;
     if (b == 0) {
         offsets[tid] = off;
-        if (tid == 255) offsets[NMOE_EXPERTS] = s_scan[255];
+        if (tid == 255) offsets[NMOE_EXPERTS] = off + total;
     }
     s_base[tid] = off + before;
     for (int i = tid; i < 4 * (NMOE_EXPERTS + 1); i += 256) (&s_wc[0][0])[i] = 0;
@@ -170,7 +213,13 @@ __device__ __forceinline__ void nmoe_dispatch_scatter(const uint32_t *idx, int n
     const int q0 = b * per, q1 = min(n, (b + 1) * per);
     for (int c0 = q0; c0 < q1; c0 += 256) {
         const int q = c0 + tid;
-        const uint32_t e = q < q1 ? nmoe_entry_expert(idx, q, k) : (uint32_t)NMOE_EXPERTS;
+        /* chunk j: read up front for the first NMOE_DISPATCH_PRE, else now */
+        const int j = (c0 - q0) / 256;
+        uint32_t e = (uint32_t)NMOE_EXPERTS;
+#pragma unroll
+        for (int jj = 0; jj < NMOE_DISPATCH_PRE; jj++)
+            if (j == jj) e = ev[jj];
+        if (j >= NMOE_DISPATCH_PRE && q < q1) e = nmoe_entry_expert(idx, q, k);
         uint64_t peers = ~0ull;
 #pragma unroll
         for (int bit = 0; bit < 9; bit++) {
@@ -234,40 +283,52 @@ __device__ __forceinline__ void nmoe_grouped_xprep(const XT *x, uint16_t *xhi, u
     if ((tid & 7) == 0) xs[(size_t)t * (NMOE_HIDDEN / NMOE_GROUP) + (tid >> 3)] = sum;
 }
 
-/* One launch for the grouped path's preparation: blocks 0..15 run the
+/* One launch for the grouped path's preparation: blocks 0 .. nd-1 run the
  * dispatch (D1, then D2 once every slice's histogram is in), the blocks
- * after them prepare one token's x each (none when x is NULL).  The 16
- * dispatch blocks are the grid's first, so they are resident together;
- * they meet at a counter in the sync words that only ever grows by 16 per
- * launch (bounded wait; an expired wait sets the status word). */
+ * after them prepare one token's x each (none when x is NULL).  With more
+ * than one dispatch block, the nd blocks (the grid's first, so resident
+ * together) meet at a counter in the sync words that grows by exactly 64
+ * per launch (64 / nd from each block; bounded wait, an expired wait sets
+ * the status word); a single block keeps its histogram in LDS. */
 template <int BITS, typename XT>
-__global__ void __launch_bounds__(256) nmoe_grouped_prep_kernel(const uint32_t *idx, int ntok, int k, uint32_t *counts,
-                                                                uint32_t *perm, uint32_t *offsets, uint32_t *sync,
-                                                                const XT *x, uint16_t *xhi, uint16_t *xlo, float *xs) {
+__global__ void __launch_bounds__(256) nmoe_grouped_prep_kernel(const uint32_t *idx, int ntok, int k, int nd,
+                                                                uint32_t *counts, uint32_t *perm, uint32_t *offsets,
+                                                                uint32_t *sync, const XT *x, uint16_t *xhi,
+                                                                uint16_t *xlo, float *xs) {
     const int b = blockIdx.x;
-    if (b >= NMOE_DISPATCH_BLOCKS) {
-        nmoe_grouped_xprep<BITS, XT>(x, xhi, xlo, xs, b - NMOE_DISPATCH_BLOCKS);
+    if (b >= nd) {
+        nmoe_grouped_xprep<BITS, XT>(x, xhi, xlo, xs, b - nd);
         return;
     }
-    nmoe_dispatch_count(idx, ntok, k, counts, b);
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent"); /* this slice's histogram, to the other blocks */
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        uint32_t *cnt = sync + NMOE_SYNC_DISPATCH;
-        const uint32_t old = nmoe_add_u32_dev(cnt, 1u);
-        const uint32_t target = (old / NMOE_DISPATCH_BLOCKS + 1u) * NMOE_DISPATCH_BLOCKS;
-        uint32_t spins = 0;
-        while ((int32_t)(nmoe_ld_u32_dev(cnt) - target) < 0) {
-            __builtin_amdgcn_s_sleep(1);
-            if (++spins > NMOE_SPIN_LIMIT) {
-                __hip_atomic_store(sync + NMOE_SYNC_STATUS, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                break;
+    uint32_t ev[NMOE_DISPATCH_PRE];
+    nmoe_dispatch_entries(idx, ntok, k, b, nd, ev);
+    __shared__ uint32_t h[NMOE_EXPERTS + 1];
+    nmoe_dispatch_count(idx, ntok, k, h, b, nd, ev);
+    if (nd > 1) {
+        /* publish the histogram with device-coherent stores, completed
+         * (vmcnt 0) before the arrival is counted: no agent-scope release
+         * fence, whose L2 writeback would wait for every dirty line of the
+         * die (the x planes the other blocks are writing) */
+        for (int i = threadIdx.x; i <= NMOE_EXPERTS; i += 256)
+            __hip_atomic_store(&counts[b * (NMOE_EXPERTS + 1) + i], h[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __builtin_amdgcn_s_waitcnt(0x0F70); /* vmcnt(0) */
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            uint32_t *cnt = sync + NMOE_SYNC_DISPATCH;
+            const uint32_t old = nmoe_add_u32_dev(cnt, (uint32_t)(NMOE_DISPATCH_MAX / nd));
+            const uint32_t target = (old / NMOE_DISPATCH_MAX + 1u) * NMOE_DISPATCH_MAX;
+            uint32_t spins = 0;
+            while ((int32_t)(nmoe_ld_u32_dev(cnt) - target) < 0) {
+                __builtin_amdgcn_s_sleep(1);
+                if (++spins > NMOE_SPIN_LIMIT) {
+                    __hip_atomic_store(sync + NMOE_SYNC_STATUS, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    break;
+                }
             }
         }
+        __syncthreads(); /* (the histograms are then read with device-coherent loads) */
     }
-    __syncthreads();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent"); /* the other slices' histograms */
-    nmoe_dispatch_scatter(idx, ntok, k, counts, perm, offsets, b);
+    nmoe_dispatch_scatter(idx, ntok, k, counts, h, perm, offsets, b, nd, ev);
 }
 
 /* ------------------------------------------------------------ stage ring */
@@ -967,7 +1028,7 @@ __global__ void __launch_bounds__(256) nmoe_grouped_combine_kernel(const float *
 extern "C" int nmoe_grouped_init(nmoe_hip_ctx *ctx) {
     const size_t mt = (size_t)ctx->max_tokens, rows = mt * NMOE_MAX_K;
     ctx->grouped_min_tokens = 8;
-    if (hipMalloc((void **)&ctx->g_counts, NMOE_DISPATCH_BLOCKS * (NMOE_EXPERTS + 1) * sizeof(uint32_t)) != hipSuccess ||
+    if (hipMalloc((void **)&ctx->g_counts, NMOE_DISPATCH_MAX * (NMOE_EXPERTS + 1) * sizeof(uint32_t)) != hipSuccess ||
         hipMalloc((void **)&ctx->g_perm, rows * sizeof(uint32_t)) != hipSuccess ||
         hipMalloc((void **)&ctx->g_offsets, (NMOE_EXPERTS + 1) * sizeof(uint32_t)) != hipSuccess ||
         hipMalloc((void **)&ctx->g_xhi, mt * NMOE_HIDDEN * sizeof(uint16_t)) != hipSuccess ||
@@ -991,8 +1052,9 @@ extern "C" void nmoe_grouped_free(nmoe_hip_ctx *ctx) {
 /* D1 + D2 into perm / offsets (any device buffers of T*k and 257 words). */
 extern "C" int nmoe_grouped_dispatch(nmoe_hip_ctx *ctx, const uint32_t *idx, int ntok, int k, uint32_t *perm,
                                      uint32_t *offsets, hipStream_t s) {
-    hipLaunchKernelGGL((nmoe_grouped_prep_kernel<4, uint16_t>), dim3(NMOE_DISPATCH_BLOCKS), dim3(256), 0, s, idx, ntok,
-                       k, ctx->g_counts, perm, offsets, ctx->sync, (const uint16_t *)NULL, (uint16_t *)NULL,
+    const int nd = nmoe_dispatch_blocks(ntok * k);
+    hipLaunchKernelGGL((nmoe_grouped_prep_kernel<4, uint16_t>), dim3(nd), dim3(256), 0, s, idx, ntok, k, nd,
+                       ctx->g_counts, perm, offsets, ctx->sync, (const uint16_t *)NULL, (uint16_t *)NULL,
                        (uint16_t *)NULL, (float *)NULL);
     const hipError_t e = hipGetLastError();
     return e == hipSuccess ? NMOE_HIP_OK : nmoe_hip_check(ctx, e, "dispatch launch");
@@ -1003,13 +1065,14 @@ static int nmoe_grouped_run(nmoe_hip_ctx *ctx, const uint8_t *pack, const void *
                             const uint32_t *idx, const float *w, const float *h_mid, const float *shared_out,
                             const float *shared_gate_raw, float *out, hipStream_t s) {
     const bool bf = x_dtype == NMOE_HIP_BF16;
-    const dim3 gprep(NMOE_DISPATCH_BLOCKS + ntok);
+    const int nd = nmoe_dispatch_blocks(ntok * k);
+    const dim3 gprep(nd + ntok);
     if (bf)
-        hipLaunchKernelGGL((nmoe_grouped_prep_kernel<BITS, uint16_t>), gprep, dim3(256), 0, s, idx, ntok, k,
+        hipLaunchKernelGGL((nmoe_grouped_prep_kernel<BITS, uint16_t>), gprep, dim3(256), 0, s, idx, ntok, k, nd,
                            ctx->g_counts, ctx->g_perm, ctx->g_offsets, ctx->sync, (const uint16_t *)x, ctx->g_xhi,
                            (uint16_t *)NULL, ctx->g_xs);
     else
-        hipLaunchKernelGGL((nmoe_grouped_prep_kernel<BITS, float>), gprep, dim3(256), 0, s, idx, ntok, k,
+        hipLaunchKernelGGL((nmoe_grouped_prep_kernel<BITS, float>), gprep, dim3(256), 0, s, idx, ntok, k, nd,
                            ctx->g_counts, ctx->g_perm, ctx->g_offsets, ctx->sync, (const float *)x, ctx->g_xhi,
                            ctx->g_xlo, ctx->g_xs);
     constexpr int NW = NMOE_GROUPED_NW;

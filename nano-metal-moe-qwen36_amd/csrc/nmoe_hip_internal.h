@@ -86,7 +86,7 @@ struct nmoe_hip_ctx {
     int use_xcd_local;    /* NMOE_HIP_OPT_XCD_LOCAL */
     /* grouped (matrix-core) path for many tokens, sized for max_tokens */
     int grouped_min_tokens; /* NMOE_HIP_OPT_GROUPED_MIN_TOKENS */
-    uint32_t *g_counts;     /* [16][257] per-block expert histograms */
+    uint32_t *g_counts;     /* [64][257] per-block expert histograms */
     uint32_t *g_perm;       /* [T*8] entries grouped by expert */
     uint32_t *g_offsets;    /* [257] */
     uint16_t *g_xhi, *g_xlo; /* [T][2048] x in operand order (bf16 hi / lo) */

@@ -547,6 +547,32 @@ def test_dispatch_matches_oracle(big, ntok, k, kind):
     np.testing.assert_array_equal(got_p[:int(want_o[256])], want_p)
 
 
+def test_dispatch_long_slices(nh):
+    """10,000 tokens x 8 = 80,000 entries: 64 dispatch blocks of 1,250
+    entries, so each slice spans five 256-entry chunks (four read up front,
+    the fifth read in the scatter, ragged), with Zipf routing and some
+    entries outside the layer."""
+    c = nh.Context(0, max_tokens=10000)
+    try:
+        rng = np.random.default_rng(5000)
+        ntok, k = 10000, 8
+        idx = zipf_idx(rng, ntok, k)
+        idx[rng.integers(0, ntok, 50), rng.integers(0, k, 50)] = 256 + rng.integers(0, 100, 50)
+        flat = idx[:, :k].reshape(-1)
+        valid = flat < 256
+        perm, offs = c.alloc(ntok * k * 4), c.alloc(257 * 4)
+        c._check(c.dispatch(c.to_device(idx), ntok, k, perm, offs))
+        got_p, got_o = perm.download(np.uint32, ntok * k), offs.download(np.uint32, 257)
+        keys = np.where(valid, flat, 256)
+        want_p = np.argsort(keys, kind="stable")[:valid.sum()].astype(np.uint32)
+        want_o = np.concatenate([[0], np.cumsum(np.bincount(flat[valid], minlength=256))]).astype(np.uint32)
+        np.testing.assert_array_equal(got_o, want_o)
+        np.testing.assert_array_equal(got_p[:int(want_o[256])], want_p)
+        assert c.device_status() == nh.OK
+    finally:
+        c.close()
+
+
 @pytest.mark.parametrize("bits", [4, 2])
 @pytest.mark.parametrize("ntok,k,xkind,ikind", [(8, 8, "bf16", "uniform"), (64, 8, "bf16", "zipf"),
                                                (64, 6, "f32", "zipf"), (40, 8, "f32", "uniform")])
