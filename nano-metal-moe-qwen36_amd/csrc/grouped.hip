@@ -165,10 +165,11 @@ __device__ __forceinline__ void nmoe_dispatch_count(const uint32_t *idx, int nto
  * its rank among the equal-expert lanes of its wavefront (a 9-bit
  * multi-split by ballots) plus the counts of the earlier wavefronts. */
 __device__ __forceinline__ void nmoe_dispatch_scatter(const uint32_t *idx, int ntok, int k, uint32_t *counts,
-                                                      const uint32_t *h, uint32_t *perm, uint32_t *offsets, int b,
-                                                      int nd, const uint32_t *ev) {
+                                                      const uint32_t *h, uint32_t *perm, uint32_t *offsets,
+                                                      uint4 *rank, int b, int nd, const uint32_t *ev) {
     __shared__ uint32_t s_base[NMOE_EXPERTS];
     __shared__ uint32_t s_scan[4]; /* the wavefronts' totals */
+    __shared__ uint32_t s_bk[64]; /* the work buckets of the expert order */
     __shared__ uint32_t s_wc[4][NMOE_EXPERTS + 1];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, n = ntok * k;
     const int per = (n + nd - 1) / nd;
@@ -206,6 +207,28 @@ __device__ __forceinline__ void nmoe_dispatch_scatter(const uint32_t *idx, int n
     if (b == 0) {
         offsets[tid] = off;
         if (tid == 255) offsets[NMOE_EXPERTS] = off + total;
+        /* the experts by work, most first: bucket = 16-entry row blocks
+         * (63 and more together), a counting sort over the buckets, any
+         * order within one (the GEMM blocks' results do not depend on their
+         * order).  The GEMM blocks take the experts in this order, so the
+         * longest tiles start first and the launch's tail is short. */
+        const int bk = 63 - (int)min((total + 15u) / 16u, 63u);
+        if (tid < 64) s_bk[tid] = 0;
+        __syncthreads();
+        atomicAdd(&s_bk[bk], 1u);
+        __syncthreads();
+        if (tid < 64) { /* exclusive scan of the 64 bucket sizes (one wavefront) */
+            const uint32_t c = s_bk[tid];
+            uint32_t inc = c;
+#pragma unroll
+            for (int d = 1; d < 64; d <<= 1) {
+                const uint32_t v = (uint32_t)__shfl_up((int)inc, d, 64);
+                inc += lane >= d ? v : 0u;
+            }
+            s_bk[tid] = inc - c;
+        }
+        __syncthreads();
+        rank[atomicAdd(&s_bk[bk], 1u)] = make_uint4((uint32_t)tid, off, total, 0u);
     }
     s_base[tid] = off + before;
     for (int i = tid; i < 4 * (NMOE_EXPERTS + 1); i += 256) (&s_wc[0][0])[i] = 0;
@@ -293,8 +316,8 @@ __device__ __forceinline__ void nmoe_grouped_xprep(const XT *x, uint16_t *xhi, u
 template <int BITS, typename XT>
 __global__ void __launch_bounds__(256) nmoe_grouped_prep_kernel(const uint32_t *idx, int ntok, int k, int nd,
                                                                 uint32_t *counts, uint32_t *perm, uint32_t *offsets,
-                                                                uint32_t *sync, const XT *x, uint16_t *xhi,
-                                                                uint16_t *xlo, float *xs) {
+                                                                uint4 *rank, uint32_t *sync, const XT *x,
+                                                                uint16_t *xhi, uint16_t *xlo, float *xs) {
     const int b = blockIdx.x;
     if (b >= nd) {
         nmoe_grouped_xprep<BITS, XT>(x, xhi, xlo, xs, b - nd);
@@ -328,7 +351,7 @@ __global__ void __launch_bounds__(256) nmoe_grouped_prep_kernel(const uint32_t *
         }
         __syncthreads(); /* (the histograms are then read with device-coherent loads) */
     }
-    nmoe_dispatch_scatter(idx, ntok, k, counts, h, perm, offsets, b, nd, ev);
+    nmoe_dispatch_scatter(idx, ntok, k, counts, h, perm, offsets, rank, b, nd, ev);
 }
 
 /* ------------------------------------------------------------ stage ring */
@@ -561,7 +584,7 @@ __host__ __device__ constexpr int nmoe_gu_stages(int bits, int xpl, int nw) {
 template <int BITS, int XPL, int NW>
 __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
 nmoe_grouped_gateup_kernel(const uint8_t *pack, const uint16_t *xhi, const uint16_t *xlo, const float *xs,
-                           const uint32_t *perm, const uint32_t *offsets, int k, int lanes, uint16_t *ahi,
+                           const uint32_t *perm, const uint4 *rank, int k, int lanes, uint16_t *ahi,
                            uint16_t *alo, float *as) {
     using Q = nmoe_q<BITS>;
     using L = nmoe_layout<BITS>;
@@ -594,9 +617,13 @@ nmoe_grouped_gateup_kernel(const uint8_t *pack, const uint16_t *xhi, const uint1
     /* pass lane pl of `lanes`: passes pl, pl + lanes, ... of tile (e, nt) */
     constexpr int NTILE = NMOE_INTER / NT;
     const int pl = blockIdx.x / (NMOE_EXPERTS * NTILE);
-    int e, nt;
-    nmoe_die_tile(blockIdx.x % (NMOE_EXPERTS * NTILE), NTILE, e, nt);
-    const uint32_t p0 = offsets[e], n = offsets[e + 1] - p0;
+    /* the tile's expert is the es-th by entries (most first), so the
+     * longest tiles start first */
+    int es, nt;
+    nmoe_die_tile(blockIdx.x % (NMOE_EXPERTS * NTILE), NTILE, es, nt);
+    const uint4 rk = rank[es];
+    const int e = (int)rk.x;
+    const uint32_t p0 = rk.y, n = rk.z;
     if (n <= (uint32_t)(pl * MCH)) return;
     const int tid = threadIdx.x, lane = tid & 63, col = lane & 15, kb = lane >> 4;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -823,7 +850,7 @@ __host__ __device__ constexpr int nmoe_dn_stages(int bits, int nw) {
 template <int BITS, int NW>
 __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
 nmoe_grouped_down_kernel(const uint8_t *pack, const uint16_t *ahi, const uint16_t *alo, const float *as,
-                         const uint32_t *perm, const uint32_t *offsets, int lanes, float *y) {
+                         const uint32_t *perm, const uint4 *rank, int lanes, float *y) {
     using Q = nmoe_q<BITS>;
     using L = nmoe_layout<BITS>;
     constexpr int G = NMOE_INTER / NMOE_GROUP; /* 8 groups */
@@ -847,9 +874,13 @@ nmoe_grouped_down_kernel(const uint8_t *pack, const uint16_t *ahi, const uint16_
     __shared__ uint32_t s_q[MCH]; /* the chunk's output slots */
     constexpr int NTILE = NMOE_HIDDEN / NT;
     const int pl = blockIdx.x / (NMOE_EXPERTS * NTILE); /* pass lane, as in the gate/up kernel */
-    int e, nt;
-    nmoe_die_tile(blockIdx.x % (NMOE_EXPERTS * NTILE), NTILE, e, nt);
-    const uint32_t p0 = offsets[e], n = offsets[e + 1] - p0;
+    /* the tile's expert is the es-th by entries (most first), so the
+     * longest tiles start first */
+    int es, nt;
+    nmoe_die_tile(blockIdx.x % (NMOE_EXPERTS * NTILE), NTILE, es, nt);
+    const uint4 rk = rank[es];
+    const int e = (int)rk.x;
+    const uint32_t p0 = rk.y, n = rk.z;
     if (n <= (uint32_t)(pl * MCH)) return;
     const int tid = threadIdx.x, lane = tid & 63, col = lane & 15, kb = lane >> 4;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1031,6 +1062,7 @@ extern "C" int nmoe_grouped_init(nmoe_hip_ctx *ctx) {
     if (hipMalloc((void **)&ctx->g_counts, NMOE_DISPATCH_MAX * (NMOE_EXPERTS + 1) * sizeof(uint32_t)) != hipSuccess ||
         hipMalloc((void **)&ctx->g_perm, rows * sizeof(uint32_t)) != hipSuccess ||
         hipMalloc((void **)&ctx->g_offsets, (NMOE_EXPERTS + 1) * sizeof(uint32_t)) != hipSuccess ||
+        hipMalloc((void **)&ctx->g_rank, NMOE_EXPERTS * 4 * sizeof(uint32_t)) != hipSuccess ||
         hipMalloc((void **)&ctx->g_xhi, mt * NMOE_HIDDEN * sizeof(uint16_t)) != hipSuccess ||
         hipMalloc((void **)&ctx->g_xlo, mt * NMOE_HIDDEN * sizeof(uint16_t)) != hipSuccess ||
         hipMalloc((void **)&ctx->g_xs, mt * (NMOE_HIDDEN / NMOE_GROUP) * sizeof(float)) != hipSuccess ||
@@ -1043,8 +1075,8 @@ extern "C" int nmoe_grouped_init(nmoe_hip_ctx *ctx) {
 }
 
 extern "C" void nmoe_grouped_free(nmoe_hip_ctx *ctx) {
-    void *p[] = {ctx->g_counts, ctx->g_perm, ctx->g_offsets, ctx->g_xhi, ctx->g_xlo,
-                 ctx->g_xs,     ctx->g_ahi,  ctx->g_alo,     ctx->g_as,  ctx->g_y};
+    void *p[] = {ctx->g_counts, ctx->g_perm, ctx->g_offsets, ctx->g_rank, ctx->g_xhi, ctx->g_xlo,
+                 ctx->g_xs,     ctx->g_ahi,  ctx->g_alo,     ctx->g_as,   ctx->g_y};
     for (void *q : p)
         if (q != NULL) (void)hipFree(q);
 }
@@ -1054,8 +1086,8 @@ extern "C" int nmoe_grouped_dispatch(nmoe_hip_ctx *ctx, const uint32_t *idx, int
                                      uint32_t *offsets, hipStream_t s) {
     const int nd = nmoe_dispatch_blocks(ntok * k);
     hipLaunchKernelGGL((nmoe_grouped_prep_kernel<4, uint16_t>), dim3(nd), dim3(256), 0, s, idx, ntok, k, nd,
-                       ctx->g_counts, perm, offsets, ctx->sync, (const uint16_t *)NULL, (uint16_t *)NULL,
-                       (uint16_t *)NULL, (float *)NULL);
+                       ctx->g_counts, perm, offsets, (uint4 *)ctx->g_rank, ctx->sync, (const uint16_t *)NULL,
+                       (uint16_t *)NULL, (uint16_t *)NULL, (float *)NULL);
     const hipError_t e = hipGetLastError();
     return e == hipSuccess ? NMOE_HIP_OK : nmoe_hip_check(ctx, e, "dispatch launch");
 }
@@ -1069,11 +1101,13 @@ static int nmoe_grouped_run(nmoe_hip_ctx *ctx, const uint8_t *pack, const void *
     const dim3 gprep(nd + ntok);
     if (bf)
         hipLaunchKernelGGL((nmoe_grouped_prep_kernel<BITS, uint16_t>), gprep, dim3(256), 0, s, idx, ntok, k, nd,
-                           ctx->g_counts, ctx->g_perm, ctx->g_offsets, ctx->sync, (const uint16_t *)x, ctx->g_xhi,
+                           ctx->g_counts, ctx->g_perm, ctx->g_offsets, (uint4 *)ctx->g_rank, ctx->sync,
+                           (const uint16_t *)x, ctx->g_xhi,
                            (uint16_t *)NULL, ctx->g_xs);
     else
         hipLaunchKernelGGL((nmoe_grouped_prep_kernel<BITS, float>), gprep, dim3(256), 0, s, idx, ntok, k, nd,
-                           ctx->g_counts, ctx->g_perm, ctx->g_offsets, ctx->sync, (const float *)x, ctx->g_xhi,
+                           ctx->g_counts, ctx->g_perm, ctx->g_offsets, (uint4 *)ctx->g_rank, ctx->sync,
+                           (const float *)x, ctx->g_xhi,
                            ctx->g_xlo, ctx->g_xs);
     constexpr int NW = NMOE_GROUPED_NW;
     const dim3 blk(64 * NW);
@@ -1084,17 +1118,18 @@ static int nmoe_grouped_run(nmoe_hip_ctx *ctx, const uint8_t *pack, const void *
     const dim3 ggu(lanes * NMOE_EXPERTS * (NMOE_INTER / nmoe_gu_rows(bf ? 1 : 2, NW))),
         gdn(lanes * NMOE_EXPERTS * (NMOE_HIDDEN / nmoe_dn_rows(NW)));
     const uint16_t *xhi = (const uint16_t *)ctx->g_xhi, *xlo = (const uint16_t *)ctx->g_xlo;
-    const uint32_t *perm = (const uint32_t *)ctx->g_perm, *offsets = (const uint32_t *)ctx->g_offsets;
+    const uint32_t *perm = (const uint32_t *)ctx->g_perm;
+    const uint4 *rank = (const uint4 *)ctx->g_rank;
     const uint16_t *ahi = (const uint16_t *)ctx->g_ahi, *alo = (const uint16_t *)ctx->g_alo;
     const float *xs = (const float *)ctx->g_xs, *as = (const float *)ctx->g_as;
     /* gate/up, then down */
     if (bf)
-        hipLaunchKernelGGL((nmoe_grouped_gateup_kernel<BITS, 1, NW>), ggu, blk, 0, s, pack, xhi, xlo, xs, perm, offsets, k,
+        hipLaunchKernelGGL((nmoe_grouped_gateup_kernel<BITS, 1, NW>), ggu, blk, 0, s, pack, xhi, xlo, xs, perm, rank, k,
                            lanes, ctx->g_ahi, ctx->g_alo, ctx->g_as);
     else
-        hipLaunchKernelGGL((nmoe_grouped_gateup_kernel<BITS, 2, NW>), ggu, blk, 0, s, pack, xhi, xlo, xs, perm, offsets, k,
+        hipLaunchKernelGGL((nmoe_grouped_gateup_kernel<BITS, 2, NW>), ggu, blk, 0, s, pack, xhi, xlo, xs, perm, rank, k,
                            lanes, ctx->g_ahi, ctx->g_alo, ctx->g_as);
-    hipLaunchKernelGGL((nmoe_grouped_down_kernel<BITS, NW>), gdn, blk, 0, s, pack, ahi, alo, as, perm, offsets, lanes,
+    hipLaunchKernelGGL((nmoe_grouped_down_kernel<BITS, NW>), gdn, blk, 0, s, pack, ahi, alo, as, perm, rank, lanes,
                        ctx->g_y);
     if (nmoe_aligned(h_mid, 16) && nmoe_aligned(out, 16) && (shared_out == NULL || nmoe_aligned(shared_out, 16)))
         hipLaunchKernelGGL(nmoe_grouped_combine_kernel, dim3(NMOE_HIDDEN / 1024, ntok), dim3(256), 0, s,
