@@ -9,17 +9,20 @@
  * counting sort), and each expert's weights are read once for all of its
  * tokens:
  *
- *   D1/D2  dispatch: per-block expert histograms, then offsets[257] and the
- *          stable permutation perm[] of the entries q = t*k + s (ties by t,
- *          then s).  Entries whose index is outside the layer are left out.
- *   X      per token: x in the matrix-core operand order (bf16; fp32 input
+ *   prep   one launch: D1/D2 dispatch (per-slice expert histograms, then
+ *          offsets[257], the stable permutation perm[] of the entries
+ *          q = t*k + s (ties by t, then s; entries whose index is outside
+ *          the layer are left out) and the experts ranked by work), and X
+ *          per token: x in the matrix-core operand order (bf16; fp32 input
  *          also gets a low plane x - bf16(x)) and its 32 group sums.
- *   G      per (expert, 64 gate/up rows): Act = SwiGLU(X_e Wg^T, X_e Wu^T)
- *          for all of the expert's rows, as hi + lo bf16 planes, and the
- *          8 group sums of each act row.
- *   Dn     per (expert, 64 down rows): Y_e = Act_e Wd^T -> Y[q][2048].
+ *   G      per (expert, 128 gate and 128 up rows): Act = SwiGLU(X_e Wg^T,
+ *          X_e Wu^T) for all of the expert's rows, as hi + lo bf16 planes,
+ *          and the 8 group sums of each act row.
+ *   Dn     per (expert, 256 down rows): Y_e = Act_e Wd^T -> Y[q][2048].
  *   C      per token: out = h_mid + sum_s w_s y_s in slot order
  *          (kernels.metal:1394-1423) (+ sigmoid(g) * shared).
+ * (Tile rows as built with four-wavefront blocks; NMOE_GROUPED_NW=8 doubles
+ * them.)
  *
  * Exactness on the matrix cores.  The dequantised weight is q*scale + bias
  * per group of 64 (math.m:206-234).  A bf16 weight would round q*scale, so
