@@ -32,8 +32,10 @@
  *     sum_k w_k x_k = sum_g s_g P_g + sum_g (b_g - 128 s_g) xs_g,
  *     P_g = sum_{k in g} (128 + q_k) x_k,   xs_g = sum_{k in g} x_k,
  * with P_g from v_mfma_f32_16x16x32_bf16 (bf16 products are exact in fp32),
- * the s_g scaling applied per group in fp32, and the second sum from
- * v_mfma_f32_16x16x4_f32 over the 32 (gate/up) or 8 (down) groups.  x is
+ * the s_g scaling applied per group in fp32, and the second sum over the
+ * 32 (gate/up) groups from the same bf16 MFMA (xs as three exact bf16
+ * parts; b and s are bf16), over the 8 (down) groups from
+ * v_mfma_f32_16x16x4_f32.  x is
  * bf16 (exact) or a hi + lo bf16 pair; act is a hi + lo pair (16
  * significant bits).  So the only rounding beyond fp32 accumulation is
  * act's 2^-17.
@@ -271,10 +273,12 @@ __device__ __forceinline__ void nmoe_dispatch_scatter(const uint32_t *idx, int n
 /* ------------------------------------------------------------ X prep */
 
 /* xp[t][16 span + slot] = x[t][16 span + kperm(slot)] as bf16 (hi plane; the
- * lo plane x - hi when x is fp32), xs[t][g] = sum of the 64 values of group
- * g (hi + lo, in a fixed order). */
+ * lo plane x - hi when x is fp32); xs3[t][p][g] = part p of the sum of the 64
+ * values of group g (hi + lo, in a fixed order) as three bf16 whose sum is
+ * the fp32 sum exactly (8 + 8 + 8 significant bits), the matrix-core
+ * operand of the correction. */
 template <int BITS, typename XT>
-__device__ __forceinline__ void nmoe_grouped_xprep(const XT *x, uint16_t *xhi, uint16_t *xlo, float *xs, int t) {
+__device__ __forceinline__ void nmoe_grouped_xprep(const XT *x, uint16_t *xhi, uint16_t *xlo, uint16_t *xs3, int t) {
     const int tid = threadIdx.x; /* 8 elements per thread: half a span */
     const int span = tid >> 1, half = tid & 1;
     float v[8];
@@ -306,7 +310,17 @@ __device__ __forceinline__ void nmoe_grouped_xprep(const XT *x, uint16_t *xhi, u
     sum = sum + nmoe_dpp_f<NMOE_DPP_XOR1>(sum);
     sum = sum + nmoe_dpp_f<NMOE_DPP_XOR2>(sum);
     sum = sum + nmoe_dpp_f<NMOE_DPP_HALF_MIRROR>(sum);
-    if ((tid & 7) == 0) xs[(size_t)t * (NMOE_HIDDEN / NMOE_GROUP) + (tid >> 3)] = sum;
+    if ((tid & 7) == 0) {
+        constexpr int G = NMOE_HIDDEN / NMOE_GROUP;
+        const uint32_t h = nmoe_bf16_rne(sum);
+        const float r = sum - nmoe_bf16f(h); /* exact */
+        const uint32_t m = nmoe_bf16_rne(r);
+        const uint32_t l = nmoe_bf16_rne(r - nmoe_bf16f(m)); /* exact: the last 8 bits */
+        uint16_t *o = xs3 + (size_t)t * 3 * G + (tid >> 3);
+        o[0] = (uint16_t)h;
+        o[G] = (uint16_t)m;
+        o[2 * G] = (uint16_t)l;
+    }
 }
 
 /* One launch for the grouped path's preparation: blocks 0 .. nd-1 run the
@@ -320,10 +334,10 @@ template <int BITS, typename XT>
 __global__ void __launch_bounds__(256) nmoe_grouped_prep_kernel(const uint32_t *idx, int ntok, int k, int nd,
                                                                 uint32_t *counts, uint32_t *perm, uint32_t *offsets,
                                                                 uint4 *rank, uint32_t *sync, const XT *x,
-                                                                uint16_t *xhi, uint16_t *xlo, float *xs) {
+                                                                uint16_t *xhi, uint16_t *xlo, uint16_t *xs3) {
     const int b = blockIdx.x;
     if (b >= nd) {
-        nmoe_grouped_xprep<BITS, XT>(x, xhi, xlo, xs, b - nd);
+        nmoe_grouped_xprep<BITS, XT>(x, xhi, xlo, xs3, b - nd);
         return;
     }
     uint32_t ev[NMOE_DISPATCH_PRE];
@@ -583,10 +597,12 @@ __host__ __device__ constexpr int nmoe_gu_stages(int bits, int xpl, int nw) {
  *
  * y = sum_g s_g P_g + sum_g (b_g - 128 s_g) xs_g with P_g the MFMA product
  * of the group's A rows and the codes as bf16(128 + q); the second sum runs
- * first, on the fp32 matrix cores. */
+ * first, as sum_g xs_g b_g - 128 sum_g xs_g s_g over the 32 groups: one bf16
+ * MFMA (K = 32) per part of xs (three exact bf16 parts) and per operand (the
+ * bf16 biases and scales as they are), fp32 accumulate. */
 template <int BITS, int XPL, int NW>
 __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
-nmoe_grouped_gateup_kernel(const uint8_t *pack, const uint16_t *xhi, const uint16_t *xlo, const float *xs,
+nmoe_grouped_gateup_kernel(const uint8_t *pack, const uint16_t *xhi, const uint16_t *xlo, const uint16_t *xs3,
                            const uint32_t *perm, const uint4 *rank, int k, int lanes, uint16_t *ahi,
                            uint16_t *alo, float *as) {
     using Q = nmoe_q<BITS>;
@@ -663,80 +679,68 @@ nmoe_grouped_gateup_kernel(const uint8_t *pack, const uint16_t *xhi, const uint1
         const int nb = (int)min((n - m0 + 15) / 16, (uint32_t)MB);
         nmoe_f32x4 acc[2][NB][MB];
         {
-                /* The correction's operands go out first and the first ring
-                 * stages right after them: loads retire in order, so the
-                 * small loads then return without waiting for the stages,
-                 * and the correction's MFMAs run while the stages stream in.
-                 * A lane = (entry col, groups 8kb + tq), B lane = (row col,
-                 * groups 8kb + tq): a lane's eight groups are contiguous (two
-                 * 16-byte loads of xs, one of the biases). */
-                constexpr int PER = 2 * NT * G / 8 / NTH;
-                static_assert(PER * NTH == 2 * NT * G / 8, "scale chunks split evenly over the threads");
-                /* the tile's scales straight into LDS, every pass (later
-                 * passes hit L2): wavefront w's q-th 1 KB at uint4 NTH q + 64w */
+            /* The correction's operands go out first and the first ring
+             * stages right after them: loads retire in order, so the
+             * small loads then return without waiting for the stages,
+             * and the correction's MFMAs run while the stages stream in.
+             * A lane = (entry col, groups 8kb .. 8kb+7), B lane = (row
+             * col, the same groups): a lane's eight groups are contiguous
+             * (one 16-byte load per part of xs, one of the biases, one
+             * LDS read of the scales). */
+            constexpr int PER = 2 * NT * G / 8 / NTH;
+            static_assert(PER * NTH == 2 * NT * G / 8, "scale chunks split evenly over the threads");
+            /* the tile's scales straight into LDS, every pass (later
+             * passes hit L2): wavefront w's q-th 1 KB at uint4 NTH q + 64w */
 #pragma unroll
-                for (int q = 0; q < PER; q++) {
-                    /* LDS chunk i = (mat, chunk, row) <- global chunk row * G/8 + chunk of the matrix */
-                    const int i = tid + NTH * q, mat = i / (NT * G / 8), j = i % (NT * G / 8);
-                    const int ch = j / NT, row = j % NT;
-                    const uint4 *src = (const uint4 *)(ex + (mat == 0 ? L::gate_s : L::up_s) + (size_t)nt * NT * G * 2) +
-                                       row * (G / 8) + ch;
-                    __builtin_amdgcn_global_load_lds(
-                        (const void *)src, (nmoe_lds_void *)((uint4 *)&s_s[0][0][0][0] + NTH * q + 64 * wave), 16, 0, 0);
-                }
-                float4 xv4[MB][2];
-                uint4 bv[2][NB];
+            for (int q = 0; q < PER; q++) {
+                /* LDS chunk i = (mat, chunk, row) <- global chunk row * G/8 + chunk of the matrix */
+                const int i = tid + NTH * q, mat = i / (NT * G / 8), j = i % (NT * G / 8);
+                const int ch = j / NT, row = j % NT;
+                const uint4 *src = (const uint4 *)(ex + (mat == 0 ? L::gate_s : L::up_s) + (size_t)nt * NT * G * 2) +
+                                   row * (G / 8) + ch;
+                __builtin_amdgcn_global_load_lds(
+                    (const void *)src, (nmoe_lds_void *)((uint4 *)&s_s[0][0][0][0] + NTH * q + 64 * wave), 16, 0, 0);
+            }
+            uint4 xq[MB][3];
+            uint4 bv[2][NB];
 #pragma unroll
-                for (int mb = 0; mb < MB; mb++) {
-                    const float4 *xsr = (const float4 *)(xs + (size_t)s_tok[16 * mb + col] * G + 8 * kb);
-                    xv4[mb][0] = xsr[0];
-                    xv4[mb][1] = xsr[1];
-                }
+            for (int mb = 0; mb < MB; mb++)
 #pragma unroll
-                for (int mat = 0; mat < 2; mat++)
+                for (int p = 0; p < 3; p++)
+                    xq[mb][p] = *(const uint4 *)(xs3 + ((size_t)s_tok[16 * mb + col] * 3 + p) * G + 8 * kb);
 #pragma unroll
-                    for (int b2 = 0; b2 < NB; b2++)
-                        bv[mat][b2] = *(const uint4 *)(bias[mat] + (rt0 + 16 * b2) * G + 8 * kb);
+            for (int mat = 0; mat < 2; mat++)
 #pragma unroll
-                for (int st = 0; st < NS - 1; st++) issue(st, st);
-                /* scales, xs and biases have landed once only the stages'
-                 * loads are in flight; then every wavefront's scales are in
-                 * LDS */
-                nmoe_wait_vm<(NS - 1) * (XPL * AI + CP::PER_WAVE)>();
-                nmoe_lds_barrier();
-                float xv[MB][G / 4];
+                for (int b2 = 0; b2 < NB; b2++)
+                    bv[mat][b2] = *(const uint4 *)(bias[mat] + (rt0 + 16 * b2) * G + 8 * kb);
 #pragma unroll
-                for (int mb = 0; mb < MB; mb++) {
-                    xv[mb][0] = xv4[mb][0].x, xv[mb][1] = xv4[mb][0].y, xv[mb][2] = xv4[mb][0].z;
-                    xv[mb][3] = xv4[mb][0].w, xv[mb][4] = xv4[mb][1].x, xv[mb][5] = xv4[mb][1].y;
-                    xv[mb][6] = xv4[mb][1].z, xv[mb][7] = xv4[mb][1].w;
-                }
-                float cv[2][NB][G / 4];
+            for (int st = 0; st < NS - 1; st++) issue(st, st);
+            /* scales, xs and biases have landed once only the stages'
+             * loads are in flight; then every wavefront's scales are in
+             * LDS */
+            nmoe_wait_vm<(NS - 1) * (XPL * AI + CP::PER_WAVE)>();
+            nmoe_lds_barrier();
 #pragma unroll
-                for (int mat = 0; mat < 2; mat++)
+            for (int mat = 0; mat < 2; mat++)
 #pragma unroll
-                    for (int b2 = 0; b2 < NB; b2++) {
-                        float bf[8], sf[8];
-                        nmoe_unpack_bf16x8(bv[mat][b2], bf);
-                        nmoe_unpack_bf16x8(*(const uint4 *)&s_s[mat][kb][rt0 + 16 * b2][0], sf);
+                for (int b2 = 0; b2 < NB; b2++) {
+                    const uint4 sv = *(const uint4 *)&s_s[mat][kb][rt0 + 16 * b2][0];
 #pragma unroll
-                        for (int tq = 0; tq < G / 4; tq++) cv[mat][b2][tq] = bf[tq] - 128.0f * sf[tq];
+                    for (int mb = 0; mb < MB; mb++) {
+                        nmoe_f32x4 a = nmoe_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+                        if (mb < nb) {
+                            nmoe_f32x4 t = nmoe_mfma16(xq[mb][0], sv, nmoe_f32x4{0.0f, 0.0f, 0.0f, 0.0f});
+                            t = nmoe_mfma16(xq[mb][1], sv, t);
+                            t = nmoe_mfma16(xq[mb][2], sv, t);
+                            a = nmoe_mfma16(xq[mb][0], bv[mat][b2], a);
+                            a = nmoe_mfma16(xq[mb][1], bv[mat][b2], a);
+                            a = nmoe_mfma16(xq[mb][2], bv[mat][b2], a);
 #pragma unroll
-                        for (int mb = 0; mb < MB; mb++) acc[mat][b2][mb] = nmoe_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+                            for (int i = 0; i < 4; i++) a[i] = __builtin_fmaf(-128.0f, t[i], a[i]);
+                        }
+                        acc[mat][b2][mb] = a;
                     }
-                /* group-slice outermost: the 2 NB MB accumulator chains
-                 * interleave, so each MFMA's latency hides behind the others' */
-#pragma unroll
-                for (int tq = 0; tq < G / 4; tq++)
-#pragma unroll
-                    for (int mb = 0; mb < MB; mb++)
-                        if (mb < nb)
-#pragma unroll
-                        for (int mat = 0; mat < 2; mat++)
-#pragma unroll
-                            for (int b2 = 0; b2 < NB; b2++)
-                                acc[mat][b2][mb] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[mb][tq], cv[mat][b2][tq],
-                                                                                        acc[mat][b2][mb], 0, 0, 0);
+                }
         }
         auto step = [&](int g, const int st, const bool ahead) {
             nmoe_ring_step_barrier<XPL * AI + CP::PER_WAVE, G, NS>(g);
@@ -916,42 +920,42 @@ nmoe_grouped_down_kernel(const uint8_t *pack, const uint16_t *ahi, const uint16_
         const int nb = (int)min((n - m0 + 15) / 16, (uint32_t)MB);
         nmoe_f32x4 acc[NB][MB];
         {
-                /* as in the gate/up kernel: the correction's operands
-                 * (scales straight into LDS, one 16-byte chunk a thread,
-                 * every pass), then the first ring stages, then a wait that
-                 * leaves only the stages in flight.
-                 * A lane = (entry col, groups 2kb + tq), B lane = (row col,
-                 * groups 2kb + tq) */
-                static_assert(NT * G / 8 == 64 * NW, "one scale chunk per thread");
-                __builtin_amdgcn_global_load_lds(
-                    (const void *)((const uint4 *)(ex + L::down_s + (size_t)nt * NT * G * 2) + tid),
-                    (nmoe_lds_void *)((uint4 *)&s_s[0][0] + 64 * wave), 16, 0, 0);
-                float2 av[MB];
-                uint32_t bv[NB];
+            /* as in the gate/up kernel: the correction's operands
+             * (scales straight into LDS, one 16-byte chunk a thread,
+             * every pass), then the first ring stages, then a wait that
+             * leaves only the stages in flight.
+             * A lane = (entry col, groups 2kb + tq), B lane = (row col,
+             * groups 2kb + tq) */
+            static_assert(NT * G / 8 == 64 * NW, "one scale chunk per thread");
+            __builtin_amdgcn_global_load_lds(
+                (const void *)((const uint4 *)(ex + L::down_s + (size_t)nt * NT * G * 2) + tid),
+                (nmoe_lds_void *)((uint4 *)&s_s[0][0] + 64 * wave), 16, 0, 0);
+            float2 av[MB];
+            uint32_t bv[NB];
+#pragma unroll
+            for (int mb = 0; mb < MB; mb++)
+                av[mb] = *(const float2 *)(as + (size_t)(p0 + min(m0 + 16 * mb + col, n - 1)) * G + 2 * kb);
+#pragma unroll
+            for (int b2 = 0; b2 < NB; b2++) bv[b2] = *(const uint32_t *)(bias + (rt0 + 16 * b2) * G + 2 * kb);
+#pragma unroll
+            for (int st = 0; st < NS - 1; st++) issue(st, st);
+            nmoe_wait_vm<(NS - 1) * (2 * AI + CP::PER_WAVE)>();
+            if (tid < MCH) s_q[tid] = qv;
+            nmoe_lds_barrier(); /* the scales and s_q */
+            float cv[NB][G / 4];
+#pragma unroll
+            for (int b2 = 0; b2 < NB; b2++) {
+                const uint32_t sw = *(const uint32_t *)&s_s[rt0 + 16 * b2][2 * kb];
+                cv[b2][0] = __uint_as_float(bv[b2] << 16) - 128.0f * __uint_as_float(sw << 16);
+                cv[b2][1] = __uint_as_float(bv[b2] & 0xffff0000u) - 128.0f * __uint_as_float(sw & 0xffff0000u);
+#pragma unroll
+                for (int mb = 0; mb < MB; mb++) acc[b2][mb] = nmoe_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            }
+#pragma unroll
+            for (int tq = 0; tq < G / 4; tq++)
 #pragma unroll
                 for (int mb = 0; mb < MB; mb++)
-                    av[mb] = *(const float2 *)(as + (size_t)(p0 + min(m0 + 16 * mb + col, n - 1)) * G + 2 * kb);
-#pragma unroll
-                for (int b2 = 0; b2 < NB; b2++) bv[b2] = *(const uint32_t *)(bias + (rt0 + 16 * b2) * G + 2 * kb);
-#pragma unroll
-                for (int st = 0; st < NS - 1; st++) issue(st, st);
-                nmoe_wait_vm<(NS - 1) * (2 * AI + CP::PER_WAVE)>();
-                if (tid < MCH) s_q[tid] = qv;
-                nmoe_lds_barrier(); /* the scales and s_q */
-                float cv[NB][G / 4];
-#pragma unroll
-                for (int b2 = 0; b2 < NB; b2++) {
-                    const uint32_t sw = *(const uint32_t *)&s_s[rt0 + 16 * b2][2 * kb];
-                    cv[b2][0] = __uint_as_float(bv[b2] << 16) - 128.0f * __uint_as_float(sw << 16);
-                    cv[b2][1] = __uint_as_float(bv[b2] & 0xffff0000u) - 128.0f * __uint_as_float(sw & 0xffff0000u);
-#pragma unroll
-                    for (int mb = 0; mb < MB; mb++) acc[b2][mb] = nmoe_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-                }
-#pragma unroll
-                for (int tq = 0; tq < G / 4; tq++)
-#pragma unroll
-                    for (int mb = 0; mb < MB; mb++)
-                        if (mb < nb)
+                    if (mb < nb)
 #pragma unroll
                         for (int b2 = 0; b2 < NB; b2++)
                             acc[b2][mb] = __builtin_amdgcn_mfma_f32_16x16x4f32(tq == 0 ? av[mb].x : av[mb].y,
@@ -1068,7 +1072,7 @@ extern "C" int nmoe_grouped_init(nmoe_hip_ctx *ctx) {
         hipMalloc((void **)&ctx->g_rank, NMOE_EXPERTS * 4 * sizeof(uint32_t)) != hipSuccess ||
         hipMalloc((void **)&ctx->g_xhi, mt * NMOE_HIDDEN * sizeof(uint16_t)) != hipSuccess ||
         hipMalloc((void **)&ctx->g_xlo, mt * NMOE_HIDDEN * sizeof(uint16_t)) != hipSuccess ||
-        hipMalloc((void **)&ctx->g_xs, mt * (NMOE_HIDDEN / NMOE_GROUP) * sizeof(float)) != hipSuccess ||
+        hipMalloc((void **)&ctx->g_xs, mt * 3 * (NMOE_HIDDEN / NMOE_GROUP) * sizeof(uint16_t)) != hipSuccess ||
         hipMalloc((void **)&ctx->g_ahi, rows * NMOE_INTER * sizeof(uint16_t)) != hipSuccess ||
         hipMalloc((void **)&ctx->g_alo, rows * NMOE_INTER * sizeof(uint16_t)) != hipSuccess ||
         hipMalloc((void **)&ctx->g_as, rows * (NMOE_INTER / NMOE_GROUP) * sizeof(float)) != hipSuccess ||
@@ -1090,7 +1094,7 @@ extern "C" int nmoe_grouped_dispatch(nmoe_hip_ctx *ctx, const uint32_t *idx, int
     const int nd = nmoe_dispatch_blocks(ntok * k);
     hipLaunchKernelGGL((nmoe_grouped_prep_kernel<4, uint16_t>), dim3(nd), dim3(256), 0, s, idx, ntok, k, nd,
                        ctx->g_counts, perm, offsets, (uint4 *)ctx->g_rank, ctx->sync, (const uint16_t *)NULL,
-                       (uint16_t *)NULL, (uint16_t *)NULL, (float *)NULL);
+                       (uint16_t *)NULL, (uint16_t *)NULL, (uint16_t *)NULL);
     const hipError_t e = hipGetLastError();
     return e == hipSuccess ? NMOE_HIP_OK : nmoe_hip_check(ctx, e, "dispatch launch");
 }
@@ -1124,13 +1128,14 @@ static int nmoe_grouped_run(nmoe_hip_ctx *ctx, const uint8_t *pack, const void *
     const uint32_t *perm = (const uint32_t *)ctx->g_perm;
     const uint4 *rank = (const uint4 *)ctx->g_rank;
     const uint16_t *ahi = (const uint16_t *)ctx->g_ahi, *alo = (const uint16_t *)ctx->g_alo;
-    const float *xs = (const float *)ctx->g_xs, *as = (const float *)ctx->g_as;
+    const uint16_t *xs3 = ctx->g_xs;
+    const float *as = (const float *)ctx->g_as;
     /* gate/up, then down */
     if (bf)
-        hipLaunchKernelGGL((nmoe_grouped_gateup_kernel<BITS, 1, NW>), ggu, blk, 0, s, pack, xhi, xlo, xs, perm, rank, k,
+        hipLaunchKernelGGL((nmoe_grouped_gateup_kernel<BITS, 1, NW>), ggu, blk, 0, s, pack, xhi, xlo, xs3, perm, rank, k,
                            lanes, ctx->g_ahi, ctx->g_alo, ctx->g_as);
     else
-        hipLaunchKernelGGL((nmoe_grouped_gateup_kernel<BITS, 2, NW>), ggu, blk, 0, s, pack, xhi, xlo, xs, perm, rank, k,
+        hipLaunchKernelGGL((nmoe_grouped_gateup_kernel<BITS, 2, NW>), ggu, blk, 0, s, pack, xhi, xlo, xs3, perm, rank, k,
                            lanes, ctx->g_ahi, ctx->g_alo, ctx->g_as);
     hipLaunchKernelGGL((nmoe_grouped_down_kernel<BITS, NW>), gdn, blk, 0, s, pack, ahi, alo, as, perm, rank, lanes,
                        ctx->g_y);
