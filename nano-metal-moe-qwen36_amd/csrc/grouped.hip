@@ -126,6 +126,16 @@ __device__ __forceinline__ uint32_t nmoe_bf16_rne(float f) {
     return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
 }
 
+/* The same by the hardware conversion (v_cvt_pk_bf16_f32, round to nearest
+ * even), one instruction. */
+__device__ __forceinline__ uint32_t nmoe_bf16_cvt(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
+
+/* A raw buffer resource over p: base in scalar registers, range 2 GB (the
+ * offsets used stay far inside the allocation), untyped access. */
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t nmoe_buffer(void *p) {
+    return __builtin_amdgcn_make_buffer_rsrc(p, (short)0, 0x7fffffff, 0x00020000);
+}
+
 /* ------------------------------------------------------------ dispatch */
 
 __device__ __forceinline__ uint32_t nmoe_entry_expert(const uint32_t *idx, int q, int k) {
@@ -789,29 +799,38 @@ nmoe_grouped_gateup_kernel(const uint8_t *pack, const uint16_t *xhi, const uint1
              * kernel's operand order; group sums of act rows (a down group
              * is 64 act columns, WPD wavefronts of this tile) */
             float part_sum[MB][4] = {};
+            /* the act planes as buffers: a scalar base and a 32-bit lane
+             * offset per store (no 64-bit address arithmetic) */
+            const __amdgpu_buffer_rsrc_t rhi = nmoe_buffer(ahi), rlo = nmoe_buffer(alo);
+            /* byte offset of this lane's act column in a row, per column block */
+            uint32_t cb[NB];
 #pragma unroll
             for (int b2 = 0; b2 < NB; b2++) {
                 const int r = nt * NT + rt0 + 16 * b2; /* act column */
-                const int span = r >> 4;
-                const int slot = nmoe_kperm_inv<BITS>(r & 15);
+                cb[b2] = 2u * (uint32_t)(16 * (r >> 4) + nmoe_kperm_inv<BITS>(r & 15));
+            }
 #pragma unroll
-                for (int mb = 0; mb < MB; mb++) {
-                    if (mb >= nb) continue;
+            for (int mb = 0; mb < MB; mb++) {
+                if (mb >= nb) continue;
 #pragma unroll
-                    for (int i = 0; i < 4; i++) {
-                        const uint32_t m = m0 + 16 * mb + 4 * kb + i;
+                for (int i = 0; i < 4; i++) {
+                    const uint32_t m = m0 + 16 * mb + 4 * kb + i;
+                    /* the row's byte offset from the (uniform) plane base */
+                    const uint32_t ro = (p0 + min(m, n - 1)) * (uint32_t)(NMOE_INTER * 2);
+                    float part = 0.0f;
+#pragma unroll
+                    for (int b2 = 0; b2 < NB; b2++) {
                         const float av = nmoe_silu_fast(acc[0][b2][mb][i]) * acc[1][b2][mb][i];
-                        const uint32_t h = nmoe_bf16_rne(av);
-                        const uint32_t l = nmoe_bf16_rne(av - nmoe_bf16f(h));
-                        float part = nmoe_bf16f(h) + nmoe_bf16f(l);
+                        const uint32_t h = nmoe_bf16_cvt(av);
+                        const uint32_t l = nmoe_bf16_cvt(av - nmoe_bf16f(h));
+                        part = part + (nmoe_bf16f(h) + nmoe_bf16f(l));
                         if (m < n) {
-                            const size_t o = (size_t)(p0 + m) * NMOE_INTER + 16 * span + slot;
-                            ahi[o] = (uint16_t)h;
-                            alo[o] = (uint16_t)l;
+                            __builtin_amdgcn_raw_buffer_store_b16((uint16_t)h, rhi, ro + cb[b2], 0, 0);
+                            __builtin_amdgcn_raw_buffer_store_b16((uint16_t)l, rlo, ro + cb[b2], 0, 0);
                         }
-                        part = nmoe_dpp_group_sum<16>(part); /* the 16 rows of this column block */
-                        part_sum[mb][i] = b2 == 0 ? part : part_sum[mb][i] + part;
                     }
+                    /* the wavefront's 2 NB x 16 act columns of this row */
+                    part_sum[mb][i] = nmoe_dpp_group_sum<16>(part);
                 }
             }
             if (col == 0)
