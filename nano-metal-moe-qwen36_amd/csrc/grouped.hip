@@ -388,7 +388,7 @@ __global__ void __launch_bounds__(256) nmoe_grouped_prep_kernel(const uint32_t *
  * direct global->LDS loads (global_load_lds_dwordx4: lane l of a wavefront
  * writes bytes 16l..16l+15 of the instruction's 1 KB), so a group is
  * requested NS - 1 steps before it is multiplied.  A stage holds
- *   - the A rows of the group: PL planes of 64 or 128 rows x 64 bf16 (128 B); the
+ *   - the A rows of the group: PL planes of 64 rows x 64 bf16 (128 B); the
  *     16-byte chunk c of row r sits at slot c ^ ((r >> 1) & 7), so the 16
  *     rows of one ds_read_b128 pass cover all 64 banks;
  *   - the codes of the tile's weight rows for the group: q4 as rows of
