@@ -104,6 +104,26 @@ NMOE_HIP_API int nmoe_hip_check_device_status(nmoe_hip_ctx *ctx);
  * permutation, then each expert's weights read once for all its tokens);
  * fewer tokens run the per-token kernels. */
 #define NMOE_HIP_OPT_GROUPED_MIN_TOKENS 3
+/* NMOE_HIP_OPT_SPIN_LIMIT (default 0 = 2^20): unsuccessful poll rounds a
+ * persistent kernel's bounded wait tolerates before it gives up (a round
+ * trip to memory is about 1 us); at most NMOE_HIP_SPIN_LIMIT_MAX.  A wait
+ * that gives up sets the device status word (nmoe_hip_check_device_status
+ * returns NMOE_HIP_ETIMEDOUT) and makes every output the launch still writes
+ * NaN, so the failure also shows in the data without a host round trip. */
+#define NMOE_HIP_OPT_SPIN_LIMIT 4
+#define NMOE_HIP_SPIN_LIMIT_MAX (1 << 26)
+/* NMOE_HIP_OPT_SYNC_CHECK (default 0): 1 makes nmoe_moe_experts_*,
+ * nmoe_moe_layer, nmoe_moe_layer_rmsnorm and nmoe_moe_stack wait for their
+ * stream and return NMOE_HIP_ETIMEDOUT when a bounded wait expired (the
+ * call is then synchronous; nmoe_moe_stack checks once, after its last
+ * layer). */
+#define NMOE_HIP_OPT_SYNC_CHECK 5
+/* NMOE_HIP_OPT_SKEW_EPOCH (value = block 0..255; for tests of the failure
+ * path): moves that block's launch epoch one ahead, so the next fused
+ * launch cannot complete and ends through its bounded waits, as a launch
+ * whose blocks are not all resident would.  nmoe_hip_check_device_status
+ * then realigns the epochs.  Synchronous. */
+#define NMOE_HIP_OPT_SKEW_EPOCH 6
 NMOE_HIP_API int nmoe_hip_set_option(nmoe_hip_ctx *ctx, int option, int value);
 
 /* ---- buffers (backend.h:64-66: register_shared_buffer / register_state_buffer

@@ -13,7 +13,7 @@
 #include <stdlib.h>
 #include <string.h>
 
-#include "nmoe_hip_internal.h"
+#include "nmoe_device.h"
 
 #pragma clang fp contract(off)
 
@@ -43,6 +43,7 @@ extern "C" int nmoe_hip_create(int device, int max_tokens, nmoe_hip_ctx **out) {
     ctx->device = device;
     ctx->max_tokens = max_tokens;
     ctx->use_fused = 1;
+    ctx->spin_limit = NMOE_SPIN_LIMIT;
     hipDeviceProp_t prop;
     if (hipGetDeviceProperties(&prop, device) != hipSuccess || hipStreamCreate(&ctx->stream) != hipSuccess) {
         free(ctx);
@@ -116,7 +117,38 @@ extern "C" int nmoe_hip_set_option(nmoe_hip_ctx *ctx, int option, int value) {
         ctx->use_xcd_local = value != 0;
         return NMOE_HIP_OK;
     }
+    if (option == NMOE_HIP_OPT_SPIN_LIMIT) {
+        if (value < 0 || value > NMOE_HIP_SPIN_LIMIT_MAX)
+            return nmoe_fail(ctx, NMOE_HIP_EINVAL, "spin limit %d outside 0..%d", value, NMOE_HIP_SPIN_LIMIT_MAX);
+        ctx->spin_limit = value == 0 ? NMOE_SPIN_LIMIT : (uint32_t)value;
+        return NMOE_HIP_OK;
+    }
+    if (option == NMOE_HIP_OPT_SYNC_CHECK) {
+        ctx->sync_check = value != 0;
+        return NMOE_HIP_OK;
+    }
+    if (option == NMOE_HIP_OPT_SKEW_EPOCH) {
+        /* Moves block `value`'s launch epoch one ahead of the others, so the
+         * next fused launch cannot complete: its bounded waits expire and it
+         * reports ETIMEDOUT, the failure a block that is not resident would
+         * cause.  Synchronous; for tests of that path. */
+        if (value < 0 || value >= NMOE_SYNC_BLOCKS)
+            return nmoe_fail(ctx, NMOE_HIP_EINVAL, "block %d outside 0..%d", value, NMOE_SYNC_BLOCKS - 1);
+        uint32_t ep = 0;
+        NMOE_HIP_TRY(ctx, hipSetDevice(ctx->device));
+        NMOE_HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+        NMOE_HIP_TRY(ctx, hipMemcpy(&ep, ctx->sync + NMOE_SYNC_EPOCH(value), sizeof(ep), hipMemcpyDeviceToHost));
+        ep += 1u;
+        NMOE_HIP_TRY(ctx, hipMemcpy(ctx->sync + NMOE_SYNC_EPOCH(value), &ep, sizeof(ep), hipMemcpyHostToDevice));
+        return NMOE_HIP_OK;
+    }
     return nmoe_fail(ctx, NMOE_HIP_EINVAL, "unknown option %d", option);
+}
+
+extern "C" int nmoe_sync_check(nmoe_hip_ctx *ctx, void *stream) {
+    if (!ctx->sync_check) return NMOE_HIP_OK;
+    NMOE_HIP_TRY(ctx, hipStreamSynchronize(nmoe_stream_of(ctx, stream)));
+    return nmoe_hip_check_device_status(ctx);
 }
 
 extern "C" const char *nmoe_hip_last_error(const nmoe_hip_ctx *ctx) { return ctx != NULL ? ctx->err : "no context"; }

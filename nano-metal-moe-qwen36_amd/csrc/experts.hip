@@ -256,8 +256,9 @@ extern "C" int nmoe_moe_experts_q4(nmoe_hip_ctx *ctx, int layer, const void *x, 
     int rc = nmoe_check_experts(ctx, layer, 4, x, x_dtype, ntok, k, idx, w, h_mid, shared_out, shared_gate_raw, out,
                                 &pack);
     if (rc != NMOE_HIP_OK) return rc;
-    return nmoe_experts_dispatch<4>(ctx, pack, x, x_dtype, ntok, k, idx, w, h_mid, shared_out, shared_gate_raw, out,
-                                    nmoe_stream_of(ctx, stream));
+    rc = nmoe_experts_dispatch<4>(ctx, pack, x, x_dtype, ntok, k, idx, w, h_mid, shared_out, shared_gate_raw, out,
+                                  nmoe_stream_of(ctx, stream));
+    return rc != NMOE_HIP_OK ? rc : nmoe_sync_check(ctx, stream);
 }
 
 extern "C" int nmoe_moe_experts_q2(nmoe_hip_ctx *ctx, int layer, const void *x, int x_dtype, int ntok, int k,
@@ -267,8 +268,9 @@ extern "C" int nmoe_moe_experts_q2(nmoe_hip_ctx *ctx, int layer, const void *x, 
     int rc = nmoe_check_experts(ctx, layer, 2, x, x_dtype, ntok, k, idx, w, h_mid, shared_out, shared_gate_raw, out,
                                 &pack);
     if (rc != NMOE_HIP_OK) return rc;
-    return nmoe_experts_dispatch<2>(ctx, pack, x, x_dtype, ntok, k, idx, w, h_mid, shared_out, shared_gate_raw, out,
-                                    nmoe_stream_of(ctx, stream));
+    rc = nmoe_experts_dispatch<2>(ctx, pack, x, x_dtype, ntok, k, idx, w, h_mid, shared_out, shared_gate_raw, out,
+                                  nmoe_stream_of(ctx, stream));
+    return rc != NMOE_HIP_OK ? rc : nmoe_sync_check(ctx, stream);
 }
 
 extern "C" int nmoe_moe_layer(nmoe_hip_ctx *ctx, int layer, const nmoe_hip_router *router, const void *x, int x_dtype,
@@ -288,10 +290,12 @@ extern "C" int nmoe_moe_layer(nmoe_hip_ctx *ctx, int layer, const nmoe_hip_route
     if (h_mid == NULL || out == NULL) return nmoe_fail(ctx, NMOE_HIP_EINVAL, "NULL h_mid/out");
     if ((shared_out == NULL) != (shared_gate_raw == NULL))
         return nmoe_fail(ctx, NMOE_HIP_EINVAL, "shared_out and shared_gate_raw must both be set or both NULL");
-    if (ntok == 1 && ctx->fused_blocks > 0 && ctx->use_fused)
-        return nmoe_fused_decode(ctx, ctx->packs[layer].bits, 1, x, x_dtype, 0.0f, k, router, NULL, NULL,
-                                 h_mid, shared_out, shared_gate_raw, out, idx, w, logits,
-                                 (const uint8_t *)ctx->packs[layer].dev, nmoe_stream_of(ctx, stream));
+    if (ntok == 1 && ctx->fused_blocks > 0 && ctx->use_fused) {
+        rc = nmoe_fused_decode(ctx, ctx->packs[layer].bits, 1, x, x_dtype, 0.0f, k, router, NULL, NULL, h_mid,
+                               shared_out, shared_gate_raw, out, idx, w, logits,
+                               (const uint8_t *)ctx->packs[layer].dev, nmoe_stream_of(ctx, stream));
+        return rc != NMOE_HIP_OK ? rc : nmoe_sync_check(ctx, stream);
+    }
     uint32_t *ri = idx != NULL ? idx : ctx->idx;
     float *rw = w != NULL ? w : ctx->w;
     rc = nmoe_moe_route(ctx, router, x, x_dtype, ntok, k, ri, rw, logits, stream);
@@ -303,9 +307,11 @@ extern "C" int nmoe_moe_layer(nmoe_hip_ctx *ctx, int layer, const nmoe_hip_route
                                stream);
 }
 
-extern "C" int nmoe_moe_layer_rmsnorm(nmoe_hip_ctx *ctx, int layer, const nmoe_hip_router *router,
-                                      const float *h_in, float eps, int k, float *h_out, uint32_t *idx, float *w,
-                                      float *logits, void *stream) {
+/* nmoe_moe_layer_rmsnorm without the NMOE_HIP_OPT_SYNC_CHECK wait (the
+ * stack checks once, after its last layer). */
+extern "C" int nmoe_layer_rmsnorm_launch(nmoe_hip_ctx *ctx, int layer, const nmoe_hip_router *router,
+                                         const float *h_in, float eps, int k, float *h_out, uint32_t *idx, float *w,
+                                         float *logits, void *stream) {
     if (ctx == NULL) return NMOE_HIP_EINVAL;
     if (layer < 0 || layer >= NMOE_HIP_MAX_LAYERS || ctx->packs[layer].dev == NULL)
         return nmoe_fail(ctx, NMOE_HIP_ENOENT, "layer %d has no resident pack", layer);
@@ -322,4 +328,11 @@ extern "C" int nmoe_moe_layer_rmsnorm(nmoe_hip_ctx *ctx, int layer, const nmoe_h
     return nmoe_fused_decode(ctx, ctx->packs[layer].bits, 1, h_in, 2 /* XNORM */, eps, k, router, NULL, NULL,
                              h_in, NULL, NULL, h_out, idx, w, logits, (const uint8_t *)ctx->packs[layer].dev,
                              nmoe_stream_of(ctx, stream));
+}
+
+extern "C" int nmoe_moe_layer_rmsnorm(nmoe_hip_ctx *ctx, int layer, const nmoe_hip_router *router,
+                                      const float *h_in, float eps, int k, float *h_out, uint32_t *idx, float *w,
+                                      float *logits, void *stream) {
+    const int rc = nmoe_layer_rmsnorm_launch(ctx, layer, router, h_in, eps, k, h_out, idx, w, logits, stream);
+    return rc != NMOE_HIP_OK ? rc : nmoe_sync_check(ctx, stream);
 }

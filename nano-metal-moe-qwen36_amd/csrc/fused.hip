@@ -110,6 +110,8 @@ struct nmoe_fused_args {
     uint64_t *xch;
     uint32_t *sync;
     int xcd_local; /* act travels through the die's L2 (a group's blocks share a die) */
+    uint32_t spin; /* unsuccessful poll rounds a wait tolerates before it gives up */
+    uint32_t epoch_arg; /* nonzero: the launch epoch (no per-block epoch words) */
 };
 
 /* Die-local exchange: words written and read only by blocks of one
@@ -141,11 +143,23 @@ __device__ __forceinline__ uint32_t nmoe_xcc_id() {
     return v;
 }
 
-/* Polls n tagged words until all carry `epoch` (bounded); returns the
- * values.  Each lane polls its own words. */
+/* A bounded wait that gave up: the status word tells the host, and the
+ * block's LDS flag makes everything the block publishes from then on NaN,
+ * so a result computed from words that never arrived cannot pass for a
+ * valid one.  Nothing read afterwards is used as an address without a
+ * clamp, so the block still finishes in bounds. */
+__device__ __forceinline__ void nmoe_wait_expired(uint32_t *status, uint32_t *bad) {
+    __hip_atomic_store(status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(bad, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+/* Polls n tagged words until all carry `epoch` (at most `spin` unsuccessful
+ * rounds); returns the values (a word that never arrived leaves v[i] as it
+ * was).  Each lane polls its own words. */
 template <int N>
 __device__ __forceinline__ void nmoe_poll(const uint64_t *const p[N], uint32_t epoch, float v[N], uint32_t *status,
-                                          bool die_local = false, uint32_t need = (1u << N) - 1u) {
+                                          uint32_t *bad, uint32_t spin, bool die_local = false,
+                                          uint32_t need = (1u << N) - 1u) {
     /* a word, once seen with this epoch, is not loaded again: after the
      * first round only the stragglers' words are re-polled, which keeps the
      * polling traffic off the memory channels the late writers need.  need:
@@ -165,8 +179,8 @@ __device__ __forceinline__ void nmoe_poll(const uint64_t *const p[N], uint32_t e
             }
         if (need == 0) return;
         __builtin_amdgcn_s_sleep(1);
-        if (++spins > NMOE_SPIN_LIMIT) {
-            __hip_atomic_store(status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (++spins > spin) {
+            nmoe_wait_expired(status, bad);
             return;
         }
     }
@@ -178,9 +192,9 @@ __device__ __forceinline__ void nmoe_poll(const uint64_t *const p[N], uint32_t e
  * trip later instead of two.  All N words are loaded each round (they
  * must be valid addresses); only those in `need` are waited for. */
 template <int N>
-__device__ __forceinline__ void nmoe_poll2(const uint64_t *const p[N], uint32_t epoch, float v[N], uint32_t *status,
-                                           uint32_t need) {
-    if (need == 0) return;
+__device__ __forceinline__ bool nmoe_poll2(const uint64_t *const p[N], uint32_t epoch, float v[N], uint32_t *status,
+                                           uint32_t *bad, uint32_t spin, uint32_t need) {
+    if (need == 0) return false;
     uint32_t spins = 0;
     uint64_t wa[N], wb[N];
     auto issue = [&](uint64_t(&w)[N]) { /* every word, so each round is N loads and the wait is vmcnt(N) */
@@ -201,30 +215,38 @@ __device__ __forceinline__ void nmoe_poll2(const uint64_t *const p[N], uint32_t 
         issue(wb);
         __builtin_amdgcn_sched_barrier(0);
         check(wa);
-        if (need == 0) return;
+        if (need == 0) return false;
         __builtin_amdgcn_s_sleep(4);
         issue(wa);
         __builtin_amdgcn_sched_barrier(0);
         check(wb);
-        if (need == 0) return;
-        if (++spins > NMOE_SPIN_LIMIT / 2) {
-            __hip_atomic_store(status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            return;
+        if (need == 0) return false;
+        if (++spins > spin / 2) {
+            nmoe_wait_expired(status, bad);
+            return true;
         }
     }
 }
 
 /* Waits (bounded) until the LDS word *w exceeds v: a hand-off from another
- * wavefront of the block that needs no block-wide barrier. */
-__device__ __forceinline__ void nmoe_lds_wait_above(uint32_t *w, uint32_t v, uint32_t *status) {
+ * wavefront of the block that needs no block-wide barrier.  An LDS poll
+ * round is about 32 times shorter than a round trip to memory, so the bound
+ * is 32 times the rounds of the memory polls: the waiting wavefront then
+ * gives up no sooner than the wavefront it waits for. */
+__device__ __forceinline__ void nmoe_lds_wait_above(uint32_t *w, uint32_t v, uint32_t *status, uint32_t *bad,
+                                                    uint32_t spin) {
     uint32_t spins = 0;
     while (__hip_atomic_load(w, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) <= v) {
         __builtin_amdgcn_s_sleep(1);
-        if (++spins > NMOE_SPIN_LIMIT) {
-            __hip_atomic_store(status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (++spins > 32u * spin) {
+            nmoe_wait_expired(status, bad);
             return;
         }
     }
+}
+
+__device__ __forceinline__ bool nmoe_lds_flag(uint32_t *f) {
+    return __hip_atomic_load(f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) != 0u;
 }
 
 /* The lane's n activations at columns c0.. (fp32, bf16, or normalised h).
@@ -277,6 +299,7 @@ __global__ void __launch_bounds__(NMOE_FUSED_THREADS) nmoe_fused_decode_kernel(n
     __shared__ float s_f[1];
     __shared__ uint32_t s_epoch;
     __shared__ uint32_t s_ncand, s_confirm, s_lgok; /* control -> workers / control -> control hand-offs */
+    __shared__ uint32_t s_bad; /* a wait of this block gave up: what it publishes is NaN */
     __shared__ __align__(16) float s_h[XMODE == NMOE_XNORM ? NMOE_HIDDEN : 4];
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -292,9 +315,10 @@ __global__ void __launch_bounds__(NMOE_FUSED_THREADS) nmoe_fused_decode_kernel(n
     /* Independent loads go out first and unconditionally (loads retire in
      * order, so a later wait on one of them must not cover the big ones):
      * the launch epoch, the exp2 table entry, the residual row this thread
-     * may combine; then the control wavefront's router row and x columns. */
+     * may combine; then the control wavefront's router row and x columns.
+     * The epoch is the block's own launch count, or the host's when given. */
     uint32_t *ep = a.sync + NMOE_SYNC_EPOCH(blockIdx.x);
-    const uint32_t ep_old = nmoe_ld_u32_dev(ep);
+    const uint32_t ep_old = a.epoch_arg != 0u ? 0u : nmoe_ld_u32_dev(ep);
     const uint64_t tab_v = nmoe_fused_exp2_tab[tid & 31];
     const int crow = j * NMOE_FUSED_CHUNK + (tid & (NMOE_FUSED_CHUNK - 1));
     const float hm = a.h_mid[crow];
@@ -303,7 +327,7 @@ __global__ void __launch_bounds__(NMOE_FUSED_THREADS) nmoe_fused_decode_kernel(n
     uint4 wv[4];
     uint32_t wq[4];
     uint16_t rsr[4], rbr[4];
-    float xs_r[32], lv[4];
+    float xs_r[32], lv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     if (ROUTE && cwave) {
         if (ROUTE == NMOE_ROUTE_Q4) {
             /* q4 router row: words lane + 64q (columns 8 word .. +7) and their
@@ -326,13 +350,25 @@ __global__ void __launch_bounds__(NMOE_FUSED_THREADS) nmoe_fused_decode_kernel(n
             for (int q = 0; q < 4; q++) nmoe_x_cols<XMODE>(a.x, (lane + 64 * q) * 8, 8, 1.0, xs_r + 8 * q);
     }
     if (tid < 32) s_tab[tid] = tab_v;
-    if (tid < NMOE_MAX_K) s_cand[tid] = 0u;
+    if (tid < NMOE_MAX_K) { /* in-range defaults for every routing word a wait may leave unwritten */
+        s_cand[tid] = 0u;
+        s_gx[tid] = 0u;
+        s_slotg[tid] = (uint32_t)tid;
+        s_w[tid] = 0.0f;
+        s_t[tid] = 0u;
+        s_t[NMOE_MAX_K + tid] = 0u;
+    }
     if (tid == 0) {
-        __hip_atomic_store(ep, ep_old + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        s_epoch = ep_old + 1u;
+        uint32_t e = a.epoch_arg;
+        if (e == 0u) {
+            e = ep_old + 1u;
+            __hip_atomic_store(ep, e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        s_epoch = e;
         s_ncand = 0u;
         s_confirm = 0u;
         s_lgok = 0u;
+        s_bad = 0u;
     }
     if (XMODE == NMOE_XNORM) {
         /* x = h / rms once per block, into LDS in the workers' swizzled
@@ -374,7 +410,7 @@ __global__ void __launch_bounds__(NMOE_FUSED_THREADS) nmoe_fused_decode_kernel(n
              * settles. */
             const uint64_t *pl[4] = {xlg + NMOE_XCH_SP * lane, xlg + NMOE_XCH_SP * (lane + 64),
                                      xlg + NMOE_XCH_SP * (lane + 128), xlg + NMOE_XCH_SP * (lane + 192)};
-            nmoe_poll<4>(pl, epoch, lv, status);
+            nmoe_poll<4>(pl, epoch, lv, status, &s_bad, a.spin);
 #pragma unroll
             for (int q = 0; q < 4; q++) s_lg[lane + 64 * q] = lv[q];
             if (lane == 0) __hip_atomic_store(&s_lgok, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
@@ -418,14 +454,14 @@ __global__ void __launch_bounds__(NMOE_FUSED_THREADS) nmoe_fused_decode_kernel(n
          * the moment the logits are in, alongside the candidate rounds and
          * the expert loads; then the expert of each group. */
         __builtin_amdgcn_s_setprio(2);
-        nmoe_lds_wait_above(&s_lgok, 0u, status);
+        nmoe_lds_wait_above(&s_lgok, 0u, status, &s_bad, a.spin);
         float l[4], p[4];
 #pragma unroll
         for (int q = 0; q < 4; q++) l[q] = s_lg[lane + 64 * q];
         nmoe_wave_softmax(l, NMOE_EXPERTS, s_scratch, s_tab, p);
 #pragma unroll
         for (int q = 0; q < 4; q++) s_scratch[lane + 64 * q] = p[q];
-        nmoe_lds_wait_above(&s_ncand, (uint32_t)(k - 1), status);
+        nmoe_lds_wait_above(&s_ncand, (uint32_t)(k - 1), status, &s_bad, a.spin);
         /* lane s < k: group s's candidate and its probability.  With p8 the
          * smallest of these, math.m's top-k is {p > p8} plus the lowest
          * entries with p == p8, since p8 is at most the k-th largest
@@ -434,7 +470,8 @@ __global__ void __launch_bounds__(NMOE_FUSED_THREADS) nmoe_fused_decode_kernel(n
          * is the candidate set, each group keeps its expert and only the
          * slot order (probability, ties to the lower entry) is left. */
         const bool mine = lane < k;
-        const uint32_t c = mine ? s_cand[lane] - 1u : 0u;
+        const uint32_t sc = mine ? s_cand[lane] : 0u; /* 1..256 once published */
+        const uint32_t c = sc != 0u ? min(sc - 1u, (uint32_t)(NMOE_EXPERTS - 1)) : 0u;
         const uint32_t pcb = mine ? __float_as_uint(s_scratch[c]) : 0xffffffffu; /* p >= 0: bits order like values */
         uint32_t p8 = 0xffffffffu;
 #pragma unroll
@@ -591,8 +628,9 @@ __global__ void __launch_bounds__(NMOE_FUSED_THREADS) nmoe_fused_decode_kernel(n
 #pragma unroll
             for (int c = 0; c < XV; c++) xr[c] = xp[c];
         if (ROUTE) /* candidate g published by the control wavefront */
-            nmoe_lds_wait_above(&s_cand[g], 0u, status);
-        cand_g = s_cand[g] - 1u;
+            nmoe_lds_wait_above(&s_cand[g], 0u, status, &s_bad, a.spin);
+        const uint32_t cg = s_cand[g]; /* 0 only if that wait gave up */
+        cand_g = cg != 0u ? min(cg - 1u, (uint32_t)(NMOE_EXPERTS - 1)) : 0u;
         __builtin_amdgcn_sched_barrier(0);
         load_expert(cand_g);
         /* keep every weight load above in one burst: no compute hoisted into it */
@@ -632,13 +670,16 @@ __global__ void __launch_bounds__(NMOE_FUSED_THREADS) nmoe_fused_decode_kernel(n
     if (!ctrl) {
         gate_up();
         if (ROUTE) {
-            nmoe_lds_wait_above(&s_confirm, 0u, status);
-            const uint32_t xg = s_gx[g];
+            nmoe_lds_wait_above(&s_confirm, 0u, status, &s_bad, a.spin);
+            const uint32_t xg = min(s_gx[g], (uint32_t)(NMOE_EXPERTS - 1));
             if (xg != cand_g) { /* probability tie at the boundary: redo with the selected expert */
                 load_expert(xg);
                 gate_up();
             }
         }
+        if (ROUTE && nmoe_lds_flag(&s_bad)) /* the routing this act rests on is not the token's */
+#pragma unroll
+            for (int i = 0; i < GSTEPS; i++) actv[i] = __builtin_nanf("");
         if (gl == 0) {
 #pragma unroll
             for (int i = 0; i < GSTEPS; i++) {
@@ -664,8 +705,11 @@ __global__ void __launch_bounds__(NMOE_FUSED_THREADS) nmoe_fused_decode_kernel(n
         const uint64_t *pa[APT];
         float av[APT];
 #pragma unroll
-        for (int q = 0; q < APT; q++) pa[q] = xact + NMOE_XCH_ASP * (tid + 64 * NMOE_FUSED_WORKERS * q);
-        nmoe_poll<APT>(pa, epoch, av, status, a.xcd_local != 0);
+        for (int q = 0; q < APT; q++) {
+            pa[q] = xact + NMOE_XCH_ASP * (tid + 64 * NMOE_FUSED_WORKERS * q);
+            av[q] = 0.0f;
+        }
+        nmoe_poll<APT>(pa, epoch, av, status, &s_bad, a.spin, a.xcd_local != 0);
 #pragma unroll
         for (int q = 0; q < APT; q++) s_act[nmoe_act_slot<Q::CPL / 4>(tid + 64 * NMOE_FUSED_WORKERS * q)] = av[q];
     }
@@ -698,9 +742,10 @@ __global__ void __launch_bounds__(NMOE_FUSED_THREADS) nmoe_fused_decode_kernel(n
      * tagged words and are done.  The combiner polls the K-1 partials of its
      * chunk: one round trip after the last one is written. */
     const int row = j * NMOE_FUSED_CHUNK + tid;
+    const bool poisoned = nmoe_lds_flag(&s_bad); /* every wait of the block is behind the barrier above */
     if (tid < NMOE_FUSED_CHUNK) {
         if (g != j % k) {
-            nmoe_st_tagged(ypart + g * NMOE_HIDDEN + row, epoch, s_y[tid]);
+            nmoe_st_tagged(ypart + g * NMOE_HIDDEN + row, epoch, poisoned ? __builtin_nanf("") : s_y[tid]);
         } else {
             const uint64_t *pp[NMOE_MAX_K];
             float ys[NMOE_MAX_K];
@@ -722,7 +767,8 @@ __global__ void __launch_bounds__(NMOE_FUSED_THREADS) nmoe_fused_decode_kernel(n
                 ident = ident && sgl[s] == (uint32_t)s;
             }
             const float gsig = a.shared_out != NULL ? nmoe_sigmoid_dev(sgr) : 0.0f;
-            nmoe_poll2<NMOE_MAX_K>(pp, epoch, ys, status, ((1u << k) - 1u) & ~(1u << g));
+            const bool expired = nmoe_poll2<NMOE_MAX_K>(pp, epoch, ys, status, &s_bad, a.spin,
+                                                        ((1u << k) - 1u) & ~(1u << g));
             /* slot order: slot s is streamed by group sgl[s] */
             float moe = 0.0f;
             if (ident) {
@@ -743,13 +789,13 @@ __global__ void __launch_bounds__(NMOE_FUSED_THREADS) nmoe_fused_decode_kernel(n
             }
             float r = hm + moe;
             if (a.shared_out != NULL) r = r + gsig * sh;
-            a.out[row] = r;
+            a.out[row] = poisoned || expired ? __builtin_nanf("") : r;
         }
     }
     if (ROUTE && blockIdx.x == 0 && cwave) {
         if (lane < NMOE_MAX_K) {
-            if (a.idx_out != NULL) a.idx_out[lane] = s_t[lane];
-            if (a.w_out != NULL) a.w_out[lane] = s_w[lane];
+            if (a.idx_out != NULL) a.idx_out[lane] = min(s_t[lane], (uint32_t)(NMOE_EXPERTS - 1));
+            if (a.w_out != NULL) a.w_out[lane] = poisoned ? __builtin_nanf("") : s_w[lane];
         }
         if (a.logits_out != NULL)
 #pragma unroll
@@ -879,6 +925,8 @@ extern "C" int nmoe_fused_decode(nmoe_hip_ctx *ctx, int bits, int route, const v
     a.xch = ctx->xch;
     a.sync = ctx->sync;
     a.xcd_local = ctx->use_xcd_local;
+    a.spin = ctx->spin_limit;
+    a.epoch_arg = 0u;
     hipError_t e = hipErrorInvalidValue;
     const int r = !route ? NMOE_ROUTE_GIVEN : q4r ? NMOE_ROUTE_Q4 : NMOE_ROUTE_BF16;
     if (bits == 4)

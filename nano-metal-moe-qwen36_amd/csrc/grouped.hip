@@ -270,7 +270,9 @@ __device__ __forceinline__ void nmoe_dispatch_scatter(const uint32_t *idx, int n
         if (e < NMOE_EXPERTS) {
             uint32_t pos = s_base[e] + rank;
             for (int w = 0; w < wave; w++) pos += s_wc[w][e];
-            perm[pos] = (uint32_t)q;
+            /* pos < n unless the slices' meeting gave up (then the counts of
+             * the other slices may be stale and the launch reports it) */
+            if (pos < (uint32_t)n) perm[pos] = (uint32_t)q;
         }
         __syncthreads();
         s_base[tid] += s_wc[0][tid] + s_wc[1][tid] + s_wc[2][tid] + s_wc[3][tid];
@@ -343,8 +345,9 @@ __device__ __forceinline__ void nmoe_grouped_xprep(const XT *x, uint16_t *xhi, u
 template <int BITS, typename XT>
 __global__ void __launch_bounds__(256) nmoe_grouped_prep_kernel(const uint32_t *idx, int ntok, int k, int nd,
                                                                 uint32_t *counts, uint32_t *perm, uint32_t *offsets,
-                                                                uint4 *rank, uint32_t *sync, const XT *x,
-                                                                uint16_t *xhi, uint16_t *xlo, uint16_t *xs3) {
+                                                                uint4 *rank, uint32_t *sync, uint32_t spin,
+                                                                const XT *x, uint16_t *xhi, uint16_t *xlo,
+                                                                uint16_t *xs3) {
     const int b = blockIdx.x;
     if (b >= nd) {
         nmoe_grouped_xprep<BITS, XT>(x, xhi, xlo, xs3, b - nd);
@@ -370,7 +373,7 @@ __global__ void __launch_bounds__(256) nmoe_grouped_prep_kernel(const uint32_t *
             uint32_t spins = 0;
             while ((int32_t)(nmoe_ld_u32_dev(cnt) - target) < 0) {
                 __builtin_amdgcn_s_sleep(1);
-                if (++spins > NMOE_SPIN_LIMIT) {
+                if (++spins > spin) {
                     __hip_atomic_store(sync + NMOE_SYNC_STATUS, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                     break;
                 }
@@ -613,7 +616,7 @@ __host__ __device__ constexpr int nmoe_gu_stages(int bits, int xpl, int nw) {
 template <int BITS, int XPL, int NW>
 __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
 nmoe_grouped_gateup_kernel(const uint8_t *pack, const uint16_t *xhi, const uint16_t *xlo, const uint16_t *xs3,
-                           const uint32_t *perm, const uint4 *rank, int k, int lanes, uint16_t *ahi,
+                           const uint32_t *perm, const uint4 *rank, int k, int lanes, int nrows, uint16_t *ahi,
                            uint16_t *alo, float *as) {
     using Q = nmoe_q<BITS>;
     using L = nmoe_layout<BITS>;
@@ -650,9 +653,11 @@ nmoe_grouped_gateup_kernel(const uint8_t *pack, const uint16_t *xhi, const uint1
      * longest tiles start first */
     int es, nt;
     nmoe_die_tile(blockIdx.x % (NMOE_EXPERTS * NTILE), NTILE, es, nt);
+    /* (e, first entry, entries) of a dispatch whose meeting gave up can be
+     * anything; the clamps keep every access inside the buffers */
     const uint4 rk = rank[es];
-    const int e = (int)rk.x;
-    const uint32_t p0 = rk.y, n = rk.z;
+    const int e = (int)min(rk.x, (uint32_t)(NMOE_EXPERTS - 1));
+    const uint32_t p0 = min(rk.y, (uint32_t)nrows), n = min(rk.z, (uint32_t)nrows - p0);
     if (n <= (uint32_t)(pl * MCH)) return;
     const int tid = threadIdx.x, lane = tid & 63, col = lane & 15, kb = lane >> 4;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -667,7 +672,7 @@ nmoe_grouped_gateup_kernel(const uint8_t *pack, const uint16_t *xhi, const uint1
                                (const uint16_t *)(ex + L::up_b) + (size_t)nt * NT * G};
 
     for (uint32_t m0 = pl * MCH; m0 < n; m0 += lanes * MCH) {
-        if (tid < MCH) s_tok[tid] = perm[p0 + min(m0 + tid, n - 1)] / (uint32_t)k;
+        if (tid < MCH) s_tok[tid] = min(perm[p0 + min(m0 + tid, n - 1)], (uint32_t)nrows - 1u) / (uint32_t)k;
         nmoe_lds_barrier();
         /* this lane's A row for instruction wave + NW i: entry 8 (wave + NW i) + lane / 8 */
         uint32_t row_off[AI];
@@ -876,7 +881,7 @@ __host__ __device__ constexpr int nmoe_dn_stages(int bits, int nw) {
 template <int BITS, int NW>
 __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
 nmoe_grouped_down_kernel(const uint8_t *pack, const uint16_t *ahi, const uint16_t *alo, const float *as,
-                         const uint32_t *perm, const uint4 *rank, int lanes, float *y) {
+                         const uint32_t *perm, const uint4 *rank, int lanes, int nrows, float *y) {
     using Q = nmoe_q<BITS>;
     using L = nmoe_layout<BITS>;
     constexpr int G = NMOE_INTER / NMOE_GROUP; /* 8 groups */
@@ -904,9 +909,9 @@ nmoe_grouped_down_kernel(const uint8_t *pack, const uint16_t *ahi, const uint16_
      * longest tiles start first */
     int es, nt;
     nmoe_die_tile(blockIdx.x % (NMOE_EXPERTS * NTILE), NTILE, es, nt);
-    const uint4 rk = rank[es];
-    const int e = (int)rk.x;
-    const uint32_t p0 = rk.y, n = rk.z;
+    const uint4 rk = rank[es]; /* clamped as in the gate/up kernel */
+    const int e = (int)min(rk.x, (uint32_t)(NMOE_EXPERTS - 1));
+    const uint32_t p0 = min(rk.y, (uint32_t)nrows), n = min(rk.z, (uint32_t)nrows - p0);
     if (n <= (uint32_t)(pl * MCH)) return;
     const int tid = threadIdx.x, lane = tid & 63, col = lane & 15, kb = lane >> 4;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -918,7 +923,7 @@ nmoe_grouped_down_kernel(const uint8_t *pack, const uint16_t *ahi, const uint16_
         /* the chunk's output slots, stored to LDS after the stages are issued
          * (so that this load's wait does not hold them back) and visible
          * after the barrier below */
-        const uint32_t qv = tid < MCH ? perm[p0 + min(m0 + tid, n - 1)] : 0u;
+        const uint32_t qv = tid < MCH ? min(perm[p0 + min(m0 + tid, n - 1)], (uint32_t)nrows - 1u) : 0u;
         /* this lane's A row for instruction wave + NW i: act row p0 + m0 + 8 (wave + NW i) + lane / 8 */
         uint32_t row_off[AI];
 #pragma unroll
@@ -1032,11 +1037,19 @@ nmoe_grouped_down_kernel(const uint8_t *pack, const uint16_t *ahi, const uint16_
 /* out[t] = h_mid[t] + sum_{s<k} w[t][s] y[t*k+s] in slot order
  * (kernels.metal:1394-1423) (+ sigmoid(g) * shared_out); a slot whose index
  * is outside the layer contributes nothing (runtime.m:2977-2981). */
+/* A set status word (a bounded wait of this or an earlier launch gave up
+ * and the host has not read the status yet) makes the combine write NaN:
+ * y may rest on a dispatch that never completed. */
+__device__ __forceinline__ bool nmoe_status_set(const uint32_t *status) {
+    return __hip_atomic_load((uint32_t *)status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u;
+}
+
 /* The same for rows not 16-byte aligned: one row per thread. */
 __global__ void __launch_bounds__(256) nmoe_grouped_combine_rows_kernel(const float *y, const uint32_t *idx,
                                                                          const float *w, int k, const float *h_mid,
                                                                          const float *shared_out,
-                                                                         const float *shared_gate_raw, float *out) {
+                                                                         const float *shared_gate_raw,
+                                                                         const uint32_t *status, float *out) {
     const int t = blockIdx.y, r = blockIdx.x * 256 + threadIdx.x;
     float moe = 0.0f;
     for (int s = 0; s < k; s++) {
@@ -1045,13 +1058,14 @@ __global__ void __launch_bounds__(256) nmoe_grouped_combine_rows_kernel(const fl
     }
     float o = h_mid[(size_t)t * NMOE_HIDDEN + r] + moe;
     if (shared_out != NULL) o = o + nmoe_sigmoid_dev(shared_gate_raw[t]) * shared_out[(size_t)t * NMOE_HIDDEN + r];
-    out[(size_t)t * NMOE_HIDDEN + r] = o;
+    out[(size_t)t * NMOE_HIDDEN + r] = nmoe_status_set(status) ? __builtin_nanf("") : o;
 }
 
 __global__ void __launch_bounds__(256) nmoe_grouped_combine_kernel(const float *y, const uint32_t *idx,
                                                                     const float *w, int k, const float *h_mid,
                                                                     const float *shared_out,
-                                                                    const float *shared_gate_raw, float *out) {
+                                                                    const float *shared_gate_raw,
+                                                                    const uint32_t *status, float *out) {
     /* four consecutive rows per thread; all k partial rows are loaded before
      * the sum (an invalid slot's row was never written: its value is
      * dropped by the select, never multiplied into the sum) */
@@ -1077,6 +1091,7 @@ __global__ void __launch_bounds__(256) nmoe_grouped_combine_kernel(const float *
         const float4 sh = *(const float4 *)(shared_out + (size_t)t * NMOE_HIDDEN + r);
         o[0] = o[0] + g * sh.x, o[1] = o[1] + g * sh.y, o[2] = o[2] + g * sh.z, o[3] = o[3] + g * sh.w;
     }
+    if (nmoe_status_set(status)) o[0] = o[1] = o[2] = o[3] = __builtin_nanf("");
     *(float4 *)(out + (size_t)t * NMOE_HIDDEN + r) = make_float4(o[0], o[1], o[2], o[3]);
 }
 
@@ -1097,6 +1112,14 @@ extern "C" int nmoe_grouped_init(nmoe_hip_ctx *ctx) {
         hipMalloc((void **)&ctx->g_as, rows * (NMOE_INTER / NMOE_GROUP) * sizeof(float)) != hipSuccess ||
         hipMalloc((void **)&ctx->g_y, rows * NMOE_HIDDEN * sizeof(float)) != hipSuccess)
         return NMOE_HIP_ENOMEM;
+    /* the dispatch's words start in range: a launch whose slices' meeting
+     * gives up then reads zeros, never uninitialised counts */
+    if (hipMemset(ctx->g_counts, 0, NMOE_DISPATCH_MAX * (NMOE_EXPERTS + 1) * sizeof(uint32_t)) != hipSuccess ||
+        hipMemset(ctx->g_perm, 0, rows * sizeof(uint32_t)) != hipSuccess ||
+        hipMemset(ctx->g_offsets, 0, (NMOE_EXPERTS + 1) * sizeof(uint32_t)) != hipSuccess ||
+        hipMemset(ctx->g_rank, 0, NMOE_EXPERTS * 4 * sizeof(uint32_t)) != hipSuccess ||
+        hipDeviceSynchronize() != hipSuccess)
+        return NMOE_HIP_EHIP;
     return NMOE_HIP_OK;
 }
 
@@ -1112,8 +1135,8 @@ extern "C" int nmoe_grouped_dispatch(nmoe_hip_ctx *ctx, const uint32_t *idx, int
                                      uint32_t *offsets, hipStream_t s) {
     const int nd = nmoe_dispatch_blocks(ntok * k);
     hipLaunchKernelGGL((nmoe_grouped_prep_kernel<4, uint16_t>), dim3(nd), dim3(256), 0, s, idx, ntok, k, nd,
-                       ctx->g_counts, perm, offsets, (uint4 *)ctx->g_rank, ctx->sync, (const uint16_t *)NULL,
-                       (uint16_t *)NULL, (uint16_t *)NULL, (uint16_t *)NULL);
+                       ctx->g_counts, perm, offsets, (uint4 *)ctx->g_rank, ctx->sync, ctx->spin_limit,
+                       (const uint16_t *)NULL, (uint16_t *)NULL, (uint16_t *)NULL, (uint16_t *)NULL);
     const hipError_t e = hipGetLastError();
     return e == hipSuccess ? NMOE_HIP_OK : nmoe_hip_check(ctx, e, "dispatch launch");
 }
@@ -1128,12 +1151,12 @@ static int nmoe_grouped_run(nmoe_hip_ctx *ctx, const uint8_t *pack, const void *
     if (bf)
         hipLaunchKernelGGL((nmoe_grouped_prep_kernel<BITS, uint16_t>), gprep, dim3(256), 0, s, idx, ntok, k, nd,
                            ctx->g_counts, ctx->g_perm, ctx->g_offsets, (uint4 *)ctx->g_rank, ctx->sync,
-                           (const uint16_t *)x, ctx->g_xhi,
+                           ctx->spin_limit, (const uint16_t *)x, ctx->g_xhi,
                            (uint16_t *)NULL, ctx->g_xs);
     else
         hipLaunchKernelGGL((nmoe_grouped_prep_kernel<BITS, float>), gprep, dim3(256), 0, s, idx, ntok, k, nd,
                            ctx->g_counts, ctx->g_perm, ctx->g_offsets, (uint4 *)ctx->g_rank, ctx->sync,
-                           (const float *)x, ctx->g_xhi,
+                           ctx->spin_limit, (const float *)x, ctx->g_xhi,
                            ctx->g_xlo, ctx->g_xs);
     constexpr int NW = NMOE_GROUPED_NW;
     const dim3 blk(64 * NW);
@@ -1149,21 +1172,23 @@ static int nmoe_grouped_run(nmoe_hip_ctx *ctx, const uint8_t *pack, const void *
     const uint16_t *ahi = (const uint16_t *)ctx->g_ahi, *alo = (const uint16_t *)ctx->g_alo;
     const uint16_t *xs3 = ctx->g_xs;
     const float *as = (const float *)ctx->g_as;
+    const int nrows = ntok * k;
     /* gate/up, then down */
     if (bf)
         hipLaunchKernelGGL((nmoe_grouped_gateup_kernel<BITS, 1, NW>), ggu, blk, 0, s, pack, xhi, xlo, xs3, perm, rank, k,
-                           lanes, ctx->g_ahi, ctx->g_alo, ctx->g_as);
+                           lanes, nrows, ctx->g_ahi, ctx->g_alo, ctx->g_as);
     else
         hipLaunchKernelGGL((nmoe_grouped_gateup_kernel<BITS, 2, NW>), ggu, blk, 0, s, pack, xhi, xlo, xs3, perm, rank, k,
-                           lanes, ctx->g_ahi, ctx->g_alo, ctx->g_as);
+                           lanes, nrows, ctx->g_ahi, ctx->g_alo, ctx->g_as);
     hipLaunchKernelGGL((nmoe_grouped_down_kernel<BITS, NW>), gdn, blk, 0, s, pack, ahi, alo, as, perm, rank, lanes,
-                       ctx->g_y);
+                       nrows, ctx->g_y);
+    const uint32_t *status = ctx->sync + NMOE_SYNC_STATUS;
     if (nmoe_aligned(h_mid, 16) && nmoe_aligned(out, 16) && (shared_out == NULL || nmoe_aligned(shared_out, 16)))
         hipLaunchKernelGGL(nmoe_grouped_combine_kernel, dim3(NMOE_HIDDEN / 1024, ntok), dim3(256), 0, s,
-                           (const float *)ctx->g_y, idx, w, k, h_mid, shared_out, shared_gate_raw, out);
+                           (const float *)ctx->g_y, idx, w, k, h_mid, shared_out, shared_gate_raw, status, out);
     else
         hipLaunchKernelGGL(nmoe_grouped_combine_rows_kernel, dim3(NMOE_HIDDEN / 256, ntok), dim3(256), 0, s,
-                           (const float *)ctx->g_y, idx, w, k, h_mid, shared_out, shared_gate_raw, out);
+                           (const float *)ctx->g_y, idx, w, k, h_mid, shared_out, shared_gate_raw, status, out);
     const hipError_t e = hipGetLastError();
     return e == hipSuccess ? NMOE_HIP_OK : nmoe_hip_check(ctx, e, "grouped expert launch");
 }

@@ -1,8 +1,9 @@
 /*
  * nmoe_device.h -- device building blocks shared by the decode kernels:
  * DPP reductions, q4/q2 row dot products, the router row, bit-exact routing
- * of one token by one wavefront, and the grid barrier of the persistent
- * kernel.  Header-only (every .hip file is its own code object).
+ * of one token by one wavefront, the tagged words the persistent kernels
+ * exchange and the exact RMSNorm.  Header-only (every .hip file is its own
+ * code object).
  */
 #ifndef NMOE_DEVICE_H
 #define NMOE_DEVICE_H
@@ -261,12 +262,21 @@ __device__ __forceinline__ float nmoe_router_row_bf16(const uint4 wv[4], const f
     return nmoe_wave_sum_tree(acc);
 }
 
-/* Router logit of one q4 row (the model's router, metal/kernels.metal:472-513
- * semantics) by one wavefront: lane L owns the words L, L+64, L+128, L+192
- * (columns 8 word .. +7) and their groups' raw bf16 scale and bias;
- * w = fma(q, s, b), acc = fma(w, x, acc) in column order, lanes combined by
- * the pairwise tree -- the order of the multi-launch q4 router kernel, so both
- * paths give the same logits. */
+/* One element of the q4 router's dot product in the reference's per-element
+ * form (metal/kernels.metal:500-508): acc + fma(q, scale*x, bias*x), both
+ * products rounded to fp32 before the fma and the fma rounded before the add. */
+__device__ __forceinline__ float nmoe_router_q4_term(float acc, uint32_t q, float s, float b, float x) {
+#pragma clang fp contract(off)
+    const float sx = s * x, bx = b * x;
+    return acc + __builtin_fmaf((float)q, sx, bx);
+}
+
+/* Router logit of one q4 row (the model's router, metal/kernels.metal:472-513)
+ * by one wavefront: lane L owns the words L, L+64, L+128, L+192 (columns
+ * 8 word .. +7) and their groups' raw bf16 scale and bias, and accumulates
+ * its columns in order with nmoe_router_q4_term; the lane partials are
+ * combined by the pairwise tree.  The multi-launch q4 router kernel uses the
+ * same order, so both paths give the same logits. */
 __device__ __forceinline__ float nmoe_router_row_q4(const uint32_t wq[4], const uint16_t s[4], const uint16_t b[4],
                                                     const float xs[32]) {
     float acc = 0.0f;
@@ -274,8 +284,7 @@ __device__ __forceinline__ float nmoe_router_row_q4(const uint32_t wq[4], const 
     for (int j = 0; j < 4; j++) {
         const float sf = nmoe_bf16f(s[j]), bf = nmoe_bf16f(b[j]);
 #pragma unroll
-        for (int i = 0; i < 8; i++)
-            acc = __builtin_fmaf(__builtin_fmaf((float)((wq[j] >> (4 * i)) & 0xFu), sf, bf), xs[8 * j + i], acc);
+        for (int i = 0; i < 8; i++) acc = nmoe_router_q4_term(acc, (wq[j] >> (4 * i)) & 0xFu, sf, bf, xs[8 * j + i]);
     }
     return nmoe_wave_sum_tree(acc);
 }
@@ -458,29 +467,10 @@ __device__ __forceinline__ bool nmoe_tag_is(uint64_t w, uint32_t epoch) { return
 __device__ __forceinline__ float nmoe_tag_val(uint64_t w) { return __uint_as_float((uint32_t)w); }
 
 /* Bounded spin so that a grid whose blocks are not all resident still ends:
- * the waiting block gives up, records the failure in the status word and
- * carries on (the result is then wrong, and the host reports ETIMEDOUT). */
+ * the waiting block gives up after this many unsuccessful poll rounds (the
+ * default; NMOE_HIP_OPT_SPIN_LIMIT changes it), records the failure in the
+ * status word and carries on (the host then reports ETIMEDOUT). */
 #define NMOE_SPIN_LIMIT (1u << 20)
-
-/* Barrier of the blocks sharing counter `cnt`: every block adds 1 and leaves
- * once the counter reaches `target` (wrap-around safe).  Stores issued before
- * the barrier with nmoe_st_dev are visible to nmoe_ld_dev after it. */
-__device__ __forceinline__ void nmoe_group_barrier(uint32_t *cnt, uint32_t target, uint32_t *status) {
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        nmoe_add_u32_dev(cnt, 1u);
-        uint32_t spins = 0;
-        while ((int32_t)(nmoe_ld_u32_dev(cnt) - target) < 0) {
-            __builtin_amdgcn_s_sleep(1);
-            if (++spins > NMOE_SPIN_LIMIT) {
-                __hip_atomic_store(status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                break;
-            }
-        }
-    }
-    __syncthreads();
-}
 
 /* ------------------------------------------------------------ RMSNorm */
 

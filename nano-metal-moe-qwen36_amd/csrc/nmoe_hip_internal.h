@@ -84,6 +84,8 @@ struct nmoe_hip_ctx {
     int use_fused;        /* NMOE_HIP_OPT_FUSED_DECODE */
     int xcd_placed;       /* blocks dealt round-robin over 8 dies (checked at create) */
     int use_xcd_local;    /* NMOE_HIP_OPT_XCD_LOCAL */
+    uint32_t spin_limit;  /* NMOE_HIP_OPT_SPIN_LIMIT: poll rounds before a bounded wait gives up */
+    int sync_check;       /* NMOE_HIP_OPT_SYNC_CHECK */
     /* grouped (matrix-core) path for many tokens, sized for max_tokens */
     int grouped_min_tokens; /* NMOE_HIP_OPT_GROUPED_MIN_TOKENS */
     uint32_t *g_counts;     /* [64][257] per-block expert histograms */
@@ -100,6 +102,10 @@ struct nmoe_hip_ctx {
 };
 
 int nmoe_fail(nmoe_hip_ctx *ctx, int code, const char *fmt, ...);
+/* With NMOE_HIP_OPT_SYNC_CHECK set: waits for `stream` and turns an expired
+ * bounded wait into NMOE_HIP_ETIMEDOUT (nmoe_hip_check_device_status);
+ * otherwise returns NMOE_HIP_OK at once. */
+extern "C" int nmoe_sync_check(nmoe_hip_ctx *ctx, void *stream);
 int nmoe_hip_check(nmoe_hip_ctx *ctx, hipError_t e, const char *what);
 
 #define NMOE_HIP_TRY(ctx, call)                                   \

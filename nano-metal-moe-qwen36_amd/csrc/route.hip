@@ -56,8 +56,9 @@ __global__ void __launch_bounds__(64) nmoe_router_bf16_kernel(const uint16_t *__
 }
 
 /* q4 router row (the reference model's router, kernels.metal:472-513):
- * 256 words; lane L owns words L, L+64, L+128, L+192, w = fma(q, s, b),
- * acc = fma(w, x, acc); lane partials combined by the pairwise tree. */
+ * 256 words; lane L owns words L, L+64, L+128, L+192 and accumulates
+ * acc + fma(q, s*x, b*x) per column (kernels.metal:500-508); lane partials
+ * combined by the pairwise tree. */
 template <typename XT>
 __global__ void __launch_bounds__(64) nmoe_router_q4_kernel(const uint32_t *__restrict__ w,
                                                             const uint16_t *__restrict__ sc,
@@ -85,10 +86,7 @@ __global__ void __launch_bounds__(64) nmoe_router_q4_kernel(const uint32_t *__re
             float xv[8];
             nmoe_load_cols<XT>(xt, (lane + 64 * j) * 8, 8, xv);
 #pragma unroll
-            for (int i = 0; i < 8; i++) {
-                float q = (float)((wv[j] >> (4 * i)) & 0xFu);
-                acc = __builtin_fmaf(__builtin_fmaf(q, s[j], b[j]), xv[i], acc);
-            }
+            for (int i = 0; i < 8; i++) acc = nmoe_router_q4_term(acc, (wv[j] >> (4 * i)) & 0xFu, s[j], b[j], xv[i]);
         }
         acc = nmoe_wave_sum_tree(acc);
         if (lane == 0) logits[(size_t)t * num_experts + e] = acc;

@@ -14,8 +14,9 @@
 
 /* Wavefront w of block b reduces row 4b + w of gate and of up (rows
  * 0..511); block 128 wavefront 0 reduces the score row.  Lane L owns the
- * words L, L+64, L+128, L+192 of a 256-word row (columns 8 word .. +7), with
- * w = fma(q, s, b), acc = fma(w, x, acc), lanes combined by the pairwise
+ * words L, L+64, L+128, L+192 of a 256-word row (columns 8 word .. +7) and
+ * accumulates acc + fma(q, s*x, b*x) per column, the reference's form for
+ * these rows (kernels.metal:444-460, 500-508); lanes combined by the pairwise
  * tree.  The row's codes and scales stay in registers over the block's
  * tokens. */
 template <typename XT>
@@ -55,9 +56,8 @@ __global__ void __launch_bounds__(256) nmoe_shared_gateup_kernel(
             nmoe_load_cols<XT>(xt, (lane + 64 * j) * 8, 8, xv);
 #pragma unroll
             for (int i = 0; i < 8; i++) {
-                ga = __builtin_fmaf(__builtin_fmaf((float)((wa[j] >> (4 * i)) & 0xFu), sa[j], ba[j]), xv[i], ga);
-                if (!score)
-                    ua = __builtin_fmaf(__builtin_fmaf((float)((wb[j] >> (4 * i)) & 0xFu), sbv[j], bbv[j]), xv[i], ua);
+                ga = nmoe_router_q4_term(ga, (wa[j] >> (4 * i)) & 0xFu, sa[j], ba[j], xv[i]);
+                if (!score) ua = nmoe_router_q4_term(ua, (wb[j] >> (4 * i)) & 0xFu, sbv[j], bbv[j], xv[i]);
             }
         }
         ga = nmoe_wave_sum_tree(ga);
@@ -71,7 +71,9 @@ __global__ void __launch_bounds__(256) nmoe_shared_gateup_kernel(
 }
 
 /* Wavefront w of block b reduces row 4b + w (of 2048) of the shared down
- * against act: lane L owns word L of the 64-word row (columns 8L..8L+7). */
+ * against act: lane L owns word L of the 64-word row (columns 8L..8L+7) and
+ * accumulates fma(q, s, b) * x per column, the reference's form for this
+ * matrix (kernels.metal:1533), as one fma. */
 __global__ void __launch_bounds__(256) nmoe_shared_down_kernel(const uint32_t *__restrict__ dw,
                                                                const uint16_t *__restrict__ ds,
                                                                const uint16_t *__restrict__ db,

@@ -12,6 +12,9 @@
 #include "nmoe_hip.h"
 
 int nmoe_host_fail(nmoe_hip_ctx *ctx, int code, const char *msg);
+int nmoe_layer_rmsnorm_launch(nmoe_hip_ctx *ctx, int layer, const nmoe_hip_router *router, const float *h_in,
+                              float eps, int k, float *h_out, uint32_t *idx, float *w, float *logits, void *stream);
+int nmoe_sync_check(nmoe_hip_ctx *ctx, void *stream);
 
 int nmoe_moe_stack(nmoe_hip_ctx *ctx, int nlayers, const int *layers, const nmoe_hip_router *routers, int k,
                    float eps, float *h_seq, uint32_t *idx_seq, float *w_seq, void *stream) {
@@ -19,11 +22,11 @@ int nmoe_moe_stack(nmoe_hip_ctx *ctx, int nlayers, const int *layers, const nmoe
     if (nlayers < 1 || layers == NULL || routers == NULL || h_seq == NULL)
         return nmoe_host_fail(ctx, NMOE_HIP_EINVAL, "nlayers >= 1, layers, routers and h_seq are required");
     for (int l = 0; l < nlayers; l++) {
-        int rc = nmoe_moe_layer_rmsnorm(ctx, layers[l], &routers[l], h_seq + (size_t)l * NMOE_HIP_HIDDEN, eps, k,
-                                        h_seq + (size_t)(l + 1) * NMOE_HIP_HIDDEN,
-                                        idx_seq != NULL ? idx_seq + (size_t)l * NMOE_HIP_MAX_K : NULL,
-                                        w_seq != NULL ? w_seq + (size_t)l * NMOE_HIP_MAX_K : NULL, NULL, stream);
+        int rc = nmoe_layer_rmsnorm_launch(ctx, layers[l], &routers[l], h_seq + (size_t)l * NMOE_HIP_HIDDEN, eps, k,
+                                           h_seq + (size_t)(l + 1) * NMOE_HIP_HIDDEN,
+                                           idx_seq != NULL ? idx_seq + (size_t)l * NMOE_HIP_MAX_K : NULL,
+                                           w_seq != NULL ? w_seq + (size_t)l * NMOE_HIP_MAX_K : NULL, NULL, stream);
         if (rc != NMOE_HIP_OK) return rc;
     }
-    return NMOE_HIP_OK;
+    return nmoe_sync_check(ctx, stream);
 }

@@ -43,6 +43,9 @@ ETIMEDOUT = -110
 OPT_FUSED_DECODE = 1
 OPT_XCD_LOCAL = 2
 OPT_GROUPED_MIN_TOKENS = 3
+OPT_SPIN_LIMIT = 4
+OPT_SYNC_CHECK = 5
+OPT_SKEW_EPOCH = 6
 
 # q4 / q2 component offsets (scripts/convert_qwen36.py:38-64)
 OFFSETS = {
@@ -218,6 +221,9 @@ class Context:
 
     def sync(self):
         self._check(lib().nmoe_hip_synchronize(self.h))
+
+    def set_option(self, option: int, value: int) -> int:
+        return lib().nmoe_hip_set_option(self.h, option, int(value))
 
     def set_fused(self, on: bool):
         self._check(lib().nmoe_hip_set_option(self.h, OPT_FUSED_DECODE, int(bool(on))))

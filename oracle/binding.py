@@ -30,6 +30,7 @@ _ORACLE_SIGS = {
     "orc_bf16_to_f32": (_F, [C.c_uint16]),
     "orc_f32_to_bf16": (C.c_uint16, [_F]),
     "orc_bf16_to_f32_array": (None, [_P, _P, _SZ]),
+    "orc_f32_to_bf16_bits": (None, [_P, _P, _SZ]),
     "orc_sigmoid": (_F, [_F]),
     "orc_silu": (_F, [_F]),
     "orc_rms_norm": (None, [_P, _P, _P, _SZ, _F, _I]),
@@ -54,6 +55,7 @@ _ORACLE_SIGS = {
     "orc_moe_experts": (_I, [_P, _I, _P, _I, _I, _P, _P, _P, _P, _P, _P, _P]),
     "orc_dispatch": (None, [_P, _I, _I, _I, _I, _P, _P]),
     "orc_moe_layer_rmsnorm": (_I, [_P, _I, _P, _P, _F, _I, _P, _P, _P, _P]),
+    "orc_moe_block": (_I, [_P, _I, _I, _P, _P, _P, _P, _P, _P, _I, _P, _F, _I, _P, _P, _P, _P, _P, _P]),
     "orc_syn_mix64": (_U64, [_U64]),
     "orc_syn_stream": (_U64, [_U64, _U32, _U32, _U32]),
     "orc_syn_rand64": (_U64, [_U64, _U64]),
@@ -78,6 +80,7 @@ _REF_MATH_SIGS = {
     "nmoe_cpu_unpack_row": (None, [_P, _P, _SZ, _I]),
     "nmoe_cpu_dequant_row": (None, [_P, _P, _P, _P, _SZ, _I]),
     "nmoe_cpu_dequant_matvec": (None, [_P, _P, _P, _P, _P, _SZ, _SZ, _I]),
+    "orc_ref_f32_to_bf16_bits": (None, [_P, _P, _SZ]),
 }
 
 _REF_STEP_SIGS = {
@@ -205,6 +208,37 @@ def shared_expert(se: dict, x: np.ndarray):
     for t in range(x.shape[0]):
         oracle().orc_shared_expert(*args, x[t].ctypes.data, out[t].ctypes.data, g[t:].ctypes.data)
     return out, g
+
+
+def moe_block(pack: np.ndarray, bits: int, router: dict, h_mid: np.ndarray, k: int, eps: float = 1e-6,
+              post_norm=None, add_one: int = 1, shared: dict | None = None, next_norm=None, want_next=False):
+    """orc_moe_block for one token.  router: {"w": bf16 [256][2048]} or
+    {"q4": (w u32 [256][256], scales, biases)}; shared: syn_shared_expert's
+    dict or None.  Returns (out, idx8, w8, x, next_x or None)."""
+    h = np.ascontiguousarray(h_mid, np.float32)
+    out, x = np.zeros(HIDDEN, np.float32), np.zeros(HIDDEN, np.float32)
+    nx = np.zeros(HIDDEN, np.float32) if want_next else None
+    idx, w = np.zeros(MAX_K, np.uint32), np.zeros(MAX_K, np.float32)
+    keep = []
+    if "q4" in router:
+        kind, rb = 1, None
+        rq = [np.ascontiguousarray(a) for a in router["q4"]]
+        keep += rq
+        rqp = [a.ctypes.data for a in rq]
+    else:
+        kind, rb = 0, np.ascontiguousarray(router["w"])
+        keep.append(rb)
+        rqp = [None, None, None]
+    sh = None
+    if shared is not None:
+        arrs = [np.ascontiguousarray(a) for n in ("gate", "up", "down", "score") for a in shared[n]]
+        keep += arrs
+        sh = (C.c_void_p * 12)(*[a.ctypes.data for a in arrs])
+    rc = oracle().orc_moe_block(pack.ctypes.data, bits, kind, p(rb), rqp[0], rqp[1], rqp[2], sh, p(post_norm),
+                                add_one, h.ctypes.data, eps, k, out.ctypes.data, p(next_norm), p(nx),
+                                idx.ctypes.data, w.ctypes.data, x.ctypes.data)
+    assert rc == 0
+    return out, idx, w, x, nx
 
 
 def dispatch(idx: np.ndarray, ntok: int, k: int, stride: int, num_experts: int = EXPERTS):

@@ -29,6 +29,15 @@ uint16_t orc_f32_to_bf16(float v) {
     return (uint16_t)(r >> 16);
 }
 
+/* orc_f32_to_bf16 over raw bit patterns (every NaN payload reaches it as is). */
+void orc_f32_to_bf16_bits(const uint32_t *in, uint16_t *out, size_t n) {
+    for (size_t i = 0; i < n; i++) {
+        float f;
+        memcpy(&f, &in[i], sizeof(f));
+        out[i] = orc_f32_to_bf16(f);
+    }
+}
+
 void orc_bf16_to_f32_array(const uint16_t *in, float *out, size_t n) {
     for (size_t i = 0; i < n; i++) out[i] = orc_bf16_to_f32(in[i]);
 }
@@ -287,6 +296,11 @@ void orc_router_logits_bf16(const uint16_t *w, const float *x, int num_experts, 
     }
 }
 
+/* The reference model's q4 router, metal/kernels.metal:472-513: per column
+ * acc += fma(q, scale * x, bias * x) (kernels.metal:500-508: both products
+ * rounded, then the fma, then the add), the words of a row lane-strided; the
+ * reference's simd_sum order is the closed Metal compiler's, so the lanes
+ * here are the GPU kernel's 64 and their partials meet in its tree. */
 void orc_router_logits_q4(const uint32_t *w, const uint16_t *scales, const uint16_t *biases, const float *x,
                           int num_experts, int hidden, float *out) {
     int words = hidden / 8;
@@ -302,7 +316,8 @@ void orc_router_logits_q4(const uint32_t *w, const uint16_t *scales, const uint1
                 float b = orc_bf16_to_f32(biases[(size_t)e * groups + g]);
                 for (int j = 0; j < 8; j++) {
                     float q = (float)((row[c] >> (4 * j)) & 0xFu);
-                    acc = fmaf(fmaf(q, s, b), x[c * 8 + j], acc);
+                    float sx = s * x[c * 8 + j], bx = b * x[c * 8 + j];
+                    acc = acc + fmaf(q, sx, bx);
                 }
             }
             p[l] = acc;
@@ -342,18 +357,19 @@ void orc_expert_down(const uint8_t *expert, int bits, const float *act512, float
 }
 
 /* The shared expert of one token: metal/kernels.metal:421-469 (rows 0-511:
- * SiLU(gate.x) * (up.x)), 510-513 (row 768: the gate score) and 1520-1537
- * (the shared down), each matvec in math.m:236-274 form (q4). */
+ * SiLU(gate.x) * (up.x)) and 510-513 (row 768: the gate score), whose rows
+ * use the router's per-element form (orc_router_logits_q4), and 1520-1537
+ * (the shared down) as a math.m:236-274 dequant matvec (q4). */
 void orc_shared_expert(const uint32_t *gw, const uint16_t *gs, const uint16_t *gb, const uint32_t *uw,
                        const uint16_t *us, const uint16_t *ub, const uint32_t *dw, const uint16_t *ds,
                        const uint16_t *db, const uint32_t *sw, const uint16_t *ss, const uint16_t *sb, const float *x,
                        float *shared_out, float *shared_gate_raw) {
     float gate[ORC_INTER], up[ORC_INTER], act[ORC_INTER];
-    orc_dequant_matvec(gw, gs, gb, x, gate, ORC_INTER, ORC_HIDDEN, 4);
-    orc_dequant_matvec(uw, us, ub, x, up, ORC_INTER, ORC_HIDDEN, 4);
+    orc_router_logits_q4(gw, gs, gb, x, ORC_INTER, ORC_HIDDEN, gate);
+    orc_router_logits_q4(uw, us, ub, x, ORC_INTER, ORC_HIDDEN, up);
     orc_swiglu(gate, up, act, ORC_INTER);
     orc_dequant_matvec(dw, ds, db, act, shared_out, ORC_HIDDEN, ORC_INTER, 4);
-    orc_dequant_matvec(sw, ss, sb, x, shared_gate_raw, 1, ORC_HIDDEN, 4);
+    orc_router_logits_q4(sw, ss, sb, x, 1, ORC_HIDDEN, shared_gate_raw);
 }
 
 /* kernels.metal:1394-1423 (and the fused tail at 1539-1541). */
@@ -420,6 +436,42 @@ int orc_moe_layer_rmsnorm(const uint8_t *layer_pack, int bits, const uint16_t *r
     if (idx8 != NULL) memcpy(idx8, idx, sizeof(idx));
     if (w8 != NULL) memcpy(w8, w, sizeof(w));
     return orc_moe_experts(layer_pack, bits, x, 1, k, idx, w, h_in, NULL, NULL, h_out, NULL);
+}
+
+/* One token through one layer's MoE block, in the reference's order
+ * (src/runtime.m:3144-3201 then NMOEPipelinedExpertTail :2908-2999):
+ *   x      = RMSNorm(h_mid, post_norm, add_one)      (runtime.m:3148-3150, math.m:34-65)
+ *   logits = router . x  (bf16 router, or the model's q4 router kernels.metal:472-513)
+ *   route  = softmax -> top-k -> renormalise         (runtime.m:1498-1511)
+ *   shared = Wsd . (SiLU(Wsg x) * (Wsu x)), g = Wss . x  (kernels.metal:421-469, 510-513, 1520-1537)
+ *   out    = h_mid + sum_s w_s y_s + sigmoid(g) shared   (kernels.metal:1539-1541)
+ *   next_x = RMSNorm(out, next_norm, add_one)        (runtime.m:2893-2900)
+ * post_norm NULL: unit weight; shared (nullable): 12 pointers gate w/s/b,
+ * up w/s/b, down w/s/b, score w/s/b; next_norm / next_x nullable (no next
+ * norm when next_x is NULL).  idx8/w8/x_out nullable. */
+int orc_moe_block(const uint8_t *layer_pack, int bits, int router_kind, const uint16_t *router_bf16,
+                  const uint32_t *rq_w, const uint16_t *rq_s, const uint16_t *rq_b, const void *const *shared,
+                  const uint16_t *post_norm, int add_one, const float *h_mid, float eps, int k, float *out,
+                  const uint16_t *next_norm, float *next_x, uint32_t *idx8, float *w8, float *x_out) {
+    float x[ORC_HIDDEN], lg[ORC_EXPERTS], so[ORC_HIDDEN], g = 0.0f;
+    uint32_t idx[ORC_MAX_K];
+    float w[ORC_MAX_K];
+    orc_rms_norm(h_mid, post_norm, x, ORC_HIDDEN, eps, post_norm != NULL ? add_one : 0);
+    if (x_out != NULL) memcpy(x_out, x, sizeof(x));
+    if (router_kind == 0)
+        orc_router_logits_bf16(router_bf16, x, ORC_EXPERTS, ORC_HIDDEN, lg);
+    else
+        orc_router_logits_q4(rq_w, rq_s, rq_b, x, ORC_EXPERTS, ORC_HIDDEN, lg);
+    if (orc_route(lg, ORC_EXPERTS, k, idx, w, NULL) < 0) return -1;
+    if (idx8 != NULL) memcpy(idx8, idx, sizeof(idx));
+    if (w8 != NULL) memcpy(w8, w, sizeof(w));
+    if (shared != NULL)
+        orc_shared_expert(shared[0], shared[1], shared[2], shared[3], shared[4], shared[5], shared[6], shared[7],
+                          shared[8], shared[9], shared[10], shared[11], x, so, &g);
+    int rc = orc_moe_experts(layer_pack, bits, x, 1, k, idx, w, h_mid, shared != NULL ? so : NULL,
+                             shared != NULL ? &g : NULL, out, NULL);
+    if (rc == 0 && next_x != NULL) orc_rms_norm(out, next_norm, next_x, ORC_HIDDEN, eps, next_norm != NULL ? add_one : 0);
+    return rc;
 }
 
 /* ------------------------------------------------------------ dispatch */

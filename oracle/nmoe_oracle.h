@@ -40,6 +40,7 @@ extern "C" {
 float orc_bf16_to_f32(uint16_t v);
 uint16_t orc_f32_to_bf16(float v);
 void orc_bf16_to_f32_array(const uint16_t *in, float *out, size_t n);
+void orc_f32_to_bf16_bits(const uint32_t *in, uint16_t *out, size_t n);
 
 /* math.m:21-32 */
 float orc_sigmoid(float x);
@@ -113,6 +114,16 @@ int orc_moe_step_bf16router(const uint8_t *layer_pack, int bits, const uint16_t 
  * weight): x = RMSNorm(h_in); h_out = h_in + MoE(x).  idx/w/x_out nullable. */
 int orc_moe_layer_rmsnorm(const uint8_t *layer_pack, int bits, const uint16_t *router_w, const float *h_in, float eps,
                           int k, float *h_out, uint32_t *idx8, float *w8, float *x_out);
+
+/* One token through one layer's MoE block in the reference's order
+ * (runtime.m:3144-3201, 2908-2999): post-attention RMSNorm (weighted or
+ * unit), router (kind 0 bf16, 1 q4), routing, optional shared expert (12
+ * pointers: gate w/s/b, up w/s/b, down w/s/b, score w/s/b), experts,
+ * combine, optional next-layer input RMSNorm.  See nmoe_oracle.c. */
+int orc_moe_block(const uint8_t *layer_pack, int bits, int router_kind, const uint16_t *router_bf16,
+                  const uint32_t *rq_w, const uint16_t *rq_s, const uint16_t *rq_b, const void *const *shared,
+                  const uint16_t *post_norm, int add_one, const float *h_mid, float eps, int k, float *out,
+                  const uint16_t *next_norm, float *next_x, uint32_t *idx8, float *w8, float *x_out);
 
 /* Experts only (routing given): idx/w [ntok][8]. */
 int orc_moe_experts(const uint8_t *layer_pack, int bits, const float *x, int ntok, int k, const uint32_t *idx,

@@ -178,6 +178,23 @@ def main():
         o.orc_combine(h_mid.ctypes.data, ys.ctypes.data, w8.ctypes.data, got, None, None, res.ctypes.data, B.HIDDEN)
         out.update({f"{name}_logits": logits, f"{name}_idx": idx8, f"{name}_w": w8, f"{name}_out": res})
 
+    # ---- fp32 -> bf16 (math.m:14-19) on raw bit patterns: rounding ties both
+    # ways, carries into the exponent, subnormals, the largest finite values
+    # (which round to Inf), infinities and NaN payloads (which the reference's
+    # carry can turn into Inf or wrap to zero), then uniform random patterns
+    # (their own generator, so the arrays above keep their values).
+    crafted = [0x00000000, 0x80000000, 0x3F800000, 0x3F808000, 0x3F818000, 0x3F808001, 0x3F807FFF, 0x3F818001,
+               0x3FFF8000, 0x3FFFFFFF, 0x00000001, 0x00008000, 0x00018000, 0x00017FFF, 0x007FFFFF, 0x00800000,
+               0x80008000, 0x80018000, 0x7F7F7FFF, 0x7F7F8000, 0x7F7FFFFF, 0xFF7F8000, 0x7F800000, 0xFF800000,
+               0x7FC00000, 0x7F800001, 0x7F808000, 0x7FBFFFFF, 0x7FFF8000, 0x7FFFFFFF, 0xFFC00000, 0xFFFF8000,
+               0xFFFFFFFF, 0x40490FDB, 0xC2F6E979, 0x33D6BF95]
+    rb = np.random.default_rng(20261202)
+    bits_in = np.concatenate([np.array(crafted, np.uint32),
+                              rb.integers(0, 2**32, size=4096, dtype=np.uint64).astype(np.uint32)])
+    bf_out = np.zeros(bits_in.size, np.uint16)
+    ref.orc_ref_f32_to_bf16_bits(bits_in.ctypes.data, bf_out.ctypes.data, bits_in.size)
+    out.update(f2bf_in=bits_in, f2bf_out=bf_out)
+
     np.savez_compressed(OUT, **out)
     print(f"wrote {OUT}: {len(out)} arrays, {os.path.getsize(OUT)} bytes")
 

@@ -621,7 +621,7 @@ def test_grouped_experts_against_oracle(big, nh, bits, ntok, k, xkind, ikind):
 @pytest.mark.parametrize("bits", [4, 2])
 def test_prefill_2048_sampled(big, nh, bits):
     """C5 shape: 2048 tokens, uniform-random logits -> device top-8 ->
-    grouped experts; routing bit-exact for every token, outputs checked
+    grouped experts; routing bit-exact for all 2048 tokens, outputs checked
     against the oracle on a sample of 48 tokens."""
     rng = np.random.default_rng(2048 + bits)
     seed, layer, ntok, k = 33, 50 + bits, 2048, 8
@@ -637,10 +637,10 @@ def test_prefill_2048_sampled(big, nh, bits):
     idx = d_idx.download(np.uint32, (ntok, 8))
     w = d_w.download(np.float32, (ntok, 8))
     sample = rng.choice(ntok, 48, replace=False)
-    for t in sample[:8]:
+    for t in range(ntok):  # every token's routing
         oi, ow, _ = B.route(logits[t], k)
-        np.testing.assert_array_equal(idx[t], oi)
-        np.testing.assert_array_equal(w[t].view(np.uint32), ow.view(np.uint32))
+        np.testing.assert_array_equal(idx[t], oi, err_msg=f"t={t}")
+        np.testing.assert_array_equal(w[t].view(np.uint32), ow.view(np.uint32), err_msg=f"t={t}")
     got = out.download(np.float32, (ntok, 2048))[sample]
     pack = host_pack(bits, seed, layer, idx[sample, :k].ravel())
     want = B.moe_experts(pack, bits, x[sample], k, idx[sample], w[sample], h[sample])
@@ -787,3 +787,75 @@ def test_fused_layer_with_q4_router(ctx, nh, bits):
         np.testing.assert_array_equal(w.download(np.float32, 8).view(np.uint32), ow.view(np.uint32))
         assert_close(out.download(np.float32, 2048), want, what=f"q4 router fused={fused}")
     ctx.set_fused(True)
+
+
+def test_router_q4_scaled_one_hot_on_device(ctx, nh):
+    """The q4 router kernel on x = v e_j: each logit is the reference's
+    per-element form fma(q, fl(s v), fl(b v)) rounded once
+    (kernels.metal:500-508), computed here from the closed form, not from
+    the oracle; scales and biases independent, so a swapped pair, a wrong
+    group or a wrong nibble fails."""
+    rng = np.random.default_rng(55)
+    wq = rng.integers(0, 2**32, size=(256, 256), dtype=np.uint64).astype(np.uint32)
+    sq = B.f32_to_bf16((rng.standard_normal((256, 32)) * 0.02).astype(np.float32))
+    bq = B.f32_to_bf16((rng.standard_normal((256, 32)) * 0.05).astype(np.float32))
+    q = ((wq[:, :, None] >> (np.arange(8, dtype=np.uint32) * 4)) & 15).reshape(256, 2048)
+    rq = ctx.router_q4(ctx.to_device(wq), ctx.to_device(sq), ctx.to_device(bq))
+    cols = [0, 9, 63, 64, 777, 1546, 2047]
+    vals = [np.float32(1.37), np.float32(-0.7133), np.float32(123.456)]
+    X = np.zeros((len(cols) * len(vals), 2048), np.float32)
+    want = np.zeros((X.shape[0], 256), np.float32)
+    s32, b32 = B.bf16_to_f32(sq), B.bf16_to_f32(bq)
+    for i, (j, v) in enumerate((j, v) for j in cols for v in vals):
+        X[i, j] = v
+        sv, bv = s32[:, j // 64] * v, b32[:, j // 64] * v
+        want[i] = (q[:, j].astype(np.float64) * sv.astype(np.float64) + bv.astype(np.float64)).astype(np.float32)
+    ntok = X.shape[0]
+    lg = ctx.alloc(ntok * 1024)
+    ctx._check(ctx.router_logits(rq, ctx.to_device(X), nh.F32, ntok, lg))
+    got = lg.download(np.float32, (ntok, 256))
+    np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("bits", [4, 2])
+def test_fused_q4_router_with_rmsnorm(ctx, nh, bits):
+    """nmoe_moe_layer_rmsnorm with the model's q4 router: the fused
+    <q4 router, in-kernel RMSNorm> variant maps the normalised x onto its
+    router columns correctly -- routing bit-exact and output within
+    tolerance against the oracle's whole block (orc_moe_block); then a
+    two-layer stack of such layers, teacher-forced."""
+    rng = np.random.default_rng(70 + bits)
+    seed, k = 43, 8
+    layers = [34 + 2 * (bits == 2), 35 + 2 * (bits == 2)]
+    for layer in layers:
+        ctx.synth_layer(layer, bits, seed, SIGMA[bits])
+    R = []
+    for _ in layers:
+        wq = rng.integers(0, 2**32, size=(256, 256), dtype=np.uint64).astype(np.uint32)
+        sq = B.f32_to_bf16((rng.standard_normal((256, 32)) * 0.01).astype(np.float32))
+        bq = B.f32_to_bf16((rng.standard_normal((256, 32)) * 0.02).astype(np.float32))
+        R.append((wq, sq, bq))
+    dR = [ctx.router_q4(ctx.to_device(a), ctx.to_device(b_), ctx.to_device(c)) for a, b_, c in R]
+    h0 = rng.standard_normal(2048).astype(np.float32) * np.float32(3.0)
+    dh, dout = ctx.to_device(h0), ctx.alloc(8192)
+    idx, w = ctx.alloc(32), ctx.alloc(32)
+    ctx._check(ctx.moe_layer_rmsnorm(layers[0], dR[0], dh, 1e-6, k, dout, idx, w))
+    assert ctx.device_status() == nh.OK
+    full = B.syn_layer(bits, seed, layers[0], SIGMA[bits])
+    want, oi, ow, _, _ = B.moe_block(full, bits, {"q4": R[0]}, h0, k)
+    np.testing.assert_array_equal(idx.download(np.uint32, 8), oi)
+    np.testing.assert_array_equal(w.download(np.float32, 8).view(np.uint32), ow.view(np.uint32))
+    assert_close(dout.download(np.float32, 2048), want, what=f"q{bits} q4-router rmsnorm layer")
+    hs = ctx.alloc(3 * 8192)
+    hs.upload(h0)
+    idx_s, w_s = ctx.alloc(64), ctx.alloc(64)
+    ctx._check(ctx.moe_stack(layers, dR, k, 1e-6, hs, idx_s, w_s))
+    assert ctx.device_status() == nh.OK
+    H = hs.download(np.float32, (3, 2048))
+    I, Wt = idx_s.download(np.uint32, (2, 8)), w_s.download(np.float32, (2, 8))
+    for l in range(2):
+        pack = full if l == 0 else B.syn_layer(bits, seed, layers[1], SIGMA[bits])
+        want, oi, ow, _, _ = B.moe_block(pack, bits, {"q4": R[l]}, H[l], k)
+        np.testing.assert_array_equal(I[l], oi, err_msg=f"layer {l}")
+        np.testing.assert_array_equal(Wt[l].view(np.uint32), ow.view(np.uint32), err_msg=f"layer {l}")
+        assert_close(H[l + 1], want, what=f"q{bits} q4-router stack layer {l}")

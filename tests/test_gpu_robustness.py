@@ -1,0 +1,118 @@
+"""The failure path of the persistent kernels, forced from the host.
+
+A fused decode launch needs all 256 of its blocks resident at once; when
+one is not, the others' bounded waits give up.  The host forces exactly
+that outcome without starving the device: NMOE_HIP_OPT_SKEW_EPOCH moves one
+block's launch epoch ahead, so no other block ever sees its words (and it
+sees none of theirs), and NMOE_HIP_OPT_SPIN_LIMIT shortens every wait to a
+few thousand polls.  Every kernel still runs to its end; the test checks
+that the launch reports ETIMEDOUT, that everything it wrote is NaN (no
+result from words that never arrived passes for a valid one), and that the
+next launch after nmoe_hip_check_device_status is correct again (the
+reference's rule that every error path still signals its waiters,
+src/runtime.m:2944-2959)."""
+import numpy as np
+import pytest
+
+from conftest import assert_close
+from oracle import binding as B
+
+pytestmark = pytest.mark.gpu
+
+SPIN = 4096  # poll rounds: a few ms per wait instead of about a second
+
+
+@pytest.fixture(scope="module")
+def nh():
+    import nmoe_hip
+    return nmoe_hip
+
+
+def _layer_setup(ctx, nh, bits=4, seed=5, layer=3):
+    ctx.synth_layer(layer, bits, seed, 0.02)
+    W = B.syn_bf16(256 * 2048, seed, layer, 16, 0.02).reshape(256, 2048)
+    x = B.bf16_to_f32(B.syn_bf16(2048, seed, layer, 17, 1.0))
+    rng = np.random.default_rng(seed)
+    h = rng.standard_normal(2048).astype(np.float32)
+    idx, w, _ = B.route(B.router_logits_bf16(W, x), 8)
+    pack = np.zeros(256 * B.EXPERT_SIZE[bits], np.uint8)
+    esz = B.EXPERT_SIZE[bits]
+    for e in idx:
+        pack[int(e) * esz:(int(e) + 1) * esz] = B.syn_expert(bits, seed, layer, int(e), 0.02)
+    want = B.moe_experts(pack, bits, x[None], 8, idx[None], w[None], h[None])[0]
+    return dict(W=ctx.to_device(W), x=ctx.to_device(x), h=ctx.to_device(h), idx=idx, w=w, want=want, layer=layer)
+
+
+def _run(ctx, nh, s, out, di, dw):
+    return ctx.moe_layer(s["layer"], ctx.router_bf16(s["W"]), s["x"], nh.F32, 1, 8, s["h"], out, di, dw)
+
+
+def test_expired_wait_poisons_output_and_recovers(nh):
+    with nh.Context(0, max_tokens=4) as ctx:
+        s = _layer_setup(ctx, nh)
+        out, di, dw = ctx.alloc(2048 * 4), ctx.alloc(32), ctx.alloc(32)
+        ctx._check(ctx.set_option(nh.OPT_SPIN_LIMIT, SPIN))
+        # a clean launch first
+        ctx._check(_run(ctx, nh, s, out, di, dw))
+        assert ctx.device_status() == nh.OK
+        good = out.download(np.float32, 2048)
+        assert_close(good, s["want"], what="before")
+        for block in (0, 37, 255):
+            print(f"[robust] skewed block {block}", flush=True)
+            ctx._check(ctx.set_option(nh.OPT_SKEW_EPOCH, block))
+            assert _run(ctx, nh, s, out, di, dw) == nh.OK  # asynchronous: the failure shows at the check
+            got = out.download(np.float32, 2048)
+            assert np.isnan(got).all(), f"block {block}: {np.count_nonzero(~np.isnan(got))} rows not poisoned"
+            assert np.isnan(dw.download(np.float32, 8)).all()
+            assert ctx.device_status() == nh.ETIMEDOUT
+            assert ctx.device_status() == nh.OK  # the check cleared and realigned
+            ctx._check(_run(ctx, nh, s, out, di, dw))
+            assert ctx.device_status() == nh.OK
+            again = out.download(np.float32, 2048)
+            np.testing.assert_array_equal(again.view(np.uint32), good.view(np.uint32))
+            np.testing.assert_array_equal(di.download(np.uint32, 8), s["idx"])
+        ctx._check(ctx.set_option(nh.OPT_SPIN_LIMIT, 0))
+
+
+def test_sync_check_returns_etimedout(nh):
+    """With NMOE_HIP_OPT_SYNC_CHECK the layer call itself reports the
+    expired wait, and the stack reports it once, after its last layer; the
+    stack's poisoned layers feed NaN forward (no layer after the failure
+    produces numbers)."""
+    with nh.Context(0, max_tokens=4) as ctx:
+        s = _layer_setup(ctx, nh)
+        out, di, dw = ctx.alloc(2048 * 4), ctx.alloc(32), ctx.alloc(32)
+        ctx._check(ctx.set_option(nh.OPT_SPIN_LIMIT, SPIN))
+        ctx._check(ctx.set_option(nh.OPT_SYNC_CHECK, 1))
+        ctx._check(_run(ctx, nh, s, out, di, dw))
+        ctx._check(ctx.set_option(nh.OPT_SKEW_EPOCH, 100))
+        assert _run(ctx, nh, s, out, di, dw) == nh.ETIMEDOUT
+        assert np.isnan(out.download(np.float32, 2048)).all()
+        ctx._check(_run(ctx, nh, s, out, di, dw))  # realigned by the failed call's check
+        assert_close(out.download(np.float32, 2048), s["want"], what="after sync-check recovery")
+        # the stack: three layers over the same pack, failure from the first
+        nl = 3
+        rng = np.random.default_rng(9)
+        h0 = rng.standard_normal(2048).astype(np.float32)
+        h_seq = ctx.alloc((nl + 1) * 2048 * 4)
+        h_seq.upload(h0)
+        r = ctx.router_bf16(s["W"])
+        ctx._check(ctx.set_option(nh.OPT_SKEW_EPOCH, 200))
+        assert ctx.moe_stack([s["layer"]] * nl, [r] * nl, 8, 1e-6, h_seq) == nh.ETIMEDOUT
+        hs = h_seq.download(np.float32, (nl + 1, 2048))
+        np.testing.assert_array_equal(hs[0], h0)
+        assert np.isnan(hs[1:]).all()
+        ctx._check(ctx.moe_stack([s["layer"]] * nl, [r] * nl, 8, 1e-6, h_seq))
+        hs = h_seq.download(np.float32, (nl + 1, 2048))
+        assert np.isfinite(hs).all()
+        ctx._check(ctx.set_option(nh.OPT_SYNC_CHECK, 0))
+        ctx._check(ctx.set_option(nh.OPT_SPIN_LIMIT, 0))
+
+
+def test_option_arguments_validated(nh):
+    with nh.Context(0, max_tokens=4) as ctx:
+        assert ctx.set_option(nh.OPT_SPIN_LIMIT, -1) == nh.EINVAL
+        assert ctx.set_option(nh.OPT_SPIN_LIMIT, (1 << 26) + 1) == nh.EINVAL
+        assert ctx.set_option(nh.OPT_SKEW_EPOCH, 256) == nh.EINVAL
+        assert ctx.set_option(nh.OPT_SKEW_EPOCH, -1) == nh.EINVAL
+        assert ctx.set_option(99, 0) == nh.EINVAL

@@ -111,3 +111,17 @@ def test_oracle_against_live_ref_when_built():
         np.testing.assert_array_equal(op.view(np.uint32), v.view(np.uint32))
         np.testing.assert_array_equal(oi[:got], idx[:got].astype(np.uint32))
         np.testing.assert_array_equal(ow[:got].view(np.uint32), val[:got].view(np.uint32))
+
+
+def test_f32_to_bf16_matches_math_m_golden(golden):
+    """orc_f32_to_bf16 (math.m:14-19) on raw bit patterns against the compiled
+    reference: ties to even, carries into the exponent and the sign bit,
+    subnormals, the finite values that round to Inf, NaN payloads."""
+    bits_in, want = golden["f2bf_in"], golden["f2bf_out"]
+    got = np.zeros(bits_in.size, np.uint16)
+    B.oracle().orc_f32_to_bf16_bits(bits_in.ctypes.data, got.ctypes.data, bits_in.size)
+    np.testing.assert_array_equal(got, want)
+    # the vectorised copy the tests use to build bf16 data
+    np.testing.assert_array_equal(B.f32_to_bf16(bits_in.view(np.float32)), want)
+    # the crafted half covers both tie directions and the exponent carry
+    assert want[3] == 0x3F80 and want[4] == 0x3F82 and want[8] == 0x4000

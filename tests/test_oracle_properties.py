@@ -245,3 +245,69 @@ def test_pack_layout_closed_form():
         arr = (ctypes.c_size_t * 9)()
         B.oracle().orc_expert_offsets(bits, arr)
         assert list(arr) == list(offs[:9])
+
+
+def _q4_router_case(seed):
+    """A q4 router with scales and biases drawn independently (a swapped
+    scale/bias, a wrong group or nibble then shows), and its dense float64
+    dequantisation."""
+    rng = np.random.default_rng(seed)
+    wq = rng.integers(0, 2**32, size=(256, 256), dtype=np.uint64).astype(np.uint32)
+    sq = B.f32_to_bf16((rng.standard_normal((256, 32)) * 0.02).astype(np.float32))
+    bq = B.f32_to_bf16((rng.standard_normal((256, 32)) * 0.05).astype(np.float32))
+    q = ((wq[:, :, None] >> (np.arange(8, dtype=np.uint32) * 4)) & 15).reshape(256, 2048)
+    dense = q * np.repeat(B.bf16_to_f32(sq), 64, 1).astype(np.float64) + np.repeat(B.bf16_to_f32(bq), 64, 1)
+    return rng, wq, sq, bq, q, dense
+
+
+def _q4_logits(wq, sq, bq, x):
+    out = np.zeros(256, np.float32)
+    x = np.ascontiguousarray(x, np.float32)
+    B.oracle().orc_router_logits_q4(wq.ctypes.data, sq.ctypes.data, bq.ctypes.data, x.ctypes.data, 256, 2048,
+                                    out.ctypes.data)
+    return out
+
+
+def test_router_q4_against_float64_dot():
+    """orc_router_logits_q4 (kernels.metal:472-513) against a float64 dot of
+    the dequantised router: within a bound of 64 fp32 roundings of the
+    largest partial sum, far from a shifted row."""
+    rng, wq, sq, bq, q, dense = _q4_router_case(31)
+    for _ in range(3):
+        x = rng.standard_normal(2048).astype(np.float32)
+        got = _q4_logits(wq, sq, bq, x)
+        want = dense @ x.astype(np.float64)
+        bound = 64 * 2.0**-24 * np.abs(dense * x.astype(np.float64)).sum(1)
+        assert np.all(np.abs(got - want) <= bound)
+        assert np.abs(got - np.roll(want, 1)).max() > 1.0
+
+
+def test_router_q4_scaled_one_hot_closed_form():
+    """x = v e_j leaves one term: the logit of row e is exactly the
+    reference's per-element form fma(q, fl(s v), fl(b v)) rounded once
+    (kernels.metal:500-508), with q the nibble j % 8 of word j / 8 and s, b
+    the scale and bias of group j / 64.  The same value through the other
+    association, fl(fl(q s + b) v), differs on most rows, so the test tells
+    the two forms apart."""
+    from fractions import Fraction
+    _, wq, sq, bq, q, _ = _q4_router_case(32)
+    s32, b32 = B.bf16_to_f32(sq), B.bf16_to_f32(bq)
+    differs = 0
+    for j in (0, 7, 8, 63, 64, 1000, 1543, 2047):
+        for v in (np.float32(1.37), np.float32(-0.7133), np.float32(3.1e-3), np.float32(123.456)):
+            x = np.zeros(2048, np.float32)
+            x[j] = v
+            got = _q4_logits(wq, sq, bq, x)
+            g = j // 64
+            sv = s32[:, g] * v  # fp32 products, correctly rounded
+            bv = b32[:, g] * v
+            qj = q[:, j].astype(np.float64)
+            exact = qj * sv.astype(np.float64) + bv.astype(np.float64)
+            for e in (0, 77, 255):  # the sum is exact in double, so one rounding to fp32 is the fma
+                assert Fraction(float(exact[e])) == Fraction(int(q[e, j])) * Fraction(float(sv[e])) + \
+                    Fraction(float(bv[e]))
+            want = exact.astype(np.float32)
+            np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32), err_msg=f"j={j} v={v}")
+            other = ((q[:, j].astype(np.float32) * s32[:, g] + b32[:, g]) * v).astype(np.float32)
+            differs += int(np.count_nonzero(other.view(np.uint32) != want.view(np.uint32)))
+    assert differs > 100
