@@ -278,6 +278,28 @@ NMOE_HIP_API int nmoe_moe_layer_rmsnorm(nmoe_hip_ctx *ctx, int layer, const nmoe
 NMOE_HIP_API int nmoe_moe_stack(nmoe_hip_ctx *ctx, int nlayers, const int *layers, const nmoe_hip_router *routers,
                                 int k, float eps, float *h_seq, uint32_t *idx_seq, float *w_seq, void *stream);
 
+/* ---- the per-layer MoE call without allocation and without a context.
+ * No counterpart in the reference (its runtime allocates every buffer at
+ * start-up, runtime.m:1542-1584).  It is for callers that cannot allocate
+ * device memory: code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc.  Same computation as nmoe_moe_layer on
+ * the current device: layer_pack is a resident layer (256 experts of
+ * nmoe_hip_expert_size(bits) bytes, e.g. nmoe_hip_layer_pack's address),
+ * router a 256-expert router, and for ntok > 1 the per-token kernels run
+ * (never the grouped ones).  Calls no hipMalloc/hipFree and no allocating
+ * library routine: its scratch is a fixed device array of
+ * NMOE_HIP_STATIC_SCRATCH_BYTES per GPU, held until the process ends, so
+ * ntok is at most NMOE_HIP_STATIC_MAX_TOKENS (EINVAL beyond).  Calls share
+ * that array: calls that overlap on one GPU race.  idx/w (nullable) receive
+ * the routing.  A bounded wait that gives up shows as NaN in out and w
+ * (there is no context to hold a status). */
+#define NMOE_HIP_STATIC_MAX_TOKENS 16
+#define NMOE_HIP_STATIC_SCRATCH_BYTES 722944u
+NMOE_HIP_API int nmoe_moe_layer_static(const void *layer_pack, int bits, const nmoe_hip_router *router,
+                                       const void *x, int x_dtype, int ntok, int k, const float *h_mid,
+                                       const float *shared_out, const float *shared_gate_raw, float *out,
+                                       uint32_t *idx, float *w, void *stream);
+
 /* ---- bit-exact dequant probe (kernels.metal:1066-1106 nmoe_dequant_row_q4/q2,
  * math.m:206-234): out[r][c] = q*scale + bias for `rows` rows of `in_dim`. */
 NMOE_HIP_API int nmoe_dequant_rows(nmoe_hip_ctx *ctx, int bits, const uint32_t *packed, const uint16_t *scales,

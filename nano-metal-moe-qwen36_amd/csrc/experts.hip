@@ -209,24 +209,45 @@ extern "C" int nmoe_moe_dispatch(nmoe_hip_ctx *ctx, const uint32_t *idx, int nto
     return nmoe_grouped_dispatch(ctx, idx, ntok, k, perm, offsets, nmoe_stream_of(ctx, stream));
 }
 
+/* The per-token expert kernels (gate/up + SwiGLU into act [ntok][8][512],
+ * then down + combine), arguments already checked. */
 template <int BITS>
-static int nmoe_launch_experts(nmoe_hip_ctx *ctx, const uint8_t *pack, const void *x, int x_dtype, int ntok, int k,
-                               const uint32_t *idx, const float *w, const float *h_mid, const float *shared_out,
-                               const float *shared_gate_raw, float *out, hipStream_t s) {
+static hipError_t nmoe_launch_experts_act(const uint8_t *pack, const void *x, int x_dtype, int ntok, int k,
+                                          const uint32_t *idx, const float *w, const float *h_mid,
+                                          const float *shared_out, const float *shared_gate_raw, float *out,
+                                          float *act, hipStream_t s) {
     using Q = nmoe_q<BITS>;
     dim3 g1(NMOE_INTER / NMOE_GU_ROWS_PER_BLOCK, k, ntok);
     if (x_dtype == NMOE_HIP_BF16)
         hipLaunchKernelGGL((nmoe_gateup_kernel<BITS, uint16_t>), g1, dim3(256), 0, s, pack, (const uint16_t *)x, idx,
-                           ctx->act);
+                           act);
     else
-        hipLaunchKernelGGL((nmoe_gateup_kernel<BITS, float>), g1, dim3(256), 0, s, pack, (const float *)x, idx,
-                           ctx->act);
-    NMOE_HIP_TRY(ctx, hipGetLastError());
+        hipLaunchKernelGGL((nmoe_gateup_kernel<BITS, float>), g1, dim3(256), 0, s, pack, (const float *)x, idx, act);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
     constexpr int RPB = (NMOE_WAVE / Q::LPR_D) * NMOE_DC_WAVES;
     dim3 g2(NMOE_HIDDEN / RPB, ntok);
-    hipLaunchKernelGGL((nmoe_down_combine_kernel<BITS>), g2, dim3(256), 0, s, pack, k, idx, w, ctx->act, h_mid,
-                       shared_out, shared_gate_raw, out);
-    NMOE_HIP_TRY(ctx, hipGetLastError());
+    hipLaunchKernelGGL((nmoe_down_combine_kernel<BITS>), g2, dim3(256), 0, s, pack, k, idx, w, act, h_mid, shared_out,
+                       shared_gate_raw, out);
+    return hipGetLastError();
+}
+
+extern "C" hipError_t nmoe_experts_launch(int bits, const uint8_t *pack, const void *x, int x_dtype, int ntok, int k,
+                                         const uint32_t *idx, const float *w, const float *h_mid,
+                                         const float *shared_out, const float *shared_gate_raw, float *out,
+                                         float *act, hipStream_t s) {
+    return bits == 4 ? nmoe_launch_experts_act<4>(pack, x, x_dtype, ntok, k, idx, w, h_mid, shared_out,
+                                                   shared_gate_raw, out, act, s)
+                     : nmoe_launch_experts_act<2>(pack, x, x_dtype, ntok, k, idx, w, h_mid, shared_out,
+                                                   shared_gate_raw, out, act, s);
+}
+
+template <int BITS>
+static int nmoe_launch_experts(nmoe_hip_ctx *ctx, const uint8_t *pack, const void *x, int x_dtype, int ntok, int k,
+                               const uint32_t *idx, const float *w, const float *h_mid, const float *shared_out,
+                               const float *shared_gate_raw, float *out, hipStream_t s) {
+    NMOE_HIP_TRY(ctx, nmoe_launch_experts_act<BITS>(pack, x, x_dtype, ntok, k, idx, w, h_mid, shared_out,
+                                                    shared_gate_raw, out, ctx->act, s));
     return NMOE_HIP_OK;
 }
 

@@ -78,6 +78,7 @@ static __constant__ uint64_t nmoe_fused_exp2_tab[32] = NMOE_EXP2_TAB32;
 #define NMOE_XCH_ACT (NMOE_XCH_SP * NMOE_EXPERTS)
 #define NMOE_XCH_YPART (NMOE_XCH_ACT + NMOE_XCH_SP * NMOE_FUSED_GROUPS * NMOE_INTER)
 #define NMOE_XCH_WORDS (NMOE_XCH_YPART + NMOE_FUSED_GROUPS * NMOE_HIDDEN) /* tagged partials, polled by one block */
+static_assert(NMOE_XCH_WORDS * sizeof(uint64_t) == NMOE_FUSED_XCH_BYTES, "exchange size as the host allocates it");
 
 /* x sources: XF32 / XBF16 = activations given; XNORM = x is RMSNorm(h). */
 #define NMOE_XF32 0
@@ -840,34 +841,30 @@ __global__ void nmoe_xcc_probe_kernel(uint32_t *out) {
  * between launches).  The blocks of a group (b % 8 equal) then share a die
  * and its L2, which the die-local exchange relies on.  Checked over launches
  * with different rotations (a 1-block launch in between shifts c). */
-static int nmoe_check_xcd_placement(int *placed) {
-    uint32_t *d = NULL, h[NMOE_FUSED_BLOCKS];
+extern "C" int nmoe_probe_xcd_placement(uint32_t *d, int *placed) {
+    uint32_t h[NMOE_FUSED_BLOCKS];
     *placed = 0;
-    if (hipMalloc((void **)&d, sizeof(h)) != hipSuccess) return NMOE_HIP_ENOMEM;
     int ok = 1;
     for (int rep = 0; rep < 4 && ok; rep++) {
         hipLaunchKernelGGL(nmoe_xcc_probe_kernel, dim3(NMOE_FUSED_BLOCKS), dim3(NMOE_FUSED_THREADS), 0, 0, d);
-        if (hipGetLastError() != hipSuccess || hipMemcpy(h, d, sizeof(h), hipMemcpyDeviceToHost) != hipSuccess) {
-            (void)hipFree(d);
+        if (hipGetLastError() != hipSuccess || hipMemcpy(h, d, sizeof(h), hipMemcpyDeviceToHost) != hipSuccess)
             return NMOE_HIP_EHIP;
-        }
         const uint32_t c = h[0] % NMOE_FUSED_GROUPS;
         for (int b = 0; b < NMOE_FUSED_BLOCKS; b++) ok = ok && h[b] == (uint32_t)(b + c) % NMOE_FUSED_GROUPS;
         hipLaunchKernelGGL(nmoe_xcc_probe_kernel, dim3(1 + rep), dim3(64), 0, 0, d); /* shift the rotation */
     }
-    (void)hipFree(d);
+    if (hipDeviceSynchronize() != hipSuccess) return NMOE_HIP_EHIP;
     *placed = ok;
     return NMOE_HIP_OK;
 }
 
 /* The fused path needs all 256 blocks resident at once (its blocks wait for
- * each other's exchange words); decided here from the occupancy of every
- * variant. */
-extern "C" int nmoe_decode_init(nmoe_hip_ctx *ctx) {
-    int n = ctx->num_cus;
+ * each other's exchange words): 1 when every variant's occupancy allows
+ * that on num_cus compute units. */
+extern "C" int nmoe_fused_resident(int num_cus) {
     int ok = 1;
 #define NMOE_FITS_ALL(B, R) \
-    ok = ok && nmoe_fused_fits_all<B, R>(n)
+    ok = ok && nmoe_fused_fits_all<B, R>(num_cus)
     NMOE_FITS_ALL(4, NMOE_ROUTE_BF16);
     NMOE_FITS_ALL(4, NMOE_ROUTE_Q4);
     NMOE_FITS_ALL(4, NMOE_ROUTE_GIVEN);
@@ -875,16 +872,22 @@ extern "C" int nmoe_decode_init(nmoe_hip_ctx *ctx) {
     NMOE_FITS_ALL(2, NMOE_ROUTE_Q4);
     NMOE_FITS_ALL(2, NMOE_ROUTE_GIVEN);
 #undef NMOE_FITS_ALL
+    return ok;
+}
+
+extern "C" int nmoe_decode_init(nmoe_hip_ctx *ctx) {
+    const int ok = nmoe_fused_resident(ctx->num_cus);
     ctx->fused_blocks = ok ? NMOE_FUSED_BLOCKS : 0;
     ctx->xcd_placed = 0;
-    if (ok) {
-        int r = nmoe_check_xcd_placement(&ctx->xcd_placed);
+    ctx->xch_bytes = NMOE_FUSED_XCH_BYTES;
+    if (hipMalloc((void **)&ctx->xch, ctx->xch_bytes) != hipSuccess) return NMOE_HIP_ENOMEM;
+    if (ok) { /* the probe writes into the exchange buffer, cleared afterwards */
+        int r = nmoe_probe_xcd_placement((uint32_t *)ctx->xch, &ctx->xcd_placed);
         if (r != NMOE_HIP_OK) return r;
     }
     ctx->use_xcd_local = ctx->xcd_placed;
-    ctx->xch_bytes = (size_t)NMOE_XCH_WORDS * sizeof(uint64_t);
-    if (hipMalloc((void **)&ctx->xch, ctx->xch_bytes) != hipSuccess) return NMOE_HIP_ENOMEM;
-    if (hipMemset(ctx->xch, 0, ctx->xch_bytes) != hipSuccess) return NMOE_HIP_EHIP;
+    if (hipMemset(ctx->xch, 0, ctx->xch_bytes) != hipSuccess || hipDeviceSynchronize() != hipSuccess)
+        return NMOE_HIP_EHIP;
     return NMOE_HIP_OK;
 }
 
@@ -896,13 +899,19 @@ static hipError_t nmoe_fused_launch_x(int xmode, const nmoe_fused_args &a, hipSt
     return hipErrorInvalidValue;
 }
 
-/* One token.  route != 0: routing computed from `router` (bf16 or q4); else given by
- * idx_in / w_in.  xmode: NMOE_XF32 / NMOE_XBF16 / NMOE_XNORM. */
-extern "C" int nmoe_fused_decode(nmoe_hip_ctx *ctx, int bits, int route, const void *x, int xmode, float eps, int k,
-                                 const nmoe_hip_router *router, const uint32_t *idx_in, const float *w_in,
-                                 const float *h_mid, const float *shared_out, const float *shared_gate_raw, float *out,
-                                 uint32_t *idx_out, float *w_out, float *logits_out, const uint8_t *pack,
-                                 hipStream_t s) {
+/* One token through the fused launch, every buffer given: xch
+ * (NMOE_FUSED_XCH_BYTES), sync (NMOE_SYNC_WORDS words: status and the
+ * per-block epochs), epoch 0 = the blocks' own launch counts, else the
+ * launch epoch (the caller never repeats one while words of an earlier
+ * launch with it may remain).  route != 0: routing computed from `router`
+ * (bf16 or q4); else given by idx_in / w_in.  xmode: NMOE_XF32 / NMOE_XBF16
+ * / NMOE_XNORM. */
+extern "C" hipError_t nmoe_fused_launch_core(int bits, int route, const void *x, int xmode, float eps, int k,
+                                             const nmoe_hip_router *router, const uint32_t *idx_in, const float *w_in,
+                                             const float *h_mid, const float *shared_out, const float *shared_gate_raw,
+                                             float *out, uint32_t *idx_out, float *w_out, float *logits_out,
+                                             const uint8_t *pack, uint64_t *xch, uint32_t *sync, int xcd_local,
+                                             uint32_t spin, uint32_t epoch, hipStream_t s) {
     nmoe_fused_args a;
     a.pack = pack;
     const bool q4r = router != NULL && router->kind == NMOE_HIP_ROUTER_Q4;
@@ -922,11 +931,11 @@ extern "C" int nmoe_fused_decode(nmoe_hip_ctx *ctx, int bits, int route, const v
     a.idx_out = idx_out;
     a.w_out = w_out;
     a.logits_out = logits_out;
-    a.xch = ctx->xch;
-    a.sync = ctx->sync;
-    a.xcd_local = ctx->use_xcd_local;
-    a.spin = ctx->spin_limit;
-    a.epoch_arg = 0u;
+    a.xch = xch;
+    a.sync = sync;
+    a.xcd_local = xcd_local;
+    a.spin = spin;
+    a.epoch_arg = epoch;
     hipError_t e = hipErrorInvalidValue;
     const int r = !route ? NMOE_ROUTE_GIVEN : q4r ? NMOE_ROUTE_Q4 : NMOE_ROUTE_BF16;
     if (bits == 4)
@@ -937,6 +946,17 @@ extern "C" int nmoe_fused_decode(nmoe_hip_ctx *ctx, int bits, int route, const v
         e = r == NMOE_ROUTE_Q4     ? nmoe_fused_launch_x<2, NMOE_ROUTE_Q4>(xmode, a, s)
             : r == NMOE_ROUTE_BF16 ? nmoe_fused_launch_x<2, NMOE_ROUTE_BF16>(xmode, a, s)
                                    : nmoe_fused_launch_x<2, NMOE_ROUTE_GIVEN>(xmode, a, s);
+    return e;
+}
+
+extern "C" int nmoe_fused_decode(nmoe_hip_ctx *ctx, int bits, int route, const void *x, int xmode, float eps, int k,
+                                 const nmoe_hip_router *router, const uint32_t *idx_in, const float *w_in,
+                                 const float *h_mid, const float *shared_out, const float *shared_gate_raw, float *out,
+                                 uint32_t *idx_out, float *w_out, float *logits_out, const uint8_t *pack,
+                                 hipStream_t s) {
+    const hipError_t e = nmoe_fused_launch_core(bits, route, x, xmode, eps, k, router, idx_in, w_in, h_mid, shared_out,
+                                                shared_gate_raw, out, idx_out, w_out, logits_out, pack, ctx->xch,
+                                                ctx->sync, ctx->use_xcd_local, ctx->spin_limit, 0u, s);
     if (e != hipSuccess) return nmoe_hip_check(ctx, e, "fused decode launch");
     return NMOE_HIP_OK;
 }

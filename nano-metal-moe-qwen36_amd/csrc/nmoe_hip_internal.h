@@ -50,6 +50,8 @@ struct nmoe_layout<2> {
 #define NMOE_SYNC_EPOCH(b) (64 + 16 * (b))     /* per-block launch epochs, 64 bytes apart */
 #define NMOE_SYNC_DISPATCH 4352                /* arrival counter of the dispatch blocks */
 #define NMOE_SYNC_BLOCKS 256
+/* The fused launch's exchange words (tagged logits, act and partial y). */
+#define NMOE_FUSED_XCH_BYTES 409600u
 
 struct nmoe_pack_slot {
     void *dev;

@@ -147,16 +147,11 @@ int nmoe_check_x(nmoe_hip_ctx *ctx, const void *x, int x_dtype, int ntok) {
     return NMOE_HIP_OK;
 }
 
-extern "C" int nmoe_moe_router_logits(nmoe_hip_ctx *ctx, const nmoe_hip_router *router, const void *x, int x_dtype,
-                                      int ntok, float *logits, void *stream) {
-    if (ctx == NULL) return NMOE_HIP_EINVAL;
-    int rc = nmoe_check_router(ctx, router);
-    if (rc == NMOE_HIP_OK) rc = nmoe_check_x(ctx, x, x_dtype, ntok);
-    if (rc != NMOE_HIP_OK) return rc;
-    if (logits == NULL) return nmoe_fail(ctx, NMOE_HIP_EINVAL, "NULL logits");
+/* The router launch with its arguments already checked. */
+extern "C" hipError_t nmoe_router_logits_launch(const nmoe_hip_router *router, const void *x, int x_dtype, int ntok,
+                                               float *logits, hipStream_t s) {
     int tpb = ntok <= 4 ? ntok : 4;
     dim3 grid(router->num_experts, (ntok + tpb - 1) / tpb);
-    hipStream_t s = nmoe_stream_of(ctx, stream);
     if (router->kind == NMOE_HIP_ROUTER_BF16) {
         if (x_dtype == NMOE_HIP_BF16)
             hipLaunchKernelGGL(nmoe_router_bf16_kernel<uint16_t>, grid, dim3(64), 0, s, router->w_bf16,
@@ -172,7 +167,23 @@ extern "C" int nmoe_moe_router_logits(nmoe_hip_ctx *ctx, const nmoe_hip_router *
             hipLaunchKernelGGL(nmoe_router_q4_kernel<float>, grid, dim3(64), 0, s, router->w_q4, router->scales,
                                router->biases, (const float *)x, ntok, router->num_experts, tpb, logits);
     }
-    NMOE_HIP_TRY(ctx, hipGetLastError());
+    return hipGetLastError();
+}
+
+extern "C" hipError_t nmoe_topk_launch(const float *logits, int ntok, int num_experts, int k, uint32_t *idx, float *w,
+                                      float *probs, hipStream_t s) {
+    hipLaunchKernelGGL(nmoe_topk_kernel, dim3(ntok), dim3(64), 0, s, logits, ntok, num_experts, k, idx, w, probs);
+    return hipGetLastError();
+}
+
+extern "C" int nmoe_moe_router_logits(nmoe_hip_ctx *ctx, const nmoe_hip_router *router, const void *x, int x_dtype,
+                                      int ntok, float *logits, void *stream) {
+    if (ctx == NULL) return NMOE_HIP_EINVAL;
+    int rc = nmoe_check_router(ctx, router);
+    if (rc == NMOE_HIP_OK) rc = nmoe_check_x(ctx, x, x_dtype, ntok);
+    if (rc != NMOE_HIP_OK) return rc;
+    if (logits == NULL) return nmoe_fail(ctx, NMOE_HIP_EINVAL, "NULL logits");
+    NMOE_HIP_TRY(ctx, nmoe_router_logits_launch(router, x, x_dtype, ntok, logits, nmoe_stream_of(ctx, stream)));
     return NMOE_HIP_OK;
 }
 
@@ -184,9 +195,7 @@ extern "C" int nmoe_moe_topk(nmoe_hip_ctx *ctx, const float *logits, int ntok, i
     if (num_experts < 1 || num_experts > NMOE_EXPERTS)
         return nmoe_fail(ctx, NMOE_HIP_EINVAL, "num_experts %d outside 1..256", num_experts);
     if (ntok < 1) return nmoe_fail(ctx, NMOE_HIP_EINVAL, "ntok must be >= 1");
-    hipLaunchKernelGGL(nmoe_topk_kernel, dim3(ntok), dim3(64), 0, nmoe_stream_of(ctx, stream), logits, ntok,
-                       num_experts, k, idx, w, probs);
-    NMOE_HIP_TRY(ctx, hipGetLastError());
+    NMOE_HIP_TRY(ctx, nmoe_topk_launch(logits, ntok, num_experts, k, idx, w, probs, nmoe_stream_of(ctx, stream)));
     return NMOE_HIP_OK;
 }
 

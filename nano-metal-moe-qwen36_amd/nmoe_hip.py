@@ -113,6 +113,7 @@ _SIGS = {
     "nmoe_moe_experts_q4": (_I, [_P, _I, _P, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P]),
     "nmoe_moe_experts_q2": (_I, [_P, _I, _P, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P]),
     "nmoe_moe_layer": (_I, [_P, _I, C.POINTER(Router), _P, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P]),
+    "nmoe_moe_layer_static": (_I, [_P, _I, C.POINTER(Router), _P, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P]),
     "nmoe_dequant_rows": (_I, [_P, _I, _P, _P, _P, _I, _I, _P, _P]),
     "nmoe_moe_layer_rmsnorm": (_I, [_P, _I, C.POINTER(Router), _P, C.c_float, _I, _P, _P, _P, _P, _P]),
     "nmoe_moe_stack": (_I, [_P, _I, C.POINTER(_I), C.POINTER(Router), _I, C.c_float, _P, _P, _P, _P]),
@@ -340,6 +341,19 @@ class Context:
     def dequant_rows(self, bits: int, packed, scales, biases, rows: int, in_dim: int, out, stream=None) -> int:
         return lib().nmoe_dequant_rows(self.h, bits, _ptr(packed), _ptr(scales), _ptr(biases), rows, in_dim,
                                        _ptr(out), stream)
+
+
+STATIC_MAX_TOKENS = 16
+
+
+def moe_layer_static(layer_pack, bits: int, router: Router, x, x_dtype: int, ntok: int, k: int, h_mid, out,
+                     idx=None, w=None, shared_out=None, shared_gate_raw=None, stream=None) -> int:
+    """nmoe_moe_layer_static: the per-layer call with no context and no
+    allocation, on the current device (layer_pack: a resident layer's device
+    address)."""
+    return lib().nmoe_moe_layer_static(_ptr(layer_pack), bits, C.byref(router), _ptr(x), x_dtype, ntok, k,
+                                       _ptr(h_mid), _ptr(shared_out), _ptr(shared_gate_raw), _ptr(out), _ptr(idx),
+                                       _ptr(w), stream)
 
 
 def validate_layout(path: str):
