@@ -42,6 +42,7 @@ _ORACLE_SIGS = {
     "orc_dequant_row": (None, [_P, _P, _P, _P, _SZ, _I]),
     "orc_dequant_matvec": (None, [_P, _P, _P, _P, _P, _SZ, _SZ, _I]),
     "orc_route": (_I, [_P, _I, _I, _P, _P, _P]),
+    "orc_quantize_rows": (None, [_P, _I, _I, _I, _P, _P, _P]),
     "orc_expf_restated": (_F, [_F]),
     "orc_router_logits_bf16": (None, [_P, _P, _I, _I, _P]),
     "orc_router_logits_q4": (None, [_P, _P, _P, _P, _I, _I, _P]),
@@ -208,6 +209,18 @@ def shared_expert(se: dict, x: np.ndarray):
     for t in range(x.shape[0]):
         oracle().orc_shared_expert(*args, x[t].ctypes.data, out[t].ctypes.data, g[t:].ctypes.data)
     return out, g
+
+
+def quantize_rows(rows_bf16: np.ndarray, bits: int):
+    """orc_quantize_rows: (packed u32, scales u16, biases u16)."""
+    rows_bf16 = np.ascontiguousarray(rows_bf16, np.uint16)
+    rows, cols = rows_bf16.shape
+    packed = np.zeros((rows, cols * bits // 32), np.uint32)
+    scales = np.zeros((rows, cols // GROUP), np.uint16)
+    biases = np.zeros((rows, cols // GROUP), np.uint16)
+    oracle().orc_quantize_rows(rows_bf16.ctypes.data, rows, cols, bits, packed.ctypes.data, scales.ctypes.data,
+                               biases.ctypes.data)
+    return packed, scales, biases
 
 
 def moe_block(pack: np.ndarray, bits: int, router: dict, h_mid: np.ndarray, k: int, eps: float = 1e-6,

@@ -201,6 +201,45 @@ void orc_dequant_matvec(const uint32_t *packed, const uint16_t *scales, const ui
     }
 }
 
+/* ------------------------------------------------------- the writer side */
+
+/* scripts/convert_qwen36.py:167-211 (quantize_rows_bf16 / _2bit with
+ * pack_4bit / pack_2bit): per group of 64 columns of a bf16 row, min and max
+ * in fp32, scale = (max - min) / 15 (q4) or / 3 (q2) in fp32, a zero scale
+ * replaced by 1 for the division only, q = rint((x - min) / scale) (ties to
+ * even, the default rounding mode) clipped to the code range, column 8w + v
+ * (16w + v for q2) in field v of word w; scale and min stored as bf16 by the
+ * math.m:14-19 rule (the converter's f32_to_bf16, :151-155).  Inputs are
+ * finite. */
+void orc_quantize_rows(const uint16_t *rows_bf16, int rows, int in_dim, int bits, uint32_t *packed,
+                       uint16_t *scales, uint16_t *biases) {
+    const int vpw = 32 / bits, groups = in_dim / ORC_GROUP;
+    const float qmax = bits == 4 ? 15.0f : 3.0f;
+    for (int r = 0; r < rows; r++) {
+        const uint16_t *row = rows_bf16 + (size_t)r * in_dim;
+        uint32_t *pr = packed + (size_t)r * (in_dim / vpw);
+        memset(pr, 0, sizeof(uint32_t) * (size_t)(in_dim / vpw));
+        for (int g = 0; g < groups; g++) {
+            float mn = orc_bf16_to_f32(row[g * ORC_GROUP]), mx = mn;
+            for (int i = 1; i < ORC_GROUP; i++) {
+                const float v = orc_bf16_to_f32(row[g * ORC_GROUP + i]);
+                if (v < mn) mn = v;
+                if (v > mx) mx = v;
+            }
+            const float scale = (mx - mn) / qmax;
+            const float safe = scale == 0.0f ? 1.0f : scale;
+            for (int i = 0; i < ORC_GROUP; i++) {
+                const int c = g * ORC_GROUP + i;
+                float q = rintf((orc_bf16_to_f32(row[c]) - mn) / safe);
+                q = q < 0.0f ? 0.0f : q > qmax ? qmax : q;
+                pr[c / vpw] |= (uint32_t)q << (bits * (c % vpw));
+            }
+            scales[(size_t)r * groups + g] = orc_f32_to_bf16(scale);
+            biases[(size_t)r * groups + g] = orc_f32_to_bf16(mn);
+        }
+    }
+}
+
 /* ------------------------------------------------------------- routing */
 
 /* runtime.m:1498-1511 with the slot padding of kernels.metal:1767-1775. */

@@ -63,6 +63,12 @@ void orc_dequant_row(const uint32_t *packed_row, const uint16_t *scales_row, con
 void orc_dequant_matvec(const uint32_t *packed, const uint16_t *scales, const uint16_t *biases,
                         const float *input, float *output, size_t out_dim, size_t in_dim, int quant_bits);
 
+/* The converter's quantiser and packer, convert_qwen36.py:147-211: bf16
+ * rows [rows][in_dim] -> packed u32 [rows][in_dim*bits/32], bf16 scales and
+ * biases [rows][in_dim/64].  Finite inputs. */
+void orc_quantize_rows(const uint16_t *rows_bf16, int rows, int in_dim, int bits, uint32_t *packed,
+                       uint16_t *scales, uint16_t *biases);
+
 /* runtime.m:1498-1511 (softmax -> top-k -> renormalise on one token's logits).
  * idx/w are padded to 8 slots: unused slots get index 0 and weight 0
  * (kernels.metal:1767-1775).  probs (nullable) receives the softmax output.

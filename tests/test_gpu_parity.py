@@ -859,3 +859,56 @@ def test_fused_q4_router_with_rmsnorm(ctx, nh, bits):
         np.testing.assert_array_equal(I[l], oi, err_msg=f"layer {l}")
         np.testing.assert_array_equal(Wt[l].view(np.uint32), ow.view(np.uint32), err_msg=f"layer {l}")
         assert_close(H[l + 1], want, what=f"q{bits} q4-router stack layer {l}")
+
+
+@pytest.mark.parametrize("bits", [4, 2])
+def test_converter_packs_on_device(ctx, nh, bits):
+    """The writer side of the format, end to end.  (a) The converter's own
+    quantised rows (tests/golden/converter_golden.npz, from
+    scripts/convert_qwen36.py:147-211) dequantised by the device probe equal
+    math.m's dequant (math.m:206-234) bit for bit.  (b) Experts quantised the
+    converter's way (orc_quantize_rows, pinned to the converter's outputs)
+    and laid out at its offsets (convert_qwen36.py:38-64, 402-406), uploaded
+    unchanged, run through the expert path within tolerance of the oracle."""
+    import os
+    cg = np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "converter_golden.npz"))
+    o = B.oracle()
+    for name, cols in (("gu", 2048), ("dn", 512)):
+        packed, sc, bi = (cg[f"{name}_q{bits}_{t}"] for t in ("packed", "scales", "biases"))
+        rows = packed.shape[0]
+        out = ctx.alloc(rows * cols * 4)
+        ctx._check(ctx.dequant_rows(bits, ctx.to_device(packed), ctx.to_device(sc), ctx.to_device(bi), rows, cols, out))
+        got = out.download(np.float32, (rows, cols))
+        for r in range(rows):
+            want = np.zeros(cols, np.float32)
+            o.orc_dequant_row(np.ascontiguousarray(packed[r]).ctypes.data, np.ascontiguousarray(sc[r]).ctypes.data,
+                              np.ascontiguousarray(bi[r]).ctypes.data, want.ctypes.data, cols, bits)
+            np.testing.assert_array_equal(got[r].view(np.uint32), want.view(np.uint32), err_msg=f"{name} row {r}")
+    # (b) a layer of converter-quantised experts
+    rng = np.random.default_rng(300 + bits)
+    layer, k = 46 + bits, 8
+    experts = [3, 77, 140, 255, 0, 9, 200, 31]
+    esz = B.EXPERT_SIZE[bits]
+    off = np.zeros(9, np.uint64)
+    o.orc_expert_offsets(bits, off.ctypes.data)
+    pack = np.zeros(256 * esz, np.uint8)
+    for e in experts:
+        base = e * esz
+        for i, (r_, c_) in enumerate(((512, 2048), (512, 2048), (2048, 512))):
+            w = B.f32_to_bf16((rng.standard_normal((r_, c_)) * 0.02).astype(np.float32))
+            pk, s_, b_ = B.quantize_rows(w, bits)
+            for j, arr in enumerate((pk, s_, b_)):
+                raw = arr.view(np.uint8).ravel()
+                o0 = base + int(off[3 * i + j])
+                pack[o0:o0 + raw.size] = raw
+    ctx.upload_layer(layer, bits, pack)
+    x = B.f32_to_bf16(rng.standard_normal((1, 2048)).astype(np.float32))
+    h = rng.standard_normal((1, 2048)).astype(np.float32)
+    idx = np.array([experts], np.uint32)
+    w = rng.dirichlet(np.ones(k), size=1).astype(np.float32)
+    want = B.moe_experts(pack, bits, B.bf16_to_f32(x).reshape(1, 2048), k, idx, w, h)
+    out = ctx.alloc(8192)
+    ctx._check(ctx.experts(bits, layer, ctx.to_device(x), nh.BF16, 1, k, ctx.to_device(idx), ctx.to_device(w),
+                           ctx.to_device(h), out))
+    assert ctx.device_status() == nh.OK
+    assert_close(out.download(np.float32, (1, 2048)), want, what=f"converter-quantised q{bits} layer")
