@@ -5,8 +5,13 @@ token through one routed-expert layer of Qwen3.6-35B-A3B -- bf16 router
 [256][2048], softmax/top-8/renormalise, eight q4 group-64 experts
 (2048 -> 512 gate/up, SwiGLU, 512 -> 2048 down), weighted combine into the
 fp32 residual.  Steps rotate over 40 synthetic layers resident in HBM
-(40 x 453 MB = 18.1 GB, far above the 256 MB last-level cache) with a
-distinct router and input per layer, so weights stream from HBM.
+(40 x 453 MB = 18.1 GB, far above the 256 MB last-level cache) and over 320
+routers (320 MB), so experts and router rows stream from HBM.  The timed
+steps come after the warm-up's, never on the layers it just read.
+
+The same JSON line carries two sub-objects measured in the same run: "c3"
+(128 decode tokens through the 40-layer stack) and "c5" (the 2048-token
+prefill on the grouped matrix-core path, with its MFMA utilisation).
 
 A step is one call of the per-layer MoE entry point (nmoe_moe_layer), which
 for one token is a single persistent launch (nmoe_fused_decode_kernel).
@@ -28,7 +33,7 @@ reference sources into oracle/_ref, single-threaded, -O3) on a bounded
 sample of the same workload; the repository's C restatement ("port") when
 oracle/_ref was not built.
 
-    python bench.py [--gpus 1] [--steps 400] [--warmup 40]
+    python bench.py [--gpus 1] [--steps 400] [--warmup 40] [--no-extra] [--workload c1|c3|c4|c5]
 """
 from __future__ import annotations
 
@@ -159,112 +164,187 @@ def cpu_baseline(bits: int, k: int, seed: int, nsteps: int, nlayers: int = 4) ->
 
 
 MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 (no sparsity)
+# Routers rotate over this many copies (320 MB of bf16 routers, above the
+# 256 MB memory-side cache), so a step's router row comes from HBM as it does
+# in real decode, where the other weights of a token evict the routers.
+ROUTER_POOL = 320
 
 
-def synth_routers(ctx, buf, NL: int, args) -> list:
-    """One synthetic router per layer in `buf` (NL * ROUTER_BYTES): dense bf16
+def synth_routers(ctx, buf, NR: int, args) -> list:
+    """NR synthetic routers in `buf` (NR * ROUTER_BYTES): dense bf16
     N(0, 0.02) [256][2048], or the model's q4 form (codes uniform 0..15,
-    scale bf16(N(0, 0.002)), bias bf16(-8 scale), all from the repository's
-    seeded generators) packed into the same slot."""
+    scale bf16(N(0, 0.002)), bias bf16(-8 scale), from seeded generators)
+    packed into the same slot."""
     rts = []
-    for layer in range(NL):
-        base = buf.ptr + layer * ROUTER_BYTES
+    for r in range(NR):
+        base = buf.ptr + r * ROUTER_BYTES
         if args.router == "bf16":
-            ctx.synth_bf16(buf, 256 * 2048, args.seed, layer, 16, 0.02, offset=layer * ROUTER_BYTES)
+            ctx.synth_bf16(buf, 256 * 2048, args.seed, r, 16, 0.02, offset=r * ROUTER_BYTES)
             rts.append(ctx.router_bf16(base))
         else:
-            rng = np.random.default_rng(args.seed * 1000 + layer)
+            rng = np.random.default_rng(args.seed * 1000 + r)
             wq = rng.integers(0, 2**32, size=256 * 256, dtype=np.uint64).astype(np.uint32)
             sc = (rng.standard_normal(256 * 32) * 0.002).astype(np.float32)
             s16 = ((sc.view(np.uint32).astype(np.uint64) + 0x7FFF + ((sc.view(np.uint32) >> 16) & 1)) >> 16).astype(np.uint16)
             bi = (-8.0 * (s16.astype(np.uint32) << 16).view(np.float32)).astype(np.float32)
             b16 = ((bi.view(np.uint32).astype(np.uint64) + 0x7FFF + ((bi.view(np.uint32) >> 16) & 1)) >> 16).astype(np.uint16)
-            buf.upload(wq, offset=layer * ROUTER_BYTES)
-            buf.upload(s16, offset=layer * ROUTER_BYTES + wq.nbytes)
-            buf.upload(b16, offset=layer * ROUTER_BYTES + wq.nbytes + s16.nbytes)
+            buf.upload(wq, offset=r * ROUTER_BYTES)
+            buf.upload(s16, offset=r * ROUTER_BYTES + wq.nbytes)
+            buf.upload(b16, offset=r * ROUTER_BYTES + wq.nbytes + s16.nbytes)
             rts.append(ctx.router_q4(base, base + wq.nbytes, base + wq.nbytes + s16.nbytes))
     return rts
 
 
-def bench_stack(args, nh):
-    """C3: the routed-expert stack of one decode token through 40 resident
-    layers, h_{l+1} = h_l + MoE_l(RMSNorm(h_l)) (unit weight, eps 1e-6), one
-    fused launch per layer (nmoe_moe_stack); a step is one token's 40 layers,
-    over 128 distinct synthetic tokens.  tokens/s = 1 / (time for 40 layers)."""
-    bits, k, NL = args.bits, args.k, 40
-    ntok = 128
-    sigma = 0.02 if bits == 4 else 0.05
-    ctx = nh.Context(0, max_tokens=8)
+class Pool:
+    """The resident data every workload draws from: NL synthetic layers
+    (40 q4 layers = 18.1 GB, far above the memory-side cache), ROUTER_POOL
+    routers, and one bf16 x and fp32 residual per router slot."""
+
+    def __init__(self, nh, args, max_tokens: int):
+        self.nh, self.args = nh, args
+        self.NL, self.NR = args.layers, max(ROUTER_POOL, args.layers)
+        bits = args.bits
+        self.ctx = ctx = nh.Context(0, max_tokens=max_tokens)
+        print(f"[bench] device 0: {ctx.cus} CUs; {self.NL} q{bits} layers, {self.NR} {args.router} routers",
+              file=sys.stderr, flush=True)
+        for layer in range(self.NL):
+            ctx.synth_layer(layer, bits, args.seed, 0.02 if bits == 4 else 0.05)
+        self.routers = ctx.alloc(self.NR * ROUTER_BYTES, "bench.routers")
+        self.rts = synth_routers(ctx, self.routers, self.NR, args)
+        self.X = ctx.alloc(self.NR * 4096, "bench.x")
+        Hb = ctx.alloc(self.NR * 4096, "bench.hb")
+        ctx.synth_bf16(self.X, self.NR * 2048, args.seed, 0, 17, 1.0)
+        ctx.synth_bf16(Hb, self.NR * 2048, args.seed, 0, 18, 1.0)
+        hb = Hb.download(np.uint16, (self.NR, 2048))
+        self.H = ctx.to_device((hb.astype(np.uint32) << 16).view(np.float32), "bench.h")
+        self.h0 = (hb.astype(np.uint32) << 16).view(np.float32)
+        ctx.sync()
+
+
+def run_c1(pool, args) -> dict:
+    """The headline: one decode token through one q4 top-8 layer per step.
+    Step i uses layer i % 40 and router / x / residual slot i % 320; the
+    timed steps are W .. W+K-1, after the K warm-up steps 0 .. W-1, so no
+    timed step re-reads a layer or router the warm-up just brought in."""
+    nh, ctx, bits, k = pool.nh, pool.ctx, args.bits, args.k
     stream = ctx.stream
-    print(f"[bench] c3: {NL}-layer stack, q{bits} top-{k}, {ntok} tokens", file=sys.stderr, flush=True)
-    for layer in range(NL):
-        ctx.synth_layer(layer, bits, args.seed, sigma)
-    routers = ctx.alloc(NL * ROUTER_BYTES, "bench.routers")
-    rts = synth_routers(ctx, routers, NL, args)
-    H0 = ctx.alloc(ntok * 2048 * 2, "bench.h0")
-    ctx.synth_bf16(H0, ntok * 2048, args.seed, 99, 18, 1.0)
-    h0 = (H0.download(np.uint16, (ntok, 2048)).astype(np.uint32) << 16).view(np.float32)
-    HS = ctx.alloc(ntok * (NL + 1) * 2048 * 4, "bench.hseq")
-    row = (NL + 1) * 2048 * 4
-    for t in range(ntok):
-        HS.upload(h0[t], offset=t * row)
-    layers = list(range(NL))
-    ctx.sync()
+    NL, NR = pool.NL, pool.NR
+    OUT, IDX, WT = ctx.alloc(NL * 8192, "c1.out"), ctx.alloc(NL * 32, "c1.idx"), ctx.alloc(NL * 32, "c1.w")
 
     def step(i):
-        return ctx.moe_stack(layers, rts, k, 1e-6, HS.ptr + (i % ntok) * row, stream=stream)
+        layer, r = i % NL, i % NR
+        return ctx.moe_layer(layer, pool.rts[r], pool.X.ptr + r * 4096, nh.BF16, 1, k, pool.H.ptr + r * 8192,
+                             OUT.ptr + layer * 8192, IDX.ptr + layer * 32, WT.ptr + layer * 32, stream=stream)
 
-    warm = min(args.warmup, 8)
-    for i in range(warm):
+    for i in range(args.warmup):
         ctx._check(step(i))
     ctx.sync()
-    steps = args.steps if args.steps != 400 else ntok
     ev = HipEvents()
     e0, e1 = ev.create(2)
     ev.record(e0, stream)
-    for i in range(steps):
-        step(i)
+    for i in range(args.steps):
+        step(args.warmup + i)
     ev.record(e1, stream)
-    ms = ev.ms(e0, e1) / steps
+    ms = ev.ms(e0, e1) / args.steps
+    ctx.sync()
+    if ctx.device_status() != 0:
+        raise SystemExit(f"device status error: {ctx.last_error()}")
+    ev.destroy([e0, e1])
+    B = step_bytes(bits, k, args.router)
+    achieved = B / (ms * 1e-3) / 1e9
+    return {
+        "metric": "routed-MoE tokens/s + achieved HBM GB/s (q4, top-8, batch 1, 1 GPU)",
+        "value": round(1e3 / ms, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "hbm_gbps": round(achieved, 1),
+        "config": {
+            "workload": f"c1: single-layer q{bits} top-{k} batch-1 routed-MoE decode step ({args.router} router, "
+                        f"hidden 2048, 256 experts, FFN 512), rotating over {NL} HBM-resident layers and {NR} routers",
+            "bits": bits, "k": k, "batch": 1, "layers_rotated": NL, "routers_rotated": NR, "bytes_per_step": B,
+            "router": args.router, "entry_point": "nmoe_moe_layer",
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": profiled_traffic(bits, k) if args.router == "bf16" else None,
+            "kernel": f"nmoe_fused_decode_kernel<{bits}, 1, 1> (one launch per step)",
+            "kernel_ms": round(ms, 5),
+        },
+    }
+
+
+def run_c3(pool, args, ntok: int = 128) -> dict:
+    """C3: 128 decode tokens, each through the 40 resident layers,
+    h_{l+1} = h_l + MoE_l(RMSNorm(h_l)) (nmoe_moe_stack); token t takes its
+    routers from block t % 8 of the pool (320 MB between reuses).  Four
+    untimed tokens with their own inputs go first."""
+    nh, ctx, bits, k, NL = pool.nh, pool.ctx, args.bits, args.k, pool.NL
+    stream = ctx.stream
+    sets = pool.NR // NL
+    layers = list(range(NL))
+    row = (NL + 1) * 2048 * 4
+    warm = 4
+    HS = ctx.alloc((ntok + warm) * row, "c3.hseq")
+    for t in range(ntok + warm):
+        HS.upload(pool.h0[t % pool.NR], offset=t * row)
+    ctx.sync()
+
+    def step(t):
+        rs = [pool.rts[(t % sets) * NL + l] for l in layers]
+        return ctx.moe_stack(layers, rs, k, 1e-6, HS.ptr + t * row, stream=stream)
+
+    for t in range(ntok, ntok + warm):
+        ctx._check(step(t))
+    ctx.sync()
+    ev = HipEvents()
+    e0, e1 = ev.create(2)
+    ev.record(e0, stream)
+    for t in range(ntok):
+        step(t)
+    ev.record(e1, stream)
+    ms = ev.ms(e0, e1) / ntok
     ctx.sync()
     if ctx.device_status() != 0:
         raise SystemExit(f"device status error: {ctx.last_error()}")
     ev.destroy([e0, e1])
     B = NL * step_bytes(bits, k, args.router)
-    result = {
+    gbs = B / (ms * 1e-3) / 1e9
+    return {
         "metric": f"routed-MoE stack tokens/s (c3: {NL} layers, q{bits}, top-{k}, batch 1, 1 GPU)",
-        "value": round(1e3 / ms, 1), "unit": "tokens/s", "n_gpus": 1, "steps": steps, "warmup": warm,
-        "ms_per_step": round(ms, 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "f32", "data": "synthetic",
-        "config": {"workload": "c3", "layers": NL, "tokens": ntok, "bits": bits, "k": k, "bytes_per_token": B,
-                   "router": args.router,
-                   "entry_point": "nmoe_moe_stack (one nmoe_moe_layer_rmsnorm launch per layer)"},
-        "hbm_gbps": round(B / (ms * 1e-3) / 1e9, 1),
-        "us_per_layer": round(ms * 1e3 / NL, 2),
+        "value": round(1e3 / ms, 1), "unit": "tokens/s", "tokens": ntok, "ms_per_token": round(ms, 5),
+        "us_per_layer": round(ms * 1e3 / NL, 2), "hbm_gbps": round(gbs, 1),
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4)},
+        "config": {"workload": "c3", "layers": NL, "bits": bits, "k": k, "bytes_per_token": B, "router": args.router,
+                   "routers_rotated": pool.NR, "entry_point": "nmoe_moe_stack"},
     }
-    ctx.close()
-    print(json.dumps(result), flush=True)
 
 
-def bench_grouped(args, nh):
+def run_grouped(pool, args, workload: str, NLg: int = 8) -> dict:
     """C4 (64 tokens, Zipf-skewed logits = ln p_e + Gumbel, p_e ~ rank^-1.1)
     or C5 (2048 tokens, uniform U(0,1) logits): a step is device top-k on
     the given logits + the grouped expert path (dispatch, gate/up + SwiGLU
-    and down on the matrix cores, slot-order combine), rotating over
-    `layers` resident layers (default 8) so the weights stream from HBM."""
-    bits, k = args.bits, args.k
-    ntok = 64 if args.workload == "c4" else 2048
-    NL = args.layers if args.layers != 40 else 8
-    sigma = 0.02 if bits == 4 else 0.05
-    rng = np.random.default_rng(args.seed)
-    ctx = nh.Context(0, max_tokens=ntok)
+    and down on the matrix cores, slot-order combine).  Timed steps rotate
+    over layers 0 .. NLg-1; the warm-up runs layers NLg .. 2 NLg - 1 first."""
+    nh, ctx, bits, k = pool.nh, pool.ctx, args.bits, args.k
     stream = ctx.stream
-    print(f"[bench] {args.workload}: {ntok} tokens, q{bits} top-{k}, {NL} layers", file=sys.stderr, flush=True)
-    for layer in range(NL):
-        ctx.synth_layer(layer, bits, args.seed, sigma)
+    ntok = 64 if workload == "c4" else 2048
+    rng = np.random.default_rng(args.seed + (4 if workload == "c4" else 5))
     logits, xs, hs, touched = [], [], [], []
-    for layer in range(NL):
-        if args.workload == "c4":
+    for layer in range(2 * NLg):
+        if workload == "c4":
             order = rng.permutation(256)
             logp = np.empty(256)
             logp[order] = -1.1 * np.log(np.arange(1, 257))
@@ -280,21 +360,19 @@ def bench_grouped(args, nh):
     IDX, WT, OUT = ctx.alloc(ntok * 32), ctx.alloc(ntok * 32), ctx.alloc(ntok * 2048 * 4)
     ctx.sync()
 
-    def step(i):
-        layer = i % NL
+    def step(layer):
         ctx._check(ctx.topk(logits[layer], ntok, 256, k, IDX, WT, stream=stream))
         ctx._check(ctx.experts(bits, layer, xs[layer], nh.BF16, ntok, k, IDX, WT, hs[layer], OUT, stream=stream))
 
-    steps = args.steps if args.steps != 400 else (100 if args.workload == "c4" else 30)
-    warm = min(args.warmup, 10)
-    for i in range(warm):
-        step(i)
+    steps = 100 if workload == "c4" else 30
+    for i in range(2 * NLg):
+        step(NLg + i % NLg)
     ctx.sync()
     ev = HipEvents()
     e0, e1 = ev.create(2)
     ev.record(e0, stream)
     for i in range(steps):
-        step(i)
+        step(i % NLg)
     ev.record(e1, stream)
     ms = ev.ms(e0, e1) / steps
     ctx.sync()
@@ -302,34 +380,27 @@ def bench_grouped(args, nh):
         raise SystemExit(f"device status error: {ctx.last_error()}")
     ev.destroy([e0, e1])
     esz = EXPERT_BYTES[bits]
-    U = float(np.mean([touched[i % NL] for i in range(steps)]))
+    U = float(np.mean([touched[i % NLg] for i in range(steps)]))
     act_bytes = ntok * (4096 + 8192 + 8192 + 64) + ntok * 256 * 4  # x, h, out, idx/w, logits
     B = U * esz + act_bytes
     flops = 2.0 * ntok * k * 3 * 2048 * 512
     tflops = flops / (ms * 1e-3) / 1e12
-    result = {
-        "metric": f"routed-MoE tokens/s ({args.workload}: {ntok} tokens, q{bits}, top-{k}, 1 GPU)",
-        "value": round(ntok / (ms * 1e-3), 1),
-        "unit": "tokens/s",
-        "n_gpus": 1,
-        "steps": steps,
-        "warmup": warm,
-        "ms_per_step": round(ms, 5),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
+    gbs = B / (ms * 1e-3) / 1e9
+    return {
+        "metric": f"routed-MoE tokens/s ({workload}: {ntok} tokens, q{bits}, top-{k}, 1 GPU)",
+        "value": round(ntok / (ms * 1e-3), 1), "unit": "tokens/s", "steps": steps, "ms_per_step": round(ms, 5),
         "dtype": "bf16 x (exact integer codes) on the matrix cores, fp32 accumulate",
-        "data": "synthetic",
-        "config": {"workload": args.workload, "tokens": ntok, "bits": bits, "k": k, "layers_rotated": NL,
+        "hbm_gbps": round(gbs, 1), "roofline_hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+        "mfma_tflops": round(tflops, 1), "mfma_utilisation": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
+        "roofline": {"bound": "mfma" if workload == "c5" else "hbm",
+                     "achieved": round(tflops, 1) if workload == "c5" else round(gbs, 1),
+                     "peak": MFMA_BF16_PEAK_TFLOPS if workload == "c5" else HBM_PEAK_GBS,
+                     "unit": "TFLOP/s" if workload == "c5" else "GB/s",
+                     "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS if workload == "c5" else gbs / HBM_PEAK_GBS, 4)},
+        "config": {"workload": workload, "tokens": ntok, "bits": bits, "k": k, "layers_rotated": NLg,
                    "distinct_experts_per_step": round(U, 1), "bytes_per_step": int(B), "flops_per_step": int(flops),
                    "entry_point": "nmoe_moe_topk + nmoe_moe_experts_q%d (grouped path)" % bits},
-        "hbm_gbps": round(B / (ms * 1e-3) / 1e9, 1),
-        "roofline_hbm_frac": round(B / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-        "mfma_tflops": round(tflops, 1),
-        "mfma_utilisation": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
     }
-    ctx.close()
-    print(json.dumps(result), flush=True)
 
 
 def main():
@@ -343,14 +414,15 @@ def main():
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--cpu-steps", type=int, default=630)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-extra", action="store_true", help="c1 only: no c3 / c5 sub-objects")
     ap.add_argument("--copy-calib", type=int, default=0, metavar="MIB",
                     help="only run 5 device-to-device copies of MIB MiB (counter calibration) and exit")
     ap.add_argument("--router", default="bf16", choices=("bf16", "q4"),
                     help="c1/c3: the benchmark configs' dense bf16 router (default) or the model's q4 router")
     ap.add_argument("--workload", default="c1", choices=("c1", "c3", "c4", "c5"),
-                    help="c1: the headline single-layer decode step (default); c3: 40-layer routed-expert stack of "
-                         "one decode token, 128 tokens; c4: batched decode, 64 tokens, Zipf-skewed routing; "
-                         "c5: 2048-token prefill (grouped matrix-core path)")
+                    help="c1: the headline single-layer decode step, with c3 and c5 sub-objects (default); "
+                         "c3 / c4 / c5 alone: 40-layer stack of 128 tokens / batched decode of 64 Zipf-routed "
+                         "tokens / 2048-token prefill on the grouped matrix-core path")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -371,95 +443,22 @@ def main():
         ctx.close()
         return
 
+    grouped = args.workload in ("c4", "c5") or (args.workload == "c1" and not args.no_extra)
+    pool = Pool(nh, args, max_tokens=2048 if grouped else 8)
     if args.workload == "c3":
-        return bench_stack(args, nh)
-    if args.workload != "c1":
-        return bench_grouped(args, nh)
-
-    bits, k, NL = args.bits, args.k, args.layers
-    sigma = 0.02 if bits == 4 else 0.05
-    ctx = nh.Context(0, max_tokens=8)
-    stream = ctx.stream
-    print(f"[bench] device 0: {ctx.cus} CUs; building {NL} q{bits} layers", file=sys.stderr, flush=True)
-    for layer in range(NL):
-        ctx.synth_layer(layer, bits, args.seed, sigma)
-    routers = ctx.alloc(NL * ROUTER_BYTES, "bench.routers")
-    rts = synth_routers(ctx, routers, NL, args)
-    X = ctx.alloc(NL * 2048 * 2, "bench.x")
-    Hb = ctx.alloc(NL * 2048 * 2, "bench.hb")
-    for layer in range(NL):
-        ctx.synth_bf16(X, 2048, args.seed, layer, 17, 1.0, offset=layer * 4096)
-        ctx.synth_bf16(Hb, 2048, args.seed, layer, 18, 1.0, offset=layer * 4096)
-    hb = Hb.download(np.uint16, (NL, 2048))
-    H = ctx.to_device((hb.astype(np.uint32) << 16).view(np.float32), "bench.h")
-    OUT = ctx.alloc(NL * 2048 * 4, "bench.out")
-    IDX = ctx.alloc(NL * 32, "bench.idx")
-    WT = ctx.alloc(NL * 32, "bench.w")
-    ctx.sync()
-
-    def step(i):
-        layer = i % NL
-        return ctx.moe_layer(layer, rts[layer], X.ptr + layer * 4096, nh.BF16, 1, k, H.ptr + layer * 8192,
-                             OUT.ptr + layer * 8192, IDX.ptr + layer * 32, WT.ptr + layer * 32, stream=stream)
-
-    for i in range(args.warmup):
-        ctx._check(step(i))
-    ctx.sync()
-
-    ev = HipEvents()
-    e0, e1 = ev.create(2)
-    ctx.sync()
-    ev.record(e0, stream)
-    for i in range(args.steps):
-        step(i)
-    ev.record(e1, stream)
-    total_ms = ev.ms(e0, e1)
-    ctx.sync()
-    if ctx.device_status() != 0:
-        raise SystemExit(f"device status error: {ctx.last_error()}")
-    ms_per_step = total_ms / args.steps
-
-    ev.destroy([e0, e1])
-    kern_ms = ms_per_step  # one launch per step
-
-    B = step_bytes(bits, k, args.router)
-    tps = 1e3 / ms_per_step
-    achieved = B / (kern_ms * 1e-3) / 1e9
-    result = {
-        "metric": "routed-MoE tokens/s + achieved HBM GB/s (q4, top-8, batch 1, 1 GPU)",
-        "value": round(tps, 1),
-        "unit": "tokens/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(ms_per_step, 5),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "f32",
-        "data": "synthetic",
-        "hbm_gbps": round(B / (ms_per_step * 1e-3) / 1e9, 1),
-        "config": {
-            "workload": f"single-layer q{bits} top-{k} batch-1 routed-MoE decode step ({args.router} router, hidden 2048, "
-                        f"256 experts, FFN 512), rotating over {NL} HBM-resident layers",
-            "bits": bits, "k": k, "batch": 1, "layers_rotated": NL, "bytes_per_step": B, "router": args.router,
-            "entry_point": "nmoe_moe_layer",
-        },
-        "roofline": {
-            "bound": "hbm",
-            "achieved": round(achieved, 1),
-            "peak": HBM_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": profiled_traffic(bits, k) if args.router == "bf16" else None,
-            "kernel": f"nmoe_fused_decode_kernel<{bits},true,bf16> (one launch per step)",
-            "kernel_ms": round(kern_ms, 5),
-        },
-    }
-    if not args.no_cpu:
-        print("[bench] cpu baseline ...", file=sys.stderr, flush=True)
-        result["cpu_baseline"] = cpu_baseline(bits, k, args.seed, args.cpu_steps)
-    ctx.close()
+        result = run_c3(pool, args)
+    elif args.workload in ("c4", "c5"):
+        result = run_grouped(pool, args, args.workload)
+    else:
+        result = run_c1(pool, args)
+        if not args.no_extra:
+            print("[bench] c3 and c5 sub-benchmarks ...", file=sys.stderr, flush=True)
+            result["c3"] = run_c3(pool, args)
+            result["c5"] = run_grouped(pool, args, "c5")
+        if not args.no_cpu:
+            print("[bench] cpu baseline ...", file=sys.stderr, flush=True)
+            result["cpu_baseline"] = cpu_baseline(args.bits, args.k, args.seed, args.cpu_steps)
+    pool.ctx.close()
     print(json.dumps(result), flush=True)
 
 
