@@ -269,6 +269,53 @@ NMOE_HIP_API int nmoe_moe_layer_rmsnorm(nmoe_hip_ctx *ctx, int layer, const nmoe
                                         const float *h_in, float eps, int k, float *h_out, uint32_t *idx, float *w,
                                         float *logits, void *stream);
 
+/* ---- the MoE half of one layer, whole, for one token in one launch: the
+ * route/shared stage of the attention step's tail (src/runtime.m:3144-3201:
+ * post-attention RMSNorm, the q4 router, the shared expert's gate/up and
+ * score, kernels.metal:384-514), the expert tail NMOEPipelinedExpertTail
+ * (runtime.m:2908-2999, the shared down in the combine, kernels.metal:
+ * 1456-1542) and the next layer's input norm (runtime.m:2893-2900):
+ *   x      = RMSNorm(h_mid) * w_post       (math.m:34-65; w = 1 + weight with
+ *                                           add_one, unit weight when NULL)
+ *   idx, w = softmax / top-k / renormalise of router . x
+ *   out    = h_mid + sum_s w_s down_s(SwiGLU(gate_s x, up_s x))
+ *            + sigmoid(score . x) * shared_down(SwiGLU(shared_gate x, shared_up x))
+ *   next_x = RMSNorm(out) * w_next         (when next_x is not NULL)
+ * out may alias h_mid (the residual is updated in place, runtime.m:2827-2831);
+ * h_mid 16-byte aligned.  nmoe_hip_layer_block fills the descriptor from
+ * weights loaded by nmoe_hip_load_model_weights. */
+typedef struct nmoe_hip_moe_block {
+    nmoe_hip_router router;        /* the layer's router: the model's q4 .mlp.gate, or bf16 */
+    int has_shared;                /* 1: `shared` holds the layer's shared expert */
+    nmoe_hip_shared_expert shared; /* .mlp.shared_expert.{gate,up,down}_proj, .mlp.shared_expert_gate */
+    const uint16_t *post_norm;     /* bf16 [2048] post_attention_layernorm.weight, NULL = unit */
+    const uint16_t *next_norm;     /* bf16 [2048] the next layer's input_layernorm.weight, NULL = unit */
+    int add_one;                   /* 1: the norm weights enter as 1 + w (the model's, runtime.m:3149, 2898) */
+    float eps;                     /* rms_norm_eps */
+} nmoe_hip_moe_block;
+
+NMOE_HIP_API int nmoe_moe_block(nmoe_hip_ctx *ctx, int layer, const nmoe_hip_moe_block *blk, const float *h_mid,
+                                int k, float *out, float *next_x, uint32_t *idx, float *w, float *logits,
+                                void *stream);
+
+/* ---- the model's non-expert weights of the MoE path, from the converter's
+ * model_weights.bin / model_weights.json (scripts/convert_qwen36.py:266-327;
+ * read by src/manifest.m:229-316).  For layers 0 .. n-1 (n = nlayers, or
+ * config.num_hidden_layers when 0) the tensors the MoE block needs
+ * (runtime.m:2349-2369: input_layernorm / post_attention_layernorm .weight
+ * BF16; mlp.gate, mlp.shared_expert.{gate,up,down}_proj, mlp.shared_expert_gate
+ * as .weight U32 + .scales/.biases BF16) are checked -- present, dtype and
+ * range as NMOETensorPointer (runtime.m:2271-2299), size as the kernels read
+ * them -- and made resident; the manifest may take any of the shapes the
+ * reference's reader walks.  layers_out (nullable) receives n. */
+NMOE_HIP_API int nmoe_hip_load_model_weights(nmoe_hip_ctx *ctx, const char *bin_path, const char *json_path,
+                                             int nlayers, int *layers_out);
+/* The MoE block of a loaded layer: q4 router, shared expert, its
+ * post-attention norm, the next layer's input norm (NULL for the last
+ * loaded layer), add_one 1, eps = config.rms_norm_eps.  ENOENT if the
+ * layer's weights are not loaded. */
+NMOE_HIP_API int nmoe_hip_layer_block(const nmoe_hip_ctx *ctx, int layer, nmoe_hip_moe_block *out);
+
 /* ---- the routed-expert stack of one decode token (the layer loop of
  * NMOEProcessToken, runtime.m:3732-3777, restricted to the MoE tails):
  * h_seq[l+1] = h_seq[l] + MoE_l(RMSNorm(h_seq[l])) for l < nlayers.

@@ -468,5 +468,20 @@ extern "C" int nmoe_dequant_rows(nmoe_hip_ctx *ctx, int bits, const uint32_t *pa
     return NMOE_HIP_OK;
 }
 
+/* The model weights' MoE blocks (set by host/weights.c). */
+extern "C" int nmoe_ctx_set_block(nmoe_hip_ctx *ctx, int layer, const nmoe_hip_moe_block *b) {
+    if (ctx == NULL || b == NULL || layer < 0 || layer >= NMOE_HIP_MAX_LAYERS) return NMOE_HIP_EINVAL;
+    ctx->blocks[layer] = *b;
+    ctx->block_set[layer] = 1;
+    return NMOE_HIP_OK;
+}
+
+extern "C" int nmoe_hip_layer_block(const nmoe_hip_ctx *ctx, int layer, nmoe_hip_moe_block *out) {
+    if (ctx == NULL || out == NULL || layer < 0 || layer >= NMOE_HIP_MAX_LAYERS) return NMOE_HIP_EINVAL;
+    if (!ctx->block_set[layer]) return NMOE_HIP_ENOENT;
+    *out = ctx->blocks[layer];
+    return NMOE_HIP_OK;
+}
+
 /* Error hook for the C host files of the library. */
 extern "C" int nmoe_host_fail(nmoe_hip_ctx *ctx, int code, const char *msg) { return nmoe_fail(ctx, code, "%s", msg); }

@@ -21,6 +21,8 @@
  * for every row.  Nibbles/crumbs are expanded with byte masks and
  * v_cvt_f32_ubyte{0..3}; accumulation is fp32.
  */
+#include <string.h>
+
 #include "nmoe_device.h"
 
 /* ----------------------------------------------------------- gate/up */
@@ -355,5 +357,49 @@ extern "C" int nmoe_moe_layer_rmsnorm(nmoe_hip_ctx *ctx, int layer, const nmoe_h
                                       const float *h_in, float eps, int k, float *h_out, uint32_t *idx, float *w,
                                       float *logits, void *stream) {
     const int rc = nmoe_layer_rmsnorm_launch(ctx, layer, router, h_in, eps, k, h_out, idx, w, logits, stream);
+    return rc != NMOE_HIP_OK ? rc : nmoe_sync_check(ctx, stream);
+}
+
+extern "C" int nmoe_fused_block(nmoe_hip_ctx *ctx, int bits, const nmoe_hip_router *router, const float *h_mid,
+                                float eps, int k, const nmoe_block_ext *blk, float *out, uint32_t *idx_out,
+                                float *w_out, float *logits_out, const uint8_t *pack, hipStream_t s);
+
+static bool nmoe_qtensor_set(const nmoe_hip_qtensor &q) {
+    return q.w != NULL && q.scales != NULL && q.biases != NULL && nmoe_aligned(q.w, 16) && nmoe_aligned(q.scales, 2) &&
+           nmoe_aligned(q.biases, 2);
+}
+
+extern "C" int nmoe_moe_block(nmoe_hip_ctx *ctx, int layer, const nmoe_hip_moe_block *blk, const float *h_mid, int k,
+                              float *out, float *next_x, uint32_t *idx, float *w, float *logits, void *stream) {
+    if (ctx == NULL) return NMOE_HIP_EINVAL;
+    if (blk == NULL) return nmoe_fail(ctx, NMOE_HIP_EINVAL, "NULL block descriptor");
+    if (layer < 0 || layer >= NMOE_HIP_MAX_LAYERS || ctx->packs[layer].dev == NULL)
+        return nmoe_fail(ctx, NMOE_HIP_ENOENT, "layer %d has no resident pack", layer);
+    int rc = nmoe_check_router(ctx, &blk->router);
+    if (rc != NMOE_HIP_OK) return rc;
+    if (blk->router.num_experts != NMOE_EXPERTS)
+        return nmoe_fail(ctx, NMOE_HIP_EINVAL, "a layer pack holds 256 experts; router has %d", blk->router.num_experts);
+    if (k < 1 || k > NMOE_MAX_K) return nmoe_fail(ctx, NMOE_HIP_EINVAL, "k=%d outside 1..8", k);
+    if (h_mid == NULL || out == NULL || !nmoe_aligned(h_mid, 16) || !nmoe_aligned(out, 4) ||
+        (next_x != NULL && !nmoe_aligned(next_x, 4)))
+        return nmoe_fail(ctx, NMOE_HIP_EINVAL, "h_mid (16-byte aligned) and out are required");
+    if (blk->has_shared && !(nmoe_qtensor_set(blk->shared.gate) && nmoe_qtensor_set(blk->shared.up) &&
+                             nmoe_qtensor_set(blk->shared.down) && nmoe_qtensor_set(blk->shared.score)))
+        return nmoe_fail(ctx, NMOE_HIP_EINVAL, "shared expert: NULL or misaligned tensor (w 16 B, scales/biases 2 B)");
+    if ((blk->post_norm != NULL && !nmoe_aligned(blk->post_norm, 2)) ||
+        (blk->next_norm != NULL && !nmoe_aligned(blk->next_norm, 2)))
+        return nmoe_fail(ctx, NMOE_HIP_EINVAL, "misaligned norm weight");
+    if (!(blk->eps >= 0.0f)) return nmoe_fail(ctx, NMOE_HIP_EINVAL, "eps must be >= 0");
+    if (ctx->fused_blocks == 0)
+        return nmoe_fail(ctx, NMOE_HIP_EINVAL, "the device cannot hold the 256-block fused grid");
+    nmoe_block_ext ext;
+    memset(&ext, 0, sizeof(ext));
+    ext.norm_w = blk->post_norm;
+    ext.next_w = blk->next_norm;
+    ext.add_one = blk->add_one != 0;
+    ext.next_x = next_x;
+    if (blk->has_shared) ext.sh = blk->shared;
+    rc = nmoe_fused_block(ctx, ctx->packs[layer].bits, &blk->router, h_mid, blk->eps, k, &ext, out, idx, w, logits,
+                          (const uint8_t *)ctx->packs[layer].dev, nmoe_stream_of(ctx, stream));
     return rc != NMOE_HIP_OK ? rc : nmoe_sync_check(ctx, stream);
 }

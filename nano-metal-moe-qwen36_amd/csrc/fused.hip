@@ -47,6 +47,8 @@
  * combine of a chunk polls the chunk's K-1 other partials in one block.
  * Idle groups (K < 8) exit after their router row.  Every wait is bounded.
  */
+#include <string.h>
+
 #include "nmoe_device.h"
 
 #pragma clang fp contract(off)
@@ -79,11 +81,24 @@ static __constant__ uint64_t nmoe_fused_exp2_tab[32] = NMOE_EXP2_TAB32;
 #define NMOE_XCH_YPART (NMOE_XCH_ACT + NMOE_XCH_SP * NMOE_FUSED_GROUPS * NMOE_INTER)
 #define NMOE_XCH_WORDS (NMOE_XCH_YPART + NMOE_FUSED_GROUPS * NMOE_HIDDEN) /* tagged partials, polled by one block */
 static_assert(NMOE_XCH_WORDS * sizeof(uint64_t) == NMOE_FUSED_XCH_BYTES, "exchange size as the host allocates it");
+/* The whole-block form (XBLOCK) adds: the shared expert's activations
+ * [512] (64 B apart, polled by the 32 combining blocks), each combining
+ * block's double-double sum of squares of its output rows (4 words on a
+ * 64-byte line of its own) and its output rows themselves (dense, read only
+ * on the exact-replay path of the next-layer norm). */
+#define NMOE_XCH_SHACT NMOE_XCH_WORDS
+#define NMOE_XCH_NSQ (NMOE_XCH_SHACT + NMOE_XCH_SP * NMOE_INTER)
+#define NMOE_XCH_NOUT (NMOE_XCH_NSQ + NMOE_XCH_SP * NMOE_FUSED_GROUP_BLOCKS)
+#define NMOE_XCH_WORDS_BLOCK (NMOE_XCH_NOUT + NMOE_HIDDEN)
+static_assert(NMOE_XCH_WORDS_BLOCK * sizeof(uint64_t) == NMOE_FUSED_XCH_BYTES_BLOCK, "the whole-block exchange size");
 
-/* x sources: XF32 / XBF16 = activations given; XNORM = x is RMSNorm(h). */
+/* x sources: XF32 / XBF16 = activations given; XNORM = x is RMSNorm(h);
+ * XBLOCK = the whole MoE half of a layer: x is the weighted RMSNorm of h,
+ * with the shared expert and the next layer's input norm optional. */
 #define NMOE_XF32 0
 #define NMOE_XBF16 1
 #define NMOE_XNORM 2
+#define NMOE_XBLOCK 3
 
 /* ROUTE: routing given (idx_in / w_in), or computed from a bf16 or a q4 router */
 #define NMOE_ROUTE_GIVEN 0
@@ -113,6 +128,12 @@ struct nmoe_fused_args {
     int xcd_local; /* act travels through the die's L2 (a group's blocks share a die) */
     uint32_t spin; /* unsuccessful poll rounds a wait tolerates before it gives up */
     uint32_t epoch_arg; /* nonzero: the launch epoch (no per-block epoch words) */
+    /* XBLOCK only */
+    const uint16_t *norm_w; /* bf16 [2048] weight of x's RMSNorm (NULL: unit) */
+    const uint16_t *next_w; /* bf16 [2048] weight of the next-layer norm (NULL: unit) */
+    int add_one;            /* the weights enter as 1 + w */
+    float *next_x;          /* RMSNorm(out, next_w), or NULL */
+    nmoe_hip_shared_expert sh; /* the shared expert (sh.gate.w == NULL: none) */
 };
 
 /* Die-local exchange: words written and read only by blocks of one
@@ -262,9 +283,22 @@ __device__ __forceinline__ void nmoe_x_cols(const void *x, int c0, int n, double
         nmoe_load_cols<uint16_t>((const uint16_t *)x, c0, n, out);
     } else {
         nmoe_load_cols<float>((const float *)x, c0, n, out);
-        if (XMODE == NMOE_XNORM)
+        if (XMODE == NMOE_XNORM || XMODE == NMOE_XBLOCK)
             for (int i = 0; i < n; i++) out[i] = (float)((double)out[i] * rinv);
     }
+}
+
+/* The weight math.m:34-65 multiplies by: bf16 w (+1 for the model's
+ * zero-centred norms, math.m:58-60), 1 without a weight tensor. */
+__device__ __forceinline__ float nmoe_norm_weight(const uint16_t *w, int c, int add_one) {
+    if (w == NULL) return 1.0f;
+    const float v = nmoe_bf16f(w[c]);
+    return add_one ? v + 1.0f : v;
+}
+
+/* A tagged word with a raw 32-bit payload (halves of a double). */
+__device__ __forceinline__ void nmoe_st_tagged_u32(uint64_t *p, uint32_t epoch, uint32_t v) {
+    __hip_atomic_store(p, ((uint64_t)epoch << 32) | v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 /* LDS slot of act element e.  Lane dl of a down row reads float4 chunks
@@ -286,6 +320,8 @@ __global__ void __launch_bounds__(NMOE_FUSED_THREADS) nmoe_fused_decode_kernel(n
     constexpr int RPW_D = NMOE_WAVE / Q::LPR_D; /* down rows per wave step: 4 (q4) / 8 (q2) */
     constexpr int DSTEPS = NMOE_FUSED_CHUNK / NMOE_FUSED_WORKERS / RPW_D; /* down rows per worker, in steps */
     static_assert(GSTEPS >= 1 && DSTEPS >= 1, "rows split evenly over the worker wavefronts");
+    constexpr bool NORM = XMODE == NMOE_XNORM || XMODE == NMOE_XBLOCK; /* x = RMSNorm(h) in the block */
+    constexpr bool BLK = XMODE == NMOE_XBLOCK;
     __shared__ uint64_t s_tab[32];
     __shared__ float s_scratch[NMOE_EXPERTS];
     __shared__ float s_lg[NMOE_EXPERTS]; /* the token's logits, candidate -> exact wavefront */
@@ -301,13 +337,22 @@ __global__ void __launch_bounds__(NMOE_FUSED_THREADS) nmoe_fused_decode_kernel(n
     __shared__ uint32_t s_epoch;
     __shared__ uint32_t s_ncand, s_confirm, s_lgok; /* control -> workers / control -> control hand-offs */
     __shared__ uint32_t s_bad; /* a wait of this block gave up: what it publishes is NaN */
-    __shared__ __align__(16) float s_h[XMODE == NMOE_XNORM ? NMOE_HIDDEN : 4];
+    __shared__ __align__(16) float s_h[NORM ? NMOE_HIDDEN : 4];
+    /* XBLOCK: the shared expert (gate values of this block's two rows, the
+     * combining block's copy of all 512 activations, its 64 shared-down
+     * rows and gate score) and the hand-offs between the wavefronts */
+    __shared__ __align__(16) float s_sact[BLK ? NMOE_INTER : 4];
+    __shared__ float s_shd[BLK ? NMOE_FUSED_CHUNK : 1];
+    __shared__ float s_shg[2], s_sgr[1];
+    __shared__ uint32_t s_shok, s_sacnt;
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const bool ctrl = wave >= NMOE_FUSED_CTRL; /* either control wavefront */
     const bool cwave = wave == NMOE_FUSED_CTRL;
     const int g = blockIdx.x % NMOE_FUSED_GROUPS, j = blockIdx.x / NMOE_FUSED_GROUPS;
     const int k = a.k;
+    const bool comb = g == j % k;               /* this block combines rows 64j .. 64j+63 */
+    const bool has_sh = BLK && a.sh.gate.w != NULL;
     uint32_t *status = a.sync + NMOE_SYNC_STATUS;
     uint64_t *xlg = a.xch + NMOE_XCH_LOGITS;
     uint64_t *xact = a.xch + NMOE_XCH_ACT + NMOE_XCH_ASP * g * NMOE_INTER;
@@ -322,9 +367,12 @@ __global__ void __launch_bounds__(NMOE_FUSED_THREADS) nmoe_fused_decode_kernel(n
     const uint32_t ep_old = a.epoch_arg != 0u ? 0u : nmoe_ld_u32_dev(ep);
     const uint64_t tab_v = nmoe_fused_exp2_tab[tid & 31];
     const int crow = j * NMOE_FUSED_CHUNK + (tid & (NMOE_FUSED_CHUNK - 1));
-    const float hm = a.h_mid[crow];
-    const float sh = a.shared_out != NULL ? a.shared_out[crow] : 0.0f;
-    const float sgr = a.shared_out != NULL ? a.shared_gate_raw[0] : 0.0f;
+    /* XBLOCK may write out over h_mid: only the combining block reads the
+     * rows it will overwrite (every block's reads of h end before its first
+     * barrier, long before any block writes out) */
+    const float hm = !BLK || comb ? a.h_mid[crow] : 0.0f;
+    const float sh = !BLK && a.shared_out != NULL ? a.shared_out[crow] : 0.0f;
+    const float sgr = !BLK && a.shared_out != NULL ? a.shared_gate_raw[0] : 0.0f;
     uint4 wv[4];
     uint32_t wq[4];
     uint16_t rsr[4], rbr[4];
@@ -346,9 +394,22 @@ __global__ void __launch_bounds__(NMOE_FUSED_THREADS) nmoe_fused_decode_kernel(n
 #pragma unroll
             for (int q = 0; q < 4; q++) wv[q] = row[lane + 64 * q];
         }
-        if (XMODE != NMOE_XNORM)
+        if (!NORM)
 #pragma unroll
             for (int q = 0; q < 4; q++) nmoe_x_cols<XMODE>(a.x, (lane + 64 * q) * 8, 8, 1.0, xs_r + 8 * q);
+    }
+    /* XBLOCK, combining block: the shared expert's gate-score row
+     * (kernels.metal:510-513), a router-like row the candidate wavefront
+     * reduces after its router row */
+    uint32_t sq_w[4];
+    uint16_t sq_s[4], sq_b[4];
+    if (has_sh && cwave && comb) {
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            sq_w[q] = a.sh.score.w[lane + 64 * q];
+            sq_s[q] = a.sh.score.scales[(lane + 64 * q) / 8];
+            sq_b[q] = a.sh.score.biases[(lane + 64 * q) / 8];
+        }
     }
     if (tid < 32) s_tab[tid] = tab_v;
     if (tid < NMOE_MAX_K) { /* in-range defaults for every routing word a wait may leave unwritten */
@@ -370,18 +431,26 @@ __global__ void __launch_bounds__(NMOE_FUSED_THREADS) nmoe_fused_decode_kernel(n
         s_confirm = 0u;
         s_lgok = 0u;
         s_bad = 0u;
+        s_shok = 0u;
+        s_sacnt = 0u;
     }
-    if (XMODE == NMOE_XNORM) {
-        /* x = h / rms once per block, into LDS in the workers' swizzled
-         * chunk order (as the act): the workers then hold no raw h and do
-         * no double arithmetic of their own */
+    if (NORM) {
+        /* x = h / rms (times the norm weight, XBLOCK) once per block, into
+         * LDS in the workers' swizzled chunk order (as the act): the workers
+         * then hold no raw h and do no double arithmetic of their own */
         const double rinv = 1.0 / (double)nmoe_block_rms_exact((const float *)a.x, a.eps, s_h, s_dd, s_f);
         if (tid < NMOE_HIDDEN / 8) {
 #pragma unroll
             for (int q = 0; q < 2; q++) {
                 const int c0 = 8 * tid + 4 * q;
                 float4 v;
-                nmoe_x_cols<NMOE_XNORM>(a.x, c0, 4, rinv, &v.x);
+                nmoe_x_cols<XMODE>(a.x, c0, 4, rinv, &v.x);
+                if (BLK && a.norm_w != NULL) { /* math.m:63: (h / rms) * weight */
+                    v.x = v.x * nmoe_norm_weight(a.norm_w, c0, a.add_one);
+                    v.y = v.y * nmoe_norm_weight(a.norm_w, c0 + 1, a.add_one);
+                    v.z = v.z * nmoe_norm_weight(a.norm_w, c0 + 2, a.add_one);
+                    v.w = v.w * nmoe_norm_weight(a.norm_w, c0 + 3, a.add_one);
+                }
                 ((float4 *)s_h)[nmoe_act_slot<Q::CPL / 4>(c0) / 4] = v;
             }
         }
@@ -389,12 +458,89 @@ __global__ void __launch_bounds__(NMOE_FUSED_THREADS) nmoe_fused_decode_kernel(n
     __syncthreads();
     const uint32_t epoch = s_epoch;
 
+    if (has_sh && wave < 4) {
+        /* ---- S1 (XBLOCK, every block): shared gate/up rows 2b, 2b+1
+         * (kernels.metal:421-469) in the router's per-element form, while
+         * the routing runs: wavefronts 0, 1 reduce the gate rows, 2, 3 the
+         * up rows and publish SiLU(gate) * up for the combining blocks */
+        const int srow = 2 * blockIdx.x + (wave & 1);
+        const nmoe_hip_qtensor T = wave < 2 ? a.sh.gate : a.sh.up;
+        uint32_t w4[4];
+        uint16_t s4[4], b4[4];
+        float xq[32];
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            w4[q] = T.w[(size_t)srow * (NMOE_HIDDEN / 8) + lane + 64 * q];
+            s4[q] = T.scales[(size_t)srow * (NMOE_HIDDEN / NMOE_GROUP) + (lane + 64 * q) / 8];
+            b4[q] = T.biases[(size_t)srow * (NMOE_HIDDEN / NMOE_GROUP) + (lane + 64 * q) / 8];
+        }
+#pragma unroll
+        for (int c = 0; c < 8; c++)
+            *(float4 *)(xq + 4 * c) =
+                ((const float4 *)s_h)[nmoe_act_slot<Q::CPL / 4>(8 * lane + 512 * (c >> 1) + 4 * (c & 1)) / 4];
+        const float v = nmoe_router_row_q4(w4, s4, b4, xq);
+        if (wave < 2) {
+            if (lane == 0) {
+                s_shg[wave] = v;
+                __hip_atomic_fetch_add(&s_shok, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+            }
+        } else {
+            nmoe_lds_wait_above(&s_shok, 1u, status, &s_bad, a.spin);
+            float act = nmoe_silu_dev(s_shg[wave & 1]) * v;
+            if (nmoe_lds_flag(&s_bad)) act = __builtin_nanf("");
+            if (lane == 0) nmoe_st_tagged(a.xch + NMOE_XCH_SHACT + NMOE_XCH_SP * srow, epoch, act);
+        }
+    }
+
+    /* ---- S2 (XBLOCK, combining block, both control wavefronts after their
+     * routing): all 512 shared activations into LDS, then this chunk's 64
+     * shared-down rows (kernels.metal:1520-1537), 32 per wavefront: 16 lanes
+     * a row (32 columns each, fma(fma(q, s, b), act, acc) as the shared-down
+     * kernel), four rows a step */
+    auto shared_down = [&](int half) {
+        const uint64_t *ps[4];
+        float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int q = 0; q < 4; q++) ps[q] = a.xch + NMOE_XCH_SHACT + NMOE_XCH_SP * (256 * half + lane + 64 * q);
+        nmoe_poll<4>(ps, epoch, v, status, &s_bad, a.spin);
+#pragma unroll
+        for (int q = 0; q < 4; q++) s_sact[256 * half + lane + 64 * q] = v[q];
+        if (lane == 0) __hip_atomic_fetch_add(&s_sacnt, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+        const int dl16 = lane & 15, rsub = lane >> 4;
+        uint4 dw[8];
+        uint16_t ds[8], db[8];
+#pragma unroll
+        for (int st = 0; st < 8; st++) {
+            const int row = j * NMOE_FUSED_CHUNK + 32 * half + 4 * st + rsub;
+            dw[st] = *(const uint4 *)(a.sh.down.w + (size_t)row * (NMOE_INTER / 8) + 4 * dl16);
+            ds[st] = a.sh.down.scales[(size_t)row * (NMOE_INTER / NMOE_GROUP) + dl16 / 2];
+            db[st] = a.sh.down.biases[(size_t)row * (NMOE_INTER / NMOE_GROUP) + dl16 / 2];
+        }
+        nmoe_lds_wait_above(&s_sacnt, 1u, status, &s_bad, a.spin); /* the other half is in */
+        float av[32];
+#pragma unroll
+        for (int c = 0; c < 8; c++) *(float4 *)(av + 4 * c) = ((const float4 *)s_sact)[8 * dl16 + c];
+#pragma unroll
+        for (int st = 0; st < 8; st++) {
+            const float sc = nmoe_bf16f(ds[st]), bi = nmoe_bf16f(db[st]);
+            const uint32_t wd[4] = {dw[st].x, dw[st].y, dw[st].z, dw[st].w};
+            float acc = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int n = 0; n < 8; n++)
+                    acc = __builtin_fmaf(__builtin_fmaf((float)((wd[i] >> (4 * n)) & 0xFu), sc, bi), av[8 * i + n], acc);
+            acc = nmoe_dpp_group_sum<16>(acc);
+            if (dl16 == 0) s_shd[32 * half + 4 * st + rsub] = acc;
+        }
+    };
+
     if (ROUTE && cwave) {
         /* the control wavefronts share SIMDs with workers: their routing is
          * on the critical path, the workers' multiply-adds mostly are not */
         __builtin_amdgcn_s_setprio(2);
         /* ---- R (candidate wavefront): router row blockIdx.x */
-        if (XMODE == NMOE_XNORM)
+        if (NORM)
 #pragma unroll
             for (int c = 0; c < 8; c++)
                 *(float4 *)(xs_r + 4 * c) =
@@ -402,6 +548,10 @@ __global__ void __launch_bounds__(NMOE_FUSED_THREADS) nmoe_fused_decode_kernel(n
         const float logit =
             ROUTE == NMOE_ROUTE_Q4 ? nmoe_router_row_q4(wq, rsr, rbr, xs_r) : nmoe_router_row_bf16(wv, xs_r);
         if (lane == 0) nmoe_st_tagged(xlg + NMOE_XCH_SP * blockIdx.x, epoch, logit);
+        if (has_sh && comb) { /* the shared expert's gate score, same x */
+            const float v = nmoe_router_row_q4(sq_w, sq_s, sq_b, xs_r);
+            if (lane == 0) s_sgr[0] = v;
+        }
         if (g < k) {
             /* ---- T: wait for all 256 logits and hand them to the exact
              * wavefront; the candidates are the k largest logits, published
@@ -448,6 +598,7 @@ __global__ void __launch_bounds__(NMOE_FUSED_THREADS) nmoe_fused_decode_kernel(n
                 }
             }
             if (lane == 0) __hip_atomic_store(&s_ncand, (uint32_t)k, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+            if (has_sh && comb) shared_down(0);
         }
     }
     if (ROUTE && wave == NMOE_FUSED_EXACT && g < k) {
@@ -569,6 +720,7 @@ __global__ void __launch_bounds__(NMOE_FUSED_THREADS) nmoe_fused_decode_kernel(n
             }
         }
         if (lane == 0) __hip_atomic_store(&s_confirm, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+        if (has_sh && comb) shared_down(1);
     }
     if (!ROUTE) {
         if (tid < NMOE_MAX_K) {
@@ -625,7 +777,7 @@ __global__ void __launch_bounds__(NMOE_FUSED_THREADS) nmoe_fused_decode_kernel(n
     if (!ctrl) {
         /* x first: loads retire in order, so G can start while down rows stream */
         const uint4 *xp = (const uint4 *)a.x + gl * XV;
-        if (XMODE != NMOE_XNORM)
+        if (!NORM)
 #pragma unroll
             for (int c = 0; c < XV; c++) xr[c] = xp[c];
         if (ROUTE) /* candidate g published by the control wavefront */
@@ -640,7 +792,7 @@ __global__ void __launch_bounds__(NMOE_FUSED_THREADS) nmoe_fused_decode_kernel(n
     float xs[Q::CPL];
 #pragma unroll
     for (int c = 0; c < XV; c++) {
-        if (XMODE == NMOE_XNORM) {
+        if (NORM) {
             *(float4 *)(xs + 4 * c) = ((const float4 *)s_h)[nmoe_act_slot<Q::CPL / 4>(4 * (gl * XV + c)) / 4];
         } else if (XMODE == NMOE_XBF16) {
             nmoe_unpack_bf16x8(xr[c], xs + 8 * c);
@@ -744,6 +896,7 @@ __global__ void __launch_bounds__(NMOE_FUSED_THREADS) nmoe_fused_decode_kernel(n
      * chunk: one round trip after the last one is written. */
     const int row = j * NMOE_FUSED_CHUNK + tid;
     const bool poisoned = nmoe_lds_flag(&s_bad); /* every wait of the block is behind the barrier above */
+    float rv = 0.0f; /* the combining thread's out row */
     if (tid < NMOE_FUSED_CHUNK) {
         if (g != j % k) {
             nmoe_st_tagged(ypart + g * NMOE_HIDDEN + row, epoch, poisoned ? __builtin_nanf("") : s_y[tid]);
@@ -767,7 +920,9 @@ __global__ void __launch_bounds__(NMOE_FUSED_THREADS) nmoe_fused_decode_kernel(n
                 sgl[s] = s < k ? s_slotg[s] : (uint32_t)s;
                 ident = ident && sgl[s] == (uint32_t)s;
             }
-            const float gsig = a.shared_out != NULL ? nmoe_sigmoid_dev(sgr) : 0.0f;
+            const bool shared_term = BLK ? has_sh : a.shared_out != NULL;
+            const float gsig = shared_term ? nmoe_sigmoid_dev(BLK ? s_sgr[0] : sgr) : 0.0f;
+            const float shv = BLK ? (has_sh ? s_shd[tid] : 0.0f) : sh;
             const bool expired = nmoe_poll2<NMOE_MAX_K>(pp, epoch, ys, status, &s_bad, a.spin,
                                                         ((1u << k) - 1u) & ~(1u << g));
             /* slot order: slot s is streamed by group sgl[s] */
@@ -789,9 +944,70 @@ __global__ void __launch_bounds__(NMOE_FUSED_THREADS) nmoe_fused_decode_kernel(n
                 }
             }
             float r = hm + moe;
-            if (a.shared_out != NULL) r = r + gsig * sh;
-            a.out[row] = poisoned || expired ? __builtin_nanf("") : r;
+            if (shared_term) r = r + gsig * shv;
+            rv = poisoned || expired ? __builtin_nanf("") : r;
+            a.out[row] = rv;
         }
+    }
+    if (BLK && comb && a.next_x != NULL && wave == 0) {
+        /* ---- N (XBLOCK): the next layer's input norm of out
+         * (runtime.m:2893-2900, math.m:34-65).  Each combining block
+         * publishes the double-double sum of its 64 squares (exact) and its
+         * rows; each sums the 32 partials in one fixed order, so all reach
+         * the same mean square, the float math.m's long double sum rounds
+         * to, or replay that x87 sum over all 2048 rows in index order. */
+        double S, Cc;
+        nmoe_wave_dd_sum((double)rv * (double)rv, 0.0, S, Cc);
+        uint64_t *nsq = a.xch + NMOE_XCH_NSQ;
+        if (lane == 0) {
+            const uint64_t sb = __builtin_bit_cast(uint64_t, S), cb = __builtin_bit_cast(uint64_t, Cc);
+            nmoe_st_tagged_u32(nsq + NMOE_XCH_SP * j + 0, epoch, (uint32_t)sb);
+            nmoe_st_tagged_u32(nsq + NMOE_XCH_SP * j + 1, epoch, (uint32_t)(sb >> 32));
+            nmoe_st_tagged_u32(nsq + NMOE_XCH_SP * j + 2, epoch, (uint32_t)cb);
+            nmoe_st_tagged_u32(nsq + NMOE_XCH_SP * j + 3, epoch, (uint32_t)(cb >> 32));
+        }
+        nmoe_st_tagged(a.xch + NMOE_XCH_NOUT + row, epoch, rv);
+        const int src = lane & (NMOE_FUSED_GROUP_BLOCKS - 1); /* lanes 32..63 poll nothing */
+        const uint64_t *pq[4] = {nsq + NMOE_XCH_SP * src, nsq + NMOE_XCH_SP * src + 1, nsq + NMOE_XCH_SP * src + 2,
+                                 nsq + NMOE_XCH_SP * src + 3};
+        float pv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        nmoe_poll<4>(pq, epoch, pv, status, &s_bad, a.spin, false, lane < NMOE_FUSED_GROUP_BLOCKS ? 0xFu : 0u);
+        double ps = 0.0, pc = 0.0;
+        if (lane < NMOE_FUSED_GROUP_BLOCKS) {
+            ps = __builtin_bit_cast(double, ((uint64_t)__float_as_uint(pv[1]) << 32) | __float_as_uint(pv[0]));
+            pc = __builtin_bit_cast(double, ((uint64_t)__float_as_uint(pv[3]) << 32) | __float_as_uint(pv[2]));
+        }
+        nmoe_wave_dd_sum(ps, pc, S, Cc);
+        float mean = nmoe_dd_mean_float(S, Cc);
+        if (mean < 0.0f) {
+            /* near a rounding midpoint (or tiny values): all 2048 rows, the
+             * x87 running sum in index order (s_h is free: x is consumed) */
+            for (int i0 = 0; i0 < NMOE_HIDDEN; i0 += 4 * NMOE_WAVE) {
+                const uint64_t *po[4] = {a.xch + NMOE_XCH_NOUT + i0 + lane, a.xch + NMOE_XCH_NOUT + i0 + lane + 64,
+                                         a.xch + NMOE_XCH_NOUT + i0 + lane + 128,
+                                         a.xch + NMOE_XCH_NOUT + i0 + lane + 192};
+                float ov[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+                nmoe_poll<4>(po, epoch, ov, status, &s_bad, a.spin);
+#pragma unroll
+                for (int q = 0; q < 4; q++) s_h[i0 + lane + 64 * q] = ov[q];
+            }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+            float t = 0.0f;
+            if (lane == 0) {
+                nmoe_x87 acc = nmoe_x87_zero();
+                for (int i = 0; i < NMOE_HIDDEN; i++) acc = nmoe_x87_add(acc, nmoe_x87_square(s_h[i]));
+                acc.e -= 11; /* / 2048, exact */
+                t = nmoe_x87_to_float(acc);
+            }
+            mean = nmoe_readlane_f(t, 0);
+        }
+        float rms = nmoe_sqrtf_rn(mean + a.eps);
+        rms = rms == 0.0f ? 1.0f : rms;
+        float xn = (float)((double)rv * (1.0 / (double)rms));
+        xn = a.next_w != NULL ? xn * nmoe_norm_weight(a.next_w, row, a.add_one) : xn;
+        a.next_x[row] = nmoe_lds_flag(&s_bad) ? __builtin_nanf("") : xn; /* a partial that never came */
     }
     if (ROUTE && blockIdx.x == 0 && cwave) {
         if (lane < NMOE_MAX_K) {
@@ -826,7 +1042,8 @@ static int nmoe_fused_fits(int num_cus) {
 template <int BITS, int ROUTE>
 static int nmoe_fused_fits_all(int num_cus) {
     int ok = nmoe_fused_fits<BITS, ROUTE, NMOE_XBF16>(num_cus) && nmoe_fused_fits<BITS, ROUTE, NMOE_XF32>(num_cus);
-    if constexpr (ROUTE != NMOE_ROUTE_GIVEN) ok = ok && nmoe_fused_fits<BITS, ROUTE, NMOE_XNORM>(num_cus);
+    if constexpr (ROUTE != NMOE_ROUTE_GIVEN)
+        ok = ok && nmoe_fused_fits<BITS, ROUTE, NMOE_XNORM>(num_cus) && nmoe_fused_fits<BITS, ROUTE, NMOE_XBLOCK>(num_cus);
     return ok;
 }
 
@@ -879,7 +1096,7 @@ extern "C" int nmoe_decode_init(nmoe_hip_ctx *ctx) {
     const int ok = nmoe_fused_resident(ctx->num_cus);
     ctx->fused_blocks = ok ? NMOE_FUSED_BLOCKS : 0;
     ctx->xcd_placed = 0;
-    ctx->xch_bytes = NMOE_FUSED_XCH_BYTES;
+    ctx->xch_bytes = NMOE_FUSED_XCH_BYTES_BLOCK;
     if (hipMalloc((void **)&ctx->xch, ctx->xch_bytes) != hipSuccess) return NMOE_HIP_ENOMEM;
     if (ok) { /* the probe writes into the exchange buffer, cleared afterwards */
         int r = nmoe_probe_xcd_placement((uint32_t *)ctx->xch, &ctx->xcd_placed);
@@ -895,7 +1112,10 @@ template <int BITS, int ROUTE>
 static hipError_t nmoe_fused_launch_x(int xmode, const nmoe_fused_args &a, hipStream_t s) {
     if (xmode == NMOE_XBF16) return nmoe_fused_launch<BITS, ROUTE, NMOE_XBF16>(a, s);
     if (xmode == NMOE_XF32) return nmoe_fused_launch<BITS, ROUTE, NMOE_XF32>(a, s);
-    if constexpr (ROUTE != NMOE_ROUTE_GIVEN) return nmoe_fused_launch<BITS, ROUTE, NMOE_XNORM>(a, s);
+    if constexpr (ROUTE != NMOE_ROUTE_GIVEN) {
+        if (xmode == NMOE_XNORM) return nmoe_fused_launch<BITS, ROUTE, NMOE_XNORM>(a, s);
+        if (xmode == NMOE_XBLOCK) return nmoe_fused_launch<BITS, ROUTE, NMOE_XBLOCK>(a, s);
+    }
     return hipErrorInvalidValue;
 }
 
@@ -905,14 +1125,24 @@ static hipError_t nmoe_fused_launch_x(int xmode, const nmoe_fused_args &a, hipSt
  * launch epoch (the caller never repeats one while words of an earlier
  * launch with it may remain).  route != 0: routing computed from `router`
  * (bf16 or q4); else given by idx_in / w_in.  xmode: NMOE_XF32 / NMOE_XBF16
- * / NMOE_XNORM. */
+ * / NMOE_XNORM / NMOE_XBLOCK (blk: its norm weights, next-layer norm and
+ * shared expert; xch then NMOE_FUSED_XCH_BYTES_BLOCK). */
 extern "C" hipError_t nmoe_fused_launch_core(int bits, int route, const void *x, int xmode, float eps, int k,
                                              const nmoe_hip_router *router, const uint32_t *idx_in, const float *w_in,
                                              const float *h_mid, const float *shared_out, const float *shared_gate_raw,
                                              float *out, uint32_t *idx_out, float *w_out, float *logits_out,
                                              const uint8_t *pack, uint64_t *xch, uint32_t *sync, int xcd_local,
-                                             uint32_t spin, uint32_t epoch, hipStream_t s) {
+                                             uint32_t spin, uint32_t epoch, const nmoe_block_ext *blk,
+                                             hipStream_t s) {
     nmoe_fused_args a;
+    memset(&a, 0, sizeof(a));
+    if (blk != NULL) {
+        a.norm_w = blk->norm_w;
+        a.next_w = blk->next_w;
+        a.add_one = blk->add_one;
+        a.next_x = blk->next_x;
+        a.sh = blk->sh;
+    }
     a.pack = pack;
     const bool q4r = router != NULL && router->kind == NMOE_HIP_ROUTER_Q4;
     a.router_w = router != NULL && !q4r ? router->w_bf16 : NULL;
@@ -956,7 +1186,20 @@ extern "C" int nmoe_fused_decode(nmoe_hip_ctx *ctx, int bits, int route, const v
                                  hipStream_t s) {
     const hipError_t e = nmoe_fused_launch_core(bits, route, x, xmode, eps, k, router, idx_in, w_in, h_mid, shared_out,
                                                 shared_gate_raw, out, idx_out, w_out, logits_out, pack, ctx->xch,
-                                                ctx->sync, ctx->use_xcd_local, ctx->spin_limit, 0u, s);
+                                                ctx->sync, ctx->use_xcd_local, ctx->spin_limit, 0u, NULL, s);
     if (e != hipSuccess) return nmoe_hip_check(ctx, e, "fused decode launch");
+    return NMOE_HIP_OK;
+}
+
+/* The whole MoE half of one token's layer in one launch (XBLOCK): the
+ * weighted RMSNorm of h_mid, routing, the shared expert, the experts, the
+ * combine into out (which may alias h_mid) and the next layer's norm. */
+extern "C" int nmoe_fused_block(nmoe_hip_ctx *ctx, int bits, const nmoe_hip_router *router, const float *h_mid,
+                                float eps, int k, const nmoe_block_ext *blk, float *out, uint32_t *idx_out,
+                                float *w_out, float *logits_out, const uint8_t *pack, hipStream_t s) {
+    const hipError_t e = nmoe_fused_launch_core(bits, 1, h_mid, NMOE_XBLOCK, eps, k, router, NULL, NULL, h_mid, NULL, NULL,
+                                                out, idx_out, w_out, logits_out, pack, ctx->xch, ctx->sync,
+                                                ctx->use_xcd_local, ctx->spin_limit, 0u, blk, s);
+    if (e != hipSuccess) return nmoe_hip_check(ctx, e, "fused block launch");
     return NMOE_HIP_OK;
 }

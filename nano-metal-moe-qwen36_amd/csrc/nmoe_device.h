@@ -500,6 +500,45 @@ __device__ __forceinline__ void nmoe_dd_add(double &s, double &c, double s2, dou
     c = c + c2 + e;
 }
 
+/* The double-double sum (S, C) of the wavefront's (s, c) pairs, in a fixed
+ * order (rows of 16 lanes by DPP, then the four rows in order); uniform. */
+__device__ __forceinline__ void nmoe_wave_dd_sum(double s, double c, double &S, double &C) {
+    nmoe_dd_add(s, c, nmoe_dpp_d<NMOE_DPP_XOR1>(s), nmoe_dpp_d<NMOE_DPP_XOR1>(c));
+    nmoe_dd_add(s, c, nmoe_dpp_d<NMOE_DPP_XOR2>(s), nmoe_dpp_d<NMOE_DPP_XOR2>(c));
+    nmoe_dd_add(s, c, nmoe_dpp_d<NMOE_DPP_HALF_MIRROR>(s), nmoe_dpp_d<NMOE_DPP_HALF_MIRROR>(c));
+    nmoe_dd_add(s, c, nmoe_dpp_d<NMOE_DPP_MIRROR>(s), nmoe_dpp_d<NMOE_DPP_MIRROR>(c));
+    S = nmoe_readlane_d(s, 0);
+    C = nmoe_readlane_d(c, 0);
+    nmoe_dd_add(S, C, nmoe_readlane_d(s, 16), nmoe_readlane_d(c, 16));
+    nmoe_dd_add(S, C, nmoe_readlane_d(s, 32), nmoe_readlane_d(c, 32));
+    nmoe_dd_add(S, C, nmoe_readlane_d(s, 48), nmoe_readlane_d(c, 48));
+}
+
+/* math.m:46-52's mean square as a float, from the sum of the 2048 squares
+ * as a double-double S + C (exact to far below 2^-90 relative): math.m sums
+ * them in an x87 long double (64-bit significand), within 2^-53 relative of
+ * the exact sum, so when no float rounding midpoint lies within 2^-51 of the
+ * exact mean, both round to the same float.  Returns that float, or -1 when
+ * the caller must replay the x87 sum (a near-midpoint, or tiny values). */
+__device__ __forceinline__ float nmoe_dd_mean_float(double S, double Cc) {
+    double hi, lo;
+    nmoe_two_sum(S, Cc, hi, lo);
+    hi *= 1.0 / 2048.0; /* exact */
+    lo *= 1.0 / 2048.0;
+    const float f = (float)hi;
+    const uint32_t fb = __float_as_uint(f);
+    int fast = 0;
+    if (hi == 0.0 && lo == 0.0) {
+        fast = 1;
+    } else if (fb >= 0x00800000u && fb < 0x7f000000u) {
+        const double up = ((double)f + (double)__uint_as_float(fb + 1u)) * 0.5;
+        const double dn = ((double)f + (double)__uint_as_float(fb - 1u)) * 0.5;
+        const double margin = hi * 0x1p-51;
+        fast = ((up - hi) - lo) > margin && ((hi - dn) + lo) > margin;
+    }
+    return fast ? f : -1.0f;
+}
+
 /* rms of math.m:34-65 (unit weight) over the 2048 fp32 values h, by a whole
  * block of 256 or more threads (threads 0..255 hold the data, the rest
  * only take part in the barriers); uniform result.  math.m sums the squares in an x87
@@ -527,16 +566,10 @@ __device__ float nmoe_block_rms_exact(const float *h, float eps, float *lds_h, d
         nmoe_two_sum(s, q, s, e);
         c += e;
     }
-    nmoe_dd_add(s, c, nmoe_dpp_d<NMOE_DPP_XOR1>(s), nmoe_dpp_d<NMOE_DPP_XOR1>(c));
-    nmoe_dd_add(s, c, nmoe_dpp_d<NMOE_DPP_XOR2>(s), nmoe_dpp_d<NMOE_DPP_XOR2>(c));
-    nmoe_dd_add(s, c, nmoe_dpp_d<NMOE_DPP_HALF_MIRROR>(s), nmoe_dpp_d<NMOE_DPP_HALF_MIRROR>(c));
-    nmoe_dd_add(s, c, nmoe_dpp_d<NMOE_DPP_MIRROR>(s), nmoe_dpp_d<NMOE_DPP_MIRROR>(c));
     /* cross-row combination with every lane active (reading other lanes
      * from inside a lane-divergent branch would read undefined values) */
-    double ws = nmoe_readlane_d(s, 0), wc = nmoe_readlane_d(c, 0);
-    nmoe_dd_add(ws, wc, nmoe_readlane_d(s, 16), nmoe_readlane_d(c, 16));
-    nmoe_dd_add(ws, wc, nmoe_readlane_d(s, 32), nmoe_readlane_d(c, 32));
-    nmoe_dd_add(ws, wc, nmoe_readlane_d(s, 48), nmoe_readlane_d(c, 48));
+    double ws, wc;
+    nmoe_wave_dd_sum(s, c, ws, wc);
     if (lane == 0 && holds) {
         lds_dd[2 * wave] = ws;
         lds_dd[2 * wave + 1] = wc;
@@ -545,22 +578,7 @@ __device__ float nmoe_block_rms_exact(const float *h, float eps, float *lds_h, d
     if (tid == 0) {
         double S = lds_dd[0], Cc = lds_dd[1];
         for (int w = 1; w < 4; w++) nmoe_dd_add(S, Cc, lds_dd[2 * w], lds_dd[2 * w + 1]);
-        double hi, lo;
-        nmoe_two_sum(S, Cc, hi, lo);
-        hi *= 1.0 / 2048.0; /* exact */
-        lo *= 1.0 / 2048.0;
-        float f = (float)hi;
-        uint32_t fb = __float_as_uint(f);
-        int fast = 0;
-        if (hi == 0.0 && lo == 0.0) {
-            fast = 1;
-        } else if (fb >= 0x00800000u && fb < 0x7f000000u) {
-            double up = ((double)f + (double)__uint_as_float(fb + 1u)) * 0.5;
-            double dn = ((double)f + (double)__uint_as_float(fb - 1u)) * 0.5;
-            double margin = hi * 0x1p-51;
-            fast = ((up - hi) - lo) > margin && ((hi - dn) + lo) > margin;
-        }
-        lds_f[0] = fast ? f : -1.0f;
+        lds_f[0] = nmoe_dd_mean_float(S, Cc);
     }
     __syncthreads();
     float mean = lds_f[0];

@@ -50,8 +50,20 @@ struct nmoe_layout<2> {
 #define NMOE_SYNC_EPOCH(b) (64 + 16 * (b))     /* per-block launch epochs, 64 bytes apart */
 #define NMOE_SYNC_DISPATCH 4352                /* arrival counter of the dispatch blocks */
 #define NMOE_SYNC_BLOCKS 256
-/* The fused launch's exchange words (tagged logits, act and partial y). */
+/* The fused launch's exchange words (tagged logits, act and partial y),
+ * and with the whole-block form's shared activations and next-norm sums. */
 #define NMOE_FUSED_XCH_BYTES 409600u
+#define NMOE_FUSED_XCH_BYTES_BLOCK 460800u
+
+/* The whole-block parts of a fused launch (XBLOCK): norm weights, the
+ * next-layer norm output and the shared expert. */
+struct nmoe_block_ext {
+    const uint16_t *norm_w;
+    const uint16_t *next_w;
+    int add_one;
+    float *next_x;
+    nmoe_hip_shared_expert sh; /* sh.gate.w == NULL: none */
+};
 
 struct nmoe_pack_slot {
     void *dev;
@@ -100,6 +112,9 @@ struct nmoe_hip_ctx {
     float *g_as;            /* [T*8][8] group sums of act */
     float *g_y;             /* [T*8][2048] per-entry expert outputs */
     float *s_act;           /* [T][512] shared-expert activations */
+    /* the MoE blocks of the model weights loaded by nmoe_hip_load_model_weights */
+    nmoe_hip_moe_block blocks[NMOE_HIP_MAX_LAYERS];
+    unsigned char block_set[NMOE_HIP_MAX_LAYERS];
     char err[256];
 };
 

@@ -23,172 +23,7 @@
 
 int nmoe_host_fail(nmoe_hip_ctx *ctx, int code, const char *msg);
 
-/* ------------------------------------------------------------ JSON */
-
-enum { J_NULL, J_BOOL, J_NUM, J_STR, J_ARR, J_OBJ };
-
-typedef struct jv {
-    int type;
-    double num;
-    char *str;           /* J_STR: value; object members: key */
-    struct jv *kids;     /* J_ARR / J_OBJ: children (objects: each child's str_key set) */
-    char **keys;         /* J_OBJ: member keys, parallel to kids */
-    int n;
-} jv;
-
-typedef struct {
-    const char *p, *end;
-    int depth;
-} jparser;
-
-static void jv_free(jv *v) {
-    if (v == NULL) return;
-    free(v->str);
-    for (int i = 0; i < v->n; i++) {
-        jv_free(&v->kids[i]);
-        if (v->keys != NULL) free(v->keys[i]);
-    }
-    free(v->kids);
-    free(v->keys);
-}
-
-static void jskip(jparser *ps) {
-    while (ps->p < ps->end && isspace((unsigned char)*ps->p)) ps->p++;
-}
-
-static int jparse(jparser *ps, jv *out);
-
-static int jstring(jparser *ps, char **out) {
-    if (ps->p >= ps->end || *ps->p != '"') return -1;
-    ps->p++;
-    size_t cap = 16, len = 0;
-    char *s = (char *)malloc(cap);
-    if (s == NULL) return -1;
-    while (ps->p < ps->end && *ps->p != '"') {
-        char c = *ps->p++;
-        if (c == '\\') {
-            if (ps->p >= ps->end) break;
-            char e = *ps->p++;
-            c = e == 'n' ? '\n' : e == 't' ? '\t' : e == 'r' ? '\r' : e == 'b' ? '\b' : e == 'f' ? '\f' : e;
-            if (e == 'u') { /* the layout uses ASCII only: keep \uXXXX as '?' */
-                if (ps->end - ps->p < 4) break;
-                ps->p += 4;
-                c = '?';
-            }
-        }
-        if (len + 2 > cap) {
-            char *t = (char *)realloc(s, cap *= 2);
-            if (t == NULL) {
-                free(s);
-                return -1;
-            }
-            s = t;
-        }
-        s[len++] = c;
-    }
-    if (ps->p >= ps->end) {
-        free(s);
-        return -1;
-    }
-    ps->p++; /* closing quote */
-    s[len] = 0;
-    *out = s;
-    return 0;
-}
-
-static int jpush(jv *v, jv *kid, char *key) {
-    jv *k2 = (jv *)realloc(v->kids, sizeof(jv) * (size_t)(v->n + 1));
-    if (k2 == NULL) return -1;
-    v->kids = k2;
-    if (v->type == J_OBJ) {
-        char **kk = (char **)realloc(v->keys, sizeof(char *) * (size_t)(v->n + 1));
-        if (kk == NULL) return -1;
-        v->keys = kk;
-        v->keys[v->n] = key;
-    }
-    v->kids[v->n++] = *kid;
-    return 0;
-}
-
-static int jparse(jparser *ps, jv *out) {
-    memset(out, 0, sizeof(*out));
-    if (++ps->depth > 32) return -1;
-    jskip(ps);
-    if (ps->p >= ps->end) return -1;
-    char c = *ps->p;
-    int rc = 0;
-    if (c == '{' || c == '[') {
-        out->type = c == '{' ? J_OBJ : J_ARR;
-        ps->p++;
-        jskip(ps);
-        if (ps->p < ps->end && *ps->p == (c == '{' ? '}' : ']')) {
-            ps->p++;
-        } else {
-            for (;;) {
-                char *key = NULL;
-                jskip(ps);
-                if (out->type == J_OBJ) {
-                    if (jstring(ps, &key) != 0) return -1;
-                    jskip(ps);
-                    if (ps->p >= ps->end || *ps->p != ':') {
-                        free(key);
-                        return -1;
-                    }
-                    ps->p++;
-                }
-                jv kid;
-                if (jparse(ps, &kid) != 0 || jpush(out, &kid, key) != 0) {
-                    jv_free(&kid);
-                    free(key);
-                    return -1;
-                }
-                jskip(ps);
-                if (ps->p < ps->end && *ps->p == ',') {
-                    ps->p++;
-                    continue;
-                }
-                if (ps->p < ps->end && *ps->p == (out->type == J_OBJ ? '}' : ']')) {
-                    ps->p++;
-                    break;
-                }
-                return -1;
-            }
-        }
-    } else if (c == '"') {
-        out->type = J_STR;
-        rc = jstring(ps, &out->str);
-    } else if (c == '-' || isdigit((unsigned char)c)) {
-        char *e = NULL;
-        out->type = J_NUM;
-        out->num = strtod(ps->p, &e);
-        if (e == ps->p || e > ps->end) return -1;
-        ps->p = e;
-    } else if (ps->end - ps->p >= 4 && strncmp(ps->p, "true", 4) == 0) {
-        out->type = J_BOOL, out->num = 1, ps->p += 4;
-    } else if (ps->end - ps->p >= 5 && strncmp(ps->p, "false", 5) == 0) {
-        out->type = J_BOOL, ps->p += 5;
-    } else if (ps->end - ps->p >= 4 && strncmp(ps->p, "null", 4) == 0) {
-        out->type = J_NULL, ps->p += 4;
-    } else {
-        return -1;
-    }
-    ps->depth--;
-    return rc;
-}
-
-static const jv *jget(const jv *o, const char *key) {
-    if (o == NULL || o->type != J_OBJ) return NULL;
-    for (int i = 0; i < o->n; i++)
-        if (strcmp(o->keys[i], key) == 0) return &o->kids[i];
-    return NULL;
-}
-
-static int jint(const jv *v, unsigned long long *out) {
-    if (v == NULL || v->type != J_NUM || v->num < 0 || v->num > 9.0e15 || v->num != (double)(unsigned long long)v->num)
-        return -1;
-    *out = (unsigned long long)v->num;
-    return 0;
-}
+#include "json.h"
 
 /* ------------------------------------------------------------ the layout */
 
@@ -250,10 +85,7 @@ int nmoe_hip_validate_layout(const char *path, int *bits_out, int *num_layers_ou
     memset(&root, 0, sizeof(root));
     int rc = NMOE_HIP_OK;
     if (toolong) LFAIL("layout file larger than 1 MiB");
-    jparser ps = {text, text + len, 0};
-    if (jparse(&ps, &root) != 0) LFAIL("layout is not valid JSON");
-    jskip(&ps);
-    if (ps.p != ps.end) LFAIL("trailing characters after the layout object");
+    if (jparse_text(text, len, &root) != 0) LFAIL("layout is not valid JSON (or has trailing characters)");
     if (root.type != J_OBJ) LFAIL("layout must be a JSON object");
 
     const jv *qv = jget(&root, "bits");

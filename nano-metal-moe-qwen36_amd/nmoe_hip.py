@@ -83,6 +83,12 @@ class SharedExpert(C.Structure):
     _fields_ = [("gate", QTensor), ("up", QTensor), ("down", QTensor), ("score", QTensor)]
 
 
+class MoeBlock(C.Structure):
+    """nmoe_hip_moe_block: one layer's MoE half (router, shared expert, norms)."""
+    _fields_ = [("router", Router), ("has_shared", C.c_int), ("shared", SharedExpert), ("post_norm", C.c_void_p),
+                ("next_norm", C.c_void_p), ("add_one", C.c_int), ("eps", C.c_float)]
+
+
 _lib = None
 
 _P = C.c_void_p
@@ -121,6 +127,9 @@ _SIGS = {
     "nmoe_moe_shared_expert": (_I, [_P, C.POINTER(SharedExpert), _P, _I, _I, _P, _P, _P]),
     "nmoe_hip_validate_layout": (_I, [C.c_char_p, C.POINTER(_I), C.POINTER(_I), C.c_char_p, C.c_size_t]),
     "nmoe_hip_load_expert_dir": (_I, [_P, C.c_char_p, _I, C.POINTER(_I), C.POINTER(_I)]),
+    "nmoe_moe_block": (_I, [_P, _I, C.POINTER(MoeBlock), _P, _I, _P, _P, _P, _P, _P, _P]),
+    "nmoe_hip_load_model_weights": (_I, [_P, C.c_char_p, C.c_char_p, _I, C.POINTER(_I)]),
+    "nmoe_hip_layer_block": (_I, [_P, _I, C.POINTER(MoeBlock)]),
 }
 
 
@@ -337,6 +346,23 @@ class Context:
                       stream=None) -> int:
         return lib().nmoe_moe_shared_expert(self.h, C.byref(se), _ptr(x), x_dtype, ntok, _ptr(shared_out),
                                             _ptr(shared_gate_raw), stream)
+
+    def moe_block(self, layer: int, blk: MoeBlock, h_mid, k: int, out, next_x=None, idx=None, w=None, logits=None,
+                  stream=None) -> int:
+        return lib().nmoe_moe_block(self.h, layer, C.byref(blk), _ptr(h_mid), k, _ptr(out), _ptr(next_x), _ptr(idx),
+                                    _ptr(w), _ptr(logits), stream)
+
+    def load_model_weights(self, bin_path: str, json_path: str, nlayers: int = 0) -> int:
+        """Makes the MoE-path tensors of model_weights.bin resident; returns the layer count."""
+        n = C.c_int(0)
+        self._check(lib().nmoe_hip_load_model_weights(self.h, bin_path.encode(), json_path.encode(), nlayers,
+                                                      C.byref(n)))
+        return n.value
+
+    def layer_block(self, layer: int) -> MoeBlock:
+        b = MoeBlock()
+        self._check(lib().nmoe_hip_layer_block(self.h, layer, C.byref(b)))
+        return b
 
     def dequant_rows(self, bits: int, packed, scales, biases, rows: int, in_dim: int, out, stream=None) -> int:
         return lib().nmoe_dequant_rows(self.h, bits, _ptr(packed), _ptr(scales), _ptr(biases), rows, in_dim,

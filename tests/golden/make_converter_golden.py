@@ -1,5 +1,6 @@
 """Writes tests/golden/converter_golden.npz: input/output vectors of the
-reference converter's quantiser and packers.
+reference converter's quantiser and packers; and model_weights_mini.json /
+.sha256: what its model-weights writer makes of a two-layer mini model.
 
 The writer side of the expert-pack format is scripts/convert_qwen36.py's
 quantize_rows_bf16 / quantize_rows_bf16_2bit / pack_4bit / pack_2bit
@@ -93,6 +94,31 @@ def main():
                pack2_codes=codes2, pack2_words=cq.pack_2bit(codes2).astype(np.uint32))
     np.savez_compressed(OUT, **out)
     print(f"wrote {OUT}: {len(out)} arrays, {os.path.getsize(OUT)} bytes")
+    weights_golden(cq)
+
+
+def weights_golden(cq):
+    """The converter's export_model_weights (convert_qwen36.py:266-327) on
+    the two-layer mini model of model_weights_recipe.py: its manifest is
+    committed as is, its bin by SHA-256 (the tests rebuild the bytes)."""
+    import shutil
+    import tempfile
+    from pathlib import Path
+
+    sys.path.insert(0, HERE)
+    import model_weights_recipe as R
+
+    with tempfile.TemporaryDirectory() as tmp:
+        src, dst = Path(tmp) / "model", Path(tmp) / "out"
+        src.mkdir()
+        dst.mkdir()
+        R.write_safetensors(str(src / "model-00001-of-00001.safetensors"), R.tensors())
+        cq.export_model_weights(cq.scan_model(src), dst, 4096)
+        shutil.copyfile(dst / "model_weights.json", os.path.join(HERE, "model_weights_mini.json"))
+        digest, size = R.sha256(str(dst / "model_weights.bin")), os.path.getsize(dst / "model_weights.bin")
+    with open(os.path.join(HERE, "model_weights_mini.sha256"), "w") as f:
+        f.write(f"{digest} {size}\n")
+    print(f"wrote model_weights_mini.json and .sha256 ({size} bytes of bin)")
 
 
 if __name__ == "__main__":

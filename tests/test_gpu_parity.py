@@ -912,3 +912,100 @@ def test_converter_packs_on_device(ctx, nh, bits):
                            ctx.to_device(h), out))
     assert ctx.device_status() == nh.OK
     assert_close(out.download(np.float32, (1, 2048)), want, what=f"converter-quantised q{bits} layer")
+
+
+def _mini_weights(tmp_path):
+    import json
+    import shutil
+    import sys
+    import os
+    gold = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+    sys.path.insert(0, gold)
+    import model_weights_recipe as R
+    bin_path, json_path = str(tmp_path / "model_weights.bin"), str(tmp_path / "model_weights.json")
+    R.write_model_weights(bin_path)
+    shutil.copyfile(os.path.join(gold, "model_weights_mini.json"), json_path)
+    return R, bin_path, json_path
+
+
+@pytest.mark.parametrize("bits,k", [(4, 8), (2, 6)])
+def test_moe_block_from_model_weights(ctx, nh, tmp_path, bits, k):
+    """f1/f3: the model's per-layer MoE half in one launch (nmoe_moe_block)
+    with the tensors nmoe_hip_load_model_weights made resident from a
+    converter-format model_weights.bin: weighted post-attention RMSNorm, q4
+    router, shared expert, experts, combine and the next layer's weighted
+    input norm, against the whole-block oracle (orc_moe_block, the
+    reference's order runtime.m:3144-3201, 2908-2999, 2893-2900): routing
+    bit-exact, out and next_x within tolerance; the in-place form (out over
+    h_mid) gives the same bits."""
+    R, bin_path, json_path = _mini_weights(tmp_path)
+    assert ctx.load_model_weights(bin_path, json_path, 2) == 2
+    rng = np.random.default_rng(500 + bits)
+    seed = 71
+    for l in range(2):
+        layer = 60 + l
+        ctx.synth_layer(layer, bits, seed, SIGMA[bits])
+        blk = ctx.layer_block(l)
+        assert blk.has_shared == 1 and blk.add_one == 1 and abs(blk.eps - 1e-6) < 1e-12
+        assert (blk.next_norm is None) == (l == 1)
+        h = (rng.standard_normal(2048) * 2.0).astype(np.float32)
+        dh, out, nx, di, dw = ctx.to_device(h), ctx.alloc(8192), ctx.alloc(8192), ctx.alloc(32), ctx.alloc(32)
+        ctx._check(ctx.moe_block(layer, blk, dh, k, out, nx, di, dw))
+        assert ctx.device_status() == nh.OK
+        got_out, got_nx = out.download(np.float32, 2048), nx.download(np.float32, 2048)
+        gi, gw = di.download(np.uint32, 8), dw.download(np.float32, 8)
+        host = R.layer_host(l)
+        next_norm = R.layer_host(l + 1)["input_norm"] if l == 0 else None
+        pack = host_pack(bits, seed, layer, gi[:k])
+        want, oi, ow, _, want_nx = B.moe_block(pack, bits, {"q4": host["router"]}, h, k, post_norm=host["post_norm"],
+                                               add_one=1, shared=host["shared"], next_norm=next_norm, want_next=True)
+        np.testing.assert_array_equal(gi, oi, err_msg=f"layer {l}")
+        np.testing.assert_array_equal(gw.view(np.uint32), ow.view(np.uint32), err_msg=f"layer {l}")
+        assert_close(got_out, want, what=f"block q{bits} layer {l} out")
+        assert_close(got_nx, want_nx, what=f"block q{bits} layer {l} next_x")
+        # in place: out over h_mid
+        ctx._check(ctx.moe_block(layer, blk, dh, k, dh, nx))
+        np.testing.assert_array_equal(dh.download(np.float32, 2048).view(np.uint32), got_out.view(np.uint32))
+
+
+def test_moe_block_plain_equals_layer_rmsnorm(ctx, nh):
+    """With unit norms, no shared expert and no next norm the block is the
+    layer with its input RMSNorm: the same bits as nmoe_moe_layer_rmsnorm."""
+    seed, layer, k = 73, 62, 8
+    ctx.synth_layer(layer, 4, seed, 0.02)
+    W = ctx.to_device(B.syn_bf16(256 * 2048, seed, layer, 16, 0.02))
+    blk = nh.MoeBlock()
+    blk.router = ctx.router_bf16(W)
+    blk.eps = 1e-6
+    h = (np.random.default_rng(5).standard_normal(2048) * 1.5).astype(np.float32)
+    dh, o1, o2 = ctx.to_device(h), ctx.alloc(8192), ctx.alloc(8192)
+    ctx._check(ctx.moe_block(layer, blk, dh, k, o1))
+    ctx._check(ctx.moe_layer_rmsnorm(layer, ctx.router_bf16(W), dh, 1e-6, k, o2))
+    assert ctx.device_status() == nh.OK
+    np.testing.assert_array_equal(o1.download(np.float32, 2048).view(np.uint32),
+                                  o2.download(np.float32, 2048).view(np.uint32))
+
+
+def test_load_model_weights_rejects(ctx, nh, tmp_path):
+    """Missing layers, a wrong dtype, a truncated file and broken JSON are
+    refused with the reference's categories (runtime.m:2278-2297)."""
+    import json
+    R, bin_path, json_path = _mini_weights(tmp_path)
+    lib = nh.lib()
+    n = __import__("ctypes").c_int(0)
+    # config.num_hidden_layers is 40, the file holds 2
+    assert lib.nmoe_hip_load_model_weights(ctx.h, bin_path.encode(), json_path.encode(), 0, None) == nh.ENOENT
+    assert "model.layers.2." in ctx.last_error()
+    m = json.load(open(json_path))
+    m["tensors"]["model.layers.1.mlp.gate.scales"]["dtype"] = "F32"
+    bad = str(tmp_path / "bad.json")
+    json.dump(m, open(bad, "w"))
+    assert lib.nmoe_hip_load_model_weights(ctx.h, bin_path.encode(), bad.encode(), 2, None) == nh.EINVAL
+    with open(bad, "w") as f:
+        f.write("{\"tensors\": {")
+    assert lib.nmoe_hip_load_model_weights(ctx.h, bin_path.encode(), bad.encode(), 2, None) == nh.EINVAL
+    short = str(tmp_path / "short.bin")
+    with open(bin_path, "rb") as f, open(short, "wb") as g:
+        g.write(f.read(1 << 20))
+    assert lib.nmoe_hip_load_model_weights(ctx.h, short.encode(), json_path.encode(), 2, None) == nh.EIO
+    del n
