@@ -403,6 +403,36 @@ def run_grouped(pool, args, workload: str, NLg: int = 8) -> dict:
     }
 
 
+def run_stream(pool, args) -> dict:
+    """The streaming ceiling of the c1 step: nmoe_hip_read_probe over the
+    bytes of 8 q4 experts (14,155,776 B), all loads in flight at once, one
+    launch per step, rotating over the 40 layers (no reuse within 18 GB)."""
+    ctx, stream = pool.ctx, pool.ctx.stream
+    nbytes = 8 * EXPERT_BYTES[args.bits]
+    sink = ctx.alloc(2048 * 4, "stream.sink")
+    packs = [ctx.layer_pack_ptr(l) for l in range(pool.NL)]
+
+    def step(i):
+        ctx._check(ctx.read_probe(packs[i % pool.NL] + ((i // pool.NL) % 8) * nbytes, nbytes, sink, stream=stream))
+
+    for i in range(args.warmup):
+        step(i)
+    ctx.sync()
+    ev = HipEvents()
+    e0, e1 = ev.create(2)
+    ev.record(e0, stream)
+    for i in range(args.steps):
+        step(args.warmup + i)
+    ev.record(e1, stream)
+    ms = ev.ms(e0, e1) / args.steps
+    ctx.sync()
+    ev.destroy([e0, e1])
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {"metric": "streaming ceiling of the c1 step's expert bytes (read probe, 1 GPU)", "value": round(gbs, 1),
+            "unit": "GB/s", "us_per_launch": round(ms * 1e3, 3), "bytes": nbytes, "steps": args.steps,
+            "frac": round(gbs / HBM_PEAK_GBS, 4), "config": {"workload": "stream", "entry_point": "nmoe_hip_read_probe"}}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -414,15 +444,16 @@ def main():
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--cpu-steps", type=int, default=630)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--no-extra", action="store_true", help="c1 only: no c3 / c5 sub-objects")
+    ap.add_argument("--no-extra", action="store_true", help="c1 only: no c3 / c5 / stream sub-objects")
     ap.add_argument("--copy-calib", type=int, default=0, metavar="MIB",
                     help="only run 5 device-to-device copies of MIB MiB (counter calibration) and exit")
     ap.add_argument("--router", default="bf16", choices=("bf16", "q4"),
                     help="c1/c3: the benchmark configs' dense bf16 router (default) or the model's q4 router")
-    ap.add_argument("--workload", default="c1", choices=("c1", "c3", "c4", "c5"),
+    ap.add_argument("--workload", default="c1", choices=("c1", "c3", "c4", "c5", "stream"),
                     help="c1: the headline single-layer decode step, with c3 and c5 sub-objects (default); "
                          "c3 / c4 / c5 alone: 40-layer stack of 128 tokens / batched decode of 64 Zipf-routed "
-                         "tokens / 2048-token prefill on the grouped matrix-core path")
+                         "tokens / 2048-token prefill on the grouped matrix-core path; stream: the streaming ceiling "
+                         "of the c1 step's expert bytes (nmoe_hip_read_probe)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -447,6 +478,8 @@ def main():
     pool = Pool(nh, args, max_tokens=2048 if grouped else 8)
     if args.workload == "c3":
         result = run_c3(pool, args)
+    elif args.workload == "stream":
+        result = run_stream(pool, args)
     elif args.workload in ("c4", "c5"):
         result = run_grouped(pool, args, args.workload)
     else:
@@ -455,6 +488,7 @@ def main():
             print("[bench] c3 and c5 sub-benchmarks ...", file=sys.stderr, flush=True)
             result["c3"] = run_c3(pool, args)
             result["c5"] = run_grouped(pool, args, "c5")
+            result["stream"] = run_stream(pool, args)
         if not args.no_cpu:
             print("[bench] cpu baseline ...", file=sys.stderr, flush=True)
             result["cpu_baseline"] = cpu_baseline(args.bits, args.k, args.seed, args.cpu_steps)

@@ -347,6 +347,16 @@ NMOE_HIP_API int nmoe_moe_layer_static(const void *layer_pack, int bits, const n
                                        const float *shared_out, const float *shared_gate_raw, float *out,
                                        uint32_t *idx, float *w, void *stream);
 
+/* ---- the streaming ceiling of the decode step (a measurement entry point;
+ * no reference counterpart, like the reference's matvec micro-benchmark
+ * scripts/matvec_bench.m): reads `bytes` (a multiple of 16, at most 16 MiB)
+ * from src once, with the fused step's expert-load pattern (256 blocks, all
+ * of a block's 16-byte non-temporal loads in flight before any is used),
+ * folding them into sink[2048] words.  Its launch time is the floor of the
+ * step's expert phase: the step's expert bytes streamed from a cold start
+ * with no routing before and no exchange after. */
+NMOE_HIP_API int nmoe_hip_read_probe(nmoe_hip_ctx *ctx, const void *src, size_t bytes, uint32_t *sink, void *stream);
+
 /* ---- bit-exact dequant probe (kernels.metal:1066-1106 nmoe_dequant_row_q4/q2,
  * math.m:206-234): out[r][c] = q*scale + bias for `rows` rows of `in_dim`. */
 NMOE_HIP_API int nmoe_dequant_rows(nmoe_hip_ctx *ctx, int bits, const uint32_t *packed, const uint16_t *scales,
