@@ -292,6 +292,7 @@ def run_c3(pool, args, ntok: int = 128) -> dict:
     untimed tokens with their own inputs go first."""
     nh, ctx, bits, k, NL = pool.nh, pool.ctx, args.bits, args.k, pool.NL
     stream = ctx.stream
+    ctx._check(ctx.set_option(nh.OPT_STACK_LOOP, args.stack_loop))
     sets = pool.NR // NL
     layers = list(range(NL))
     row = (NL + 1) * 2048 * 4
@@ -328,7 +329,8 @@ def run_c3(pool, args, ntok: int = 128) -> dict:
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4)},
         "config": {"workload": "c3", "layers": NL, "bits": bits, "k": k, "bytes_per_token": B, "router": args.router,
-                   "routers_rotated": pool.NR, "entry_point": "nmoe_moe_stack"},
+                   "routers_rotated": pool.NR, "entry_point": "nmoe_moe_stack",
+                   "launches_per_token": -(-NL // 64) if args.stack_loop else NL},
     }
 
 
@@ -444,6 +446,8 @@ def main():
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--cpu-steps", type=int, default=630)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--stack-loop", type=int, default=1, choices=(0, 1),
+                    help="c3: the token's layers in one persistent launch (1, default) or one launch per layer (0)")
     ap.add_argument("--no-extra", action="store_true", help="c1 only: no c3 / c5 / stream sub-objects")
     ap.add_argument("--copy-calib", type=int, default=0, metavar="MIB",
                     help="only run 5 device-to-device copies of MIB MiB (counter calibration) and exit")

@@ -124,6 +124,12 @@ NMOE_HIP_API int nmoe_hip_check_device_status(nmoe_hip_ctx *ctx);
  * whose blocks are not all resident would.  nmoe_hip_check_device_status
  * then realigns the epochs.  Synchronous. */
 #define NMOE_HIP_OPT_SKEW_EPOCH 6
+/* NMOE_HIP_OPT_STACK_LOOP (default 1): nmoe_moe_stack runs the token's
+ * layers in one persistent launch (up to 64 layers per launch; the next
+ * layer's router row is fetched while the current one streams, and no
+ * launch boundary separates the layers) when all its packs have one bit
+ * width and all its routers one kind; 0 runs one launch per layer. */
+#define NMOE_HIP_OPT_STACK_LOOP 7
 NMOE_HIP_API int nmoe_hip_set_option(nmoe_hip_ctx *ctx, int option, int value);
 
 /* ---- buffers (backend.h:64-66: register_shared_buffer / register_state_buffer
@@ -320,8 +326,10 @@ NMOE_HIP_API int nmoe_hip_layer_block(const nmoe_hip_ctx *ctx, int layer, nmoe_h
  * NMOEProcessToken, runtime.m:3732-3777, restricted to the MoE tails):
  * h_seq[l+1] = h_seq[l] + MoE_l(RMSNorm(h_seq[l])) for l < nlayers.
  * layers[l]: resident pack of layer l; routers[l]: its router (bf16 or q4).
- * h_seq: fp32 [nlayers+1][2048] (row 0 = input); idx_seq / w_seq: nullable
- * [nlayers][8]. */
+ * h_seq: fp32 [nlayers+1][2048] (row 0 = input, 16-byte aligned);
+ * idx_seq / w_seq: nullable [nlayers][8].  One launch for all layers
+ * (NMOE_HIP_OPT_STACK_LOOP), else one per layer; the results are the
+ * same bits either way. */
 NMOE_HIP_API int nmoe_moe_stack(nmoe_hip_ctx *ctx, int nlayers, const int *layers, const nmoe_hip_router *routers,
                                 int k, float eps, float *h_seq, uint32_t *idx_seq, float *w_seq, void *stream);
 

@@ -43,6 +43,7 @@ extern "C" int nmoe_hip_create(int device, int max_tokens, nmoe_hip_ctx **out) {
     ctx->device = device;
     ctx->max_tokens = max_tokens;
     ctx->use_fused = 1;
+    ctx->stack_loop = 1;
     ctx->spin_limit = NMOE_SPIN_LIMIT;
     hipDeviceProp_t prop;
     if (hipGetDeviceProperties(&prop, device) != hipSuccess || hipStreamCreate(&ctx->stream) != hipSuccess) {
@@ -125,6 +126,10 @@ extern "C" int nmoe_hip_set_option(nmoe_hip_ctx *ctx, int option, int value) {
     }
     if (option == NMOE_HIP_OPT_SYNC_CHECK) {
         ctx->sync_check = value != 0;
+        return NMOE_HIP_OK;
+    }
+    if (option == NMOE_HIP_OPT_STACK_LOOP) {
+        ctx->stack_loop = value != 0;
         return NMOE_HIP_OK;
     }
     if (option == NMOE_HIP_OPT_SKEW_EPOCH) {

@@ -353,6 +353,53 @@ extern "C" int nmoe_layer_rmsnorm_launch(nmoe_hip_ctx *ctx, int layer, const nmo
                              nmoe_stream_of(ctx, stream));
 }
 
+extern "C" int nmoe_fused_stack(nmoe_hip_ctx *ctx, int bits, int q4r, int nl, const uint8_t *const *packs,
+                                const nmoe_hip_router *routers, float *h_seq, float eps, int k, uint32_t *idx_seq,
+                                float *w_seq, hipStream_t s);
+
+/* nmoe_moe_stack as persistent launches, each running up to 64 of the
+ * token's layers.  Checks every layer as nmoe_layer_rmsnorm_launch does
+ * (so both forms reject the same calls); returns 1, having launched
+ * nothing, when the layers do not share one bit width and one router kind
+ * or the option is off. */
+extern "C" int nmoe_stack_loop_launch(nmoe_hip_ctx *ctx, int nlayers, const int *layers,
+                                      const nmoe_hip_router *routers, int k, float eps, float *h_seq,
+                                      uint32_t *idx_seq, float *w_seq, void *stream) {
+    constexpr int CHUNK = 64;
+    if (ctx == NULL) return NMOE_HIP_EINVAL;
+    if (!ctx->stack_loop || ctx->fused_blocks == 0) return 1;
+    int bits = 0, q4r = 0;
+    for (int l = 0; l < nlayers; l++) {
+        const int layer = layers[l];
+        if (layer < 0 || layer >= NMOE_HIP_MAX_LAYERS || ctx->packs[layer].dev == NULL)
+            return nmoe_fail(ctx, NMOE_HIP_ENOENT, "layer %d has no resident pack", layer);
+        const int rc = nmoe_check_router(ctx, &routers[l]);
+        if (rc != NMOE_HIP_OK) return rc;
+        if (routers[l].num_experts != NMOE_EXPERTS)
+            return nmoe_fail(ctx, NMOE_HIP_EINVAL, "nmoe_moe_layer_rmsnorm needs a router of 256 experts");
+        const int q = routers[l].kind == NMOE_HIP_ROUTER_Q4;
+        if (l == 0) {
+            bits = ctx->packs[layer].bits;
+            q4r = q;
+        } else if (ctx->packs[layer].bits != bits || q != q4r) {
+            return 1;
+        }
+    }
+    if (k < 1 || k > NMOE_MAX_K) return nmoe_fail(ctx, NMOE_HIP_EINVAL, "k=%d outside 1..8", k);
+    if (!nmoe_aligned(h_seq, 16)) return nmoe_fail(ctx, NMOE_HIP_EINVAL, "h_in (16-byte aligned) and h_out are required");
+    const uint8_t *packs[CHUNK];
+    for (int c = 0; c < nlayers; c += CHUNK) {
+        const int n = nlayers - c < CHUNK ? nlayers - c : CHUNK;
+        for (int l = 0; l < n; l++) packs[l] = (const uint8_t *)ctx->packs[layers[c + l]].dev;
+        const int rc = nmoe_fused_stack(ctx, bits, q4r, n, packs, routers + c, h_seq + (size_t)c * NMOE_HIDDEN, eps, k,
+                                        idx_seq != NULL ? idx_seq + (size_t)c * NMOE_MAX_K : NULL,
+                                        w_seq != NULL ? w_seq + (size_t)c * NMOE_MAX_K : NULL,
+                                        nmoe_stream_of(ctx, stream));
+        if (rc != NMOE_HIP_OK) return rc;
+    }
+    return NMOE_HIP_OK;
+}
+
 extern "C" int nmoe_moe_layer_rmsnorm(nmoe_hip_ctx *ctx, int layer, const nmoe_hip_router *router,
                                       const float *h_in, float eps, int k, float *h_out, uint32_t *idx, float *w,
                                       float *logits, void *stream) {

@@ -91,6 +91,19 @@ static_assert(NMOE_XCH_WORDS * sizeof(uint64_t) == NMOE_FUSED_XCH_BYTES, "exchan
 #define NMOE_XCH_NOUT (NMOE_XCH_NSQ + NMOE_XCH_SP * NMOE_FUSED_GROUP_BLOCKS)
 #define NMOE_XCH_WORDS_BLOCK (NMOE_XCH_NOUT + NMOE_HIDDEN)
 static_assert(NMOE_XCH_WORDS_BLOCK * sizeof(uint64_t) == NMOE_FUSED_XCH_BYTES_BLOCK, "the whole-block exchange size");
+/* The stack form (XSTACK) routes within each die: per die and layer
+ * parity the 256 logits its 32 blocks compute (8 each, dense), per die
+ * the 2048 words of the next h its blocks gather followed by its 32
+ * blocks' sums of squares (a double as two words each), and a second set of
+ * partial-sum words (dies may run up to a layer apart once routing no
+ * longer crosses them; alternating by layer parity, no block overwrites a
+ * partial or a logit another block still waits for). */
+#define NMOE_XCH_LGD NMOE_XCH_WORDS_BLOCK
+#define NMOE_XCH_HG (NMOE_XCH_LGD + 2 * NMOE_FUSED_GROUPS * NMOE_EXPERTS)
+#define NMOE_XCH_HGS (NMOE_HIDDEN + 2 * NMOE_FUSED_GROUP_BLOCKS) /* a die's words */
+#define NMOE_XCH_YPART2 (NMOE_XCH_HG + NMOE_FUSED_GROUPS * NMOE_XCH_HGS)
+#define NMOE_XCH_WORDS_STACK (NMOE_XCH_YPART2 + NMOE_FUSED_GROUPS * NMOE_HIDDEN)
+static_assert(NMOE_XCH_WORDS_STACK * sizeof(uint64_t) == NMOE_FUSED_XCH_BYTES_STACK, "the stack exchange size");
 
 /* x sources: XF32 / XBF16 = activations given; XNORM = x is RMSNorm(h);
  * XBLOCK = the whole MoE half of a layer: x is the weighted RMSNorm of h,
@@ -99,6 +112,9 @@ static_assert(NMOE_XCH_WORDS_BLOCK * sizeof(uint64_t) == NMOE_FUSED_XCH_BYTES_BL
 #define NMOE_XBF16 1
 #define NMOE_XNORM 2
 #define NMOE_XBLOCK 3
+/* XSTACK: all layers of one token in one launch (per layer as XNORM:
+ * x_l = RMSNorm(h_l), h_{l+1} = h_l + MoE_l(x_l)) */
+#define NMOE_XSTACK 4
 
 /* ROUTE: routing given (idx_in / w_in), or computed from a bf16 or a q4 router */
 #define NMOE_ROUTE_GIVEN 0
@@ -134,6 +150,16 @@ struct nmoe_fused_args {
     int add_one;            /* the weights enter as 1 + w */
     float *next_x;          /* RMSNorm(out, next_w), or NULL */
     nmoe_hip_shared_expert sh; /* the shared expert (sh.gate.w == NULL: none) */
+    /* XSTACK: x = h_seq row 0, out = rows 1..nl, idx_out / w_out 8 per layer */
+    int nl;
+};
+
+/* XSTACK's layer table, passed by value (kernel arguments: no upload, no
+ * allocation): per layer the resident pack, the router words (bf16 rows or
+ * q4 words) and the q4 router's scales and biases. */
+#define NMOE_STACK_MAX_LAYERS 64
+struct nmoe_stack_tab {
+    const void *p[4 * NMOE_STACK_MAX_LAYERS];
 };
 
 /* Die-local exchange: words written and read only by blocks of one
@@ -283,7 +309,7 @@ __device__ __forceinline__ void nmoe_x_cols(const void *x, int c0, int n, double
         nmoe_load_cols<uint16_t>((const uint16_t *)x, c0, n, out);
     } else {
         nmoe_load_cols<float>((const float *)x, c0, n, out);
-        if (XMODE == NMOE_XNORM || XMODE == NMOE_XBLOCK)
+        if (XMODE == NMOE_XNORM || XMODE == NMOE_XBLOCK || XMODE == NMOE_XSTACK)
             for (int i = 0; i < n; i++) out[i] = (float)((double)out[i] * rinv);
     }
 }
@@ -312,7 +338,7 @@ __device__ __forceinline__ int nmoe_act_slot(int e) {
 }
 
 template <int BITS, int ROUTE, int XMODE>
-__global__ void __launch_bounds__(NMOE_FUSED_THREADS) nmoe_fused_decode_kernel(nmoe_fused_args a) {
+__device__ __forceinline__ void nmoe_fused_body(nmoe_fused_args a, const nmoe_stack_tab *stab) {
     using Q = nmoe_q<BITS>;
     using L = nmoe_layout<BITS>;
     constexpr int RPS = NMOE_WAVE / Q::LPR_G;   /* gate/up rows per wave step: 1 (q4) / 2 (q2) */
@@ -320,7 +346,8 @@ __global__ void __launch_bounds__(NMOE_FUSED_THREADS) nmoe_fused_decode_kernel(n
     constexpr int RPW_D = NMOE_WAVE / Q::LPR_D; /* down rows per wave step: 4 (q4) / 8 (q2) */
     constexpr int DSTEPS = NMOE_FUSED_CHUNK / NMOE_FUSED_WORKERS / RPW_D; /* down rows per worker, in steps */
     static_assert(GSTEPS >= 1 && DSTEPS >= 1, "rows split evenly over the worker wavefronts");
-    constexpr bool NORM = XMODE == NMOE_XNORM || XMODE == NMOE_XBLOCK; /* x = RMSNorm(h) in the block */
+    constexpr bool STK = XMODE == NMOE_XSTACK;
+    constexpr bool NORM = XMODE == NMOE_XNORM || XMODE == NMOE_XBLOCK || STK; /* x = RMSNorm(h) in the block */
     constexpr bool BLK = XMODE == NMOE_XBLOCK;
     __shared__ uint64_t s_tab[32];
     __shared__ float s_scratch[NMOE_EXPERTS];
@@ -345,18 +372,23 @@ __global__ void __launch_bounds__(NMOE_FUSED_THREADS) nmoe_fused_decode_kernel(n
     __shared__ float s_shd[BLK ? NMOE_FUSED_CHUNK : 1];
     __shared__ float s_shg[2], s_sgr[1];
     __shared__ uint32_t s_shok, s_sacnt;
+    /* XSTACK: h of this layer and the next (the gather of the next one
+     * never touches the rows the combine still reads), the layer's router
+     * rows 8j .. 8j+7 (fetched a layer ahead; bf16: 8 x 4 KB; q4: 8 x 1 KB
+     * of words, then 8 x 64 B of scales and of biases), the layer table */
+    __shared__ __align__(16) float s_hin[2][STK ? NMOE_HIDDEN : 4];
+    __shared__ __align__(16) uint32_t s_rrow[STK ? 8 * NMOE_HIDDEN / 2 : 4];
+    __shared__ const void *s_stk[STK ? 4 * NMOE_STACK_MAX_LAYERS : 1];
+    __shared__ double s_rinv; /* XSTACK: the next layer's 1 / rms, or -1 (the block computes it) */
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const bool ctrl = wave >= NMOE_FUSED_CTRL; /* either control wavefront */
     const bool cwave = wave == NMOE_FUSED_CTRL;
     const int g = blockIdx.x % NMOE_FUSED_GROUPS, j = blockIdx.x / NMOE_FUSED_GROUPS;
     const int k = a.k;
-    const bool comb = g == j % k;               /* this block combines rows 64j .. 64j+63 */
+    const bool comb = STK || g == j % k; /* this block combines rows 64j .. 64j+63 (XSTACK: each die does) */
     const bool has_sh = BLK && a.sh.gate.w != NULL;
     uint32_t *status = a.sync + NMOE_SYNC_STATUS;
-    uint64_t *xlg = a.xch + NMOE_XCH_LOGITS;
-    uint64_t *xact = a.xch + NMOE_XCH_ACT + NMOE_XCH_ASP * g * NMOE_INTER;
-    uint64_t *ypart = a.xch + NMOE_XCH_YPART;
 
     /* Independent loads go out first and unconditionally (loads retire in
      * order, so a later wait on one of them must not cover the big ones):
@@ -370,14 +402,14 @@ __global__ void __launch_bounds__(NMOE_FUSED_THREADS) nmoe_fused_decode_kernel(n
     /* XBLOCK may write out over h_mid: only the combining block reads the
      * rows it will overwrite (every block's reads of h end before its first
      * barrier, long before any block writes out) */
-    const float hm = !BLK || comb ? a.h_mid[crow] : 0.0f;
+    const float hm = STK ? 0.0f : !BLK || comb ? a.h_mid[crow] : 0.0f;
     const float sh = !BLK && a.shared_out != NULL ? a.shared_out[crow] : 0.0f;
     const float sgr = !BLK && a.shared_out != NULL ? a.shared_gate_raw[0] : 0.0f;
-    uint4 wv[4];
-    uint32_t wq[4];
-    uint16_t rsr[4], rbr[4];
-    float xs_r[32], lv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    if (ROUTE && cwave) {
+    uint4 wv0[4]; /* the router row (not XSTACK: there it comes from LDS) */
+    uint32_t wq0[4];
+    uint16_t rsr0[4], rbr0[4];
+    float xs_r0[32];
+    if (ROUTE && cwave && !STK) {
         if (ROUTE == NMOE_ROUTE_Q4) {
             /* q4 router row: words lane + 64q (columns 8 word .. +7) and their
              * groups' scale and bias, kept raw until the dot product */
@@ -385,18 +417,18 @@ __global__ void __launch_bounds__(NMOE_FUSED_THREADS) nmoe_fused_decode_kernel(n
             const size_t g0 = (size_t)blockIdx.x * (NMOE_HIDDEN / NMOE_GROUP);
 #pragma unroll
             for (int q = 0; q < 4; q++) {
-                wq[q] = rowq[lane + 64 * q];
-                rsr[q] = a.router_s[g0 + (lane + 64 * q) / 8];
-                rbr[q] = a.router_b[g0 + (lane + 64 * q) / 8];
+                wq0[q] = rowq[lane + 64 * q];
+                rsr0[q] = a.router_s[g0 + (lane + 64 * q) / 8];
+                rbr0[q] = a.router_b[g0 + (lane + 64 * q) / 8];
             }
         } else {
             const uint4 *row = (const uint4 *)(a.router_w + (size_t)blockIdx.x * NMOE_HIDDEN);
 #pragma unroll
-            for (int q = 0; q < 4; q++) wv[q] = row[lane + 64 * q];
+            for (int q = 0; q < 4; q++) wv0[q] = row[lane + 64 * q];
         }
         if (!NORM)
 #pragma unroll
-            for (int q = 0; q < 4; q++) nmoe_x_cols<XMODE>(a.x, (lane + 64 * q) * 8, 8, 1.0, xs_r + 8 * q);
+            for (int q = 0; q < 4; q++) nmoe_x_cols<XMODE>(a.x, (lane + 64 * q) * 8, 8, 1.0, xs_r0 + 8 * q);
     }
     /* XBLOCK, combining block: the shared expert's gate-score row
      * (kernels.metal:510-513), a router-like row the candidate wavefront
@@ -412,6 +444,74 @@ __global__ void __launch_bounds__(NMOE_FUSED_THREADS) nmoe_fused_decode_kernel(n
         }
     }
     if (tid < 32) s_tab[tid] = tab_v;
+    /* XSTACK: router rows 8j .. 8j+7 of a layer into LDS (the exact
+     * wavefront, a layer ahead of their use), by loads that write LDS
+     * directly: no registers held, all 32 KB in flight at once.  The wave
+     * waits for them (vmcnt) before the next layer's first barrier. */
+    typedef __attribute__((address_space(3))) void nmoe_lds_void;
+    auto load_rrow = [&](const void *rw, const void *rs, const void *rb) {
+        const int j8 = 8 * (blockIdx.x / NMOE_FUSED_GROUPS);
+        if (ROUTE == NMOE_ROUTE_Q4) {
+            const uint8_t *w = (const uint8_t *)rw + (size_t)j8 * (NMOE_HIDDEN / 2);
+#pragma unroll
+            for (int i = 0; i < 8; i++)
+                __builtin_amdgcn_global_load_lds(w + 1024 * i + 16 * lane, (nmoe_lds_void *)((uint8_t *)s_rrow + 1024 * i),
+                                                 16, 0, 0);
+            if (lane < 32) {
+                const uint8_t *sc = (const uint8_t *)rs + (size_t)j8 * (NMOE_HIDDEN / NMOE_GROUP) * 2;
+                const uint8_t *bi = (const uint8_t *)rb + (size_t)j8 * (NMOE_HIDDEN / NMOE_GROUP) * 2;
+                __builtin_amdgcn_global_load_lds(sc + 16 * lane, (nmoe_lds_void *)((uint8_t *)s_rrow + 8192), 16, 0, 0);
+                __builtin_amdgcn_global_load_lds(bi + 16 * lane, (nmoe_lds_void *)((uint8_t *)s_rrow + 8704), 16, 0, 0);
+            }
+        } else {
+            const uint8_t *w = (const uint8_t *)rw + (size_t)j8 * NMOE_HIDDEN * 2;
+#pragma unroll
+            for (int i = 0; i < 32; i++)
+                __builtin_amdgcn_global_load_lds(w + 1024 * i + 16 * lane, (nmoe_lds_void *)((uint8_t *)s_rrow + 1024 * i),
+                                                 16, 0, 0);
+        }
+    };
+    if (STK) { /* the layer table, h_0 and layer 0's router row */
+        if (tid < 4 * a.nl) s_stk[tid] = stab->p[tid];
+        if (tid < NMOE_HIDDEN / 4) ((float4 *)s_hin[0])[tid] = ((const float4 *)a.x)[tid];
+        if (wave == NMOE_FUSED_EXACT) load_rrow(stab->p[1], stab->p[2], stab->p[3]);
+    }
+    const int nl = STK ? a.nl : 1;
+    auto layer = [&](const int ly) {
+    if (STK && wave == NMOE_FUSED_EXACT) __builtin_amdgcn_s_waitcnt(0); /* this layer's router rows are in LDS */
+    if (STK) __syncthreads(); /* the layer before is done: h_l, its router rows and the LDS hand-offs are free */
+    /* XSTACK: an opaque copy of the thread index, so that the per-lane
+     * addresses derived from it are recomputed in each layer instead of
+     * hoisted out of the loop and kept live across all of it (the wave
+     * index stays the uniform one) */
+    int tid_o = (int)threadIdx.x;
+    if (STK) asm volatile("" : "+v"(tid_o));
+    const int tid = tid_o, lane = tid_o & 63;
+    uint4 wv[4];
+    uint32_t wq[4];
+    uint16_t rsr[4], rbr[4];
+    float xs_r[32], lv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (!STK) {
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            wv[q] = wv0[q];
+            wq[q] = wq0[q];
+            rsr[q] = rsr0[q];
+            rbr[q] = rbr0[q];
+        }
+#pragma unroll
+        for (int c = 0; c < 32; c++) xs_r[c] = xs_r0[c];
+    }
+    /* XSTACK: an opaque copy of the exchange base, so that no per-lane
+     * exchange address is hoisted out of the layer loop (they would stay
+     * live across every layer) */
+    uint64_t *xch = a.xch;
+    if (STK) asm volatile("" : "+s"(xch));
+    const uint8_t *pack = STK ? (const uint8_t *)s_stk[4 * ly] : a.pack;
+    uint64_t *xlg = xch + NMOE_XCH_LOGITS;
+    uint64_t *xlgd = xch + NMOE_XCH_LGD + (ly & 1) * (NMOE_FUSED_GROUPS * NMOE_EXPERTS) + g * NMOE_EXPERTS; /* XSTACK */
+    uint64_t *xact = xch + NMOE_XCH_ACT + NMOE_XCH_ASP * g * NMOE_INTER;
+    uint64_t *ypart = xch + (STK && (ly & 1) ? NMOE_XCH_YPART2 : NMOE_XCH_YPART);
     if (tid < NMOE_MAX_K) { /* in-range defaults for every routing word a wait may leave unwritten */
         s_cand[tid] = 0u;
         s_gx[tid] = 0u;
@@ -421,30 +521,38 @@ __global__ void __launch_bounds__(NMOE_FUSED_THREADS) nmoe_fused_decode_kernel(n
         s_t[NMOE_MAX_K + tid] = 0u;
     }
     if (tid == 0) {
-        uint32_t e = a.epoch_arg;
-        if (e == 0u) {
-            e = ep_old + 1u;
-            __hip_atomic_store(ep, e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (ly == 0) {
+            /* XSTACK: layer l runs with epoch e + l, and the block's word
+             * keeps the last one it uses */
+            uint32_t e = a.epoch_arg;
+            if (e == 0u) {
+                e = ep_old + 1u;
+                __hip_atomic_store(ep, STK ? ep_old + (uint32_t)nl : e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+            s_epoch = e;
+            s_bad = 0u;
+            s_shok = 0u;
+            s_sacnt = 0u;
         }
-        s_epoch = e;
         s_ncand = 0u;
         s_confirm = 0u;
         s_lgok = 0u;
-        s_bad = 0u;
-        s_shok = 0u;
-        s_sacnt = 0u;
     }
     if (NORM) {
         /* x = h / rms (times the norm weight, XBLOCK) once per block, into
          * LDS in the workers' swizzled chunk order (as the act): the workers
          * then hold no raw h and do no double arithmetic of their own */
-        const double rinv = 1.0 / (double)nmoe_block_rms_exact((const float *)a.x, a.eps, s_h, s_dd, s_f);
+        const float *hsrc = STK ? s_hin[ly & 1] : (const float *)a.x;
+        /* XSTACK after layer 0: from the 32 partial sums of squares the
+         * candidate wavefront summed while h was gathered */
+        const double ri_pre = STK && ly > 0 ? s_rinv : -1.0;
+        const double rinv = ri_pre >= 0.0 ? ri_pre : 1.0 / (double)nmoe_block_rms_exact(hsrc, a.eps, s_h, s_dd, s_f);
         if (tid < NMOE_HIDDEN / 8) {
 #pragma unroll
             for (int q = 0; q < 2; q++) {
                 const int c0 = 8 * tid + 4 * q;
                 float4 v;
-                nmoe_x_cols<XMODE>(a.x, c0, 4, rinv, &v.x);
+                nmoe_x_cols<XMODE>(hsrc, c0, 4, rinv, &v.x);
                 if (BLK && a.norm_w != NULL) { /* math.m:63: (h / rms) * weight */
                     v.x = v.x * nmoe_norm_weight(a.norm_w, c0, a.add_one);
                     v.y = v.y * nmoe_norm_weight(a.norm_w, c0 + 1, a.add_one);
@@ -456,7 +564,7 @@ __global__ void __launch_bounds__(NMOE_FUSED_THREADS) nmoe_fused_decode_kernel(n
         }
     }
     __syncthreads();
-    const uint32_t epoch = s_epoch;
+    const uint32_t epoch = s_epoch + (STK ? (uint32_t)ly : 0u);
 
     if (has_sh && wave < 4) {
         /* ---- S1 (XBLOCK, every block): shared gate/up rows 2b, 2b+1
@@ -535,24 +643,61 @@ __global__ void __launch_bounds__(NMOE_FUSED_THREADS) nmoe_fused_decode_kernel(n
         }
     };
 
+    if (STK && !ctrl) {
+        /* ---- R (XSTACK, worker wavefront w): router row 8j + w from LDS,
+         * published to this die's logit words (the die's 32 blocks cover
+         * all 256 rows, so routing never leaves the die) */
+        float xq[32];
+#pragma unroll
+        for (int c = 0; c < 8; c++)
+            *(float4 *)(xq + 4 * c) =
+                ((const float4 *)s_h)[nmoe_act_slot<Q::CPL / 4>(8 * lane + 512 * (c >> 1) + 4 * (c & 1)) / 4];
+        float logit;
+        if (ROUTE == NMOE_ROUTE_Q4) {
+            uint32_t w4[4];
+            uint16_t s4[4], b4[4];
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                w4[q] = s_rrow[256 * wave + lane + 64 * q];
+                s4[q] = ((const uint16_t *)s_rrow)[4096 + 32 * wave + (lane + 64 * q) / 8];
+                b4[q] = ((const uint16_t *)s_rrow)[4352 + 32 * wave + (lane + 64 * q) / 8];
+            }
+            logit = nmoe_router_row_q4(w4, s4, b4, xq);
+        } else {
+            uint4 w4[4];
+#pragma unroll
+            for (int q = 0; q < 4; q++) w4[q] = ((const uint4 *)s_rrow)[256 * wave + lane + 64 * q];
+            logit = nmoe_router_row_bf16(w4, xq);
+        }
+        if (nmoe_lds_flag(&s_bad)) logit = __builtin_nanf(""); /* a layer before went wrong: so do all after */
+        if (lane == 0) {
+            if (a.xcd_local)
+                nmoe_st_tagged_die(xlgd + 8 * j + wave, epoch, logit);
+            else
+                nmoe_st_tagged(xlgd + 8 * j + wave, epoch, logit);
+        }
+    }
     if (ROUTE && cwave) {
         /* the control wavefronts share SIMDs with workers: their routing is
          * on the critical path, the workers' multiply-adds mostly are not */
         __builtin_amdgcn_s_setprio(2);
-        /* ---- R (candidate wavefront): router row blockIdx.x */
-        if (NORM)
+        /* ---- R (candidate wavefront): router row blockIdx.x (XSTACK: the
+         * worker wavefronts, below) */
+        if (NORM && !STK)
 #pragma unroll
             for (int c = 0; c < 8; c++)
                 *(float4 *)(xs_r + 4 * c) =
                     ((const float4 *)s_h)[nmoe_act_slot<Q::CPL / 4>(8 * lane + 512 * (c >> 1) + 4 * (c & 1)) / 4];
-        const float logit =
-            ROUTE == NMOE_ROUTE_Q4 ? nmoe_router_row_q4(wq, rsr, rbr, xs_r) : nmoe_router_row_bf16(wv, xs_r);
-        if (lane == 0) nmoe_st_tagged(xlg + NMOE_XCH_SP * blockIdx.x, epoch, logit);
+        if (!STK) {
+            const float logit =
+                ROUTE == NMOE_ROUTE_Q4 ? nmoe_router_row_q4(wq, rsr, rbr, xs_r) : nmoe_router_row_bf16(wv, xs_r);
+            if (lane == 0) nmoe_st_tagged(xlg + NMOE_XCH_SP * blockIdx.x, epoch, logit);
+        }
         if (has_sh && comb) { /* the shared expert's gate score, same x */
             const float v = nmoe_router_row_q4(sq_w, sq_s, sq_b, xs_r);
             if (lane == 0) s_sgr[0] = v;
         }
-        if (g < k) {
+        if (g < k || STK) {
             /* ---- T: wait for all 256 logits and hand them to the exact
              * wavefront; the candidates are the k largest logits, published
              * one per selection round so that group s starts streaming its
@@ -561,7 +706,11 @@ __global__ void __launch_bounds__(NMOE_FUSED_THREADS) nmoe_fused_decode_kernel(n
              * settles. */
             const uint64_t *pl[4] = {xlg + NMOE_XCH_SP * lane, xlg + NMOE_XCH_SP * (lane + 64),
                                      xlg + NMOE_XCH_SP * (lane + 128), xlg + NMOE_XCH_SP * (lane + 192)};
-            nmoe_poll<4>(pl, epoch, lv, status, &s_bad, a.spin);
+            const uint64_t *pd[4] = {xlgd + lane, xlgd + lane + 64, xlgd + lane + 128, xlgd + lane + 192};
+            if (STK) /* this die's 256 logits */
+                nmoe_poll<4>(pd, epoch, lv, status, &s_bad, a.spin, a.xcd_local != 0);
+            else
+                nmoe_poll<4>(pl, epoch, lv, status, &s_bad, a.spin);
 #pragma unroll
             for (int q = 0; q < 4; q++) s_lg[lane + 64 * q] = lv[q];
             if (lane == 0) __hip_atomic_store(&s_lgok, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
@@ -601,7 +750,7 @@ __global__ void __launch_bounds__(NMOE_FUSED_THREADS) nmoe_fused_decode_kernel(n
             if (has_sh && comb) shared_down(0);
         }
     }
-    if (ROUTE && wave == NMOE_FUSED_EXACT && g < k) {
+    if (ROUTE && wave == NMOE_FUSED_EXACT && (g < k || STK)) {
         /* ---- exact routing (math.m softmax / top-k / renormalise), from
          * the moment the logits are in, alongside the candidate rounds and
          * the expert loads; then the expert of each group. */
@@ -721,6 +870,9 @@ __global__ void __launch_bounds__(NMOE_FUSED_THREADS) nmoe_fused_decode_kernel(n
         }
         if (lane == 0) __hip_atomic_store(&s_confirm, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
         if (has_sh && comb) shared_down(1);
+        /* XSTACK: the next layer's router row, while this layer streams
+         * (the candidate wavefront read this one before the logits came) */
+        if (STK && ly + 1 < nl) load_rrow(s_stk[4 * (ly + 1) + 1], s_stk[4 * (ly + 1) + 2], s_stk[4 * (ly + 1) + 3]);
     }
     if (!ROUTE) {
         if (tid < NMOE_MAX_K) {
@@ -735,7 +887,8 @@ __global__ void __launch_bounds__(NMOE_FUSED_THREADS) nmoe_fused_decode_kernel(n
         }
         __syncthreads();
     }
-    if (g >= k) return; /* group g streams one expert */
+    if (!STK && g >= k) return; /* group g streams one expert (XSTACK: idle groups still combine) */
+    const bool active = !STK || g < k;
 
     /* ---- P (workers): issue all weight loads of this wavefront */
     const int gsub = lane / Q::LPR_G, gl = lane % Q::LPR_G, ggrp = gl * Q::CPL / NMOE_GROUP;
@@ -750,7 +903,7 @@ __global__ void __launch_bounds__(NMOE_FUSED_THREADS) nmoe_fused_decode_kernel(n
     uint4 gwv[GSTEPS], uwv[GSTEPS], dwv[DSTEPS];
     uint32_t gsc[GSTEPS], gbi[GSTEPS], usc[GSTEPS], ubi[GSTEPS], dsc[DSTEPS], dbi[DSTEPS];
     auto load_expert = [&](uint32_t e) {
-        const uint8_t *ex = a.pack + (size_t)e * L::expert_size;
+        const uint8_t *ex = pack + (size_t)e * L::expert_size;
 #pragma unroll
         for (int i = 0; i < GSTEPS; i++) {
             int row = grow0 + i * RPS;
@@ -774,7 +927,7 @@ __global__ void __launch_bounds__(NMOE_FUSED_THREADS) nmoe_fused_decode_kernel(n
         }
     };
     uint32_t cand_g = 0;
-    if (!ctrl) {
+    if (!ctrl && active) {
         /* x first: loads retire in order, so G can start while down rows stream */
         const uint4 *xp = (const uint4 *)a.x + gl * XV;
         if (!NORM)
@@ -820,7 +973,7 @@ __global__ void __launch_bounds__(NMOE_FUSED_THREADS) nmoe_fused_decode_kernel(n
             actv[i] = nmoe_silu_dev(gv) * uv;
         }
     };
-    if (!ctrl) {
+    if (!ctrl && active) {
         gate_up();
         if (ROUTE) {
             nmoe_lds_wait_above(&s_confirm, 0u, status, &s_bad, a.spin);
@@ -848,12 +1001,12 @@ __global__ void __launch_bounds__(NMOE_FUSED_THREADS) nmoe_fused_decode_kernel(n
      * multiply-adds only (q2 has no registers to spare for this) */
     constexpr bool DPRE = BITS == 4;
     float dwf[DPRE ? DSTEPS : 1][DPRE ? Q::CPL : 1];
-    if (DPRE && !ctrl)
+    if (DPRE && !ctrl && active)
 #pragma unroll
         for (int i = 0; i < DSTEPS; i++) nmoe_unpack_q4(dwv[i], dwf[i]);
 
     /* ---- D (workers): wait for act[g], then y_g for rows 64j..64j+63 */
-    if (!ctrl) {
+    if (!ctrl && active) {
         constexpr int APT = NMOE_INTER / (64 * NMOE_FUSED_WORKERS); /* act words per worker thread */
         const uint64_t *pa[APT];
         float av[APT];
@@ -867,7 +1020,7 @@ __global__ void __launch_bounds__(NMOE_FUSED_THREADS) nmoe_fused_decode_kernel(n
         for (int q = 0; q < APT; q++) s_act[nmoe_act_slot<Q::CPL / 4>(tid + 64 * NMOE_FUSED_WORKERS * q)] = av[q];
     }
     __syncthreads();
-    if (!ctrl) {
+    if (!ctrl && active) {
         /* this lane's CPL act columns, read once (conflict-free: swizzled) */
         float as[Q::CPL];
 #pragma unroll
@@ -897,10 +1050,11 @@ __global__ void __launch_bounds__(NMOE_FUSED_THREADS) nmoe_fused_decode_kernel(n
     const int row = j * NMOE_FUSED_CHUNK + tid;
     const bool poisoned = nmoe_lds_flag(&s_bad); /* every wait of the block is behind the barrier above */
     float rv = 0.0f; /* the combining thread's out row */
+    uint64_t *xhg = xch + NMOE_XCH_HG + g * NMOE_XCH_HGS; /* XSTACK: the die's next h */
     if (tid < NMOE_FUSED_CHUNK) {
-        if (g != j % k) {
+        if (!comb || (STK && active))
             nmoe_st_tagged(ypart + g * NMOE_HIDDEN + row, epoch, poisoned ? __builtin_nanf("") : s_y[tid]);
-        } else {
+        if (comb) {
             const uint64_t *pp[NMOE_MAX_K];
             float ys[NMOE_MAX_K];
 #pragma unroll
@@ -924,7 +1078,7 @@ __global__ void __launch_bounds__(NMOE_FUSED_THREADS) nmoe_fused_decode_kernel(n
             const float gsig = shared_term ? nmoe_sigmoid_dev(BLK ? s_sgr[0] : sgr) : 0.0f;
             const float shv = BLK ? (has_sh ? s_shd[tid] : 0.0f) : sh;
             const bool expired = nmoe_poll2<NMOE_MAX_K>(pp, epoch, ys, status, &s_bad, a.spin,
-                                                        ((1u << k) - 1u) & ~(1u << g));
+                                                        ((1u << k) - 1u) & ~(active ? 1u << g : 0u));
             /* slot order: slot s is streamed by group sgl[s] */
             float moe = 0.0f;
             if (ident) {
@@ -943,10 +1097,39 @@ __global__ void __launch_bounds__(NMOE_FUSED_THREADS) nmoe_fused_decode_kernel(n
                     }
                 }
             }
-            float r = hm + moe;
+            float r = (STK ? s_hin[ly & 1][row] : hm) + moe;
             if (shared_term) r = r + gsig * shv;
             rv = poisoned || expired ? __builtin_nanf("") : r;
-            a.out[row] = rv;
+            if (!STK) {
+                a.out[row] = rv;
+            } else {
+                /* every die holds the same rows: one writes them out, each
+                 * publishes them to its own 32 blocks */
+                if (g == (j & (NMOE_FUSED_GROUPS - 1))) a.out[(size_t)ly * NMOE_HIDDEN + row] = rv;
+                if (a.xcd_local)
+                    nmoe_st_tagged_die(xhg + row, epoch, rv);
+                else
+                    nmoe_st_tagged(xhg + row, epoch, rv);
+                /* and the sum of their squares for the next layer's norm:
+                 * exact squares, a tree of depth 6 (4 DPP levels in a row
+                 * of 16 lanes, 2 over the rows); the 32 partials' tree adds
+                 * 5 (nmoe_mean_sq_from_sum allows 11) */
+                double sq = (double)rv * (double)rv;
+                sq = sq + nmoe_dpp_d<NMOE_DPP_XOR1>(sq);
+                sq = sq + nmoe_dpp_d<NMOE_DPP_XOR2>(sq);
+                sq = sq + nmoe_dpp_d<NMOE_DPP_HALF_MIRROR>(sq);
+                sq = sq + nmoe_dpp_d<NMOE_DPP_MIRROR>(sq);
+                const double ps =
+                    (nmoe_readlane_d(sq, 0) + nmoe_readlane_d(sq, 16)) + (nmoe_readlane_d(sq, 32) + nmoe_readlane_d(sq, 48));
+                if (tid < 2) {
+                    const uint64_t pb = __builtin_bit_cast(uint64_t, ps);
+                    const uint32_t half = tid == 0 ? (uint32_t)pb : (uint32_t)(pb >> 32);
+                    if (a.xcd_local)
+                        nmoe_st_tagged_die(xhg + NMOE_HIDDEN + 2 * j + tid, epoch, __uint_as_float(half));
+                    else
+                        nmoe_st_tagged_u32(xhg + NMOE_HIDDEN + 2 * j + tid, epoch, half);
+                }
+            }
         }
     }
     if (BLK && comb && a.next_x != NULL && wave == 0) {
@@ -1010,14 +1193,65 @@ __global__ void __launch_bounds__(NMOE_FUSED_THREADS) nmoe_fused_decode_kernel(n
         a.next_x[row] = nmoe_lds_flag(&s_bad) ? __builtin_nanf("") : xn; /* a partial that never came */
     }
     if (ROUTE && blockIdx.x == 0 && cwave) {
+        const int o = STK ? NMOE_MAX_K * ly : 0;
         if (lane < NMOE_MAX_K) {
-            if (a.idx_out != NULL) a.idx_out[lane] = min(s_t[lane], (uint32_t)(NMOE_EXPERTS - 1));
-            if (a.w_out != NULL) a.w_out[lane] = poisoned ? __builtin_nanf("") : s_w[lane];
+            if (a.idx_out != NULL) a.idx_out[o + lane] = min(s_t[lane], (uint32_t)(NMOE_EXPERTS - 1));
+            if (a.w_out != NULL) a.w_out[o + lane] = poisoned ? __builtin_nanf("") : s_w[lane];
         }
         if (a.logits_out != NULL)
 #pragma unroll
             for (int q = 0; q < 4; q++) a.logits_out[lane + 64 * q] = lv[q];
     }
+    if (STK && ly + 1 < nl && tid < NMOE_HIDDEN / 4) {
+        /* ---- H (XSTACK): the die's 32 blocks gather h_{l+1} (all of it,
+         * 4 words a thread) into the other h buffer */
+        const uint64_t *ph[4] = {xhg + tid, xhg + tid + 512, xhg + tid + 1024, xhg + tid + 1536};
+        float hv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        nmoe_poll<4>(ph, epoch, hv, status, &s_bad, a.spin, a.xcd_local != 0);
+#pragma unroll
+        for (int q = 0; q < 4; q++) s_hin[(ly + 1) & 1][tid + 512 * q] = hv[q];
+    }
+    if (STK && ly + 1 < nl && cwave) {
+        /* ---- H (XSTACK, candidate wavefront): the die's 32 sums of
+         * squares (lanes 0..31, two words each) -> the next layer's 1 / rms,
+         * or -1 where the float mean needs the x87 replay */
+        const int src = lane & (NMOE_FUSED_GROUP_BLOCKS - 1);
+        const uint64_t *pq[2] = {xhg + NMOE_HIDDEN + 2 * src, xhg + NMOE_HIDDEN + 2 * src + 1};
+        float pv[2] = {0.0f, 0.0f};
+        nmoe_poll<2>(pq, epoch, pv, status, &s_bad, a.spin, a.xcd_local != 0, lane < NMOE_FUSED_GROUP_BLOCKS ? 3u : 0u);
+        double ps = lane < NMOE_FUSED_GROUP_BLOCKS
+                        ? __builtin_bit_cast(double, ((uint64_t)__float_as_uint(pv[1]) << 32) | __float_as_uint(pv[0]))
+                        : 0.0;
+        ps = ps + nmoe_dpp_d<NMOE_DPP_XOR1>(ps);
+        ps = ps + nmoe_dpp_d<NMOE_DPP_XOR2>(ps);
+        ps = ps + nmoe_dpp_d<NMOE_DPP_HALF_MIRROR>(ps);
+        ps = ps + nmoe_dpp_d<NMOE_DPP_MIRROR>(ps);
+        const float mean = nmoe_mean_sq_from_sum(nmoe_readlane_d(ps, 0) + nmoe_readlane_d(ps, 16));
+        double ri = -1.0;
+        if (mean >= 0.0f) {
+            float rms = nmoe_sqrtf_rn(mean + a.eps);
+            rms = rms == 0.0f ? 1.0f : rms;
+            ri = 1.0 / (double)rms;
+        }
+        if (lane == 0) s_rinv = ri;
+    }
+    };
+    if constexpr (STK) {
+        for (int ly = 0; ly < nl; ly++) layer(ly);
+    } else {
+        layer(0);
+    }
+}
+
+template <int BITS, int ROUTE, int XMODE>
+__global__ void __launch_bounds__(NMOE_FUSED_THREADS) nmoe_fused_decode_kernel(nmoe_fused_args a) {
+    nmoe_fused_body<BITS, ROUTE, XMODE>(a, nullptr);
+}
+
+/* XSTACK: the token's layers in one launch (the layer table by value) */
+template <int BITS, int ROUTE>
+__global__ void __launch_bounds__(NMOE_FUSED_THREADS) nmoe_fused_stack_kernel(nmoe_fused_args a, nmoe_stack_tab t) {
+    nmoe_fused_body<BITS, ROUTE, NMOE_XSTACK>(a, &t);
 }
 
 /* ----------------------------------------------------------- launching */
@@ -1040,10 +1274,20 @@ static int nmoe_fused_fits(int num_cus) {
 /* Every x form the launcher may use with this router kind (the RMSNorm
  * form needs the kernel to route). */
 template <int BITS, int ROUTE>
+static int nmoe_stack_fits(int num_cus) {
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, nmoe_fused_stack_kernel<BITS, ROUTE>, NMOE_FUSED_THREADS,
+                                                     0) != hipSuccess)
+        return 0;
+    return per_cu >= 1 && per_cu * num_cus >= NMOE_FUSED_BLOCKS;
+}
+
+template <int BITS, int ROUTE>
 static int nmoe_fused_fits_all(int num_cus) {
     int ok = nmoe_fused_fits<BITS, ROUTE, NMOE_XBF16>(num_cus) && nmoe_fused_fits<BITS, ROUTE, NMOE_XF32>(num_cus);
     if constexpr (ROUTE != NMOE_ROUTE_GIVEN)
-        ok = ok && nmoe_fused_fits<BITS, ROUTE, NMOE_XNORM>(num_cus) && nmoe_fused_fits<BITS, ROUTE, NMOE_XBLOCK>(num_cus);
+        ok = ok && nmoe_fused_fits<BITS, ROUTE, NMOE_XNORM>(num_cus) && nmoe_fused_fits<BITS, ROUTE, NMOE_XBLOCK>(num_cus) &&
+             nmoe_stack_fits<BITS, ROUTE>(num_cus);
     return ok;
 }
 
@@ -1096,7 +1340,7 @@ extern "C" int nmoe_decode_init(nmoe_hip_ctx *ctx) {
     const int ok = nmoe_fused_resident(ctx->num_cus);
     ctx->fused_blocks = ok ? NMOE_FUSED_BLOCKS : 0;
     ctx->xcd_placed = 0;
-    ctx->xch_bytes = NMOE_FUSED_XCH_BYTES_BLOCK;
+    ctx->xch_bytes = NMOE_FUSED_XCH_BYTES_STACK;
     if (hipMalloc((void **)&ctx->xch, ctx->xch_bytes) != hipSuccess) return NMOE_HIP_ENOMEM;
     if (ok) { /* the probe writes into the exchange buffer, cleared afterwards */
         int r = nmoe_probe_xcd_placement((uint32_t *)ctx->xch, &ctx->xcd_placed);
@@ -1201,5 +1445,51 @@ extern "C" int nmoe_fused_block(nmoe_hip_ctx *ctx, int bits, const nmoe_hip_rout
                                                 out, idx_out, w_out, logits_out, pack, ctx->xch, ctx->sync,
                                                 ctx->use_xcd_local, ctx->spin_limit, 0u, blk, s);
     if (e != hipSuccess) return nmoe_hip_check(ctx, e, "fused block launch");
+    return NMOE_HIP_OK;
+}
+
+/* Every layer of one token in one launch (XSTACK), at most
+ * NMOE_STACK_MAX_LAYERS: layer l streams packs[l] and routes with
+ * routers[l] (all of one kind, q4r), x_l = RMSNorm(h_l) (unit weight),
+ * h_seq rows 1..nl receive h_{l+1} = h_l + MoE_l(x_l), idx_seq / w_seq
+ * (nullable) 8 words per layer. */
+extern "C" int nmoe_fused_stack(nmoe_hip_ctx *ctx, int bits, int q4r, int nl, const uint8_t *const *packs,
+                                const nmoe_hip_router *routers, float *h_seq, float eps, int k, uint32_t *idx_seq,
+                                float *w_seq, hipStream_t s) {
+    if (nl < 1 || nl > NMOE_STACK_MAX_LAYERS) return nmoe_fail(ctx, NMOE_HIP_EINVAL, "stack of %d layers", nl);
+    nmoe_fused_args a;
+    memset(&a, 0, sizeof(a));
+    nmoe_stack_tab t;
+    memset(&t, 0, sizeof(t));
+    for (int l = 0; l < nl; l++) {
+        t.p[4 * l] = packs[l];
+        t.p[4 * l + 1] = q4r ? (const void *)routers[l].w_q4 : (const void *)routers[l].w_bf16;
+        t.p[4 * l + 2] = q4r ? routers[l].scales : NULL;
+        t.p[4 * l + 3] = q4r ? routers[l].biases : NULL;
+    }
+    a.x = h_seq;
+    a.out = h_seq + NMOE_HIDDEN;
+    a.eps = eps;
+    a.k = k;
+    a.idx_out = idx_seq;
+    a.w_out = w_seq;
+    a.xch = ctx->xch;
+    a.sync = ctx->sync;
+    a.xcd_local = ctx->use_xcd_local;
+    a.spin = ctx->spin_limit;
+    a.nl = nl;
+    if (bits == 4) {
+        if (q4r)
+            hipLaunchKernelGGL((nmoe_fused_stack_kernel<4, NMOE_ROUTE_Q4>), dim3(NMOE_FUSED_BLOCKS), dim3(NMOE_FUSED_THREADS), 0, s, a, t);
+        else
+            hipLaunchKernelGGL((nmoe_fused_stack_kernel<4, NMOE_ROUTE_BF16>), dim3(NMOE_FUSED_BLOCKS), dim3(NMOE_FUSED_THREADS), 0, s, a, t);
+    } else {
+        if (q4r)
+            hipLaunchKernelGGL((nmoe_fused_stack_kernel<2, NMOE_ROUTE_Q4>), dim3(NMOE_FUSED_BLOCKS), dim3(NMOE_FUSED_THREADS), 0, s, a, t);
+        else
+            hipLaunchKernelGGL((nmoe_fused_stack_kernel<2, NMOE_ROUTE_BF16>), dim3(NMOE_FUSED_BLOCKS), dim3(NMOE_FUSED_THREADS), 0, s, a, t);
+    }
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return nmoe_hip_check(ctx, e, "fused stack launch");
     return NMOE_HIP_OK;
 }

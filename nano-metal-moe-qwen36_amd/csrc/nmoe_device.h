@@ -541,13 +541,14 @@ __device__ __forceinline__ float nmoe_dd_mean_float(double S, double Cc) {
 
 /* rms of math.m:34-65 (unit weight) over the 2048 fp32 values h, by a whole
  * block of 256 or more threads (threads 0..255 hold the data, the rest
- * only take part in the barriers); uniform result.  math.m sums the squares in an x87
- * `long double` (64-bit significand) running sum, so its mean square differs
- * from the exact one by less than 2^-53 relative.  The block computes the
- * exact mean square as a double-double; if no float rounding midpoint lies
- * within 2^-51 of it, rounding it to float gives math.m's value.  Otherwise
- * (a near-tie, or tiny values) lane 0 replays the x87 running sum in index
- * order.  lds_h: 2048 floats of LDS, lds_dd: 8 doubles, lds_f: 1 float. */
+ * only take part in the barriers); uniform result.  math.m sums the squares
+ * in an x87 `long double` (64-bit significand) running sum.  The block sums
+ * the squares in double as a tree of depth 11 (3 levels in a thread, 4 DPP
+ * levels in a row of 16 lanes, 2 over the rows, 2 over the 4 wavefronts),
+ * a short dependency chain; nmoe_mean_sq_from_sum turns that into math.m's
+ * float wherever no rounding midpoint is near, and otherwise (a near-tie,
+ * or tiny values) lane 0 replays the x87 running sum in index order.
+ * lds_h: 2048 floats of LDS, lds_dd: 8 doubles, lds_f: 1 float. */
 __device__ float nmoe_block_rms_exact(const float *h, float eps, float *lds_h, double *lds_dd, float *lds_f) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const float4 *h4 = (const float4 *)h;
@@ -558,28 +559,22 @@ __device__ float nmoe_block_rms_exact(const float *h, float eps, float *lds_h, d
         v1 = h4[2 * tid + 1];
     }
     float vv[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
-    double s = 0.0, c = 0.0;
+    double q[8];
 #pragma unroll
-    for (int i = 0; i < 8; i++) {
-        double q = (double)vv[i] * (double)vv[i]; /* exact: 48 significant bits */
-        double e;
-        nmoe_two_sum(s, q, s, e);
-        c += e;
-    }
-    /* cross-row combination with every lane active (reading other lanes
-     * from inside a lane-divergent branch would read undefined values) */
-    double ws, wc;
-    nmoe_wave_dd_sum(s, c, ws, wc);
-    if (lane == 0 && holds) {
-        lds_dd[2 * wave] = ws;
-        lds_dd[2 * wave + 1] = wc;
-    }
+    for (int i = 0; i < 8; i++) q[i] = (double)vv[i] * (double)vv[i]; /* exact: 48 significant bits */
+    double s = ((q[0] + q[1]) + (q[2] + q[3])) + ((q[4] + q[5]) + (q[6] + q[7]));
+    /* with every lane active (reading other lanes from inside a
+     * lane-divergent branch would read undefined values); each step adds
+     * the same two sums in both lanes of a pair, so a row's 16 lanes end
+     * with equal values */
+    s = s + nmoe_dpp_d<NMOE_DPP_XOR1>(s);
+    s = s + nmoe_dpp_d<NMOE_DPP_XOR2>(s);
+    s = s + nmoe_dpp_d<NMOE_DPP_HALF_MIRROR>(s);
+    s = s + nmoe_dpp_d<NMOE_DPP_MIRROR>(s);
+    const double ws = (nmoe_readlane_d(s, 0) + nmoe_readlane_d(s, 16)) + (nmoe_readlane_d(s, 32) + nmoe_readlane_d(s, 48));
+    if (lane == 0 && holds) lds_dd[wave] = ws;
     __syncthreads();
-    if (tid == 0) {
-        double S = lds_dd[0], Cc = lds_dd[1];
-        for (int w = 1; w < 4; w++) nmoe_dd_add(S, Cc, lds_dd[2 * w], lds_dd[2 * w + 1]);
-        lds_f[0] = nmoe_dd_mean_float(S, Cc);
-    }
+    if (tid == 0) lds_f[0] = nmoe_mean_sq_from_sum((lds_dd[0] + lds_dd[1]) + (lds_dd[2] + lds_dd[3]));
     __syncthreads();
     float mean = lds_f[0];
     if (mean < 0.0f) {

@@ -292,4 +292,26 @@ NMOE_HD float nmoe_sqrtf_rn(float v) {
     return r;
 }
 
+/* math.m:46-52's mean square of 2048 floats as a float, from S, their
+ * squares (each exact in double) summed in double as a binary tree of
+ * depth at most 11.  Summing non-negative terms, a tree of depth d is
+ * within (1 + 2^-53)^d - 1 < 11.001 * 2^-53 relative of the exact sum;
+ * math.m's x87 long double running sum is within 2047 * 2^-64 < 2^-53 of
+ * it, and dividing by 2048 is exact in both.  So when no float rounding
+ * midpoint lies within 2^-48 (= 32 * 2^-53) relative of S / 2048, math.m's
+ * mean rounds to the float S / 2048 rounds to.  Returns that float, or -1
+ * when the caller must replay the x87 sum (a near-midpoint, or a mean
+ * outside the normal float range). */
+NMOE_HD float nmoe_mean_sq_from_sum(double S) {
+    const double m = S * (1.0 / 2048.0); /* exact */
+    if (m == 0.0) return 0.0f;           /* every square, hence every term, is 0 */
+    const float f = (float)m;
+    const uint32_t fb = nmoe_flt_bits(f);
+    if (fb < 0x00800000u || fb >= 0x7f000000u) return -1.0f;
+    const double up = ((double)f + (double)nmoe_bits_flt(fb + 1u)) * 0.5;
+    const double dn = ((double)f + (double)nmoe_bits_flt(fb - 1u)) * 0.5;
+    const double margin = m * 0x1p-48;
+    return (up - m) > margin && (m - dn) > margin ? f : -1.0f;
+}
+
 #endif

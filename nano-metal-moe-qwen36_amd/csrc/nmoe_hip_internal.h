@@ -54,6 +54,7 @@ struct nmoe_layout<2> {
  * and with the whole-block form's shared activations and next-norm sums. */
 #define NMOE_FUSED_XCH_BYTES 409600u
 #define NMOE_FUSED_XCH_BYTES_BLOCK 460800u
+#define NMOE_FUSED_XCH_BYTES_STACK 759808u /* the block form's words + the layer loop's */
 
 /* The whole-block parts of a fused launch (XBLOCK): norm weights, the
  * next-layer norm output and the shared expert. */
@@ -100,6 +101,7 @@ struct nmoe_hip_ctx {
     int use_xcd_local;    /* NMOE_HIP_OPT_XCD_LOCAL */
     uint32_t spin_limit;  /* NMOE_HIP_OPT_SPIN_LIMIT: poll rounds before a bounded wait gives up */
     int sync_check;       /* NMOE_HIP_OPT_SYNC_CHECK */
+    int stack_loop;       /* NMOE_HIP_OPT_STACK_LOOP */
     /* grouped (matrix-core) path for many tokens, sized for max_tokens */
     int grouped_min_tokens; /* NMOE_HIP_OPT_GROUPED_MIN_TOKENS */
     uint32_t *g_counts;     /* [64][257] per-block expert histograms */

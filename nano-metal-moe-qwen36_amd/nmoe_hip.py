@@ -46,6 +46,7 @@ OPT_GROUPED_MIN_TOKENS = 3
 OPT_SPIN_LIMIT = 4
 OPT_SYNC_CHECK = 5
 OPT_SKEW_EPOCH = 6
+OPT_STACK_LOOP = 7
 
 # q4 / q2 component offsets (scripts/convert_qwen36.py:38-64)
 OFFSETS = {

@@ -52,6 +52,34 @@ float h_native_mean_sq(const float *v, int n) {
     return (float)(acc / (long double)n);
 }
 
+/* nmoe_block_rms_exact's double tree over 2048 values, in its order:
+ * 8 per thread pairwise, then rows of 16 threads (DPP xor 1, xor 2, half
+ * mirror, mirror), the 4 rows of a wavefront, the 4 wavefronts; then
+ * nmoe_mean_sq_from_sum (-1: the x87 replay is needed) */
+float h_tree_mean_sq(const float *v) {
+    double t[256], w[4];
+    for (int i = 0; i < 256; i++) {
+        double q[8];
+        for (int k = 0; k < 8; k++) q[k] = (double)v[8 * i + k] * (double)v[8 * i + k];
+        t[i] = ((q[0] + q[1]) + (q[2] + q[3])) + ((q[4] + q[5]) + (q[6] + q[7]));
+    }
+    for (int wv = 0; wv < 4; wv++) {
+        double r[4];
+        for (int row = 0; row < 4; row++) {
+            double a[16];
+            for (int i = 0; i < 16; i++) a[i] = t[64 * wv + 16 * row + i];
+            double b[16];
+            for (int i = 0; i < 16; i++) b[i] = a[i] + a[i ^ 1];
+            for (int i = 0; i < 16; i++) a[i] = b[i] + b[i ^ 2];
+            for (int i = 0; i < 16; i++) b[i] = a[i] + a[(i & 8) | (7 - (i & 7))];
+            for (int i = 0; i < 16; i++) a[i] = b[i] + b[15 - i];
+            r[row] = a[0];
+        }
+        w[wv] = (r[0] + r[1]) + (r[2] + r[3]);
+    }
+    return nmoe_mean_sq_from_sum((w[0] + w[1]) + (w[2] + w[3]));
+}
+
 float h_u64e_to_f32(uint64_t m, int e) { return nmoe_u64e_to_f32_rne(m, e); }
 
 float h_sqrtf(float v) { return nmoe_sqrtf_rn(v); }

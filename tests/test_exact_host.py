@@ -35,6 +35,7 @@ def h(tmp_path_factory):
     lib.h_fixed_sum.restype, lib.h_fixed_sum.argtypes = ctypes.c_int, [P, ctypes.c_int, P]
     lib.h_u64e_to_f32.restype, lib.h_u64e_to_f32.argtypes = ctypes.c_float, [ctypes.c_uint64, ctypes.c_int]
     lib.h_sqrtf.restype, lib.h_sqrtf.argtypes = ctypes.c_float, [ctypes.c_float]
+    lib.h_tree_mean_sq.restype, lib.h_tree_mean_sq.argtypes = ctypes.c_float, [P]
     return lib
 
 
@@ -76,6 +77,34 @@ def test_x87_mean_square_matches_long_double(h):
         a = h.h_x87_mean_sq(v.ctypes.data, 2048, 11)
         b = h.h_native_mean_sq(v.ctypes.data, 2048)
         assert np.float32(a).view(np.uint32) == np.float32(b).view(np.uint32), trial
+
+
+def test_tree_mean_square_fast_path(h):
+    """The device norm's double tree sum: wherever it takes its fast path
+    the float equals math.m's long double mean square bit for bit; at float
+    rounding midpoints it declines (the x87 replay takes over)."""
+    rng = np.random.default_rng(15)
+    taken = 0
+    for trial in range(400):
+        scale = rng.choice([1e-18, 1e-3, 1.0, 50.0, 1e15])
+        v = (rng.standard_normal(2048) * scale).astype(np.float32)
+        if trial % 4 == 1:  # wide dynamic range within one vector
+            v *= (np.float32(2.0) ** rng.integers(-40, 40, 2048)).astype(np.float32)
+        if trial % 4 == 2:  # few large terms
+            v[rng.integers(0, 2048, 5)] = np.float32(1e4)
+        m = h.h_tree_mean_sq(v.ctypes.data)
+        want = h.h_native_mean_sq(v.ctypes.data, 2048)
+        if m >= 0.0:
+            taken += 1
+            assert np.float32(m).view(np.uint32) == np.float32(want).view(np.uint32), trial
+    assert taken >= 300  # declines: means outside the normal float range
+    # exact midpoints of two floats: mean 1 + 2^-11 + 2^-24 (h = 1 + 2^-12)
+    for v in (np.full(2048, 1 + 2 ** -12, np.float32), np.full(2048, 2 * (1 + 2 ** -12), np.float32)):
+        assert h.h_tree_mean_sq(v.ctypes.data) == -1.0
+    z = np.zeros(2048, np.float32)
+    assert h.h_tree_mean_sq(z.ctypes.data) == 0.0
+    tiny = np.full(2048, 1e-30, np.float32)  # mean square below the normal range
+    assert h.h_tree_mean_sq(tiny.ctypes.data) == -1.0
 
 
 def test_fixed_point_fast_path(h):
