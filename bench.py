@@ -1,6 +1,6 @@
 """Benchmark: routed-MoE tokens/s and achieved HBM GB/s (q4, top-8, batch 1).
 
-Workload (BASELINE.json metric, first config shape, on the GPU): one decode
+Workload (the headline metric's configuration, on the GPU): one decode
 token through one routed-expert layer of Qwen3.6-35B-A3B -- bf16 router
 [256][2048], softmax/top-8/renormalise, eight q4 group-64 experts
 (2048 -> 512 gate/up, SwiGLU, 512 -> 2048 down), weighted combine into the
@@ -9,9 +9,11 @@ fp32 residual.  Steps rotate over 40 synthetic layers resident in HBM
 routers (320 MB), so experts and router rows stream from HBM.  The timed
 steps come after the warm-up's, never on the layers it just read.
 
-The same JSON line carries two sub-objects measured in the same run: "c3"
-(128 decode tokens through the 40-layer stack) and "c5" (the 2048-token
-prefill on the grouped matrix-core path, with its MFMA utilisation).
+The same JSON line carries sub-objects measured in the same run: "c3"
+(128 decode tokens through the 40-layer stack, one persistent launch per
+token), "c5" (the 2048-token prefill on the grouped matrix-core path, with
+its MFMA utilisation) and "stream" (the streaming floor of the step's expert
+bytes, nmoe_hip_read_probe).
 
 A step is one call of the per-layer MoE entry point (nmoe_moe_layer), which
 for one token is a single persistent launch (nmoe_fused_decode_kernel).

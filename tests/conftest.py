@@ -15,7 +15,7 @@ for p in (ROOT, PKG):
     if p not in sys.path:
         sys.path.insert(0, p)
 
-# max-abs / relative-L2 bounds for floating-point outputs
+# max-abs / relative-L2 bounds for floating-point outputs (the path's stated tolerance)
 MAX_ABS = 2e-3
 REL_L2 = 1e-3
 

@@ -930,7 +930,7 @@ def _mini_weights(tmp_path):
 
 @pytest.mark.parametrize("bits,k", [(4, 8), (2, 6)])
 def test_moe_block_from_model_weights(ctx, nh, tmp_path, bits, k):
-    """f1/f3: the model's per-layer MoE half in one launch (nmoe_moe_block)
+    """The model's per-layer MoE half in one launch (nmoe_moe_block)
     with the tensors nmoe_hip_load_model_weights made resident from a
     converter-format model_weights.bin: weighted post-attention RMSNorm, q4
     router, shared expert, experts, combine and the next layer's weighted
