@@ -148,3 +148,32 @@ def test_stack_loop_expired_wait_poisons_and_recovers(ctx, nh):
             _same(again, ref)
     finally:
         ctx._check(ctx.set_option(nh.OPT_SPIN_LIMIT, 0))
+
+
+@pytest.mark.parametrize("nl,xcd_local", [(1, 1), (4, 0)])
+def test_stack_loop_one_layer_and_without_die_local_words(ctx, nh, nl, xcd_local):
+    """A one-layer stack (no gather, no prefetch), and the loop with every
+    exchange word device-coherent (NMOE_HIP_OPT_XCD_LOCAL off, as on a device
+    whose blocks are not dealt round-robin over its dies): both bit for bit
+    the one-launch-per-layer form."""
+    bits, seed, k = 4, 61, 8
+    layers = [44 + i for i in range(nl)]
+    for layer in layers:
+        ctx.synth_layer(layer, bits, seed, SIGMA[bits])
+    routers, host = _routers(ctx, "bf16", layers, seed)
+    h0 = B.bf16_to_f32(B.syn_bf16(2048, seed, 96, 18, 1.0))
+    if xcd_local == 0:
+        ctx._check(ctx.set_option(nh.OPT_XCD_LOCAL, 0))
+    try:
+        rc, got = _run(ctx, nh, True, layers, routers, k, h0)
+        assert rc == nh.OK and ctx.device_status() == nh.OK
+        rc, per_layer = _run(ctx, nh, False, layers, routers, k, h0)
+        assert rc == nh.OK and ctx.device_status() == nh.OK
+    finally:
+        ctx.set_option(nh.OPT_XCD_LOCAL, 1)  # back on where the device's placement allows it
+    _same(got, per_layer)
+    H, I, Wt = got
+    pack = _pack(bits, seed, layers[-1], I[-1][:k])
+    want, oi, ow, _, _ = B.moe_block(pack, bits, host[-1], H[-2], k)
+    np.testing.assert_array_equal(I[-1], oi)
+    assert_close(H[-1], want, what="last layer")
