@@ -14,7 +14,9 @@
  *                       device 0 with the repository's synthetic layer,
  *                       router and input (seed 0, layer 0); writes idx[8],
  *                       w[8] and out[2048] to OUT for the test to check
- *                       against the oracle
+ *                       against the oracle; then a 3-layer nmoe_moe_stack
+ *                       on that layer, as one launch and as one launch per
+ *                       layer, which must agree bit for bit
  */
 #include <stddef.h>
 #include <stdint.h>
@@ -43,6 +45,10 @@ static int run_layout(void) {
     printf("shared %zu %zu %zu %zu %zu\n", sizeof(nmoe_hip_shared_expert), offsetof(nmoe_hip_shared_expert, gate),
            offsetof(nmoe_hip_shared_expert, up), offsetof(nmoe_hip_shared_expert, down),
            offsetof(nmoe_hip_shared_expert, score));
+    printf("block %zu %zu %zu %zu %zu %zu %zu %zu\n", sizeof(nmoe_hip_moe_block), offsetof(nmoe_hip_moe_block, router),
+           offsetof(nmoe_hip_moe_block, has_shared), offsetof(nmoe_hip_moe_block, shared),
+           offsetof(nmoe_hip_moe_block, post_norm), offsetof(nmoe_hip_moe_block, next_norm),
+           offsetof(nmoe_hip_moe_block, add_one), offsetof(nmoe_hip_moe_block, eps));
     return 0;
 }
 
@@ -137,10 +143,36 @@ static int run_gpu(const char *out_path) {
     int ok = f != NULL && fwrite(hi, sizeof hi, 1, f) == 1 && fwrite(hw, sizeof hw, 1, f) == 1 &&
              fwrite(ho, 2048 * sizeof(float), 1, f) == 1;
     if (f != NULL) fclose(f);
-    free(ho);
     printf("experts %u %u %u %u %u %u %u %u\n", hi[0], hi[1], hi[2], hi[3], hi[4], hi[5], hi[6], hi[7]);
+
+    /* the token's layer loop (three entries of layer 0, the step's out as
+     * h_0): one persistent launch, then one launch per layer */
+    enum { NL = 3 };
+    const int layers[NL] = {0, 0, 0};
+    const nmoe_hip_router routers[NL] = {r, r, r};
+    void *hseq = NULL, *iseq = NULL;
+    float *hh[2] = {NULL, NULL};
+    uint32_t si[2][NL * 8];
+    CHECK(nmoe_hip_register_state_buffer(ctx, "hseq", (NL + 1) * 2048 * 4, &hseq));
+    CHECK(nmoe_hip_register_state_buffer(ctx, "iseq", NL * 8 * 4, &iseq));
+    for (int loop = 0; loop < 2; loop++) {
+        hh[loop] = (float *)malloc((NL + 1) * 2048 * sizeof(float));
+        if (hh[loop] == NULL) return 1;
+        CHECK(nmoe_hip_set_option(ctx, NMOE_HIP_OPT_STACK_LOOP, loop));
+        CHECK(nmoe_hip_copy_to_device(ctx, hseq, ho, 2048 * sizeof(float)));
+        CHECK(nmoe_moe_stack(ctx, NL, layers, routers, 8, 1e-6f, (float *)hseq, (uint32_t *)iseq, NULL, NULL));
+        CHECK(nmoe_hip_synchronize(ctx));
+        CHECK(nmoe_hip_check_device_status(ctx));
+        CHECK(nmoe_hip_copy_to_host(ctx, hh[loop], hseq, (NL + 1) * 2048 * sizeof(float)));
+        CHECK(nmoe_hip_copy_to_host(ctx, si[loop], iseq, sizeof si[loop]));
+    }
+    const int same = memcmp(hh[0], hh[1], (NL + 1) * 2048 * sizeof(float)) == 0 && memcmp(si[0], si[1], sizeof si[0]) == 0;
+    printf("stack: one launch equals one launch per layer: %s\n", same ? "yes" : "NO");
+    free(hh[0]);
+    free(hh[1]);
+    free(ho);
     nmoe_hip_destroy(ctx);
-    return ok ? 0 : 1;
+    return ok && same ? 0 : 1;
 }
 
 int main(int argc, char **argv) {

@@ -63,6 +63,10 @@ def test_struct_layouts_match_binding(clients):
                                             ("kind", "num_experts", "w_bf16", "w_q4", "scales", "biases")]
     assert got["qtensor"] == [C.sizeof(Q)] + [getattr(Q, f).offset for f in ("w", "scales", "biases")]
     assert got["shared"] == [C.sizeof(S)] + [getattr(S, f).offset for f in ("gate", "up", "down", "score")]
+    M = nh.MoeBlock
+    assert got["block"] == [C.sizeof(M)] + [getattr(M, f).offset for f in
+                                           ("router", "has_shared", "shared", "post_norm", "next_norm", "add_one",
+                                            "eps")]
 
 
 def _kind(ctype_name):
@@ -109,12 +113,14 @@ def test_binding_signatures_match_header():
 def test_client_runs_a_layer_on_device(tmp_path):
     """One q4 top-8 decode step driven from C (synthetic layer, router and x
     of seed 0, zero h_mid): routing bit-exact with the oracle, output within
-    max-abs 2e-3 / rel-L2 1e-3."""
+    max-abs 2e-3 / rel-L2 1e-3; and a 3-layer stack from C, its one-launch
+    and per-layer forms bit for bit equal."""
     from oracle import binding as B
     assert os.path.exists(PREBUILT), "build first: python -c 'import __graft_entry__ as g; g.build()'"
     out = tmp_path / "step.bin"
     r = subprocess.run([PREBUILT, "gpu", str(out)], capture_output=True, text=True, timeout=120)
     assert r.returncode == 0, r.stdout + r.stderr
+    assert "stack: one launch equals one launch per layer: yes" in r.stdout
     raw = np.fromfile(out, np.uint8)
     idx, w, got = raw[:32].view(np.uint32), raw[32:64].view(np.float32), raw[64:].view(np.float32)
     W = B.syn_bf16(256 * 2048, 0, 0, 16, 0.02).reshape(256, 2048)
