@@ -46,6 +46,17 @@
  * (each block increments its own word once per launch, so all agree).  The
  * combine of a chunk polls the chunk's K-1 other partials in one block.
  * Idle groups (K < 8) exit after their router row.  Every wait is bounded.
+ *
+ * Forms (XMODE): x given (fp32 / bf16), x = RMSNorm(h) (XNORM), the whole
+ * MoE half of a model layer (XBLOCK: weighted norms, the shared expert in
+ * phases S1/S2, the next layer's norm N), and the layer loop of one token
+ * (XSTACK, nmoe_fused_stack_kernel): all layers in one launch, with the
+ * routing kept inside each die (the die's 32 blocks compute all 256 logits
+ * from router rows fetched into LDS a layer ahead), every block combining
+ * its chunk so that each die holds the whole next h, and the next layer's
+ * norm from the combining blocks' partial sums of squares.  In the loop,
+ * layer l's words carry epoch e + l, and the regions a die a layer ahead
+ * could overwrite early (logits, partials) come in two sets by layer parity.
  */
 #include <string.h>
 
