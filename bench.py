@@ -407,6 +407,90 @@ def run_grouped(pool, args, workload: str, NLg: int = 8) -> dict:
     }
 
 
+def _q4_tensor(rng, rows: int, cols: int, sigma: float):
+    """A q4 tensor in the model's stored form: codes uniform 0..15, scales
+    bf16(N(0, sigma)), biases bf16(-8 scale) (u32 words, bf16 scales, bf16
+    biases as one byte string)."""
+    w = rng.integers(0, 2**32, size=rows * cols // 8, dtype=np.uint64).astype(np.uint32)
+    sc = (rng.standard_normal(rows * cols // 64) * sigma).astype(np.float32)
+    s16 = ((sc.view(np.uint32).astype(np.uint64) + 0x7FFF + ((sc.view(np.uint32) >> 16) & 1)) >> 16).astype(np.uint16)
+    bi = (-8.0 * (s16.astype(np.uint32) << 16).view(np.float32)).astype(np.float32)
+    b16 = ((bi.view(np.uint32).astype(np.uint64) + 0x7FFF + ((bi.view(np.uint32) >> 16) & 1)) >> 16).astype(np.uint16)
+    return [w.tobytes(), s16.tobytes(), b16.tobytes()]
+
+
+def run_block(pool, args) -> dict:
+    """The model's per-layer MoE half as the drop-in runs it (nmoe_moe_block):
+    post-attention RMSNorm (1 + w), the q4 router, the shared expert (q4
+    gate/up/down and gate score), the routed experts, the combine and the
+    next layer's input norm, one launch per layer.  Each of the pool's
+    layers gets its own synthetic model tensors (seeded); step i runs layer
+    i % 40 on residual slot i % 320, after the warm-up's steps."""
+    nh, ctx, bits, k, NL = pool.nh, pool.ctx, args.bits, args.k, pool.NL
+    stream = ctx.stream
+    rng = np.random.default_rng(args.seed * 7919 + 11)
+    blks, keep = [], []
+    for layer in range(NL):
+        parts = {"router": _q4_tensor(rng, 256, 2048, 0.002), "gate": _q4_tensor(rng, 512, 2048, 0.002),
+                 "up": _q4_tensor(rng, 512, 2048, 0.002), "down": _q4_tensor(rng, 2048, 512, 0.004),
+                 "score": _q4_tensor(rng, 1, 2048, 0.002)}
+        norms = [(rng.standard_normal(2048) * 0.1).astype(np.float32) for _ in range(2)]
+        norms = [((n.view(np.uint32).astype(np.uint64) + 0x7FFF + ((n.view(np.uint32) >> 16) & 1)) >> 16)
+                 .astype(np.uint16).tobytes() for n in norms]
+        blob, offs = b"", {}
+        for name in ("router", "gate", "up", "down", "score"):
+            offs[name] = []
+            for piece in parts[name]:
+                blob += b"\0" * ((-len(blob)) % 256)
+                offs[name].append(len(blob))
+                blob += piece
+        for i, piece in enumerate(norms):
+            blob += b"\0" * ((-len(blob)) % 256)
+            offs[f"norm{i}"] = len(blob)
+            blob += piece
+        dev = ctx.to_device(np.frombuffer(blob, np.uint8), f"bench.block.{layer}")
+        keep.append(dev)
+        P = lambda name: [dev.ptr + o for o in offs[name]]
+        se = ctx.shared_expert_desc(P("gate"), P("up"), P("down"), P("score"))
+        blk = nh.MoeBlock(ctx.router_q4(*P("router")), 1, se, dev.ptr + offs["norm0"], dev.ptr + offs["norm1"],
+                          1, 1e-6)
+        blks.append(blk)
+    out, nx, di, dw = ctx.alloc(8192), ctx.alloc(8192), ctx.alloc(32), ctx.alloc(32)
+    ctx.sync()
+
+    def step(i):
+        ctx._check(ctx.moe_block(i % NL, blks[i % NL], pool.H.ptr + (i % pool.NR) * 8192, k, out, nx, di, dw,
+                                 stream=stream))
+
+    for i in range(args.warmup):
+        step(i)
+    ctx.sync()
+    if ctx.device_status() != 0:
+        raise SystemExit(f"device status error: {ctx.last_error()}")
+    ev = HipEvents()
+    e0, e1 = ev.create(2)
+    ev.record(e0, stream)
+    for i in range(args.steps):
+        step(args.warmup + i)
+    ev.record(e1, stream)
+    ms = ev.ms(e0, e1) / args.steps
+    ctx.sync()
+    if ctx.device_status() != 0:
+        raise SystemExit(f"device status error: {ctx.last_error()}")
+    ev.destroy([e0, e1])
+    shared_bytes = 2 * (512 * 1024 + 2 * 512 * 32 * 2) + (2048 * 256 + 2 * 2048 * 8 * 2) + (1024 + 2 * 32 * 2)
+    B = k * EXPERT_BYTES[bits] + ROUTER_Q4_BYTES + shared_bytes + 2 * 4096 + 3 * 8192 + 64
+    gbs = B / (ms * 1e-3) / 1e9
+    return {"metric": f"routed-MoE block tokens/s (the model's per-layer MoE half: q4 router, shared expert, "
+                      f"norms; q{bits}, top-{k}, batch 1, 1 GPU)",
+            "value": round(1e3 / ms, 1), "unit": "tokens/s", "us_per_layer": round(ms * 1e3, 3),
+            "hbm_gbps": round(gbs, 1),
+            "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(gbs / HBM_PEAK_GBS, 4)},
+            "config": {"workload": "block", "layers_rotated": NL, "bits": bits, "k": k, "bytes_per_step": B,
+                       "entry_point": "nmoe_moe_block"}}
+
+
 def run_stream(pool, args) -> dict:
     """The streaming ceiling of the c1 step: nmoe_hip_read_probe over the
     bytes of 8 q4 experts (14,155,776 B), all loads in flight at once, one
@@ -455,11 +539,12 @@ def main():
                     help="only run 5 device-to-device copies of MIB MiB (counter calibration) and exit")
     ap.add_argument("--router", default="bf16", choices=("bf16", "q4"),
                     help="c1/c3: the benchmark configs' dense bf16 router (default) or the model's q4 router")
-    ap.add_argument("--workload", default="c1", choices=("c1", "c3", "c4", "c5", "stream"),
+    ap.add_argument("--workload", default="c1", choices=("c1", "c3", "c4", "c5", "stream", "block"),
                     help="c1: the headline single-layer decode step, with c3 and c5 sub-objects (default); "
                          "c3 / c4 / c5 alone: 40-layer stack of 128 tokens / batched decode of 64 Zipf-routed "
                          "tokens / 2048-token prefill on the grouped matrix-core path; stream: the streaming ceiling "
-                         "of the c1 step's expert bytes (nmoe_hip_read_probe)")
+                         "of the c1 step's expert bytes (nmoe_hip_read_probe); block: the model's per-layer MoE "
+                         "half (nmoe_moe_block)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -486,6 +571,8 @@ def main():
         result = run_c3(pool, args)
     elif args.workload == "stream":
         result = run_stream(pool, args)
+    elif args.workload == "block":
+        result = run_block(pool, args)
     elif args.workload in ("c4", "c5"):
         result = run_grouped(pool, args, args.workload)
     else:

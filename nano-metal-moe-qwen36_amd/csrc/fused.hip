@@ -383,6 +383,12 @@ __device__ __forceinline__ void nmoe_fused_body(nmoe_fused_args a, const nmoe_st
     __shared__ float s_shd[BLK ? NMOE_FUSED_CHUNK : 1];
     __shared__ float s_shg[2], s_sgr[1];
     __shared__ uint32_t s_shok, s_sacnt;
+    /* XBLOCK, combining block: the chunk's 64 shared-down rows (codes, then
+     * their scales, then their biases), loaded straight into LDS while the
+     * logits are exchanged: read after the routing, they would queue behind
+     * the expert stream.  s_shdok: they are in. */
+    __shared__ __align__(16) uint8_t s_shdw[BLK ? NMOE_FUSED_CHUNK * (NMOE_INTER / 2 + 2 * 2 * NMOE_INTER / NMOE_GROUP) : 16];
+    __shared__ uint32_t s_shdok;
     /* XSTACK: h of this layer and the next (the gather of the next one
      * never touches the rows the combine still reads), the layer's router
      * rows 8j .. 8j+7 (fetched a layer ahead; bf16: 8 x 4 KB; q4: 8 x 1 KB
@@ -397,7 +403,10 @@ __device__ __forceinline__ void nmoe_fused_body(nmoe_fused_args a, const nmoe_st
     const bool cwave = wave == NMOE_FUSED_CTRL;
     const int g = blockIdx.x % NMOE_FUSED_GROUPS, j = blockIdx.x / NMOE_FUSED_GROUPS;
     const int k = a.k;
-    const bool comb = STK || g == j % k; /* this block combines rows 64j .. 64j+63 (XSTACK: each die does) */
+    /* this block combines rows 64j .. 64j+63: XSTACK every die; XBLOCK the
+     * blocks of group 0, all on one die, so that the next-layer norm's
+     * partial sums never leave it; otherwise group j % k */
+    const bool comb = STK || (BLK ? g == 0 : g == j % k);
     const bool has_sh = BLK && a.sh.gate.w != NULL;
     uint32_t *status = a.sync + NMOE_SYNC_STATUS;
 
@@ -416,6 +425,17 @@ __device__ __forceinline__ void nmoe_fused_body(nmoe_fused_args a, const nmoe_st
     const float hm = STK ? 0.0f : !BLK || comb ? a.h_mid[crow] : 0.0f;
     const float sh = !BLK && a.shared_out != NULL ? a.shared_out[crow] : 0.0f;
     const float sgr = !BLK && a.shared_out != NULL ? a.shared_gate_raw[0] : 0.0f;
+    /* XBLOCK: the norm weights this thread multiplies by, loaded with the
+     * other independent loads (read where they are used, each is a memory
+     * round trip in the middle of the norm and of the next-layer norm) */
+    float nwv[BLK ? 8 : 1];
+    float nxw = 1.0f;
+    if (BLK) {
+        if (tid < NMOE_HIDDEN / 8)
+#pragma unroll
+            for (int i = 0; i < 8; i++) nwv[i] = nmoe_norm_weight(a.norm_w, 8 * tid + i, a.add_one);
+        if (comb && tid < NMOE_FUSED_CHUNK) nxw = nmoe_norm_weight(a.next_w, crow, a.add_one);
+    }
     uint4 wv0[4]; /* the router row (not XSTACK: there it comes from LDS) */
     uint32_t wq0[4];
     uint16_t rsr0[4], rbr0[4];
@@ -544,6 +564,7 @@ __device__ __forceinline__ void nmoe_fused_body(nmoe_fused_args a, const nmoe_st
             s_bad = 0u;
             s_shok = 0u;
             s_sacnt = 0u;
+            s_shdok = 0u;
         }
         s_ncand = 0u;
         s_confirm = 0u;
@@ -564,11 +585,13 @@ __device__ __forceinline__ void nmoe_fused_body(nmoe_fused_args a, const nmoe_st
                 const int c0 = 8 * tid + 4 * q;
                 float4 v;
                 nmoe_x_cols<XMODE>(hsrc, c0, 4, rinv, &v.x);
-                if (BLK && a.norm_w != NULL) { /* math.m:63: (h / rms) * weight */
-                    v.x = v.x * nmoe_norm_weight(a.norm_w, c0, a.add_one);
-                    v.y = v.y * nmoe_norm_weight(a.norm_w, c0 + 1, a.add_one);
-                    v.z = v.z * nmoe_norm_weight(a.norm_w, c0 + 2, a.add_one);
-                    v.w = v.w * nmoe_norm_weight(a.norm_w, c0 + 3, a.add_one);
+                if constexpr (BLK) {
+                    if (a.norm_w != NULL) { /* math.m:63: (h / rms) * weight */
+                        v.x = v.x * nwv[4 * q];
+                        v.y = v.y * nwv[4 * q + 1];
+                        v.z = v.z * nwv[4 * q + 2];
+                        v.w = v.w * nwv[4 * q + 3];
+                    }
                 }
                 ((float4 *)s_h)[nmoe_act_slot<Q::CPL / 4>(c0) / 4] = v;
             }
@@ -612,47 +635,76 @@ __device__ __forceinline__ void nmoe_fused_body(nmoe_fused_args a, const nmoe_st
     }
 
     /* ---- S2 (XBLOCK, combining block, both control wavefronts after their
-     * routing): all 512 shared activations into LDS, then this chunk's 64
-     * shared-down rows (kernels.metal:1520-1537), 32 per wavefront: 16 lanes
-     * a row (32 columns each, fma(fma(q, s, b), act, acc) as the shared-down
-     * kernel), four rows a step */
-    auto shared_down = [&](int half) {
-        const uint64_t *ps[4];
-        float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+     * routing): this chunk's 64 shared-down rows (kernels.metal:1520-1537)
+     * from LDS, rows r0 .. r0 + 4n - 1 by one wavefront: 16 lanes a row (32
+     * columns each, fma(fma(q, s, b), act, acc) as the shared-down kernel),
+     * four rows a step.  The candidate wavefront, free first, brings all
+     * 512 shared activations into LDS. */
+    auto shared_down = [&](int r0, int n) {
+        if (cwave) {
+            const uint64_t *ps[8];
+            float v[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int q = 0; q < 4; q++) ps[q] = a.xch + NMOE_XCH_SHACT + NMOE_XCH_SP * (256 * half + lane + 64 * q);
-        nmoe_poll<4>(ps, epoch, v, status, &s_bad, a.spin);
+            for (int q = 0; q < 8; q++) ps[q] = a.xch + NMOE_XCH_SHACT + NMOE_XCH_SP * (lane + 64 * q);
+            nmoe_poll<8>(ps, epoch, v, status, &s_bad, a.spin);
 #pragma unroll
-        for (int q = 0; q < 4; q++) s_sact[256 * half + lane + 64 * q] = v[q];
-        if (lane == 0) __hip_atomic_fetch_add(&s_sacnt, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
-        const int dl16 = lane & 15, rsub = lane >> 4;
-        uint4 dw[8];
-        uint16_t ds[8], db[8];
-#pragma unroll
-        for (int st = 0; st < 8; st++) {
-            const int row = j * NMOE_FUSED_CHUNK + 32 * half + 4 * st + rsub;
-            dw[st] = *(const uint4 *)(a.sh.down.w + (size_t)row * (NMOE_INTER / 8) + 4 * dl16);
-            ds[st] = a.sh.down.scales[(size_t)row * (NMOE_INTER / NMOE_GROUP) + dl16 / 2];
-            db[st] = a.sh.down.biases[(size_t)row * (NMOE_INTER / NMOE_GROUP) + dl16 / 2];
+            for (int q = 0; q < 8; q++) s_sact[lane + 64 * q] = v[q];
+            if (lane == 0) __hip_atomic_store(&s_sacnt, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
         }
-        nmoe_lds_wait_above(&s_sacnt, 1u, status, &s_bad, a.spin); /* the other half is in */
+        nmoe_lds_wait_above(&s_shdok, 0u, status, &s_bad, a.spin); /* the rows */
+        nmoe_lds_wait_above(&s_sacnt, 0u, status, &s_bad, a.spin); /* the activations */
+        const int dl16 = lane & 15, rsub = lane >> 4;
+        const uint16_t *sds = (const uint16_t *)(s_shdw + NMOE_FUSED_CHUNK * (NMOE_INTER / 2));
+        const uint16_t *sdb = sds + NMOE_FUSED_CHUNK * (NMOE_INTER / NMOE_GROUP);
         float av[32];
 #pragma unroll
         for (int c = 0; c < 8; c++) *(float4 *)(av + 4 * c) = ((const float4 *)s_sact)[8 * dl16 + c];
-#pragma unroll
-        for (int st = 0; st < 8; st++) {
-            const float sc = nmoe_bf16f(ds[st]), bi = nmoe_bf16f(db[st]);
-            const uint32_t wd[4] = {dw[st].x, dw[st].y, dw[st].z, dw[st].w};
+        for (int st = 0; st < n; st++) {
+            const int rr = r0 + 4 * st + rsub;
+            const uint4 dw = *(const uint4 *)(s_shdw + rr * (NMOE_INTER / 2) + 16 * dl16);
+            const float sc = nmoe_bf16f(sds[rr * (NMOE_INTER / NMOE_GROUP) + dl16 / 2]);
+            const float bi = nmoe_bf16f(sdb[rr * (NMOE_INTER / NMOE_GROUP) + dl16 / 2]);
+            const uint32_t wd[4] = {dw.x, dw.y, dw.z, dw.w};
             float acc = 0.0f;
 #pragma unroll
             for (int i = 0; i < 4; i++)
 #pragma unroll
-                for (int n = 0; n < 8; n++)
-                    acc = __builtin_fmaf(__builtin_fmaf((float)((wd[i] >> (4 * n)) & 0xFu), sc, bi), av[8 * i + n], acc);
+                for (int m = 0; m < 8; m++)
+                    acc = __builtin_fmaf(__builtin_fmaf((float)((wd[i] >> (4 * m)) & 0xFu), sc, bi), av[8 * i + m], acc);
             acc = nmoe_dpp_group_sum<16>(acc);
-            if (dl16 == 0) s_shd[32 * half + 4 * st + rsub] = acc;
+            if (dl16 == 0) s_shd[rr] = acc;
         }
     };
+    if (has_sh && comb && wave == NMOE_FUSED_EXACT) {
+        /* the chunk's shared-down rows into LDS (18 KB: codes, scales,
+         * biases, each contiguous over rows 64j .. 64j+63), by loads that
+         * write LDS directly, while the logits are exchanged (at the start
+         * they would delay the loads of h).  This wavefront is idle until
+         * the logits are in, long after these loads are. */
+        typedef __attribute__((address_space(3))) void nmoe_lds_void_sd;
+        const size_t r0 = (size_t)j * NMOE_FUSED_CHUNK;
+        const uint8_t *cw = (const uint8_t *)a.sh.down.w + r0 * (NMOE_INTER / 2);
+        const uint8_t *cs = (const uint8_t *)(a.sh.down.scales + r0 * (NMOE_INTER / NMOE_GROUP));
+        const uint8_t *cb = (const uint8_t *)(a.sh.down.biases + r0 * (NMOE_INTER / NMOE_GROUP));
+        constexpr int WB = NMOE_FUSED_CHUNK * (NMOE_INTER / 2), SB = NMOE_FUSED_CHUNK * (NMOE_INTER / NMOE_GROUP) * 2;
+        static_assert(WB % 1024 == 0 && SB == 1024, "one 16-byte load per lane covers 1 KB");
+#pragma unroll
+        for (int i = 0; i < WB / 1024; i++)
+            __builtin_amdgcn_global_load_lds(cw + 1024 * i + 16 * lane, (nmoe_lds_void_sd *)(s_shdw + 1024 * i), 16, 0, 0);
+        if ((((uintptr_t)cs | (uintptr_t)cb) & 15u) == 0u) {
+            __builtin_amdgcn_global_load_lds(cs + 16 * lane, (nmoe_lds_void_sd *)(s_shdw + WB), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(cb + 16 * lane, (nmoe_lds_void_sd *)(s_shdw + WB + SB), 16, 0, 0);
+        } else { /* scales and biases need only be 2-byte aligned: 2-byte loads */
+            uint16_t *d = (uint16_t *)(s_shdw + WB);
+#pragma unroll
+            for (int q = 0; q < SB / 128; q++) {
+                d[lane + 64 * q] = ((const uint16_t *)cs)[lane + 64 * q];
+                d[SB / 2 + lane + 64 * q] = ((const uint16_t *)cb)[lane + 64 * q];
+            }
+        }
+        __builtin_amdgcn_s_waitcnt(0);
+        if (lane == 0) __hip_atomic_store(&s_shdok, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
 
     if (STK && !ctrl) {
         /* ---- R (XSTACK, worker wavefront w): router row 8j + w from LDS,
@@ -758,7 +810,12 @@ __device__ __forceinline__ void nmoe_fused_body(nmoe_fused_args a, const nmoe_st
                 }
             }
             if (lane == 0) __hip_atomic_store(&s_ncand, (uint32_t)k, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
-            if (has_sh && comb) shared_down(0);
+            if (has_sh && comb) {
+                /* off the routing's critical path: at the workers' priority,
+                 * whose expert loads and SwiGLU share these SIMDs */
+                __builtin_amdgcn_s_setprio(0);
+                shared_down(0, 8);
+            }
         }
     }
     if (ROUTE && wave == NMOE_FUSED_EXACT && (g < k || STK)) {
@@ -880,7 +937,10 @@ __device__ __forceinline__ void nmoe_fused_body(nmoe_fused_args a, const nmoe_st
             }
         }
         if (lane == 0) __hip_atomic_store(&s_confirm, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
-        if (has_sh && comb) shared_down(1);
+        if (has_sh && comb) {
+            __builtin_amdgcn_s_setprio(0);
+            shared_down(32, 8);
+        }
         /* XSTACK: the next layer's router row, while this layer streams
          * (the candidate wavefront read this one before the logits came) */
         if (STK && ly + 1 < nl) load_rrow(s_stk[4 * (ly + 1) + 1], s_stk[4 * (ly + 1) + 2], s_stk[4 * (ly + 1) + 3]);
@@ -1121,17 +1181,9 @@ __device__ __forceinline__ void nmoe_fused_body(nmoe_fused_args a, const nmoe_st
                     nmoe_st_tagged_die(xhg + row, epoch, rv);
                 else
                     nmoe_st_tagged(xhg + row, epoch, rv);
-                /* and the sum of their squares for the next layer's norm:
-                 * exact squares, a tree of depth 6 (4 DPP levels in a row
-                 * of 16 lanes, 2 over the rows); the 32 partials' tree adds
-                 * 5 (nmoe_mean_sq_from_sum allows 11) */
-                double sq = (double)rv * (double)rv;
-                sq = sq + nmoe_dpp_d<NMOE_DPP_XOR1>(sq);
-                sq = sq + nmoe_dpp_d<NMOE_DPP_XOR2>(sq);
-                sq = sq + nmoe_dpp_d<NMOE_DPP_HALF_MIRROR>(sq);
-                sq = sq + nmoe_dpp_d<NMOE_DPP_MIRROR>(sq);
-                const double ps =
-                    (nmoe_readlane_d(sq, 0) + nmoe_readlane_d(sq, 16)) + (nmoe_readlane_d(sq, 32) + nmoe_readlane_d(sq, 48));
+                /* and the sum of their squares for the next layer's norm
+                 * (a tree of depth 6; the 32 partials' tree adds 5) */
+                const double ps = nmoe_wave_sq_tree(rv);
                 if (tid < 2) {
                     const uint64_t pb = __builtin_bit_cast(uint64_t, ps);
                     const uint32_t half = tid == 0 ? (uint32_t)pb : (uint32_t)(pb >> 32);
@@ -1146,33 +1198,36 @@ __device__ __forceinline__ void nmoe_fused_body(nmoe_fused_args a, const nmoe_st
     if (BLK && comb && a.next_x != NULL && wave == 0) {
         /* ---- N (XBLOCK): the next layer's input norm of out
          * (runtime.m:2893-2900, math.m:34-65).  Each combining block
-         * publishes the double-double sum of its 64 squares (exact) and its
-         * rows; each sums the 32 partials in one fixed order, so all reach
-         * the same mean square, the float math.m's long double sum rounds
-         * to, or replay that x87 sum over all 2048 rows in index order. */
-        double S, Cc;
-        nmoe_wave_dd_sum((double)rv * (double)rv, 0.0, S, Cc);
+         * publishes the sum of its 64 squares (a tree of depth 6) and its
+         * rows; each adds the 32 partials in one fixed order (depth 5), so
+         * all reach the same mean square: the float math.m's long double
+         * sum rounds to where no rounding midpoint is near, or else the
+         * replay of that x87 sum over all 2048 rows in index order.  The
+         * combining blocks all run on one die when blocks are dealt
+         * round-robin over the dies (xcd_local): then these words stay in
+         * that die's L2. */
+        const double sq = nmoe_wave_sq_tree(rv);
         uint64_t *nsq = a.xch + NMOE_XCH_NSQ;
-        if (lane == 0) {
-            const uint64_t sb = __builtin_bit_cast(uint64_t, S), cb = __builtin_bit_cast(uint64_t, Cc);
-            nmoe_st_tagged_u32(nsq + NMOE_XCH_SP * j + 0, epoch, (uint32_t)sb);
-            nmoe_st_tagged_u32(nsq + NMOE_XCH_SP * j + 1, epoch, (uint32_t)(sb >> 32));
-            nmoe_st_tagged_u32(nsq + NMOE_XCH_SP * j + 2, epoch, (uint32_t)cb);
-            nmoe_st_tagged_u32(nsq + NMOE_XCH_SP * j + 3, epoch, (uint32_t)(cb >> 32));
+        const bool dl = a.xcd_local != 0;
+        auto put = [&](uint64_t *p, uint32_t v) {
+            if (dl)
+                nmoe_st_tagged_die(p, epoch, __uint_as_float(v));
+            else
+                nmoe_st_tagged_u32(p, epoch, v);
+        };
+        if (lane < 2) {
+            const uint64_t sb = __builtin_bit_cast(uint64_t, sq);
+            put(nsq + 2 * j + lane, lane == 0 ? (uint32_t)sb : (uint32_t)(sb >> 32));
         }
-        nmoe_st_tagged(a.xch + NMOE_XCH_NOUT + row, epoch, rv);
+        put(a.xch + NMOE_XCH_NOUT + row, __float_as_uint(rv));
         const int src = lane & (NMOE_FUSED_GROUP_BLOCKS - 1); /* lanes 32..63 poll nothing */
-        const uint64_t *pq[4] = {nsq + NMOE_XCH_SP * src, nsq + NMOE_XCH_SP * src + 1, nsq + NMOE_XCH_SP * src + 2,
-                                 nsq + NMOE_XCH_SP * src + 3};
-        float pv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-        nmoe_poll<4>(pq, epoch, pv, status, &s_bad, a.spin, false, lane < NMOE_FUSED_GROUP_BLOCKS ? 0xFu : 0u);
-        double ps = 0.0, pc = 0.0;
-        if (lane < NMOE_FUSED_GROUP_BLOCKS) {
-            ps = __builtin_bit_cast(double, ((uint64_t)__float_as_uint(pv[1]) << 32) | __float_as_uint(pv[0]));
-            pc = __builtin_bit_cast(double, ((uint64_t)__float_as_uint(pv[3]) << 32) | __float_as_uint(pv[2]));
-        }
-        nmoe_wave_dd_sum(ps, pc, S, Cc);
-        float mean = nmoe_dd_mean_float(S, Cc);
+        const uint64_t *pq[2] = {nsq + 2 * src, nsq + 2 * src + 1};
+        float pv[2] = {0.0f, 0.0f};
+        nmoe_poll<2>(pq, epoch, pv, status, &s_bad, a.spin, dl, lane < NMOE_FUSED_GROUP_BLOCKS ? 3u : 0u);
+        const double ps = lane < NMOE_FUSED_GROUP_BLOCKS
+                              ? __builtin_bit_cast(double, ((uint64_t)__float_as_uint(pv[1]) << 32) | __float_as_uint(pv[0]))
+                              : 0.0;
+        float mean = nmoe_mean_sq_from_sum(nmoe_sum32_tree(ps));
         if (mean < 0.0f) {
             /* near a rounding midpoint (or tiny values): all 2048 rows, the
              * x87 running sum in index order (s_h is free: x is consumed) */
@@ -1181,7 +1236,7 @@ __device__ __forceinline__ void nmoe_fused_body(nmoe_fused_args a, const nmoe_st
                                          a.xch + NMOE_XCH_NOUT + i0 + lane + 128,
                                          a.xch + NMOE_XCH_NOUT + i0 + lane + 192};
                 float ov[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-                nmoe_poll<4>(po, epoch, ov, status, &s_bad, a.spin);
+                nmoe_poll<4>(po, epoch, ov, status, &s_bad, a.spin, dl);
 #pragma unroll
                 for (int q = 0; q < 4; q++) s_h[i0 + lane + 64 * q] = ov[q];
             }
@@ -1200,7 +1255,7 @@ __device__ __forceinline__ void nmoe_fused_body(nmoe_fused_args a, const nmoe_st
         float rms = nmoe_sqrtf_rn(mean + a.eps);
         rms = rms == 0.0f ? 1.0f : rms;
         float xn = (float)((double)rv * (1.0 / (double)rms));
-        xn = a.next_w != NULL ? xn * nmoe_norm_weight(a.next_w, row, a.add_one) : xn;
+        xn = a.next_w != NULL ? xn * nxw : xn;
         a.next_x[row] = nmoe_lds_flag(&s_bad) ? __builtin_nanf("") : xn; /* a partial that never came */
     }
     if (ROUTE && blockIdx.x == 0 && cwave) {
@@ -1230,14 +1285,10 @@ __device__ __forceinline__ void nmoe_fused_body(nmoe_fused_args a, const nmoe_st
         const uint64_t *pq[2] = {xhg + NMOE_HIDDEN + 2 * src, xhg + NMOE_HIDDEN + 2 * src + 1};
         float pv[2] = {0.0f, 0.0f};
         nmoe_poll<2>(pq, epoch, pv, status, &s_bad, a.spin, a.xcd_local != 0, lane < NMOE_FUSED_GROUP_BLOCKS ? 3u : 0u);
-        double ps = lane < NMOE_FUSED_GROUP_BLOCKS
-                        ? __builtin_bit_cast(double, ((uint64_t)__float_as_uint(pv[1]) << 32) | __float_as_uint(pv[0]))
-                        : 0.0;
-        ps = ps + nmoe_dpp_d<NMOE_DPP_XOR1>(ps);
-        ps = ps + nmoe_dpp_d<NMOE_DPP_XOR2>(ps);
-        ps = ps + nmoe_dpp_d<NMOE_DPP_HALF_MIRROR>(ps);
-        ps = ps + nmoe_dpp_d<NMOE_DPP_MIRROR>(ps);
-        const float mean = nmoe_mean_sq_from_sum(nmoe_readlane_d(ps, 0) + nmoe_readlane_d(ps, 16));
+        const double ps = lane < NMOE_FUSED_GROUP_BLOCKS
+                              ? __builtin_bit_cast(double, ((uint64_t)__float_as_uint(pv[1]) << 32) | __float_as_uint(pv[0]))
+                              : 0.0;
+        const float mean = nmoe_mean_sq_from_sum(nmoe_sum32_tree(ps));
         double ri = -1.0;
         if (mean >= 0.0f) {
             float rms = nmoe_sqrtf_rn(mean + a.eps);

@@ -474,12 +474,6 @@ __device__ __forceinline__ float nmoe_tag_val(uint64_t w) { return __uint_as_flo
 
 /* ------------------------------------------------------------ RMSNorm */
 
-__device__ __forceinline__ void nmoe_two_sum(double a, double b, double &s, double &e) {
-    s = a + b;
-    double bb = s - a;
-    e = (a - (s - bb)) + (b - bb);
-}
-
 template <int CTRL>
 __device__ __forceinline__ double nmoe_dpp_d(double v) {
     uint64_t u = __builtin_bit_cast(uint64_t, v);
@@ -494,49 +488,29 @@ __device__ __forceinline__ double nmoe_readlane_d(double v, int lane) {
     return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
 }
 
-__device__ __forceinline__ void nmoe_dd_add(double &s, double &c, double s2, double c2) {
-    double e;
-    nmoe_two_sum(s, s2, s, e);
-    c = c + c2 + e;
+/* The sum of v * v over a wavefront, one v per lane: exact squares (a
+ * float times a float fits a double), added as a tree of depth 6 (4 DPP
+ * levels within each row of 16 lanes, then rows (0 + 16) + (32 + 48)).
+ * Uniform.  Every lane must be active. */
+__device__ __forceinline__ double nmoe_wave_sq_tree(float v) {
+    double sq = (double)v * (double)v;
+    sq = sq + nmoe_dpp_d<NMOE_DPP_XOR1>(sq);
+    sq = sq + nmoe_dpp_d<NMOE_DPP_XOR2>(sq);
+    sq = sq + nmoe_dpp_d<NMOE_DPP_HALF_MIRROR>(sq);
+    sq = sq + nmoe_dpp_d<NMOE_DPP_MIRROR>(sq);
+    return (nmoe_readlane_d(sq, 0) + nmoe_readlane_d(sq, 16)) + (nmoe_readlane_d(sq, 32) + nmoe_readlane_d(sq, 48));
 }
 
-/* The double-double sum (S, C) of the wavefront's (s, c) pairs, in a fixed
- * order (rows of 16 lanes by DPP, then the four rows in order); uniform. */
-__device__ __forceinline__ void nmoe_wave_dd_sum(double s, double c, double &S, double &C) {
-    nmoe_dd_add(s, c, nmoe_dpp_d<NMOE_DPP_XOR1>(s), nmoe_dpp_d<NMOE_DPP_XOR1>(c));
-    nmoe_dd_add(s, c, nmoe_dpp_d<NMOE_DPP_XOR2>(s), nmoe_dpp_d<NMOE_DPP_XOR2>(c));
-    nmoe_dd_add(s, c, nmoe_dpp_d<NMOE_DPP_HALF_MIRROR>(s), nmoe_dpp_d<NMOE_DPP_HALF_MIRROR>(c));
-    nmoe_dd_add(s, c, nmoe_dpp_d<NMOE_DPP_MIRROR>(s), nmoe_dpp_d<NMOE_DPP_MIRROR>(c));
-    S = nmoe_readlane_d(s, 0);
-    C = nmoe_readlane_d(c, 0);
-    nmoe_dd_add(S, C, nmoe_readlane_d(s, 16), nmoe_readlane_d(c, 16));
-    nmoe_dd_add(S, C, nmoe_readlane_d(s, 32), nmoe_readlane_d(c, 32));
-    nmoe_dd_add(S, C, nmoe_readlane_d(s, 48), nmoe_readlane_d(c, 48));
-}
-
-/* math.m:46-52's mean square as a float, from the sum of the 2048 squares
- * as a double-double S + C (exact to far below 2^-90 relative): math.m sums
- * them in an x87 long double (64-bit significand), within 2^-53 relative of
- * the exact sum, so when no float rounding midpoint lies within 2^-51 of the
- * exact mean, both round to the same float.  Returns that float, or -1 when
- * the caller must replay the x87 sum (a near-midpoint, or tiny values). */
-__device__ __forceinline__ float nmoe_dd_mean_float(double S, double Cc) {
-    double hi, lo;
-    nmoe_two_sum(S, Cc, hi, lo);
-    hi *= 1.0 / 2048.0; /* exact */
-    lo *= 1.0 / 2048.0;
-    const float f = (float)hi;
-    const uint32_t fb = __float_as_uint(f);
-    int fast = 0;
-    if (hi == 0.0 && lo == 0.0) {
-        fast = 1;
-    } else if (fb >= 0x00800000u && fb < 0x7f000000u) {
-        const double up = ((double)f + (double)__uint_as_float(fb + 1u)) * 0.5;
-        const double dn = ((double)f + (double)__uint_as_float(fb - 1u)) * 0.5;
-        const double margin = hi * 0x1p-51;
-        fast = ((up - hi) - lo) > margin && ((hi - dn) + lo) > margin;
-    }
-    return fast ? f : -1.0f;
+/* The sum of 32 doubles held by lanes 0..31 (the other lanes hold 0), a
+ * tree of depth 5 in a fixed order.  Uniform.  Every lane must be active.
+ * 32 partials from nmoe_wave_sq_tree make a tree of depth 11 over 2048
+ * squares, the depth nmoe_mean_sq_from_sum allows for. */
+__device__ __forceinline__ double nmoe_sum32_tree(double ps) {
+    ps = ps + nmoe_dpp_d<NMOE_DPP_XOR1>(ps);
+    ps = ps + nmoe_dpp_d<NMOE_DPP_XOR2>(ps);
+    ps = ps + nmoe_dpp_d<NMOE_DPP_HALF_MIRROR>(ps);
+    ps = ps + nmoe_dpp_d<NMOE_DPP_MIRROR>(ps);
+    return nmoe_readlane_d(ps, 0) + nmoe_readlane_d(ps, 16);
 }
 
 /* rms of math.m:34-65 (unit weight) over the 2048 fp32 values h, by a whole
