@@ -71,6 +71,7 @@ static __constant__ uint64_t nmoe_fused_exp2_tab[32] = NMOE_EXP2_TAB32;
 #define NMOE_FUSED_GROUP_BLOCKS (NMOE_FUSED_BLOCKS / NMOE_FUSED_GROUPS) /* 32 */
 #define NMOE_FUSED_CHUNK (NMOE_HIDDEN / NMOE_FUSED_GROUP_BLOCKS)         /* 64 output rows per block */
 #define NMOE_FUSED_GU_ROWS (NMOE_INTER / NMOE_FUSED_GROUP_BLOCKS)        /* 16 gate/up rows per block */
+#define NMOE_FUSED_S2_ROWS (NMOE_FUSED_CHUNK / NMOE_FUSED_GROUPS)        /* 8 shared-down rows per block */
 #define NMOE_FUSED_WORKERS 8 /* worker wavefronts per block, plus two control wavefronts */
 #define NMOE_FUSED_THREADS (64 * (NMOE_FUSED_WORKERS + 2))
 #define NMOE_FUSED_CTRL NMOE_FUSED_WORKERS        /* router row, candidate selection */
@@ -93,14 +94,16 @@ static __constant__ uint64_t nmoe_fused_exp2_tab[32] = NMOE_EXP2_TAB32;
 #define NMOE_XCH_WORDS (NMOE_XCH_YPART + NMOE_FUSED_GROUPS * NMOE_HIDDEN) /* tagged partials, polled by one block */
 static_assert(NMOE_XCH_WORDS * sizeof(uint64_t) == NMOE_FUSED_XCH_BYTES, "exchange size as the host allocates it");
 /* The whole-block form (XBLOCK) adds: the shared expert's activations
- * [512] (64 B apart, polled by the 32 combining blocks), each combining
- * block's double-double sum of squares of its output rows (4 words on a
- * 64-byte line of its own) and its output rows themselves (dense, read only
- * on the exact-replay path of the next-layer norm). */
+ * [512] (dense: every block reads all of them once, mostly after they are
+ * written), each combining block's sum of squares of its output rows (a
+ * double as two words), its output rows themselves (read only on the
+ * exact-replay path of the next-layer norm) and the shared expert's down
+ * rows [2048] (each polled by the one combining block of its chunk). */
 #define NMOE_XCH_SHACT NMOE_XCH_WORDS
-#define NMOE_XCH_NSQ (NMOE_XCH_SHACT + NMOE_XCH_SP * NMOE_INTER)
-#define NMOE_XCH_NOUT (NMOE_XCH_NSQ + NMOE_XCH_SP * NMOE_FUSED_GROUP_BLOCKS)
-#define NMOE_XCH_WORDS_BLOCK (NMOE_XCH_NOUT + NMOE_HIDDEN)
+#define NMOE_XCH_NSQ (NMOE_XCH_SHACT + NMOE_INTER)
+#define NMOE_XCH_NOUT (NMOE_XCH_NSQ + 2 * NMOE_FUSED_GROUP_BLOCKS)
+#define NMOE_XCH_SHD (NMOE_XCH_NOUT + NMOE_HIDDEN)
+#define NMOE_XCH_WORDS_BLOCK (NMOE_XCH_SHD + NMOE_HIDDEN)
 static_assert(NMOE_XCH_WORDS_BLOCK * sizeof(uint64_t) == NMOE_FUSED_XCH_BYTES_BLOCK, "the whole-block exchange size");
 /* The stack form (XSTACK) routes within each die: per die and layer
  * parity the 256 logits its 32 blocks compute (8 each, dense), per die
@@ -380,15 +383,13 @@ __device__ __forceinline__ void nmoe_fused_body(nmoe_fused_args a, const nmoe_st
      * combining block's copy of all 512 activations, its 64 shared-down
      * rows and gate score) and the hand-offs between the wavefronts */
     __shared__ __align__(16) float s_sact[BLK ? NMOE_INTER : 4];
-    __shared__ float s_shd[BLK ? NMOE_FUSED_CHUNK : 1];
     __shared__ float s_shg[2], s_sgr[1];
-    __shared__ uint32_t s_shok, s_sacnt;
-    /* XBLOCK, combining block: the chunk's 64 shared-down rows (codes, then
-     * their scales, then their biases), loaded straight into LDS while the
-     * logits are exchanged: read after the routing, they would queue behind
-     * the expert stream.  s_shdok: they are in. */
-    __shared__ __align__(16) uint8_t s_shdw[BLK ? NMOE_FUSED_CHUNK * (NMOE_INTER / 2 + 2 * 2 * NMOE_INTER / NMOE_GROUP) : 16];
-    __shared__ uint32_t s_shdok;
+    __shared__ uint32_t s_shok;
+    /* XBLOCK: the block's 8 shared-down rows (codes; scales, then biases),
+     * loaded while the logits are exchanged; s_s2ok: they are in */
+    __shared__ __align__(16) uint8_t s_s2w[BLK ? NMOE_FUSED_S2_ROWS * (NMOE_INTER / 2) : 16];
+    __shared__ uint16_t s_s2sb[BLK ? 2 * NMOE_FUSED_S2_ROWS * (NMOE_INTER / NMOE_GROUP) : 2];
+    __shared__ uint32_t s_s2ok;
     /* XSTACK: h of this layer and the next (the gather of the next one
      * never touches the rows the combine still reads), the layer's router
      * rows 8j .. 8j+7 (fetched a layer ahead; bf16: 8 x 4 KB; q4: 8 x 1 KB
@@ -563,8 +564,7 @@ __device__ __forceinline__ void nmoe_fused_body(nmoe_fused_args a, const nmoe_st
             s_epoch = e;
             s_bad = 0u;
             s_shok = 0u;
-            s_sacnt = 0u;
-            s_shdok = 0u;
+            s_s2ok = 0u;
         }
         s_ncand = 0u;
         s_confirm = 0u;
@@ -600,110 +600,64 @@ __device__ __forceinline__ void nmoe_fused_body(nmoe_fused_args a, const nmoe_st
     __syncthreads();
     const uint32_t epoch = s_epoch + (STK ? (uint32_t)ly : 0u);
 
-    if (has_sh && wave < 4) {
-        /* ---- S1 (XBLOCK, every block): shared gate/up rows 2b, 2b+1
-         * (kernels.metal:421-469) in the router's per-element form, while
-         * the routing runs: wavefronts 0, 1 reduce the gate rows, 2, 3 the
-         * up rows and publish SiLU(gate) * up for the combining blocks */
-        const int srow = 2 * blockIdx.x + (wave & 1);
-        const nmoe_hip_qtensor T = wave < 2 ? a.sh.gate : a.sh.up;
-        uint32_t w4[4];
-        uint16_t s4[4], b4[4];
-        float xq[32];
+    /* ---- S2 (XBLOCK, every block's candidate wavefront after its routing):
+     * shared-down rows 64j + 8g .. +7 (kernels.metal:1520-1537), published
+     * for the block that combines chunk j.  All 512 shared activations into
+     * LDS, then 16 lanes a row (32 columns each, the routed down rows' form
+     * s * sum(q a) + b * sum(a) per 64-column group), four rows a step. */
+    const int s2r0 = j * NMOE_FUSED_CHUNK + NMOE_FUSED_S2_ROWS * g;
+    auto shared_rows = [&]() {
+        const uint64_t *ps[8];
+        float v[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int q = 0; q < 4; q++) {
-            w4[q] = T.w[(size_t)srow * (NMOE_HIDDEN / 8) + lane + 64 * q];
-            s4[q] = T.scales[(size_t)srow * (NMOE_HIDDEN / NMOE_GROUP) + (lane + 64 * q) / 8];
-            b4[q] = T.biases[(size_t)srow * (NMOE_HIDDEN / NMOE_GROUP) + (lane + 64 * q) / 8];
-        }
+        for (int q = 0; q < 8; q++) ps[q] = a.xch + NMOE_XCH_SHACT + lane + 64 * q;
+        nmoe_poll<8>(ps, epoch, v, status, &s_bad, a.spin);
 #pragma unroll
-        for (int c = 0; c < 8; c++)
-            *(float4 *)(xq + 4 * c) =
-                ((const float4 *)s_h)[nmoe_act_slot<Q::CPL / 4>(8 * lane + 512 * (c >> 1) + 4 * (c & 1)) / 4];
-        const float v = nmoe_router_row_q4(w4, s4, b4, xq);
-        if (wave < 2) {
-            if (lane == 0) {
-                s_shg[wave] = v;
-                __hip_atomic_fetch_add(&s_shok, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
-            }
-        } else {
-            nmoe_lds_wait_above(&s_shok, 1u, status, &s_bad, a.spin);
-            float act = nmoe_silu_dev(s_shg[wave & 1]) * v;
-            if (nmoe_lds_flag(&s_bad)) act = __builtin_nanf("");
-            if (lane == 0) nmoe_st_tagged(a.xch + NMOE_XCH_SHACT + NMOE_XCH_SP * srow, epoch, act);
-        }
-    }
-
-    /* ---- S2 (XBLOCK, combining block, both control wavefronts after their
-     * routing): this chunk's 64 shared-down rows (kernels.metal:1520-1537)
-     * from LDS, rows r0 .. r0 + 4n - 1 by one wavefront: 16 lanes a row (32
-     * columns each, fma(fma(q, s, b), act, acc) as the shared-down kernel),
-     * four rows a step.  The candidate wavefront, free first, brings all
-     * 512 shared activations into LDS. */
-    auto shared_down = [&](int r0, int n) {
-        if (cwave) {
-            const uint64_t *ps[8];
-            float v[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-            for (int q = 0; q < 8; q++) ps[q] = a.xch + NMOE_XCH_SHACT + NMOE_XCH_SP * (lane + 64 * q);
-            nmoe_poll<8>(ps, epoch, v, status, &s_bad, a.spin);
-#pragma unroll
-            for (int q = 0; q < 8; q++) s_sact[lane + 64 * q] = v[q];
-            if (lane == 0) __hip_atomic_store(&s_sacnt, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
-        }
-        nmoe_lds_wait_above(&s_shdok, 0u, status, &s_bad, a.spin); /* the rows */
-        nmoe_lds_wait_above(&s_sacnt, 0u, status, &s_bad, a.spin); /* the activations */
+        for (int q = 0; q < 8; q++) s_sact[lane + 64 * q] = v[q];
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+        nmoe_lds_wait_above(&s_s2ok, 0u, status, &s_bad, a.spin); /* the rows */
+        /* the multiply-adds below the workers' priority: they fill the
+         * workers' waits (their loads, the act exchange), and the combine
+         * needs them only after the workers are done */
+        __builtin_amdgcn_s_setprio(0);
         const int dl16 = lane & 15, rsub = lane >> 4;
-        const uint16_t *sds = (const uint16_t *)(s_shdw + NMOE_FUSED_CHUNK * (NMOE_INTER / 2));
-        const uint16_t *sdb = sds + NMOE_FUSED_CHUNK * (NMOE_INTER / NMOE_GROUP);
         float av[32];
 #pragma unroll
         for (int c = 0; c < 8; c++) *(float4 *)(av + 4 * c) = ((const float4 *)s_sact)[8 * dl16 + c];
-        for (int st = 0; st < n; st++) {
-            const int rr = r0 + 4 * st + rsub;
-            const uint4 dw = *(const uint4 *)(s_shdw + rr * (NMOE_INTER / 2) + 16 * dl16);
-            const float sc = nmoe_bf16f(sds[rr * (NMOE_INTER / NMOE_GROUP) + dl16 / 2]);
-            const float bi = nmoe_bf16f(sdb[rr * (NMOE_INTER / NMOE_GROUP) + dl16 / 2]);
-            const uint32_t wd[4] = {dw.x, dw.y, dw.z, dw.w};
-            float acc = 0.0f;
+        float asum = 0.0f;
 #pragma unroll
-            for (int i = 0; i < 4; i++)
+        for (int c = 0; c < 32; c++) asum += av[c];
+        const bool poisoned = nmoe_lds_flag(&s_bad);
 #pragma unroll
-                for (int m = 0; m < 8; m++)
-                    acc = __builtin_fmaf(__builtin_fmaf((float)((wd[i] >> (4 * m)) & 0xFu), sc, bi), av[8 * i + m], acc);
-            acc = nmoe_dpp_group_sum<16>(acc);
-            if (dl16 == 0) s_shd[rr] = acc;
+        for (int st = 0; st < NMOE_FUSED_S2_ROWS / 4; st++) {
+            const int rr = 4 * st + rsub;
+            const uint4 dw = *(const uint4 *)(s_s2w + rr * (NMOE_INTER / 2) + 16 * dl16);
+            const float sc = nmoe_bf16f(s_s2sb[rr * (NMOE_INTER / NMOE_GROUP) + dl16 / 2]);
+            const float bi = nmoe_bf16f(s_s2sb[NMOE_FUSED_S2_ROWS * (NMOE_INTER / NMOE_GROUP) +
+                                                rr * (NMOE_INTER / NMOE_GROUP) + dl16 / 2]);
+            float y = __builtin_fmaf(sc, nmoe_dot16<4>(dw, av), bi * asum);
+            y = nmoe_dpp_group_sum<16>(y);
+            if (dl16 == 0) nmoe_st_tagged(a.xch + NMOE_XCH_SHD + s2r0 + rr, epoch, poisoned ? __builtin_nanf("") : y);
         }
     };
-    if (has_sh && comb && wave == NMOE_FUSED_EXACT) {
-        /* the chunk's shared-down rows into LDS (18 KB: codes, scales,
-         * biases, each contiguous over rows 64j .. 64j+63), by loads that
-         * write LDS directly, while the logits are exchanged (at the start
-         * they would delay the loads of h).  This wavefront is idle until
-         * the logits are in, long after these loads are. */
+    if (has_sh && wave == NMOE_FUSED_EXACT) {
+        /* the block's shared-down rows into LDS (2 KB of codes by loads that
+         * write LDS directly, 256 B of scales and biases), while the logits
+         * are exchanged (at the start they would delay the loads of h).
+         * This wavefront is idle until the logits are in, long after. */
         typedef __attribute__((address_space(3))) void nmoe_lds_void_sd;
-        const size_t r0 = (size_t)j * NMOE_FUSED_CHUNK;
-        const uint8_t *cw = (const uint8_t *)a.sh.down.w + r0 * (NMOE_INTER / 2);
-        const uint8_t *cs = (const uint8_t *)(a.sh.down.scales + r0 * (NMOE_INTER / NMOE_GROUP));
-        const uint8_t *cb = (const uint8_t *)(a.sh.down.biases + r0 * (NMOE_INTER / NMOE_GROUP));
-        constexpr int WB = NMOE_FUSED_CHUNK * (NMOE_INTER / 2), SB = NMOE_FUSED_CHUNK * (NMOE_INTER / NMOE_GROUP) * 2;
-        static_assert(WB % 1024 == 0 && SB == 1024, "one 16-byte load per lane covers 1 KB");
+        const uint8_t *cw = (const uint8_t *)a.sh.down.w + (size_t)s2r0 * (NMOE_INTER / 2);
+        constexpr int WB = NMOE_FUSED_S2_ROWS * (NMOE_INTER / 2), SN = NMOE_FUSED_S2_ROWS * (NMOE_INTER / NMOE_GROUP);
+        static_assert(WB % 1024 == 0 && SN == NMOE_WAVE, "16-byte loads of whole rows; one scale a lane");
 #pragma unroll
         for (int i = 0; i < WB / 1024; i++)
-            __builtin_amdgcn_global_load_lds(cw + 1024 * i + 16 * lane, (nmoe_lds_void_sd *)(s_shdw + 1024 * i), 16, 0, 0);
-        if ((((uintptr_t)cs | (uintptr_t)cb) & 15u) == 0u) {
-            __builtin_amdgcn_global_load_lds(cs + 16 * lane, (nmoe_lds_void_sd *)(s_shdw + WB), 16, 0, 0);
-            __builtin_amdgcn_global_load_lds(cb + 16 * lane, (nmoe_lds_void_sd *)(s_shdw + WB + SB), 16, 0, 0);
-        } else { /* scales and biases need only be 2-byte aligned: 2-byte loads */
-            uint16_t *d = (uint16_t *)(s_shdw + WB);
-#pragma unroll
-            for (int q = 0; q < SB / 128; q++) {
-                d[lane + 64 * q] = ((const uint16_t *)cs)[lane + 64 * q];
-                d[SB / 2 + lane + 64 * q] = ((const uint16_t *)cb)[lane + 64 * q];
-            }
-        }
+            __builtin_amdgcn_global_load_lds(cw + 1024 * i + 16 * lane, (nmoe_lds_void_sd *)(s_s2w + 1024 * i), 16, 0, 0);
+        s_s2sb[lane] = a.sh.down.scales[(size_t)s2r0 * (NMOE_INTER / NMOE_GROUP) + lane];
+        s_s2sb[SN + lane] = a.sh.down.biases[(size_t)s2r0 * (NMOE_INTER / NMOE_GROUP) + lane];
         __builtin_amdgcn_s_waitcnt(0);
-        if (lane == 0) __hip_atomic_store(&s_shdok, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+        if (lane == 0) __hip_atomic_store(&s_s2ok, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
     }
 
     if (STK && !ctrl) {
@@ -740,6 +694,41 @@ __device__ __forceinline__ void nmoe_fused_body(nmoe_fused_args a, const nmoe_st
                 nmoe_st_tagged(xlgd + 8 * j + wave, epoch, logit);
         }
     }
+    if (has_sh && wave < 4) {
+        /* ---- S1 (XBLOCK, every block): shared gate/up rows 2b, 2b+1
+         * (kernels.metal:421-469) in the router's per-element form, while
+         * the routing runs: wavefronts 0, 1 reduce the gate rows, 2, 3 the
+         * up rows and publish SiLU(gate) * up for every block's
+         * shared-down rows */
+        const int srow = 2 * blockIdx.x + (wave & 1);
+        const nmoe_hip_qtensor T = wave < 2 ? a.sh.gate : a.sh.up;
+        uint32_t w4[4];
+        uint16_t s4[4], b4[4];
+        float xq[32];
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            w4[q] = T.w[(size_t)srow * (NMOE_HIDDEN / 8) + lane + 64 * q];
+            s4[q] = T.scales[(size_t)srow * (NMOE_HIDDEN / NMOE_GROUP) + (lane + 64 * q) / 8];
+            b4[q] = T.biases[(size_t)srow * (NMOE_HIDDEN / NMOE_GROUP) + (lane + 64 * q) / 8];
+        }
+#pragma unroll
+        for (int c = 0; c < 8; c++)
+            *(float4 *)(xq + 4 * c) =
+                ((const float4 *)s_h)[nmoe_act_slot<Q::CPL / 4>(8 * lane + 512 * (c >> 1) + 4 * (c & 1)) / 4];
+        const float v = nmoe_router_row_q4(w4, s4, b4, xq);
+        if (wave < 2) {
+            if (lane == 0) {
+                s_shg[wave] = v;
+                __hip_atomic_fetch_add(&s_shok, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+            }
+        } else {
+            nmoe_lds_wait_above(&s_shok, 1u, status, &s_bad, a.spin);
+            float act = nmoe_silu_dev(s_shg[wave & 1]) * v;
+            if (nmoe_lds_flag(&s_bad)) act = __builtin_nanf("");
+            if (lane == 0) nmoe_st_tagged(a.xch + NMOE_XCH_SHACT + srow, epoch, act);
+        }
+    }
+
     if (ROUTE && cwave) {
         /* the control wavefronts share SIMDs with workers: their routing is
          * on the critical path, the workers' multiply-adds mostly are not */
@@ -810,13 +799,8 @@ __device__ __forceinline__ void nmoe_fused_body(nmoe_fused_args a, const nmoe_st
                 }
             }
             if (lane == 0) __hip_atomic_store(&s_ncand, (uint32_t)k, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
-            if (has_sh && comb) {
-                /* off the routing's critical path: at the workers' priority,
-                 * whose expert loads and SwiGLU share these SIMDs */
-                __builtin_amdgcn_s_setprio(0);
-                shared_down(0, 8);
-            }
         }
+        if (has_sh) shared_rows(); /* (an idle group's block: right after its logit) */
     }
     if (ROUTE && wave == NMOE_FUSED_EXACT && (g < k || STK)) {
         /* ---- exact routing (math.m softmax / top-k / renormalise), from
@@ -937,10 +921,6 @@ __device__ __forceinline__ void nmoe_fused_body(nmoe_fused_args a, const nmoe_st
             }
         }
         if (lane == 0) __hip_atomic_store(&s_confirm, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
-        if (has_sh && comb) {
-            __builtin_amdgcn_s_setprio(0);
-            shared_down(32, 8);
-        }
         /* XSTACK: the next layer's router row, while this layer streams
          * (the candidate wavefront read this one before the logits came) */
         if (STK && ly + 1 < nl) load_rrow(s_stk[4 * (ly + 1) + 1], s_stk[4 * (ly + 1) + 2], s_stk[4 * (ly + 1) + 3]);
@@ -1126,12 +1106,19 @@ __device__ __forceinline__ void nmoe_fused_body(nmoe_fused_args a, const nmoe_st
         if (!comb || (STK && active))
             nmoe_st_tagged(ypart + g * NMOE_HIDDEN + row, epoch, poisoned ? __builtin_nanf("") : s_y[tid]);
         if (comb) {
-            const uint64_t *pp[NMOE_MAX_K];
-            float ys[NMOE_MAX_K];
+            /* the k - 1 other groups' partials and (XBLOCK) the shared
+             * expert's down row */
+            constexpr int NP = BLK ? NMOE_MAX_K + 1 : NMOE_MAX_K;
+            const uint64_t *pp[NP];
+            float ys[NP];
 #pragma unroll
             for (int q = 0; q < NMOE_MAX_K; q++) {
                 pp[q] = ypart + q * NMOE_HIDDEN + row;
                 ys[q] = s_y[tid];
+            }
+            if constexpr (BLK) {
+                pp[NMOE_MAX_K] = a.xch + NMOE_XCH_SHD + row;
+                ys[NMOE_MAX_K] = 0.0f;
             }
             /* everything but the partials before the wait: slot s's weight
              * and the group that streams it (usually group s), the shared
@@ -1147,9 +1134,9 @@ __device__ __forceinline__ void nmoe_fused_body(nmoe_fused_args a, const nmoe_st
             }
             const bool shared_term = BLK ? has_sh : a.shared_out != NULL;
             const float gsig = shared_term ? nmoe_sigmoid_dev(BLK ? s_sgr[0] : sgr) : 0.0f;
-            const float shv = BLK ? (has_sh ? s_shd[tid] : 0.0f) : sh;
-            const bool expired = nmoe_poll2<NMOE_MAX_K>(pp, epoch, ys, status, &s_bad, a.spin,
-                                                        ((1u << k) - 1u) & ~(active ? 1u << g : 0u));
+            const uint32_t need = (((1u << k) - 1u) & ~(active ? 1u << g : 0u)) | (has_sh ? 1u << NMOE_MAX_K : 0u);
+            const bool expired = nmoe_poll2<NP>(pp, epoch, ys, status, &s_bad, a.spin, need);
+            const float shv = BLK ? ys[NP - 1] : sh; /* (XBLOCK without a shared expert: unused) */
             /* slot order: slot s is streamed by group sgl[s] */
             float moe = 0.0f;
             if (ident) {

@@ -53,8 +53,8 @@ struct nmoe_layout<2> {
 /* The fused launch's exchange words (tagged logits, act and partial y),
  * and with the whole-block form's shared activations and next-norm sums. */
 #define NMOE_FUSED_XCH_BYTES 409600u
-#define NMOE_FUSED_XCH_BYTES_BLOCK 460800u
-#define NMOE_FUSED_XCH_BYTES_STACK 759808u /* the block form's words + the layer loop's */
+#define NMOE_FUSED_XCH_BYTES_BLOCK 446976u
+#define NMOE_FUSED_XCH_BYTES_STACK 745984u /* the block form's words + the layer loop's */
 
 /* The whole-block parts of a fused launch (XBLOCK): norm weights, the
  * next-layer norm output and the shared expert. */

@@ -74,6 +74,51 @@ def test_expired_wait_poisons_output_and_recovers(nh):
         ctx._check(ctx.set_option(nh.OPT_SPIN_LIMIT, 0))
 
 
+def test_block_expired_wait_poisons_and_recovers(nh):
+    """The whole-block form (nmoe_moe_block with the shared expert and the
+    next layer's norm): its waits span the shared expert's activations and
+    down rows, the combine and the norm's partial sums.  A skewed block --
+    a combining block, another block of its chunk, an idle group's block
+    (k = 6) -- makes the launch report ETIMEDOUT with out, next_x and the
+    weights all NaN, and the next launch gives the clean bits again."""
+    with nh.Context(0, max_tokens=4) as ctx:
+        seed, layer, k = 31, 5, 6
+        ctx.synth_layer(layer, 4, seed, 0.02)
+        W = ctx.to_device(B.syn_bf16(256 * 2048, seed, layer, 16, 0.02))
+        se = B.syn_shared_expert(13)
+        dev = {n: tuple(ctx.to_device(np.ascontiguousarray(a)) for a in se[n]) for n in se}
+        blk = nh.MoeBlock()
+        blk.router = ctx.router_bf16(W)
+        blk.has_shared = 1
+        blk.shared = nh.Context.shared_expert_desc(dev["gate"], dev["up"], dev["down"], dev["score"])
+        blk.eps = 1e-6
+        h = (np.random.default_rng(seed).standard_normal(2048) * 1.5).astype(np.float32)
+        dh, out, nx, di, dw = ctx.to_device(h), ctx.alloc(8192), ctx.alloc(8192), ctx.alloc(32), ctx.alloc(32)
+        run = lambda: ctx.moe_block(layer, blk, dh, k, out, nx, di, dw)
+        ctx._check(ctx.set_option(nh.OPT_SPIN_LIMIT, SPIN))
+        try:
+            ctx._check(run())
+            assert ctx.device_status() == nh.OK
+            good = out.download(np.float32, 2048), nx.download(np.float32, 2048), di.download(np.uint32, 8)
+            assert np.isfinite(good[0]).all() and np.isfinite(good[1]).all()
+            for block in (0, 8 * 5 + 3, 8 * 9 + 7):  # combining (group 0), routed (group 3), idle (group 7)
+                print(f"[robust] block form, skewed block {block}", flush=True)
+                ctx._check(ctx.set_option(nh.OPT_SKEW_EPOCH, block))
+                assert run() == nh.OK
+                assert np.isnan(out.download(np.float32, 2048)).all(), f"block {block}: out not poisoned"
+                assert np.isnan(nx.download(np.float32, 2048)).all(), f"block {block}: next_x not poisoned"
+                assert np.isnan(dw.download(np.float32, 8)[:k]).all()
+                assert ctx.device_status() == nh.ETIMEDOUT
+                assert ctx.device_status() == nh.OK
+                ctx._check(run())
+                assert ctx.device_status() == nh.OK
+                again = out.download(np.float32, 2048), nx.download(np.float32, 2048), di.download(np.uint32, 8)
+                for a, b in zip(again, good):
+                    np.testing.assert_array_equal(a.view(np.uint32), b.view(np.uint32))
+        finally:
+            ctx.set_option(nh.OPT_SPIN_LIMIT, 0)
+
+
 def test_sync_check_returns_etimedout(nh):
     """With NMOE_HIP_OPT_SYNC_CHECK the layer call itself reports the
     expired wait, and the stack reports it once, after its last layer; the
