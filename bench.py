@@ -407,59 +407,67 @@ def run_grouped(pool, args, workload: str, NLg: int = 8) -> dict:
     }
 
 
-def _q4_tensor(rng, rows: int, cols: int, sigma: float):
-    """A q4 tensor in the model's stored form: codes uniform 0..15, scales
-    bf16(N(0, sigma)), biases bf16(-8 scale) (u32 words, bf16 scales, bf16
-    biases as one byte string)."""
-    w = rng.integers(0, 2**32, size=rows * cols // 8, dtype=np.uint64).astype(np.uint32)
-    sc = (rng.standard_normal(rows * cols // 64) * sigma).astype(np.float32)
-    s16 = ((sc.view(np.uint32).astype(np.uint64) + 0x7FFF + ((sc.view(np.uint32) >> 16) & 1)) >> 16).astype(np.uint16)
-    bi = (-8.0 * (s16.astype(np.uint32) << 16).view(np.float32)).astype(np.float32)
-    b16 = ((bi.view(np.uint32).astype(np.uint64) + 0x7FFF + ((bi.view(np.uint32) >> 16) & 1)) >> 16).astype(np.uint16)
-    return [w.tobytes(), s16.tobytes(), b16.tobytes()]
+BLOCK_SLOTS = 160  # per-layer model tensors rotated by the block workload: 160 x 2.1 MB, above the 256 MB MALL
+
+
+def _block_tensors(rng, ns: int):
+    """ns slots of one layer's MoE-half model tensors in their stored form,
+    each tensor 256-byte aligned inside its slot: q4 router [256][2048],
+    shared gate/up [512][2048], down [2048][512] and gate score [1][2048]
+    (codes uniform 0..15, scales bf16(N(0, sigma)), biases bf16(-8 scale)),
+    then the post-attention and next-layer norm weights (bf16, N(0, 0.1)).
+    Returns (uint8 [ns][slot bytes], {name: [offsets in a slot]})."""
+    def bf16(v):
+        u = v.astype(np.float32).view(np.uint32).astype(np.uint64)
+        return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+    shapes = {"router": (256, 2048, 0.002), "gate": (512, 2048, 0.002), "up": (512, 2048, 0.002),
+              "down": (2048, 512, 0.004), "score": (1, 2048, 0.002)}
+    offs, pos = {}, 0
+    al = lambda n: (n + 255) // 256 * 256
+    for name, (r, c, _) in shapes.items():
+        offs[name] = [pos, pos + al(r * c // 2), pos + al(r * c // 2) + al(r * c // 32)]
+        pos = offs[name][2] + al(r * c // 32)
+    offs["norm"] = [pos, pos + al(4096)]
+    slot = pos + 2 * al(4096)
+    buf = np.zeros((ns, slot), np.uint8)
+    for name, (r, c, sigma) in shapes.items():
+        w0, s0, b0 = offs[name]
+        buf[:, w0:w0 + r * c // 2] = rng.integers(0, 256, size=(ns, r * c // 2), dtype=np.uint8)
+        sc = bf16(rng.standard_normal((ns, r * c // 64)) * sigma)
+        bi = bf16(-8.0 * (sc.astype(np.uint32) << 16).view(np.float32))
+        buf[:, s0:s0 + r * c // 32] = sc.view(np.uint8).reshape(ns, -1)
+        buf[:, b0:b0 + r * c // 32] = bi.view(np.uint8).reshape(ns, -1)
+    for i in range(2):
+        buf[:, offs["norm"][i]:offs["norm"][i] + 4096] = bf16(rng.standard_normal((ns, 2048)) * 0.1).view(np.uint8)
+    return buf, offs
 
 
 def run_block(pool, args) -> dict:
     """The model's per-layer MoE half as the drop-in runs it (nmoe_moe_block):
     post-attention RMSNorm (1 + w), the q4 router, the shared expert (q4
     gate/up/down and gate score), the routed experts, the combine and the
-    next layer's input norm, one launch per layer.  Each of the pool's
-    layers gets its own synthetic model tensors (seeded); step i runs layer
-    i % 40 on residual slot i % 320, after the warm-up's steps."""
+    next layer's input norm, one launch per layer.  Step i runs the experts
+    of layer i % 40 with model-tensor slot i % 160 (router, shared expert,
+    norms: 160 x 2.1 MB, more than the memory-side cache holds) on residual
+    slot i % 320, after the warm-up's steps."""
     nh, ctx, bits, k, NL = pool.nh, pool.ctx, args.bits, args.k, pool.NL
     stream = ctx.stream
-    rng = np.random.default_rng(args.seed * 7919 + 11)
-    blks, keep = [], []
-    for layer in range(NL):
-        parts = {"router": _q4_tensor(rng, 256, 2048, 0.002), "gate": _q4_tensor(rng, 512, 2048, 0.002),
-                 "up": _q4_tensor(rng, 512, 2048, 0.002), "down": _q4_tensor(rng, 2048, 512, 0.004),
-                 "score": _q4_tensor(rng, 1, 2048, 0.002)}
-        norms = [(rng.standard_normal(2048) * 0.1).astype(np.float32) for _ in range(2)]
-        norms = [((n.view(np.uint32).astype(np.uint64) + 0x7FFF + ((n.view(np.uint32) >> 16) & 1)) >> 16)
-                 .astype(np.uint16).tobytes() for n in norms]
-        blob, offs = b"", {}
-        for name in ("router", "gate", "up", "down", "score"):
-            offs[name] = []
-            for piece in parts[name]:
-                blob += b"\0" * ((-len(blob)) % 256)
-                offs[name].append(len(blob))
-                blob += piece
-        for i, piece in enumerate(norms):
-            blob += b"\0" * ((-len(blob)) % 256)
-            offs[f"norm{i}"] = len(blob)
-            blob += piece
-        dev = ctx.to_device(np.frombuffer(blob, np.uint8), f"bench.block.{layer}")
-        keep.append(dev)
-        P = lambda name: [dev.ptr + o for o in offs[name]]
+    NS = max(BLOCK_SLOTS, NL)
+    buf, offs = _block_tensors(np.random.default_rng(args.seed * 7919 + 11), NS)
+    dev = ctx.to_device(buf, "bench.block")
+    slot = buf.shape[1]
+    blks = []
+    for i in range(NS):
+        P = lambda name: [dev.ptr + i * slot + o for o in offs[name]]
         se = ctx.shared_expert_desc(P("gate"), P("up"), P("down"), P("score"))
-        blk = nh.MoeBlock(ctx.router_q4(*P("router")), 1, se, dev.ptr + offs["norm0"], dev.ptr + offs["norm1"],
-                          1, 1e-6)
-        blks.append(blk)
+        n0, n1 = P("norm")
+        blks.append(nh.MoeBlock(ctx.router_q4(*P("router")), 1, se, n0, n1, 1, 1e-6))
     out, nx, di, dw = ctx.alloc(8192), ctx.alloc(8192), ctx.alloc(32), ctx.alloc(32)
     ctx.sync()
 
     def step(i):
-        ctx._check(ctx.moe_block(i % NL, blks[i % NL], pool.H.ptr + (i % pool.NR) * 8192, k, out, nx, di, dw,
+        ctx._check(ctx.moe_block(i % NL, blks[i % NS], pool.H.ptr + (i % pool.NR) * 8192, k, out, nx, di, dw,
                                  stream=stream))
 
     for i in range(args.warmup):
@@ -487,8 +495,8 @@ def run_block(pool, args) -> dict:
             "hbm_gbps": round(gbs, 1),
             "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": round(gbs / HBM_PEAK_GBS, 4)},
-            "config": {"workload": "block", "layers_rotated": NL, "bits": bits, "k": k, "bytes_per_step": B,
-                       "entry_point": "nmoe_moe_block"}}
+            "config": {"workload": "block", "layers_rotated": NL, "tensor_slots_rotated": NS, "bits": bits, "k": k,
+                       "bytes_per_step": B, "entry_point": "nmoe_moe_block"}}
 
 
 def run_stream(pool, args) -> dict:
@@ -534,13 +542,13 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--stack-loop", type=int, default=1, choices=(0, 1),
                     help="c3: the token's layers in one persistent launch (1, default) or one launch per layer (0)")
-    ap.add_argument("--no-extra", action="store_true", help="c1 only: no c3 / c5 / stream sub-objects")
+    ap.add_argument("--no-extra", action="store_true", help="c1 only: no c3 / c5 / stream / block sub-objects")
     ap.add_argument("--copy-calib", type=int, default=0, metavar="MIB",
                     help="only run 5 device-to-device copies of MIB MiB (counter calibration) and exit")
     ap.add_argument("--router", default="bf16", choices=("bf16", "q4"),
                     help="c1/c3: the benchmark configs' dense bf16 router (default) or the model's q4 router")
     ap.add_argument("--workload", default="c1", choices=("c1", "c3", "c4", "c5", "stream", "block"),
-                    help="c1: the headline single-layer decode step, with c3 and c5 sub-objects (default); "
+                    help="c1: the headline single-layer decode step, with c3, c5, stream and block sub-objects (default); "
                          "c3 / c4 / c5 alone: 40-layer stack of 128 tokens / batched decode of 64 Zipf-routed "
                          "tokens / 2048-token prefill on the grouped matrix-core path; stream: the streaming ceiling "
                          "of the c1 step's expert bytes (nmoe_hip_read_probe); block: the model's per-layer MoE "
@@ -582,6 +590,7 @@ def main():
             result["c3"] = run_c3(pool, args)
             result["c5"] = run_grouped(pool, args, "c5")
             result["stream"] = run_stream(pool, args)
+            result["block"] = run_block(pool, args)
         if not args.no_cpu:
             print("[bench] cpu baseline ...", file=sys.stderr, flush=True)
             result["cpu_baseline"] = cpu_baseline(args.bits, args.k, args.seed, args.cpu_steps)
