@@ -968,6 +968,60 @@ def test_moe_block_from_model_weights(ctx, nh, tmp_path, bits, k):
         np.testing.assert_array_equal(dh.download(np.float32, 2048).view(np.uint32), got_out.view(np.uint32))
 
 
+def test_moe_block_coherent_words_and_2_byte_scales(ctx, nh):
+    """The block form with every exchange word device-coherent
+    (NMOE_HIP_OPT_XCD_LOCAL off) gives the same bits as the die-local form,
+    and both match orc_moe_block; the shared expert's scales and biases sit
+    at 2-byte (not 16-byte) aligned addresses, the alignment the entry point
+    accepts for them, and the bf16 router is used."""
+    seed, layer, k = 77, 63, 8
+    ctx.synth_layer(layer, 4, seed, SIGMA[4])
+    W = B.syn_bf16(256 * 2048, seed, layer, 16, 0.02).reshape(256, 2048)
+    se = B.syn_shared_expert(14)
+    keep = []
+
+    def odd(a):  # a device copy at an address 2 bytes past a 256-byte boundary
+        a = np.ascontiguousarray(a)
+        buf = ctx.alloc(a.nbytes + 256)
+        keep.append(buf)
+        buf.upload(a, offset=2)
+        return buf.ptr + 2
+
+    dev = {n: (ctx.to_device(np.ascontiguousarray(se[n][0])), odd(se[n][1]), odd(se[n][2])) for n in se}
+    rng = np.random.default_rng(seed)
+    post = B.f32_to_bf16((rng.standard_normal(2048) * 0.1).astype(np.float32))
+    nxt = B.f32_to_bf16((rng.standard_normal(2048) * 0.1).astype(np.float32))
+    blk = nh.MoeBlock()
+    blk.router = ctx.router_bf16(ctx.to_device(W))
+    blk.has_shared = 1
+    blk.shared = nh.Context.shared_expert_desc(dev["gate"], dev["up"], dev["down"], dev["score"])
+    blk.post_norm, blk.next_norm = ctx.to_device(post).ptr, ctx.to_device(nxt).ptr
+    blk.add_one, blk.eps = 1, 1e-6
+    h = (rng.standard_normal(2048) * 1.5).astype(np.float32)
+    dh = ctx.to_device(h)
+    got = []
+    for xl in (1, 0):
+        out, nx, di, dw = ctx.alloc(8192), ctx.alloc(8192), ctx.alloc(32), ctx.alloc(32)
+        ctx._check(ctx.set_option(nh.OPT_XCD_LOCAL, xl))
+        try:
+            ctx._check(ctx.moe_block(layer, blk, dh, k, out, nx, di, dw))
+            assert ctx.device_status() == nh.OK
+        finally:
+            ctx.set_option(nh.OPT_XCD_LOCAL, 1)  # back on where the device's placement allows it
+        got.append((out.download(np.float32, 2048), nx.download(np.float32, 2048), di.download(np.uint32, 8),
+                    dw.download(np.float32, 8)))
+    for a, b in zip(got[0], got[1]):
+        np.testing.assert_array_equal(a.view(np.uint32), b.view(np.uint32))
+    out, nx, gi, gw = got[0]
+    pack = host_pack(4, seed, layer, gi[:k])
+    want, oi, ow, _, want_nx = B.moe_block(pack, 4, {"w": W}, h, k, post_norm=post, add_one=1, shared=se,
+                                           next_norm=nxt, want_next=True)
+    np.testing.assert_array_equal(gi, oi)
+    np.testing.assert_array_equal(gw.view(np.uint32), ow.view(np.uint32))
+    assert_close(out, want, what="block out")
+    assert_close(nx, want_nx, what="block next_x")
+
+
 def test_moe_block_plain_equals_layer_rmsnorm(ctx, nh):
     """With unit norms, no shared expert and no next norm the block is the
     layer with its input RMSNorm: the same bits as nmoe_moe_layer_rmsnorm."""
