@@ -101,21 +101,17 @@ NMOE_HD int nmoe_clz64(uint64_t v) {
 
 /* glibc expf, FMA variant.  tab = NMOE_EXP2_TAB32 (constant memory on the
  * device).  Special cases follow e_expf.c: -inf -> 0, NaN/inf propagate,
- * overflow -> inf, x < log(2^-150) -> 0. */
+ * overflow -> inf, x < log(2^-150) -> 0.  Branch-free: the main path runs
+ * for every x (its table index is in range for any input) and the special
+ * cases are selected afterwards -- the same result as e_expf.c's early
+ * returns, which apply only where |x| >= 88 (or x is not finite) and there
+ * give exactly these values. */
 NMOE_HD float nmoe_expf_glibc(float x, const uint64_t *tab) {
     const double invln2n = 0x1.71547652b82fep+0 * 32;
     const double shift = 0x1.8p+52;
     const double c0 = 0x1.c6af84b912394p-5 / 32 / 32 / 32;
     const double c1 = 0x1.ebfce50fac4f3p-3 / 32 / 32;
     const double c2 = 0x1.62e42ff0c52d6p-1 / 32;
-    uint32_t ux = nmoe_flt_bits(x);
-    uint32_t abstop = (ux >> 20) & 0x7ffu;
-    if (abstop >= 0x42bu) { /* top12 of 88.0f */
-        if (ux == 0xff800000u) return 0.0f;
-        if (abstop >= 0x7f8u) return x + x;
-        if (x > 0x1.62e42ep6f) return nmoe_bits_flt(0x7f800000u);
-        if (x < -0x1.9fe368p6f) return 0.0f;
-    }
     double xd = (double)x;
     double kd = fma(invln2n, xd, shift);
     uint64_t ki = nmoe_dbl_bits(kd);
@@ -128,7 +124,10 @@ NMOE_HD float nmoe_expf_glibc(float x, const uint64_t *tab) {
     double y = fma(c2, r, 1.0);
     y = fma(z, r2, y);
     y = y * s;
-    return (float)y;
+    float res = (float)y;
+    res = x > 0x1.62e42ep6f ? nmoe_bits_flt(0x7f800000u) : res; /* overflow (and +inf) */
+    res = x < -0x1.9fe368p6f ? 0.0f : res;                       /* underflow (and -inf) */
+    return x != x ? x + x : res;                                 /* NaN */
 }
 
 /* ---------------------------------------------------------------------
@@ -262,17 +261,15 @@ NMOE_HD float nmoe_u64_scaled_to_f32_rne(uint64_t u) { return nmoe_u64e_to_f32_r
  * below 2^63: math.m's running long double sum is then exact, equal to this
  * integer sum.  Returns 0 and leaves *out untouched if the term is too small. */
 NMOE_HD int nmoe_softmax_term_fixed(float e, uint64_t *out) {
-    uint32_t b = nmoe_flt_bits(e);
-    if (b == 0) {
-        *out = 0;
-        return 1;
-    }
-    uint32_t ex = b >> 23;
-    if (ex < 127u - 32u || ex > 127u) return 0;
-    uint64_t mant = (uint64_t)((b & 0x7fffffu) | 0x800000u);
-    /* e = mant * 2^(ex-150); times 2^55 -> mant << (ex - 95) */
-    *out = mant << (ex - 95u);
-    return 1;
+    const uint32_t b = nmoe_flt_bits(e);
+    const uint32_t ex = b >> 23;
+    const int fits = ex >= 127u - 32u && ex <= 127u;
+    const uint64_t mant = (uint64_t)((b & 0x7fffffu) | 0x800000u);
+    /* e = mant * 2^(ex-150); times 2^55 -> mant << (ex - 95) (branch-free:
+     * the shift count is clamped into range where the term does not fit) */
+    const uint64_t v = mant << (fits ? ex - 95u : 0u);
+    if (b == 0 || fits) *out = b == 0 ? 0 : v;
+    return b == 0 || fits;
 }
 
 /* Correctly rounded single-precision square root of v >= 0 (normal range),

@@ -12,6 +12,20 @@ static const uint64_t tab[32] = NMOE_EXP2_TAB32;
 uint64_t h_tab(int i) { return tab[i]; }
 float h_expf(float x) { return nmoe_expf_glibc(x, tab); }
 
+/* The bit patterns start, start + stride, ... below end (as floats) where
+ * the restatement and libm expf differ; returns their count. */
+long h_expf_mismatches(uint32_t start, uint32_t end, uint32_t stride) {
+    long bad = 0;
+    for (uint64_t u = start; u < end; u += stride) {
+        union { uint32_t u; float f; } a, r, w;
+        a.u = (uint32_t)u;
+        r.f = nmoe_expf_glibc(a.f, tab);
+        w.f = expf(a.f);
+        if (r.u != w.u && !(r.f != r.f && w.f != w.f)) bad++;
+    }
+    return bad;
+}
+
 float h_x87_sum(const float *v, int n) {
     nmoe_x87 acc = nmoe_x87_zero();
     for (int i = 0; i < n; i++) acc = nmoe_x87_add(acc, nmoe_x87_from_float(v[i]));

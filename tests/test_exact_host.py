@@ -55,6 +55,21 @@ def test_expf_matches_libm(h):
         assert np.float32(h.h_expf(x)).view(np.uint32) == np.float32(LIBM.expf(x)).view(np.uint32)
 
 
+def test_expf_matches_libm_densely(h):
+    """Every 61st bit pattern of the whole float line (both signs: the
+    softmax's arguments are <= 0, NaN or -inf; the rest covers overflow), and
+    every bit pattern from -88 to -104, where e_expf.c's special-case block
+    begins, against libm expf."""
+    h.h_expf_mismatches.restype = ctypes.c_long
+    h.h_expf_mismatches.argtypes = [ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32]
+    assert h.h_expf_mismatches(0, 0xFFFFFFFF, 61) == 0
+    lo, hi = int(np.float32(-88.0).view(np.uint32)), int(np.float32(-104.0).view(np.uint32))
+    assert h.h_expf_mismatches(lo, hi + 1, 1) == 0
+    for x in (float("nan"), float("inf"), 88.72283935546875, 88.7228469848632812, -103.97207641601562):
+        a, b = np.float32(h.h_expf(x)), np.float32(LIBM.expf(x))
+        assert (np.isnan(a) and np.isnan(b)) or a.view(np.uint32) == b.view(np.uint32), x
+
+
 def test_x87_emulation_matches_long_double(h):
     rng = np.random.default_rng(11)
     for trial in range(400):
