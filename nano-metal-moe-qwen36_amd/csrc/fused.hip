@@ -27,7 +27,8 @@
  *   G  gate/up dot products + SwiGLU -> act[g][512].
  *   D  block j waits for act[g], computes y_g = down_g . act[g] for rows
  *      64j..64j+63 -> ypart[g].
- *   C  block j of group j % K polls the other groups' partials of rows
+ *   C  block j of group j % K (XBLOCK: of group 0, so that all combining
+ *      blocks share a die) polls the other groups' partials of rows
  *      64j..64j+63 and combines out = h_mid + sum_s w_s y_s
  *      (+ sigmoid(g) * shared) in slot order.
  *
@@ -45,7 +46,8 @@
  * L2-wide cache maintenance.  The epoch is the launch count, kept per block
  * (each block increments its own word once per launch, so all agree).  The
  * combine of a chunk polls the chunk's K-1 other partials in one block.
- * Idle groups (K < 8) exit after their router row.  Every wait is bounded.
+ * Idle groups (K < 8) exit after their router row (XBLOCK: and their
+ * shared-down rows).  Every wait is bounded.
  *
  * Forms (XMODE): x given (fp32 / bf16), x = RMSNorm(h) (XNORM), the whole
  * MoE half of a model layer (XBLOCK: weighted norms, the shared expert in
