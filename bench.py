@@ -542,7 +542,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--stack-loop", type=int, default=1, choices=(0, 1),
                     help="c3: the token's layers in one persistent launch (1, default) or one launch per layer (0)")
-    ap.add_argument("--no-extra", action="store_true", help="c1 only: no c3 / c5 / stream / block sub-objects")
+    ap.add_argument("--no-extra", action="store_true", help="c1 only: no c3 / c4 / c5 / stream / block sub-objects")
     ap.add_argument("--copy-calib", type=int, default=0, metavar="MIB",
                     help="only run 5 device-to-device copies of MIB MiB (counter calibration) and exit")
     ap.add_argument("--router", default="bf16", choices=("bf16", "q4"),
@@ -586,8 +586,9 @@ def main():
     else:
         result = run_c1(pool, args)
         if not args.no_extra:
-            print("[bench] c3 and c5 sub-benchmarks ...", file=sys.stderr, flush=True)
+            print("[bench] c3, c4, c5, stream and block sub-benchmarks ...", file=sys.stderr, flush=True)
             result["c3"] = run_c3(pool, args)
+            result["c4"] = run_grouped(pool, args, "c4")
             result["c5"] = run_grouped(pool, args, "c5")
             result["stream"] = run_stream(pool, args)
             result["block"] = run_block(pool, args)
