@@ -161,3 +161,78 @@ def test_option_arguments_validated(nh):
         assert ctx.set_option(nh.OPT_SKEW_EPOCH, 256) == nh.EINVAL
         assert ctx.set_option(nh.OPT_SKEW_EPOCH, -1) == nh.EINVAL
         assert ctx.set_option(99, 0) == nh.EINVAL
+
+
+def test_repeated_launches_bit_identical(nh):
+    """Every launch form, run 100 times on the same inputs, gives the same
+    bits each time: the fused single-token layer, the grouped 64-token
+    layer, the layer loop in both forms (one launch per token, one per layer)
+    and the block form with its shared expert and next-layer norm.  A late
+    or lost word in the inter-block exchanges, or an epoch counter that
+    does not reset between launches, would show here as a changed bit."""
+    with nh.Context(0, max_tokens=64) as ctx:
+        seed, k, nl, ni = 5, 8, 4, 8
+        for l in range(nl):
+            ctx.synth_layer(l, 4, seed, 0.02)
+        R = ctx.alloc(nl * 256 * 4096)
+        for l in range(nl):
+            ctx.synth_bf16(R, 256 * 2048, seed, l, 16, 0.02, offset=l * 256 * 4096)
+        rts = [ctx.router_bf16(R.ptr + l * 256 * 4096) for l in range(nl)]
+        X, hb = ctx.alloc(64 * 4096), ctx.alloc(64 * 4096)
+        ctx.synth_bf16(X, 64 * 2048, seed, 0, 17, 1.0)
+        ctx.synth_bf16(hb, 64 * 2048, seed, 0, 18, 1.0)
+        h = (hb.download(np.uint16, (64, 2048)).astype(np.uint32) << 16).view(np.float32)
+        H = ctx.to_device(h)
+        o1, i1, w1 = ctx.alloc(ni * 8192), ctx.alloc(ni * 32), ctx.alloc(ni * 32)
+        og, ig, wg = ctx.alloc(64 * 8192), ctx.alloc(64 * 32), ctx.alloc(64 * 32)
+        row = (nl + 1) * 8192
+        HS, IS, WS = ctx.alloc(ni * row), ctx.alloc(ni * nl * 32), ctx.alloc(ni * nl * 32)
+        se = B.syn_shared_expert(13)
+        dev = {n: tuple(ctx.to_device(np.ascontiguousarray(a)) for a in se[n]) for n in se}
+        blk = nh.MoeBlock()
+        blk.router, blk.has_shared, blk.eps = rts[1], 1, 1e-6
+        blk.shared = nh.Context.shared_expert_desc(dev["gate"], dev["up"], dev["down"], dev["score"])
+        nrm = ctx.to_device(B.f32_to_bf16((np.random.default_rng(seed).standard_normal(2048) * 0.1).astype(np.float32)))
+        blk.post_norm, blk.next_norm, blk.add_one = nrm.ptr, nrm.ptr, 1
+        ob, nb, ib, wb = ctx.alloc(ni * 8192), ctx.alloc(ni * 8192), ctx.alloc(ni * 32), ctx.alloc(ni * 32)
+
+        def c1():
+            for i in range(ni):
+                ctx._check(ctx.moe_layer(i % nl, rts[i % nl], X.ptr + i * 4096, nh.BF16, 1, k, H.ptr + i * 8192,
+                                         o1.ptr + i * 8192, i1.ptr + i * 32, w1.ptr + i * 32))
+            return o1, i1, w1
+
+        def grouped():
+            ctx._check(ctx.moe_layer(2, rts[2], X, nh.BF16, 64, k, H, og, ig, wg))
+            return og, ig, wg
+
+        def stack(loop):
+            ctx._check(ctx.set_option(nh.OPT_STACK_LOOP, loop))
+            for t in range(ni):
+                HS.upload(h[t], offset=t * row)
+            for t in range(ni):
+                ctx._check(ctx.moe_stack(list(range(nl)), rts, k, 1e-6, HS.ptr + t * row, IS.ptr + t * nl * 32,
+                                         WS.ptr + t * nl * 32))
+            return HS, IS, WS
+
+        def block():
+            for i in range(ni):
+                ctx._check(ctx.moe_block(1, blk, H.ptr + i * 8192, k, ob.ptr + i * 8192, nb.ptr + i * 8192,
+                                         ib.ptr + i * 32, wb.ptr + i * 32))
+            return ob, nb, ib, wb
+
+        forms = {"fused layer": c1, "grouped layer": grouped, "stack, one launch per token": lambda: stack(1),
+                 "stack, one launch per layer": lambda: stack(0), "block": block}
+        try:
+            for name, f in forms.items():
+                first = [b.download(np.uint32, b.nbytes // 4) for b in f()]
+                assert ctx.device_status() == nh.OK
+                assert all(np.isfinite(a.view(np.float32)).all() for a in first), name
+                print(f"[robust] repeated launches: {name}", flush=True)
+                for r in range(100):
+                    got = [b.download(np.uint32, b.nbytes // 4) for b in f()]
+                    for j, (a, b) in enumerate(zip(got, first)):
+                        assert np.array_equal(a, b), f"{name}: repeat {r}, output {j} changed in {int((a != b).sum())} words"
+                assert ctx.device_status() == nh.OK
+        finally:
+            ctx.set_option(nh.OPT_STACK_LOOP, 1)
