@@ -68,6 +68,14 @@ __host__ __device__ constexpr int nmoe_dispatch_blocks(int n) {
 #ifndef NMOE_GROUPED_NW
 #define NMOE_GROUPED_NW 4
 #endif
+/* The small form: an expert of at most NMOE_SMALL_PASS entries (batched
+ * decode leaves most experts with a few) runs one pass of one 16-row block
+ * whose ring steps take NMOE_SMALL_GPS groups at a time, so each weight row
+ * is read 64 B a step instead of 32 B and the A stage holds 16 rows, not
+ * 64.  Built with four-wavefront blocks (one A load per wavefront a step). */
+#define NMOE_SMALL_PASS 16
+#define NMOE_SMALL_GPS 2
+__host__ __device__ constexpr bool nmoe_small_form(int nw) { return nw == 4; }
 
 /* k offset (within a lane's 16-k span) of operand element `slot`
  * (slot = 8 * slice + 2 * dword + half). */
@@ -409,6 +417,14 @@ struct nmoe_stage {
     uint32_t b[CW];
 };
 
+/* One stage buffer for both forms (the small form's stage where it is
+ * built, else the big form's again). */
+template <typename B, typename S>
+union nmoe_stage_buf {
+    B big;
+    S small;
+};
+
 /* A direct load into LDS from a wavefront-uniform base plus a 32-bit
  * per-lane byte offset: the compiler can address it as a scalar base and a
  * vector offset, so the stages' per-group addresses cost no vector
@@ -438,56 +454,86 @@ __device__ __forceinline__ void nmoe_stage_operand(const uint4 *plane, int r, in
     a1 = plane[8 * r + ((2 * kb + 1) ^ h)];
 }
 
-/* The direct loads of one stage's codes (NR weight rows of 32 B (q4) or
- * 16 B (q2)) over the NW wavefronts of a block: 1-KB instructions (16 B a
- * lane) where each wavefront has at least 1 KB to load, else 256-byte ones
- * (4 B a lane).  Every wavefront issues the same number, so the ring waits
- * are compile-time constants. */
-template <int BITS, int NR, int NW>
+/* A stage holds GPS groups of each weight row: the row's GPS * 32 B (q4)
+ * or GPS * 16 B (q2) of codes side by side, RB bytes a stage row.  Its
+ * 16-byte parts are rotated by the row (part c of row r sits at c ^ swz(r))
+ * so that the 16 rows a column block reads at once fall on distinct banks:
+ * 32-byte rows swap halves on row bit 3, 64-byte rows rotate by row bits
+ * 2-3. */
+template <int BITS, int GPS>
+struct nmoe_code_row {
+    static constexpr int RB = GPS * (BITS == 4 ? 32 : 16); /* stage bytes a row */
+    static constexpr int WPS = RB / 4;                      /* stage words a row */
+    static constexpr int LPR = RB / 16;                     /* 16-byte parts a row */
+    static_assert(LPR == 1 || LPR == 2 || LPR == 4, "a row is one, two or four 16-byte parts");
+    __device__ static __forceinline__ int swz(int r) { return LPR == 4 ? (r >> 2) & 3 : LPR == 2 ? (r >> 3) & 1 : 0; }
+};
+
+/* The direct loads of one stage's codes (NR weight rows of RB bytes) over
+ * the NW wavefronts of a block: 1-KB instructions (16 B a lane) where each
+ * wavefront has at least 1 KB to load, else 256-byte ones (4 B a lane).
+ * Every wavefront issues the same number, so the ring waits are
+ * compile-time constants. */
+template <int BITS, int NR, int NW, int GPS = 1>
 struct nmoe_code_plan {
-    static constexpr int BYTES = NR * (BITS == 4 ? 32 : 16);
+    static constexpr int BYTES = NR * nmoe_code_row<BITS, GPS>::RB;
     static constexpr bool WIDE = BYTES / NW >= 1024;
     static constexpr int INS_BYTES = WIDE ? 1024 : 256;
     static constexpr int PER_WAVE = BYTES / NW / INS_BYTES;
     static_assert(PER_WAVE >= 1 && PER_WAVE * INS_BYTES * NW == BYTES, "codes split evenly over the wavefronts");
-    static_assert(WIDE || BITS == 2, "a q4 wavefront loads at least 1 KB of codes");
+    static_assert(WIDE || (BITS == 2 && GPS == 1), "only q2 rows of one group load in 4-byte lanes");
 };
 
 /* Words of group g from a row's first word: 8 (q4) or 4 (q2). */
 template <int BITS>
 __host__ __device__ constexpr int nmoe_gwords() { return BITS == 4 ? 8 : 4; }
 
-/* Instruction j of one group's codes for one matrix of NR rows, in the
- * stage layout above: gbase is the matrix's first row at the group's first
- * word (uniform), rows wpr words apart. */
-template <int BITS, int NR, bool WIDE>
+/* Instruction j of one stage's codes for one matrix of NR rows, in the
+ * stage layout above: gbase is the matrix's first row at the stage's first
+ * word (uniform), rows wpr words apart.  A 1-KB instruction covers 64 / LPR
+ * rows, LPR lanes a row. */
+template <int BITS, int NR, bool WIDE, int GPS = 1>
 __device__ __forceinline__ void nmoe_stage_codes(uint32_t *stage, const uint32_t *gbase, int wpr, int j, int lane) {
-    if (BITS == 4) {
-        /* rows 32j + lane / 2, half (lane % 2) ^ row bit 3 */
-        const int row = 32 * j + (lane >> 1), half = (lane & 1) ^ ((row >> 3) & 1);
-        nmoe_dma<16>(gbase, 4u * (uint32_t)(row * wpr + 4 * half), stage + 256 * j);
-    } else if (WIDE) {
-        const int row = 64 * j + lane;
-        nmoe_dma<16>(gbase, 4u * (uint32_t)(row * wpr), stage + 256 * j);
+    using CR = nmoe_code_row<BITS, GPS>;
+    if (WIDE) {
+        const int row = (64 / CR::LPR) * j + lane / CR::LPR, part = (lane % CR::LPR) ^ CR::swz(row);
+        nmoe_dma<16>(gbase, 4u * (uint32_t)(row * wpr + 4 * part), stage + 256 * j);
     } else {
-        /* rows 16j + lane / 4, word lane % 4 */
+        /* q2, one group: rows 16j + lane / 4, word lane % 4 */
         const int row = 16 * j + (lane >> 2);
         nmoe_dma<4>(gbase, 4u * (uint32_t)(row * wpr + (lane & 3)), stage + 64 * j);
     }
 }
 
-/* The lane's code words of stage row r (of NR): q4 words 2kb, 2kb+1; q2
- * word kb. */
-template <int BITS, int NR>
-__device__ __forceinline__ void nmoe_stage_code_words(const uint32_t *stage, int r, int kb, uint32_t &w0,
-                                                      uint32_t &w1) {
+/* Byte offset, in a matrix's stage codes, of the lane's code words of
+ * group u (of the stage's GPS) in stage row r: q4 words 2kb, 2kb+1; q2
+ * word kb.  Computed once per lane, before the ring, and kept opaque: an
+ * offset summed from its parts at every read becomes a chain of address
+ * steps deep enough that the compiler no longer knows which stage the read
+ * belongs to, and then makes it wait for every stage's loads. */
+template <int BITS, int GPS = 1>
+__device__ __forceinline__ uint32_t nmoe_code_off(int r, int u, int kb) {
+    using CR = nmoe_code_row<BITS, GPS>;
+    uint32_t off;
     if (BITS == 4) {
-        const uint2 *rowp = (const uint2 *)(stage + 8 * r);
-        const uint2 v = rowp[kb ^ (2 * ((r >> 3) & 1))];
+        const int c = 2 * u + (kb >> 1); /* the 16-byte part holding words 2kb, 2kb+1 of group u */
+        off = (uint32_t)(CR::RB * r + 16 * (c ^ CR::swz(r)) + 8 * (kb & 1));
+    } else {
+        off = (uint32_t)(CR::RB * r + 16 * (u ^ CR::swz(r)) + 4 * kb);
+    }
+    asm("" : "+v"(off));
+    return off;
+}
+
+/* The code words at byte offset off of a matrix's stage codes. */
+template <int BITS>
+__device__ __forceinline__ void nmoe_code_read(const uint32_t *codes, uint32_t off, uint32_t &w0, uint32_t &w1) {
+    if (BITS == 4) {
+        const uint2 v = *(const uint2 *)((const char *)codes + off);
         w0 = v.x;
         w1 = v.y;
     } else {
-        w0 = stage[4 * r + kb];
+        w0 = *(const uint32_t *)((const char *)codes + off);
         w1 = 0;
     }
 }
@@ -587,11 +633,23 @@ __device__ __forceinline__ float nmoe_silu_fast(float x) {
  * (one A plane), 16 for fp32 x (hi + lo planes). */
 __host__ __device__ constexpr int nmoe_gu_rows(int xpl, int nw) { return nw * 32 / xpl; }
 
-/* LDS bytes of a gate/up block with ns stages: the stages (A rows, codes),
- * the scales, s_tok and s_as. */
+/* Bytes of one gate/up stage with mch entries a pass and gps groups a step:
+ * A rows (xpl planes x gps groups x mch rows x 128 B) and the codes of the
+ * tile's gate and up rows. */
+__host__ __device__ constexpr int nmoe_gu_stage(int bits, int xpl, int nw, int mch, int gps) {
+    return xpl * gps * mch * 128 + 2 * nmoe_gu_rows(xpl, nw) * gps * (bits == 4 ? 32 : 16);
+}
+/* A stage buffer holds the stage of either form. */
+__host__ __device__ constexpr int nmoe_gu_stage_max(int bits, int xpl, int nw) {
+    return nmoe_small_form(nw) && nmoe_gu_stage(bits, xpl, nw, NMOE_SMALL_PASS, NMOE_SMALL_GPS) >
+                                      nmoe_gu_stage(bits, xpl, nw, NMOE_MCHUNK, 1)
+               ? nmoe_gu_stage(bits, xpl, nw, NMOE_SMALL_PASS, NMOE_SMALL_GPS)
+               : nmoe_gu_stage(bits, xpl, nw, NMOE_MCHUNK, 1);
+}
+/* LDS bytes of a gate/up block with ns stages: the stages, the scales,
+ * s_tok and s_as. */
 __host__ __device__ constexpr int nmoe_gu_lds(int bits, int xpl, int nw, int ns) {
-    return ns * (xpl * NMOE_MCHUNK * 128 + 2 * nmoe_gu_rows(xpl, nw) * (bits == 4 ? 32 : 16)) +
-           2 * nmoe_gu_rows(xpl, nw) * 64 + 4 * NMOE_MCHUNK * (1 + nw);
+    return ns * nmoe_gu_stage_max(bits, xpl, nw) + 2 * nmoe_gu_rows(xpl, nw) * 64 + 4 * NMOE_MCHUNK * (1 + nw);
 }
 /* Stages: four where they fit the block's share of the CU's 160 KB (the
  * whole of it for eight wavefronts, half for four), else three. */
@@ -601,12 +659,12 @@ __host__ __device__ constexpr int nmoe_gu_stages(int bits, int xpl, int nw) {
 
 
 /* Expert e, gate and up rows NT * nt .. +NT-1: act rows of all the
- * expert's entries, 64 entries per pass.  NW wavefronts (eight: one block a
- * CU; four: two blocks a CU, whose set-up and epilogue then overlap the
- * other's ring), two per SIMD either way; wavefront w owns gate and up rows
- * (NT/NW)w .. +NT/NW-1 of the tile as NB 16-row MFMA column blocks each,
- * over the pass's (up to four) 16-entry row blocks, so a lane holds gate and
- * up of the same (entry, row).
+ * expert's entries, 64 entries per pass (16 in one pass in the small
+ * form).  NW wavefronts (eight: one block a CU; four: two blocks a CU, whose
+ * set-up and epilogue then overlap the other's ring), two per SIMD either
+ * way; wavefront w owns gate and up rows (NT/NW)w .. +NT/NW-1 of the tile as
+ * NB 16-row MFMA column blocks each, over the pass's (up to four) 16-entry
+ * row blocks, so a lane holds gate and up of the same (entry, row).
  *
  * y = sum_g s_g P_g + sum_g (b_g - 128 s_g) xs_g with P_g the MFMA product
  * of the group's A rows and the codes as bf16(128 + q); the second sum runs
@@ -625,27 +683,24 @@ nmoe_grouped_gateup_kernel(const uint8_t *pack, const uint16_t *xhi, const uint1
     static_assert(NW == 8 || NW == 4, "eight or four wavefronts");
     constexpr int NT = nmoe_gu_rows(XPL, NW);
     constexpr int NB = NT / (16 * NW);          /* column blocks per wavefront and matrix */
-    constexpr int MB = 4;                       /* row blocks per full pass */
-    constexpr int MCH = NMOE_MCHUNK;            /* entries per pass */
-    constexpr int AI = 8 / NW;                  /* A instructions per plane and wavefront */
     constexpr int NTH = 64 * NW;
-    constexpr int WPG = BITS == 4 ? 8 : 4;
-    using CP = nmoe_code_plan<BITS, 2 * NT, NW>;
-    constexpr int CPM = CP::BYTES / 2 / CP::INS_BYTES; /* code instructions per matrix */
     /* gate and up scales of the tile, chunk-major: 16-byte chunk q (groups
      * 8q..8q+7) of row r at [mat][q][r], so a ring step's 16 rows of one
      * group sit 16 bytes apart (distinct banks; row-major rows 64 bytes
      * apart put four rows on each bank) */
     __shared__ uint16_t s_s[2][G / 8][NT][8];
     constexpr int NS = nmoe_gu_stages(BITS, XPL, NW); /* (five measured no faster than four) */
-    typedef nmoe_stage<XPL, MCH, 2 * NT * WPG> Stage;
-    __shared__ Stage s_st0, s_st1, s_st2, s_st3;
-    auto stage = [&](int st) -> Stage & {
-        if constexpr (NS == 3) return st == 0 ? s_st0 : st == 1 ? s_st1 : s_st2;
-        else return st == 0 ? s_st0 : st == 1 ? s_st1 : st == 2 ? s_st2 : s_st3;
-    };
-    __shared__ uint32_t s_tok[MCH];
-    __shared__ float s_as[NW][MCH];
+    /* the stage buffers, each holding one stage of either form: a typed
+     * variable of its own per stage, so that the compiler tells the stages'
+     * direct loads apart */
+    typedef nmoe_stage<XPL, NMOE_MCHUNK, 2 * NT * nmoe_code_row<BITS, 1>::WPS> StageB;
+    typedef nmoe_stage<XPL, NMOE_SMALL_GPS * NMOE_SMALL_PASS, 2 * NT * nmoe_code_row<BITS, NMOE_SMALL_GPS>::WPS>
+        StageS;
+    typedef nmoe_stage_buf<StageB, typename std::conditional<nmoe_small_form(NW), StageS, StageB>::type> StageU;
+    static_assert(sizeof(StageU) == nmoe_gu_stage_max(BITS, XPL, NW), "stage buffer size");
+    __shared__ StageU s_st0, s_st1, s_st2, s_st3;
+    __shared__ uint32_t s_tok[NMOE_MCHUNK];
+    __shared__ float s_as[NW][NMOE_MCHUNK];
     /* pass lane pl of `lanes`: passes pl, pl + lanes, ... of tile (e, nt) */
     constexpr int NTILE = NMOE_INTER / NT;
     const int pl = blockIdx.x / (NMOE_EXPERTS * NTILE);
@@ -658,7 +713,7 @@ nmoe_grouped_gateup_kernel(const uint8_t *pack, const uint16_t *xhi, const uint1
     const uint4 rk = rank[es];
     const int e = (int)min(rk.x, (uint32_t)(NMOE_EXPERTS - 1));
     const uint32_t p0 = min(rk.y, (uint32_t)nrows), n = min(rk.z, (uint32_t)nrows - p0);
-    if (n <= (uint32_t)(pl * MCH)) return;
+    if (n <= (uint32_t)(pl * NMOE_MCHUNK)) return;
     const int tid = threadIdx.x, lane = tid & 63, col = lane & 15, kb = lane >> 4;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint8_t *ex = pack + (size_t)e * L::expert_size;
@@ -671,25 +726,54 @@ nmoe_grouped_gateup_kernel(const uint8_t *pack, const uint16_t *xhi, const uint1
     const uint16_t *bias[2] = {(const uint16_t *)(ex + L::gate_b) + (size_t)nt * NT * G,
                                (const uint16_t *)(ex + L::up_b) + (size_t)nt * NT * G};
 
+    /* the passes of one form: MCH entries a pass, GPS groups a ring step */
+    auto run = [&](auto mch_c, auto gps_c) {
+    constexpr int MCH = decltype(mch_c)::value, GPS = decltype(gps_c)::value;
+    constexpr int MB = MCH / 16;                /* row blocks per full pass */
+    constexpr int AI = GPS * MCH / 8 / NW;      /* A instructions per plane and wavefront a step */
+    static_assert(AI >= 1 && AI * NW * 8 == GPS * MCH, "A rows split evenly over the wavefronts");
+    using CR = nmoe_code_row<BITS, GPS>;
+    using CP = nmoe_code_plan<BITS, 2 * NT, NW, GPS>;
+    constexpr int CPM = CP::BYTES / 2 / CP::INS_BYTES; /* code instructions per matrix */
+    /* A rows of group u of a step at rows u MCH .. of each plane */
+    typedef nmoe_stage<XPL, GPS * MCH, 2 * NT * CR::WPS> Stage;
+    auto stage = [&](int st) -> Stage & {
+        StageU &b = st == 0 ? s_st0 : st == 1 ? s_st1 : st == 2 ? s_st2 : s_st3;
+        if constexpr (MCH == NMOE_MCHUNK) return b.big;
+        else return b.small;
+    };
+    /* the lane's code-word offsets in a matrix's stage codes, per group of
+     * a step and column block (the same in both matrices) */
+    uint32_t coff[GPS][NB];
+#pragma unroll
+    for (int u = 0; u < GPS; u++)
+#pragma unroll
+        for (int b2 = 0; b2 < NB; b2++) coff[u][b2] = nmoe_code_off<BITS, GPS>(rt0 + 16 * b2, u, kb);
+
     for (uint32_t m0 = pl * MCH; m0 < n; m0 += lanes * MCH) {
         if (tid < MCH) s_tok[tid] = min(perm[p0 + min(m0 + tid, n - 1)], (uint32_t)nrows - 1u) / (uint32_t)k;
         nmoe_lds_barrier();
-        /* this lane's A row for instruction wave + NW i: entry 8 (wave + NW i) + lane / 8 */
+        /* this lane's A row for instruction j = wave + NW i (rows 8j .. 8j+7
+         * of the stage plane: group j / (MCH / 8), entries 8 (j % (MCH / 8))
+         * + lane / 8) */
         uint32_t row_off[AI];
 #pragma unroll
         for (int i = 0; i < AI; i++)
-            row_off[i] = s_tok[8 * (wave + NW * i) + (lane >> 3)] * (uint32_t)(NMOE_HIDDEN * 2);
+            row_off[i] = s_tok[8 * ((wave + NW * i) % (MCH / 8)) + (lane >> 3)] * (uint32_t)(NMOE_HIDDEN * 2);
         const uint16_t *xpl[2] = {xhi, xlo};
-        auto issue = [&](int g, int st) {
+        auto issue = [&](int gs, int st) {
 #pragma unroll
             for (int pl = 0; pl < XPL; pl++)
 #pragma unroll
-                for (int i = 0; i < AI; i++)
-                    nmoe_stage_rows(stage(st).a[pl], xpl[pl] + 64 * g, row_off[i], wave + NW * i, lane);
+                for (int i = 0; i < AI; i++) {
+                    const int j = wave + NW * i;
+                    nmoe_stage_rows(stage(st).a[pl], xpl[pl] + 64 * (GPS * gs + j / (MCH / 8)), row_off[i], j, lane);
+                }
 #pragma unroll
             for (int i = 0; i < CP::PER_WAVE; i++)
-                nmoe_stage_codes<BITS, NT, CP::WIDE>(stage(st).b + cmat * NT * WPG, cbase + nmoe_gwords<BITS>() * g,
-                                                     Q::WPR_G, (CP::PER_WAVE * wave + i) % CPM, lane);
+                nmoe_stage_codes<BITS, NT, CP::WIDE, GPS>(stage(st).b + cmat * NT * CR::WPS,
+                                                          cbase + nmoe_gwords<BITS>() * GPS * gs, Q::WPR_G,
+                                                          (CP::PER_WAVE * wave + i) % CPM, lane);
         };
         const int nb = (int)min((n - m0 + 15) / 16, (uint32_t)MB);
         nmoe_f32x4 acc[2][NB][MB];
@@ -757,48 +841,61 @@ nmoe_grouped_gateup_kernel(const uint8_t *pack, const uint16_t *xhi, const uint1
                     }
                 }
         }
-        auto step = [&](int g, const int st, const bool ahead) {
-            nmoe_ring_step_barrier<XPL * AI + CP::PER_WAVE, G, NS>(g);
-            if (ahead) issue(g + NS - 1, (st + NS - 1) % NS);
-            uint4 bq[2][NB][2];
-            float sg[2][NB];
+        auto step = [&](int gs, const int st, const bool ahead) {
+            nmoe_ring_step_barrier<XPL * AI + CP::PER_WAVE, G / GPS, NS>(gs);
+            if (ahead) issue(gs + NS - 1, (st + NS - 1) % NS);
+            /* the step's scales: one bf16, or both groups' in one word */
+            uint32_t sw[2][NB];
 #pragma unroll
             for (int mat = 0; mat < 2; mat++)
 #pragma unroll
                 for (int b2 = 0; b2 < NB; b2++) {
-                    uint32_t w0, w1;
-                    /* kept apart: a read merged across the two matrices loses
-                     * the stage it belongs to, and then waits for every stage */
-                    if (mat == 1 && b2 == 0) asm volatile("" ::: "memory");
-                    nmoe_stage_code_words<BITS, NT>(stage(st).b + mat * NT * WPG, rt0 + 16 * b2, kb, w0, w1);
-                    nmoe_codes_bf16<BITS>(w0, w1, bq[mat][b2][0], bq[mat][b2][1]);
-                    sg[mat][b2] = nmoe_bf16f(s_s[mat][g >> 3][rt0 + 16 * b2][g & 7]);
+                    const uint16_t *sp = &s_s[mat][(GPS * gs) >> 3][rt0 + 16 * b2][(GPS * gs) & 7];
+                    sw[mat][b2] = GPS == 2 ? *(const uint32_t *)sp : (uint32_t)*sp;
                 }
 #pragma unroll
-            for (int mb = 0; mb < MB; mb++) {
-                if (mb < nb) {
-                    uint4 a[XPL][2];
+            for (int u = 0; u < GPS; u++) {
+                uint4 bq[2][NB][2];
+                float sg[2][NB];
 #pragma unroll
-                    for (int pl = 0; pl < XPL; pl++)
-                        nmoe_stage_operand(stage(st).a[pl], 16 * mb + col, kb, a[pl][0], a[pl][1]);
+                for (int mat = 0; mat < 2; mat++)
 #pragma unroll
-                    for (int mat = 0; mat < 2; mat++)
+                    for (int b2 = 0; b2 < NB; b2++) {
+                        uint32_t w0, w1;
+                        /* kept apart: two reads merged into one instruction lose
+                         * the stage they belong to, and then wait for every stage */
+                        if (u + mat + b2 > 0) asm volatile("" ::: "memory");
+                        nmoe_code_read<BITS>(stage(st).b + mat * NT * CR::WPS, coff[u][b2], w0, w1);
+                        nmoe_codes_bf16<BITS>(w0, w1, bq[mat][b2][0], bq[mat][b2][1]);
+                        sg[mat][b2] = nmoe_bf16f((uint16_t)(sw[mat][b2] >> (16 * u)));
+                    }
 #pragma unroll
-                        for (int b2 = 0; b2 < NB; b2++) {
-                            nmoe_f32x4 pp = nmoe_mfma16(a[0][0], bq[mat][b2][0], nmoe_f32x4{0.0f, 0.0f, 0.0f, 0.0f});
-                            pp = nmoe_mfma16(a[0][1], bq[mat][b2][1], pp);
-                            if (XPL == 2) {
-                                pp = nmoe_mfma16(a[XPL - 1][0], bq[mat][b2][0], pp);
-                                pp = nmoe_mfma16(a[XPL - 1][1], bq[mat][b2][1], pp);
+                for (int mb = 0; mb < MB; mb++) {
+                    if (mb < nb) {
+                        uint4 a[XPL][2];
+#pragma unroll
+                        for (int pl = 0; pl < XPL; pl++)
+                            nmoe_stage_operand(stage(st).a[pl], MCH * u + 16 * mb + col, kb, a[pl][0], a[pl][1]);
+#pragma unroll
+                        for (int mat = 0; mat < 2; mat++)
+#pragma unroll
+                            for (int b2 = 0; b2 < NB; b2++) {
+                                nmoe_f32x4 pp =
+                                    nmoe_mfma16(a[0][0], bq[mat][b2][0], nmoe_f32x4{0.0f, 0.0f, 0.0f, 0.0f});
+                                pp = nmoe_mfma16(a[0][1], bq[mat][b2][1], pp);
+                                if (XPL == 2) {
+                                    pp = nmoe_mfma16(a[XPL - 1][0], bq[mat][b2][0], pp);
+                                    pp = nmoe_mfma16(a[XPL - 1][1], bq[mat][b2][1], pp);
+                                }
+#pragma unroll
+                                for (int i = 0; i < 4; i++)
+                                    acc[mat][b2][mb][i] = __builtin_fmaf(sg[mat][b2], pp[i], acc[mat][b2][mb][i]);
                             }
-#pragma unroll
-                            for (int i = 0; i < 4; i++)
-                                acc[mat][b2][mb][i] = __builtin_fmaf(sg[mat][b2], pp[i], acc[mat][b2][mb][i]);
-                        }
+                    }
                 }
             }
         };
-        nmoe_ring_run<G, NS>(step);
+        nmoe_ring_run<G / GPS, NS>(step);
         {
             /* epilogue: act = SiLU(gate) * up as hi + lo bf16, in the down
              * kernel's operand order; group sums of act rows (a down group
@@ -857,6 +954,15 @@ nmoe_grouped_gateup_kernel(const uint8_t *pack, const uint16_t *xhi, const uint1
         }
         nmoe_lds_barrier(); /* s_tok, s_as and the stages are reused by the next pass */
     }
+    };
+    /* block-uniform: the expert's entry count picks the form */
+    if constexpr (nmoe_small_form(NW)) {
+        if (n <= (uint32_t)NMOE_SMALL_PASS) {
+            run(std::integral_constant<int, NMOE_SMALL_PASS>{}, std::integral_constant<int, NMOE_SMALL_GPS>{});
+            return;
+        }
+    }
+    run(std::integral_constant<int, NMOE_MCHUNK>{}, std::integral_constant<int, 1>{});
 }
 
 /* ------------------------------------------------------------ down */
@@ -864,20 +970,31 @@ nmoe_grouped_gateup_kernel(const uint8_t *pack, const uint16_t *xhi, const uint1
 /* Down rows per block of NW wavefronts: 64 a wavefront. */
 __host__ __device__ constexpr int nmoe_dn_rows(int nw) { return nw * 64; }
 
-/* LDS bytes of a down block with ns stages: the stages (act hi and lo rows,
- * codes), the scales and s_q. */
+/* Bytes of one down stage (act hi and lo rows, codes) with mch entries a
+ * pass and gps groups a step; a stage buffer holds either form's. */
+__host__ __device__ constexpr int nmoe_dn_stage(int bits, int nw, int mch, int gps) {
+    return 2 * gps * mch * 128 + nmoe_dn_rows(nw) * gps * (bits == 4 ? 32 : 16);
+}
+__host__ __device__ constexpr int nmoe_dn_stage_max(int bits, int nw) {
+    return nmoe_small_form(nw) && nmoe_dn_stage(bits, nw, NMOE_SMALL_PASS, NMOE_SMALL_GPS) >
+                                      nmoe_dn_stage(bits, nw, NMOE_MCHUNK, 1)
+               ? nmoe_dn_stage(bits, nw, NMOE_SMALL_PASS, NMOE_SMALL_GPS)
+               : nmoe_dn_stage(bits, nw, NMOE_MCHUNK, 1);
+}
+/* LDS bytes of a down block with ns stages: the stages, the scales and
+ * s_q. */
 __host__ __device__ constexpr int nmoe_dn_lds(int bits, int nw, int ns) {
-    return ns * (2 * NMOE_MCHUNK * 128 + nmoe_dn_rows(nw) * (bits == 4 ? 32 : 16)) + nmoe_dn_rows(nw) * 16 +
-           4 * NMOE_MCHUNK;
+    return ns * nmoe_dn_stage_max(bits, nw) + nmoe_dn_rows(nw) * 16 + 4 * NMOE_MCHUNK;
 }
 __host__ __device__ constexpr int nmoe_dn_stages(int bits, int nw) {
     return nmoe_dn_lds(bits, nw, 4) <= (nw == 8 ? 160 : 80) * 1024 - 512 ? 4 : 3;
 }
 
 /* Expert e, down rows NT * nt .. +NT-1: y[q][row] for all the expert's
- * entries q, 64 per pass.  NW wavefronts (as in the gate/up kernel);
- * wavefront w owns rows (NT/NW)w .. +NT/NW-1 of the tile as NB 16-row
- * column blocks.  act enters as hi and lo bf16 planes. */
+ * entries q, 64 per pass (16 in one pass in the small form).  NW
+ * wavefronts (as in the gate/up kernel); wavefront w owns rows
+ * (NT/NW)w .. +NT/NW-1 of the tile as NB 16-row column blocks.  act enters
+ * as hi and lo bf16 planes. */
 template <int BITS, int NW>
 __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
 nmoe_grouped_down_kernel(const uint8_t *pack, const uint16_t *ahi, const uint16_t *alo, const float *as,
@@ -889,20 +1006,16 @@ nmoe_grouped_down_kernel(const uint8_t *pack, const uint16_t *ahi, const uint16_
     static_assert(NW == 8 || NW == 4, "eight or four wavefronts");
     constexpr int NT = nmoe_dn_rows(NW);
     constexpr int NB = NT / (16 * NW);
-    constexpr int MB = 4;           /* row blocks per full pass */
-    constexpr int MCH = NMOE_MCHUNK; /* entries per pass */
-    constexpr int AI = 8 / NW;      /* A instructions per plane and wavefront */
     constexpr int NS = nmoe_dn_stages(BITS, NW);
-    constexpr int WPG = BITS == 4 ? 8 : 4;
-    using CP = nmoe_code_plan<BITS, NT, NW>;
     __shared__ uint16_t s_s[NT][G]; /* scales of the tile */
-    typedef nmoe_stage<2, MCH, NT * WPG> Stage;
-    __shared__ Stage s_st0, s_st1, s_st2, s_st3;
-    auto stage = [&](int st) -> Stage & {
-        if constexpr (NS == 3) return st == 0 ? s_st0 : st == 1 ? s_st1 : s_st2;
-        else return st == 0 ? s_st0 : st == 1 ? s_st1 : st == 2 ? s_st2 : s_st3;
-    };
-    __shared__ uint32_t s_q[MCH]; /* the chunk's output slots */
+    /* stage buffers holding one stage of either form, one typed variable
+     * per stage (as in the gate/up kernel) */
+    typedef nmoe_stage<2, NMOE_MCHUNK, NT * nmoe_code_row<BITS, 1>::WPS> StageB;
+    typedef nmoe_stage<2, NMOE_SMALL_GPS * NMOE_SMALL_PASS, NT * nmoe_code_row<BITS, NMOE_SMALL_GPS>::WPS> StageS;
+    typedef nmoe_stage_buf<StageB, typename std::conditional<nmoe_small_form(NW), StageS, StageB>::type> StageU;
+    static_assert(sizeof(StageU) == nmoe_dn_stage_max(BITS, NW), "stage buffer size");
+    __shared__ StageU s_st0, s_st1, s_st2, s_st3;
+    __shared__ uint32_t s_q[NMOE_MCHUNK]; /* the chunk's output slots */
     constexpr int NTILE = NMOE_HIDDEN / NT;
     const int pl = blockIdx.x / (NMOE_EXPERTS * NTILE); /* pass lane, as in the gate/up kernel */
     /* the tile's expert is the es-th by entries (most first), so the
@@ -912,34 +1025,60 @@ nmoe_grouped_down_kernel(const uint8_t *pack, const uint16_t *ahi, const uint16_
     const uint4 rk = rank[es]; /* clamped as in the gate/up kernel */
     const int e = (int)min(rk.x, (uint32_t)(NMOE_EXPERTS - 1));
     const uint32_t p0 = min(rk.y, (uint32_t)nrows), n = min(rk.z, (uint32_t)nrows - p0);
-    if (n <= (uint32_t)(pl * MCH)) return;
+    if (n <= (uint32_t)(pl * NMOE_MCHUNK)) return;
     const int tid = threadIdx.x, lane = tid & 63, col = lane & 15, kb = lane >> 4;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint8_t *ex = pack + (size_t)e * L::expert_size;
     const int rt0 = (NT / NW) * wave + col; /* tile row of column block nb: rt0 + 16 nb */
     const uint32_t *cbase = (const uint32_t *)(ex + L::down_w) + (size_t)nt * NT * Q::WPR_D;
     const uint16_t *bias = (const uint16_t *)(ex + L::down_b) + (size_t)nt * NT * G;
+
+    /* the passes of one form: MCH entries a pass, GPS groups a ring step */
+    auto run = [&](auto mch_c, auto gps_c) {
+    constexpr int MCH = decltype(mch_c)::value, GPS = decltype(gps_c)::value;
+    constexpr int MB = MCH / 16;           /* row blocks per full pass */
+    constexpr int AI = GPS * MCH / 8 / NW; /* A instructions per plane and wavefront a step */
+    static_assert(AI >= 1 && AI * NW * 8 == GPS * MCH, "A rows split evenly over the wavefronts");
+    using CR = nmoe_code_row<BITS, GPS>;
+    using CP = nmoe_code_plan<BITS, NT, NW, GPS>;
+    typedef nmoe_stage<2, GPS * MCH, NT * CR::WPS> Stage;
+    auto stage = [&](int st) -> Stage & {
+        StageU &b = st == 0 ? s_st0 : st == 1 ? s_st1 : st == 2 ? s_st2 : s_st3;
+        if constexpr (MCH == NMOE_MCHUNK) return b.big;
+        else return b.small;
+    };
+    /* the lane's code-word offsets in the stage codes (as in the gate/up kernel) */
+    uint32_t coff[GPS][NB];
+#pragma unroll
+    for (int u = 0; u < GPS; u++)
+#pragma unroll
+        for (int b2 = 0; b2 < NB; b2++) coff[u][b2] = nmoe_code_off<BITS, GPS>(rt0 + 16 * b2, u, kb);
     for (uint32_t m0 = pl * MCH; m0 < n; m0 += lanes * MCH) {
         /* the chunk's output slots, stored to LDS after the stages are issued
          * (so that this load's wait does not hold them back) and visible
          * after the barrier below */
         const uint32_t qv = tid < MCH ? min(perm[p0 + min(m0 + tid, n - 1)], (uint32_t)nrows - 1u) : 0u;
-        /* this lane's A row for instruction wave + NW i: act row p0 + m0 + 8 (wave + NW i) + lane / 8 */
+        /* this lane's A row for instruction j = wave + NW i (group
+         * j / (MCH / 8) of the step): act row p0 + m0 + 8 (j % (MCH / 8)) +
+         * lane / 8 */
         uint32_t row_off[AI];
 #pragma unroll
         for (int i = 0; i < AI; i++)
-            row_off[i] = (p0 + min(m0 + 8 * (wave + NW * i) + (lane >> 3), n - 1)) * (uint32_t)(NMOE_INTER * 2);
+            row_off[i] = (p0 + min(m0 + 8 * ((wave + NW * i) % (MCH / 8)) + (lane >> 3), n - 1)) *
+                         (uint32_t)(NMOE_INTER * 2);
         const uint16_t *apl[2] = {ahi, alo};
-        auto issue = [&](int g, int st) {
+        auto issue = [&](int gs, int st) {
 #pragma unroll
             for (int pl = 0; pl < 2; pl++)
 #pragma unroll
-                for (int i = 0; i < AI; i++)
-                    nmoe_stage_rows(stage(st).a[pl], apl[pl] + 64 * g, row_off[i], wave + NW * i, lane);
+                for (int i = 0; i < AI; i++) {
+                    const int j = wave + NW * i;
+                    nmoe_stage_rows(stage(st).a[pl], apl[pl] + 64 * (GPS * gs + j / (MCH / 8)), row_off[i], j, lane);
+                }
 #pragma unroll
             for (int i = 0; i < CP::PER_WAVE; i++)
-                nmoe_stage_codes<BITS, NT, CP::WIDE>(stage(st).b, cbase + nmoe_gwords<BITS>() * g, Q::WPR_D,
-                                                     CP::PER_WAVE * wave + i, lane);
+                nmoe_stage_codes<BITS, NT, CP::WIDE, GPS>(stage(st).b, cbase + nmoe_gwords<BITS>() * GPS * gs,
+                                                          Q::WPR_D, CP::PER_WAVE * wave + i, lane);
         };
         const int nb = (int)min((n - m0 + 15) / 16, (uint32_t)MB);
         nmoe_f32x4 acc[NB][MB];
@@ -985,37 +1124,50 @@ nmoe_grouped_down_kernel(const uint8_t *pack, const uint16_t *ahi, const uint16_
                             acc[b2][mb] = __builtin_amdgcn_mfma_f32_16x16x4f32(tq == 0 ? av[mb].x : av[mb].y,
                                                                                cv[b2][tq], acc[b2][mb], 0, 0, 0);
         }
-        auto step = [&](int g, const int st, const bool ahead) {
-            nmoe_ring_step_barrier<2 * AI + CP::PER_WAVE, G, NS>(g);
-            if (ahead) issue(g + NS - 1, (st + NS - 1) % NS);
-            uint4 bq[NB][2];
-            float sg[NB];
+        auto step = [&](int gs, const int st, const bool ahead) {
+            nmoe_ring_step_barrier<2 * AI + CP::PER_WAVE, G / GPS, NS>(gs);
+            if (ahead) issue(gs + NS - 1, (st + NS - 1) % NS);
+            /* the step's scales: one bf16, or both groups' in one word */
+            uint32_t sw[NB];
 #pragma unroll
             for (int b2 = 0; b2 < NB; b2++) {
-                uint32_t w0, w1;
-                nmoe_stage_code_words<BITS, NT>(stage(st).b, rt0 + 16 * b2, kb, w0, w1);
-                nmoe_codes_bf16<BITS>(w0, w1, bq[b2][0], bq[b2][1]);
-                sg[b2] = nmoe_bf16f(s_s[rt0 + 16 * b2][g]);
+                const uint16_t *sp = &s_s[rt0 + 16 * b2][GPS * gs];
+                sw[b2] = GPS == 2 ? *(const uint32_t *)sp : (uint32_t)*sp;
             }
 #pragma unroll
-            for (int mb = 0; mb < MB; mb++) {
-                if (mb < nb) {
-                    uint4 h0, h1, l0, l1;
-                    nmoe_stage_operand(stage(st).a[0], 16 * mb + col, kb, h0, h1);
-                    nmoe_stage_operand(stage(st).a[1], 16 * mb + col, kb, l0, l1);
+            for (int u = 0; u < GPS; u++) {
+                uint4 bq[NB][2];
+                float sg[NB];
 #pragma unroll
-                    for (int b2 = 0; b2 < NB; b2++) {
-                        nmoe_f32x4 pp = nmoe_mfma16(h0, bq[b2][0], nmoe_f32x4{0.0f, 0.0f, 0.0f, 0.0f});
-                        pp = nmoe_mfma16(h1, bq[b2][1], pp);
-                        pp = nmoe_mfma16(l0, bq[b2][0], pp);
-                        pp = nmoe_mfma16(l1, bq[b2][1], pp);
+                for (int b2 = 0; b2 < NB; b2++) {
+                    uint32_t w0, w1;
+                    /* kept apart, as in the gate/up kernel */
+                    if (u + b2 > 0) asm volatile("" ::: "memory");
+                    nmoe_code_read<BITS>(stage(st).b, coff[u][b2], w0, w1);
+                    nmoe_codes_bf16<BITS>(w0, w1, bq[b2][0], bq[b2][1]);
+                    sg[b2] = nmoe_bf16f((uint16_t)(sw[b2] >> (16 * u)));
+                }
 #pragma unroll
-                        for (int i = 0; i < 4; i++) acc[b2][mb][i] = __builtin_fmaf(sg[b2], pp[i], acc[b2][mb][i]);
+                for (int mb = 0; mb < MB; mb++) {
+                    if (mb < nb) {
+                        uint4 h0, h1, l0, l1;
+                        nmoe_stage_operand(stage(st).a[0], MCH * u + 16 * mb + col, kb, h0, h1);
+                        nmoe_stage_operand(stage(st).a[1], MCH * u + 16 * mb + col, kb, l0, l1);
+#pragma unroll
+                        for (int b2 = 0; b2 < NB; b2++) {
+                            nmoe_f32x4 pp = nmoe_mfma16(h0, bq[b2][0], nmoe_f32x4{0.0f, 0.0f, 0.0f, 0.0f});
+                            pp = nmoe_mfma16(h1, bq[b2][1], pp);
+                            pp = nmoe_mfma16(l0, bq[b2][0], pp);
+                            pp = nmoe_mfma16(l1, bq[b2][1], pp);
+#pragma unroll
+                            for (int i = 0; i < 4; i++)
+                                acc[b2][mb][i] = __builtin_fmaf(sg[b2], pp[i], acc[b2][mb][i]);
+                        }
                     }
                 }
             }
         };
-        nmoe_ring_run<G, NS>(step);
+        nmoe_ring_run<G / GPS, NS>(step);
 #pragma unroll
         for (int b2 = 0; b2 < NB; b2++) {
             const int r = nt * NT + rt0 + 16 * b2;
@@ -1030,6 +1182,15 @@ nmoe_grouped_down_kernel(const uint8_t *pack, const uint16_t *ahi, const uint16_
         }
         nmoe_lds_barrier(); /* the stages and s_q are reused by the next pass */
     }
+    };
+    /* block-uniform: the expert's entry count picks the form */
+    if constexpr (nmoe_small_form(NW)) {
+        if (n <= (uint32_t)NMOE_SMALL_PASS) {
+            run(std::integral_constant<int, NMOE_SMALL_PASS>{}, std::integral_constant<int, NMOE_SMALL_GPS>{});
+            return;
+        }
+    }
+    run(std::integral_constant<int, NMOE_MCHUNK>{}, std::integral_constant<int, 1>{});
 }
 
 /* ------------------------------------------------------------ combine */

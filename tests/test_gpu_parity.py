@@ -619,6 +619,46 @@ def test_grouped_experts_against_oracle(big, nh, bits, ntok, k, xkind, ikind):
 
 
 @pytest.mark.parametrize("bits", [4, 2])
+@pytest.mark.parametrize("xkind", ["bf16", "f32"])
+def test_grouped_small_and_big_forms(big, nh, bits, xkind):
+    """Experts of at most 16 entries take the small form (one 16-entry pass,
+    two groups a ring step), larger ones the 64-entry passes, in the same
+    launch: experts of exactly 16, 17, 64, 65 and 1 entries, every token's
+    output against the oracle."""
+    rng = np.random.default_rng(700 + 10 * bits + (xkind == "f32"))
+    seed, layer, ntok, k = 29, 45 + bits, 80, 8
+    big.synth_layer(layer, bits, seed, SIGMA[bits])
+    want_n = {5: 16, 6: 17, 7: 64, 8: 65, 9: 1}
+    idx = np.zeros((ntok, 8), np.uint32)
+    rest = np.array([e for e in range(256) if e not in want_n])
+    for t in range(ntok):
+        idx[t, :k] = rng.choice(rest, k, replace=False)
+    slot = 0
+    for e, cnt in want_n.items():  # expert e replaces one slot of cnt distinct tokens
+        for t in rng.choice(ntok, cnt, replace=False):
+            idx[t, slot] = e
+        slot += 1
+    counts = np.bincount(idx[:, :k].ravel(), minlength=256)
+    for e, cnt in want_n.items():
+        assert counts[e] == cnt
+    w = rng.dirichlet(np.ones(k), size=ntok).astype(np.float32)
+    xf = rng.standard_normal((ntok, 2048)).astype(np.float32)
+    if xkind == "bf16":
+        xb = B.f32_to_bf16(xf)
+        x, xdev, dt = B.bf16_to_f32(xb).reshape(ntok, 2048), xb, nh.BF16
+    else:
+        x, xdev, dt = xf, xf, nh.F32
+    h = rng.standard_normal((ntok, 2048)).astype(np.float32)
+    d = [big.to_device(a) for a in (xdev, idx, w, h)]
+    out = big.alloc(ntok * 2048 * 4)
+    big._check(big.experts(bits, layer, d[0], dt, ntok, k, d[1], d[2], d[3], out))
+    assert big.device_status() == nh.OK
+    pack = host_pack(bits, seed, layer, idx[:, :k].ravel())
+    want = B.moe_experts(pack, bits, x, k, idx, w, h)
+    assert_close(out.download(np.float32, (ntok, 2048)), want, what=f"small/big forms q{bits} x={xkind}")
+
+
+@pytest.mark.parametrize("bits", [4, 2])
 def test_prefill_2048_sampled(big, nh, bits):
     """C5 shape: 2048 tokens, uniform-random logits -> device top-8 ->
     grouped experts; routing bit-exact for all 2048 tokens, outputs checked
