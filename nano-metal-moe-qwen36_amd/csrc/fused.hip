@@ -189,7 +189,7 @@ __device__ __forceinline__ void nmoe_st_tagged_die(uint64_t *p, uint32_t epoch, 
     asm volatile("global_store_dwordx2 %0, %1, off" ::"v"(p), "v"(w) : "memory");
 }
 __device__ __forceinline__ uint64_t nmoe_ld_tagged_die(const uint64_t *p) {
-    return __hip_atomic_load((uint64_t *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    return __hip_atomic_load((nmoe_g64 *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
 /* A 16-byte load marked non-temporal (the expert weights are read once per
@@ -197,6 +197,12 @@ __device__ __forceinline__ uint64_t nmoe_ld_tagged_die(const uint64_t *p) {
 typedef unsigned int nmoe_u32x4 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ uint4 nmoe_ld_nt4(const uint4 *p) {
     const nmoe_u32x4 v = __builtin_nontemporal_load((const nmoe_u32x4 *)p);
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+typedef __attribute__((address_space(1))) nmoe_u32x4 nmoe_gv4;
+typedef __attribute__((address_space(1))) uint16_t nmoe_g16;
+__device__ __forceinline__ uint4 nmoe_ld_nt4(const nmoe_gv4 *p) {
+    const nmoe_u32x4 v = __builtin_nontemporal_load(p);
     return make_uint4(v.x, v.y, v.z, v.w);
 }
 
@@ -213,7 +219,7 @@ __device__ __forceinline__ uint32_t nmoe_xcc_id() {
  * valid one.  Nothing read afterwards is used as an address without a
  * clamp, so the block still finishes in bounds. */
 __device__ __forceinline__ void nmoe_wait_expired(uint32_t *status, uint32_t *bad) {
-    __hip_atomic_store(status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store((nmoe_g32 *)status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __hip_atomic_store(bad, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 
@@ -297,10 +303,26 @@ __device__ __forceinline__ bool nmoe_poll2(const uint64_t *const p[N], uint32_t 
  * round is about 32 times shorter than a round trip to memory, so the bound
  * is 32 times the rounds of the memory polls: the waiting wavefront then
  * gives up no sooner than the wavefront it waits for. */
+/* An LDS word read by another wavefront's hand-off: ds_read_b32 written
+ * out, followed by its own lgkmcnt wait.  An atomic LDS load would do, but
+ * it reaches the compiler's wait placement without the alias scope that
+ * tells it which LDS variable it reads; in a kernel that also loads LDS
+ * directly from memory (the stack's router rows, the block form's
+ * shared-down rows) the compiler then makes it wait for every load in
+ * flight, the expert weight stream included.  The clobbers keep the
+ * surrounding LDS accesses in program order; the hardware completes one
+ * wavefront's LDS accesses in order. */
+__device__ __forceinline__ uint32_t nmoe_lds_read_flag(const uint32_t *w) {
+    uint32_t v;
+    asm volatile("ds_read_b32 %0, %1" : "=v"(v) : "v"((uint32_t)(size_t)w) : "memory");
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(v) : : "memory");
+    return v;
+}
+
 __device__ __forceinline__ void nmoe_lds_wait_above(uint32_t *w, uint32_t v, uint32_t *status, uint32_t *bad,
                                                     uint32_t spin) {
     uint32_t spins = 0;
-    while (__hip_atomic_load(w, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) <= v) {
+    while (nmoe_lds_read_flag(w) <= v) {
         __builtin_amdgcn_s_sleep(1);
         if (++spins > 32u * spin) {
             nmoe_wait_expired(status, bad);
@@ -309,9 +331,7 @@ __device__ __forceinline__ void nmoe_lds_wait_above(uint32_t *w, uint32_t v, uin
     }
 }
 
-__device__ __forceinline__ bool nmoe_lds_flag(uint32_t *f) {
-    return __hip_atomic_load(f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) != 0u;
-}
+__device__ __forceinline__ bool nmoe_lds_flag(uint32_t *f) { return nmoe_lds_read_flag(f) != 0u; }
 
 /* The lane's n activations at columns c0.. (fp32, bf16, or normalised h).
  * Normalised: math.m:63 computes (input / rms) * 1.0f.  With rinv the double
@@ -340,7 +360,7 @@ __device__ __forceinline__ float nmoe_norm_weight(const uint16_t *w, int c, int 
 
 /* A tagged word with a raw 32-bit payload (halves of a double). */
 __device__ __forceinline__ void nmoe_st_tagged_u32(uint64_t *p, uint32_t epoch, uint32_t v) {
-    __hip_atomic_store(p, ((uint64_t)epoch << 32) | v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store((nmoe_g64 *)p, ((uint64_t)epoch << 32) | v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 /* LDS slot of act element e.  Lane dl of a down row reads float4 chunks
@@ -561,7 +581,8 @@ __device__ __forceinline__ void nmoe_fused_body(nmoe_fused_args a, const nmoe_st
             uint32_t e = a.epoch_arg;
             if (e == 0u) {
                 e = ep_old + 1u;
-                __hip_atomic_store(ep, STK ? ep_old + (uint32_t)nl : e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store((nmoe_g32 *)ep, STK ? ep_old + (uint32_t)nl : e, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
             }
             s_epoch = e;
             s_bad = 0u;
@@ -924,8 +945,17 @@ __device__ __forceinline__ void nmoe_fused_body(nmoe_fused_args a, const nmoe_st
         }
         if (lane == 0) __hip_atomic_store(&s_confirm, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
         /* XSTACK: the next layer's router row, while this layer streams
-         * (the candidate wavefront read this one before the logits came) */
-        if (STK && ly + 1 < nl) load_rrow(s_stk[4 * (ly + 1) + 1], s_stk[4 * (ly + 1) + 2], s_stk[4 * (ly + 1) + 3]);
+         * (the candidate wavefront read this one before the logits came).
+         * This wavefront has nothing else to do until the block's next
+         * barrier, so it waits for those loads here: then no direct LDS load
+         * is pending where its path joins the workers', and the compiler
+         * keeps the workers' waits for their weight rows exact (with one
+         * pending, loads of two kinds share the counter and every wait after
+         * the join becomes a wait for all loads) */
+        if (STK && ly + 1 < nl) {
+            load_rrow(s_stk[4 * (ly + 1) + 1], s_stk[4 * (ly + 1) + 2], s_stk[4 * (ly + 1) + 3]);
+            __builtin_amdgcn_s_waitcnt(0);
+        }
     }
     if (!ROUTE) {
         if (tid < NMOE_MAX_K) {
@@ -955,15 +985,20 @@ __device__ __forceinline__ void nmoe_fused_body(nmoe_fused_args a, const nmoe_st
     uint4 xr[XV];
     uint4 gwv[GSTEPS], uwv[GSTEPS], dwv[DSTEPS];
     uint32_t gsc[GSTEPS], gbi[GSTEPS], usc[GSTEPS], ubi[GSTEPS], dsc[DSTEPS], dbi[DSTEPS];
+    /* the weights through a global-memory pointer (the stack form takes the
+     * pack from its layer table in LDS as a generic one): as global loads
+     * they complete in order, so the gate/up rows are used while the down
+     * rows are still in flight (flat loads would make the first use wait for
+     * all of them) */
     auto load_expert = [&](uint32_t e) {
-        const uint8_t *ex = pack + (size_t)e * L::expert_size;
+        const nmoe_gu8 *ex = (const nmoe_gu8 *)pack + (size_t)e * L::expert_size;
 #pragma unroll
         for (int i = 0; i < GSTEPS; i++) {
             int row = grow0 + i * RPS;
-            gwv[i] = nmoe_ld_nt4(&((const uint4 *)(ex + L::gate_w))[(size_t)row * (Q::WPR_G / 4) + gl]);
-            uwv[i] = nmoe_ld_nt4(&((const uint4 *)(ex + L::up_w))[(size_t)row * (Q::WPR_G / 4) + gl]);
-            const uint16_t *gs = (const uint16_t *)(ex + L::gate_s) + row * Q::GPR_G + ggrp;
-            const uint16_t *us = (const uint16_t *)(ex + L::up_s) + row * Q::GPR_G + ggrp;
+            gwv[i] = nmoe_ld_nt4((const nmoe_gv4 *)(ex + L::gate_w) + (size_t)row * (Q::WPR_G / 4) + gl);
+            uwv[i] = nmoe_ld_nt4((const nmoe_gv4 *)(ex + L::up_w) + (size_t)row * (Q::WPR_G / 4) + gl);
+            const nmoe_g16 *gs = (const nmoe_g16 *)(ex + L::gate_s) + row * Q::GPR_G + ggrp;
+            const nmoe_g16 *us = (const nmoe_g16 *)(ex + L::up_s) + row * Q::GPR_G + ggrp;
             gsc[i] = __builtin_nontemporal_load(gs);
             gbi[i] = __builtin_nontemporal_load(gs + NMOE_INTER * Q::GPR_G);
             usc[i] = __builtin_nontemporal_load(us);
@@ -973,10 +1008,27 @@ __device__ __forceinline__ void nmoe_fused_body(nmoe_fused_args a, const nmoe_st
 #pragma unroll
         for (int i = 0; i < DSTEPS; i++) {
             int row = drow0 + i * RPW_D;
-            dwv[i] = nmoe_ld_nt4(&((const uint4 *)(ex + L::down_w))[(size_t)row * (Q::WPR_D / 4) + dl]);
-            const uint16_t *ds = (const uint16_t *)(ex + L::down_s) + row * Q::GPR_D + dgrp;
+            dwv[i] = nmoe_ld_nt4((const nmoe_gv4 *)(ex + L::down_w) + (size_t)row * (Q::WPR_D / 4) + dl);
+            const nmoe_g16 *ds = (const nmoe_g16 *)(ex + L::down_s) + row * Q::GPR_D + dgrp;
             dsc[i] = __builtin_nontemporal_load(ds);
             dbi[i] = __builtin_nontemporal_load(ds + NMOE_HIDDEN * Q::GPR_D);
+        }
+    };
+    float xs[Q::CPL];
+    /* ---- G (workers): gate/up + SwiGLU -> act[g], published once the
+     * control wavefront has confirmed the expert */
+    float actv[GSTEPS];
+    auto gate_up = [&]() {
+        float xsum = 0.0f;
+#pragma unroll
+        for (int c = 0; c < Q::CPL; c++) xsum += xs[c];
+#pragma unroll
+        for (int i = 0; i < GSTEPS; i++) {
+            float gv = __builtin_fmaf(nmoe_bf16f(gsc[i]), nmoe_dot16<BITS>(gwv[i], xs), nmoe_bf16f(gbi[i]) * xsum);
+            float uv = __builtin_fmaf(nmoe_bf16f(usc[i]), nmoe_dot16<BITS>(uwv[i], xs), nmoe_bf16f(ubi[i]) * xsum);
+            gv = nmoe_lanes_sum<Q::LPR_G>(gv);
+            uv = nmoe_lanes_sum<Q::LPR_G>(uv);
+            actv[i] = nmoe_silu_dev(gv) * uv;
         }
     };
     uint32_t cand_g = 0;
@@ -994,40 +1046,27 @@ __device__ __forceinline__ void nmoe_fused_body(nmoe_fused_args a, const nmoe_st
         load_expert(cand_g);
         /* keep every weight load above in one burst: no compute hoisted into it */
         __builtin_amdgcn_sched_barrier(0);
-    }
-    float xs[Q::CPL];
+        /* x as floats, and G right away: the first use of the weight
+         * registers stays on this path, so the compiler waits for the gate/up
+         * rows only (where the control wavefronts' path joins this one, it
+         * would wait for every load in flight: their direct LDS loads count
+         * in the same counter) */
 #pragma unroll
-    for (int c = 0; c < XV; c++) {
-        if (NORM) {
-            *(float4 *)(xs + 4 * c) = ((const float4 *)s_h)[nmoe_act_slot<Q::CPL / 4>(4 * (gl * XV + c)) / 4];
-        } else if (XMODE == NMOE_XBF16) {
-            nmoe_unpack_bf16x8(xr[c], xs + 8 * c);
-        } else {
-            xs[4 * c] = __uint_as_float(xr[c].x);
-            xs[4 * c + 1] = __uint_as_float(xr[c].y);
-            xs[4 * c + 2] = __uint_as_float(xr[c].z);
-            xs[4 * c + 3] = __uint_as_float(xr[c].w);
+        for (int c = 0; c < XV; c++) {
+            if (NORM) {
+                *(float4 *)(xs + 4 * c) = ((const float4 *)s_h)[nmoe_act_slot<Q::CPL / 4>(4 * (gl * XV + c)) / 4];
+            } else if (XMODE == NMOE_XBF16) {
+                nmoe_unpack_bf16x8(xr[c], xs + 8 * c);
+            } else {
+                xs[4 * c] = __uint_as_float(xr[c].x);
+                xs[4 * c + 1] = __uint_as_float(xr[c].y);
+                xs[4 * c + 2] = __uint_as_float(xr[c].z);
+                xs[4 * c + 3] = __uint_as_float(xr[c].w);
+            }
         }
-    }
-
-    /* ---- G (workers): gate/up + SwiGLU -> act[g], published once the
-     * control wavefront has confirmed the expert */
-    float actv[GSTEPS];
-    auto gate_up = [&]() {
-        float xsum = 0.0f;
-#pragma unroll
-        for (int c = 0; c < Q::CPL; c++) xsum += xs[c];
-#pragma unroll
-        for (int i = 0; i < GSTEPS; i++) {
-            float gv = __builtin_fmaf(nmoe_bf16f(gsc[i]), nmoe_dot16<BITS>(gwv[i], xs), nmoe_bf16f(gbi[i]) * xsum);
-            float uv = __builtin_fmaf(nmoe_bf16f(usc[i]), nmoe_dot16<BITS>(uwv[i], xs), nmoe_bf16f(ubi[i]) * xsum);
-            gv = nmoe_lanes_sum<Q::LPR_G>(gv);
-            uv = nmoe_lanes_sum<Q::LPR_G>(uv);
-            actv[i] = nmoe_silu_dev(gv) * uv;
-        }
-    };
-    if (!ctrl && active) {
         gate_up();
+    }
+    if (!ctrl && active) {
         if (ROUTE) {
             nmoe_lds_wait_above(&s_confirm, 0u, status, &s_bad, a.spin);
             const uint32_t xg = min(s_gx[g], (uint32_t)(NMOE_EXPERTS - 1));

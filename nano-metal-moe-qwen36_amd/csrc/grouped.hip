@@ -371,7 +371,8 @@ __global__ void __launch_bounds__(256) nmoe_grouped_prep_kernel(const uint32_t *
          * fence, whose L2 writeback would wait for every dirty line of the
          * die (the x planes the other blocks are writing) */
         for (int i = threadIdx.x; i <= NMOE_EXPERTS; i += 256)
-            __hip_atomic_store(&counts[b * (NMOE_EXPERTS + 1) + i], h[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store((nmoe_g32 *)&counts[b * (NMOE_EXPERTS + 1) + i], h[i], __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
         __builtin_amdgcn_s_waitcnt(0x0F70); /* vmcnt(0) */
         __syncthreads();
         if (threadIdx.x == 0) {
@@ -382,7 +383,8 @@ __global__ void __launch_bounds__(256) nmoe_grouped_prep_kernel(const uint32_t *
             while ((int32_t)(nmoe_ld_u32_dev(cnt) - target) < 0) {
                 __builtin_amdgcn_s_sleep(1);
                 if (++spins > spin) {
-                    __hip_atomic_store(sync + NMOE_SYNC_STATUS, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    __hip_atomic_store((nmoe_g32 *)(sync + NMOE_SYNC_STATUS), 1u, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
                     break;
                 }
             }
@@ -1202,7 +1204,7 @@ nmoe_grouped_down_kernel(const uint8_t *pack, const uint16_t *ahi, const uint16_
  * and the host has not read the status yet) makes the combine write NaN:
  * y may rest on a dispatch that never completed. */
 __device__ __forceinline__ bool nmoe_status_set(const uint32_t *status) {
-    return __hip_atomic_load((uint32_t *)status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u;
+    return __hip_atomic_load((nmoe_g32 *)status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u;
 }
 
 /* The same for rows not 16-byte aligned: one row per thread. */

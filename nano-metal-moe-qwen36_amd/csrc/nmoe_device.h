@@ -439,18 +439,27 @@ __device__ __forceinline__ int nmoe_wave_route(const float *lg, int num_experts,
 /* Device-coherent loads/stores of values exchanged between blocks of one
  * launch: agent-scope relaxed atomics (global_load/store ... sc1), so no
  * L2-wide writeback or invalidate is needed; ordering comes from s_waitcnt
- * before the counter update that publishes them. */
+ * before the counter update that publishes them.
+ *
+ * Every such pointer is cast to the global address space first.  Through a
+ * generic pointer the access is a flat instruction, which may reach LDS as
+ * far as the compiler knows: in a kernel that also loads LDS directly from
+ * memory (global_load_lds), it then waits for all of those loads (and with
+ * them every other load in flight) before each exchange access. */
+typedef __attribute__((address_space(1))) uint32_t nmoe_g32;
+typedef __attribute__((address_space(1))) uint64_t nmoe_g64;
+typedef __attribute__((address_space(1))) uint8_t nmoe_gu8;
 __device__ __forceinline__ void nmoe_st_dev(float *p, float v) {
-    __hip_atomic_store((uint32_t *)p, __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store((nmoe_g32 *)p, __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ float nmoe_ld_dev(const float *p) {
-    return __uint_as_float(__hip_atomic_load((uint32_t *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    return __uint_as_float(__hip_atomic_load((nmoe_g32 *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
 }
 __device__ __forceinline__ uint32_t nmoe_ld_u32_dev(uint32_t *p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return __hip_atomic_load((nmoe_g32 *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ uint32_t nmoe_add_u32_dev(uint32_t *p, uint32_t v) {
-    return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return __hip_atomic_fetch_add((nmoe_g32 *)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 /* Values exchanged between the blocks of one launch travel as 64-bit words
@@ -458,10 +467,11 @@ __device__ __forceinline__ uint32_t nmoe_add_u32_dev(uint32_t *p, uint32_t v) {
  * device-coherent access: a consumer polls the data itself until every word
  * carries the current epoch, so no separate counter round trip is needed. */
 __device__ __forceinline__ void nmoe_st_tagged(uint64_t *p, uint32_t epoch, float v) {
-    __hip_atomic_store(p, ((uint64_t)epoch << 32) | __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store((nmoe_g64 *)p, ((uint64_t)epoch << 32) | __float_as_uint(v), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ uint64_t nmoe_ld_tagged(const uint64_t *p) {
-    return __hip_atomic_load((uint64_t *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return __hip_atomic_load((nmoe_g64 *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ bool nmoe_tag_is(uint64_t w, uint32_t epoch) { return (uint32_t)(w >> 32) == epoch; }
 __device__ __forceinline__ float nmoe_tag_val(uint64_t w) { return __uint_as_float((uint32_t)w); }
