@@ -311,7 +311,10 @@ __device__ __forceinline__ bool nmoe_poll2(const uint64_t *const p[N], uint32_t 
  * shared-down rows) the compiler then makes it wait for every load in
  * flight, the expert weight stream included.  The clobbers keep the
  * surrounding LDS accesses in program order; the hardware completes one
- * wavefront's LDS accesses in order. */
+ * wavefront's LDS accesses in order.  The address operand is the LDS
+ * offset: the low 32 bits of a generic pointer into LDS (the shared
+ * aperture's base has none set), as the compiler's own generic-to-LDS
+ * conversion takes it. */
 __device__ __forceinline__ uint32_t nmoe_lds_read_flag(const uint32_t *w) {
     uint32_t v;
     asm volatile("ds_read_b32 %0, %1" : "=v"(v) : "v"((uint32_t)(size_t)w) : "memory");
