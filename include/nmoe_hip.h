@@ -347,7 +347,12 @@ NMOE_HIP_API int nmoe_moe_stack(nmoe_hip_ctx *ctx, int nlayers, const int *layer
  * ntok is at most NMOE_HIP_STATIC_MAX_TOKENS (EINVAL beyond).  Calls share
  * that array: calls that overlap on one GPU race.  idx/w (nullable) receive
  * the routing.  A bounded wait that gives up shows as NaN in out and w
- * (there is no context to hold a status). */
+ * (there is no context to hold a status).  Any call, the first on a device
+ * included, may be made while `stream` is being captured into a HIP graph:
+ * it then only launches kernels on it (the one-time die-placement check,
+ * a launch and a copy back, waits for the first call on a stream that is
+ * not capturing), and every replay of the graph is a new launch with its
+ * own synchronisation epoch, counted on the device. */
 #define NMOE_HIP_STATIC_MAX_TOKENS 16
 #define NMOE_HIP_STATIC_SCRATCH_BYTES 722944u
 NMOE_HIP_API int nmoe_moe_layer_static(const void *layer_pack, int bits, const nmoe_hip_router *router,

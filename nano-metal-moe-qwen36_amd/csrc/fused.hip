@@ -583,9 +583,11 @@ __device__ __forceinline__ void nmoe_fused_body(nmoe_fused_args a, const nmoe_st
              * keeps the last one it uses */
             uint32_t e = a.epoch_arg;
             if (e == 0u) {
+                /* epochs skip 0, the tag of a cleared word: a launch whose
+                 * epochs would reach it after 2^32 - 1 starts again at 1 */
                 e = ep_old + 1u;
-                __hip_atomic_store((nmoe_g32 *)ep, STK ? ep_old + (uint32_t)nl : e, __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT);
+                if (e == 0u || e + (uint32_t)(nl - 1) < e) e = 1u;
+                __hip_atomic_store((nmoe_g32 *)ep, e + (uint32_t)(nl - 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
             s_epoch = e;
             s_bad = 0u;
@@ -1394,20 +1396,24 @@ __global__ void nmoe_xcc_probe_kernel(uint32_t *out) {
  * dispatcher continues its rotation from the previous launch, so c varies
  * between launches).  The blocks of a group (b % 8 equal) then share a die
  * and its L2, which the die-local exchange relies on.  Checked over launches
- * with different rotations (a 1-block launch in between shifts c). */
-extern "C" int nmoe_probe_xcd_placement(uint32_t *d, int *placed) {
+ * with different rotations (a 1-block launch in between shifts c).  Runs on
+ * stream s and waits for that stream only (never for the whole device), so
+ * it can run while another stream is being captured into a graph; it must
+ * not run on a stream that is itself capturing. */
+extern "C" int nmoe_probe_xcd_placement(uint32_t *d, int *placed, hipStream_t s) {
     uint32_t h[NMOE_FUSED_BLOCKS];
     *placed = 0;
     int ok = 1;
     for (int rep = 0; rep < 4 && ok; rep++) {
-        hipLaunchKernelGGL(nmoe_xcc_probe_kernel, dim3(NMOE_FUSED_BLOCKS), dim3(NMOE_FUSED_THREADS), 0, 0, d);
-        if (hipGetLastError() != hipSuccess || hipMemcpy(h, d, sizeof(h), hipMemcpyDeviceToHost) != hipSuccess)
+        hipLaunchKernelGGL(nmoe_xcc_probe_kernel, dim3(NMOE_FUSED_BLOCKS), dim3(NMOE_FUSED_THREADS), 0, s, d);
+        if (hipGetLastError() != hipSuccess || hipMemcpyAsync(h, d, sizeof(h), hipMemcpyDeviceToHost, s) != hipSuccess ||
+            hipStreamSynchronize(s) != hipSuccess)
             return NMOE_HIP_EHIP;
         const uint32_t c = h[0] % NMOE_FUSED_GROUPS;
         for (int b = 0; b < NMOE_FUSED_BLOCKS; b++) ok = ok && h[b] == (uint32_t)(b + c) % NMOE_FUSED_GROUPS;
-        hipLaunchKernelGGL(nmoe_xcc_probe_kernel, dim3(1 + rep), dim3(64), 0, 0, d); /* shift the rotation */
+        hipLaunchKernelGGL(nmoe_xcc_probe_kernel, dim3(1 + rep), dim3(64), 0, s, d); /* shift the rotation */
     }
-    if (hipDeviceSynchronize() != hipSuccess) return NMOE_HIP_EHIP;
+    if (hipStreamSynchronize(s) != hipSuccess) return NMOE_HIP_EHIP;
     *placed = ok;
     return NMOE_HIP_OK;
 }
@@ -1436,7 +1442,7 @@ extern "C" int nmoe_decode_init(nmoe_hip_ctx *ctx) {
     ctx->xch_bytes = NMOE_FUSED_XCH_BYTES_STACK;
     if (hipMalloc((void **)&ctx->xch, ctx->xch_bytes) != hipSuccess) return NMOE_HIP_ENOMEM;
     if (ok) { /* the probe writes into the exchange buffer, cleared afterwards */
-        int r = nmoe_probe_xcd_placement((uint32_t *)ctx->xch, &ctx->xcd_placed);
+        int r = nmoe_probe_xcd_placement((uint32_t *)ctx->xch, &ctx->xcd_placed, ctx->stream);
         if (r != NMOE_HIP_OK) return r;
     }
     ctx->use_xcd_local = ctx->xcd_placed;

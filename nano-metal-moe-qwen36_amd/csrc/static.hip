@@ -15,18 +15,28 @@
  *
  * Layout of scratch (bytes from its start, each part 256-byte aligned):
  *   xch     the fused launch's exchange words (one token per launch)
- *   sync    its status word (set when a bounded wait gives up); the
- *           per-block epoch words are not used: each launch takes its epoch
- *           from a per-device host counter
+ *   sync    its status word (set when a bounded wait gives up) and the
+ *           per-block launch epochs: each launch's blocks count their own
+ *           launches on the device, so every replay of a call captured into
+ *           a graph takes a new epoch, as every eager call does
  *   act     [16][8][512] fp32 SwiGLU activations of the per-token kernels
  *   logits  [16][256] fp32
  *   idx, w  [16][8] routing, used when the caller passes none
- *   probe   [256] u32: the die-placement probe at set-up
+ *   probe   [256] u32: the die-placement probe
  * Calls share their GPU's copy and leave their contents in it; calls that
  * overlap on one GPU (two host threads, or two streams without ordering)
- * race.  Epochs restart from 1 after 2^32 - 1 launches, and the exchange
- * words are cleared then (by a kernel: nothing is allocated), so a word
- * written by an earlier launch never carries the current epoch.
+ * race.  The array starts zeroed (so the first epoch is 1); epochs skip 0
+ * and wrap after 2^32 - 1 launches, so an exchange word that no launch
+ * rewrote for that many launches could be taken as current.
+ *
+ * Set-up needs no stream work except the die-placement probe (a launch and
+ * a copy back, which a stream being captured cannot do).  A call whose
+ * stream is capturing therefore skips the probe and uses the
+ * device-coherent exchange (correct wherever the blocks run); the first
+ * call on a stream that is not capturing runs the probe, and later calls
+ * use the die-local exchange where the probe allows it.  Launches of either
+ * kind may follow each other: a launch accepts only words that carry its
+ * own epoch, which only its own blocks write.
  */
 #include <atomic>
 #include <mutex>
@@ -57,7 +67,7 @@ extern "C" hipError_t nmoe_fused_launch_core(int bits, int route, const void *x,
                                              uint32_t spin, uint32_t epoch, const nmoe_block_ext *blk,
                                              hipStream_t s);
 extern "C" int nmoe_fused_resident(int num_cus);
-extern "C" int nmoe_probe_xcd_placement(uint32_t *d, int *placed);
+extern "C" int nmoe_probe_xcd_placement(uint32_t *d, int *placed, hipStream_t s);
 extern "C" hipError_t nmoe_router_logits_launch(const nmoe_hip_router *router, const void *x, int x_dtype, int ntok,
                                                float *logits, hipStream_t s);
 extern "C" hipError_t nmoe_topk_launch(const float *logits, int ntok, int num_experts, int k, uint32_t *idx, float *w,
@@ -69,20 +79,24 @@ extern "C" hipError_t nmoe_experts_launch(int bits, const uint8_t *pack, const v
 
 /* Per-device state, set up once with the device current. */
 struct nmoe_static_dev {
-    std::atomic<int> ready; /* 1 once set up, -1 if set-up failed */
-    uint8_t *ptr;           /* this device's copy of scratch */
-    int fused;              /* the 256-block fused grid is resident-capable */
-    int xcd_local;          /* blocks dealt round-robin over the 8 dies */
-    std::atomic<uint32_t> epoch;
+    std::atomic<int> ready;  /* 1 once set up, -1 if set-up failed */
+    std::atomic<int> probed; /* 0: placement not probed yet, 1: probed, -1: the probe failed */
+    uint8_t *ptr;            /* this device's copy of scratch */
+    int fused;               /* the 256-block fused grid is resident-capable */
+    std::atomic<int> xcd_local; /* blocks dealt round-robin over the 8 dies (probed) */
 };
 static nmoe_static_dev nmoe_static_devs[NMOE_STATIC_MAX_DEVICES];
 static std::mutex nmoe_static_lock;
 
-__global__ void nmoe_static_clear_kernel(uint64_t *p, uint32_t n) {
-    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) p[i] = 0u;
+/* 1 when work issued to s is being captured into a graph (or the runtime
+ * cannot tell: then the probe is not run either). */
+static int nmoe_static_capturing(hipStream_t s) {
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(s, &st) != hipSuccess) return 1;
+    return st != hipStreamCaptureStatusNone;
 }
 
-static int nmoe_static_setup(int dev, nmoe_static_dev **out) {
+static int nmoe_static_setup(int dev, hipStream_t s, nmoe_static_dev **out) {
     nmoe_static_dev *d = &nmoe_static_devs[dev];
     if (d->ready.load(std::memory_order_acquire) == 0) {
         std::lock_guard<std::mutex> g(nmoe_static_lock);
@@ -96,14 +110,23 @@ static int nmoe_static_setup(int dev, nmoe_static_dev **out) {
             if (rc == NMOE_HIP_OK) {
                 d->ptr = (uint8_t *)p;
                 d->fused = nmoe_fused_resident(cus);
-                d->xcd_local = 0;
-                if (d->fused) rc = nmoe_probe_xcd_placement((uint32_t *)(d->ptr + NMOE_STATIC_PROBE), &d->xcd_local);
             }
-            d->epoch.store(0u, std::memory_order_relaxed);
+            d->xcd_local.store(0, std::memory_order_relaxed);
+            d->probed.store(d->fused ? 0 : 1, std::memory_order_relaxed);
             d->ready.store(rc == NMOE_HIP_OK ? 1 : -1, std::memory_order_release);
         }
     }
     if (d->ready.load(std::memory_order_acquire) != 1) return NMOE_HIP_EHIP;
+    if (d->probed.load(std::memory_order_acquire) == 0 && !nmoe_static_capturing(s)) {
+        std::lock_guard<std::mutex> g(nmoe_static_lock);
+        if (d->probed.load(std::memory_order_relaxed) == 0) {
+            int placed = 0;
+            const int rc = nmoe_probe_xcd_placement((uint32_t *)(d->ptr + NMOE_STATIC_PROBE), &placed, s);
+            d->xcd_local.store(rc == NMOE_HIP_OK ? placed : 0, std::memory_order_relaxed);
+            d->probed.store(rc == NMOE_HIP_OK ? 1 : -1, std::memory_order_release);
+            if (rc != NMOE_HIP_OK) return rc;
+        }
+    }
     *out = d;
     return NMOE_HIP_OK;
 }
@@ -130,24 +153,17 @@ extern "C" int nmoe_moe_layer_static(const void *layer_pack, int bits, const nmo
     if ((idx != NULL && !nmoe_aligned(idx, 4)) || (w != NULL && !nmoe_aligned(w, 4))) return NMOE_HIP_EINVAL;
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= NMOE_STATIC_MAX_DEVICES) return NMOE_HIP_ENODEV;
-    nmoe_static_dev *d = NULL;
-    int rc = nmoe_static_setup(dev, &d);
-    if (rc != NMOE_HIP_OK) return rc;
     hipStream_t s = (hipStream_t)stream;
+    nmoe_static_dev *d = NULL;
+    int rc = nmoe_static_setup(dev, s, &d);
+    if (rc != NMOE_HIP_OK) return rc;
     uint8_t *ptr = d->ptr;
     const uint8_t *pack = (const uint8_t *)layer_pack;
-    if (ntok == 1 && d->fused) {
-        uint32_t epoch = d->epoch.fetch_add(1u, std::memory_order_relaxed) + 1u;
-        if (epoch == 0u) { /* after 2^32 - 1 launches: clear the words, start again at 1 */
-            hipLaunchKernelGGL(nmoe_static_clear_kernel, dim3(64), dim3(256), 0, s, (uint64_t *)(ptr + NMOE_STATIC_XCH),
-                               (uint32_t)(NMOE_FUSED_XCH_BYTES / 8u));
-            if (hipGetLastError() != hipSuccess) return NMOE_HIP_EHIP;
-            epoch = d->epoch.fetch_add(1u, std::memory_order_relaxed) + 1u;
-        }
+    if (ntok == 1 && d->fused) { /* epoch 0: the blocks count their launches on the device */
         const hipError_t e = nmoe_fused_launch_core(
             bits, 1, x, x_dtype, 0.0f, k, router, NULL, NULL, h_mid, shared_out, shared_gate_raw, out, idx, w, NULL, pack,
-            (uint64_t *)(ptr + NMOE_STATIC_XCH), (uint32_t *)(ptr + NMOE_STATIC_SYNC), d->xcd_local, NMOE_SPIN_LIMIT,
-            epoch, NULL, s);
+            (uint64_t *)(ptr + NMOE_STATIC_XCH), (uint32_t *)(ptr + NMOE_STATIC_SYNC),
+            d->xcd_local.load(std::memory_order_relaxed), NMOE_SPIN_LIMIT, 0u, NULL, s);
         return e == hipSuccess ? NMOE_HIP_OK : NMOE_HIP_EHIP;
     }
     /* several tokens: router, top-k and the per-token expert kernels */

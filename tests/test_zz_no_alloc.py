@@ -3,6 +3,10 @@ scratch a fixed device array) against nmoe_moe_layer, through the C ABI:
 two calls in a row, the second with fewer tokens, each compared with the
 context entry point on the same inputs -- routing bit-exact, outputs within
 max-abs 2e-3 / rel-L2 1e-3 (here they are the same kernels, so also equal)."""
+import os
+import subprocess
+import sys
+
 import numpy as np
 import pytest
 
@@ -77,3 +81,20 @@ def test_static_layer_rejects_bad_arguments(nh):
         assert nh.moe_layer_static(pack, 4, r, x, nh.F32, 1, 8, h, out, shared_out=h) == nh.EINVAL
         r_bad = nh.Context.router_bf16(W, num_experts=128)
         assert nh.moe_layer_static(pack, 4, r_bad, x, nh.F32, 1, 8, h, out) == nh.EINVAL
+
+
+@pytest.mark.parametrize("bits,router,k", [(4, "bf16", 8), (2, "q4", 6)])
+def test_static_layer_first_call_under_graph_capture(bits, router, k):
+    """The first call on the device made inside hipStreamBeginCapture (global
+    mode) captures one kernel node and nothing else; four replays with new
+    inputs, an eager call, and two more replays each equal nmoe_moe_layer bit
+    for bit (each replay takes a new epoch on the device, so no replay can
+    accept the previous one's exchange words).  A fresh process, so that the
+    call under capture is the first on the device."""
+    client = os.path.join(os.path.dirname(os.path.abspath(__file__)), "static_capture_client.py")
+    print(f"[no-alloc] capture client q{bits} {router} k={k}", flush=True)
+    r = subprocess.run([sys.executable, "-u", client, str(bits), router, str(k)], capture_output=True, text=True,
+                       timeout=110)
+    print(r.stdout[-4000:], r.stderr[-4000:], flush=True)
+    assert r.returncode == 0, f"capture client exited {r.returncode}"
+    assert "[static-capture] ok" in r.stdout
