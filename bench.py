@@ -9,11 +9,15 @@ fp32 residual.  Steps rotate over 40 synthetic layers resident in HBM
 routers (320 MB), so experts and router rows stream from HBM.  The timed
 steps come after the warm-up's, never on the layers it just read.
 
-The same JSON line carries sub-objects measured in the same run: "c3"
-(128 decode tokens through the 40-layer stack, one persistent launch per
-token), "c5" (the 2048-token prefill on the grouped matrix-core path, with
-its MFMA utilisation) and "stream" (the streaming floor of the step's expert
-bytes, nmoe_hip_read_probe).
+The same JSON line carries sub-objects measured in the same run: "c2" (the
+q2 single-layer step at top-8 and top-6), "c3" (128 decode tokens through
+the 40-layer stack, one persistent launch per token), "c4" (64-token batched
+decode), "c5" and "c5_q2" (the 2048-token prefill on the grouped
+matrix-core path, q4 and q2, with its MFMA utilisation), "block" (the
+model's per-layer MoE half, nmoe_moe_block) and "stream" (the streaming
+floor of the step's expert bytes, nmoe_hip_read_probe).  Each carries a
+cpu_baseline of its own (the per-token configs extrapolated from a token
+subset, labelled so).
 
 A step is one call of the per-layer MoE entry point (nmoe_moe_layer), which
 for one token is a single persistent launch (nmoe_fused_decode_kernel).
@@ -109,18 +113,79 @@ class HipEvents:
             self.rt.hipEventDestroy(e)
 
 
+class HipGraph:
+    """Back-to-back launches captured into one HIP graph (hipStreamBeginCapture
+    .. hipGraphInstantiate, through ctypes on the same HIP runtime), so that
+    a launch period can be measured without the host's per-launch cost."""
+
+    def __init__(self, rt, stream, issue):
+        P = C.c_void_p
+        for n, a in (("hipStreamBeginCapture", [P, C.c_int]), ("hipStreamEndCapture", [P, C.POINTER(P)]),
+                     ("hipGraphInstantiate", [C.POINTER(P), P, P, C.c_char_p, C.c_size_t]),
+                     ("hipGraphLaunch", [P, P]), ("hipGraphExecDestroy", [P]), ("hipGraphDestroy", [P])):
+            getattr(rt, n).restype, getattr(rt, n).argtypes = C.c_int, a
+        self.rt, self.stream = rt, stream
+        self.graph, self.exe = C.c_void_p(), C.c_void_p()
+        assert rt.hipStreamBeginCapture(stream, 1) == 0  # thread-local capture mode
+        rcs = issue()
+        assert rt.hipStreamEndCapture(stream, C.byref(self.graph)) == 0
+        assert not any(rcs), rcs
+        assert rt.hipGraphInstantiate(C.byref(self.exe), self.graph, None, None, 0) == 0
+
+    def launch(self):
+        assert self.rt.hipGraphLaunch(self.exe, self.stream) == 0
+
+    def destroy(self):
+        self.rt.hipGraphExecDestroy(self.exe)
+        self.rt.hipGraphDestroy(self.graph)
+
+
+def check_timed(ctx, rcs):
+    """After a timed region: every call's status (a call its host-side checks
+    rejected launched nothing, so it must not count as a step) and the
+    device status word (a bounded wait that gave up)."""
+    bad = [(i, rc) for i, rc in enumerate(rcs) if rc != 0]
+    if bad:
+        raise SystemExit(f"{len(bad)} timed calls failed, first: call {bad[0][0]} returned {bad[0][1]}: "
+                         f"{ctx.last_error()}")
+    if ctx.device_status() != 0:
+        raise SystemExit(f"device status error: {ctx.last_error()}")
+
+
+KERNEL_SOURCES = ("csrc/fused.hip", "csrc/nmoe_device.h", "csrc/nmoe_exact.h")
+
+
+def kernel_source_digest() -> str:
+    """sha256 over the fused kernel's sources, as the profile summaries record
+    it: a summary measured on other sources does not describe this build."""
+    import hashlib
+    h = hashlib.sha256()
+    for rel in KERNEL_SOURCES:
+        with open(os.path.join(PKG, rel), "rb") as f:
+            h.update(f.read())
+    return h.hexdigest()
+
+
 def profiled_traffic(bits: int, k: int):
     """HBM bytes per launch from the committed rocprofv3 counter summary of
-    this workload (None for a workload without one)."""
+    this workload: (bytes, True) when the summary was measured on the
+    current kernel sources, (None, False) when it was not, (None, None)
+    without a summary."""
     path = os.path.join(ROOT, "profiles", f"fused_decode_q{bits}_k{k}.md")
+    vals = {}
     try:
         with open(path) as f:
             for line in f:
-                if line.startswith("traffic_bytes_per_launch = "):
-                    return int(line.split("=")[1])
+                for key in ("traffic_bytes_per_launch", "kernel_source_sha256"):
+                    if line.startswith(key + " = "):
+                        vals[key] = line.split("=", 1)[1].strip()
     except OSError:
-        pass
-    return None
+        return None, None
+    if "traffic_bytes_per_launch" not in vals:
+        return None, None
+    if vals.get("kernel_source_sha256") != kernel_source_digest():
+        return None, False
+    return int(vals["traffic_bytes_per_launch"]), True
 
 
 def cpu_baseline(bits: int, k: int, seed: int, nsteps: int, nlayers: int = 4) -> dict:
@@ -163,6 +228,77 @@ def cpu_baseline(bits: int, k: int, seed: int, nsteps: int, nlayers: int = 4) ->
                    f"(median repeat), {wall:.1f} s of CPU work on 1 of {os.cpu_count()} host threads; "
                    f"{sec * 1e3:.2f} ms/step, {step_bytes(bits, k) / sec / 1e9:.3f} GB/s algorithmic"),
     }
+
+
+def _cpu_fn(name: str):
+    """The CPU routine `name` from oracle/_ref (the reference's math.m) when
+    it was built, else from the C restatement: (fn, kind)."""
+    from oracle import binding as B
+    ref = B.ref_step()
+    if ref is not None:
+        return getattr(ref, name + "_ref"), "reference"
+    return getattr(B.oracle(), name + "_port"), "port"
+
+
+def cpu_tokens_baseline(bits: int, k: int, seed: int, layer: int, lg: np.ndarray, x: np.ndarray, h: np.ndarray,
+                        ntok_step: int, sample: int = 64, repeats: int = 3) -> dict:
+    """The batched-decode / prefill configs on the CPU: the reference runs a
+    prompt one token at a time (runtime.m:3814-3818), so its per-token time
+    on a fixed subset of the step's tokens (given logits, the same synthetic
+    layer) extrapolates to the whole step."""
+    from oracle import binding as B
+    fn, kind = _cpu_fn("orc_cpu_tokens_bench")
+    n = min(sample, lg.shape[0])
+    lg = np.ascontiguousarray(lg[:n], np.float32)
+    x = np.ascontiguousarray(x[:n], np.float32)
+    h = np.ascontiguousarray(h[:n], np.float32)
+    esz = EXPERT_BYTES[bits]
+    pack = np.zeros(256 * esz, np.uint8)
+    sel = set()
+    for t in range(n):
+        idx, _, m = B.route(lg[t], k)
+        sel.update(int(e) for e in idx[:m])
+    for e in sel:  # only the experts the sample routes to
+        pack[e * esz:(e + 1) * esz] = B.syn_expert(bits, seed, layer, e, 0.02 if bits == 4 else 0.05)
+    out = np.zeros(2048, np.float32)
+    t0 = time.time()
+    sec = fn(pack.ctypes.data, bits, lg.ctypes.data, x.ctypes.data, h.ctypes.data, n, k, repeats, out.ctypes.data)
+    wall = time.time() - t0
+    return {"value": round(1.0 / sec, 3), "unit": "tokens/s", "cores": 1, "kind": kind,
+            "sample": (f"{n} of the step's {ntok_step} tokens (layer {layer}, {len(sel)} experts), {repeats} passes, "
+                       f"median; one token at a time as the reference's prompt loop; {wall:.1f} s of CPU work on 1 "
+                       f"of {os.cpu_count()} host threads; {sec * 1e3:.2f} ms/token, so the {ntok_step}-token step "
+                       f"extrapolates to {ntok_step * sec * 1e3:.0f} ms"),
+            "extrapolated": True}
+
+
+def cpu_stack_baseline(bits: int, k: int, seed: int, nl: int, h0: np.ndarray, npacks: int = 2, ntok: int = 1,
+                       repeats: int = 3) -> dict:
+    """The 40-layer stack on the CPU: x = RMSNorm(h), h += MoE_l(x) for each
+    layer, the layers taking `npacks` distinct synthetic layer packs and
+    routers in turn (the CPU time per layer does not depend on which)."""
+    from oracle import binding as B
+    fn, kind = _cpu_fn("orc_cpu_stack_bench")
+    sigma = 0.02 if bits == 4 else 0.05
+    esz = EXPERT_BYTES[bits]
+    packs = []
+    for l in range(npacks):
+        p = np.empty(256 * esz, np.uint8)
+        for e in range(256):
+            p[e * esz:(e + 1) * esz] = B.syn_expert(bits, seed, l, e, sigma)
+        packs.append(p)
+    routers = [B.syn_bf16(256 * 2048, seed, r, 16, 0.02) for r in range(npacks)]
+    pp = (C.c_void_p * npacks)(*[p.ctypes.data for p in packs])
+    rp = (C.c_void_p * npacks)(*[r.ctypes.data for r in routers])
+    h0 = np.ascontiguousarray(h0[:ntok], np.float32)
+    out = np.zeros(2048, np.float32)
+    t0 = time.time()
+    sec = fn(pp, rp, npacks, nl, bits, h0.ctypes.data, ntok, k, 1e-6, repeats, out.ctypes.data)
+    wall = time.time() - t0
+    return {"value": round(1.0 / sec, 3), "unit": "tokens/s", "cores": 1, "kind": kind,
+            "sample": (f"{repeats}x{ntok} tokens through {nl} layers ({npacks} distinct synthetic q{bits} layers in "
+                       f"turn), median pass; {wall:.1f} s of CPU work on 1 of {os.cpu_count()} host threads; "
+                       f"{sec * 1e3:.1f} ms/token")}
 
 
 MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 (no sparsity)
@@ -231,7 +367,7 @@ def run_c1(pool, args) -> dict:
     nh, ctx, bits, k = pool.nh, pool.ctx, args.bits, args.k
     stream = ctx.stream
     NL, NR = pool.NL, pool.NR
-    OUT, IDX, WT = ctx.alloc(NL * 8192, "c1.out"), ctx.alloc(NL * 32, "c1.idx"), ctx.alloc(NL * 32, "c1.w")
+    OUT, IDX, WT = ctx.alloc(NL * 8192), ctx.alloc(NL * 32), ctx.alloc(NL * 32)
 
     def step(i):
         layer, r = i % NL, i % NR
@@ -244,16 +380,15 @@ def run_c1(pool, args) -> dict:
     ev = HipEvents()
     e0, e1 = ev.create(2)
     ev.record(e0, stream)
-    for i in range(args.steps):
-        step(args.warmup + i)
+    rcs = [step(args.warmup + i) for i in range(args.steps)]
     ev.record(e1, stream)
     ms = ev.ms(e0, e1) / args.steps
     ctx.sync()
-    if ctx.device_status() != 0:
-        raise SystemExit(f"device status error: {ctx.last_error()}")
+    check_timed(ctx, rcs)
     ev.destroy([e0, e1])
     B = step_bytes(bits, k, args.router)
     achieved = B / (ms * 1e-3) / 1e9
+    traffic, current = profiled_traffic(bits, k) if args.router == "bf16" else (None, None)
     return {
         "metric": "routed-MoE tokens/s + achieved HBM GB/s (q4, top-8, batch 1, 1 GPU)",
         "value": round(1e3 / ms, 1),
@@ -280,11 +415,23 @@ def run_c1(pool, args) -> dict:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": profiled_traffic(bits, k) if args.router == "bf16" else None,
+            "traffic": traffic,
+            "traffic_profile_current": current,
             "kernel": f"nmoe_fused_decode_kernel<{bits}, 1, 1> (one launch per step)",
             "kernel_ms": round(ms, 5),
         },
     }
+
+
+def single_step_summary(r: dict, args, cpu_steps: int) -> dict:
+    """A single-layer decode line (run_c1's) as a sub-object, with its own
+    CPU baseline."""
+    out = {key: r[key] for key in ("value", "unit", "ms_per_step", "hbm_gbps", "roofline", "config")}
+    out["metric"] = f"routed-MoE tokens/s (q{args.bits}, top-{args.k}, batch 1, 1 GPU)"
+    if not args.no_cpu:
+        print(f"[bench] q{args.bits} top-{args.k} cpu baseline ...", file=sys.stderr, flush=True)
+        out["cpu_baseline"] = cpu_baseline(args.bits, args.k, args.seed, cpu_steps)
+    return out
 
 
 def run_c3(pool, args, ntok: int = 128) -> dict:
@@ -314,17 +461,20 @@ def run_c3(pool, args, ntok: int = 128) -> dict:
     ev = HipEvents()
     e0, e1 = ev.create(2)
     ev.record(e0, stream)
-    for t in range(ntok):
-        step(t)
+    rcs = [step(t) for t in range(ntok)]
     ev.record(e1, stream)
     ms = ev.ms(e0, e1) / ntok
     ctx.sync()
-    if ctx.device_status() != 0:
-        raise SystemExit(f"device status error: {ctx.last_error()}")
+    check_timed(ctx, rcs)
     ev.destroy([e0, e1])
     B = NL * step_bytes(bits, k, args.router)
     gbs = B / (ms * 1e-3) / 1e9
+    cpu = None
+    if not args.no_cpu and args.router == "bf16":
+        print("[bench] c3 cpu baseline ...", file=sys.stderr, flush=True)
+        cpu = cpu_stack_baseline(bits, k, args.seed, NL, pool.h0)
     return {
+        "cpu_baseline": cpu,
         "metric": f"routed-MoE stack tokens/s (c3: {NL} layers, q{bits}, top-{k}, batch 1, 1 GPU)",
         "value": round(1e3 / ms, 1), "unit": "tokens/s", "tokens": ntok, "ms_per_token": round(ms, 5),
         "us_per_layer": round(ms * 1e3 / NL, 2), "hbm_gbps": round(gbs, 1),
@@ -355,10 +505,14 @@ def run_grouped(pool, args, workload: str, NLg: int = 8) -> dict:
             lg = (logp[None, :] + rng.gumbel(size=(ntok, 256))).astype(np.float32)
         else:
             lg = rng.random((ntok, 256), dtype=np.float32)
+        xb = np.ascontiguousarray(
+            (rng.standard_normal((ntok, 2048)).astype(np.float32).view(np.uint32) >> 16).astype(np.uint16))
+        hf = rng.standard_normal((ntok, 2048)).astype(np.float32)
+        if layer == 0:
+            host0 = (lg, (xb.astype(np.uint32) << 16).view(np.float32), hf)
         logits.append(ctx.to_device(lg))
-        xs.append(ctx.to_device(np.ascontiguousarray(
-            (rng.standard_normal((ntok, 2048)).astype(np.float32).view(np.uint32) >> 16).astype(np.uint16))))
-        hs.append(ctx.to_device(rng.standard_normal((ntok, 2048)).astype(np.float32)))
+        xs.append(ctx.to_device(xb))
+        hs.append(ctx.to_device(hf))
         top = np.argsort(-lg, axis=1, kind="stable")[:, :k]
         touched.append(len(np.unique(top)))
     IDX, WT, OUT = ctx.alloc(ntok * 32), ctx.alloc(ntok * 32), ctx.alloc(ntok * 2048 * 4)
@@ -383,6 +537,10 @@ def run_grouped(pool, args, workload: str, NLg: int = 8) -> dict:
     if ctx.device_status() != 0:
         raise SystemExit(f"device status error: {ctx.last_error()}")
     ev.destroy([e0, e1])
+    cpu = None
+    if not args.no_cpu:
+        print(f"[bench] {workload} q{bits} cpu baseline ...", file=sys.stderr, flush=True)
+        cpu = cpu_tokens_baseline(bits, k, args.seed, 0, *host0, ntok_step=ntok)
     esz = EXPERT_BYTES[bits]
     U = float(np.mean([touched[i % NLg] for i in range(steps)]))
     act_bytes = ntok * (4096 + 8192 + 8192 + 64) + ntok * 256 * 4  # x, h, out, idx/w, logits
@@ -391,6 +549,7 @@ def run_grouped(pool, args, workload: str, NLg: int = 8) -> dict:
     tflops = flops / (ms * 1e-3) / 1e12
     gbs = B / (ms * 1e-3) / 1e9
     return {
+        "cpu_baseline": cpu,
         "metric": f"routed-MoE tokens/s ({workload}: {ntok} tokens, q{bits}, top-{k}, 1 GPU)",
         "value": round(ntok / (ms * 1e-3), 1), "unit": "tokens/s", "steps": steps, "ms_per_step": round(ms, 5),
         "dtype": "bf16 x (exact integer codes) on the matrix cores, fp32 accumulate",
@@ -529,6 +688,87 @@ def run_stream(pool, args) -> dict:
             "frac": round(gbs / HBM_PEAK_GBS, 4), "config": {"workload": "stream", "entry_point": "nmoe_hip_read_probe"}}
 
 
+SWEEP_POOL = 9 << 29  # 4.5 GiB of synthetic words the sweep's reads rotate over
+
+
+def run_probe_sweep(nh, args) -> dict:
+    """The part's streaming ceiling against size and launch shape
+    (nmoe_hip_read_probe_grid), the counterpart of the reference's
+    scripts/matvec_bench.m sweep: each size read back to back from offsets
+    rotating over a 4.5 GiB pool (no launch re-reads what the one before it
+    read, and each size beyond the 256 MB memory-side cache comes from HBM),
+    at 256 .. 2048 blocks and 4 .. 16 loads a thread a round; then the
+    period of a near-empty launch (16 bytes) of 256 .. 1024 blocks.  HIP
+    events around the launches of each point; the median of three repeats."""
+    ctx = nh.Context(0, max_tokens=1)
+    stream = ctx.stream
+    buf = ctx.alloc(SWEEP_POOL, "sweep.pool")
+    ctx.synth_bf16(buf, SWEEP_POOL // 2, args.seed, 0, 21, 1.0)
+    sink = ctx.alloc(8192 * 1024 // 64 * 4, "sweep.sink")
+    ctx.sync()
+    ev = HipEvents()
+    e = ev.create(2)
+
+    def point(nbytes, blocks, threads, loads, launches, graph=False):
+        span = SWEEP_POOL - nbytes
+        stride = (nbytes + 4095) // 4096 * 4096 + 4096
+        offs = [(i * stride) % max(span, 1) // 4096 * 4096 for i in range(3 * launches + 2)]
+        issue = lambda i: ctx.read_probe_grid(buf.ptr + offs[i], nbytes, blocks, threads, loads, sink, stream=stream)
+        for i in range(2):
+            ctx._check(issue(i))
+        graphs = [HipGraph(ev.rt, stream, lambda r=r: [issue(2 + r * launches + i) for i in range(launches)])
+                  for r in range(3)] if graph else None
+        reps = []
+        for r in range(3):
+            ev.record(e[0], stream)
+            if graph:
+                graphs[r].launch()
+                rcs = []
+            else:
+                rcs = [issue(2 + r * launches + i) for i in range(launches)]
+            ev.record(e[1], stream)
+            reps.append(ev.ms(e[0], e[1]) / launches)
+            check_timed(ctx, rcs)
+        for gr in graphs or ():
+            gr.destroy()
+        ms = sorted(reps)[1]
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        row = {"bytes": nbytes, "blocks": blocks, "threads": threads, "loads": loads, "launches": launches,
+               "launch": "graph" if graph else "eager",
+               "us_per_launch": round(ms * 1e3, 3), "gbs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
+        print(f"[sweep] {json.dumps(row)}", file=sys.stderr, flush=True)
+        return row
+
+    rows = []
+    step_bytes_q4 = 8 * EXPERT_BYTES[4]
+    sizes = [(step_bytes_q4, 200), (64 << 20, 60), (256 << 20, 20), (1 << 30, 8), (4 << 30, 3)]
+    for nbytes, launches in sizes:
+        for blocks in (256, 512, 1024, 2048):
+            for loads in (4, 8, 16):
+                rows.append(point(nbytes, blocks, 512, loads, launches))
+    for threads in (256, 1024):  # the step's size at other block sizes
+        for blocks in (256, 512, 1024):
+            rows.append(point(step_bytes_q4, blocks, threads, 8, 200))
+    for blocks in (256, 512, 1024):  # the step's size, the launches in one graph (no host cost per launch)
+        rows.append(point(step_bytes_q4, blocks, 512, 8, 200, graph=True))
+    empty = []
+    for graph in (False, True):
+        for blocks in (256, 512, 1024):
+            for threads in (64, 512, 1024):
+                r = point(16, blocks, threads, 1, 400, graph=graph)
+                empty.append({k: r[k] for k in ("blocks", "threads", "launch", "us_per_launch")})
+    ev.destroy(e)
+    ctx.close()
+    step_rows = [r for r in rows if r["bytes"] == step_bytes_q4 and r["launch"] == "eager"]
+    best_step = min(step_rows, key=lambda r: r["us_per_launch"])
+    big = [r for r in rows if r["bytes"] >= 1 << 30]
+    best_big = max(big, key=lambda r: r["gbs"])
+    return {"metric": "streaming read ceiling against size and launch shape (read probe, 1 GPU)",
+            "unit": "GB/s", "value": best_big["gbs"],
+            "sustained_best": best_big, "step_bytes_best": best_step, "points": rows, "empty_launch": empty,
+            "config": {"workload": "probe-sweep", "pool_bytes": SWEEP_POOL, "entry_point": "nmoe_hip_read_probe_grid"}}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -547,12 +787,12 @@ def main():
                     help="only run 5 device-to-device copies of MIB MiB (counter calibration) and exit")
     ap.add_argument("--router", default="bf16", choices=("bf16", "q4"),
                     help="c1/c3: the benchmark configs' dense bf16 router (default) or the model's q4 router")
-    ap.add_argument("--workload", default="c1", choices=("c1", "c3", "c4", "c5", "stream", "block"),
+    ap.add_argument("--workload", default="c1", choices=("c1", "c3", "c4", "c5", "stream", "block", "probe-sweep"),
                     help="c1: the headline single-layer decode step, with c3, c5, stream and block sub-objects (default); "
                          "c3 / c4 / c5 alone: 40-layer stack of 128 tokens / batched decode of 64 Zipf-routed "
                          "tokens / 2048-token prefill on the grouped matrix-core path; stream: the streaming ceiling "
                          "of the c1 step's expert bytes (nmoe_hip_read_probe); block: the model's per-layer MoE "
-                         "half (nmoe_moe_block)")
+                         "half (nmoe_moe_block); probe-sweep: the read ceiling against size and launch shape")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -571,6 +811,10 @@ def main():
         ctx.sync()
         print(json.dumps({"copy_calib_bytes": n, "copies": 5}), flush=True)
         ctx.close()
+        return
+
+    if args.workload == "probe-sweep":
+        print(json.dumps(run_probe_sweep(nh, args)), flush=True)
         return
 
     grouped = args.workload in ("c4", "c5") or (args.workload == "c1" and not args.no_extra)
@@ -595,6 +839,19 @@ def main():
         if not args.no_cpu:
             print("[bench] cpu baseline ...", file=sys.stderr, flush=True)
             result["cpu_baseline"] = cpu_baseline(args.bits, args.k, args.seed, args.cpu_steps)
+        if not args.no_extra and args.bits == 4:
+            # the q2 configs on their own pool of 40 resident q2 layers (the q4 pool freed first)
+            pool.ctx.close()
+            a2 = argparse.Namespace(**vars(args))
+            a2.bits = 2
+            print("[bench] c2 (q2 top-8, top-6) and c5 q2 sub-benchmarks ...", file=sys.stderr, flush=True)
+            pool = Pool(nh, a2, max_tokens=2048)
+            result["c2"] = {}
+            for k2 in (8, 6):
+                a2.k = k2
+                result["c2"][f"k{k2}"] = single_step_summary(run_c1(pool, a2), a2, cpu_steps=300)
+            a2.k = 8
+            result["c5_q2"] = run_grouped(pool, a2, "c5")
     pool.ctx.close()
     print(json.dumps(result), flush=True)
 

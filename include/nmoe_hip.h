@@ -362,13 +362,24 @@ NMOE_HIP_API int nmoe_moe_layer_static(const void *layer_pack, int bits, const n
 
 /* ---- the streaming ceiling of the decode step (a measurement entry point;
  * no reference counterpart, like the reference's matvec micro-benchmark
- * scripts/matvec_bench.m): reads `bytes` (a multiple of 16, at most 16 MiB)
- * from src once, with the fused step's expert-load pattern (256 blocks, all
- * of a block's 16-byte non-temporal loads in flight before any is used),
- * folding them into sink[2048] words.  Its launch time is the floor of the
- * step's expert phase: the step's expert bytes streamed from a cold start
- * with no routing before and no exchange after. */
+ * scripts/matvec_bench.m): reads `bytes` (a multiple of 16) from src once,
+ * with the fused step's expert-load pattern (256 blocks of 512 threads, 8
+ * non-temporal 16-byte loads a thread in flight before any is used, in
+ * rounds of 16 MiB), folding them into sink[2048] words.  Its launch time
+ * is the floor of the step's expert phase: the step's expert bytes streamed
+ * from a cold start with no routing before and no exchange after. */
 NMOE_HIP_API int nmoe_hip_read_probe(nmoe_hip_ctx *ctx, const void *src, size_t bytes, uint32_t *sink, void *stream);
+
+/* The same read at any launch shape: `blocks` (1..8192) blocks of `threads`
+ * (64..1024, a multiple of 64), `loads` (1, 2, 4, 8 or 16) 16-byte loads a
+ * thread a round.  Block b reads the 16-byte items [b*per, min((b+1)*per, n)),
+ * per = ceil(n / blocks), in rounds of threads*loads items; sink receives
+ * blocks*threads/64 words, word b*(threads/64)+w the XOR of every 32-bit
+ * word wavefront w of block b read.  For the sweep of the part's sustained
+ * read rate against size and shape; a 16-byte read gives the period of a
+ * near-empty launch of the grid. */
+NMOE_HIP_API int nmoe_hip_read_probe_grid(nmoe_hip_ctx *ctx, const void *src, size_t bytes, int blocks, int threads,
+                                          int loads, uint32_t *sink, void *stream);
 
 /* ---- bit-exact dequant probe (kernels.metal:1066-1106 nmoe_dequant_row_q4/q2,
  * math.m:206-234): out[r][c] = q*scale + bias for `rows` rows of `in_dim`. */

@@ -132,6 +132,7 @@ _SIGS = {
     "nmoe_hip_load_model_weights": (_I, [_P, C.c_char_p, C.c_char_p, _I, C.POINTER(_I)]),
     "nmoe_hip_layer_block": (_I, [_P, _I, C.POINTER(MoeBlock)]),
     "nmoe_hip_read_probe": (_I, [_P, _P, C.c_size_t, _P, _P]),
+    "nmoe_hip_read_probe_grid": (_I, [_P, _P, C.c_size_t, _I, _I, _I, _P, _P]),
 }
 
 
@@ -368,6 +369,9 @@ class Context:
 
     def read_probe(self, src, nbytes: int, sink, stream=None) -> int:
         return lib().nmoe_hip_read_probe(self.h, _ptr(src), nbytes, _ptr(sink), stream)
+
+    def read_probe_grid(self, src, nbytes: int, blocks: int, threads: int, loads: int, sink, stream=None) -> int:
+        return lib().nmoe_hip_read_probe_grid(self.h, _ptr(src), nbytes, blocks, threads, loads, _ptr(sink), stream)
 
     def dequant_rows(self, bits: int, packed, scales, biases, rows: int, in_dim: int, out, stream=None) -> int:
         return lib().nmoe_dequant_rows(self.h, bits, _ptr(packed), _ptr(scales), _ptr(biases), rows, in_dim,

@@ -66,6 +66,8 @@ _ORACLE_SIGS = {
     "orc_syn_bf16_normal": (None, [_P, _SZ, _U64, _U32, _U32, _F]),
     "orc_cpu_step_port": (_I, [_P, _I, _P, _P, _I, _P, _P, _P, _P]),
     "orc_cpu_step_bench_port": (C.c_double, [_P, _P, _I, _I, _P, _P, _I, _I, _I, _I, _P]),
+    "orc_cpu_tokens_bench_port": (C.c_double, [_P, _I, _P, _P, _P, _I, _I, _I, _P]),
+    "orc_cpu_stack_bench_port": (C.c_double, [_P, _P, _I, _I, _I, _P, _I, _I, _F, _I, _P]),
 }
 
 _REF_MATH_SIGS = {
@@ -87,6 +89,8 @@ _REF_MATH_SIGS = {
 _REF_STEP_SIGS = {
     "orc_cpu_step_ref": (_I, [_P, _I, _P, _P, _I, _P, _P, _P, _P]),
     "orc_cpu_step_bench_ref": (C.c_double, [_P, _P, _I, _I, _P, _P, _I, _I, _I, _I, _P]),
+    "orc_cpu_tokens_bench_ref": (C.c_double, [_P, _I, _P, _P, _P, _I, _I, _I, _P]),
+    "orc_cpu_stack_bench_ref": (C.c_double, [_P, _P, _I, _I, _I, _P, _I, _I, _F, _I, _P]),
 }
 
 _cache: dict[str, C.CDLL] = {}

@@ -32,6 +32,7 @@
 #define STEP_RENORM(v, n) nmoe_cpu_renormalize((v), (n))
 #define STEP_SWIGLU(g, u, o, n) nmoe_cpu_swiglu((g), (u), (o), (n))
 #define STEP_MATVEC nmoe_cpu_dequant_matvec
+#define STEP_RMSNORM(in, o, n, eps) nmoe_cpu_rms_norm((in), NULL, (o), (n), (eps), 0)
 static size_t step_topk(const float *v, size_t n, size_t k, uint32_t *idx, float *val) {
     size_t tmp[ORC_MAX_K];
     size_t got = nmoe_cpu_topk(v, n, k, tmp, val);
@@ -44,22 +45,18 @@ static size_t step_topk(const float *v, size_t n, size_t k, uint32_t *idx, float
 #define STEP_RENORM(v, n) orc_renormalize((v), (n))
 #define STEP_SWIGLU(g, u, o, n) orc_swiglu((g), (u), (o), (n))
 #define STEP_MATVEC orc_dequant_matvec
+#define STEP_RMSNORM(in, o, n, eps) orc_rms_norm((in), NULL, (o), (n), (eps), 0)
 static size_t step_topk(const float *v, size_t n, size_t k, uint32_t *idx, float *val) {
     return orc_topk(v, n, k, idx, val);
 }
 #define STEP_NAME(x) x##_port
 #endif
 
-/* One decode step for one token.  Returns the number of selected experts. */
-int STEP_NAME(orc_cpu_step)(const uint8_t *layer_pack, int bits, const uint16_t *router_w, const float *x, int k,
-                            const float *h_mid, float *out, uint32_t *idx8, float *w8) {
-    float logits[ORC_EXPERTS];
-    for (int e = 0; e < ORC_EXPERTS; e++) {
-        const uint16_t *row = router_w + (size_t)e * ORC_HIDDEN;
-        float acc = 0.0f;
-        for (int j = 0; j < ORC_HIDDEN; j++) acc += orc_bf16_to_f32(row[j]) * x[j];
-        logits[e] = acc;
-    }
+/* The expert half of one token: routing from its logits (softmax, top-k,
+ * renormalise; `logits` is overwritten with the probabilities), the
+ * selected experts, the combine.  Returns the number of selected experts. */
+static int STEP_NAME(step_experts)(const uint8_t *layer_pack, int bits, float *logits, const float *x, int k,
+                                   const float *h_mid, float *out, uint32_t *idx8, float *w8) {
     STEP_SOFTMAX(logits, ORC_EXPERTS);
     uint32_t idx[ORC_MAX_K] = {0};
     float val[ORC_MAX_K] = {0};
@@ -89,6 +86,29 @@ int STEP_NAME(orc_cpu_step)(const uint8_t *layer_pack, int bits, const uint16_t 
     return (int)n;
 }
 
+/* One decode step for one token.  Returns the number of selected experts. */
+int STEP_NAME(orc_cpu_step)(const uint8_t *layer_pack, int bits, const uint16_t *router_w, const float *x, int k,
+                            const float *h_mid, float *out, uint32_t *idx8, float *w8) {
+    float logits[ORC_EXPERTS];
+    for (int e = 0; e < ORC_EXPERTS; e++) {
+        const uint16_t *row = router_w + (size_t)e * ORC_HIDDEN;
+        float acc = 0.0f;
+        for (int j = 0; j < ORC_HIDDEN; j++) acc += orc_bf16_to_f32(row[j]) * x[j];
+        logits[e] = acc;
+    }
+    return STEP_NAME(step_experts)(layer_pack, bits, logits, x, k, h_mid, out, idx8, w8);
+}
+
+static double STEP_NAME(median)(double *times, int n) {
+    for (int i = 1; i < n; i++)
+        for (int j = i; j > 0 && times[j] < times[j - 1]; j--) {
+            double tmp = times[j];
+            times[j] = times[j - 1];
+            times[j - 1] = tmp;
+        }
+    return times[n / 2];
+}
+
 static double step_now(void) {
     struct timespec ts;
     clock_gettime(CLOCK_MONOTONIC, &ts);
@@ -116,12 +136,61 @@ double STEP_NAME(orc_cpu_step_bench)(const uint8_t *const *layer_packs, const ui
         }
         times[r] = (step_now() - t0) / (double)steps;
     }
-    for (int i = 1; i < repeats; i++)
-        for (int j = i; j > 0 && times[j] < times[j - 1]; j--) {
-            double tmp = times[j];
-            times[j] = times[j - 1];
-            times[j - 1] = tmp;
-        }
     if (out_last != NULL) memcpy(out_last, out, sizeof(out));
-    return times[repeats / 2];
+    return STEP_NAME(median)(times, repeats);
+}
+
+/* Tokens with given router logits (the batched-decode and prefill configs,
+ * whose logits are inputs), one token at a time as the reference's prompt
+ * loop runs them (runtime.m:3814-3818): logits [ntok][256], x and h_mid
+ * [ntok][2048] fp32, one layer pack.  Returns the median seconds per token
+ * over `repeats` passes over all ntok tokens. */
+double STEP_NAME(orc_cpu_tokens_bench)(const uint8_t *layer_pack, int bits, const float *logits, const float *x,
+                                       const float *h_mid, int ntok, int k, int repeats, float *out_last) {
+    double times[64];
+    if (repeats > 64) repeats = 64;
+    float lg[ORC_EXPERTS], out[ORC_HIDDEN];
+    uint32_t idx[ORC_MAX_K];
+    float w[ORC_MAX_K];
+    for (int r = 0; r < repeats; r++) {
+        double t0 = step_now();
+        for (int t = 0; t < ntok; t++) {
+            memcpy(lg, logits + (size_t)t * ORC_EXPERTS, sizeof(lg));
+            STEP_NAME(step_experts)(layer_pack, bits, lg, x + (size_t)t * ORC_HIDDEN, k,
+                                    h_mid + (size_t)t * ORC_HIDDEN, out, idx, w);
+        }
+        times[r] = (step_now() - t0) / (double)ntok;
+    }
+    if (out_last != NULL) memcpy(out_last, out, sizeof(out));
+    return STEP_NAME(median)(times, repeats);
+}
+
+/* The routed-expert stack of one decode token (the layer loop of
+ * runtime.m:3732-3777 restricted to the MoE tails): for l < nl,
+ * x = RMSNorm(h) (math.m:34-65, unit weight), h = h + MoE_l(x), with layer
+ * l taking pack and router l % npacks.  h0 [ntok][2048].  Returns the
+ * median seconds per token over `repeats` passes over all ntok tokens;
+ * h_last receives the last token's final h. */
+double STEP_NAME(orc_cpu_stack_bench)(const uint8_t *const *layer_packs, const uint16_t *const *routers, int npacks,
+                                      int nl, int bits, const float *h0, int ntok, int k, float eps, int repeats,
+                                      float *h_last) {
+    double times[64];
+    if (repeats > 64) repeats = 64;
+    float h[ORC_HIDDEN], x[ORC_HIDDEN], out[ORC_HIDDEN];
+    uint32_t idx[ORC_MAX_K];
+    float w[ORC_MAX_K];
+    for (int r = 0; r < repeats; r++) {
+        double t0 = step_now();
+        for (int t = 0; t < ntok; t++) {
+            memcpy(h, h0 + (size_t)t * ORC_HIDDEN, sizeof(h));
+            for (int l = 0; l < nl; l++) {
+                STEP_RMSNORM(h, x, ORC_HIDDEN, eps);
+                STEP_NAME(orc_cpu_step)(layer_packs[l % npacks], bits, routers[l % npacks], x, k, h, out, idx, w);
+                memcpy(h, out, sizeof(h));
+            }
+        }
+        times[r] = (step_now() - t0) / (double)ntok;
+    }
+    if (h_last != NULL) memcpy(h_last, h, sizeof(h));
+    return STEP_NAME(median)(times, repeats);
 }
