@@ -688,6 +688,96 @@ def run_stream(pool, args) -> dict:
             "frac": round(gbs / HBM_PEAK_GBS, 4), "config": {"workload": "stream", "entry_point": "nmoe_hip_read_probe"}}
 
 
+def run_timeline(pool, args) -> dict:
+    """The phase timeline of a fused workload from the timeline build of the
+    library (libnmoe_hip_tl.so, bench.py --timeline): `--steps` launches (c1,
+    block) or 16 tokens of 40 layers (c3) record the device clock at each
+    block's phase boundaries.  Per launch (per layer for c3), times are taken
+    from the first block's start; each event's figure is the median over the
+    launches of the median over the blocks that record it ("median_us") and
+    of the latest block ("latest_us")."""
+    nh, ctx, k = pool.nh, pool.ctx, args.k
+    stream = ctx.stream
+    wl = args.workload
+    ev = HipEvents()
+    e0, e1 = ev.create(2)
+    if wl == "c3":
+        ctx._check(ctx.set_option(nh.OPT_STACK_LOOP, 1))
+        NL, ntok = pool.NL, 16
+        row = (NL + 1) * 2048 * 4
+        HS = ctx.alloc((ntok + 2) * row)
+        for t in range(ntok + 2):
+            HS.upload(pool.h0[t % pool.NR], offset=t * row)
+        step = lambda t: ctx.moe_stack(list(range(NL)), [pool.rts[(t % 8) * NL + l] for l in range(NL)], k, 1e-6,
+                                       HS.ptr + t * row, stream=stream)
+        warm, timed, per = [ntok, ntok + 1], list(range(ntok)), NL
+    elif wl == "block":
+        NS = max(BLOCK_SLOTS, pool.NL)
+        buf, offs = _block_tensors(np.random.default_rng(args.seed * 7919 + 11), NS)
+        dev = ctx.to_device(buf)
+        slot = buf.shape[1]
+        blks = []
+        for i in range(NS):
+            P = lambda name: [dev.ptr + i * slot + o for o in offs[name]]
+            blks.append(nh.MoeBlock(ctx.router_q4(*P("router")), 1,
+                                    ctx.shared_expert_desc(P("gate"), P("up"), P("down"), P("score")),
+                                    *P("norm"), 1, 1e-6))
+        out, nx = ctx.alloc(8192), ctx.alloc(8192)
+        step = lambda i: ctx.moe_block(i % pool.NL, blks[i % NS], pool.H.ptr + (i % pool.NR) * 8192, k, out, nx,
+                                       stream=stream)
+        warm, timed, per = list(range(args.warmup)), [args.warmup + i for i in range(args.steps)], 1
+    else:
+        OUT = ctx.alloc(pool.NL * 8192)
+        step = lambda i: ctx.moe_layer(i % pool.NL, pool.rts[i % pool.NR], pool.X.ptr + (i % pool.NR) * 4096, nh.BF16,
+                                       1, k, pool.H.ptr + (i % pool.NR) * 8192, OUT.ptr + (i % pool.NL) * 8192,
+                                       stream=stream)
+        warm, timed, per = list(range(args.warmup)), [args.warmup + i for i in range(args.steps)], 1
+    slots = len(timed) * per
+    stamps = ctx.alloc(slots * 256 * 16 * 8)
+    stamps.upload(np.zeros(slots * 256 * 16, np.uint64))
+    for i in warm:
+        ctx._check(step(i))
+    ctx.sync()
+    ctx._check(ctx.set_timeline(stamps, slots))
+    ev.record(e0, stream)
+    rcs = [step(i) for i in timed]
+    ev.record(e1, stream)
+    ms = ev.ms(e0, e1)
+    ctx.sync()
+    check_timed(ctx, rcs)
+    ctx._check(ctx.set_timeline(None, 0))
+    ev.destroy([e0, e1])
+    st = stamps.download(np.uint64, (slots, 256, 16)).astype(np.int64)
+    have = st > 0
+    t0 = np.where(have[:, :, 0], st[:, :, 0], np.iinfo(np.int64).max).min(axis=1)  # each slot's first block start
+    span = int(st[have].max() - t0.min())
+    mhz = span / (ms * 1e3)  # clock ticks per microsecond over the timed region (the region adds the launch gaps)
+    tick_us = 0.01  # s_memrealtime counts at 100 MHz on this part
+    events = {}
+    for i, name in enumerate(nh.TL_EVENTS):
+        med, late = [], []
+        for sl in range(slots):
+            v = st[sl, have[sl, :, i], i]
+            if v.size:
+                rel = (v - t0[sl]) * tick_us
+                med.append(float(np.median(rel)))
+                late.append(float(rel.max()))
+        if med:
+            events[name] = {"median_us": round(float(np.median(med)), 3), "latest_us": round(float(np.median(late)), 3),
+                            "blocks": int(have[:, :, i].sum() // slots)}
+    period = None
+    if per > 1:  # c3: the layer period, start to start within a launch
+        starts = t0.reshape(len(timed), per)
+        period = round(float(np.median(np.diff(starts, axis=1))) * tick_us, 3)
+    for name, e in events.items():
+        print(f"[timeline] {name:16s} median {e['median_us']:7.3f} us  latest {e['latest_us']:7.3f} us  "
+              f"({e['blocks']} blocks)", file=sys.stderr, flush=True)
+    return {"metric": f"phase timeline of the {wl} fused launch (timeline build)", "workload": wl,
+            "launches": len(timed), "slots": slots, "ms_timed_region": round(ms, 4),
+            "us_per_launch": round(ms * 1e3 / len(timed), 3), "layer_period_us": period,
+            "stamp_ticks_per_us_over_region": round(mhz, 2), "events": events}
+
+
 SWEEP_POOL = 9 << 29  # 4.5 GiB of synthetic words the sweep's reads rotate over
 
 
@@ -785,6 +875,9 @@ def main():
     ap.add_argument("--no-extra", action="store_true", help="c1 only: no c3 / c4 / c5 / stream / block sub-objects")
     ap.add_argument("--copy-calib", type=int, default=0, metavar="MIB",
                     help="only run 5 device-to-device copies of MIB MiB (counter calibration) and exit")
+    ap.add_argument("--timeline", action="store_true",
+                    help="c1 / c3 / block: load the phase-timeline build (libnmoe_hip_tl.so) and print the medians of "
+                         "each phase boundary instead of the bench line")
     ap.add_argument("--router", default="bf16", choices=("bf16", "q4"),
                     help="c1/c3: the benchmark configs' dense bf16 router (default) or the model's q4 router")
     ap.add_argument("--workload", default="c1", choices=("c1", "c3", "c4", "c5", "stream", "block", "probe-sweep"),
@@ -800,6 +893,15 @@ def main():
         sys.exit(2)
 
     import nmoe_hip as nh
+
+    if args.timeline:
+        if args.workload not in ("c1", "c3", "block"):
+            raise SystemExit("--timeline: workloads c1, c3 and block (the fused launches)")
+        nh.use_timeline_build()
+        pool = Pool(nh, args, max_tokens=8)
+        print(json.dumps(run_timeline(pool, args)), flush=True)
+        pool.ctx.close()
+        return
 
     if args.copy_calib:
         ctx = nh.Context(0, max_tokens=1)

@@ -132,6 +132,17 @@ NMOE_HIP_API int nmoe_hip_check_device_status(nmoe_hip_ctx *ctx);
 #define NMOE_HIP_OPT_STACK_LOOP 7
 NMOE_HIP_API int nmoe_hip_set_option(nmoe_hip_ctx *ctx, int option, int value);
 
+/* Per-stage timing of the fused launches (the counterpart of the
+ * reference's --timing stage clocks, src/runtime.m:56-78, 2139-2143,
+ * 3843-3894).  Only a library built with the phase timeline
+ * (libnmoe_hip_tl.so, `make timeline`) records it; the product build returns
+ * NMOE_HIP_EINVAL.  stamps: device memory of slots x 256 x 16 uint64; each
+ * fused launch (each layer of a stack launch) takes the next slot in turn,
+ * and block b writes the device's real-time clock at its phase boundaries
+ * to stamps[slot][b][event] (events in nmoe_hip.py's TL_EVENTS; unwritten
+ * stamps keep their contents).  NULL and 0 stop the recording. */
+NMOE_HIP_API int nmoe_hip_set_timeline(nmoe_hip_ctx *ctx, void *stamps, int slots);
+
 /* ---- buffers (backend.h:64-66: register_shared_buffer / register_state_buffer
  *      / lookup_shared_buffer).  The context owns them until destroy. */
 NMOE_HIP_API int nmoe_hip_register_state_buffer(nmoe_hip_ctx *ctx, const char *label, size_t size, void **dev_out);

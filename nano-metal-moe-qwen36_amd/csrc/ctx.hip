@@ -150,6 +150,22 @@ extern "C" int nmoe_hip_set_option(nmoe_hip_ctx *ctx, int option, int value) {
     return nmoe_fail(ctx, NMOE_HIP_EINVAL, "unknown option %d", option);
 }
 
+extern "C" int nmoe_hip_set_timeline(nmoe_hip_ctx *ctx, void *stamps, int slots) {
+    if (ctx == NULL) return NMOE_HIP_EINVAL;
+#if NMOE_TIMELINE
+    if ((stamps == NULL) != (slots == 0) || slots < 0 || (stamps != NULL && !nmoe_aligned(stamps, 8)))
+        return nmoe_fail(ctx, NMOE_HIP_EINVAL, "timeline: a buffer of slots x 256 x 16 stamps, or NULL and 0");
+    ctx->tl = (uint64_t *)stamps;
+    ctx->tl_slots = slots;
+    ctx->tl_next = 0;
+    return NMOE_HIP_OK;
+#else
+    (void)stamps;
+    (void)slots;
+    return nmoe_fail(ctx, NMOE_HIP_EINVAL, "this library was built without the phase timeline (NMOE_TIMELINE)");
+#endif
+}
+
 extern "C" int nmoe_sync_check(nmoe_hip_ctx *ctx, void *stream) {
     if (!ctx->sync_check) return NMOE_HIP_OK;
     NMOE_HIP_TRY(ctx, hipStreamSynchronize(nmoe_stream_of(ctx, stream)));

@@ -168,7 +168,43 @@ struct nmoe_fused_args {
     nmoe_hip_shared_expert sh; /* the shared expert (sh.gate.w == NULL: none) */
     /* XSTACK: x = h_seq row 0, out = rows 1..nl, idx_out / w_out 8 per layer */
     int nl;
+    uint64_t *tl; /* NMOE_TIMELINE builds: this launch's stamps [layers][256][16], or NULL */
 };
+
+/* When each worker asks for its down rows.  0: in the same burst as its
+ * gate/up rows; 1 (default): once it has used its gate/up rows; 2: once
+ * every group's candidate is known, so that the whole chip's gate/up
+ * requests are ahead of the down requests; 3: once it has published its
+ * act, for the confirmed expert.  Measured (q4 top-8, us): C1 step 11.62 /
+ * 11.33 / 11.39 / 11.86, C3 layer 10.85 / 10.26 / 10.83 / 10.78, MoE block
+ * 15.2 / 15.05 / 15.1 / 15.6.  With 1 the gate/up burst is a third smaller,
+ * so it is issued sooner and the gate/up rows (two thirds of the bytes)
+ * arrive sooner, while the down rows still arrive before the act exchange
+ * ends; 3 waits a memory round trip too long. */
+#ifndef NMOE_FUSED_DOWN_AFTER
+#define NMOE_FUSED_DOWN_AFTER 1
+#endif
+
+/* Phase timeline (NMOE_TIMELINE builds): the real-time clock at a phase
+ * boundary, written by the one lane that calls it to this block's stamp of
+ * event ev (the order of nmoe_hip.py's TL_EVENTS) in layer ly's slot.  The
+ * store is a vector store written out, so that nothing moves it. */
+enum {
+    NMOE_TL_START, NMOE_TL_X, NMOE_TL_LOGIT, NMOE_TL_LOGITS_IN, NMOE_TL_CAND0, NMOE_TL_CANDS, NMOE_TL_CONFIRM,
+    NMOE_TL_LOADS, NMOE_TL_GU, NMOE_TL_ACT_PUB, NMOE_TL_ACT_IN, NMOE_TL_DOWN, NMOE_TL_PARTS_IN, NMOE_TL_OUT,
+    NMOE_TL_NEXT, NMOE_TL_END
+};
+static_assert(NMOE_TL_END + 1 == NMOE_TL_EVENTS, "one stamp an event");
+__device__ __forceinline__ void nmoe_tl_stamp(uint64_t *tl, int ly, int ev, float after = 0.0f) {
+    if constexpr (NMOE_TIMELINE) {
+        if (tl != nullptr) {
+            asm volatile("" ::"v"(after)); /* a value the stamp must follow */
+            const uint64_t t = __builtin_amdgcn_s_memrealtime();
+            uint64_t *p = tl + ((size_t)ly * NMOE_FUSED_BLOCKS + blockIdx.x) * NMOE_TL_EVENTS + ev;
+            asm volatile("global_store_dwordx2 %0, %1, off" ::"v"(p), "v"(t) : "memory");
+        }
+    }
+}
 
 /* XSTACK's layer table, passed by value (kernel arguments: no upload, no
  * allocation): per layer the resident pack, the router words (bf16 rows or
@@ -425,6 +461,7 @@ __device__ __forceinline__ void nmoe_fused_body(nmoe_fused_args a, const nmoe_st
     __shared__ double s_rinv; /* XSTACK: the next layer's 1 / rms, or -1 (the block computes it) */
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    if (!STK && tid == 0) nmoe_tl_stamp(a.tl, 0, NMOE_TL_START);
     const bool ctrl = wave >= NMOE_FUSED_CTRL; /* either control wavefront */
     const bool cwave = wave == NMOE_FUSED_CTRL;
     const int g = blockIdx.x % NMOE_FUSED_GROUPS, j = blockIdx.x / NMOE_FUSED_GROUPS;
@@ -537,6 +574,7 @@ __device__ __forceinline__ void nmoe_fused_body(nmoe_fused_args a, const nmoe_st
     auto layer = [&](const int ly) {
     if (STK && wave == NMOE_FUSED_EXACT) __builtin_amdgcn_s_waitcnt(0); /* this layer's router rows are in LDS */
     if (STK) __syncthreads(); /* the layer before is done: h_l, its router rows and the LDS hand-offs are free */
+    if (STK && threadIdx.x == 0) nmoe_tl_stamp(a.tl, ly, NMOE_TL_START);
     /* XSTACK: an opaque copy of the thread index, so that the per-lane
      * addresses derived from it are recomputed in each layer instead of
      * hoisted out of the loop and kept live across all of it (the wave
@@ -626,6 +664,7 @@ __device__ __forceinline__ void nmoe_fused_body(nmoe_fused_args a, const nmoe_st
         }
     }
     __syncthreads();
+    if (tid == 0) nmoe_tl_stamp(a.tl, ly, NMOE_TL_X);
     const uint32_t epoch = s_epoch + (STK ? (uint32_t)ly : 0u);
 
     /* ---- S2 (XBLOCK, every block's candidate wavefront after its routing):
@@ -720,6 +759,7 @@ __device__ __forceinline__ void nmoe_fused_body(nmoe_fused_args a, const nmoe_st
                 nmoe_st_tagged_die(xlgd + 8 * j + wave, epoch, logit);
             else
                 nmoe_st_tagged(xlgd + 8 * j + wave, epoch, logit);
+            if (wave == 0) nmoe_tl_stamp(a.tl, ly, NMOE_TL_LOGIT);
         }
     }
     if (has_sh && wave < 4) {
@@ -771,7 +811,10 @@ __device__ __forceinline__ void nmoe_fused_body(nmoe_fused_args a, const nmoe_st
         if (!STK) {
             const float logit =
                 ROUTE == NMOE_ROUTE_Q4 ? nmoe_router_row_q4(wq, rsr, rbr, xs_r) : nmoe_router_row_bf16(wv, xs_r);
-            if (lane == 0) nmoe_st_tagged(xlg + NMOE_XCH_SP * blockIdx.x, epoch, logit);
+            if (lane == 0) {
+                nmoe_st_tagged(xlg + NMOE_XCH_SP * blockIdx.x, epoch, logit);
+                nmoe_tl_stamp(a.tl, ly, NMOE_TL_LOGIT);
+            }
         }
         if (has_sh && comb) { /* the shared expert's gate score, same x */
             const float v = nmoe_router_row_q4(sq_w, sq_s, sq_b, xs_r);
@@ -793,7 +836,10 @@ __device__ __forceinline__ void nmoe_fused_body(nmoe_fused_args a, const nmoe_st
                 nmoe_poll<4>(pl, epoch, lv, status, &s_bad, a.spin);
 #pragma unroll
             for (int q = 0; q < 4; q++) s_lg[lane + 64 * q] = lv[q];
-            if (lane == 0) __hip_atomic_store(&s_lgok, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+            if (lane == 0) {
+                __hip_atomic_store(&s_lgok, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+                nmoe_tl_stamp(a.tl, ly, NMOE_TL_LOGITS_IN);
+            }
             /* one wave maximum per round: the key's top 24 bits with the
              * complemented entry below make every key distinct and name
              * its entry (logits that agree in those bits go lowest entry
@@ -816,8 +862,10 @@ __device__ __forceinline__ void nmoe_fused_body(nmoe_fused_args a, const nmoe_st
             for (int s = 0; s < NMOE_MAX_K; s++) {
                 if (s < k) {
                     const uint32_t best = nmoe_wave_max_u32(key[0]);
-                    if (lane == 0)
+                    if (lane == 0) {
                         __hip_atomic_store(&s_cand[s], 256u - (best & 255u), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+                        if (s == 0) nmoe_tl_stamp(a.tl, ly, NMOE_TL_CAND0);
+                    }
                     if (key[0] == best) {
                         key[0] = key[1];
                         key[1] = key[2];
@@ -826,7 +874,10 @@ __device__ __forceinline__ void nmoe_fused_body(nmoe_fused_args a, const nmoe_st
                     }
                 }
             }
-            if (lane == 0) __hip_atomic_store(&s_ncand, (uint32_t)k, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+            if (lane == 0) {
+                __hip_atomic_store(&s_ncand, (uint32_t)k, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+                nmoe_tl_stamp(a.tl, ly, NMOE_TL_CANDS);
+            }
         }
         if (has_sh) shared_rows(); /* (an idle group's block: right after its logit) */
     }
@@ -948,7 +999,10 @@ __device__ __forceinline__ void nmoe_fused_body(nmoe_fused_args a, const nmoe_st
                 s_t[lane] = et; /* written out at the end */
             }
         }
-        if (lane == 0) __hip_atomic_store(&s_confirm, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+        if (lane == 0) {
+            __hip_atomic_store(&s_confirm, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+            nmoe_tl_stamp(a.tl, ly, NMOE_TL_CONFIRM);
+        }
         /* XSTACK: the next layer's router row, while this layer streams
          * (the candidate wavefront read this one before the logits came).
          * This wavefront has nothing else to do until the block's next
@@ -995,7 +1049,7 @@ __device__ __forceinline__ void nmoe_fused_body(nmoe_fused_args a, const nmoe_st
      * they complete in order, so the gate/up rows are used while the down
      * rows are still in flight (flat loads would make the first use wait for
      * all of them) */
-    auto load_expert = [&](uint32_t e) {
+    auto load_gate_up = [&](uint32_t e) {
         const nmoe_gu8 *ex = (const nmoe_gu8 *)pack + (size_t)e * L::expert_size;
 #pragma unroll
         for (int i = 0; i < GSTEPS; i++) {
@@ -1009,7 +1063,9 @@ __device__ __forceinline__ void nmoe_fused_body(nmoe_fused_args a, const nmoe_st
             usc[i] = __builtin_nontemporal_load(us);
             ubi[i] = __builtin_nontemporal_load(us + NMOE_INTER * Q::GPR_G);
         }
-        __builtin_amdgcn_sched_barrier(0); /* gate/up rows ahead of the down rows */
+    };
+    auto load_down = [&](uint32_t e) {
+        const nmoe_gu8 *ex = (const nmoe_gu8 *)pack + (size_t)e * L::expert_size;
 #pragma unroll
         for (int i = 0; i < DSTEPS; i++) {
             int row = drow0 + i * RPW_D;
@@ -1018,6 +1074,11 @@ __device__ __forceinline__ void nmoe_fused_body(nmoe_fused_args a, const nmoe_st
             dsc[i] = __builtin_nontemporal_load(ds);
             dbi[i] = __builtin_nontemporal_load(ds + NMOE_HIDDEN * Q::GPR_D);
         }
+    };
+    auto load_expert = [&](uint32_t e) {
+        load_gate_up(e);
+        __builtin_amdgcn_sched_barrier(0); /* gate/up rows ahead of the down rows */
+        load_down(e);
     };
     float xs[Q::CPL];
     /* ---- G (workers): gate/up + SwiGLU -> act[g], published once the
@@ -1048,9 +1109,20 @@ __device__ __forceinline__ void nmoe_fused_body(nmoe_fused_args a, const nmoe_st
         const uint32_t cg = s_cand[g]; /* 0 only if that wait gave up */
         cand_g = cg != 0u ? min(cg - 1u, (uint32_t)(NMOE_EXPERTS - 1)) : 0u;
         __builtin_amdgcn_sched_barrier(0);
-        load_expert(cand_g);
+        if (NMOE_FUSED_DOWN_AFTER == 0 || (NMOE_FUSED_DOWN_AFTER == 2 && !ROUTE) ||
+            (NMOE_FUSED_DOWN_AFTER == 3 && !ROUTE)) {
+            load_expert(cand_g);
+        } else {
+            load_gate_up(cand_g);
+            if (NMOE_FUSED_DOWN_AFTER == 2) { /* the down rows once every group's gate/up rows are asked for */
+                nmoe_lds_wait_above(&s_ncand, (uint32_t)(k - 1), status, &s_bad, a.spin);
+                __builtin_amdgcn_sched_barrier(0);
+                load_down(cand_g);
+            }
+        }
         /* keep every weight load above in one burst: no compute hoisted into it */
         __builtin_amdgcn_sched_barrier(0);
+        if (tid == 0) nmoe_tl_stamp(a.tl, ly, NMOE_TL_LOADS);
         /* x as floats, and G right away: the first use of the weight
          * registers stays on this path, so the compiler waits for the gate/up
          * rows only (where the control wavefronts' path joins this one, it
@@ -1070,14 +1142,24 @@ __device__ __forceinline__ void nmoe_fused_body(nmoe_fused_args a, const nmoe_st
             }
         }
         gate_up();
+        if (tid == 0) nmoe_tl_stamp(a.tl, ly, NMOE_TL_GU, actv[GSTEPS - 1]);
+        if (NMOE_FUSED_DOWN_AFTER == 1) {
+            /* the down rows behind the gate/up rows the whole chip asked for */
+            __builtin_amdgcn_sched_barrier(0);
+            load_down(cand_g);
+        }
     }
     if (!ctrl && active) {
         if (ROUTE) {
             nmoe_lds_wait_above(&s_confirm, 0u, status, &s_bad, a.spin);
             const uint32_t xg = min(s_gx[g], (uint32_t)(NMOE_EXPERTS - 1));
             if (xg != cand_g) { /* probability tie at the boundary: redo with the selected expert */
-                load_expert(xg);
+                if (NMOE_FUSED_DOWN_AFTER == 3)
+                    load_gate_up(xg);
+                else
+                    load_expert(xg);
                 gate_up();
+                cand_g = xg;
             }
         }
         if (ROUTE && nmoe_lds_flag(&s_bad)) /* the routing this act rests on is not the token's */
@@ -1091,6 +1173,11 @@ __device__ __forceinline__ void nmoe_fused_body(nmoe_fused_args a, const nmoe_st
                 else
                     nmoe_st_tagged(xact + NMOE_XCH_ASP * (grow0 + i * RPS), epoch, actv[i]);
             }
+        }
+        if (tid == 0) nmoe_tl_stamp(a.tl, ly, NMOE_TL_ACT_PUB);
+        if (NMOE_FUSED_DOWN_AFTER == 3 && ROUTE) { /* the down rows of the confirmed expert, after its act is out */
+            __builtin_amdgcn_sched_barrier(0);
+            load_down(cand_g);
         }
     }
 
@@ -1115,6 +1202,7 @@ __device__ __forceinline__ void nmoe_fused_body(nmoe_fused_args a, const nmoe_st
         nmoe_poll<APT>(pa, epoch, av, status, &s_bad, a.spin, a.xcd_local != 0);
 #pragma unroll
         for (int q = 0; q < APT; q++) s_act[nmoe_act_slot<Q::CPL / 4>(tid + 64 * NMOE_FUSED_WORKERS * q)] = av[q];
+        if (tid == 0) nmoe_tl_stamp(a.tl, ly, NMOE_TL_ACT_IN);
     }
     __syncthreads();
     if (!ctrl && active) {
@@ -1140,6 +1228,7 @@ __device__ __forceinline__ void nmoe_fused_body(nmoe_fused_args a, const nmoe_st
         }
     }
     __syncthreads();
+    if (tid == 0) nmoe_tl_stamp(a.tl, ly, NMOE_TL_DOWN);
     /* ---- C: group j % K combines rows 64j..64j+63 (out = h_mid + sum_s
      * w_s y_s in slot order); the other groups publish their partials as
      * tagged words and are done.  The combiner polls the K-1 partials of its
@@ -1182,6 +1271,7 @@ __device__ __forceinline__ void nmoe_fused_body(nmoe_fused_args a, const nmoe_st
             const float gsig = shared_term ? nmoe_sigmoid_dev(BLK ? s_sgr[0] : sgr) : 0.0f;
             const uint32_t need = (((1u << k) - 1u) & ~(active ? 1u << g : 0u)) | (has_sh ? 1u << NMOE_MAX_K : 0u);
             const bool expired = nmoe_poll2<NP>(pp, epoch, ys, status, &s_bad, a.spin, need);
+            if (tid == 0) nmoe_tl_stamp(a.tl, ly, NMOE_TL_PARTS_IN);
             const float shv = BLK ? ys[NP - 1] : sh; /* (XBLOCK without a shared expert: unused) */
             /* slot order: slot s is streamed by group sgl[s] */
             float moe = 0.0f;
@@ -1206,6 +1296,7 @@ __device__ __forceinline__ void nmoe_fused_body(nmoe_fused_args a, const nmoe_st
             rv = poisoned || expired ? __builtin_nanf("") : r;
             if (!STK) {
                 a.out[row] = rv;
+                if (tid == 0) nmoe_tl_stamp(a.tl, ly, NMOE_TL_OUT);
             } else {
                 /* every die holds the same rows: one writes them out, each
                  * publishes them to its own 32 blocks */
@@ -1290,6 +1381,7 @@ __device__ __forceinline__ void nmoe_fused_body(nmoe_fused_args a, const nmoe_st
         float xn = (float)((double)rv * (1.0 / (double)rms));
         xn = a.next_w != NULL ? xn * nxw : xn;
         a.next_x[row] = nmoe_lds_flag(&s_bad) ? __builtin_nanf("") : xn; /* a partial that never came */
+        if (lane == 0) nmoe_tl_stamp(a.tl, ly, NMOE_TL_NEXT);
     }
     if (ROUTE && blockIdx.x == 0 && cwave) {
         const int o = STK ? NMOE_MAX_K * ly : 0;
@@ -1309,6 +1401,7 @@ __device__ __forceinline__ void nmoe_fused_body(nmoe_fused_args a, const nmoe_st
         nmoe_poll<4>(ph, epoch, hv, status, &s_bad, a.spin, a.xcd_local != 0);
 #pragma unroll
         for (int q = 0; q < 4; q++) s_hin[(ly + 1) & 1][tid + 512 * q] = hv[q];
+        if (tid == 0) nmoe_tl_stamp(a.tl, ly, NMOE_TL_NEXT);
     }
     if (STK && ly + 1 < nl && cwave) {
         /* ---- H (XSTACK, candidate wavefront): the die's 32 sums of
@@ -1330,6 +1423,7 @@ __device__ __forceinline__ void nmoe_fused_body(nmoe_fused_args a, const nmoe_st
         }
         if (lane == 0) s_rinv = ri;
     }
+    if (threadIdx.x == 0) nmoe_tl_stamp(a.tl, ly, NMOE_TL_END);
     };
     if constexpr (STK) {
         for (int ly = 0; ly < nl; ly++) layer(ly);
@@ -1469,16 +1563,18 @@ static hipError_t nmoe_fused_launch_x(int xmode, const nmoe_fused_args &a, hipSt
  * launch with it may remain).  route != 0: routing computed from `router`
  * (bf16 or q4); else given by idx_in / w_in.  xmode: NMOE_XF32 / NMOE_XBF16
  * / NMOE_XNORM / NMOE_XBLOCK (blk: its norm weights, next-layer norm and
- * shared expert; xch then NMOE_FUSED_XCH_BYTES_BLOCK). */
+ * shared expert; xch then NMOE_FUSED_XCH_BYTES_BLOCK).  tl: the launch's
+ * timeline stamps (NMOE_TIMELINE builds), or NULL. */
 extern "C" hipError_t nmoe_fused_launch_core(int bits, int route, const void *x, int xmode, float eps, int k,
                                              const nmoe_hip_router *router, const uint32_t *idx_in, const float *w_in,
                                              const float *h_mid, const float *shared_out, const float *shared_gate_raw,
                                              float *out, uint32_t *idx_out, float *w_out, float *logits_out,
                                              const uint8_t *pack, uint64_t *xch, uint32_t *sync, int xcd_local,
                                              uint32_t spin, uint32_t epoch, const nmoe_block_ext *blk,
-                                             hipStream_t s) {
+                                             hipStream_t s, uint64_t *tl) {
     nmoe_fused_args a;
     memset(&a, 0, sizeof(a));
+    a.tl = tl;
     if (blk != NULL) {
         a.norm_w = blk->norm_w;
         a.next_w = blk->next_w;
@@ -1522,6 +1618,16 @@ extern "C" hipError_t nmoe_fused_launch_core(int bits, int route, const void *x,
     return e;
 }
 
+/* The next n timeline slots of the context (NMOE_TIMELINE builds; NULL
+ * when no timeline buffer is set). */
+static uint64_t *nmoe_tl_take(nmoe_hip_ctx *ctx, int n) {
+    if (!NMOE_TIMELINE || ctx->tl == NULL || n > ctx->tl_slots) return NULL;
+    if (ctx->tl_next + n > ctx->tl_slots) ctx->tl_next = 0;
+    uint64_t *p = ctx->tl + (size_t)ctx->tl_next * NMOE_FUSED_BLOCKS * NMOE_TL_EVENTS;
+    ctx->tl_next += n;
+    return p;
+}
+
 extern "C" int nmoe_fused_decode(nmoe_hip_ctx *ctx, int bits, int route, const void *x, int xmode, float eps, int k,
                                  const nmoe_hip_router *router, const uint32_t *idx_in, const float *w_in,
                                  const float *h_mid, const float *shared_out, const float *shared_gate_raw, float *out,
@@ -1529,7 +1635,8 @@ extern "C" int nmoe_fused_decode(nmoe_hip_ctx *ctx, int bits, int route, const v
                                  hipStream_t s) {
     const hipError_t e = nmoe_fused_launch_core(bits, route, x, xmode, eps, k, router, idx_in, w_in, h_mid, shared_out,
                                                 shared_gate_raw, out, idx_out, w_out, logits_out, pack, ctx->xch,
-                                                ctx->sync, ctx->use_xcd_local, ctx->spin_limit, 0u, NULL, s);
+                                                ctx->sync, ctx->use_xcd_local, ctx->spin_limit, 0u, NULL, s,
+                                                nmoe_tl_take(ctx, 1));
     if (e != hipSuccess) return nmoe_hip_check(ctx, e, "fused decode launch");
     return NMOE_HIP_OK;
 }
@@ -1542,7 +1649,7 @@ extern "C" int nmoe_fused_block(nmoe_hip_ctx *ctx, int bits, const nmoe_hip_rout
                                 float *w_out, float *logits_out, const uint8_t *pack, hipStream_t s) {
     const hipError_t e = nmoe_fused_launch_core(bits, 1, h_mid, NMOE_XBLOCK, eps, k, router, NULL, NULL, h_mid, NULL, NULL,
                                                 out, idx_out, w_out, logits_out, pack, ctx->xch, ctx->sync,
-                                                ctx->use_xcd_local, ctx->spin_limit, 0u, blk, s);
+                                                ctx->use_xcd_local, ctx->spin_limit, 0u, blk, s, nmoe_tl_take(ctx, 1));
     if (e != hipSuccess) return nmoe_hip_check(ctx, e, "fused block launch");
     return NMOE_HIP_OK;
 }
@@ -1577,6 +1684,7 @@ extern "C" int nmoe_fused_stack(nmoe_hip_ctx *ctx, int bits, int q4r, int nl, co
     a.xcd_local = ctx->use_xcd_local;
     a.spin = ctx->spin_limit;
     a.nl = nl;
+    a.tl = nmoe_tl_take(ctx, nl);
     if (bits == 4) {
         if (q4r)
             hipLaunchKernelGGL((nmoe_fused_stack_kernel<4, NMOE_ROUTE_Q4>), dim3(NMOE_FUSED_BLOCKS), dim3(NMOE_FUSED_THREADS), 0, s, a, t);

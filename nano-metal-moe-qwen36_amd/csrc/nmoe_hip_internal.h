@@ -78,6 +78,15 @@ struct nmoe_buf_entry {
     size_t size;
 };
 
+/* 1 in the phase-timeline build (make timeline -> libnmoe_hip_tl.so): the
+ * fused launches stamp the device's real-time clock at their phase
+ * boundaries into the buffer nmoe_hip_set_timeline names.  0 in the product
+ * build, where the stamps compile to nothing. */
+#ifndef NMOE_TIMELINE
+#define NMOE_TIMELINE 0
+#endif
+#define NMOE_TL_EVENTS 16
+
 struct nmoe_hip_ctx {
     int device;
     int num_cus;
@@ -102,6 +111,10 @@ struct nmoe_hip_ctx {
     uint32_t spin_limit;  /* NMOE_HIP_OPT_SPIN_LIMIT: poll rounds before a bounded wait gives up */
     int sync_check;       /* NMOE_HIP_OPT_SYNC_CHECK */
     int stack_loop;       /* NMOE_HIP_OPT_STACK_LOOP */
+    /* phase timeline (builds with NMOE_TIMELINE only): [tl_slots][256][16]
+     * stamps, one slot a launch (a layer of a stack launch), in turn */
+    uint64_t *tl;
+    int tl_slots, tl_next;
     /* grouped (matrix-core) path for many tokens, sized for max_tokens */
     int grouped_min_tokens; /* NMOE_HIP_OPT_GROUPED_MIN_TOKENS */
     uint32_t *g_counts;     /* [64][257] per-block expert histograms */

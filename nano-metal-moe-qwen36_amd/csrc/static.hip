@@ -65,7 +65,7 @@ extern "C" hipError_t nmoe_fused_launch_core(int bits, int route, const void *x,
                                              float *out, uint32_t *idx_out, float *w_out, float *logits_out,
                                              const uint8_t *pack, uint64_t *xch, uint32_t *sync, int xcd_local,
                                              uint32_t spin, uint32_t epoch, const nmoe_block_ext *blk,
-                                             hipStream_t s);
+                                             hipStream_t s, uint64_t *tl);
 extern "C" int nmoe_fused_resident(int num_cus);
 extern "C" int nmoe_probe_xcd_placement(uint32_t *d, int *placed, hipStream_t s);
 extern "C" hipError_t nmoe_router_logits_launch(const nmoe_hip_router *router, const void *x, int x_dtype, int ntok,
@@ -163,7 +163,7 @@ extern "C" int nmoe_moe_layer_static(const void *layer_pack, int bits, const nmo
         const hipError_t e = nmoe_fused_launch_core(
             bits, 1, x, x_dtype, 0.0f, k, router, NULL, NULL, h_mid, shared_out, shared_gate_raw, out, idx, w, NULL, pack,
             (uint64_t *)(ptr + NMOE_STATIC_XCH), (uint32_t *)(ptr + NMOE_STATIC_SYNC),
-            d->xcd_local.load(std::memory_order_relaxed), NMOE_SPIN_LIMIT, 0u, NULL, s);
+            d->xcd_local.load(std::memory_order_relaxed), NMOE_SPIN_LIMIT, 0u, NULL, s, NULL);
         return e == hipSuccess ? NMOE_HIP_OK : NMOE_HIP_EHIP;
     }
     /* several tokens: router, top-k and the per-token expert kernels */

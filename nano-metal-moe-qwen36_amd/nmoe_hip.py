@@ -20,6 +20,14 @@ import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libnmoe_hip.so")
+# the phase-timeline build of the same sources (make timeline): the fused
+# launches also record their phase boundaries (nmoe_hip_set_timeline)
+TIMELINE_LIB_PATH = os.path.join(HERE, "libnmoe_hip_tl.so")
+# stamp slots of a fused launch's timeline, in the order the stamps are laid
+# out (block b of slot s: stamps[s][b][i] for event TL_EVENTS[i])
+TL_EVENTS = ("start", "x_ready", "logit_published", "logits_in", "candidate_0", "candidates", "confirmed",
+             "loads_issued", "gate_up_done", "act_published", "act_in", "down_done", "partials_in", "out_written",
+             "next_ready", "end")
 
 HIDDEN = 2048
 INTER = 512
@@ -133,6 +141,7 @@ _SIGS = {
     "nmoe_hip_layer_block": (_I, [_P, _I, C.POINTER(MoeBlock)]),
     "nmoe_hip_read_probe": (_I, [_P, _P, C.c_size_t, _P, _P]),
     "nmoe_hip_read_probe_grid": (_I, [_P, _P, C.c_size_t, _I, _I, _I, _P, _P]),
+    "nmoe_hip_set_timeline": (_I, [_P, _P, _I]),
 }
 
 
@@ -143,6 +152,15 @@ def header_symbols() -> list[str]:
     with open(hdr) as f:
         text = f.read()
     return sorted(set(re.findall(r"NMOE_HIP_API\s+[\w\s\*]*?\b(nmoe_\w+)\s*\(", text)))
+
+
+def use_timeline_build():
+    """Loads the phase-timeline build instead of the product build (before
+    the first call into either)."""
+    global LIB_PATH
+    if _lib is not None and LIB_PATH != TIMELINE_LIB_PATH:
+        raise RuntimeError("the product library is already loaded")
+    LIB_PATH = TIMELINE_LIB_PATH
 
 
 def lib() -> C.CDLL:
@@ -369,6 +387,9 @@ class Context:
 
     def read_probe(self, src, nbytes: int, sink, stream=None) -> int:
         return lib().nmoe_hip_read_probe(self.h, _ptr(src), nbytes, _ptr(sink), stream)
+
+    def set_timeline(self, stamps, slots: int) -> int:
+        return lib().nmoe_hip_set_timeline(self.h, _ptr(stamps), slots)
 
     def read_probe_grid(self, src, nbytes: int, blocks: int, threads: int, loads: int, sink, stream=None) -> int:
         return lib().nmoe_hip_read_probe_grid(self.h, _ptr(src), nbytes, blocks, threads, loads, _ptr(sink), stream)
