@@ -615,6 +615,45 @@ __device__ __forceinline__ void nmoe_fused_body(nmoe_fused_args a, const nmoe_st
         s_t[tid] = 0u;
         s_t[NMOE_MAX_K + tid] = 0u;
     }
+    if (NORM) {
+        /* x = h / rms (times the norm weight, XBLOCK) once per block, into
+         * LDS in the workers' swizzled chunk order (as the act): the workers
+         * then hold no raw h and do no double arithmetic of their own */
+        const float *hsrc = STK ? s_hin[ly & 1] : (const float *)a.x;
+        /* XSTACK after layer 0: from the 32 partial sums of squares the
+         * candidate wavefront summed while h was gathered */
+        const double ri_pre = STK && ly > 0 ? s_rinv : -1.0;
+        /* the thread's 8 h values (columns 8 tid ..), loaded once for both
+         * the norm and x */
+        float hv8[8];
+        const double rinv = ri_pre >= 0.0 ? ri_pre : 1.0 / (double)nmoe_block_rms_exact(hsrc, a.eps, s_h, s_dd, s_f, hv8);
+        if (tid < NMOE_HIDDEN / 8) {
+#pragma unroll
+            for (int q = 0; q < 2; q++) {
+                const int c0 = 8 * tid + 4 * q;
+                float4 v;
+                if (ri_pre >= 0.0) {
+                    nmoe_x_cols<XMODE>(hsrc, c0, 4, rinv, &v.x);
+                } else { /* x = h / rms as (float)(h * (1 / rms)), as nmoe_x_cols computes it */
+                    v.x = (float)((double)hv8[4 * q] * rinv);
+                    v.y = (float)((double)hv8[4 * q + 1] * rinv);
+                    v.z = (float)((double)hv8[4 * q + 2] * rinv);
+                    v.w = (float)((double)hv8[4 * q + 3] * rinv);
+                }
+                if constexpr (BLK) {
+                    if (a.norm_w != NULL) { /* math.m:63: (h / rms) * weight */
+                        v.x = v.x * nwv[4 * q];
+                        v.y = v.y * nwv[4 * q + 1];
+                        v.z = v.z * nwv[4 * q + 2];
+                        v.w = v.w * nwv[4 * q + 3];
+                    }
+                }
+                ((float4 *)s_h)[nmoe_act_slot<Q::CPL / 4>(c0) / 4] = v;
+            }
+        }
+    }
+    /* after the norm: thread 0 waits here for the launch epoch it loaded at
+     * the start (a memory round trip), not before its loads of h */
     if (tid == 0) {
         if (ly == 0) {
             /* XSTACK: layer l runs with epoch e + l, and the block's word
@@ -635,33 +674,6 @@ __device__ __forceinline__ void nmoe_fused_body(nmoe_fused_args a, const nmoe_st
         s_ncand = 0u;
         s_confirm = 0u;
         s_lgok = 0u;
-    }
-    if (NORM) {
-        /* x = h / rms (times the norm weight, XBLOCK) once per block, into
-         * LDS in the workers' swizzled chunk order (as the act): the workers
-         * then hold no raw h and do no double arithmetic of their own */
-        const float *hsrc = STK ? s_hin[ly & 1] : (const float *)a.x;
-        /* XSTACK after layer 0: from the 32 partial sums of squares the
-         * candidate wavefront summed while h was gathered */
-        const double ri_pre = STK && ly > 0 ? s_rinv : -1.0;
-        const double rinv = ri_pre >= 0.0 ? ri_pre : 1.0 / (double)nmoe_block_rms_exact(hsrc, a.eps, s_h, s_dd, s_f);
-        if (tid < NMOE_HIDDEN / 8) {
-#pragma unroll
-            for (int q = 0; q < 2; q++) {
-                const int c0 = 8 * tid + 4 * q;
-                float4 v;
-                nmoe_x_cols<XMODE>(hsrc, c0, 4, rinv, &v.x);
-                if constexpr (BLK) {
-                    if (a.norm_w != NULL) { /* math.m:63: (h / rms) * weight */
-                        v.x = v.x * nwv[4 * q];
-                        v.y = v.y * nwv[4 * q + 1];
-                        v.z = v.z * nwv[4 * q + 2];
-                        v.w = v.w * nwv[4 * q + 3];
-                    }
-                }
-                ((float4 *)s_h)[nmoe_act_slot<Q::CPL / 4>(c0) / 4] = v;
-            }
-        }
     }
     __syncthreads();
     if (tid == 0) nmoe_tl_stamp(a.tl, ly, NMOE_TL_X);

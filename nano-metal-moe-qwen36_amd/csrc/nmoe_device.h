@@ -532,8 +532,10 @@ __device__ __forceinline__ double nmoe_sum32_tree(double ps) {
  * a short dependency chain; nmoe_mean_sq_from_sum turns that into math.m's
  * float wherever no rounding midpoint is near, and otherwise (a near-tie,
  * or tiny values) lane 0 replays the x87 running sum in index order.
- * lds_h: 2048 floats of LDS, lds_dd: 8 doubles, lds_f: 1 float. */
-__device__ float nmoe_block_rms_exact(const float *h, float eps, float *lds_h, double *lds_dd, float *lds_f) {
+ * lds_h: 2048 floats of LDS, lds_dd: 8 doubles, lds_f: 1 float.  vals
+ * (nullable) receives the thread's 8 values h[8 tid ..] (0 beyond 2048). */
+__device__ float nmoe_block_rms_exact(const float *h, float eps, float *lds_h, double *lds_dd, float *lds_f,
+                                      float *vals = nullptr) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const float4 *h4 = (const float4 *)h;
     const bool holds = tid < NMOE_HIDDEN / 8;
@@ -543,6 +545,9 @@ __device__ float nmoe_block_rms_exact(const float *h, float eps, float *lds_h, d
         v1 = h4[2 * tid + 1];
     }
     float vv[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+    if (vals != nullptr)
+#pragma unroll
+        for (int i = 0; i < 8; i++) vals[i] = vv[i];
     double q[8];
 #pragma unroll
     for (int i = 0; i < 8; i++) q[i] = (double)vv[i] * (double)vv[i]; /* exact: 48 significant bits */
