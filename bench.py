@@ -488,9 +488,10 @@ def run_c3(pool, args, ntok: int = 128) -> dict:
 
 def run_grouped(pool, args, workload: str, NLg: int = 8) -> dict:
     """C4 (64 tokens, Zipf-skewed logits = ln p_e + Gumbel, p_e ~ rank^-1.1)
-    or C5 (2048 tokens, uniform U(0,1) logits): a step is device top-k on
-    the given logits + the grouped expert path (dispatch, gate/up + SwiGLU
-    and down on the matrix cores, slot-order combine).  Timed steps rotate
+    or C5 (2048 tokens, uniform U(0,1) logits): a step is the routing from
+    the given logits (math.m softmax / top-k / renormalise) + the grouped
+    expert path (dispatch, gate/up + SwiGLU and down on the matrix cores,
+    slot-order combine), by default one nmoe_moe_experts_from_logits call.  Timed steps rotate
     over layers 0 .. NLg-1; the warm-up runs layers NLg .. 2 NLg - 1 first."""
     nh, ctx, bits, k = pool.nh, pool.ctx, args.bits, args.k
     stream = ctx.stream
@@ -519,8 +520,12 @@ def run_grouped(pool, args, workload: str, NLg: int = 8) -> dict:
     ctx.sync()
 
     def step(layer):
-        ctx._check(ctx.topk(logits[layer], ntok, 256, k, IDX, WT, stream=stream))
-        ctx._check(ctx.experts(bits, layer, xs[layer], nh.BF16, ntok, k, IDX, WT, hs[layer], OUT, stream=stream))
+        if args.grouped_entry == "from-logits":
+            ctx._check(ctx.experts_from_logits(layer, logits[layer], xs[layer], nh.BF16, ntok, k, hs[layer], OUT, IDX,
+                                               WT, stream=stream))
+        else:
+            ctx._check(ctx.topk(logits[layer], ntok, 256, k, IDX, WT, stream=stream))
+            ctx._check(ctx.experts(bits, layer, xs[layer], nh.BF16, ntok, k, IDX, WT, hs[layer], OUT, stream=stream))
 
     steps = 100 if workload == "c4" else 30
     for i in range(2 * NLg):
@@ -562,7 +567,9 @@ def run_grouped(pool, args, workload: str, NLg: int = 8) -> dict:
                      "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS if workload == "c5" else gbs / HBM_PEAK_GBS, 4)},
         "config": {"workload": workload, "tokens": ntok, "bits": bits, "k": k, "layers_rotated": NLg,
                    "distinct_experts_per_step": round(U, 1), "bytes_per_step": int(B), "flops_per_step": int(flops),
-                   "entry_point": "nmoe_moe_topk + nmoe_moe_experts_q%d (grouped path)" % bits},
+                   "entry_point": ("nmoe_moe_experts_from_logits (routing in the grouped path's first launch)"
+                                   if args.grouped_entry == "from-logits"
+                                   else "nmoe_moe_topk + nmoe_moe_experts_q%d (grouped path)" % bits)},
     }
 
 
@@ -875,6 +882,9 @@ def main():
     ap.add_argument("--no-extra", action="store_true", help="c1 only: no c3 / c4 / c5 / stream / block sub-objects")
     ap.add_argument("--copy-calib", type=int, default=0, metavar="MIB",
                     help="only run 5 device-to-device copies of MIB MiB (counter calibration) and exit")
+    ap.add_argument("--grouped-entry", default="from-logits", choices=("from-logits", "topk+experts"),
+                    help="c4 / c5: one call routing from the given logits inside the grouped path (default), or "
+                         "nmoe_moe_topk then nmoe_moe_experts")
     ap.add_argument("--timeline", action="store_true",
                     help="c1 / c3 / block: load the phase-timeline build (libnmoe_hip_tl.so) and print the medians of "
                          "each phase boundary instead of the bench line")

@@ -333,6 +333,21 @@ NMOE_HIP_API int nmoe_hip_load_model_weights(nmoe_hip_ctx *ctx, const char *bin_
  * layer's weights are not loaded. */
 NMOE_HIP_API int nmoe_hip_layer_block(const nmoe_hip_ctx *ctx, int layer, nmoe_hip_moe_block *out);
 
+/* ---- routing from given router logits and the routed experts in one call
+ * (runtime.m:1498-1511 routing, then the expert tail of
+ * NMOEPipelinedExpertTail, runtime.m:2908-2999), for callers whose router
+ * logits are already on the device (batched decode, prompt processing: the
+ * reference's prompt loop runs the same per-token step, runtime.m:3814-3818).
+ * logits: fp32 [ntok][256]; idx / w: [ntok][8] receive the routing, bit for
+ * bit nmoe_moe_topk's (math.m softmax / top-k / renormalise); out as
+ * nmoe_moe_experts_q4/q2 on the layer's pack (either width).  From
+ * NMOE_HIP_OPT_GROUPED_MIN_TOKENS tokens on, the routing runs inside the
+ * grouped path's first launch instead of a launch of its own. */
+NMOE_HIP_API int nmoe_moe_experts_from_logits(nmoe_hip_ctx *ctx, int layer, const float *logits, const void *x,
+                                              int x_dtype, int ntok, int k, const float *h_mid,
+                                              const float *shared_out, const float *shared_gate_raw, float *out,
+                                              uint32_t *idx, float *w, void *stream);
+
 /* ---- the routed-expert stack of one decode token (the layer loop of
  * NMOEProcessToken, runtime.m:3732-3777, restricted to the MoE tails):
  * h_seq[l+1] = h_seq[l] + MoE_l(RMSNorm(h_seq[l])) for l < nlayers.

@@ -296,6 +296,52 @@ extern "C" int nmoe_moe_experts_q2(nmoe_hip_ctx *ctx, int layer, const void *x, 
     return rc != NMOE_HIP_OK ? rc : nmoe_sync_check(ctx, stream);
 }
 
+extern "C" int nmoe_grouped_experts_routed(nmoe_hip_ctx *ctx, int bits, const uint8_t *pack, const float *logits,
+                                           const void *x, int x_dtype, int ntok, int k, uint32_t *idx, float *w,
+                                           const float *h_mid, const float *shared_out, const float *shared_gate_raw,
+                                           float *out, hipStream_t s);
+extern "C" hipError_t nmoe_topk_launch(const float *logits, int ntok, int num_experts, int k, uint32_t *idx, float *w,
+                                      float *probs, hipStream_t s);
+extern "C" hipError_t nmoe_router_logits_launch(const nmoe_hip_router *router, const void *x, int x_dtype, int ntok,
+                                               float *logits, hipStream_t s);
+
+/* Routing from the given logits and the routed experts in one call: from
+ * grouped_min_tokens tokens on, the routing runs inside the grouped path's
+ * preparation launch (no launch of its own); below, the top-k launch and
+ * the per-token kernels. */
+static int nmoe_experts_from_logits_run(nmoe_hip_ctx *ctx, int layer, const float *logits, const void *x,
+                                        int x_dtype, int ntok, int k, const float *h_mid, const float *shared_out,
+                                        const float *shared_gate_raw, float *out, uint32_t *idx, float *w,
+                                        hipStream_t s) {
+    const int bits = ctx->packs[layer].bits;
+    const uint8_t *pack = (const uint8_t *)ctx->packs[layer].dev;
+    if (ntok >= ctx->grouped_min_tokens)
+        return nmoe_grouped_experts_routed(ctx, bits, pack, logits, x, x_dtype, ntok, k, idx, w, h_mid, shared_out,
+                                           shared_gate_raw, out, s);
+    NMOE_HIP_TRY(ctx, nmoe_topk_launch(logits, ntok, NMOE_EXPERTS, k, idx, w, NULL, s));
+    return bits == 4 ? nmoe_experts_dispatch<4>(ctx, pack, x, x_dtype, ntok, k, idx, w, h_mid, shared_out,
+                                                shared_gate_raw, out, s)
+                     : nmoe_experts_dispatch<2>(ctx, pack, x, x_dtype, ntok, k, idx, w, h_mid, shared_out,
+                                                shared_gate_raw, out, s);
+}
+
+extern "C" int nmoe_moe_experts_from_logits(nmoe_hip_ctx *ctx, int layer, const float *logits, const void *x,
+                                            int x_dtype, int ntok, int k, const float *h_mid, const float *shared_out,
+                                            const float *shared_gate_raw, float *out, uint32_t *idx, float *w,
+                                            void *stream) {
+    if (ctx == NULL) return NMOE_HIP_EINVAL;
+    if (layer < 0 || layer >= NMOE_HIP_MAX_LAYERS || ctx->packs[layer].dev == NULL)
+        return nmoe_fail(ctx, NMOE_HIP_ENOENT, "layer %d has no resident pack", layer);
+    const uint8_t *pack = NULL;
+    if (logits == NULL || !nmoe_aligned(logits, 4)) return nmoe_fail(ctx, NMOE_HIP_EINVAL, "logits NULL or misaligned");
+    int rc = nmoe_check_experts(ctx, layer, ctx->packs[layer].bits, x, x_dtype, ntok, k, idx, w, h_mid, shared_out,
+                                shared_gate_raw, out, &pack);
+    if (rc != NMOE_HIP_OK) return rc;
+    rc = nmoe_experts_from_logits_run(ctx, layer, logits, x, x_dtype, ntok, k, h_mid, shared_out, shared_gate_raw, out,
+                                      idx, w, nmoe_stream_of(ctx, stream));
+    return rc != NMOE_HIP_OK ? rc : nmoe_sync_check(ctx, stream);
+}
+
 extern "C" int nmoe_moe_layer(nmoe_hip_ctx *ctx, int layer, const nmoe_hip_router *router, const void *x, int x_dtype,
                               int ntok, int k, const float *h_mid, const float *shared_out,
                               const float *shared_gate_raw, float *out, uint32_t *idx, float *w, float *logits,
@@ -321,6 +367,17 @@ extern "C" int nmoe_moe_layer(nmoe_hip_ctx *ctx, int layer, const nmoe_hip_route
     }
     uint32_t *ri = idx != NULL ? idx : ctx->idx;
     float *rw = w != NULL ? w : ctx->w;
+    if (ntok >= ctx->grouped_min_tokens) { /* the router launch, then routing and experts from its logits */
+        const uint8_t *pack = NULL;
+        float *lg = logits != NULL ? logits : ctx->logits;
+        rc = nmoe_check_experts(ctx, layer, ctx->packs[layer].bits, x, x_dtype, ntok, k, ri, rw, h_mid, shared_out,
+                                shared_gate_raw, out, &pack);
+        if (rc != NMOE_HIP_OK) return rc;
+        NMOE_HIP_TRY(ctx, nmoe_router_logits_launch(router, x, x_dtype, ntok, lg, nmoe_stream_of(ctx, stream)));
+        rc = nmoe_experts_from_logits_run(ctx, layer, lg, x, x_dtype, ntok, k, h_mid, shared_out, shared_gate_raw, out,
+                                          ri, rw, nmoe_stream_of(ctx, stream));
+        return rc != NMOE_HIP_OK ? rc : nmoe_sync_check(ctx, stream);
+    }
     rc = nmoe_moe_route(ctx, router, x, x_dtype, ntok, k, ri, rw, logits, stream);
     if (rc != NMOE_HIP_OK) return rc;
     if (ctx->packs[layer].bits == 4)

@@ -146,8 +146,12 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t nmoe_buffer(void *p) {
 
 /* ------------------------------------------------------------ dispatch */
 
+/* The expert of entry q (token q / k, slot q % k).  COH: idx was written by
+ * other blocks of this launch, so it is read with device-coherent loads. */
+template <bool COH>
 __device__ __forceinline__ uint32_t nmoe_entry_expert(const uint32_t *idx, int q, int k) {
-    const uint32_t e = idx[(size_t)(q / k) * NMOE_MAX_K + (q % k)];
+    const uint32_t *p = idx + (size_t)(q / k) * NMOE_MAX_K + (q % k);
+    const uint32_t e = COH ? nmoe_ld_u32_dev((uint32_t *)p) : *p;
     return e < NMOE_EXPERTS ? e : (uint32_t)NMOE_EXPERTS; /* 256: left out */
 }
 
@@ -156,17 +160,19 @@ __device__ __forceinline__ uint32_t nmoe_entry_expert(const uint32_t *idx, int q
 /* This thread's entries of the first NMOE_DISPATCH_PRE chunks of slice b
  * (256 past the slice's end), all loads in flight together; read once for
  * both phases. */
+template <bool COH>
 __device__ __forceinline__ void nmoe_dispatch_entries(const uint32_t *idx, int ntok, int k, int b, int nd,
                                                       uint32_t *ev) {
     const int n = ntok * k, per = (n + nd - 1) / nd, q1 = min(n, (b + 1) * per);
 #pragma unroll
     for (int j = 0; j < NMOE_DISPATCH_PRE; j++) {
         const int q = b * per + 256 * j + (int)threadIdx.x;
-        ev[j] = q < q1 ? nmoe_entry_expert(idx, q, k) : (uint32_t)NMOE_EXPERTS;
+        ev[j] = q < q1 ? nmoe_entry_expert<COH>(idx, q, k) : (uint32_t)NMOE_EXPERTS;
     }
 }
 
 /* D1: h = expert histogram of entry slice b of nd (in LDS). */
+template <bool COH>
 __device__ __forceinline__ void nmoe_dispatch_count(const uint32_t *idx, int ntok, int k, uint32_t *h, int b, int nd,
                                                     const uint32_t *ev) {
     const int tid = threadIdx.x, n = ntok * k;
@@ -178,7 +184,7 @@ __device__ __forceinline__ void nmoe_dispatch_count(const uint32_t *idx, int nto
     for (int j = 0; j < NMOE_DISPATCH_PRE; j++)
         if (b * per + 256 * j + tid < q1) atomicAdd(&h[ev[j]], 1u);
     for (int q = b * per + 256 * NMOE_DISPATCH_PRE + tid; q < q1; q += 256)
-        atomicAdd(&h[nmoe_entry_expert(idx, q, k)], 1u);
+        atomicAdd(&h[nmoe_entry_expert<COH>(idx, q, k)], 1u);
     __syncthreads();
 }
 
@@ -187,6 +193,7 @@ __device__ __forceinline__ void nmoe_dispatch_count(const uint32_t *idx, int nto
  * chunks of 256 entries in order; within a chunk the rank of an entry is
  * its rank among the equal-expert lanes of its wavefront (a 9-bit
  * multi-split by ballots) plus the counts of the earlier wavefronts. */
+template <bool COH>
 __device__ __forceinline__ void nmoe_dispatch_scatter(const uint32_t *idx, int ntok, int k, uint32_t *counts,
                                                       const uint32_t *h, uint32_t *perm, uint32_t *offsets,
                                                       uint4 *rank, int b, int nd, const uint32_t *ev) {
@@ -265,7 +272,7 @@ __device__ __forceinline__ void nmoe_dispatch_scatter(const uint32_t *idx, int n
 #pragma unroll
         for (int jj = 0; jj < NMOE_DISPATCH_PRE; jj++)
             if (j == jj) e = ev[jj];
-        if (j >= NMOE_DISPATCH_PRE && q < q1) e = nmoe_entry_expert(idx, q, k);
+        if (j >= NMOE_DISPATCH_PRE && q < q1) e = nmoe_entry_expert<COH>(idx, q, k);
         uint64_t peers = ~0ull;
 #pragma unroll
         for (int bit = 0; bit < 9; bit++) {
@@ -343,28 +350,98 @@ __device__ __forceinline__ void nmoe_grouped_xprep(const XT *x, uint16_t *xhi, u
     }
 }
 
+static __constant__ uint64_t nmoe_grouped_exp2_tab[32] = NMOE_EXP2_TAB32;
+
+/* Bounded wait until *cnt reaches target (thread 0); an expired wait sets
+ * the status word. */
+__device__ __forceinline__ void nmoe_wait_count(uint32_t *cnt, uint32_t target, uint32_t *sync, uint32_t spin) {
+    uint32_t spins = 0;
+    while ((int32_t)(nmoe_ld_u32_dev(cnt) - target) < 0) {
+        __builtin_amdgcn_s_sleep(1);
+        if (++spins > spin) {
+            __hip_atomic_store((nmoe_g32 *)(sync + NMOE_SYNC_STATUS), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            break;
+        }
+    }
+}
+
 /* One launch for the grouped path's preparation: blocks 0 .. nd-1 run the
  * dispatch (D1, then D2 once every slice's histogram is in), the blocks
  * after them prepare one token's x each (none when x is NULL).  With more
  * than one dispatch block, the nd blocks (the grid's first, so resident
  * together) meet at a counter in the sync words that grows by exactly 64
  * per launch (64 / nd from each block; bounded wait, an expired wait sets
- * the status word); a single block keeps its histogram in LDS. */
-template <int BITS, typename XT>
+ * the status word); a single block keeps its histogram in LDS.
+ *
+ * ROUTED: the routing is computed in the same launch from the token's
+ * logits (math.m's softmax / top-k / renormalise, bit for bit, as
+ * nmoe_moe_topk) by the nr = ceil(ntok / 4) blocks after the dispatch
+ * blocks, one token a wavefront (so they are resident in the launch's
+ * first round with the dispatch blocks that wait for them); the x blocks
+ * come after them.  A wavefront writes idx / w of its token with
+ * device-coherent stores and, once they are complete, adds the token's
+ * entries to the ROUTED word of each dispatch slice they fall in (a slice's
+ * word counts only its own entries: one word for all tokens would take
+ * thousands of atomic adds in a row); dispatch block b waits (bounded)
+ * until its slice is complete, clears its word for the next launch on the
+ * stream, and reads idx with device-coherent loads. */
+template <int BITS, typename XT, bool ROUTED>
 __global__ void __launch_bounds__(256) nmoe_grouped_prep_kernel(const uint32_t *idx, int ntok, int k, int nd,
                                                                 uint32_t *counts, uint32_t *perm, uint32_t *offsets,
                                                                 uint4 *rank, uint32_t *sync, uint32_t spin,
                                                                 const XT *x, uint16_t *xhi, uint16_t *xlo,
-                                                                uint16_t *xs3) {
+                                                                uint16_t *xs3, const float *logits, uint32_t *idx_out,
+                                                                float *w_out) {
     const int b = blockIdx.x;
-    if (b >= nd) {
-        nmoe_grouped_xprep<BITS, XT>(x, xhi, xlo, xs3, b - nd);
+    const int nr = ROUTED ? (ntok + 3) / 4 : 0; /* routing blocks */
+    const int n = ntok * k, per = (n + nd - 1) / nd; /* dispatch slices */
+    if (ROUTED && b >= nd && b < nd + nr) {
+        __shared__ float s_sm[4][NMOE_EXPERTS];
+        const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, t = 4 * (b - nd) + wave;
+        if (t < ntok) {
+            uint32_t si[NMOE_MAX_K];
+            float sw[NMOE_MAX_K];
+            nmoe_wave_route(logits + (size_t)t * NMOE_EXPERTS, NMOE_EXPERTS, k, s_sm[wave], nmoe_grouped_exp2_tab, si, sw,
+                            NULL);
+            if (lane < NMOE_MAX_K) {
+                uint32_t vi = 0;
+                float vw = 0.0f;
+#pragma unroll
+                for (int q = 0; q < NMOE_MAX_K; q++)
+                    if (q == lane) {
+                        vi = si[q];
+                        vw = sw[q];
+                    }
+                __hip_atomic_store((nmoe_g32 *)&idx_out[(size_t)t * NMOE_MAX_K + lane], vi, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store((nmoe_g32 *)&w_out[(size_t)t * NMOE_MAX_K + lane], __float_as_uint(vw),
+                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+            __builtin_amdgcn_s_waitcnt(0x0F70); /* vmcnt(0): the stores are complete */
+            if (lane == 0) {
+                const int q0 = t * k, q1 = q0 + k; /* the token's entries, in one or two slices */
+                for (int sb = q0 / per; sb <= (q1 - 1) / per && sb < nd; sb++)
+                    nmoe_add_u32_dev(sync + NMOE_SYNC_ROUTED(sb), (uint32_t)(min(q1, (sb + 1) * per) - max(q0, sb * per)));
+            }
+        }
         return;
     }
+    if (b >= nd) {
+        if (x != NULL) nmoe_grouped_xprep<BITS, XT>(x, xhi, xlo, xs3, b - nd - nr);
+        return;
+    }
+    if (ROUTED) { /* this slice's entries routed: then its word starts from 0 for the next launch */
+        if (threadIdx.x == 0) {
+            uint32_t *cnt = sync + NMOE_SYNC_ROUTED(b);
+            nmoe_wait_count(cnt, (uint32_t)max(0, min(n, (b + 1) * per) - b * per), sync, spin);
+            __hip_atomic_store((nmoe_g32 *)cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        __syncthreads();
+    }
     uint32_t ev[NMOE_DISPATCH_PRE];
-    nmoe_dispatch_entries(idx, ntok, k, b, nd, ev);
+    nmoe_dispatch_entries<ROUTED>(idx, ntok, k, b, nd, ev);
     __shared__ uint32_t h[NMOE_EXPERTS + 1];
-    nmoe_dispatch_count(idx, ntok, k, h, b, nd, ev);
+    nmoe_dispatch_count<ROUTED>(idx, ntok, k, h, b, nd, ev);
     if (nd > 1) {
         /* publish the histogram with device-coherent stores, completed
          * (vmcnt 0) before the arrival is counted: no agent-scope release
@@ -379,19 +456,11 @@ __global__ void __launch_bounds__(256) nmoe_grouped_prep_kernel(const uint32_t *
             uint32_t *cnt = sync + NMOE_SYNC_DISPATCH;
             const uint32_t old = nmoe_add_u32_dev(cnt, (uint32_t)(NMOE_DISPATCH_MAX / nd));
             const uint32_t target = (old / NMOE_DISPATCH_MAX + 1u) * NMOE_DISPATCH_MAX;
-            uint32_t spins = 0;
-            while ((int32_t)(nmoe_ld_u32_dev(cnt) - target) < 0) {
-                __builtin_amdgcn_s_sleep(1);
-                if (++spins > spin) {
-                    __hip_atomic_store((nmoe_g32 *)(sync + NMOE_SYNC_STATUS), 1u, __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_AGENT);
-                    break;
-                }
-            }
+            nmoe_wait_count(cnt, target, sync, spin);
         }
         __syncthreads(); /* (the histograms are then read with device-coherent loads) */
     }
-    nmoe_dispatch_scatter(idx, ntok, k, counts, h, perm, offsets, rank, b, nd, ev);
+    nmoe_dispatch_scatter<ROUTED>(idx, ntok, k, counts, h, perm, offsets, rank, b, nd, ev);
 }
 
 /* ------------------------------------------------------------ stage ring */
@@ -1297,30 +1366,41 @@ extern "C" void nmoe_grouped_free(nmoe_hip_ctx *ctx) {
 extern "C" int nmoe_grouped_dispatch(nmoe_hip_ctx *ctx, const uint32_t *idx, int ntok, int k, uint32_t *perm,
                                      uint32_t *offsets, hipStream_t s) {
     const int nd = nmoe_dispatch_blocks(ntok * k);
-    hipLaunchKernelGGL((nmoe_grouped_prep_kernel<4, uint16_t>), dim3(nd), dim3(256), 0, s, idx, ntok, k, nd,
+    hipLaunchKernelGGL((nmoe_grouped_prep_kernel<4, uint16_t, false>), dim3(nd), dim3(256), 0, s, idx, ntok, k, nd,
                        ctx->g_counts, perm, offsets, (uint4 *)ctx->g_rank, ctx->sync, ctx->spin_limit,
-                       (const uint16_t *)NULL, (uint16_t *)NULL, (uint16_t *)NULL, (uint16_t *)NULL);
+                       (const uint16_t *)NULL, (uint16_t *)NULL, (uint16_t *)NULL, (uint16_t *)NULL,
+                       (const float *)NULL, (uint32_t *)NULL, (float *)NULL);
     const hipError_t e = hipGetLastError();
     return e == hipSuccess ? NMOE_HIP_OK : nmoe_hip_check(ctx, e, "dispatch launch");
 }
 
+/* logits != NULL: the routing from those logits in the preparation launch
+ * (idx / w are then its outputs, [ntok][8]); else idx / w are given. */
 template <int BITS>
 static int nmoe_grouped_run(nmoe_hip_ctx *ctx, const uint8_t *pack, const void *x, int x_dtype, int ntok, int k,
                             const uint32_t *idx, const float *w, const float *h_mid, const float *shared_out,
-                            const float *shared_gate_raw, float *out, hipStream_t s) {
+                            const float *shared_gate_raw, float *out, hipStream_t s, const float *logits = NULL) {
     const bool bf = x_dtype == NMOE_HIP_BF16;
     const int nd = nmoe_dispatch_blocks(ntok * k);
-    const dim3 gprep(nd + ntok);
-    if (bf)
-        hipLaunchKernelGGL((nmoe_grouped_prep_kernel<BITS, uint16_t>), gprep, dim3(256), 0, s, idx, ntok, k, nd,
-                           ctx->g_counts, ctx->g_perm, ctx->g_offsets, (uint4 *)ctx->g_rank, ctx->sync,
-                           ctx->spin_limit, (const uint16_t *)x, ctx->g_xhi,
-                           (uint16_t *)NULL, ctx->g_xs);
-    else
-        hipLaunchKernelGGL((nmoe_grouped_prep_kernel<BITS, float>), gprep, dim3(256), 0, s, idx, ntok, k, nd,
-                           ctx->g_counts, ctx->g_perm, ctx->g_offsets, (uint4 *)ctx->g_rank, ctx->sync,
-                           ctx->spin_limit, (const float *)x, ctx->g_xhi,
-                           ctx->g_xlo, ctx->g_xs);
+    const dim3 gprep(nd + (logits != NULL ? (ntok + 3) / 4 : 0) + ntok);
+    uint32_t *ri = (uint32_t *)idx;
+    float *rw = (float *)w;
+#define NMOE_PREP(XT, R, XLO)                                                                                         \
+    hipLaunchKernelGGL((nmoe_grouped_prep_kernel<BITS, XT, R>), gprep, dim3(256), 0, s, idx, ntok, k, nd, ctx->g_counts, \
+                       ctx->g_perm, ctx->g_offsets, (uint4 *)ctx->g_rank, ctx->sync, ctx->spin_limit, (const XT *)x,  \
+                       ctx->g_xhi, XLO, ctx->g_xs, logits, ri, rw)
+    if (logits != NULL) {
+        if (bf)
+            NMOE_PREP(uint16_t, true, (uint16_t *)NULL);
+        else
+            NMOE_PREP(float, true, ctx->g_xlo);
+    } else {
+        if (bf)
+            NMOE_PREP(uint16_t, false, (uint16_t *)NULL);
+        else
+            NMOE_PREP(float, false, ctx->g_xlo);
+    }
+#undef NMOE_PREP
     constexpr int NW = NMOE_GROUPED_NW;
     const dim3 blk(64 * NW);
     /* two pass lanes once an expert averages more than half a pass: the
@@ -1364,4 +1444,17 @@ extern "C" int nmoe_grouped_experts(nmoe_hip_ctx *ctx, int bits, const uint8_t *
         return nmoe_grouped_run<4>(ctx, pack, x, x_dtype, ntok, k, idx, w, h_mid, shared_out, shared_gate_raw, out,
                                    s);
     return nmoe_grouped_run<2>(ctx, pack, x, x_dtype, ntok, k, idx, w, h_mid, shared_out, shared_gate_raw, out, s);
+}
+
+/* The routing from given logits ([ntok][256]) in the preparation launch,
+ * then the grouped experts: idx / w ([ntok][8]) receive the routing. */
+extern "C" int nmoe_grouped_experts_routed(nmoe_hip_ctx *ctx, int bits, const uint8_t *pack, const float *logits,
+                                           const void *x, int x_dtype, int ntok, int k, uint32_t *idx, float *w,
+                                           const float *h_mid, const float *shared_out, const float *shared_gate_raw,
+                                           float *out, hipStream_t s) {
+    if (bits == 4)
+        return nmoe_grouped_run<4>(ctx, pack, x, x_dtype, ntok, k, idx, w, h_mid, shared_out, shared_gate_raw, out, s,
+                                   logits);
+    return nmoe_grouped_run<2>(ctx, pack, x, x_dtype, ntok, k, idx, w, h_mid, shared_out, shared_gate_raw, out, s,
+                               logits);
 }

@@ -49,6 +49,7 @@ struct nmoe_layout<2> {
 #define NMOE_SYNC_WORDS 8192   /* status + per-block launch epochs of the fused kernel */
 #define NMOE_SYNC_EPOCH(b) (64 + 16 * (b))     /* per-block launch epochs, 64 bytes apart */
 #define NMOE_SYNC_DISPATCH 4352                /* arrival counter of the dispatch blocks */
+#define NMOE_SYNC_ROUTED(b) (4368 + 16 * (b))  /* entries of dispatch slice b routed so far (b < 64), 64 B apart */
 #define NMOE_SYNC_BLOCKS 256
 /* The fused launch's exchange words (tagged logits, act and partial y),
  * and with the whole-block form's shared activations and next-norm sums. */

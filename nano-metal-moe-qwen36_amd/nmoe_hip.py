@@ -142,6 +142,7 @@ _SIGS = {
     "nmoe_hip_read_probe": (_I, [_P, _P, C.c_size_t, _P, _P]),
     "nmoe_hip_read_probe_grid": (_I, [_P, _P, C.c_size_t, _I, _I, _I, _P, _P]),
     "nmoe_hip_set_timeline": (_I, [_P, _P, _I]),
+    "nmoe_moe_experts_from_logits": (_I, [_P, _I, _P, _P, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P]),
 }
 
 
@@ -387,6 +388,12 @@ class Context:
 
     def read_probe(self, src, nbytes: int, sink, stream=None) -> int:
         return lib().nmoe_hip_read_probe(self.h, _ptr(src), nbytes, _ptr(sink), stream)
+
+    def experts_from_logits(self, layer: int, logits, x, x_dtype: int, ntok: int, k: int, h_mid, out, idx, w,
+                            shared_out=None, shared_gate_raw=None, stream=None) -> int:
+        return lib().nmoe_moe_experts_from_logits(self.h, layer, _ptr(logits), _ptr(x), x_dtype, ntok, k, _ptr(h_mid),
+                                                  _ptr(shared_out), _ptr(shared_gate_raw), _ptr(out), _ptr(idx),
+                                                  _ptr(w), stream)
 
     def set_timeline(self, stamps, slots: int) -> int:
         return lib().nmoe_hip_set_timeline(self.h, _ptr(stamps), slots)

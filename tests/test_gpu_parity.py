@@ -229,10 +229,13 @@ def test_layer_matches_math_m_golden(ctx, nh, golden, name, bits, k):
     assert ctx.device_status() == nh.OK
 
 
-@pytest.mark.parametrize("bits", [4, 2])
-def test_layer_multi_token_against_oracle(ctx, nh, bits):
-    rng = np.random.default_rng(7 + bits)
-    seed, layer, ntok, k = 11, 30 + bits, 6, 8
+@pytest.mark.parametrize("bits,ntok", [(4, 6), (2, 6), (4, 24), (2, 24)])
+def test_layer_multi_token_against_oracle(ctx, nh, bits, ntok):
+    """Several tokens through nmoe_moe_layer: 6 tokens take the per-token
+    kernels, 24 the router launch and then the routing inside the grouped
+    path's first launch."""
+    rng = np.random.default_rng(7 + bits + ntok)
+    seed, layer, k = 11, 30 + bits, 8
     ctx.synth_layer(layer, bits, seed, SIGMA[bits])
     W = B.syn_bf16(256 * 2048, seed, layer, 16, 0.02).reshape(256, 2048)
     xb = B.f32_to_bf16(rng.standard_normal((ntok, 2048)).astype(np.float32))
@@ -686,6 +689,67 @@ def test_prefill_2048_sampled(big, nh, bits):
     want = B.moe_experts(pack, bits, x[sample], k, idx[sample], w[sample], h[sample])
     assert big.device_status() == nh.OK
     assert_close(got, want, what=f"prefill q{bits}")
+
+
+@pytest.mark.parametrize("bits,ntok,k,xkind,lkind", [
+    (4, 64, 8, "bf16", "zipf"),      # C4's shape: one dispatch block
+    (2, 2048, 8, "bf16", "uniform"),  # C5's shape: 64 dispatch blocks
+    (4, 300, 6, "f32", "zipf"),       # 8 dispatch blocks, k = 6
+    (2, 8, 1, "f32", "uniform"),      # the grouped threshold, k = 1
+    (4, 5, 8, "bf16", "uniform"),     # below it: the top-k launch and the per-token kernels
+])
+def test_experts_from_logits_equals_topk_then_experts(big, nh, bits, ntok, k, xkind, lkind):
+    """nmoe_moe_experts_from_logits (the routing inside the grouped path's
+    first launch) against nmoe_moe_topk then nmoe_moe_experts on the same
+    inputs: idx, w and out bit for bit, and every token's routing against the
+    oracle's math.m routing; two calls in a row (the routing counter starts
+    from 0 for the second), the second on other logits."""
+    rng = np.random.default_rng(5000 + 100 * bits + ntok + k)
+    seed, layer = 41, 20 + bits
+    big.synth_layer(layer, bits, seed, SIGMA[bits])
+    for call in range(2):
+        print(f"[from-logits] q{bits} ntok={ntok} k={k} x={xkind} {lkind} call {call}", flush=True)
+        if lkind == "zipf":
+            order = rng.permutation(256)
+            logp = np.empty(256)
+            logp[order] = -1.1 * np.log(np.arange(1, 257))
+            logits = (logp[None, :] + rng.gumbel(size=(ntok, 256))).astype(np.float32)
+        else:
+            logits = rng.random((ntok, 256), dtype=np.float32)
+        xf = rng.standard_normal((ntok, 2048)).astype(np.float32)
+        xdev, dt = (B.f32_to_bf16(xf), nh.BF16) if xkind == "bf16" else (xf, nh.F32)
+        h = rng.standard_normal((ntok, 2048)).astype(np.float32)
+        d_lg, d_x, d_h = big.to_device(logits), big.to_device(xdev), big.to_device(h)
+        res = {}
+        for path in ("from_logits", "topk_then_experts"):
+            idx, w, out = big.alloc(ntok * 32), big.alloc(ntok * 32), big.alloc(ntok * 2048 * 4)
+            if path == "from_logits":
+                big._check(big.experts_from_logits(layer, d_lg, d_x, dt, ntok, k, d_h, out, idx, w))
+            else:
+                big._check(big.topk(d_lg, ntok, 256, k, idx, w))
+                big._check(big.experts(bits, layer, d_x, dt, ntok, k, idx, w, d_h, out))
+            res[path] = (idx.download(np.uint32, (ntok, 8)), w.download(np.float32, (ntok, 8)),
+                         out.download(np.float32, (ntok, 2048)))
+        assert big.device_status() == nh.OK
+        (ia, wa, oa), (ib, wb, ob) = res["from_logits"], res["topk_then_experts"]
+        np.testing.assert_array_equal(ia, ib)
+        np.testing.assert_array_equal(wa.view(np.uint32), wb.view(np.uint32))
+        np.testing.assert_array_equal(oa.view(np.uint32), ob.view(np.uint32))
+        for t in range(ntok):
+            oi, ow, _ = B.route(logits[t], k)
+            np.testing.assert_array_equal(ia[t], oi, err_msg=f"t={t}")
+            np.testing.assert_array_equal(wa[t].view(np.uint32), ow.view(np.uint32), err_msg=f"t={t}")
+
+
+def test_experts_from_logits_rejects(big, nh):
+    big.synth_layer(25, 4, 1, 0.02)
+    lg, x, h, out = big.alloc(64 * 1024), big.alloc(64 * 4096), big.alloc(64 * 8192), big.alloc(64 * 8192)
+    idx, w = big.alloc(64 * 32), big.alloc(64 * 32)
+    assert big.experts_from_logits(25, None, x, nh.BF16, 64, 8, h, out, idx, w) == nh.EINVAL
+    assert big.experts_from_logits(25, lg, x, nh.BF16, 64, 8, h, out, None, w) == nh.EINVAL
+    assert big.experts_from_logits(25, lg, x, nh.BF16, 64, 9, h, out, idx, w) == nh.EINVAL
+    assert big.experts_from_logits(25, lg, x, nh.BF16, 4096, 8, h, out, idx, w) == nh.EINVAL
+    assert big.experts_from_logits(26, lg, x, nh.BF16, 64, 8, h, out, idx, w) == nh.ENOENT
 
 
 @pytest.mark.parametrize("bits", [4, 2])
