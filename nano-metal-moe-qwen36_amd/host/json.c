@@ -2,9 +2,10 @@
  * json.c -- a small JSON reader for the converter's metadata files
  * (layout.json, model_weights.json): numbers, strings, arrays, objects,
  * true/false/null; nesting up to 32 levels; \\uXXXX escapes become '?'
- * (the files are ASCII).  Plain C.
+ * (the files are ASCII); numbers must be finite doubles.  Plain C.
  */
 #include <ctype.h>
+#include <math.h>
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
@@ -72,16 +73,23 @@ static int jstring(jparser *ps, char **out) {
     return 0;
 }
 
+/* Appends a member, the room doubling as it fills (a member at a time
+ * would copy the array once per member: quadratic in its length). */
 static int jpush(jv *v, jv *kid, char *key) {
-    jv *k2 = (jv *)realloc(v->kids, sizeof(jv) * (size_t)(v->n + 1));
-    if (k2 == NULL) return -1;
-    v->kids = k2;
-    if (v->type == J_OBJ) {
-        char **kk = (char **)realloc(v->keys, sizeof(char *) * (size_t)(v->n + 1));
-        if (kk == NULL) return -1;
-        v->keys = kk;
-        v->keys[v->n] = key;
+    if (v->n == v->cap) {
+        if (v->cap > (1 << 26)) return -1;
+        const int cap = v->cap ? 2 * v->cap : 8;
+        jv *k2 = (jv *)realloc(v->kids, sizeof(jv) * (size_t)cap);
+        if (k2 == NULL) return -1;
+        v->kids = k2;
+        if (v->type == J_OBJ) {
+            char **kk = (char **)realloc(v->keys, sizeof(char *) * (size_t)cap);
+            if (kk == NULL) return -1;
+            v->keys = kk;
+        }
+        v->cap = cap;
     }
+    if (v->type == J_OBJ) v->keys[v->n] = key;
     v->kids[v->n++] = *kid;
     return 0;
 }
@@ -134,11 +142,24 @@ static int jparse(jparser *ps, jv *out) {
         out->type = J_STR;
         rc = jstring(ps, &out->str);
     } else if (c == '-' || isdigit((unsigned char)c)) {
+        /* a JSON number: the token (sign, digits, '.', exponent) copied out,
+         * so that strtod never reads past the text (which need not be
+         * NUL-terminated) and never sees the nan / inf / hex forms it would
+         * also accept; a value beyond double range is an error */
+        char tok[64];
+        size_t tl = 0;
+        while (ps->p + tl < ps->end && tl < sizeof tok - 1 &&
+               (isdigit((unsigned char)ps->p[tl]) || ps->p[tl] == '-' || ps->p[tl] == '+' || ps->p[tl] == '.' ||
+                ps->p[tl] == 'e' || ps->p[tl] == 'E'))
+            tl++;
+        if (tl == sizeof tok - 1) return -1;
+        memcpy(tok, ps->p, tl);
+        tok[tl] = 0;
         char *e = NULL;
         out->type = J_NUM;
-        out->num = strtod(ps->p, &e);
-        if (e == ps->p || e > ps->end) return -1;
-        ps->p = e;
+        out->num = strtod(tok, &e);
+        if (e == tok || !isfinite(out->num)) return -1;
+        ps->p += e - tok;
     } else if (ps->end - ps->p >= 4 && strncmp(ps->p, "true", 4) == 0) {
         out->type = J_BOOL, out->num = 1, ps->p += 4;
     } else if (ps->end - ps->p >= 5 && strncmp(ps->p, "false", 5) == 0) {
@@ -160,7 +181,10 @@ const jv *jget(const jv *o, const char *key) {
 }
 
 int jint(const jv *v, unsigned long long *out) {
-    if (v == NULL || v->type != J_NUM || v->num < 0 || v->num > 9.0e15 || v->num != (double)(unsigned long long)v->num)
+    /* the range test first (it also rejects NaN), so that the cast below is
+     * defined */
+    if (v == NULL || v->type != J_NUM || !(v->num >= 0.0 && v->num <= 9.0e15) ||
+        v->num != (double)(unsigned long long)v->num)
         return -1;
     *out = (unsigned long long)v->num;
     return 0;

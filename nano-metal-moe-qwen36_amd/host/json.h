@@ -15,6 +15,7 @@ typedef struct jv {
     struct jv *kids;     /* J_ARR / J_OBJ: children (objects: each child's str_key set) */
     char **keys;         /* J_OBJ: member keys, parallel to kids */
     int n;
+    int cap;             /* J_ARR / J_OBJ: room in kids (and keys) */
 } jv;
 
 void jv_free(jv *v);

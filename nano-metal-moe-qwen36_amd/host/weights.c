@@ -171,7 +171,9 @@ int nmoe_hip_load_model_weights(nmoe_hip_ctx *ctx, const char *bin_path, const c
     const jv *cfg = jget(&root, "config");
     float eps = 1e-6f;
     const jv *ev = jget(cfg, "rms_norm_eps");
-    if (ev != NULL && ev->type == J_NUM) eps = (float)ev->num;
+    if (ev != NULL && (ev->type != J_NUM || !(ev->num >= 0.0 && ev->num < 1.0)))
+        WFAIL(NMOE_HIP_EINVAL, "config.rms_norm_eps must be a number in [0, 1)");
+    if (ev != NULL) eps = (float)ev->num;
     unsigned long long cl = 0;
     int n = nlayers;
     if (n == 0 && jint(jget(cfg, "num_hidden_layers"), &cl) == 0) n = (int)cl;

@@ -15,7 +15,14 @@ from oracle import binding as B
 
 @pytest.fixture(scope="module")
 def layers():
-    return [B.syn_layer(2, 7, l, 0.05) for l in range(2)]
+    esz = B.EXPERT_SIZE[2]
+    out = []
+    for l in range(2):
+        p = np.empty(256 * esz, np.uint8)
+        for e in range(256):
+            p[e * esz:(e + 1) * esz] = B.syn_expert(2, 7, l, e, 0.05)
+        out.append(p)
+    return out
 
 
 def _tokens(ntok, seed):
