@@ -517,6 +517,12 @@ def run_grouped(pool, args, workload: str, NLg: int = 8) -> dict:
         top = np.argsort(-lg, axis=1, kind="stable")[:, :k]
         touched.append(len(np.unique(top)))
     IDX, WT, OUT = ctx.alloc(ntok * 32), ctx.alloc(ntok * 32), ctx.alloc(ntok * 2048 * 4)
+    # the library runs gate/up and down in one launch where the device allows
+    # it and the experts average at most half a 64-entry pass (one pass lane:
+    # ntok * k <= 8192), else in two
+    one = args.grouped_launches == 1 and ctx.set_grouped_one_launch(True) and ntok * k <= 8192
+    if args.grouped_launches == 2:
+        ctx.set_grouped_one_launch(False)
     ctx.sync()
 
     def step(layer):
@@ -531,6 +537,8 @@ def run_grouped(pool, args, workload: str, NLg: int = 8) -> dict:
     for i in range(2 * NLg):
         step(NLg + i % NLg)
     ctx.sync()
+    if args.timeline:
+        return grouped_timeline(ctx, step, NLg, workload, one, dump=args.timeline_dump)
     ev = HipEvents()
     e0, e1 = ev.create(2)
     ev.record(e0, stream)
@@ -542,6 +550,7 @@ def run_grouped(pool, args, workload: str, NLg: int = 8) -> dict:
     if ctx.device_status() != 0:
         raise SystemExit(f"device status error: {ctx.last_error()}")
     ev.destroy([e0, e1])
+    ctx.set_grouped_one_launch(True)
     cpu = None
     if not args.no_cpu:
         print(f"[bench] {workload} q{bits} cpu baseline ...", file=sys.stderr, flush=True)
@@ -569,8 +578,59 @@ def run_grouped(pool, args, workload: str, NLg: int = 8) -> dict:
                    "distinct_experts_per_step": round(U, 1), "bytes_per_step": int(B), "flops_per_step": int(flops),
                    "entry_point": ("nmoe_moe_experts_from_logits (routing in the grouped path's first launch)"
                                    if args.grouped_entry == "from-logits"
-                                   else "nmoe_moe_topk + nmoe_moe_experts_q%d (grouped path)" % bits)},
+                                   else "nmoe_moe_topk + nmoe_moe_experts_q%d (grouped path)" % bits),
+                   "gemm_launches": 1 if one else 2},
     }
+
+
+GTL_SLOTS = 16  # timeline slots of one grouped step: 4 stamps a block, 1,024 blocks a slot
+
+
+def grouped_timeline(ctx, step, NLg: int, workload: str, one: bool, nsteps: int = 8, dump: str = "") -> dict:
+    """Block timeline of the grouped GEMM launches (timeline build): for
+    nsteps steps, each block of the gate/up and down launches (or of the one
+    launch) records its start, the end of its wait (down tiles of the
+    one-launch form) and its end.  Per step, from the first block's start:
+    the blocks with work of each kind (count, median duration, median
+    wait), when the last gate/up tile ends and the first down tile starts,
+    the GEMMs' span, and the mean number of blocks with work running at once
+    over that span (two a CU can run: 512)."""
+    tick_us = 0.01  # s_memrealtime counts at 100 MHz
+    words = GTL_SLOTS * 256 * 16
+    stamps = ctx.alloc(words * 8)
+    per, raw = [], []
+    for i in range(nsteps):
+        stamps.upload(np.zeros(words, np.uint64))
+        ctx._check(ctx.set_timeline(stamps, GTL_SLOTS))
+        step(i % NLg)
+        ctx.sync()
+        ctx._check(ctx.set_timeline(None, 0))
+        r = stamps.download(np.uint64, (words // 4, 4))
+        r = r[r[:, 0] > 0].astype(np.int64)
+        raw.append(r)
+        info = r[:, 3]
+        work, kind = info >> 32, (info >> 28) & 15
+        t0 = r[:, 0].min()
+        st, rd, en = (r[:, 0] - t0) * tick_us, (r[:, 1] - t0) * tick_us, (r[:, 2] - t0) * tick_us
+        gu, dn = (work > 0) & (kind == 1), (work > 0) & (kind == 2)  # gate/up and down tiles with work
+        span = float(en[gu | dn].max())
+        grid = np.arange(0.0, span, 0.25)
+        busy = ((st[gu | dn][None, :] <= grid[:, None]) & (grid[:, None] < en[gu | dn][None, :])).sum(axis=1)
+        per.append({
+            "span_us": span, "gateup_blocks": int(gu.sum()), "down_blocks": int(dn.sum()),
+            "gateup_median_us": float(np.median(en[gu] - st[gu])), "down_median_us": float(np.median(en[dn] - st[dn])),
+            "down_wait_median_us": float(np.median(rd[dn] - st[dn])), "down_wait_max_us": float((rd[dn] - st[dn]).max()),
+            "last_gateup_end_us": float(en[gu].max()), "first_down_start_us": float(st[dn].min()),
+            "busy_mean": float(busy.mean()), "busy_after_last_gateup_start_mean":
+                float(busy[grid >= st[gu].max()].mean()) if (grid >= st[gu].max()).any() else None,
+        })
+    if dump:  # the raw block records: [start, ready, end, info] ticks per block, one array per step
+        np.savez_compressed(dump, *raw)
+    med = {key: (round(float(np.median([p[key] for p in per])), 3) if per[0][key] is not None else None) for key in per[0]}
+    for key, v in med.items():
+        print(f"[timeline] {workload} {key:36s} {v}", file=sys.stderr, flush=True)
+    return {"metric": f"block timeline of the {workload} grouped GEMM launches (timeline build)", "workload": workload,
+            "gemm_launches": 1 if one else 2, "steps": nsteps, "medians": med}
 
 
 BLOCK_SLOTS = 160  # per-layer model tensors rotated by the block workload: 160 x 2.1 MB, above the 256 MB MALL
@@ -885,9 +945,15 @@ def main():
     ap.add_argument("--grouped-entry", default="from-logits", choices=("from-logits", "topk+experts"),
                     help="c4 / c5: one call routing from the given logits inside the grouped path (default), or "
                          "nmoe_moe_topk then nmoe_moe_experts")
+    ap.add_argument("--grouped-launches", type=int, default=1, choices=(1, 2),
+                    help="c4 / c5: gate/up and down of the grouped path in one launch (1, default, where the device's "
+                         "die placement allows it) or two")
     ap.add_argument("--timeline", action="store_true",
                     help="c1 / c3 / block: load the phase-timeline build (libnmoe_hip_tl.so) and print the medians of "
-                         "each phase boundary instead of the bench line")
+                         "each phase boundary instead of the bench line; c4 / c5: the block timeline of the grouped "
+                         "GEMM launches")
+    ap.add_argument("--timeline-dump", default="", metavar="PATH",
+                    help="c4 / c5 with --timeline: also write the raw block records to PATH (.npz)")
     ap.add_argument("--router", default="bf16", choices=("bf16", "q4"),
                     help="c1/c3: the benchmark configs' dense bf16 router (default) or the model's q4 router")
     ap.add_argument("--workload", default="c1", choices=("c1", "c3", "c4", "c5", "stream", "block", "probe-sweep"),
@@ -905,11 +971,13 @@ def main():
     import nmoe_hip as nh
 
     if args.timeline:
-        if args.workload not in ("c1", "c3", "block"):
-            raise SystemExit("--timeline: workloads c1, c3 and block (the fused launches)")
+        if args.workload not in ("c1", "c3", "block", "c4", "c5"):
+            raise SystemExit("--timeline: workloads c1, c3 and block (the fused launches), c4 and c5 (the grouped "
+                             "GEMM launches)")
         nh.use_timeline_build()
-        pool = Pool(nh, args, max_tokens=8)
-        print(json.dumps(run_timeline(pool, args)), flush=True)
+        pool = Pool(nh, args, max_tokens=2048 if args.workload in ("c4", "c5") else 8)
+        res = run_grouped(pool, args, args.workload) if args.workload in ("c4", "c5") else run_timeline(pool, args)
+        print(json.dumps(res), flush=True)
         pool.ctx.close()
         return
 

@@ -130,6 +130,20 @@ NMOE_HIP_API int nmoe_hip_check_device_status(nmoe_hip_ctx *ctx);
  * launch boundary separates the layers) when all its packs have one bit
  * width and all its routers one kind; 0 runs one launch per layer. */
 #define NMOE_HIP_OPT_STACK_LOOP 7
+/* NMOE_HIP_OPT_GROUPED_ONE_LAUNCH (default 1 where the device deals the
+ * blocks of a launch round-robin over its 8 dies, checked at create): the
+ * grouped path runs gate/up and down in one launch, each down tile starting
+ * once its expert's gate/up tiles are done (a bounded wait); 0 runs them as
+ * two launches.  The results are the same to the grouped path's
+ * tolerance. */
+#define NMOE_HIP_OPT_GROUPED_ONE_LAUNCH 8
+/* NMOE_HIP_OPT_SKEW_TILES (value = expert rank 0..255, by entries, most
+ * first; for tests of the failure path): the next one-launch grouped call
+ * starts that rank's count of finished gate/up tiles at an impossible
+ * value, so its down tiles find the count wrong, as they would had the
+ * tiles run on another die: the call's outputs are NaN and
+ * nmoe_hip_check_device_status returns NMOE_HIP_ETIMEDOUT.  Once. */
+#define NMOE_HIP_OPT_SKEW_TILES 9
 NMOE_HIP_API int nmoe_hip_set_option(nmoe_hip_ctx *ctx, int option, int value);
 
 /* Per-stage timing of the fused launches (the counterpart of the

@@ -132,6 +132,18 @@ extern "C" int nmoe_hip_set_option(nmoe_hip_ctx *ctx, int option, int value) {
         ctx->stack_loop = value != 0;
         return NMOE_HIP_OK;
     }
+    if (option == NMOE_HIP_OPT_SKEW_TILES) {
+        if (value < 0 || value >= NMOE_EXPERTS)
+            return nmoe_fail(ctx, NMOE_HIP_EINVAL, "expert rank %d outside 0..%d", value, NMOE_EXPERTS - 1);
+        ctx->skew_tiles = value;
+        return NMOE_HIP_OK;
+    }
+    if (option == NMOE_HIP_OPT_GROUPED_ONE_LAUNCH) {
+        if (value != 0 && !ctx->xcd_placed)
+            return nmoe_fail(ctx, NMOE_HIP_EINVAL, "this device does not deal a launch's blocks round-robin over 8 dies");
+        ctx->grouped_one_launch = value != 0;
+        return NMOE_HIP_OK;
+    }
     if (option == NMOE_HIP_OPT_SKEW_EPOCH) {
         /* Moves block `value`'s launch epoch one ahead of the others, so the
          * next fused launch cannot complete: its bounded waits expire and it
@@ -164,6 +176,14 @@ extern "C" int nmoe_hip_set_timeline(nmoe_hip_ctx *ctx, void *stamps, int slots)
     (void)slots;
     return nmoe_fail(ctx, NMOE_HIP_EINVAL, "this library was built without the phase timeline (NMOE_TIMELINE)");
 #endif
+}
+
+uint64_t *nmoe_tl_take(nmoe_hip_ctx *ctx, int n) {
+    if (!NMOE_TIMELINE || ctx->tl == NULL || n > ctx->tl_slots) return NULL;
+    if (ctx->tl_next + n > ctx->tl_slots) ctx->tl_next = 0;
+    uint64_t *p = ctx->tl + (size_t)ctx->tl_next * NMOE_TL_SLOT_WORDS;
+    ctx->tl_next += n;
+    return p;
 }
 
 extern "C" int nmoe_sync_check(nmoe_hip_ctx *ctx, void *stream) {

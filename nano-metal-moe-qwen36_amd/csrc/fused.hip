@@ -242,13 +242,6 @@ __device__ __forceinline__ uint4 nmoe_ld_nt4(const nmoe_gv4 *p) {
     return make_uint4(v.x, v.y, v.z, v.w);
 }
 
-/* Accelerator die (XCC) the calling wave runs on. */
-__device__ __forceinline__ uint32_t nmoe_xcc_id() {
-    uint32_t v;
-    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID, 0, 4)" : "=s"(v));
-    return v;
-}
-
 /* A bounded wait that gave up: the status word tells the host, and the
  * block's LDS flag makes everything the block publishes from then on NaN,
  * so a result computed from words that never arrived cannot pass for a
@@ -1628,16 +1621,6 @@ extern "C" hipError_t nmoe_fused_launch_core(int bits, int route, const void *x,
             : r == NMOE_ROUTE_BF16 ? nmoe_fused_launch_x<2, NMOE_ROUTE_BF16>(xmode, a, s)
                                    : nmoe_fused_launch_x<2, NMOE_ROUTE_GIVEN>(xmode, a, s);
     return e;
-}
-
-/* The next n timeline slots of the context (NMOE_TIMELINE builds; NULL
- * when no timeline buffer is set). */
-static uint64_t *nmoe_tl_take(nmoe_hip_ctx *ctx, int n) {
-    if (!NMOE_TIMELINE || ctx->tl == NULL || n > ctx->tl_slots) return NULL;
-    if (ctx->tl_next + n > ctx->tl_slots) ctx->tl_next = 0;
-    uint64_t *p = ctx->tl + (size_t)ctx->tl_next * NMOE_FUSED_BLOCKS * NMOE_TL_EVENTS;
-    ctx->tl_next += n;
-    return p;
 }
 
 extern "C" int nmoe_fused_decode(nmoe_hip_ctx *ctx, int bits, int route, const void *x, int xmode, float eps, int k,

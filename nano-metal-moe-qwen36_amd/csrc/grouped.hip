@@ -365,6 +365,39 @@ __device__ __forceinline__ void nmoe_wait_count(uint32_t *cnt, uint32_t target, 
     }
 }
 
+/* The one-launch GEMM's schedule words (zeroed by the preparation launch):
+ * done[256], per expert rank, counts the gate/up tiles whose act rows are
+ * stored; each adds 1 + 2^(16 + its die). */
+#define NMOE_SCHED_WORDS NMOE_EXPERTS
+
+/* An expert's done word is touched only by the blocks of one die (its
+ * gate/up and down tiles share a die): atomics performed in that die's L2
+ * (workgroup scope: no write-through to memory) and loads that bypass the
+ * L1 and are served by the L2 (sc0 sc1), a round trip through the die's L2
+ * instead of memory. */
+__device__ __forceinline__ uint32_t nmoe_add_u32_die(uint32_t *p, uint32_t v) {
+    return __hip_atomic_fetch_add((nmoe_g32 *)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+__device__ __forceinline__ uint32_t nmoe_ld_u32_die(const uint32_t *p) {
+    return __hip_atomic_load((nmoe_g32 *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
+/* A down tile waits (thread 0, bounded) until the low 16 bits of its
+ * expert's done word reach its n gate/up tiles, then checks the die bits:
+ * every one of those tiles must have run on this block's die (their act
+ * rows are in this die's L2, not yet in memory); otherwise, or when the
+ * wait gives up, it sets the status word. */
+__device__ __forceinline__ void nmoe_tile_done(uint32_t *cnt) { nmoe_add_u32_die(cnt, 1u + (1u << (16 + nmoe_xcc_id()))); }
+__device__ __forceinline__ void nmoe_wait_tiles(uint32_t *cnt, uint32_t n, uint32_t *sync, uint32_t spin) {
+    uint32_t spins = 0, v;
+    while (((v = nmoe_ld_u32_die(cnt)) & 0xffffu) < n) {
+        __builtin_amdgcn_s_sleep(1);
+        if (++spins > spin) break;
+    }
+    if (v != n + (n << (16 + nmoe_xcc_id())))
+        __hip_atomic_store((nmoe_g32 *)(sync + NMOE_SYNC_STATUS), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 /* One launch for the grouped path's preparation: blocks 0 .. nd-1 run the
  * dispatch (D1, then D2 once every slice's histogram is in), the blocks
  * after them prepare one token's x each (none when x is NULL).  With more
@@ -391,8 +424,13 @@ __global__ void __launch_bounds__(256) nmoe_grouped_prep_kernel(const uint32_t *
                                                                 uint4 *rank, uint32_t *sync, uint32_t spin,
                                                                 const XT *x, uint16_t *xhi, uint16_t *xlo,
                                                                 uint16_t *xs3, const float *logits, uint32_t *idx_out,
-                                                                float *w_out) {
+                                                                float *w_out, uint32_t *done, int skew) {
     const int b = blockIdx.x;
+    /* the one-launch GEMM's tile counts start from 0 (plain stores: the next
+     * launch on the stream sees them); rank `skew` (a test of the failure
+     * path) from a count no tiles can reach */
+    if (done != NULL && b == 0)
+        for (int i = threadIdx.x; i < NMOE_SCHED_WORDS; i += 256) done[i] = i == skew ? 0x8000u : 0u;
     const int nr = ROUTED ? (ntok + 3) / 4 : 0; /* routing blocks */
     const int n = ntok * k, per = (n + nd - 1) / nd; /* dispatch slices */
     if (ROUTED && b >= nd && b < nd + nr) {
@@ -698,6 +736,53 @@ __device__ __forceinline__ float nmoe_silu_fast(float x) {
     return x * (x >= 0.0f ? r : z * r);
 }
 
+/* Phase timeline of a GEMM launch (NMOE_TIMELINE builds; tl NULL
+ * otherwise): block b's words tl[4b .. 4b+3] = the real-time clock at its
+ * start, once its inputs are ready (a down tile of the one-launch form:
+ * after its wait; else its start) and at its end, and what it ran:
+ * entries << 32 | kind << 28 | die << 24 | expert rank << 8 | tile (kind 1
+ * gate/up, 2 down).  One lane stores, with a vector store. */
+#define NMOE_GTL_START 0
+#define NMOE_GTL_READY 1
+#define NMOE_GTL_END 2
+#define NMOE_GTL_INFO 3
+__device__ __forceinline__ void nmoe_gtl_put(uint64_t *tl, int w, uint64_t v) {
+    if constexpr (NMOE_TIMELINE) {
+        if (tl != nullptr) {
+            uint64_t *p = tl + 4 * (size_t)blockIdx.x + w;
+            asm volatile("global_store_dwordx2 %0, %1, off" ::"v"(p), "v"(v) : "memory");
+        }
+    }
+}
+__device__ __forceinline__ void nmoe_gtl_stamp(uint64_t *tl, int w) {
+    if constexpr (NMOE_TIMELINE)
+        if (tl != nullptr) nmoe_gtl_put(tl, w, __builtin_amdgcn_s_memrealtime());
+}
+/* start and ready at a block's entry, end and what it ran at its exit */
+__device__ __forceinline__ void nmoe_gtl_begin(uint64_t *tl) {
+    if constexpr (NMOE_TIMELINE) {
+        if (tl != nullptr && threadIdx.x == 0) {
+            const uint64_t t = __builtin_amdgcn_s_memrealtime();
+            nmoe_gtl_put(tl, NMOE_GTL_START, t);
+            nmoe_gtl_put(tl, NMOE_GTL_READY, t);
+        }
+    }
+}
+__device__ __forceinline__ void nmoe_gtl_end(uint64_t *tl, int kind, const uint4 *rank, int es, int nt, int pl,
+                                             int nrows) {
+    if constexpr (NMOE_TIMELINE) {
+        if (tl != nullptr && threadIdx.x == 0) {
+            nmoe_gtl_stamp(tl, NMOE_GTL_END);
+            const uint4 rk = rank[es];
+            const uint32_t p0 = min(rk.y, (uint32_t)nrows), n = min(rk.z, (uint32_t)nrows - p0);
+            const uint32_t work = n > (uint32_t)(pl * NMOE_MCHUNK) ? n : 0u;
+            nmoe_gtl_put(tl, NMOE_GTL_INFO,
+                         ((uint64_t)work << 32) | ((uint64_t)kind << 28) | ((uint64_t)nmoe_xcc_id() << 24) |
+                             ((uint64_t)es << 8) | (uint64_t)nt);
+        }
+    }
+}
+
 /* ------------------------------------------------------------ gate/up */
 
 /* Gate (and up) rows per block of NW wavefronts: 32 a wavefront for bf16 x
@@ -742,43 +827,49 @@ __host__ __device__ constexpr int nmoe_gu_stages(int bits, int xpl, int nw) {
  * first, as sum_g xs_g b_g - 128 sum_g xs_g s_g over the 32 groups: one bf16
  * MFMA (K = 32) per part of xs (three exact bf16 parts) and per operand (the
  * bf16 biases and scales as they are), fp32 accumulate. */
+/* The LDS of a gate/up block.  The tile's gate and up scales chunk-major:
+ * 16-byte chunk q (groups 8q..8q+7) of row r at [mat][q][r], so a ring
+ * step's 16 rows of one group sit 16 bytes apart (distinct banks; row-major
+ * rows 64 bytes apart put four rows on each bank).  The stage buffers hold
+ * one stage of either form each, and every stage is a typed variable of its
+ * own, so that the compiler tells the stages' direct loads apart. */
 template <int BITS, int XPL, int NW>
-__global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
-nmoe_grouped_gateup_kernel(const uint8_t *pack, const uint16_t *xhi, const uint16_t *xlo, const uint16_t *xs3,
-                           const uint32_t *perm, const uint4 *rank, int k, int lanes, int nrows, uint16_t *ahi,
-                           uint16_t *alo, float *as) {
-    using Q = nmoe_q<BITS>;
-    using L = nmoe_layout<BITS>;
-    constexpr int G = NMOE_HIDDEN / NMOE_GROUP; /* 32 groups */
-    static_assert(G == 32, "the correction's operand layout assumes 8 groups per lane");
-    static_assert(NW == 8 || NW == 4, "eight or four wavefronts");
-    constexpr int NT = nmoe_gu_rows(XPL, NW);
-    constexpr int NB = NT / (16 * NW);          /* column blocks per wavefront and matrix */
-    constexpr int NTH = 64 * NW;
-    /* gate and up scales of the tile, chunk-major: 16-byte chunk q (groups
-     * 8q..8q+7) of row r at [mat][q][r], so a ring step's 16 rows of one
-     * group sit 16 bytes apart (distinct banks; row-major rows 64 bytes
-     * apart put four rows on each bank) */
-    __shared__ uint16_t s_s[2][G / 8][NT][8];
-    constexpr int NS = nmoe_gu_stages(BITS, XPL, NW); /* (five measured no faster than four) */
-    /* the stage buffers, each holding one stage of either form: a typed
-     * variable of its own per stage, so that the compiler tells the stages'
-     * direct loads apart */
+struct nmoe_gu_lds_types {
+    static constexpr int NT = nmoe_gu_rows(XPL, NW);
+    typedef uint16_t Scales[2][NMOE_HIDDEN / NMOE_GROUP / 8][NT][8];
     typedef nmoe_stage<XPL, NMOE_MCHUNK, 2 * NT * nmoe_code_row<BITS, 1>::WPS> StageB;
     typedef nmoe_stage<XPL, NMOE_SMALL_GPS * NMOE_SMALL_PASS, 2 * NT * nmoe_code_row<BITS, NMOE_SMALL_GPS>::WPS>
         StageS;
     typedef nmoe_stage_buf<StageB, typename std::conditional<nmoe_small_form(NW), StageS, StageB>::type> StageU;
     static_assert(sizeof(StageU) == nmoe_gu_stage_max(BITS, XPL, NW), "stage buffer size");
-    __shared__ StageU s_st0, s_st1, s_st2, s_st3;
-    __shared__ uint32_t s_tok[NMOE_MCHUNK];
-    __shared__ float s_as[NW][NMOE_MCHUNK];
-    /* pass lane pl of `lanes`: passes pl, pl + lanes, ... of tile (e, nt) */
-    constexpr int NTILE = NMOE_INTER / NT;
-    const int pl = blockIdx.x / (NMOE_EXPERTS * NTILE);
-    /* the tile's expert is the es-th by entries (most first), so the
-     * longest tiles start first */
-    int es, nt;
-    nmoe_die_tile(blockIdx.x % (NMOE_EXPERTS * NTILE), NTILE, es, nt);
+};
+
+/* Gate/up tile nt of the es-th expert by entries, pass lane pl, with NS
+ * stages in the given LDS buffers (s_st3 is used only with NS = 4).  COUNT:
+ * once the tile's act rows and group sums are stored (complete, in this
+ * die's L2), the block counts itself in done[es] (nmoe_tile_done), which
+ * the down tiles of the same launch wait for. */
+template <int BITS, int XPL, int NW, int NS, bool COUNT>
+__device__ __forceinline__ void nmoe_gu_tile(const uint8_t *pack, const uint16_t *xhi, const uint16_t *xlo,
+                                             const uint16_t *xs3, const uint32_t *perm, const uint4 *rank, int k,
+                                             int lanes, int nrows, uint16_t *ahi, uint16_t *alo, float *as, int es,
+                                             int nt, int pl, typename nmoe_gu_lds_types<BITS, XPL, NW>::Scales &s_s,
+                                             typename nmoe_gu_lds_types<BITS, XPL, NW>::StageU &s_st0,
+                                             typename nmoe_gu_lds_types<BITS, XPL, NW>::StageU &s_st1,
+                                             typename nmoe_gu_lds_types<BITS, XPL, NW>::StageU &s_st2,
+                                             typename nmoe_gu_lds_types<BITS, XPL, NW>::StageU &s_st3,
+                                             uint32_t (&s_tok)[NMOE_MCHUNK], float (&s_as)[NW][NMOE_MCHUNK],
+                                             uint32_t *done) {
+    using Q = nmoe_q<BITS>;
+    using L = nmoe_layout<BITS>;
+    constexpr int G = NMOE_HIDDEN / NMOE_GROUP; /* 32 groups */
+    static_assert(G == 32, "the correction's operand layout assumes 8 groups per lane");
+    static_assert(NW == 8 || NW == 4, "eight or four wavefronts");
+    static_assert(NS == 3 || NS == 4, "three or four stages");
+    constexpr int NT = nmoe_gu_rows(XPL, NW);
+    constexpr int NB = NT / (16 * NW);          /* column blocks per wavefront and matrix */
+    constexpr int NTH = 64 * NW;
+    typedef typename nmoe_gu_lds_types<BITS, XPL, NW>::StageU StageU;
     /* (e, first entry, entries) of a dispatch whose meeting gave up can be
      * anything; the clamps keep every access inside the buffers */
     const uint4 rk = rank[es];
@@ -1028,12 +1119,45 @@ nmoe_grouped_gateup_kernel(const uint8_t *pack, const uint16_t *xhi, const uint1
     };
     /* block-uniform: the expert's entry count picks the form */
     if constexpr (nmoe_small_form(NW)) {
-        if (n <= (uint32_t)NMOE_SMALL_PASS) {
+        if (n <= (uint32_t)NMOE_SMALL_PASS)
             run(std::integral_constant<int, NMOE_SMALL_PASS>{}, std::integral_constant<int, NMOE_SMALL_GPS>{});
-            return;
-        }
+        else
+            run(std::integral_constant<int, NMOE_MCHUNK>{}, std::integral_constant<int, 1>{});
+    } else {
+        run(std::integral_constant<int, NMOE_MCHUNK>{}, std::integral_constant<int, 1>{});
     }
-    run(std::integral_constant<int, NMOE_MCHUNK>{}, std::integral_constant<int, 1>{});
+    if constexpr (COUNT) {
+        /* every wavefront's act and group-sum stores complete (vmcnt 0: in
+         * this die's L2), then the tile is counted */
+        nmoe_wait_vm<0>();
+        asm volatile("s_barrier" ::: "memory");
+        if (threadIdx.x == 0) nmoe_tile_done(done + es);
+    }
+}
+
+template <int BITS, int XPL, int NW>
+__global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
+nmoe_grouped_gateup_kernel(const uint8_t *pack, const uint16_t *xhi, const uint16_t *xlo, const uint16_t *xs3,
+                           const uint32_t *perm, const uint4 *rank, int k, int lanes, int nrows, uint16_t *ahi,
+                           uint16_t *alo, float *as, uint64_t *tl) {
+    nmoe_gtl_begin(tl);
+    typedef nmoe_gu_lds_types<BITS, XPL, NW> T;
+    __shared__ typename T::Scales s_s;
+    __shared__ typename T::StageU s_st0, s_st1, s_st2, s_st3;
+    __shared__ uint32_t s_tok[NMOE_MCHUNK];
+    __shared__ float s_as[NW][NMOE_MCHUNK];
+    /* pass lane pl of `lanes`: passes pl, pl + lanes, ... of tile (e, nt);
+     * the tile's expert is the es-th by entries (most first), so the
+     * longest tiles start first */
+    constexpr int NTILE = NMOE_INTER / T::NT;
+    const int pl = blockIdx.x / (NMOE_EXPERTS * NTILE);
+    int es, nt;
+    nmoe_die_tile(blockIdx.x % (NMOE_EXPERTS * NTILE), NTILE, es, nt);
+    /* (five stages measured no faster than four) */
+    nmoe_gu_tile<BITS, XPL, NW, nmoe_gu_stages(BITS, XPL, NW), false>(pack, xhi, xlo, xs3, perm, rank, k, lanes, nrows,
+                                                                      ahi, alo, as, es, nt, pl, s_s, s_st0, s_st1,
+                                                                      s_st2, s_st3, s_tok, s_as, NULL);
+    nmoe_gtl_end(tl, 1, rank, es, nt, pl, nrows);
 }
 
 /* ------------------------------------------------------------ down */
@@ -1041,62 +1165,78 @@ nmoe_grouped_gateup_kernel(const uint8_t *pack, const uint16_t *xhi, const uint1
 /* Down rows per block of NW wavefronts: 64 a wavefront. */
 __host__ __device__ constexpr int nmoe_dn_rows(int nw) { return nw * 64; }
 
-/* Bytes of one down stage (act hi and lo rows, codes) with mch entries a
- * pass and gps groups a step; a stage buffer holds either form's. */
-__host__ __device__ constexpr int nmoe_dn_stage(int bits, int nw, int mch, int gps) {
-    return 2 * gps * mch * 128 + nmoe_dn_rows(nw) * gps * (bits == 4 ? 32 : 16);
+/* Bytes of one down stage (act hi and lo rows, codes) of a tile of nt
+ * rows with mch entries a pass and gps groups a step; a stage buffer holds
+ * either form's. */
+__host__ __device__ constexpr int nmoe_dn_stage(int bits, int nt, int mch, int gps) {
+    return 2 * gps * mch * 128 + nt * gps * (bits == 4 ? 32 : 16);
 }
-__host__ __device__ constexpr int nmoe_dn_stage_max(int bits, int nw) {
-    return nmoe_small_form(nw) && nmoe_dn_stage(bits, nw, NMOE_SMALL_PASS, NMOE_SMALL_GPS) >
-                                      nmoe_dn_stage(bits, nw, NMOE_MCHUNK, 1)
-               ? nmoe_dn_stage(bits, nw, NMOE_SMALL_PASS, NMOE_SMALL_GPS)
-               : nmoe_dn_stage(bits, nw, NMOE_MCHUNK, 1);
+__host__ __device__ constexpr int nmoe_dn_stage_max(int bits, int nw, int nt) {
+    return nmoe_small_form(nw) && nmoe_dn_stage(bits, nt, NMOE_SMALL_PASS, NMOE_SMALL_GPS) >
+                                      nmoe_dn_stage(bits, nt, NMOE_MCHUNK, 1)
+               ? nmoe_dn_stage(bits, nt, NMOE_SMALL_PASS, NMOE_SMALL_GPS)
+               : nmoe_dn_stage(bits, nt, NMOE_MCHUNK, 1);
 }
 /* LDS bytes of a down block with ns stages: the stages, the scales and
  * s_q. */
-__host__ __device__ constexpr int nmoe_dn_lds(int bits, int nw, int ns) {
-    return ns * nmoe_dn_stage_max(bits, nw) + nmoe_dn_rows(nw) * 16 + 4 * NMOE_MCHUNK;
+__host__ __device__ constexpr int nmoe_dn_lds(int bits, int nw, int nt, int ns) {
+    return ns * nmoe_dn_stage_max(bits, nw, nt) + nt * 16 + 4 * NMOE_MCHUNK;
 }
 __host__ __device__ constexpr int nmoe_dn_stages(int bits, int nw) {
-    return nmoe_dn_lds(bits, nw, 4) <= (nw == 8 ? 160 : 80) * 1024 - 512 ? 4 : 3;
+    return nmoe_dn_lds(bits, nw, nmoe_dn_rows(nw), 4) <= (nw == 8 ? 160 : 80) * 1024 - 512 ? 4 : 3;
 }
 
-/* Expert e, down rows NT * nt .. +NT-1: y[q][row] for all the expert's
- * entries q, 64 per pass (16 in one pass in the small form).  NW
- * wavefronts (as in the gate/up kernel); wavefront w owns rows
- * (NT/NW)w .. +NT/NW-1 of the tile as NB 16-row column blocks.  act enters
- * as hi and lo bf16 planes. */
-template <int BITS, int NW>
-__global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
-nmoe_grouped_down_kernel(const uint8_t *pack, const uint16_t *ahi, const uint16_t *alo, const float *as,
-                         const uint32_t *perm, const uint4 *rank, int lanes, int nrows, float *y) {
+/* The LDS of a down block of NT-row tiles (the scales of the tile, and
+ * stage buffers as in the gate/up block). */
+template <int BITS, int NW, int NT>
+struct nmoe_dn_lds_types {
+    typedef uint16_t Scales[NT][NMOE_INTER / NMOE_GROUP];
+    typedef nmoe_stage<2, NMOE_MCHUNK, NT * nmoe_code_row<BITS, 1>::WPS> StageB;
+    typedef nmoe_stage<2, NMOE_SMALL_GPS * NMOE_SMALL_PASS, NT * nmoe_code_row<BITS, NMOE_SMALL_GPS>::WPS> StageS;
+    typedef nmoe_stage_buf<StageB, typename std::conditional<nmoe_small_form(NW), StageS, StageB>::type> StageU;
+    static_assert(sizeof(StageU) == nmoe_dn_stage_max(BITS, NW, NT), "stage buffer size");
+};
+
+/* Down tile nt (NT rows) of the es-th expert by entries, pass lane pl:
+ * y[q][row] for all the expert's entries q, 64 per pass (16 in one pass in
+ * the small form), with NS stages in the given LDS buffers.  NW wavefronts
+ * (as in the gate/up kernel); wavefront w owns rows (NT/NW)w .. +NT/NW-1 of
+ * the tile as NB 16-row column blocks.  act enters as hi and lo bf16
+ * planes.
+ *
+ * WAIT (the gate/up tiles run in the same launch): with its weight loads
+ * in flight, a bounded wait until done[es] counts all gu_tiles gate/up
+ * tiles of each pass lane that has work; those ran on this block's die (the
+ * same block index mod 8; nmoe_wait_tiles checks it), so their act rows
+ * are in this die's L2.  The act rows are then read through L1 as usual (no
+ * block of this launch read them before they were complete: an act row is
+ * 1 KB, whole cache lines), the group sums, whose 32-byte rows share cache
+ * lines with other experts' rows, with loads that bypass L1. */
+template <int BITS, int NW, int NT, int NS, bool WAIT>
+__device__ __forceinline__ void nmoe_dn_tile(const uint8_t *pack, const uint16_t *ahi, const uint16_t *alo,
+                                             const float *as, const uint32_t *perm, const uint4 *rank, int lanes,
+                                             int nrows, float *y, int es, int nt, int pl,
+                                             typename nmoe_dn_lds_types<BITS, NW, NT>::Scales &s_s,
+                                             typename nmoe_dn_lds_types<BITS, NW, NT>::StageU &s_st0,
+                                             typename nmoe_dn_lds_types<BITS, NW, NT>::StageU &s_st1,
+                                             typename nmoe_dn_lds_types<BITS, NW, NT>::StageU &s_st2,
+                                             typename nmoe_dn_lds_types<BITS, NW, NT>::StageU &s_st3,
+                                             uint32_t (&s_q)[NMOE_MCHUNK], uint32_t *done, int gu_tiles,
+                                             uint32_t *sync, uint32_t spin, uint64_t *tl) {
     using Q = nmoe_q<BITS>;
     using L = nmoe_layout<BITS>;
     constexpr int G = NMOE_INTER / NMOE_GROUP; /* 8 groups */
     static_assert(G == 8, "the correction's operand layout assumes 2 groups per lane");
     static_assert(NW == 8 || NW == 4, "eight or four wavefronts");
-    constexpr int NT = nmoe_dn_rows(NW);
+    static_assert(NS == 3 || NS == 4, "three or four stages");
+    static_assert(NT % (16 * NW) == 0, "whole column blocks per wavefront");
     constexpr int NB = NT / (16 * NW);
-    constexpr int NS = nmoe_dn_stages(BITS, NW);
-    __shared__ uint16_t s_s[NT][G]; /* scales of the tile */
-    /* stage buffers holding one stage of either form, one typed variable
-     * per stage (as in the gate/up kernel) */
-    typedef nmoe_stage<2, NMOE_MCHUNK, NT * nmoe_code_row<BITS, 1>::WPS> StageB;
-    typedef nmoe_stage<2, NMOE_SMALL_GPS * NMOE_SMALL_PASS, NT * nmoe_code_row<BITS, NMOE_SMALL_GPS>::WPS> StageS;
-    typedef nmoe_stage_buf<StageB, typename std::conditional<nmoe_small_form(NW), StageS, StageB>::type> StageU;
-    static_assert(sizeof(StageU) == nmoe_dn_stage_max(BITS, NW), "stage buffer size");
-    __shared__ StageU s_st0, s_st1, s_st2, s_st3;
-    __shared__ uint32_t s_q[NMOE_MCHUNK]; /* the chunk's output slots */
-    constexpr int NTILE = NMOE_HIDDEN / NT;
-    const int pl = blockIdx.x / (NMOE_EXPERTS * NTILE); /* pass lane, as in the gate/up kernel */
-    /* the tile's expert is the es-th by entries (most first), so the
-     * longest tiles start first */
-    int es, nt;
-    nmoe_die_tile(blockIdx.x % (NMOE_EXPERTS * NTILE), NTILE, es, nt);
+    typedef typename nmoe_dn_lds_types<BITS, NW, NT>::StageU StageU;
     const uint4 rk = rank[es]; /* clamped as in the gate/up kernel */
     const int e = (int)min(rk.x, (uint32_t)(NMOE_EXPERTS - 1));
     const uint32_t p0 = min(rk.y, (uint32_t)nrows), n = min(rk.z, (uint32_t)nrows - p0);
     if (n <= (uint32_t)(pl * NMOE_MCHUNK)) return;
+    static_assert(!WAIT || NS == 3, "the split prologue's waits are written for three stages");
     const int tid = threadIdx.x, lane = tid & 63, col = lane & 15, kb = lane >> 4;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint8_t *ex = pack + (size_t)e * L::expert_size;
@@ -1138,7 +1278,8 @@ nmoe_grouped_down_kernel(const uint8_t *pack, const uint16_t *ahi, const uint16_
             row_off[i] = (p0 + min(m0 + 8 * ((wave + NW * i) % (MCH / 8)) + (lane >> 3), n - 1)) *
                          (uint32_t)(NMOE_INTER * 2);
         const uint16_t *apl[2] = {ahi, alo};
-        auto issue = [&](int gs, int st) {
+        /* a stage's act rows (2 AI loads) and its codes (CP::PER_WAVE loads) */
+        auto issue_a = [&](int gs, int st) {
 #pragma unroll
             for (int pl = 0; pl < 2; pl++)
 #pragma unroll
@@ -1146,10 +1287,16 @@ nmoe_grouped_down_kernel(const uint8_t *pack, const uint16_t *ahi, const uint16_
                     const int j = wave + NW * i;
                     nmoe_stage_rows(stage(st).a[pl], apl[pl] + 64 * (GPS * gs + j / (MCH / 8)), row_off[i], j, lane);
                 }
+        };
+        auto issue_b = [&](int gs, int st) {
 #pragma unroll
             for (int i = 0; i < CP::PER_WAVE; i++)
                 nmoe_stage_codes<BITS, NT, CP::WIDE, GPS>(stage(st).b, cbase + nmoe_gwords<BITS>() * GPS * gs,
                                                           Q::WPR_D, CP::PER_WAVE * wave + i, lane);
+        };
+        auto issue = [&](int gs, int st) {
+            issue_a(gs, st);
+            issue_b(gs, st);
         };
         const int nb = (int)min((n - m0 + 15) / 16, (uint32_t)MB);
         nmoe_f32x4 acc[NB][MB];
@@ -1160,20 +1307,56 @@ nmoe_grouped_down_kernel(const uint8_t *pack, const uint16_t *ahi, const uint16_
              * leaves only the stages in flight.
              * A lane = (entry col, groups 2kb + tq), B lane = (row col,
              * groups 2kb + tq) */
-            static_assert(NT * G / 8 == 64 * NW, "one scale chunk per thread");
-            __builtin_amdgcn_global_load_lds(
-                (const void *)((const uint4 *)(ex + L::down_s + (size_t)nt * NT * G * 2) + tid),
-                (nmoe_lds_void *)((uint4 *)&s_s[0][0] + 64 * wave), 16, 0, 0);
+            static_assert(NT * G / 8 % 64 == 0 && NT * G / 8 <= 64 * NW, "at most one scale chunk per thread");
+            if (NT * G / 8 == 64 * NW || tid < NT * G / 8) /* wavefront-uniform */
+                __builtin_amdgcn_global_load_lds(
+                    (const void *)((const uint4 *)(ex + L::down_s + (size_t)nt * NT * G * 2) + tid),
+                    (nmoe_lds_void *)((uint4 *)&s_s[0][0] + 64 * wave), 16, 0, 0);
             float2 av[MB];
             uint32_t bv[NB];
+            auto load_av = [&]() {
 #pragma unroll
-            for (int mb = 0; mb < MB; mb++)
-                av[mb] = *(const float2 *)(as + (size_t)(p0 + min(m0 + 16 * mb + col, n - 1)) * G + 2 * kb);
+                for (int mb = 0; mb < MB; mb++) {
+                    const float *ap = as + (size_t)(p0 + min(m0 + 16 * mb + col, n - 1)) * G + 2 * kb;
+                    if constexpr (WAIT)
+                        av[mb] = __builtin_bit_cast(float2, __hip_atomic_load((nmoe_g64 *)ap, __ATOMIC_RELAXED,
+                                                                              __HIP_MEMORY_SCOPE_AGENT));
+                    else
+                        av[mb] = *(const float2 *)ap;
+                }
+            };
+            if constexpr (WAIT) {
+                /* the weights first (they do not wait for the gate/up
+                 * tiles): biases and the first stages' codes; then, on the
+                 * first pass, the wait for the expert's gate/up tiles (a
+                 * barrier that leaves the loads in flight); then the act
+                 * side: group sums and the first stages' act rows.  The wait
+                 * below leaves only stage 1's act rows in flight, so stage 0
+                 * is complete before the ring's first step. */
 #pragma unroll
-            for (int b2 = 0; b2 < NB; b2++) bv[b2] = *(const uint32_t *)(bias + (rt0 + 16 * b2) * G + 2 * kb);
+                for (int b2 = 0; b2 < NB; b2++) bv[b2] = *(const uint32_t *)(bias + (rt0 + 16 * b2) * G + 2 * kb);
 #pragma unroll
-            for (int st = 0; st < NS - 1; st++) issue(st, st);
-            nmoe_wait_vm<(NS - 1) * (2 * AI + CP::PER_WAVE)>();
+                for (int st = 0; st < NS - 1; st++) issue_b(st, st);
+                if (m0 == (uint32_t)(pl * MCH)) {
+                    if (tid == 0) {
+                        const uint32_t busy = min((uint32_t)lanes, (n + NMOE_MCHUNK - 1) / NMOE_MCHUNK);
+                        nmoe_wait_tiles(done + es, (uint32_t)gu_tiles * busy, sync, spin);
+                        nmoe_gtl_stamp(tl, NMOE_GTL_READY);
+                    }
+                    nmoe_lds_barrier();
+                }
+                load_av();
+#pragma unroll
+                for (int st = 0; st < NS - 1; st++) issue_a(st, st);
+                nmoe_wait_vm<(NS - 2) * 2 * AI>();
+            } else {
+                load_av();
+#pragma unroll
+                for (int b2 = 0; b2 < NB; b2++) bv[b2] = *(const uint32_t *)(bias + (rt0 + 16 * b2) * G + 2 * kb);
+#pragma unroll
+                for (int st = 0; st < NS - 1; st++) issue(st, st);
+                nmoe_wait_vm<(NS - 1) * (2 * AI + CP::PER_WAVE)>();
+            }
             if (tid < MCH) s_q[tid] = qv;
             nmoe_lds_barrier(); /* the scales and s_q */
             float cv[NB][G / 4];
@@ -1264,6 +1447,102 @@ nmoe_grouped_down_kernel(const uint8_t *pack, const uint16_t *ahi, const uint16_
     run(std::integral_constant<int, NMOE_MCHUNK>{}, std::integral_constant<int, 1>{});
 }
 
+template <int BITS, int NW>
+__global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
+nmoe_grouped_down_kernel(const uint8_t *pack, const uint16_t *ahi, const uint16_t *alo, const float *as,
+                         const uint32_t *perm, const uint4 *rank, int lanes, int nrows, float *y, uint64_t *tl) {
+    nmoe_gtl_begin(tl);
+    constexpr int NT = nmoe_dn_rows(NW);
+    typedef nmoe_dn_lds_types<BITS, NW, NT> T;
+    __shared__ typename T::Scales s_s;
+    __shared__ typename T::StageU s_st0, s_st1, s_st2, s_st3;
+    __shared__ uint32_t s_q[NMOE_MCHUNK]; /* the chunk's output slots */
+    /* pass lane and tile as in the gate/up kernel */
+    constexpr int NTILE = NMOE_HIDDEN / NT;
+    const int pl = blockIdx.x / (NMOE_EXPERTS * NTILE);
+    int es, nt;
+    nmoe_die_tile(blockIdx.x % (NMOE_EXPERTS * NTILE), NTILE, es, nt);
+    nmoe_dn_tile<BITS, NW, NT, nmoe_dn_stages(BITS, NW), false>(pack, ahi, alo, as, perm, rank, lanes, nrows, y, es,
+                                                                nt, pl, s_s, s_st0, s_st1, s_st2, s_st3, s_q, NULL, 0,
+                                                                NULL, 0u, NULL);
+    nmoe_gtl_end(tl, 2, rank, es, nt, pl, nrows);
+}
+
+/* ------------------------------------------------------------ gate/up + down in one launch */
+
+/* Rows of a down tile when the down tiles share the launch with the gate/up
+ * tiles: 32 a wavefront, so that a stage of either GEMM fits one stage
+ * buffer and two blocks still share a CU. */
+__host__ __device__ constexpr int nmoe_ffn_dn_rows(int nw) { return nw * 32; }
+__host__ __device__ constexpr int nmoe_imax(int a, int b) { return a > b ? a : b; }
+/* LDS bytes of the one-launch block with ns stages: stage buffers and
+ * scales of either GEMM, s_tok (s_q) and s_as. */
+__host__ __device__ constexpr int nmoe_ffn_lds(int bits, int xpl, int nw, int ns) {
+    return ns * nmoe_imax(nmoe_gu_stage_max(bits, xpl, nw), nmoe_dn_stage_max(bits, nw, nmoe_ffn_dn_rows(nw))) +
+           nmoe_imax(2 * nmoe_gu_rows(xpl, nw) * 64, nmoe_ffn_dn_rows(nw) * 16) + 4 * NMOE_MCHUNK * (1 + nw);
+}
+__host__ __device__ constexpr int nmoe_ffn_stages(int bits, int xpl, int nw) {
+    return nmoe_ffn_lds(bits, xpl, nw, 4) <= (nw == 8 ? 160 : 80) * 1024 - 512 ? 4 : 3;
+}
+
+/* Gate/up and down of the grouped experts in one launch (one pass lane):
+ * blocks 0 .. ngu-1 are the gate/up tiles (as nmoe_grouped_gateup_kernel's
+ * grid), the blocks after them the down tiles of nmoe_ffn_dn_rows(NW) rows
+ * (as nmoe_grouped_down_kernel's grid, from block ngu on).  A down tile
+ * waits (bounded) for its expert's gate/up tiles, which count themselves in
+ * done[] (zeroed by the preparation launch), so the down tiles of the
+ * experts finished first fill the CUs that the last gate/up tiles leave
+ * idle, instead of waiting for the whole gate/up launch to end.
+ *
+ * Where the tiles run: blocks are dealt to the eight dies in turn, block b
+ * to die (b + c) mod 8 with c fixed within the launch (checked at context
+ * creation, else this kernel is not used), and ngu is a multiple of 8, so
+ * the gate/up and down tiles of one expert (the same block index mod 8) run
+ * on one die and its L2 holds their act rows (nmoe_wait_tiles checks it).
+ * A die starts its blocks in index order, so every gate/up block a down
+ * block waits for has started before it, and gate/up blocks wait for
+ * nothing: each wait ends. */
+template <int BITS, int XPL, int NW>
+__global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
+nmoe_grouped_ffn_kernel(const uint8_t *pack, const uint16_t *xhi, const uint16_t *xlo, const uint16_t *xs3,
+                        const uint32_t *perm, const uint4 *rank, int k, int nrows, uint16_t *ahi, uint16_t *alo,
+                        float *as, float *y, int ngu, uint32_t *done, uint32_t *sync, uint32_t spin, uint64_t *tl) {
+    nmoe_gtl_begin(tl);
+    typedef nmoe_gu_lds_types<BITS, XPL, NW> TG;
+    constexpr int NTD = nmoe_ffn_dn_rows(NW);
+    typedef nmoe_dn_lds_types<BITS, NW, NTD> TD;
+    constexpr int NS = nmoe_ffn_stages(BITS, XPL, NW);
+    union StageV {
+        typename TG::StageU gu;
+        typename TD::StageU dn;
+    };
+    union ScalesV {
+        typename TG::Scales gu;
+        typename TD::Scales dn;
+    };
+    static_assert(sizeof(StageV) * NS + sizeof(ScalesV) + 4 * NMOE_MCHUNK * (1 + NW) ==
+                      (size_t)nmoe_ffn_lds(BITS, XPL, NW, NS),
+                  "LDS size");
+    __shared__ ScalesV s_s;
+    __shared__ StageV s_st0, s_st1, s_st2, s_st3;
+    __shared__ uint32_t s_tok[NMOE_MCHUNK]; /* the gate/up tile's tokens, the down tile's output slots */
+    __shared__ float s_as[NW][NMOE_MCHUNK];
+    constexpr int NTG = NMOE_INTER / TG::NT, NTILED = NMOE_HIDDEN / NTD;
+    int es, nt;
+    if ((int)blockIdx.x < ngu) {
+        nmoe_die_tile(blockIdx.x, NTG, es, nt);
+        nmoe_gu_tile<BITS, XPL, NW, NS, true>(pack, xhi, xlo, xs3, perm, rank, k, 1, nrows, ahi, alo, as, es, nt, 0,
+                                              s_s.gu, s_st0.gu, s_st1.gu, s_st2.gu, s_st3.gu, s_tok, s_as, done);
+        nmoe_gtl_end(tl, 1, rank, es, nt, 0, nrows);
+    } else {
+        nmoe_die_tile(blockIdx.x - ngu, NTILED, es, nt);
+        nmoe_dn_tile<BITS, NW, NTD, NS, true>(pack, ahi, alo, as, perm, rank, 1, nrows, y, es, nt, 0, s_s.dn,
+                                              s_st0.dn, s_st1.dn, s_st2.dn, s_st3.dn, s_tok, done, NTG, sync, spin,
+                                              tl);
+        nmoe_gtl_end(tl, 2, rank, es, nt, 0, nrows);
+    }
+}
+
 /* ------------------------------------------------------------ combine */
 
 /* out[t] = h_mid[t] + sum_{s<k} w[t][s] y[t*k+s] in slot order
@@ -1342,14 +1621,18 @@ extern "C" int nmoe_grouped_init(nmoe_hip_ctx *ctx) {
         hipMalloc((void **)&ctx->g_ahi, rows * NMOE_INTER * sizeof(uint16_t)) != hipSuccess ||
         hipMalloc((void **)&ctx->g_alo, rows * NMOE_INTER * sizeof(uint16_t)) != hipSuccess ||
         hipMalloc((void **)&ctx->g_as, rows * (NMOE_INTER / NMOE_GROUP) * sizeof(float)) != hipSuccess ||
-        hipMalloc((void **)&ctx->g_y, rows * NMOE_HIDDEN * sizeof(float)) != hipSuccess)
+        hipMalloc((void **)&ctx->g_y, rows * NMOE_HIDDEN * sizeof(float)) != hipSuccess ||
+        hipMalloc((void **)&ctx->g_done, NMOE_SCHED_WORDS * sizeof(uint32_t)) != hipSuccess)
         return NMOE_HIP_ENOMEM;
+    ctx->grouped_one_launch = ctx->xcd_placed;
+    ctx->skew_tiles = -1;
     /* the dispatch's words start in range: a launch whose slices' meeting
      * gives up then reads zeros, never uninitialised counts */
     if (hipMemset(ctx->g_counts, 0, NMOE_DISPATCH_MAX * (NMOE_EXPERTS + 1) * sizeof(uint32_t)) != hipSuccess ||
         hipMemset(ctx->g_perm, 0, rows * sizeof(uint32_t)) != hipSuccess ||
         hipMemset(ctx->g_offsets, 0, (NMOE_EXPERTS + 1) * sizeof(uint32_t)) != hipSuccess ||
         hipMemset(ctx->g_rank, 0, NMOE_EXPERTS * 4 * sizeof(uint32_t)) != hipSuccess ||
+        hipMemset(ctx->g_done, 0, NMOE_SCHED_WORDS * sizeof(uint32_t)) != hipSuccess ||
         hipDeviceSynchronize() != hipSuccess)
         return NMOE_HIP_EHIP;
     return NMOE_HIP_OK;
@@ -1357,7 +1640,7 @@ extern "C" int nmoe_grouped_init(nmoe_hip_ctx *ctx) {
 
 extern "C" void nmoe_grouped_free(nmoe_hip_ctx *ctx) {
     void *p[] = {ctx->g_counts, ctx->g_perm, ctx->g_offsets, ctx->g_rank, ctx->g_xhi, ctx->g_xlo,
-                 ctx->g_xs,     ctx->g_ahi,  ctx->g_alo,     ctx->g_as,   ctx->g_y};
+                 ctx->g_xs,     ctx->g_ahi,  ctx->g_alo,     ctx->g_as,   ctx->g_y,   ctx->g_done};
     for (void *q : p)
         if (q != NULL) (void)hipFree(q);
 }
@@ -1369,7 +1652,7 @@ extern "C" int nmoe_grouped_dispatch(nmoe_hip_ctx *ctx, const uint32_t *idx, int
     hipLaunchKernelGGL((nmoe_grouped_prep_kernel<4, uint16_t, false>), dim3(nd), dim3(256), 0, s, idx, ntok, k, nd,
                        ctx->g_counts, perm, offsets, (uint4 *)ctx->g_rank, ctx->sync, ctx->spin_limit,
                        (const uint16_t *)NULL, (uint16_t *)NULL, (uint16_t *)NULL, (uint16_t *)NULL,
-                       (const float *)NULL, (uint32_t *)NULL, (float *)NULL);
+                       (const float *)NULL, (uint32_t *)NULL, (float *)NULL, (uint32_t *)NULL, -1);
     const hipError_t e = hipGetLastError();
     return e == hipSuccess ? NMOE_HIP_OK : nmoe_hip_check(ctx, e, "dispatch launch");
 }
@@ -1385,10 +1668,20 @@ static int nmoe_grouped_run(nmoe_hip_ctx *ctx, const uint8_t *pack, const void *
     const dim3 gprep(nd + (logits != NULL ? (ntok + 3) / 4 : 0) + ntok);
     uint32_t *ri = (uint32_t *)idx;
     float *rw = (float *)w;
+    /* two pass lanes once an expert averages more than half a pass: the
+     * passes of a large expert's tile then run in blocks of their own, side
+     * by side (on the same die, so the second reads the codes from L2) */
+    const int lanes = (long)ntok * k > (long)NMOE_EXPERTS * NMOE_MCHUNK / 2 ? 2 : 1;
+    /* gate/up and down in one launch where the blocks' dies are known (one
+     * pass lane) */
+    const bool one = ctx->grouped_one_launch && ctx->xcd_placed && lanes == 1;
+    uint32_t *done = one ? ctx->g_done : NULL;
+    const int skew = one ? ctx->skew_tiles : -1;
+    if (one) ctx->skew_tiles = -1;
 #define NMOE_PREP(XT, R, XLO)                                                                                         \
     hipLaunchKernelGGL((nmoe_grouped_prep_kernel<BITS, XT, R>), gprep, dim3(256), 0, s, idx, ntok, k, nd, ctx->g_counts, \
                        ctx->g_perm, ctx->g_offsets, (uint4 *)ctx->g_rank, ctx->sync, ctx->spin_limit, (const XT *)x,  \
-                       ctx->g_xhi, XLO, ctx->g_xs, logits, ri, rw)
+                       ctx->g_xhi, XLO, ctx->g_xs, logits, ri, rw, done, skew)
     if (logits != NULL) {
         if (bf)
             NMOE_PREP(uint16_t, true, (uint16_t *)NULL);
@@ -1403,10 +1696,6 @@ static int nmoe_grouped_run(nmoe_hip_ctx *ctx, const uint8_t *pack, const void *
 #undef NMOE_PREP
     constexpr int NW = NMOE_GROUPED_NW;
     const dim3 blk(64 * NW);
-    /* two pass lanes once an expert averages more than half a pass: the
-     * passes of a large expert's tile then run in blocks of their own, side
-     * by side (on the same die, so the second reads the codes from L2) */
-    const int lanes = (long)ntok * k > (long)NMOE_EXPERTS * NMOE_MCHUNK / 2 ? 2 : 1;
     const dim3 ggu(lanes * NMOE_EXPERTS * (NMOE_INTER / nmoe_gu_rows(bf ? 1 : 2, NW))),
         gdn(lanes * NMOE_EXPERTS * (NMOE_HIDDEN / nmoe_dn_rows(NW)));
     const uint16_t *xhi = (const uint16_t *)ctx->g_xhi, *xlo = (const uint16_t *)ctx->g_xlo;
@@ -1416,15 +1705,32 @@ static int nmoe_grouped_run(nmoe_hip_ctx *ctx, const uint8_t *pack, const void *
     const uint16_t *xs3 = ctx->g_xs;
     const float *as = (const float *)ctx->g_as;
     const int nrows = ntok * k;
-    /* gate/up, then down */
-    if (bf)
-        hipLaunchKernelGGL((nmoe_grouped_gateup_kernel<BITS, 1, NW>), ggu, blk, 0, s, pack, xhi, xlo, xs3, perm, rank, k,
-                           lanes, nrows, ctx->g_ahi, ctx->g_alo, ctx->g_as);
-    else
-        hipLaunchKernelGGL((nmoe_grouped_gateup_kernel<BITS, 2, NW>), ggu, blk, 0, s, pack, xhi, xlo, xs3, perm, rank, k,
-                           lanes, nrows, ctx->g_ahi, ctx->g_alo, ctx->g_as);
-    hipLaunchKernelGGL((nmoe_grouped_down_kernel<BITS, NW>), gdn, blk, 0, s, pack, ahi, alo, as, perm, rank, lanes,
-                       nrows, ctx->g_y);
+    /* timeline builds: 4 stamps a block of the GEMM launches */
+    const dim3 gffn(ggu.x + NMOE_EXPERTS * (NMOE_HIDDEN / nmoe_ffn_dn_rows(NW)));
+    const size_t tl_recs = one ? gffn.x : ggu.x + gdn.x;
+    const int tl_slots = (int)((4 * tl_recs + NMOE_TL_SLOT_WORDS - 1) / NMOE_TL_SLOT_WORDS);
+    uint64_t *tl = nmoe_tl_take(ctx, tl_slots);
+    if (one) {
+        /* gate/up tiles, then the down tiles of nmoe_ffn_dn_rows rows, in one grid */
+        if (bf)
+            hipLaunchKernelGGL((nmoe_grouped_ffn_kernel<BITS, 1, NW>), gffn, blk, 0, s, pack, xhi, xlo, xs3, perm, rank,
+                               k, nrows, ctx->g_ahi, ctx->g_alo, ctx->g_as, ctx->g_y, (int)ggu.x, done, ctx->sync,
+                               ctx->spin_limit, tl);
+        else
+            hipLaunchKernelGGL((nmoe_grouped_ffn_kernel<BITS, 2, NW>), gffn, blk, 0, s, pack, xhi, xlo, xs3, perm, rank,
+                               k, nrows, ctx->g_ahi, ctx->g_alo, ctx->g_as, ctx->g_y, (int)ggu.x, done, ctx->sync,
+                               ctx->spin_limit, tl);
+    } else {
+        /* gate/up, then down */
+        if (bf)
+            hipLaunchKernelGGL((nmoe_grouped_gateup_kernel<BITS, 1, NW>), ggu, blk, 0, s, pack, xhi, xlo, xs3, perm,
+                               rank, k, lanes, nrows, ctx->g_ahi, ctx->g_alo, ctx->g_as, tl);
+        else
+            hipLaunchKernelGGL((nmoe_grouped_gateup_kernel<BITS, 2, NW>), ggu, blk, 0, s, pack, xhi, xlo, xs3, perm,
+                               rank, k, lanes, nrows, ctx->g_ahi, ctx->g_alo, ctx->g_as, tl);
+        hipLaunchKernelGGL((nmoe_grouped_down_kernel<BITS, NW>), gdn, blk, 0, s, pack, ahi, alo, as, perm, rank, lanes,
+                           nrows, ctx->g_y, tl == NULL ? tl : tl + 4 * (size_t)ggu.x);
+    }
     const uint32_t *status = ctx->sync + NMOE_SYNC_STATUS;
     if (nmoe_aligned(h_mid, 16) && nmoe_aligned(out, 16) && (shared_out == NULL || nmoe_aligned(shared_out, 16)))
         hipLaunchKernelGGL(nmoe_grouped_combine_kernel, dim3(NMOE_HIDDEN / 1024, ntok), dim3(256), 0, s,

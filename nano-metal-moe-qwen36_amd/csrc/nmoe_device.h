@@ -462,6 +462,13 @@ __device__ __forceinline__ uint32_t nmoe_add_u32_dev(uint32_t *p, uint32_t v) {
     return __hip_atomic_fetch_add((nmoe_g32 *)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+/* Accelerator die (XCC) the calling wave runs on. */
+__device__ __forceinline__ uint32_t nmoe_xcc_id() {
+    uint32_t v;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID, 0, 4)" : "=s"(v));
+    return v;
+}
+
 /* Values exchanged between the blocks of one launch travel as 64-bit words
  * (launch epoch << 32 | float bits), written and read whole with one
  * device-coherent access: a consumer polls the data itself until every word

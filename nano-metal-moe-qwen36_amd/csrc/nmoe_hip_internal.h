@@ -87,6 +87,9 @@ struct nmoe_buf_entry {
 #define NMOE_TIMELINE 0
 #endif
 #define NMOE_TL_EVENTS 16
+/* one timeline slot: the stamps of one fused launch (256 blocks x 16
+ * events), or of 1,024 blocks of a grouped GEMM launch (4 words each) */
+#define NMOE_TL_SLOT_WORDS (256 * NMOE_TL_EVENTS)
 
 struct nmoe_hip_ctx {
     int device;
@@ -118,6 +121,9 @@ struct nmoe_hip_ctx {
     int tl_slots, tl_next;
     /* grouped (matrix-core) path for many tokens, sized for max_tokens */
     int grouped_min_tokens; /* NMOE_HIP_OPT_GROUPED_MIN_TOKENS */
+    int grouped_one_launch; /* NMOE_HIP_OPT_GROUPED_ONE_LAUNCH */
+    int skew_tiles;         /* NMOE_HIP_OPT_SKEW_TILES: rank, or -1 */
+    uint32_t *g_done;       /* [256] the one-launch form's gate/up tiles done per expert rank */
     uint32_t *g_counts;     /* [64][257] per-block expert histograms */
     uint32_t *g_perm;       /* [T*8] entries grouped by expert */
     uint32_t *g_offsets;    /* [257] */
@@ -140,6 +146,9 @@ int nmoe_fail(nmoe_hip_ctx *ctx, int code, const char *fmt, ...);
  * otherwise returns NMOE_HIP_OK at once. */
 extern "C" int nmoe_sync_check(nmoe_hip_ctx *ctx, void *stream);
 int nmoe_hip_check(nmoe_hip_ctx *ctx, hipError_t e, const char *what);
+/* The next n timeline slots of the context (NMOE_TIMELINE builds; NULL
+ * when no timeline buffer is set). */
+uint64_t *nmoe_tl_take(nmoe_hip_ctx *ctx, int n);
 
 #define NMOE_HIP_TRY(ctx, call)                                   \
     do {                                                          \

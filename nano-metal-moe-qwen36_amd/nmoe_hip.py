@@ -55,6 +55,8 @@ OPT_SPIN_LIMIT = 4
 OPT_SYNC_CHECK = 5
 OPT_SKEW_EPOCH = 6
 OPT_STACK_LOOP = 7
+OPT_GROUPED_ONE_LAUNCH = 8
+OPT_SKEW_TILES = 9
 
 # q4 / q2 component offsets (scripts/convert_qwen36.py:38-64)
 OFFSETS = {
@@ -263,6 +265,15 @@ class Context:
     def set_grouped_min_tokens(self, n: int):
         """Calls with at least n tokens run the grouped (matrix-core) path."""
         self._check(lib().nmoe_hip_set_option(self.h, OPT_GROUPED_MIN_TOKENS, int(n)))
+
+    def set_grouped_one_launch(self, on: bool) -> bool:
+        """Gate/up and down of the grouped path in one launch (on) or two;
+        False when the device does not allow the one-launch form."""
+        rc = lib().nmoe_hip_set_option(self.h, OPT_GROUPED_ONE_LAUNCH, int(bool(on)))
+        if rc != OK and on:
+            return False
+        self._check(rc)
+        return True
 
     def dispatch(self, idx, ntok: int, k: int, perm, offsets, stream=None) -> int:
         return lib().nmoe_moe_dispatch(self.h, _ptr(idx), ntok, k, _ptr(perm), _ptr(offsets), stream)

@@ -576,6 +576,33 @@ def test_dispatch_long_slices(nh):
         c.close()
 
 
+def gemm_forms(big):
+    """The grouped path's GEMM forms the device runs: gate/up and down in one
+    launch (which needs the round-robin die placement checked at create) and
+    in two."""
+    forms = [(name, one) for name, one in (("one launch", True), ("two launches", False))
+             if big.set_grouped_one_launch(one)]
+    big.set_grouped_one_launch(True)
+    return forms
+
+
+def run_forms(big, fn):
+    """fn() under each GEMM form; the outputs (arrays) must be the same bits
+    in every form (each output element takes the same arithmetic whatever
+    the tile it falls in).  Returns the first form's."""
+    outs = []
+    try:
+        for name, one in gemm_forms(big):
+            big.set_grouped_one_launch(one)
+            outs.append((name, fn()))
+    finally:
+        big.set_grouped_one_launch(True)
+    for name, o in outs[1:]:
+        for a, b in zip(outs[0][1], o):
+            np.testing.assert_array_equal(a.view(np.uint32), b.view(np.uint32), err_msg=f"{outs[0][0]} vs {name}")
+    return outs[0][1]
+
+
 @pytest.mark.parametrize("bits", [4, 2])
 @pytest.mark.parametrize("ntok,k,xkind,ikind", [(8, 8, "bf16", "uniform"), (64, 8, "bf16", "zipf"),
                                                (64, 6, "f32", "zipf"), (40, 8, "f32", "uniform")])
@@ -609,13 +636,20 @@ def test_grouped_experts_against_oracle(big, nh, bits, ntok, k, xkind, ikind):
     pack = host_pack(bits, seed, layer, idx_eff[:, :k].ravel())
     want = B.moe_experts(pack, bits, x, k, idx_eff, w_eff, h, sh, gr)
     d = [big.to_device(a) for a in (xdev, idx, w, h, sh, gr)]
-    outs = {}
-    for path, nmin in (("grouped", 1), ("per-token", 1 << 20)):
-        big.set_grouped_min_tokens(nmin)
+
+    def run():
         out = big.alloc(ntok * 2048 * 4)
         big._check(big.experts(bits, layer, d[0], dt, ntok, k, d[1], d[2], d[3], out, d[4], d[5]))
-        outs[path] = out.download(np.float32, (ntok, 2048))
-    big.set_grouped_min_tokens(8)
+        return (out.download(np.float32, (ntok, 2048)),)
+
+    outs = {}
+    try:
+        big.set_grouped_min_tokens(1)
+        outs["grouped"] = run_forms(big, run)[0]
+        big.set_grouped_min_tokens(1 << 20)
+        outs["per-token"] = run()[0]
+    finally:
+        big.set_grouped_min_tokens(8)
     assert big.device_status() == nh.OK
     for path, got in outs.items():
         assert_close(got, want, what=f"{path} q{bits} ntok={ntok} k={k} x={xkind}")
@@ -653,12 +687,17 @@ def test_grouped_small_and_big_forms(big, nh, bits, xkind):
         x, xdev, dt = xf, xf, nh.F32
     h = rng.standard_normal((ntok, 2048)).astype(np.float32)
     d = [big.to_device(a) for a in (xdev, idx, w, h)]
-    out = big.alloc(ntok * 2048 * 4)
-    big._check(big.experts(bits, layer, d[0], dt, ntok, k, d[1], d[2], d[3], out))
+
+    def run():
+        out = big.alloc(ntok * 2048 * 4)
+        big._check(big.experts(bits, layer, d[0], dt, ntok, k, d[1], d[2], d[3], out))
+        return (out.download(np.float32, (ntok, 2048)),)
+
+    got = run_forms(big, run)[0]
     assert big.device_status() == nh.OK
     pack = host_pack(bits, seed, layer, idx[:, :k].ravel())
     want = B.moe_experts(pack, bits, x, k, idx, w, h)
-    assert_close(out.download(np.float32, (ntok, 2048)), want, what=f"small/big forms q{bits} x={xkind}")
+    assert_close(got, want, what=f"small/big forms q{bits} x={xkind}")
 
 
 @pytest.mark.parametrize("bits", [4, 2])
@@ -674,17 +713,21 @@ def test_prefill_2048_sampled(big, nh, bits):
     x = B.bf16_to_f32(xb).reshape(ntok, 2048)
     h = rng.standard_normal((ntok, 2048)).astype(np.float32)
     d_lg, d_x, d_h = big.to_device(logits), big.to_device(xb), big.to_device(h)
-    d_idx, d_w, out = big.alloc(ntok * 32), big.alloc(ntok * 32), big.alloc(ntok * 2048 * 4)
-    big._check(big.topk(d_lg, ntok, 256, k, d_idx, d_w))
-    big._check(big.experts(bits, layer, d_x, nh.BF16, ntok, k, d_idx, d_w, d_h, out))
-    idx = d_idx.download(np.uint32, (ntok, 8))
-    w = d_w.download(np.float32, (ntok, 8))
+
+    def run():
+        d_idx, d_w, out = big.alloc(ntok * 32), big.alloc(ntok * 32), big.alloc(ntok * 2048 * 4)
+        big._check(big.topk(d_lg, ntok, 256, k, d_idx, d_w))
+        big._check(big.experts(bits, layer, d_x, nh.BF16, ntok, k, d_idx, d_w, d_h, out))
+        return d_idx.download(np.uint32, (ntok, 8)), d_w.download(np.float32, (ntok, 8)), \
+            out.download(np.float32, (ntok, 2048))
+
+    idx, w, full = run_forms(big, run)
     sample = rng.choice(ntok, 48, replace=False)
     for t in range(ntok):  # every token's routing
         oi, ow, _ = B.route(logits[t], k)
         np.testing.assert_array_equal(idx[t], oi, err_msg=f"t={t}")
         np.testing.assert_array_equal(w[t].view(np.uint32), ow.view(np.uint32), err_msg=f"t={t}")
-    got = out.download(np.float32, (ntok, 2048))[sample]
+    got = full[sample]
     pack = host_pack(bits, seed, layer, idx[sample, :k].ravel())
     want = B.moe_experts(pack, bits, x[sample], k, idx[sample], w[sample], h[sample])
     assert big.device_status() == nh.OK
@@ -779,11 +822,16 @@ def test_grouped_zipf_1200_sampled(big, nh, bits, xkind):
         x, xdev, dt = xf, xf, nh.F32
     h = rng.standard_normal((ntok, 2048)).astype(np.float32)
     d = [big.to_device(a) for a in (xdev, idx, w, h)]
-    out = big.alloc(ntok * 2048 * 4)
-    big._check(big.experts(bits, layer, d[0], dt, ntok, k, d[1], d[2], d[3], out))
+
+    def run():
+        out = big.alloc(ntok * 2048 * 4)
+        big._check(big.experts(bits, layer, d[0], dt, ntok, k, d[1], d[2], d[3], out))
+        return (out.download(np.float32, (ntok, 2048)),)
+
+    full = run_forms(big, run)[0]
     assert big.device_status() == nh.OK
     sample = np.concatenate([[3], rng.choice(np.arange(4, ntok), 39, replace=False)])
-    got = out.download(np.float32, (ntok, 2048))[sample]
+    got = full[sample]
     pack = host_pack(bits, seed, layer, idx_eff[sample, :k].ravel())
     want = B.moe_experts(pack, bits, x[sample], k, idx_eff[sample], w_eff[sample], h[sample])
     assert_close(got, want, what=f"zipf 1200 q{bits} x={xkind}")

@@ -154,6 +154,48 @@ def test_sync_check_returns_etimedout(nh):
         ctx._check(ctx.set_option(nh.OPT_SPIN_LIMIT, 0))
 
 
+def test_grouped_one_launch_wrong_tile_count_poisons_and_recovers(nh):
+    """The one-launch grouped form: a down tile checks that its expert's
+    gate/up tiles are all counted, each from this block's die.  With the
+    count of expert rank 0 started at an impossible value
+    (NMOE_HIP_OPT_SKEW_TILES), its down tiles find it wrong: the call's
+    outputs are NaN and the status reports ETIMEDOUT; the next call is the
+    same bits as the two-launch form's."""
+    rng = np.random.default_rng(77)
+    ntok, k, layer, bits = 64, 8, 4, 4
+    with nh.Context(0, max_tokens=ntok) as ctx:
+        if not ctx.set_grouped_one_launch(True):
+            pytest.skip("the one-launch form needs the round-robin die placement")
+        ctx.synth_layer(layer, bits, 11, 0.02)
+        idx = np.zeros((ntok, 8), np.uint32)
+        for t in range(ntok):
+            idx[t, :k] = rng.choice(256, k, replace=False)
+        idx[:40, 0] = 7  # rank 0: expert 7 with 40 entries
+        w = rng.dirichlet(np.ones(k), size=ntok).astype(np.float32)
+        x = rng.standard_normal((ntok, 2048)).astype(np.float32)
+        h = rng.standard_normal((ntok, 2048)).astype(np.float32)
+        d = [ctx.to_device(a) for a in (x, idx, w, h)]
+        out = ctx.alloc(ntok * 2048 * 4)
+
+        def run():
+            ctx._check(ctx.experts(bits, layer, d[0], nh.F32, ntok, k, d[1], d[2], d[3], out))
+            return out.download(np.float32, (ntok, 2048))
+
+        ctx.set_grouped_one_launch(False)
+        want = run()
+        assert ctx.device_status() == nh.OK
+        ctx.set_grouped_one_launch(True)
+        np.testing.assert_array_equal(run().view(np.uint32), want.view(np.uint32))
+        assert ctx.device_status() == nh.OK
+        ctx._check(ctx.set_option(nh.OPT_SKEW_TILES, 0))
+        bad = run()
+        assert ctx.device_status() == nh.ETIMEDOUT
+        assert np.isnan(bad).all()
+        np.testing.assert_array_equal(run().view(np.uint32), want.view(np.uint32))
+        assert ctx.device_status() == nh.OK
+        assert ctx.set_option(nh.OPT_SKEW_TILES, 256) == nh.EINVAL
+
+
 def test_option_arguments_validated(nh):
     with nh.Context(0, max_tokens=4) as ctx:
         assert ctx.set_option(nh.OPT_SPIN_LIMIT, -1) == nh.EINVAL
