@@ -241,7 +241,11 @@ __device__ __forceinline__ void nmoe_dispatch_scatter(const uint32_t *idx, int n
          * (63 and more together), a counting sort over the buckets, any
          * order within one (the GEMM blocks' results do not depend on their
          * order).  The GEMM blocks take the experts in this order, so the
-         * longest tiles start first and the launch's tail is short. */
+         * longest tiles start first and the launch's tail is short.  Entry
+         * es runs on die (es + c) mod 8, so each round of eight is dealt
+         * back and forth (0..7, then 7..0): dealt the same way every
+         * round, the same dies would take the larger expert of every round
+         * and finish last. */
         const int bk = 63 - (int)min((total + 15u) / 16u, 63u);
         if (tid < 64) s_bk[tid] = 0;
         __syncthreads();
@@ -258,7 +262,8 @@ __device__ __forceinline__ void nmoe_dispatch_scatter(const uint32_t *idx, int n
             s_bk[tid] = inc - c;
         }
         __syncthreads();
-        rank[atomicAdd(&s_bk[bk], 1u)] = make_uint4((uint32_t)tid, off, total, 0u);
+        const uint32_t pos = atomicAdd(&s_bk[bk], 1u), round = pos >> 3;
+        rank[8u * round + ((round & 1u) ? 7u - (pos & 7u) : (pos & 7u))] = make_uint4((uint32_t)tid, off, total, 0u);
     }
     s_base[tid] = off + before;
     for (int i = tid; i < 4 * (NMOE_EXPERTS + 1); i += 256) (&s_wc[0][0])[i] = 0;
@@ -727,6 +732,23 @@ __device__ __forceinline__ void nmoe_die_tile(int b, int ntiles, int &e, int &nt
     nt = (b >> 3) % ntiles;
 }
 
+/* Entry es of the expert order (expert, first entry, entries), written by
+ * the preparation launch and only read by the GEMM launches: one scalar
+ * 16-byte load, through the constant address space, all four words needed
+ * at once.  Read as a plain pointer, the compiler made it a vector load
+ * where it could not prove the words unchanged in the launch (it then
+ * waits in the CU's vector memory queue behind the stage loads of the
+ * CU's other block) and split it into two dependent loads around the
+ * empty-expert exit. */
+__device__ __forceinline__ uint4 nmoe_rank_entry(const uint4 *rank, int es) {
+    typedef uint32_t nmoe_v4u __attribute__((ext_vector_type(4)));
+    typedef const __attribute__((address_space(4))) nmoe_v4u nmoe_const_v4u;
+    const nmoe_v4u v = *(nmoe_const_v4u *)(uintptr_t)(rank + es);
+    uint32_t x = v.x, y = v.y, z = v.z, w = v.w;
+    asm volatile("" : "+s"(x), "+s"(y), "+s"(z), "+s"(w));
+    return make_uint4(x, y, z, w);
+}
+
 /* SiLU for the grouped path (outputs are checked to a tolerance there):
  * the exp of a non-positive argument as in math.m:21-28, the reciprocal by
  * v_rcp_f32 instead of a full division. */
@@ -872,7 +894,7 @@ __device__ __forceinline__ void nmoe_gu_tile(const uint8_t *pack, const uint16_t
     typedef typename nmoe_gu_lds_types<BITS, XPL, NW>::StageU StageU;
     /* (e, first entry, entries) of a dispatch whose meeting gave up can be
      * anything; the clamps keep every access inside the buffers */
-    const uint4 rk = rank[es];
+    const uint4 rk = nmoe_rank_entry(rank, es);
     const int e = (int)min(rk.x, (uint32_t)(NMOE_EXPERTS - 1));
     const uint32_t p0 = min(rk.y, (uint32_t)nrows), n = min(rk.z, (uint32_t)nrows - p0);
     if (n <= (uint32_t)(pl * NMOE_MCHUNK)) return;
@@ -1232,7 +1254,7 @@ __device__ __forceinline__ void nmoe_dn_tile(const uint8_t *pack, const uint16_t
     static_assert(NT % (16 * NW) == 0, "whole column blocks per wavefront");
     constexpr int NB = NT / (16 * NW);
     typedef typename nmoe_dn_lds_types<BITS, NW, NT>::StageU StageU;
-    const uint4 rk = rank[es]; /* clamped as in the gate/up kernel */
+    const uint4 rk = nmoe_rank_entry(rank, es); /* clamped as in the gate/up kernel */
     const int e = (int)min(rk.x, (uint32_t)(NMOE_EXPERTS - 1));
     const uint32_t p0 = min(rk.y, (uint32_t)nrows), n = min(rk.z, (uint32_t)nrows - p0);
     if (n <= (uint32_t)(pl * NMOE_MCHUNK)) return;
