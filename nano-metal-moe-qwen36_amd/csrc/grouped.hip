@@ -76,6 +76,9 @@ __host__ __device__ constexpr int nmoe_dispatch_blocks(int n) {
 #define NMOE_SMALL_PASS 16
 #define NMOE_SMALL_GPS 2
 __host__ __device__ constexpr bool nmoe_small_form(int nw) { return nw == 4; }
+/* Gate (and up) rows per block of NW wavefronts: 32 a wavefront for bf16 x
+ * (one A plane), 16 for fp32 x (hi + lo planes). */
+__host__ __device__ constexpr int nmoe_gu_rows(int xpl, int nw) { return nw * 32 / xpl; }
 
 /* k offset (within a lane's 16-k span) of operand element `slot`
  * (slot = 8 * slice + 2 * dword + half). */
@@ -188,6 +191,21 @@ __device__ __forceinline__ void nmoe_dispatch_count(const uint32_t *idx, int nto
     __syncthreads();
 }
 
+/* The down tiles' order of the one-launch GEMM: order entry es (round
+ * g = es / 8 of die d = es mod 8) goes to entry 8 j + d of a second list.
+ * A die's large experts (more than NMOE_SMALL_PASS entries, its first nb
+ * rounds) run the longest gate/up tiles, so their down tiles, taken first,
+ * would hold their slots waiting; they now come after half of the die's
+ * other experts whose gate/up tiles run in the first round of r1 experts
+ * (rounds nb .. nb + h - 1 first, then 0 .. nb - 1, then the rest). */
+__device__ __forceinline__ uint32_t nmoe_down_entry(uint32_t es, uint32_t nbig, uint32_t r1) {
+    const uint32_t d = es & 7u, g = es >> 3, r = nbig >> 3, m = nbig & 7u;
+    const uint32_t nb = r + (uint32_t)((r & 1u) ? d >= 8u - m : d < m); /* dealt as in the order */
+    const uint32_t h = r1 > nb ? (r1 - nb) / 2u : 0u;
+    const uint32_t j = g < nb ? h + g : g < nb + h ? g - nb : g;
+    return 8u * j + d;
+}
+
 /* D2: offsets (block 0 writes them) and the stable permutation of slice b
  * (the slices' histograms from counts, or from h when there is one slice):
  * chunks of 256 entries in order; within a chunk the rank of an entry is
@@ -196,10 +214,11 @@ __device__ __forceinline__ void nmoe_dispatch_count(const uint32_t *idx, int nto
 template <bool COH>
 __device__ __forceinline__ void nmoe_dispatch_scatter(const uint32_t *idx, int ntok, int k, uint32_t *counts,
                                                       const uint32_t *h, uint32_t *perm, uint32_t *offsets,
-                                                      uint4 *rank, int b, int nd, const uint32_t *ev) {
+                                                      uint4 *rank, int b, int nd, const uint32_t *ev, uint32_t r1) {
     __shared__ uint32_t s_base[NMOE_EXPERTS];
     __shared__ uint32_t s_scan[4]; /* the wavefronts' totals */
     __shared__ uint32_t s_bk[64]; /* the work buckets of the expert order */
+    __shared__ uint32_t s_nbig;   /* the experts of more than one small pass */
     __shared__ uint32_t s_wc[4][NMOE_EXPERTS + 1];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, n = ntok * k;
     const int per = (n + nd - 1) / nd;
@@ -260,10 +279,17 @@ __device__ __forceinline__ void nmoe_dispatch_scatter(const uint32_t *idx, int n
                 inc += lane >= d ? v : 0u;
             }
             s_bk[tid] = inc - c;
+            static_assert(NMOE_SMALL_PASS == 16, "bucket 62 holds the experts of one small pass");
+            if (tid == 62) s_nbig = inc - c;
         }
         __syncthreads();
+        /* the order (its fourth word: the entry itself), and the same
+         * entries in the down tiles' order after it */
         const uint32_t pos = atomicAdd(&s_bk[bk], 1u), round = pos >> 3;
-        rank[8u * round + ((round & 1u) ? 7u - (pos & 7u) : (pos & 7u))] = make_uint4((uint32_t)tid, off, total, 0u);
+        const uint32_t es = 8u * round + ((round & 1u) ? 7u - (pos & 7u) : (pos & 7u));
+        const uint4 ent = make_uint4((uint32_t)tid, off, total, es);
+        rank[es] = ent;
+        rank[NMOE_EXPERTS + nmoe_down_entry(es, s_nbig, r1)] = ent;
     }
     s_base[tid] = off + before;
     for (int i = tid; i < 4 * (NMOE_EXPERTS + 1); i += 256) (&s_wc[0][0])[i] = 0;
@@ -503,7 +529,11 @@ __global__ void __launch_bounds__(256) nmoe_grouped_prep_kernel(const uint32_t *
         }
         __syncthreads(); /* (the histograms are then read with device-coherent loads) */
     }
-    nmoe_dispatch_scatter<ROUTED>(idx, ntok, k, counts, h, perm, offsets, rank, b, nd, ev);
+    /* experts whose gate/up tiles fill one die's first round: 32 CUs a
+     * die, two four-wavefront blocks a CU (one of eight) */
+    constexpr uint32_t R1 =
+        (256u / NMOE_GROUPED_NW) / (uint32_t)(NMOE_INTER / nmoe_gu_rows(sizeof(XT) == 2 ? 1 : 2, NMOE_GROUPED_NW));
+    nmoe_dispatch_scatter<ROUTED>(idx, ntok, k, counts, h, perm, offsets, rank, b, nd, ev, R1);
 }
 
 /* ------------------------------------------------------------ stage ring */
@@ -807,9 +837,6 @@ __device__ __forceinline__ void nmoe_gtl_end(uint64_t *tl, int kind, const uint4
 
 /* ------------------------------------------------------------ gate/up */
 
-/* Gate (and up) rows per block of NW wavefronts: 32 a wavefront for bf16 x
- * (one A plane), 16 for fp32 x (hi + lo planes). */
-__host__ __device__ constexpr int nmoe_gu_rows(int xpl, int nw) { return nw * 32 / xpl; }
 
 /* Bytes of one gate/up stage with mch entries a pass and gps groups a step:
  * A rows (xpl planes x gps groups x mch rows x 128 B) and the codes of the
@@ -1362,7 +1389,8 @@ __device__ __forceinline__ void nmoe_dn_tile(const uint8_t *pack, const uint16_t
                 if (m0 == (uint32_t)(pl * MCH)) {
                     if (tid == 0) {
                         const uint32_t busy = min((uint32_t)lanes, (n + NMOE_MCHUNK - 1) / NMOE_MCHUNK);
-                        nmoe_wait_tiles(done + es, (uint32_t)gu_tiles * busy, sync, spin);
+                        /* the entry's fourth word: its place in the gate/up order */
+                        nmoe_wait_tiles(done + (rk.w & (NMOE_EXPERTS - 1)), (uint32_t)gu_tiles * busy, sync, spin);
                         nmoe_gtl_stamp(tl, NMOE_GTL_READY);
                     }
                     nmoe_lds_barrier();
@@ -1510,17 +1538,20 @@ __host__ __device__ constexpr int nmoe_ffn_stages(int bits, int xpl, int nw) {
 /* Gate/up and down of the grouped experts in one launch (one pass lane):
  * blocks 0 .. ngu-1 are the gate/up tiles (as nmoe_grouped_gateup_kernel's
  * grid), the blocks after them the down tiles of nmoe_ffn_dn_rows(NW) rows
- * (as nmoe_grouped_down_kernel's grid, from block ngu on).  A down tile
+ * (as nmoe_grouped_down_kernel's grid, from block ngu on, over the second
+ * list of rank[]: the down tiles' order, nmoe_down_entry).  A down tile
  * waits (bounded) for its expert's gate/up tiles, which count themselves in
- * done[] (zeroed by the preparation launch), so the down tiles of the
- * experts finished first fill the CUs that the last gate/up tiles leave
- * idle, instead of waiting for the whole gate/up launch to end.
+ * done[] (zeroed by the preparation launch) at the expert's gate/up entry,
+ * so the down tiles of the experts finished first fill the CUs that the
+ * last gate/up tiles leave idle, instead of waiting for the whole gate/up
+ * launch to end.
  *
  * Where the tiles run: blocks are dealt to the eight dies in turn, block b
  * to die (b + c) mod 8 with c fixed within the launch (checked at context
  * creation, else this kernel is not used), and ngu is a multiple of 8, so
- * the gate/up and down tiles of one expert (the same block index mod 8) run
- * on one die and its L2 holds their act rows (nmoe_wait_tiles checks it).
+ * the gate/up and down tiles of one expert (the same entry mod 8 in either
+ * order) run on one die and its L2 holds their act rows (nmoe_wait_tiles
+ * checks it).
  * A die starts its blocks in index order, so every gate/up block a down
  * block waits for has started before it, and gate/up blocks wait for
  * nothing: each wait ends. */
@@ -1557,11 +1588,12 @@ nmoe_grouped_ffn_kernel(const uint8_t *pack, const uint16_t *xhi, const uint16_t
                                               s_s.gu, s_st0.gu, s_st1.gu, s_st2.gu, s_st3.gu, s_tok, s_as, done);
         nmoe_gtl_end(tl, 1, rank, es, nt, 0, nrows);
     } else {
+        /* the down tiles' order (the dispatch's second list) */
         nmoe_die_tile(blockIdx.x - ngu, NTILED, es, nt);
-        nmoe_dn_tile<BITS, NW, NTD, NS, true>(pack, ahi, alo, as, perm, rank, 1, nrows, y, es, nt, 0, s_s.dn,
-                                              s_st0.dn, s_st1.dn, s_st2.dn, s_st3.dn, s_tok, done, NTG, sync, spin,
-                                              tl);
-        nmoe_gtl_end(tl, 2, rank, es, nt, 0, nrows);
+        nmoe_dn_tile<BITS, NW, NTD, NS, true>(pack, ahi, alo, as, perm, rank + NMOE_EXPERTS, 1, nrows, y, es, nt, 0,
+                                              s_s.dn, s_st0.dn, s_st1.dn, s_st2.dn, s_st3.dn, s_tok, done, NTG, sync,
+                                              spin, tl);
+        nmoe_gtl_end(tl, 2, rank + NMOE_EXPERTS, es, nt, 0, nrows);
     }
 }
 
@@ -1636,7 +1668,7 @@ extern "C" int nmoe_grouped_init(nmoe_hip_ctx *ctx) {
     if (hipMalloc((void **)&ctx->g_counts, NMOE_DISPATCH_MAX * (NMOE_EXPERTS + 1) * sizeof(uint32_t)) != hipSuccess ||
         hipMalloc((void **)&ctx->g_perm, rows * sizeof(uint32_t)) != hipSuccess ||
         hipMalloc((void **)&ctx->g_offsets, (NMOE_EXPERTS + 1) * sizeof(uint32_t)) != hipSuccess ||
-        hipMalloc((void **)&ctx->g_rank, NMOE_EXPERTS * 4 * sizeof(uint32_t)) != hipSuccess ||
+        hipMalloc((void **)&ctx->g_rank, 2 * NMOE_EXPERTS * 4 * sizeof(uint32_t)) != hipSuccess ||
         hipMalloc((void **)&ctx->g_xhi, mt * NMOE_HIDDEN * sizeof(uint16_t)) != hipSuccess ||
         hipMalloc((void **)&ctx->g_xlo, mt * NMOE_HIDDEN * sizeof(uint16_t)) != hipSuccess ||
         hipMalloc((void **)&ctx->g_xs, mt * 3 * (NMOE_HIDDEN / NMOE_GROUP) * sizeof(uint16_t)) != hipSuccess ||
@@ -1653,7 +1685,7 @@ extern "C" int nmoe_grouped_init(nmoe_hip_ctx *ctx) {
     if (hipMemset(ctx->g_counts, 0, NMOE_DISPATCH_MAX * (NMOE_EXPERTS + 1) * sizeof(uint32_t)) != hipSuccess ||
         hipMemset(ctx->g_perm, 0, rows * sizeof(uint32_t)) != hipSuccess ||
         hipMemset(ctx->g_offsets, 0, (NMOE_EXPERTS + 1) * sizeof(uint32_t)) != hipSuccess ||
-        hipMemset(ctx->g_rank, 0, NMOE_EXPERTS * 4 * sizeof(uint32_t)) != hipSuccess ||
+        hipMemset(ctx->g_rank, 0, 2 * NMOE_EXPERTS * 4 * sizeof(uint32_t)) != hipSuccess ||
         hipMemset(ctx->g_done, 0, NMOE_SCHED_WORDS * sizeof(uint32_t)) != hipSuccess ||
         hipDeviceSynchronize() != hipSuccess)
         return NMOE_HIP_EHIP;

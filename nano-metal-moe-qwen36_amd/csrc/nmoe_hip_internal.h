@@ -127,7 +127,8 @@ struct nmoe_hip_ctx {
     uint32_t *g_counts;     /* [64][257] per-block expert histograms */
     uint32_t *g_perm;       /* [T*8] entries grouped by expert */
     uint32_t *g_offsets;    /* [257] */
-    uint32_t *g_rank;       /* [256][4] experts by entries, dealt over the dies: (expert, first entry, entries, 0) */
+    uint32_t *g_rank;       /* [2][256][4] the expert order (expert, first entry, entries, entry), then the
+                               same entries in the one-launch down tiles' order */
     uint16_t *g_xhi, *g_xlo; /* [T][2048] x in operand order (bf16 hi / lo) */
     uint16_t *g_xs;         /* [T][3][32] group sums of x as three bf16 parts */
     uint16_t *g_ahi, *g_alo; /* [T*8][512] act (bf16 hi / lo), by permuted row */
