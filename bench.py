@@ -594,13 +594,19 @@ def grouped_timeline(ctx, step, NLg: int, workload: str, one: bool, nsteps: int 
     the blocks with work of each kind (count, median duration, median
     wait), when the last gate/up tile ends and the first down tile starts,
     the GEMMs' span, and the mean number of blocks with work running at once
-    over that span (two a CU can run: 512)."""
+    over that span (two a CU can run: 512).  The preparation launch's blocks
+    record theirs too: when its routing, dispatch and x-plane blocks are
+    ready and end, from its first block's start, and the gap from its last
+    block's end to the GEMM launch's first block."""
     tick_us = 0.01  # s_memrealtime counts at 100 MHz
     words = GTL_SLOTS * 256 * 16
     stamps = ctx.alloc(words * 8)
     per, raw = [], []
     for i in range(nsteps):
         stamps.upload(np.zeros(words, np.uint64))
+        # an unstamped step first, so that the stamped one follows a step on the GPU as in the timed loop
+        # (the first launch after the copy and the synchronisation starts its blocks on the dies over several us)
+        step((i + NLg - 1) % NLg)
         ctx._check(ctx.set_timeline(stamps, GTL_SLOTS))
         step(i % NLg)
         ctx.sync()
@@ -610,10 +616,23 @@ def grouped_timeline(ctx, step, NLg: int, workload: str, one: bool, nsteps: int 
         raw.append(r)
         info = r[:, 3]
         work, kind = info >> 32, (info >> 28) & 15
-        t0 = r[:, 0].min()
+        gemm = (kind == 1) | (kind == 2)
+        t0 = r[gemm, 0].min()  # the GEMM launch's first block (preparation blocks start before it)
         st, rd, en = (r[:, 0] - t0) * tick_us, (r[:, 1] - t0) * tick_us, (r[:, 2] - t0) * tick_us
         gu, dn = (work > 0) & (kind == 1), (work > 0) & (kind == 2)  # gate/up and down tiles with work
         span = float(en[gu | dn].max())
+        # the preparation launch, from its first block's start: routing blocks (their first token
+        # routed and counted), the dispatch block (its slice routed; its end), the x-plane blocks
+        pr, pd, px = kind == 3, kind == 4, kind == 5
+        p0 = st[pr | pd | px].min()
+        prep = {
+            "prep_route_ready_median_us": float(np.median(rd[pr] - p0)) if pr.any() else None,
+            "prep_route_end_max_us": float((en[pr] - p0).max()) if pr.any() else None,
+            "prep_dispatch_ready_us": float((rd[pd] - p0).max()), "prep_dispatch_end_us": float((en[pd] - p0).max()),
+            "prep_x_end_max_us": float((en[px] - p0).max()) if px.any() else None,
+            "prep_span_us": float((en[pr | pd | px] - p0).max()),
+            "prep_end_to_gemm_start_us": float(-en[pr | pd | px].max()),
+        }
         grid = np.arange(0.0, span, 0.25)
         busy = ((st[gu | dn][None, :] <= grid[:, None]) & (grid[:, None] < en[gu | dn][None, :])).sum(axis=1)
         per.append({
@@ -623,6 +642,7 @@ def grouped_timeline(ctx, step, NLg: int, workload: str, one: bool, nsteps: int 
             "last_gateup_end_us": float(en[gu].max()), "first_down_start_us": float(st[dn].min()),
             "busy_mean": float(busy.mean()), "busy_after_last_gateup_start_mean":
                 float(busy[grid >= st[gu].max()].mean()) if (grid >= st[gu].max()).any() else None,
+            **prep,
         })
     if dump:  # the raw block records: [start, ready, end, info] ticks per block, one array per step
         np.savez_compressed(dump, *raw)

@@ -147,47 +147,164 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t nmoe_buffer(void *p) {
     return __builtin_amdgcn_make_buffer_rsrc(p, (short)0, 0x7fffffff, 0x00020000);
 }
 
+/* An LDS address as the direct global->LDS loads take it. */
+typedef __attribute__((address_space(3))) void nmoe_lds_void;
+
+/* Phase timeline of the grouped launches (NMOE_TIMELINE builds; tl NULL
+ * otherwise): block b's words tl[4b .. 4b+3] = the real-time clock at its
+ * start, once its inputs are ready (a down tile of the one-launch form:
+ * after its wait; a routing block: its first wavefront's token routed,
+ * before its stores; the dispatch block: its slice routed; else its start) and at its
+ * end, and what it ran: entries << 32 | kind << 28 | die << 24 | expert
+ * rank (or block) << 8 | tile (kind 1 gate/up, 2 down; of the preparation
+ * launch 3 routing, 4 dispatch, 5 x planes).  One lane stores, with a
+ * vector store. */
+#define NMOE_GTL_START 0
+#define NMOE_GTL_READY 1
+#define NMOE_GTL_END 2
+#define NMOE_GTL_INFO 3
+__device__ __forceinline__ void nmoe_gtl_put(uint64_t *tl, int w, uint64_t v) {
+    if constexpr (NMOE_TIMELINE) {
+        if (tl != nullptr) {
+            uint64_t *p = tl + 4 * (size_t)blockIdx.x + w;
+            asm volatile("global_store_dwordx2 %0, %1, off" ::"v"(p), "v"(v) : "memory");
+        }
+    }
+}
+__device__ __forceinline__ void nmoe_gtl_stamp(uint64_t *tl, int w) {
+    if constexpr (NMOE_TIMELINE)
+        if (tl != nullptr) nmoe_gtl_put(tl, w, __builtin_amdgcn_s_memrealtime());
+}
+/* start and ready at a block's entry, end and what it ran at its exit */
+__device__ __forceinline__ void nmoe_gtl_begin(uint64_t *tl) {
+    if constexpr (NMOE_TIMELINE) {
+        if (tl != nullptr && threadIdx.x == 0) {
+            const uint64_t t = __builtin_amdgcn_s_memrealtime();
+            nmoe_gtl_put(tl, NMOE_GTL_START, t);
+            nmoe_gtl_put(tl, NMOE_GTL_READY, t);
+        }
+    }
+}
+__device__ __forceinline__ void nmoe_gtl_end(uint64_t *tl, int kind, const uint4 *rank, int es, int nt, int pl,
+                                             int nrows) {
+    if constexpr (NMOE_TIMELINE) {
+        if (tl != nullptr && threadIdx.x == 0) {
+            nmoe_gtl_stamp(tl, NMOE_GTL_END);
+            const uint4 rk = rank[es];
+            const uint32_t p0 = min(rk.y, (uint32_t)nrows), n = min(rk.z, (uint32_t)nrows - p0);
+            const uint32_t work = n > (uint32_t)(pl * NMOE_MCHUNK) ? n : 0u;
+            nmoe_gtl_put(tl, NMOE_GTL_INFO,
+                         ((uint64_t)work << 32) | ((uint64_t)kind << 28) | ((uint64_t)nmoe_xcc_id() << 24) |
+                             ((uint64_t)es << 8) | (uint64_t)nt);
+        }
+    }
+}
+
+/* end and kind of a preparation block (thread 0) */
+__device__ __forceinline__ void nmoe_gtl_prep_end(uint64_t *tl, int kind) {
+    if constexpr (NMOE_TIMELINE) {
+        if (tl != nullptr && threadIdx.x == 0) {
+            nmoe_gtl_stamp(tl, NMOE_GTL_END);
+            nmoe_gtl_put(tl, NMOE_GTL_INFO,
+                         (1ull << 32) | ((uint64_t)kind << 28) | ((uint64_t)nmoe_xcc_id() << 24) |
+                             ((uint64_t)blockIdx.x << 8));
+        }
+    }
+}
+
 /* ------------------------------------------------------------ dispatch */
 
-/* The expert of entry q (token q / k, slot q % k).  COH: idx was written by
- * other blocks of this launch, so it is read with device-coherent loads. */
-template <bool COH>
-__device__ __forceinline__ uint32_t nmoe_entry_expert(const uint32_t *idx, int q, int k) {
-    const uint32_t *p = idx + (size_t)(q / k) * NMOE_MAX_K + (q % k);
-    const uint32_t e = COH ? nmoe_ld_u32_dev((uint32_t *)p) : *p;
+/* Where the dispatch reads the expert of entry q (token q / k, slot
+ * q % k): idx, or, when the routing runs in the same launch (ROUTED), the
+ * entry's tagged word (launch epoch << 32 | expert), written by its routing
+ * wavefront and polled (bounded) until it carries this launch's epoch: no
+ * count of routed entries to wait for and no second read of idx. */
+struct nmoe_entry_src {
+    const uint32_t *idx;
+    int k;
+    const uint64_t *tags;
+    uint32_t epoch;
+    uint32_t *sync;
+    uint32_t spin;
+};
+
+__device__ __forceinline__ uint32_t nmoe_clamp_expert(uint32_t e) {
     return e < NMOE_EXPERTS ? e : (uint32_t)NMOE_EXPERTS; /* 256: left out */
+}
+
+/* A tagged entry word of this launch: polls (bounded; an expired wait sets
+ * the status word and the word read last is used) from a first read w. */
+__device__ __forceinline__ uint32_t nmoe_entry_tagged(const nmoe_entry_src &s, int q, uint64_t w) {
+    uint32_t spins = 0;
+    while (!nmoe_tag_is(w, s.epoch)) {
+        __builtin_amdgcn_s_sleep(1);
+        w = nmoe_ld_tagged(s.tags + q);
+        if (++spins > s.spin) {
+            __hip_atomic_store((nmoe_g32 *)(s.sync + NMOE_SYNC_STATUS), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            break;
+        }
+    }
+    return nmoe_clamp_expert((uint32_t)w);
+}
+
+template <bool ROUTED>
+__device__ __forceinline__ uint32_t nmoe_entry_expert(const nmoe_entry_src &s, int q) {
+    if constexpr (ROUTED) return nmoe_entry_tagged(s, q, nmoe_ld_tagged(s.tags + q));
+    return nmoe_clamp_expert(s.idx[(size_t)(q / s.k) * NMOE_MAX_K + (q % s.k)]);
 }
 
 #define NMOE_DISPATCH_PRE 4 /* chunks of a slice whose entries are read up front */
 
 /* This thread's entries of the first NMOE_DISPATCH_PRE chunks of slice b
- * (256 past the slice's end), all loads in flight together; read once for
- * both phases. */
-template <bool COH>
-__device__ __forceinline__ void nmoe_dispatch_entries(const uint32_t *idx, int ntok, int k, int b, int nd,
-                                                      uint32_t *ev) {
-    const int n = ntok * k, per = (n + nd - 1) / nd, q1 = min(n, (b + 1) * per);
+ * (256 past the slice's end), all first reads in flight together; read once
+ * for both phases. */
+template <bool ROUTED>
+__device__ __forceinline__ void nmoe_dispatch_entries(const nmoe_entry_src &s, int ntok, int b, int nd, uint32_t *ev) {
+    const int n = ntok * s.k, per = (n + nd - 1) / nd, q1 = min(n, (b + 1) * per);
+    if constexpr (ROUTED) {
+        uint64_t w[NMOE_DISPATCH_PRE];
 #pragma unroll
-    for (int j = 0; j < NMOE_DISPATCH_PRE; j++) {
-        const int q = b * per + 256 * j + (int)threadIdx.x;
-        ev[j] = q < q1 ? nmoe_entry_expert<COH>(idx, q, k) : (uint32_t)NMOE_EXPERTS;
+        for (int j = 0; j < NMOE_DISPATCH_PRE; j++) {
+            const int q = b * per + 256 * j + (int)threadIdx.x;
+            w[j] = q < q1 ? nmoe_ld_tagged(s.tags + q) : 0ull;
+        }
+#pragma unroll
+        for (int j = 0; j < NMOE_DISPATCH_PRE; j++) {
+            const int q = b * per + 256 * j + (int)threadIdx.x;
+            ev[j] = q < q1 ? nmoe_entry_tagged(s, q, w[j]) : (uint32_t)NMOE_EXPERTS;
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < NMOE_DISPATCH_PRE; j++) {
+            const int q = b * per + 256 * j + (int)threadIdx.x;
+            ev[j] = q < q1 ? nmoe_entry_expert<false>(s, q) : (uint32_t)NMOE_EXPERTS;
+        }
     }
 }
 
+/* The scatter's LDS counts: per chunk of the first NMOE_DISPATCH_PRE and
+ * wavefront, the entries of each expert (then their first places), and
+ * the experts' work buckets.  Cleared by nmoe_dispatch_count. */
+struct nmoe_scatter_lds {
+    uint32_t wc[NMOE_DISPATCH_PRE][4][NMOE_EXPERTS + 1];
+    uint32_t bk[64];
+};
+
 /* D1: h = expert histogram of entry slice b of nd (in LDS). */
-template <bool COH>
-__device__ __forceinline__ void nmoe_dispatch_count(const uint32_t *idx, int ntok, int k, uint32_t *h, int b, int nd,
-                                                    const uint32_t *ev) {
-    const int tid = threadIdx.x, n = ntok * k;
+template <bool ROUTED>
+__device__ __forceinline__ void nmoe_dispatch_count(const nmoe_entry_src &s, int ntok, uint32_t *h, int b, int nd,
+                                                    const uint32_t *ev, nmoe_scatter_lds &sl) {
+    const int tid = threadIdx.x, n = ntok * s.k;
     const int per = (n + nd - 1) / nd;
     for (int i = tid; i <= NMOE_EXPERTS; i += 256) h[i] = 0;
+    for (int i = tid; i < (int)(sizeof(sl) / 4); i += 256) (&sl.wc[0][0][0])[i] = 0;
     __syncthreads();
     const int q1 = min(n, (b + 1) * per);
 #pragma unroll
     for (int j = 0; j < NMOE_DISPATCH_PRE; j++)
         if (b * per + 256 * j + tid < q1) atomicAdd(&h[ev[j]], 1u);
     for (int q = b * per + 256 * NMOE_DISPATCH_PRE + tid; q < q1; q += 256)
-        atomicAdd(&h[nmoe_entry_expert<COH>(idx, q, k)], 1u);
+        atomicAdd(&h[nmoe_entry_expert<ROUTED>(s, q)], 1u);
     __syncthreads();
 }
 
@@ -206,22 +323,35 @@ __device__ __forceinline__ uint32_t nmoe_down_entry(uint32_t es, uint32_t nbig, 
     return 8u * j + d;
 }
 
+/* Rank of this lane among the wavefront's lanes of the same key e
+ * (9 bits: the experts and 256, left out), and their count (a multi-split
+ * by ballots). */
+__device__ __forceinline__ uint32_t nmoe_multisplit9(uint32_t e, int lane, uint32_t &cnt) {
+    uint64_t peers = ~0ull;
+#pragma unroll
+    for (int bit = 0; bit < 9; bit++) {
+        const uint64_t m = __ballot((e >> bit) & 1u);
+        peers &= ((e >> bit) & 1u) ? m : ~m;
+    }
+    cnt = (uint32_t)__builtin_popcountll(peers);
+    return (uint32_t)__builtin_popcountll(peers & ((1ull << lane) - 1ull));
+}
+
 /* D2: offsets (block 0 writes them) and the stable permutation of slice b
  * (the slices' histograms from counts, or from h when there is one slice):
  * chunks of 256 entries in order; within a chunk the rank of an entry is
  * its rank among the equal-expert lanes of its wavefront (a 9-bit
  * multi-split by ballots) plus the counts of the earlier wavefronts. */
-template <bool COH>
-__device__ __forceinline__ void nmoe_dispatch_scatter(const uint32_t *idx, int ntok, int k, uint32_t *counts,
+template <bool ROUTED>
+__device__ __forceinline__ void nmoe_dispatch_scatter(const nmoe_entry_src &src, int ntok, uint32_t *counts,
                                                       const uint32_t *h, uint32_t *perm, uint32_t *offsets,
-                                                      uint4 *rank, int b, int nd, const uint32_t *ev, uint32_t r1) {
+                                                      uint4 *rank, int b, int nd, const uint32_t *ev, uint32_t r1,
+                                                      nmoe_scatter_lds &sl) {
     __shared__ uint32_t s_base[NMOE_EXPERTS];
     __shared__ uint32_t s_scan[4]; /* the wavefronts' totals */
-    __shared__ uint32_t s_bk[64]; /* the work buckets of the expert order */
-    __shared__ uint32_t s_nbig;   /* the experts of more than one small pass */
-    __shared__ uint32_t s_wc[4][NMOE_EXPERTS + 1];
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, n = ntok * k;
-    const int per = (n + nd - 1) / nd;
+    __shared__ uint32_t s_nbig;    /* the experts of more than one small pass */
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, n = ntok * src.k;
+    const int per = (n + nd - 1) / nd, q0 = b * per, q1 = min(n, (b + 1) * per);
     /* thread e: total of expert e and its count in the slices before b.  All
      * NMOE_DISPATCH_MAX slices are loaded at once (the buffer holds that
      * many; those at nd and above are masked), so the loads are in flight
@@ -240,6 +370,16 @@ __device__ __forceinline__ void nmoe_dispatch_scatter(const uint32_t *idx, int n
             before += bb < b ? c : 0u;
         }
     }
+    /* the experts by work, most first: bucket = 16-entry row blocks (63 and
+     * more together), a counting sort over the buckets, any order within
+     * one (the GEMM blocks' results do not depend on their order).  The
+     * GEMM blocks take the experts in this order, so the longest tiles start
+     * first and the launch's tail is short.  Entry es runs on die (es + c)
+     * mod 8, so each round of eight is dealt back and forth (0..7, then
+     * 7..0): dealt the same way every round, the same dies would take the
+     * larger expert of every round and finish last. */
+    const int bk = 63 - (int)min((total + 15u) / 16u, 63u);
+    if (b == 0) atomicAdd(&sl.bk[bk], 1u);
     /* exclusive scan of total over the 256 experts: an inclusive scan within
      * each wavefront (six shuffles), then the earlier wavefronts' totals */
     uint32_t inc = total;
@@ -249,82 +389,90 @@ __device__ __forceinline__ void nmoe_dispatch_scatter(const uint32_t *idx, int n
         inc += lane >= d ? v : 0u;
     }
     if (lane == 63) s_scan[wave] = inc;
+    /* the stable order within an expert is (chunk of 256, wavefront, lane):
+     * the first NMOE_DISPATCH_PRE chunks (their entries in ev) at once,
+     * each entry's rank among its wavefront's lanes of the same expert and
+     * each (chunk, wavefront)'s count of every expert */
+    uint32_t rk[NMOE_DISPATCH_PRE];
+#pragma unroll
+    for (int j = 0; j < NMOE_DISPATCH_PRE; j++) {
+        uint32_t cnt;
+        rk[j] = nmoe_multisplit9(ev[j], lane, cnt);
+        if (rk[j] == 0u) sl.wc[j][wave][ev[j]] = cnt;
+    }
     __syncthreads();
     uint32_t prior = 0;
     for (int w = 0; w < wave; w++) prior += s_scan[w];
     const uint32_t off = prior + inc - total;
+    /* thread e: each (chunk, wavefront)'s first place for expert e, in
+     * place of its count */
+    uint32_t at = off + before;
+#pragma unroll
+    for (int j = 0; j < NMOE_DISPATCH_PRE; j++)
+#pragma unroll
+        for (int w = 0; w < 4; w++) {
+            const uint32_t c = sl.wc[j][w][tid];
+            sl.wc[j][w][tid] = at;
+            at += c;
+        }
+    s_base[tid] = at; /* the chunks after those */
     if (b == 0) {
         offsets[tid] = off;
         if (tid == 255) offsets[NMOE_EXPERTS] = off + total;
-        /* the experts by work, most first: bucket = 16-entry row blocks
-         * (63 and more together), a counting sort over the buckets, any
-         * order within one (the GEMM blocks' results do not depend on their
-         * order).  The GEMM blocks take the experts in this order, so the
-         * longest tiles start first and the launch's tail is short.  Entry
-         * es runs on die (es + c) mod 8, so each round of eight is dealt
-         * back and forth (0..7, then 7..0): dealt the same way every
-         * round, the same dies would take the larger expert of every round
-         * and finish last. */
-        const int bk = 63 - (int)min((total + 15u) / 16u, 63u);
-        if (tid < 64) s_bk[tid] = 0;
-        __syncthreads();
-        atomicAdd(&s_bk[bk], 1u);
-        __syncthreads();
         if (tid < 64) { /* exclusive scan of the 64 bucket sizes (one wavefront) */
-            const uint32_t c = s_bk[tid];
-            uint32_t inc = c;
+            const uint32_t c = sl.bk[tid];
+            uint32_t binc = c;
 #pragma unroll
             for (int d = 1; d < 64; d <<= 1) {
-                const uint32_t v = (uint32_t)__shfl_up((int)inc, d, 64);
-                inc += lane >= d ? v : 0u;
+                const uint32_t v = (uint32_t)__shfl_up((int)binc, d, 64);
+                binc += lane >= d ? v : 0u;
             }
-            s_bk[tid] = inc - c;
+            sl.bk[tid] = binc - c;
             static_assert(NMOE_SMALL_PASS == 16, "bucket 62 holds the experts of one small pass");
-            if (tid == 62) s_nbig = inc - c;
+            if (tid == 62) s_nbig = binc - c;
         }
-        __syncthreads();
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < NMOE_DISPATCH_PRE; j++) {
+        const int q = q0 + 256 * j + tid;
+        /* pos < n unless the slices' meeting gave up (then the counts of the
+         * other slices may be stale and the launch reports it) */
+        if (q < q1 && ev[j] < (uint32_t)NMOE_EXPERTS) {
+            const uint32_t pos = sl.wc[j][wave][ev[j]] + rk[j];
+            if (pos < (uint32_t)n) perm[pos] = (uint32_t)q;
+        }
+    }
+    if (b == 0) {
         /* the order (its fourth word: the entry itself), and the same
          * entries in the down tiles' order after it */
-        const uint32_t pos = atomicAdd(&s_bk[bk], 1u), round = pos >> 3;
+        const uint32_t pos = atomicAdd(&sl.bk[bk], 1u), round = pos >> 3;
         const uint32_t es = 8u * round + ((round & 1u) ? 7u - (pos & 7u) : (pos & 7u));
         const uint4 ent = make_uint4((uint32_t)tid, off, total, es);
         rank[es] = ent;
         rank[NMOE_EXPERTS + nmoe_down_entry(es, s_nbig, r1)] = ent;
     }
-    s_base[tid] = off + before;
-    for (int i = tid; i < 4 * (NMOE_EXPERTS + 1); i += 256) (&s_wc[0][0])[i] = 0;
-    __syncthreads();
-    const int q0 = b * per, q1 = min(n, (b + 1) * per);
-    for (int c0 = q0; c0 < q1; c0 += 256) {
-        const int q = c0 + tid;
-        /* chunk j: read up front for the first NMOE_DISPATCH_PRE, else now */
-        const int j = (c0 - q0) / 256;
-        uint32_t e = (uint32_t)NMOE_EXPERTS;
+    /* slices of more than NMOE_DISPATCH_PRE chunks: the others one at a
+     * time, counted in sl.wc[0] */
+    for (int c0 = q0 + 256 * NMOE_DISPATCH_PRE; c0 < q1; c0 += 256) {
+        __syncthreads(); /* sl.wc[0] and s_base are free */
 #pragma unroll
-        for (int jj = 0; jj < NMOE_DISPATCH_PRE; jj++)
-            if (j == jj) e = ev[jj];
-        if (j >= NMOE_DISPATCH_PRE && q < q1) e = nmoe_entry_expert<COH>(idx, q, k);
-        uint64_t peers = ~0ull;
-#pragma unroll
-        for (int bit = 0; bit < 9; bit++) {
-            const uint64_t m = __ballot((e >> bit) & 1u);
-            peers &= ((e >> bit) & 1u) ? m : ~m;
-        }
-        const uint32_t rank = (uint32_t)__builtin_popcountll(peers & ((1ull << lane) - 1ull));
-        if (rank == 0) s_wc[wave][e] = (uint32_t)__builtin_popcountll(peers);
+        for (int w = 0; w < 4; w++) sl.wc[0][w][tid] = 0u;
+        if (tid < 4) sl.wc[0][tid][NMOE_EXPERTS] = 0u;
         __syncthreads();
-        if (e < NMOE_EXPERTS) {
-            uint32_t pos = s_base[e] + rank;
-            for (int w = 0; w < wave; w++) pos += s_wc[w][e];
-            /* pos < n unless the slices' meeting gave up (then the counts of
-             * the other slices may be stale and the launch reports it) */
+        const int q = c0 + tid;
+        const uint32_t e = q < q1 ? nmoe_entry_expert<ROUTED>(src, q) : (uint32_t)NMOE_EXPERTS;
+        uint32_t cnt;
+        const uint32_t r = nmoe_multisplit9(e, lane, cnt);
+        if (r == 0u) sl.wc[0][wave][e] = cnt;
+        __syncthreads();
+        if (q < q1 && e < (uint32_t)NMOE_EXPERTS) {
+            uint32_t pos = s_base[e] + r;
+            for (int w = 0; w < wave; w++) pos += sl.wc[0][w][e];
             if (pos < (uint32_t)n) perm[pos] = (uint32_t)q;
         }
         __syncthreads();
-        s_base[tid] += s_wc[0][tid] + s_wc[1][tid] + s_wc[2][tid] + s_wc[3][tid];
-        s_wc[0][tid] = s_wc[1][tid] = s_wc[2][tid] = s_wc[3][tid] = 0;
-        if (tid == 0) s_wc[0][NMOE_EXPERTS] = s_wc[1][NMOE_EXPERTS] = s_wc[2][NMOE_EXPERTS] = s_wc[3][NMOE_EXPERTS] = 0;
-        __syncthreads();
+        s_base[tid] += sl.wc[0][0][tid] + sl.wc[0][1][tid] + sl.wc[0][2][tid] + sl.wc[0][3][tid];
     }
 }
 
@@ -442,36 +590,55 @@ __device__ __forceinline__ void nmoe_wait_tiles(uint32_t *cnt, uint32_t n, uint3
  * nmoe_moe_topk) by the nr = ceil(ntok / 4) blocks after the dispatch
  * blocks, one token a wavefront (so they are resident in the launch's
  * first round with the dispatch blocks that wait for them); the x blocks
- * come after them.  A wavefront writes idx / w of its token with
- * device-coherent stores and, once they are complete, adds the token's
- * entries to the ROUTED word of each dispatch slice they fall in (a slice's
- * word counts only its own entries: one word for all tokens would take
- * thousands of atomic adds in a row); dispatch block b waits (bounded)
- * until its slice is complete, clears its word for the next launch on the
- * stream, and reads idx with device-coherent loads. */
+ * come after them.  A wavefront writes idx / w of its token (the caller's
+ * outputs) and each of its entries as a tagged word (epoch << 32 | expert,
+ * one device-coherent store) in tags[]; a dispatch block polls the tagged
+ * words of its slice (bounded) until each carries this launch's epoch.  The
+ * epoch is the PREP_EPOCH sync word + 1, read by every routing and dispatch
+ * block at its start; dispatch block 0 adds 1 to the word once every slice's
+ * entries have been read (they were all written by then, so no block of
+ * this launch can read the new value), and tagged words of earlier launches
+ * carry earlier epochs, so none is taken for this launch's. */
 template <int BITS, typename XT, bool ROUTED>
 __global__ void __launch_bounds__(256) nmoe_grouped_prep_kernel(const uint32_t *idx, int ntok, int k, int nd,
                                                                 uint32_t *counts, uint32_t *perm, uint32_t *offsets,
                                                                 uint4 *rank, uint32_t *sync, uint32_t spin,
                                                                 const XT *x, uint16_t *xhi, uint16_t *xlo,
                                                                 uint16_t *xs3, const float *logits, uint32_t *idx_out,
-                                                                float *w_out, uint32_t *done, int skew) {
+                                                                float *w_out, uint32_t *done, int skew,
+                                                                uint64_t *tags, uint64_t *tl) {
     const int b = blockIdx.x;
+    nmoe_gtl_begin(tl);
+    /* this launch's epoch of the tagged entries (read at once by every block) */
+    const uint32_t epoch = ROUTED ? nmoe_ld_u32_dev(sync + NMOE_SYNC_PREP_EPOCH) + 1u : 0u;
     /* the one-launch GEMM's tile counts start from 0 (plain stores: the next
      * launch on the stream sees them); rank `skew` (a test of the failure
      * path) from a count no tiles can reach */
     if (done != NULL && b == 0)
         for (int i = threadIdx.x; i < NMOE_SCHED_WORDS; i += 256) done[i] = i == skew ? 0x8000u : 0u;
     const int nr = ROUTED ? (ntok + 3) / 4 : 0; /* routing blocks */
-    const int n = ntok * k, per = (n + nd - 1) / nd; /* dispatch slices */
     if (ROUTED && b >= nd && b < nd + nr) {
         __shared__ float s_sm[4][NMOE_EXPERTS];
+        __shared__ uint64_t s_tab[32];
         const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, t = 4 * (b - nd) + wave;
+        /* the token's logits straight into LDS (one 1 KB direct load a
+         * wavefront) and the exp table beside them, both in flight at once:
+         * read from constant memory, each exp's table lookup was a memory
+         * round trip of its own after the logits' */
+        static_assert(NMOE_EXPERTS == 256, "a token's logits are one 1 KB direct load");
+        if (t < ntok) /* wavefront-uniform */
+            __builtin_amdgcn_global_load_lds((const void *)(logits + (size_t)t * NMOE_EXPERTS + 4 * lane),
+                                             (nmoe_lds_void *)&s_sm[wave][0], 16, 0, 0);
+        if (threadIdx.x < 32) s_tab[threadIdx.x] = nmoe_grouped_exp2_tab[threadIdx.x];
+        __builtin_amdgcn_s_waitcnt(0x0F70); /* vmcnt(0): the logits are in LDS */
+        __syncthreads();
         if (t < ntok) {
             uint32_t si[NMOE_MAX_K];
             float sw[NMOE_MAX_K];
-            nmoe_wave_route(logits + (size_t)t * NMOE_EXPERTS, NMOE_EXPERTS, k, s_sm[wave], nmoe_grouped_exp2_tab, si, sw,
-                            NULL);
+            /* (the logits are read into registers before s_sm[wave] serves as
+             * the exact sum's scratch) */
+            nmoe_wave_route(&s_sm[wave][0], NMOE_EXPERTS, k, s_sm[wave], s_tab, si, sw, NULL);
+            if (threadIdx.x == 0) nmoe_gtl_stamp(tl, NMOE_GTL_READY);
             if (lane < NMOE_MAX_K) {
                 uint32_t vi = 0;
                 float vw = 0.0f;
@@ -481,36 +648,31 @@ __global__ void __launch_bounds__(256) nmoe_grouped_prep_kernel(const uint32_t *
                         vi = si[q];
                         vw = sw[q];
                     }
-                __hip_atomic_store((nmoe_g32 *)&idx_out[(size_t)t * NMOE_MAX_K + lane], vi, __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT);
-                __hip_atomic_store((nmoe_g32 *)&w_out[(size_t)t * NMOE_MAX_K + lane], __float_as_uint(vw),
-                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            }
-            __builtin_amdgcn_s_waitcnt(0x0F70); /* vmcnt(0): the stores are complete */
-            if (lane == 0) {
-                const int q0 = t * k, q1 = q0 + k; /* the token's entries, in one or two slices */
-                for (int sb = q0 / per; sb <= (q1 - 1) / per && sb < nd; sb++)
-                    nmoe_add_u32_dev(sync + NMOE_SYNC_ROUTED(sb), (uint32_t)(min(q1, (sb + 1) * per) - max(q0, sb * per)));
+                idx_out[(size_t)t * NMOE_MAX_K + lane] = vi;
+                w_out[(size_t)t * NMOE_MAX_K + lane] = vw;
+                if (lane < k)
+                    __hip_atomic_store((nmoe_g64 *)&tags[(size_t)t * k + lane], ((uint64_t)epoch << 32) | vi,
+                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
         }
+        nmoe_gtl_prep_end(tl, 3);
         return;
     }
     if (b >= nd) {
         if (x != NULL) nmoe_grouped_xprep<BITS, XT>(x, xhi, xlo, xs3, b - nd - nr);
+        nmoe_gtl_prep_end(tl, 5);
         return;
     }
-    if (ROUTED) { /* this slice's entries routed: then its word starts from 0 for the next launch */
-        if (threadIdx.x == 0) {
-            uint32_t *cnt = sync + NMOE_SYNC_ROUTED(b);
-            nmoe_wait_count(cnt, (uint32_t)max(0, min(n, (b + 1) * per) - b * per), sync, spin);
-            __hip_atomic_store((nmoe_g32 *)cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-        __syncthreads();
-    }
+    const nmoe_entry_src src = {idx, k, tags, epoch, sync, spin};
     uint32_t ev[NMOE_DISPATCH_PRE];
-    nmoe_dispatch_entries<ROUTED>(idx, ntok, k, b, nd, ev);
+    nmoe_dispatch_entries<ROUTED>(src, ntok, b, nd, ev);
+    if (ROUTED && threadIdx.x == 0) nmoe_gtl_stamp(tl, NMOE_GTL_READY);
     __shared__ uint32_t h[NMOE_EXPERTS + 1];
-    nmoe_dispatch_count<ROUTED>(idx, ntok, k, h, b, nd, ev);
+    __shared__ nmoe_scatter_lds s_scat;
+    nmoe_dispatch_count<ROUTED>(src, ntok, h, b, nd, ev, s_scat);
+    /* every entry of this slice read (one slice), or of every slice (after
+     * the meeting below): the next launch takes the next epoch */
+    if (ROUTED && nd == 1 && threadIdx.x == 0) nmoe_add_u32_dev(sync + NMOE_SYNC_PREP_EPOCH, 1u);
     if (nd > 1) {
         /* publish the histogram with device-coherent stores, completed
          * (vmcnt 0) before the arrival is counted: no agent-scope release
@@ -526,6 +688,7 @@ __global__ void __launch_bounds__(256) nmoe_grouped_prep_kernel(const uint32_t *
             const uint32_t old = nmoe_add_u32_dev(cnt, (uint32_t)(NMOE_DISPATCH_MAX / nd));
             const uint32_t target = (old / NMOE_DISPATCH_MAX + 1u) * NMOE_DISPATCH_MAX;
             nmoe_wait_count(cnt, target, sync, spin);
+            if (ROUTED && b == 0) nmoe_add_u32_dev(sync + NMOE_SYNC_PREP_EPOCH, 1u);
         }
         __syncthreads(); /* (the histograms are then read with device-coherent loads) */
     }
@@ -533,7 +696,8 @@ __global__ void __launch_bounds__(256) nmoe_grouped_prep_kernel(const uint32_t *
      * die, two four-wavefront blocks a CU (one of eight) */
     constexpr uint32_t R1 =
         (256u / NMOE_GROUPED_NW) / (uint32_t)(NMOE_INTER / nmoe_gu_rows(sizeof(XT) == 2 ? 1 : 2, NMOE_GROUPED_NW));
-    nmoe_dispatch_scatter<ROUTED>(idx, ntok, k, counts, h, perm, offsets, rank, b, nd, ev, R1);
+    nmoe_dispatch_scatter<ROUTED>(src, ntok, counts, h, perm, offsets, rank, b, nd, ev, R1, s_scat);
+    nmoe_gtl_prep_end(tl, 4);
 }
 
 /* ------------------------------------------------------------ stage ring */
@@ -553,7 +717,6 @@ __global__ void __launch_bounds__(256) nmoe_grouped_prep_kernel(const uint32_t *
  * Each stage is a __shared__ variable of its own: the compiler then tells
  * the stages' direct loads apart and a read of one stage does not wait for
  * the loads still in flight into the others. */
-typedef __attribute__((address_space(3))) void nmoe_lds_void;
 
 template <int PL, int R, int CW>
 struct nmoe_stage {
@@ -786,53 +949,6 @@ __device__ __forceinline__ float nmoe_silu_fast(float x) {
     const float z = __expf(-fabsf(x));
     const float r = __builtin_amdgcn_rcpf(1.0f + z);
     return x * (x >= 0.0f ? r : z * r);
-}
-
-/* Phase timeline of a GEMM launch (NMOE_TIMELINE builds; tl NULL
- * otherwise): block b's words tl[4b .. 4b+3] = the real-time clock at its
- * start, once its inputs are ready (a down tile of the one-launch form:
- * after its wait; else its start) and at its end, and what it ran:
- * entries << 32 | kind << 28 | die << 24 | expert rank << 8 | tile (kind 1
- * gate/up, 2 down).  One lane stores, with a vector store. */
-#define NMOE_GTL_START 0
-#define NMOE_GTL_READY 1
-#define NMOE_GTL_END 2
-#define NMOE_GTL_INFO 3
-__device__ __forceinline__ void nmoe_gtl_put(uint64_t *tl, int w, uint64_t v) {
-    if constexpr (NMOE_TIMELINE) {
-        if (tl != nullptr) {
-            uint64_t *p = tl + 4 * (size_t)blockIdx.x + w;
-            asm volatile("global_store_dwordx2 %0, %1, off" ::"v"(p), "v"(v) : "memory");
-        }
-    }
-}
-__device__ __forceinline__ void nmoe_gtl_stamp(uint64_t *tl, int w) {
-    if constexpr (NMOE_TIMELINE)
-        if (tl != nullptr) nmoe_gtl_put(tl, w, __builtin_amdgcn_s_memrealtime());
-}
-/* start and ready at a block's entry, end and what it ran at its exit */
-__device__ __forceinline__ void nmoe_gtl_begin(uint64_t *tl) {
-    if constexpr (NMOE_TIMELINE) {
-        if (tl != nullptr && threadIdx.x == 0) {
-            const uint64_t t = __builtin_amdgcn_s_memrealtime();
-            nmoe_gtl_put(tl, NMOE_GTL_START, t);
-            nmoe_gtl_put(tl, NMOE_GTL_READY, t);
-        }
-    }
-}
-__device__ __forceinline__ void nmoe_gtl_end(uint64_t *tl, int kind, const uint4 *rank, int es, int nt, int pl,
-                                             int nrows) {
-    if constexpr (NMOE_TIMELINE) {
-        if (tl != nullptr && threadIdx.x == 0) {
-            nmoe_gtl_stamp(tl, NMOE_GTL_END);
-            const uint4 rk = rank[es];
-            const uint32_t p0 = min(rk.y, (uint32_t)nrows), n = min(rk.z, (uint32_t)nrows - p0);
-            const uint32_t work = n > (uint32_t)(pl * NMOE_MCHUNK) ? n : 0u;
-            nmoe_gtl_put(tl, NMOE_GTL_INFO,
-                         ((uint64_t)work << 32) | ((uint64_t)kind << 28) | ((uint64_t)nmoe_xcc_id() << 24) |
-                             ((uint64_t)es << 8) | (uint64_t)nt);
-        }
-    }
 }
 
 /* ------------------------------------------------------------ gate/up */
@@ -1676,7 +1792,8 @@ extern "C" int nmoe_grouped_init(nmoe_hip_ctx *ctx) {
         hipMalloc((void **)&ctx->g_alo, rows * NMOE_INTER * sizeof(uint16_t)) != hipSuccess ||
         hipMalloc((void **)&ctx->g_as, rows * (NMOE_INTER / NMOE_GROUP) * sizeof(float)) != hipSuccess ||
         hipMalloc((void **)&ctx->g_y, rows * NMOE_HIDDEN * sizeof(float)) != hipSuccess ||
-        hipMalloc((void **)&ctx->g_done, NMOE_SCHED_WORDS * sizeof(uint32_t)) != hipSuccess)
+        hipMalloc((void **)&ctx->g_done, NMOE_SCHED_WORDS * sizeof(uint32_t)) != hipSuccess ||
+        hipMalloc((void **)&ctx->g_tags, rows * sizeof(uint64_t)) != hipSuccess)
         return NMOE_HIP_ENOMEM;
     ctx->grouped_one_launch = ctx->xcd_placed;
     ctx->skew_tiles = -1;
@@ -1687,6 +1804,7 @@ extern "C" int nmoe_grouped_init(nmoe_hip_ctx *ctx) {
         hipMemset(ctx->g_offsets, 0, (NMOE_EXPERTS + 1) * sizeof(uint32_t)) != hipSuccess ||
         hipMemset(ctx->g_rank, 0, 2 * NMOE_EXPERTS * 4 * sizeof(uint32_t)) != hipSuccess ||
         hipMemset(ctx->g_done, 0, NMOE_SCHED_WORDS * sizeof(uint32_t)) != hipSuccess ||
+        hipMemset(ctx->g_tags, 0, rows * sizeof(uint64_t)) != hipSuccess ||
         hipDeviceSynchronize() != hipSuccess)
         return NMOE_HIP_EHIP;
     return NMOE_HIP_OK;
@@ -1694,7 +1812,7 @@ extern "C" int nmoe_grouped_init(nmoe_hip_ctx *ctx) {
 
 extern "C" void nmoe_grouped_free(nmoe_hip_ctx *ctx) {
     void *p[] = {ctx->g_counts, ctx->g_perm, ctx->g_offsets, ctx->g_rank, ctx->g_xhi, ctx->g_xlo,
-                 ctx->g_xs,     ctx->g_ahi,  ctx->g_alo,     ctx->g_as,   ctx->g_y,   ctx->g_done};
+                 ctx->g_xs,     ctx->g_ahi,  ctx->g_alo,     ctx->g_as,   ctx->g_y,   ctx->g_done, ctx->g_tags};
     for (void *q : p)
         if (q != NULL) (void)hipFree(q);
 }
@@ -1706,7 +1824,8 @@ extern "C" int nmoe_grouped_dispatch(nmoe_hip_ctx *ctx, const uint32_t *idx, int
     hipLaunchKernelGGL((nmoe_grouped_prep_kernel<4, uint16_t, false>), dim3(nd), dim3(256), 0, s, idx, ntok, k, nd,
                        ctx->g_counts, perm, offsets, (uint4 *)ctx->g_rank, ctx->sync, ctx->spin_limit,
                        (const uint16_t *)NULL, (uint16_t *)NULL, (uint16_t *)NULL, (uint16_t *)NULL,
-                       (const float *)NULL, (uint32_t *)NULL, (float *)NULL, (uint32_t *)NULL, -1);
+                       (const float *)NULL, (uint32_t *)NULL, (float *)NULL, (uint32_t *)NULL, -1, (uint64_t *)NULL,
+                       (uint64_t *)NULL);
     const hipError_t e = hipGetLastError();
     return e == hipSuccess ? NMOE_HIP_OK : nmoe_hip_check(ctx, e, "dispatch launch");
 }
@@ -1732,10 +1851,12 @@ static int nmoe_grouped_run(nmoe_hip_ctx *ctx, const uint8_t *pack, const void *
     uint32_t *done = one ? ctx->g_done : NULL;
     const int skew = one ? ctx->skew_tiles : -1;
     if (one) ctx->skew_tiles = -1;
+    /* timeline builds: 4 stamps a block of the preparation launch */
+    uint64_t *tlp = nmoe_tl_take(ctx, (int)((4 * (size_t)gprep.x + NMOE_TL_SLOT_WORDS - 1) / NMOE_TL_SLOT_WORDS));
 #define NMOE_PREP(XT, R, XLO)                                                                                         \
     hipLaunchKernelGGL((nmoe_grouped_prep_kernel<BITS, XT, R>), gprep, dim3(256), 0, s, idx, ntok, k, nd, ctx->g_counts, \
                        ctx->g_perm, ctx->g_offsets, (uint4 *)ctx->g_rank, ctx->sync, ctx->spin_limit, (const XT *)x,  \
-                       ctx->g_xhi, XLO, ctx->g_xs, logits, ri, rw, done, skew)
+                       ctx->g_xhi, XLO, ctx->g_xs, logits, ri, rw, done, skew, ctx->g_tags, tlp)
     if (logits != NULL) {
         if (bf)
             NMOE_PREP(uint16_t, true, (uint16_t *)NULL);

@@ -196,6 +196,49 @@ def test_grouped_one_launch_wrong_tile_count_poisons_and_recovers(nh):
         assert ctx.set_option(nh.OPT_SKEW_TILES, 256) == nh.EINVAL
 
 
+def test_grouped_routed_after_aborted_launch(nh):
+    """The routed preparation tags each entry with its launch's epoch, a
+    device counter that one block advances per launch.  After a launch that
+    is aborted (here its one-launch GEMM, through NMOE_HIP_OPT_SKEW_TILES:
+    NaN outputs, ETIMEDOUT), the recovery moves the counter past any epoch
+    that launch's entries can carry; the calls after it, each with new
+    logits, give the same routing and outputs as the two-launch form on a
+    context that never failed."""
+    rng = np.random.default_rng(78)
+    ntok, k, layer, bits = 64, 8, 5, 4
+    calls = [(rng.random((ntok, 256), dtype=np.float32), rng.standard_normal((ntok, 2048)).astype(np.float32),
+              rng.standard_normal((ntok, 2048)).astype(np.float32)) for _ in range(4)]
+
+    def run_all(ctx, skew_before):
+        ctx.synth_layer(layer, bits, 12, 0.02)
+        out, idx, w = ctx.alloc(ntok * 8192), ctx.alloc(ntok * 32), ctx.alloc(ntok * 32)
+        res = []
+        for i, (lg, x, h) in enumerate(calls):
+            if i == skew_before:
+                ctx._check(ctx.set_option(nh.OPT_SKEW_TILES, 0))
+                d = [ctx.to_device(a) for a in (lg, x, h)]
+                ctx._check(ctx.experts_from_logits(layer, d[0], d[1], nh.F32, ntok, k, d[2], out, idx, w))
+                assert ctx.device_status() == nh.ETIMEDOUT
+                assert np.isnan(out.download(np.float32, (ntok, 2048))).all()
+            d = [ctx.to_device(a) for a in (lg, x, h)]
+            ctx._check(ctx.experts_from_logits(layer, d[0], d[1], nh.F32, ntok, k, d[2], out, idx, w))
+            assert ctx.device_status() == nh.OK
+            res.append((idx.download(np.uint32, (ntok, 8)), w.download(np.float32, (ntok, 8)),
+                        out.download(np.float32, (ntok, 2048))))
+        return res
+
+    with nh.Context(0, max_tokens=ntok) as ctx:
+        ctx.set_grouped_one_launch(False)
+        want = run_all(ctx, -1)
+    with nh.Context(0, max_tokens=ntok) as ctx:
+        if not ctx.set_grouped_one_launch(True):
+            pytest.skip("the one-launch form needs the round-robin die placement")
+        got = run_all(ctx, 1)
+    for i, (g, e) in enumerate(zip(got, want)):
+        for a, b, name in zip(g, e, ("idx", "w", "out")):
+            np.testing.assert_array_equal(a.view(np.uint32), b.view(np.uint32), err_msg=f"call {i}: {name}")
+
+
 def test_option_arguments_validated(nh):
     with nh.Context(0, max_tokens=4) as ctx:
         assert ctx.set_option(nh.OPT_SPIN_LIMIT, -1) == nh.EINVAL
