@@ -154,7 +154,12 @@ NMOE_HIP_API int nmoe_hip_set_option(nmoe_hip_ctx *ctx, int option, int value);
  * fused launch (each layer of a stack launch) takes the next slot in turn,
  * and block b writes the device's real-time clock at its phase boundaries
  * to stamps[slot][b][event] (events in nmoe_hip.py's TL_EVENTS; unwritten
- * stamps keep their contents).  NULL and 0 stop the recording. */
+ * stamps keep their contents).  The grouped path's launches (the
+ * preparation, then the GEMM launch or launches) take the next slots as
+ * well, 4 words a block from the slot's start: the clock at its start, at a
+ * ready point and at its end, and what it ran (entries << 32 | kind << 28 |
+ * die << 24 | expert entry or block << 8 | tile; kind 1 gate/up, 2 down,
+ * 3 routing, 4 dispatch, 5 x planes).  NULL and 0 stop the recording. */
 NMOE_HIP_API int nmoe_hip_set_timeline(nmoe_hip_ctx *ctx, void *stamps, int slots);
 
 /* ---- buffers (backend.h:64-66: register_shared_buffer / register_state_buffer
