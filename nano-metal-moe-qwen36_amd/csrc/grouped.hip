@@ -626,9 +626,15 @@ __global__ void __launch_bounds__(256) nmoe_grouped_prep_kernel(const uint32_t *
          * read from constant memory, each exp's table lookup was a memory
          * round trip of its own after the logits' */
         static_assert(NMOE_EXPERTS == 256, "a token's logits are one 1 KB direct load");
-        if (t < ntok) /* wavefront-uniform */
-            __builtin_amdgcn_global_load_lds((const void *)(logits + (size_t)t * NMOE_EXPERTS + 4 * lane),
-                                             (nmoe_lds_void *)&s_sm[wave][0], 16, 0, 0);
+        if (t < ntok) { /* wavefront-uniform */
+            if (((uintptr_t)logits & 15u) == 0u) {
+                __builtin_amdgcn_global_load_lds((const void *)(logits + (size_t)t * NMOE_EXPERTS + 4 * lane),
+                                                 (nmoe_lds_void *)&s_sm[wave][0], 16, 0, 0);
+            } else { /* logits only 4-byte aligned: a lane a word */
+#pragma unroll
+                for (int q = 0; q < 4; q++) s_sm[wave][lane + 64 * q] = logits[(size_t)t * NMOE_EXPERTS + lane + 64 * q];
+            }
+        }
         if (threadIdx.x < 32) s_tab[threadIdx.x] = nmoe_grouped_exp2_tab[threadIdx.x];
         __builtin_amdgcn_s_waitcnt(0x0F70); /* vmcnt(0): the logits are in LDS */
         __syncthreads();

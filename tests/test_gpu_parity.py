@@ -784,6 +784,36 @@ def test_experts_from_logits_equals_topk_then_experts(big, nh, bits, ntok, k, xk
             np.testing.assert_array_equal(wa[t].view(np.uint32), ow.view(np.uint32), err_msg=f"t={t}")
 
 
+@pytest.mark.parametrize("offset", [4, 8, 12])
+def test_experts_from_logits_logits_4_byte_aligned(big, nh, offset):
+    """Logits 4-byte aligned but not 16-byte aligned (the entry point takes
+    them): the routing wavefronts read them a lane a word instead of by
+    16-byte direct loads, with the same bits as the topk launch."""
+    rng = np.random.default_rng(6100 + offset)
+    ntok, k, bits, layer = 64, 8, 4, 27
+    big.synth_layer(layer, bits, 43, SIGMA[bits])
+    logits = rng.random((ntok, 256), dtype=np.float32)
+    x = B.f32_to_bf16(rng.standard_normal((ntok, 2048)).astype(np.float32))
+    h = rng.standard_normal((ntok, 2048)).astype(np.float32)
+    d_lg = big.alloc(ntok * 1024 + 16)
+    d_lg.upload(logits, offset)
+    d_x, d_h = big.to_device(x), big.to_device(h)
+    res = []
+    for use_offset in (True, False):
+        idx, w, out = big.alloc(ntok * 32), big.alloc(ntok * 32), big.alloc(ntok * 2048 * 4)
+        if use_offset:
+            big._check(big.experts_from_logits(layer, d_lg.ptr + offset, d_x, nh.BF16, ntok, k, d_h, out, idx, w))
+        else:
+            d_al = big.to_device(logits)
+            big._check(big.topk(d_al, ntok, 256, k, idx, w))
+            big._check(big.experts(bits, layer, d_x, nh.BF16, ntok, k, idx, w, d_h, out))
+        res.append((idx.download(np.uint32, (ntok, 8)), w.download(np.float32, (ntok, 8)),
+                    out.download(np.float32, (ntok, 2048))))
+    assert big.device_status() == nh.OK
+    for a, b_, name in zip(res[0], res[1], ("idx", "w", "out")):
+        np.testing.assert_array_equal(a.view(np.uint32), b_.view(np.uint32), err_msg=name)
+
+
 def test_experts_from_logits_rejects(big, nh):
     big.synth_layer(25, 4, 1, 0.02)
     lg, x, h, out = big.alloc(64 * 1024), big.alloc(64 * 4096), big.alloc(64 * 8192), big.alloc(64 * 8192)
