@@ -814,6 +814,40 @@ def test_experts_from_logits_logits_4_byte_aligned(big, nh, offset):
         np.testing.assert_array_equal(a.view(np.uint32), b_.view(np.uint32), err_msg=name)
 
 
+def test_experts_from_logits_slices_past_four_chunks(nh):
+    """8,448 tokens x 8 = 67,584 entries: 64 dispatch slices of 1,056, so
+    each slice's last chunk is read after the first four (the tagged entries
+    polled again there).  Bit for bit against nmoe_moe_topk then
+    nmoe_moe_experts (whose dispatch reads idx), and a sample of tokens'
+    routing against the oracle's."""
+    rng = np.random.default_rng(6200)
+    ntok, k, bits, layer = 8448, 8, 2, 3
+    with nh.Context(0, max_tokens=ntok) as ctx:
+        ctx.synth_layer(layer, bits, 47, SIGMA[bits])
+        logits = rng.random((ntok, 256), dtype=np.float32)
+        x = B.f32_to_bf16(rng.standard_normal((ntok, 2048)).astype(np.float32))
+        h = rng.standard_normal((ntok, 2048)).astype(np.float32)
+        d_lg, d_x, d_h = ctx.to_device(logits), ctx.to_device(x), ctx.to_device(h)
+        res = []
+        for path in ("from_logits", "topk_then_experts"):
+            print(f"[from-logits] {ntok} tokens: {path}", flush=True)
+            idx, w, out = ctx.alloc(ntok * 32), ctx.alloc(ntok * 32), ctx.alloc(ntok * 2048 * 4)
+            if path == "from_logits":
+                ctx._check(ctx.experts_from_logits(layer, d_lg, d_x, nh.BF16, ntok, k, d_h, out, idx, w))
+            else:
+                ctx._check(ctx.topk(d_lg, ntok, 256, k, idx, w))
+                ctx._check(ctx.experts(bits, layer, d_x, nh.BF16, ntok, k, idx, w, d_h, out))
+            res.append((idx.download(np.uint32, (ntok, 8)), w.download(np.float32, (ntok, 8)),
+                        out.download(np.float32, (ntok, 2048))))
+        assert ctx.device_status() == nh.OK
+    for a, b_, name in zip(res[0], res[1], ("idx", "w", "out")):
+        np.testing.assert_array_equal(a.view(np.uint32), b_.view(np.uint32), err_msg=name)
+    for t in rng.choice(ntok, 32, replace=False):
+        oi, ow, _ = B.route(logits[t], k)
+        np.testing.assert_array_equal(res[0][0][t], oi, err_msg=f"t={t}")
+        np.testing.assert_array_equal(res[0][1][t].view(np.uint32), ow.view(np.uint32), err_msg=f"t={t}")
+
+
 def test_experts_from_logits_rejects(big, nh):
     big.synth_layer(25, 4, 1, 0.02)
     lg, x, h, out = big.alloc(64 * 1024), big.alloc(64 * 4096), big.alloc(64 * 8192), big.alloc(64 * 8192)
