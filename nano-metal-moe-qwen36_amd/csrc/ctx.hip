@@ -85,7 +85,10 @@ extern "C" void nmoe_hip_destroy(nmoe_hip_ctx *ctx) {
     hipSetDevice(ctx->device);
     if (ctx->stream != NULL) hipStreamSynchronize(ctx->stream);
     for (int l = 0; l < NMOE_HIP_MAX_LAYERS; l++)
-        if (ctx->packs[l].dev != NULL) hipFree(ctx->packs[l].dev);
+        if (ctx->packs[l].dev != NULL) {
+            hipFree(ctx->packs[l].dev);
+            hipFree(ctx->packs[l].stripes);
+        }
     for (int i = 0; i < ctx->nbufs; i++) hipFree(ctx->bufs[i].dev);
     free(ctx->bufs);
     hipFree(ctx->act);
@@ -322,12 +325,20 @@ static int nmoe_pack_alloc(nmoe_hip_ctx *ctx, int layer, int bits, void **dev_ou
     if (slot->dev != NULL && slot->bytes != bytes) {
         NMOE_HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
         hipFree(slot->dev);
-        slot->dev = NULL;
+        hipFree(slot->stripes);
+        slot->dev = slot->stripes = NULL;
     }
     if (slot->dev == NULL) {
+        /* the pack and its stripe-major copy for the grouped GEMMs */
         if (hipMalloc(&slot->dev, bytes) != hipSuccess) {
             slot->dev = NULL;
             return nmoe_fail(ctx, NMOE_HIP_ENOMEM, "hipMalloc of layer %d pack (%zu bytes) failed", layer, bytes);
+        }
+        if (hipMalloc(&slot->stripes, bytes) != hipSuccess) {
+            hipFree(slot->dev);
+            slot->dev = slot->stripes = NULL;
+            return nmoe_fail(ctx, NMOE_HIP_ENOMEM, "hipMalloc of layer %d stripe-major pack (%zu bytes) failed", layer,
+                             bytes);
         }
     }
     slot->bits = bits;
@@ -348,7 +359,7 @@ extern "C" int nmoe_hip_upload_layer_pack(nmoe_hip_ctx *ctx, int layer, int bits
     int rc = nmoe_pack_alloc(ctx, layer, bits, &dev);
     if (rc != NMOE_HIP_OK) return rc;
     NMOE_HIP_TRY(ctx, hipMemcpy(dev, host, size, hipMemcpyHostToDevice));
-    return NMOE_HIP_OK;
+    return nmoe_pack_stripe(ctx, layer);
 }
 
 extern "C" const void *nmoe_hip_layer_pack(const nmoe_hip_ctx *ctx, int layer, int *bits_out) {
@@ -453,7 +464,7 @@ extern "C" int nmoe_hip_synth_layer_pack(nmoe_hip_ctx *ctx, int layer, int bits,
     hipLaunchKernelGGL(nmoe_synth_scales_kernel, dim3(blocks), dim3(256), 0, ctx->stream, (uint16_t *)dev, seed,
                        (uint32_t)layer, esz / 2u, gs / 2u, us / 2u, ds / 2u, 16384u, sigma, bits);
     NMOE_HIP_TRY(ctx, hipGetLastError());
-    return NMOE_HIP_OK;
+    return nmoe_pack_stripe(ctx, layer);
 }
 
 extern "C" int nmoe_hip_synth_bf16(nmoe_hip_ctx *ctx, uint16_t *dev, size_t n, uint64_t seed, uint32_t layer,

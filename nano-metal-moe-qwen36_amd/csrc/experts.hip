@@ -259,16 +259,20 @@ extern "C" int nmoe_fused_decode(nmoe_hip_ctx *ctx, int bits, int route, const v
                                  uint32_t *idx_out, float *w_out, float *logits_out, const uint8_t *pack,
                                  hipStream_t s);
 
+/* The layer's pack (checked resident, of BITS), by the token count: the
+ * fused single-token launch, the grouped GEMMs (on the stripe-major copy)
+ * or the per-token kernels. */
 template <int BITS>
-static int nmoe_experts_dispatch(nmoe_hip_ctx *ctx, const uint8_t *pack, const void *x, int x_dtype, int ntok, int k,
+static int nmoe_experts_dispatch(nmoe_hip_ctx *ctx, int layer, const void *x, int x_dtype, int ntok, int k,
                                  const uint32_t *idx, const float *w, const float *h_mid, const float *shared_out,
                                  const float *shared_gate_raw, float *out, hipStream_t s) {
+    const uint8_t *pack = (const uint8_t *)ctx->packs[layer].dev;
     if (ntok == 1 && ctx->fused_blocks > 0 && ctx->use_fused)
         return nmoe_fused_decode(ctx, BITS, 0, x, x_dtype, 0.0f, k, NULL, idx, w, h_mid, shared_out, shared_gate_raw,
                                  out, NULL, NULL, NULL, pack, s);
     if (ntok >= ctx->grouped_min_tokens)
-        return nmoe_grouped_experts(ctx, BITS, pack, x, x_dtype, ntok, k, idx, w, h_mid, shared_out, shared_gate_raw,
-                                    out, s);
+        return nmoe_grouped_experts(ctx, BITS, (const uint8_t *)ctx->packs[layer].stripes, x, x_dtype, ntok, k, idx,
+                                    w, h_mid, shared_out, shared_gate_raw, out, s);
     return nmoe_launch_experts<BITS>(ctx, pack, x, x_dtype, ntok, k, idx, w, h_mid, shared_out, shared_gate_raw, out, s);
 }
 
@@ -279,7 +283,7 @@ extern "C" int nmoe_moe_experts_q4(nmoe_hip_ctx *ctx, int layer, const void *x, 
     int rc = nmoe_check_experts(ctx, layer, 4, x, x_dtype, ntok, k, idx, w, h_mid, shared_out, shared_gate_raw, out,
                                 &pack);
     if (rc != NMOE_HIP_OK) return rc;
-    rc = nmoe_experts_dispatch<4>(ctx, pack, x, x_dtype, ntok, k, idx, w, h_mid, shared_out, shared_gate_raw, out,
+    rc = nmoe_experts_dispatch<4>(ctx, layer, x, x_dtype, ntok, k, idx, w, h_mid, shared_out, shared_gate_raw, out,
                                   nmoe_stream_of(ctx, stream));
     return rc != NMOE_HIP_OK ? rc : nmoe_sync_check(ctx, stream);
 }
@@ -291,7 +295,7 @@ extern "C" int nmoe_moe_experts_q2(nmoe_hip_ctx *ctx, int layer, const void *x, 
     int rc = nmoe_check_experts(ctx, layer, 2, x, x_dtype, ntok, k, idx, w, h_mid, shared_out, shared_gate_raw, out,
                                 &pack);
     if (rc != NMOE_HIP_OK) return rc;
-    rc = nmoe_experts_dispatch<2>(ctx, pack, x, x_dtype, ntok, k, idx, w, h_mid, shared_out, shared_gate_raw, out,
+    rc = nmoe_experts_dispatch<2>(ctx, layer, x, x_dtype, ntok, k, idx, w, h_mid, shared_out, shared_gate_raw, out,
                                   nmoe_stream_of(ctx, stream));
     return rc != NMOE_HIP_OK ? rc : nmoe_sync_check(ctx, stream);
 }
@@ -314,14 +318,13 @@ static int nmoe_experts_from_logits_run(nmoe_hip_ctx *ctx, int layer, const floa
                                         const float *shared_gate_raw, float *out, uint32_t *idx, float *w,
                                         hipStream_t s) {
     const int bits = ctx->packs[layer].bits;
-    const uint8_t *pack = (const uint8_t *)ctx->packs[layer].dev;
     if (ntok >= ctx->grouped_min_tokens)
-        return nmoe_grouped_experts_routed(ctx, bits, pack, logits, x, x_dtype, ntok, k, idx, w, h_mid, shared_out,
-                                           shared_gate_raw, out, s);
+        return nmoe_grouped_experts_routed(ctx, bits, (const uint8_t *)ctx->packs[layer].stripes, logits, x, x_dtype,
+                                           ntok, k, idx, w, h_mid, shared_out, shared_gate_raw, out, s);
     NMOE_HIP_TRY(ctx, nmoe_topk_launch(logits, ntok, NMOE_EXPERTS, k, idx, w, NULL, s));
-    return bits == 4 ? nmoe_experts_dispatch<4>(ctx, pack, x, x_dtype, ntok, k, idx, w, h_mid, shared_out,
+    return bits == 4 ? nmoe_experts_dispatch<4>(ctx, layer, x, x_dtype, ntok, k, idx, w, h_mid, shared_out,
                                                 shared_gate_raw, out, s)
-                     : nmoe_experts_dispatch<2>(ctx, pack, x, x_dtype, ntok, k, idx, w, h_mid, shared_out,
+                     : nmoe_experts_dispatch<2>(ctx, layer, x, x_dtype, ntok, k, idx, w, h_mid, shared_out,
                                                 shared_gate_raw, out, s);
 }
 

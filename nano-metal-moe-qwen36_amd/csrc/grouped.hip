@@ -801,20 +801,37 @@ struct nmoe_code_plan {
 template <int BITS>
 __host__ __device__ constexpr int nmoe_gwords() { return BITS == 4 ? 8 : 4; }
 
-/* Instruction j of one stage's codes for one matrix of NR rows, in the
- * stage layout above: gbase is the matrix's first row at the stage's first
- * word (uniform), rows wpr words apart.  A 1-KB instruction covers 64 / LPR
- * rows, LPR lanes a row. */
+/* The grouped GEMMs read a stripe-major copy of each layer's code
+ * matrices (nmoe_pack_stripe): a matrix of rows of wpr words, groups of gw
+ * words, is stored as stripes of NMOE_STRIPE rows, and within a stripe
+ * group g of its rows side by side.  A ring step's codes (one or two
+ * groups of a tile's 32..256 rows) are then runs of NMOE_STRIPE * gw words
+ * (1-2 KB) instead of gw words a row, a row's length apart. */
+#define NMOE_STRIPE 64
+__host__ __device__ __forceinline__ uint32_t nmoe_stripe_word(uint32_t r, uint32_t g, uint32_t gw, uint32_t wpr) {
+    return (r / NMOE_STRIPE) * NMOE_STRIPE * wpr + (g * NMOE_STRIPE + r % NMOE_STRIPE) * gw;
+}
+
+/* Instruction j of one stage's codes for rows row0 .. row0 + NR - 1 of a
+ * stripe-major matrix at mbase, groups
+ * GPS gs .. GPS gs + GPS - 1, in the stage layout above.  A 1-KB
+ * instruction covers 64 / LPR rows, LPR lanes a row. */
 template <int BITS, int NR, bool WIDE, int GPS = 1>
-__device__ __forceinline__ void nmoe_stage_codes(uint32_t *stage, const uint32_t *gbase, int wpr, int j, int lane) {
+__device__ __forceinline__ void nmoe_stage_codes(uint32_t *stage, const uint32_t *mbase, int wpr, int row0, int gs,
+                                                 int j, int lane) {
     using CR = nmoe_code_row<BITS, GPS>;
+    constexpr uint32_t GW = nmoe_gwords<BITS>();
+    const uint32_t *gbase = mbase + (size_t)(GPS * gs) * NMOE_STRIPE * GW; /* the step's first group (uniform) */
     if (WIDE) {
         const int row = (64 / CR::LPR) * j + lane / CR::LPR, part = (lane % CR::LPR) ^ CR::swz(row);
-        nmoe_dma<16>(gbase, 4u * (uint32_t)(row * wpr + 4 * part), stage + 256 * j);
+        const uint32_t u = (16u * part) / (4u * GW), w = ((16u * part) % (4u * GW)) / 4u; /* group of the step, word */
+        nmoe_dma<16>(gbase, 4u * (nmoe_stripe_word((uint32_t)(row0 + row), u, GW, (uint32_t)wpr) + w),
+                     stage + 256 * j);
     } else {
         /* q2, one group: rows 16j + lane / 4, word lane % 4 */
         const int row = 16 * j + (lane >> 2);
-        nmoe_dma<4>(gbase, 4u * (uint32_t)(row * wpr + (lane & 3)), stage + 64 * j);
+        nmoe_dma<4>(gbase, 4u * (nmoe_stripe_word((uint32_t)(row0 + row), 0u, GW, (uint32_t)wpr) + (lane & 3)),
+                    stage + 64 * j);
     }
 }
 
@@ -1055,7 +1072,7 @@ __device__ __forceinline__ void nmoe_gu_tile(const uint8_t *pack, const uint16_t
      * matrix cmat (gate for the first half of the wavefronts, up for the
      * second) */
     const int cmat = wave / (NW / 2);
-    const uint32_t *cbase = (const uint32_t *)(ex + (cmat == 0 ? L::gate_w : L::up_w)) + (size_t)nt * NT * Q::WPR_G;
+    const uint32_t *cbase = (const uint32_t *)(ex + (cmat == 0 ? L::gate_w : L::up_w)); /* stripe-major */
     const uint16_t *bias[2] = {(const uint16_t *)(ex + L::gate_b) + (size_t)nt * NT * G,
                                (const uint16_t *)(ex + L::up_b) + (size_t)nt * NT * G};
 
@@ -1104,9 +1121,8 @@ __device__ __forceinline__ void nmoe_gu_tile(const uint8_t *pack, const uint16_t
                 }
 #pragma unroll
             for (int i = 0; i < CP::PER_WAVE; i++)
-                nmoe_stage_codes<BITS, NT, CP::WIDE, GPS>(stage(st).b + cmat * NT * CR::WPS,
-                                                          cbase + nmoe_gwords<BITS>() * GPS * gs, Q::WPR_G,
-                                                          (CP::PER_WAVE * wave + i) % CPM, lane);
+                nmoe_stage_codes<BITS, NT, CP::WIDE, GPS>(stage(st).b + cmat * NT * CR::WPS, cbase, Q::WPR_G,
+                                                          nt * NT, gs, (CP::PER_WAVE * wave + i) % CPM, lane);
         };
         const int nb = (int)min((n - m0 + 15) / 16, (uint32_t)MB);
         nmoe_f32x4 acc[2][NB][MB];
@@ -1412,7 +1428,7 @@ __device__ __forceinline__ void nmoe_dn_tile(const uint8_t *pack, const uint16_t
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint8_t *ex = pack + (size_t)e * L::expert_size;
     const int rt0 = (NT / NW) * wave + col; /* tile row of column block nb: rt0 + 16 nb */
-    const uint32_t *cbase = (const uint32_t *)(ex + L::down_w) + (size_t)nt * NT * Q::WPR_D;
+    const uint32_t *cbase = (const uint32_t *)(ex + L::down_w); /* stripe-major */
     const uint16_t *bias = (const uint16_t *)(ex + L::down_b) + (size_t)nt * NT * G;
 
     /* the passes of one form: MCH entries a pass, GPS groups a ring step */
@@ -1462,8 +1478,8 @@ __device__ __forceinline__ void nmoe_dn_tile(const uint8_t *pack, const uint16_t
         auto issue_b = [&](int gs, int st) {
 #pragma unroll
             for (int i = 0; i < CP::PER_WAVE; i++)
-                nmoe_stage_codes<BITS, NT, CP::WIDE, GPS>(stage(st).b, cbase + nmoe_gwords<BITS>() * GPS * gs,
-                                                          Q::WPR_D, CP::PER_WAVE * wave + i, lane);
+                nmoe_stage_codes<BITS, NT, CP::WIDE, GPS>(stage(st).b, cbase, Q::WPR_D, nt * NT, gs,
+                                                          CP::PER_WAVE * wave + i, lane);
         };
         auto issue = [&](int gs, int st) {
             issue_a(gs, st);
@@ -1780,6 +1796,49 @@ __global__ void __launch_bounds__(256) nmoe_grouped_combine_kernel(const float *
     }
     if (nmoe_status_set(status)) o[0] = o[1] = o[2] = o[3] = __builtin_nanf("");
     *(float4 *)(out + (size_t)t * NMOE_HIDDEN + r) = make_float4(o[0], o[1], o[2], o[3]);
+}
+
+/* ------------------------------------------------------------ stripes */
+
+/* dst = src with each expert's three code matrices stripe-major
+ * (nmoe_stripe_word) and everything else (scales, biases) in place: one
+ * 16-byte word a thread, which never straddles a group (q4 groups are 32
+ * bytes, q2 16).  The matrices all hold wpm words: gate and up 512 rows,
+ * down 2,048 rows. */
+template <int BITS>
+__global__ void __launch_bounds__(256) nmoe_stripe_kernel(const uint4 *src, uint4 *dst) {
+    using L = nmoe_layout<BITS>;
+    using Q = nmoe_q<BITS>;
+    constexpr uint32_t E16 = L::expert_size / 16u, GW = nmoe_gwords<BITS>();
+    const uint32_t mat[3] = {L::gate_w, L::up_w, L::down_w};
+    const uint32_t wpr[3] = {(uint32_t)Q::WPR_G, (uint32_t)Q::WPR_G, (uint32_t)Q::WPR_D};
+    constexpr uint32_t MW = (uint32_t)NMOE_INTER * Q::WPR_G; /* words a matrix */
+    static_assert((uint32_t)NMOE_HIDDEN * Q::WPR_D == MW, "three matrices of the same size");
+    const uint64_t n = (uint64_t)NMOE_EXPERTS * E16;
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (uint64_t)gridDim.x * blockDim.x) {
+        const uint32_t e = (uint32_t)(i / E16), b = 16u * (uint32_t)(i % E16); /* expert, byte in the expert */
+        uint32_t to = b;
+#pragma unroll
+        for (int m = 0; m < 3; m++)
+            if (b >= mat[m] && b < mat[m] + 4u * MW) {
+                const uint32_t wd = (b - mat[m]) / 4u, r = wd / wpr[m], c = wd % wpr[m];
+                to = mat[m] + 4u * (nmoe_stripe_word(r, c / GW, GW, wpr[m]) + c % GW);
+            }
+        dst[(uint64_t)e * E16 + to / 16u] = src[i];
+    }
+}
+
+int nmoe_pack_stripe(nmoe_hip_ctx *ctx, int layer) {
+    const nmoe_pack_slot *slot = &ctx->packs[layer];
+    const dim3 grid(ctx->num_cus * 8);
+    if (slot->bits == 4)
+        hipLaunchKernelGGL(nmoe_stripe_kernel<4>, grid, dim3(256), 0, ctx->stream, (const uint4 *)slot->dev,
+                           (uint4 *)slot->stripes);
+    else
+        hipLaunchKernelGGL(nmoe_stripe_kernel<2>, grid, dim3(256), 0, ctx->stream, (const uint4 *)slot->dev,
+                           (uint4 *)slot->stripes);
+    NMOE_HIP_TRY(ctx, hipGetLastError());
+    return NMOE_HIP_OK;
 }
 
 /* ------------------------------------------------------------ host */

@@ -68,7 +68,8 @@ struct nmoe_block_ext {
 };
 
 struct nmoe_pack_slot {
-    void *dev;
+    void *dev;     /* the layer's pack as uploaded (256 experts, row-major codes) */
+    void *stripes; /* the same pack with stripe-major codes, read by the grouped GEMMs */
     int bits;
     size_t bytes;
 };
@@ -151,6 +152,8 @@ int nmoe_hip_check(nmoe_hip_ctx *ctx, hipError_t e, const char *what);
 /* The next n timeline slots of the context (NMOE_TIMELINE builds; NULL
  * when no timeline buffer is set). */
 uint64_t *nmoe_tl_take(nmoe_hip_ctx *ctx, int n);
+/* Writes the stripe-major copy of layer's pack (after every write of the pack). */
+int nmoe_pack_stripe(nmoe_hip_ctx *ctx, int layer);
 
 #define NMOE_HIP_TRY(ctx, call)                                   \
     do {                                                          \

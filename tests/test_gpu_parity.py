@@ -701,6 +701,47 @@ def test_grouped_small_and_big_forms(big, nh, bits, xkind):
 
 
 @pytest.mark.parametrize("bits", [4, 2])
+def test_grouped_on_uploaded_layer_and_reupload(big, nh, bits):
+    """The grouped GEMMs read the layer's stripe-major copy, written on the
+    device after every upload: a layer uploaded from the host, then the
+    same layer uploaded again with other experts (and then synthesised on
+    the device over it), each time every token against the oracle on the
+    pack just written, never on the one before."""
+    rng = np.random.default_rng(810 + bits)
+    layer, ntok, k = 50 + bits, 24, 8
+    idx = np.zeros((ntok, 8), np.uint32)
+    for t in range(ntok):
+        idx[t, :k] = rng.choice(256, k, replace=False)
+    w = rng.dirichlet(np.ones(k), size=ntok).astype(np.float32)
+    x = rng.standard_normal((ntok, 2048)).astype(np.float32)
+    h = rng.standard_normal((ntok, 2048)).astype(np.float32)
+    d = [big.to_device(a) for a in (x, idx, w, h)]
+
+    def run():
+        out = big.alloc(ntok * 2048 * 4)
+        big._check(big.experts(bits, layer, d[0], nh.F32, ntok, k, d[1], d[2], d[3], out))
+        return (out.download(np.float32, (ntok, 2048)),)
+
+    try:
+        big.set_grouped_min_tokens(1)
+        for step, seed in enumerate((33, 34, None)):
+            if seed is None:  # synthesised on the device over the uploaded layer
+                seed = 35
+                big.synth_layer(layer, bits, seed, SIGMA[bits])
+                pack = host_pack(bits, seed, layer, idx[:, :k].ravel())
+            else:
+                pack = host_pack(bits, seed, layer, idx[:, :k].ravel())
+                big.upload_layer(layer, bits, pack)
+            got = run_forms(big, run)[0]
+            assert big.device_status() == nh.OK
+            want = B.moe_experts(pack, bits, x, k, idx, w, h)
+            assert_close(got, want, what=f"q{bits} layer written {step + 1} times (seed {seed})")
+            del pack
+    finally:
+        big.set_grouped_min_tokens(8)
+
+
+@pytest.mark.parametrize("bits", [4, 2])
 def test_prefill_2048_sampled(big, nh, bits):
     """C5 shape: 2048 tokens, uniform-random logits -> device top-8 ->
     grouped experts; routing bit-exact for all 2048 tokens, outputs checked
