@@ -174,7 +174,12 @@ NMOE_HIP_API int nmoe_hip_copy_to_host(nmoe_hip_ctx *ctx, void *host, const void
 /* ---- expert packs (expert_io.h:21-24; runtime.m:2426-2465 NMOELoadExpertLayer).
  * A layer pack is the layer_XX.bin bytes unchanged: 256 experts of
  * nmoe_hip_expert_size(bits) bytes each, component offsets as
- * convert_qwen36.py:38-64.  Packs stay resident in HBM until destroy. */
+ * convert_qwen36.py:38-64.  Packs stay resident in HBM until destroy.
+ * Each resident layer also holds a second copy of the same size, written on
+ * the device after every upload or synthesis, whose code matrices the
+ * grouped (many-token) path reads stripe-major: a layer takes twice its
+ * pack's bytes of device memory (ENOMEM when either does not fit), and the
+ * pack must be changed only through these calls. */
 NMOE_HIP_API size_t nmoe_hip_expert_size(int bits);
 NMOE_HIP_API int nmoe_hip_upload_layer_pack(nmoe_hip_ctx *ctx, int layer, int bits, const void *host, size_t size);
 NMOE_HIP_API int nmoe_hip_load_layer_file(nmoe_hip_ctx *ctx, int layer, int bits, const char *path);
@@ -195,7 +200,8 @@ NMOE_HIP_API int nmoe_hip_validate_layout(const char *layout_json_path, int *bit
  * layers_out (nullable) receive the quantisation and the layers loaded. */
 NMOE_HIP_API int nmoe_hip_load_expert_dir(nmoe_hip_ctx *ctx, const char *dir, int nlayers, int *bits_out,
                                           int *layers_out);
-/* Device address of a resident layer pack (NULL if absent). */
+/* Device address of a resident layer pack (NULL if absent), read-only: the
+ * bytes as uploaded, not the grouped path's stripe-major copy. */
 NMOE_HIP_API const void *nmoe_hip_layer_pack(const nmoe_hip_ctx *ctx, int layer, int *bits_out);
 /* Allocates layer `layer` and fills it with the repository's synthetic
  * generator (counter-based SplitMix64; codes uniform, scales bf16 of an
