@@ -381,13 +381,8 @@ __device__ __forceinline__ void nmoe_dispatch_scatter(const nmoe_entry_src &src,
     const int bk = 63 - (int)min((total + 15u) / 16u, 63u);
     if (b == 0) atomicAdd(&sl.bk[bk], 1u);
     /* exclusive scan of total over the 256 experts: an inclusive scan within
-     * each wavefront (six shuffles), then the earlier wavefronts' totals */
-    uint32_t inc = total;
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-        const uint32_t v = (uint32_t)__shfl_up((int)inc, d, 64);
-        inc += lane >= d ? v : 0u;
-    }
+     * each wavefront (DPP), then the earlier wavefronts' totals */
+    const uint32_t inc = nmoe_wave_incl_scan_u32(total);
     if (lane == 63) s_scan[wave] = inc;
     /* the stable order within an expert is (chunk of 256, wavefront, lane):
      * the first NMOE_DISPATCH_PRE chunks (their entries in ev) at once,
@@ -396,9 +391,12 @@ __device__ __forceinline__ void nmoe_dispatch_scatter(const nmoe_entry_src &src,
     uint32_t rk[NMOE_DISPATCH_PRE];
 #pragma unroll
     for (int j = 0; j < NMOE_DISPATCH_PRE; j++) {
-        uint32_t cnt;
-        rk[j] = nmoe_multisplit9(ev[j], lane, cnt);
-        if (rk[j] == 0u) sl.wc[j][wave][ev[j]] = cnt;
+        rk[j] = 0u;
+        if (q0 + 256 * j < q1) { /* (block-uniform) a chunk with entries */
+            uint32_t cnt;
+            rk[j] = nmoe_multisplit9(ev[j], lane, cnt);
+            if (rk[j] == 0u) sl.wc[j][wave][ev[j]] = cnt;
+        }
     }
     __syncthreads();
     uint32_t prior = 0;
@@ -421,12 +419,7 @@ __device__ __forceinline__ void nmoe_dispatch_scatter(const nmoe_entry_src &src,
         if (tid == 255) offsets[NMOE_EXPERTS] = off + total;
         if (tid < 64) { /* exclusive scan of the 64 bucket sizes (one wavefront) */
             const uint32_t c = sl.bk[tid];
-            uint32_t binc = c;
-#pragma unroll
-            for (int d = 1; d < 64; d <<= 1) {
-                const uint32_t v = (uint32_t)__shfl_up((int)binc, d, 64);
-                binc += lane >= d ? v : 0u;
-            }
+            const uint32_t binc = nmoe_wave_incl_scan_u32(c);
             sl.bk[tid] = binc - c;
             static_assert(NMOE_SMALL_PASS == 16, "bucket 62 holds the experts of one small pass");
             if (tid == 62) s_nbig = binc - c;

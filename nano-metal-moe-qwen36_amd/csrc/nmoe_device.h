@@ -98,6 +98,20 @@ __device__ __forceinline__ uint32_t nmoe_wave_max_u32(uint32_t v) {
     return max(max(r0, r1), max(r2, r3));
 }
 
+/* Inclusive prefix sum over the wavefront's 64 lanes by DPP: row_shr 1, 2,
+ * 4, 8 scan each row of 16 lanes (a lane with no source adds 0), then
+ * row_bcast:15 adds each even row's total to the row after it and
+ * row_bcast:31 the first two rows' total to the last two (gfx9 controls). */
+__device__ __forceinline__ uint32_t nmoe_wave_incl_scan_u32(uint32_t v) {
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x111, 0xF, 0xF, false); /* row_shr:1 */
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x112, 0xF, 0xF, false); /* row_shr:2 */
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x114, 0xF, 0xF, false); /* row_shr:4 */
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x118, 0xF, 0xF, false); /* row_shr:8 */
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x142, 0xA, 0xF, false); /* row_bcast:15, rows 1, 3 */
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x143, 0xC, 0xF, false); /* row_bcast:31, rows 2, 3 */
+    return v;
+}
+
 template <int CTRL>
 __device__ __forceinline__ uint64_t nmoe_dpp_u64(uint64_t v) {
     return ((uint64_t)nmoe_dpp_u<CTRL>((uint32_t)(v >> 32)) << 32) | nmoe_dpp_u<CTRL>((uint32_t)v);
