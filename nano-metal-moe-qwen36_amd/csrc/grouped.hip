@@ -1831,6 +1831,9 @@ int nmoe_pack_stripe(nmoe_hip_ctx *ctx, int layer) {
         hipLaunchKernelGGL(nmoe_stripe_kernel<2>, grid, dim3(256), 0, ctx->stream, (const uint4 *)slot->dev,
                            (uint4 *)slot->stripes);
     NMOE_HIP_TRY(ctx, hipGetLastError());
+    /* complete before the call returns, as the upload's copy is: a grouped
+     * call may follow on any stream */
+    NMOE_HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
     return NMOE_HIP_OK;
 }
 

@@ -152,7 +152,8 @@ int nmoe_hip_check(nmoe_hip_ctx *ctx, hipError_t e, const char *what);
 /* The next n timeline slots of the context (NMOE_TIMELINE builds; NULL
  * when no timeline buffer is set). */
 uint64_t *nmoe_tl_take(nmoe_hip_ctx *ctx, int n);
-/* Writes the stripe-major copy of layer's pack (after every write of the pack). */
+/* Writes the stripe-major copy of layer's pack (after every write of the
+ * pack) and waits for it. */
 int nmoe_pack_stripe(nmoe_hip_ctx *ctx, int layer);
 
 #define NMOE_HIP_TRY(ctx, call)                                   \
