@@ -371,7 +371,8 @@ __device__ __forceinline__ uint32_t nmoe_fkey(float f) {
  * lane L belongs to entry L + 64 j; 0 = absent), in decreasing key order,
  * ties to the lower entry -- the selection rule of math.m:95-132.  Per
  * round: the wave maximum, then the lowest entry holding it from the
- * compare masks (lowest j with a hit, then its lowest lane).  Consumes key;
+ * compare masks (lowest j with a hit, then its lowest lane); keys all below
+ * 2^30 take the shorter rounds of the first branch.  Consumes key;
  * uniform results, slots >= n zero; hook(s, entry) runs after round s. */
 struct nmoe_no_round_hook {
     __device__ void operator()(int, uint32_t) const {}
@@ -381,6 +382,48 @@ template <typename Hook = nmoe_no_round_hook>
 __device__ __forceinline__ void nmoe_wave_top_keys(uint32_t key[4], int n, uint32_t sel[NMOE_MAX_K],
                                                    uint32_t selkey[NMOE_MAX_K], Hook hook = Hook()) {
     const int lane = threadIdx.x & 63;
+    if (__ballot((key[0] | key[1] | key[2] | key[3]) >= (1u << 30)) == 0) {
+        /* Every key below 2^30 (probability keys are, unless NaN): the
+         * slot j goes into two free low bits as 3 - j, so a lane's keys are
+         * distinct and a tie between slots goes to the lower one (the lower
+         * entry, as entry = lane + 64 j); kept sorted, a round is one wave
+         * maximum of the lanes' first keys and one ballot for the lowest
+         * lane holding it.  The same selection as the rounds below. */
+        uint32_t kk[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) kk[j] = key[j] == 0u ? 0u : (key[j] << 2) | (uint32_t)(3 - j);
+        auto ce = [](uint32_t &a, uint32_t &b) {
+            const uint32_t hi = max(a, b), lo = min(a, b);
+            a = hi;
+            b = lo;
+        };
+        ce(kk[0], kk[1]);
+        ce(kk[2], kk[3]);
+        ce(kk[0], kk[2]);
+        ce(kk[1], kk[3]);
+        ce(kk[1], kk[2]);
+#pragma unroll
+        for (int s = 0; s < NMOE_MAX_K; s++) {
+            sel[s] = 0;
+            selkey[s] = 0;
+            if (s < n) {
+                const uint32_t best = nmoe_wave_max_u32(kk[0]);
+                const uint64_t m = __ballot(kk[0] == best);
+                const uint32_t l0 = (uint32_t)__ffsll((unsigned long long)m) - 1u;
+                const uint32_t win = l0 + 64u * (3u - (best & 3u));
+                if ((uint32_t)lane == l0) {
+                    kk[0] = kk[1];
+                    kk[1] = kk[2];
+                    kk[2] = kk[3];
+                    kk[3] = 0u;
+                }
+                sel[s] = win;
+                selkey[s] = best >> 2;
+                hook(s, win);
+            }
+        }
+        return;
+    }
 #pragma unroll
     for (int s = 0; s < NMOE_MAX_K; s++) {
         sel[s] = 0;
