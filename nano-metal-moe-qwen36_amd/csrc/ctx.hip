@@ -227,9 +227,8 @@ extern "C" int nmoe_hip_check_device_status(nmoe_hip_ctx *ctx) {
                 if (words[NMOE_SYNC_EPOCH(b)] > top) top = words[NMOE_SYNC_EPOCH(b)];
             for (int b = 0; b < NMOE_SYNC_BLOCKS; b++) words[NMOE_SYNC_EPOCH(b)] = top + 1u;
             words[NMOE_SYNC_STATUS] = 0u;
-            words[NMOE_SYNC_DISPATCH] = 0u; /* a part-counted dispatch round restarts */
-            /* routed entries of the aborted launch may carry the epoch after
-             * it: the next launch takes one past that */
+            /* routed entries and histogram words of the aborted launch may
+             * carry the epoch after it: the next launch takes one past that */
             words[NMOE_SYNC_PREP_EPOCH] += 2u;
             e = hipMemcpy(ctx->sync, words, NMOE_SYNC_WORDS * sizeof(uint32_t), hipMemcpyHostToDevice);
         }

@@ -54,13 +54,16 @@ typedef __attribute__((ext_vector_type(8))) __bf16 nmoe_bf16x8;
 typedef __attribute__((ext_vector_type(4))) float nmoe_f32x4;
 
 /* Dispatch blocks: one up to 1,024 entries (its histogram never leaves
- * LDS), else a power of two up to 64 so that a slice is one 256-entry chunk
- * while the entries fit (16,384 of them). */
+ * LDS), else a power of two up to 64 so that a slice is at most four
+ * 256-entry chunks (the ones a block multi-splits at once) while the
+ * entries fit (65,536 of them).  Each block reads the others' histogram
+ * words 16 slices at a time: one round up to 16,384 entries. */
 #define NMOE_DISPATCH_MAX 64
+#define NMOE_DISPATCH_READ 16
 __host__ __device__ constexpr int nmoe_dispatch_blocks(int n) {
     if (n <= 1024) return 1;
-    int nd = 8;
-    while (nd < NMOE_DISPATCH_MAX && nd * 256 < n) nd *= 2;
+    int nd = 2;
+    while (nd < NMOE_DISPATCH_MAX && nd * 1024 < n) nd *= 2;
     return nd;
 }
 #define NMOE_MCHUNK 64 /* expert rows (entries) per pass: four 16-row MFMA blocks */
@@ -342,8 +345,8 @@ __device__ __forceinline__ uint32_t nmoe_multisplit9(uint32_t e, int lane, uint3
  * chunks of 256 entries in order; within a chunk the rank of an entry is
  * its rank among the equal-expert lanes of its wavefront (a 9-bit
  * multi-split by ballots) plus the counts of the earlier wavefronts. */
-template <bool ROUTED>
-__device__ __forceinline__ void nmoe_dispatch_scatter(const nmoe_entry_src &src, int ntok, uint32_t *counts,
+template <bool ROUTED, bool MULTI>
+__device__ __forceinline__ void nmoe_dispatch_scatter(const nmoe_entry_src &src, int ntok, const uint64_t *counts,
                                                       const uint32_t *h, uint32_t *perm, uint32_t *offsets,
                                                       uint4 *rank, int b, int nd, const uint32_t *ev, uint32_t r1,
                                                       nmoe_scatter_lds &sl) {
@@ -352,23 +355,47 @@ __device__ __forceinline__ void nmoe_dispatch_scatter(const nmoe_entry_src &src,
     __shared__ uint32_t s_nbig;    /* the experts of more than one small pass */
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, n = ntok * src.k;
     const int per = (n + nd - 1) / nd, q0 = b * per, q1 = min(n, (b + 1) * per);
-    /* thread e: total of expert e and its count in the slices before b.  All
-     * NMOE_DISPATCH_MAX slices are loaded at once (the buffer holds that
-     * many; those at nd and above are masked), so the loads are in flight
-     * together rather than one latency each. */
+    /* thread e: total of expert e and its count in the slices before b,
+     * from every slice's histogram word of expert e, tagged with the
+     * launch's epoch: NMOE_DISPATCH_READ slices' loads in flight at once,
+     * then the words still without the epoch read again in one round
+     * (bounded) */
     uint32_t total = 0, before = 0;
-    if (nd == 1) {
+    if constexpr (!MULTI) {
         total = h[tid];
     } else {
-        uint32_t cs[NMOE_DISPATCH_MAX];
+        uint32_t spins = 0;
+        for (int b0 = 0; b0 < nd; b0 += NMOE_DISPATCH_READ) {
+            uint64_t w[NMOE_DISPATCH_READ];
 #pragma unroll
-        for (int bb = 0; bb < NMOE_DISPATCH_MAX; bb++) cs[bb] = nmoe_ld_u32_dev(&counts[bb * (NMOE_EXPERTS + 1) + tid]);
+            for (int i = 0; i < NMOE_DISPATCH_READ; i++)
+                w[i] = b0 + i < nd ? nmoe_ld_tagged(counts + (b0 + i) * NMOE_EXPERTS + tid) : (uint64_t)src.epoch << 32;
+            for (;;) {
+                bool seen = true;
 #pragma unroll
-        for (int bb = 0; bb < NMOE_DISPATCH_MAX; bb++) {
-            const uint32_t c = bb < nd ? cs[bb] : 0u;
-            total += c;
-            before += bb < b ? c : 0u;
+                for (int i = 0; i < NMOE_DISPATCH_READ; i++) seen = seen && nmoe_tag_is(w[i], src.epoch);
+                if (seen) break;
+                if (++spins > src.spin) {
+                    __hip_atomic_store((nmoe_g32 *)(src.sync + NMOE_SYNC_STATUS), 1u, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+                for (int i = 0; i < NMOE_DISPATCH_READ; i++)
+                    if (!nmoe_tag_is(w[i], src.epoch)) w[i] = nmoe_ld_tagged(counts + (b0 + i) * NMOE_EXPERTS + tid);
+            }
+#pragma unroll
+            for (int i = 0; i < NMOE_DISPATCH_READ; i++) {
+                const uint32_t c = b0 + i < nd ? (uint32_t)w[i] : 0u;
+                total += c;
+                before += b0 + i < b ? c : 0u;
+            }
         }
+        /* every slice read its entries, and with them every routing block
+         * this launch's epoch, before it published its histogram: the next
+         * launch takes the next epoch */
+        if (b == 0 && tid == 0) nmoe_add_u32_dev(src.sync + NMOE_SYNC_PREP_EPOCH, 1u);
     }
     /* the experts by work, most first: bucket = 16-entry row blocks (63 and
      * more together), a counting sort over the buckets, any order within
@@ -429,7 +456,7 @@ __device__ __forceinline__ void nmoe_dispatch_scatter(const nmoe_entry_src &src,
 #pragma unroll
     for (int j = 0; j < NMOE_DISPATCH_PRE; j++) {
         const int q = q0 + 256 * j + tid;
-        /* pos < n unless the slices' meeting gave up (then the counts of the
+        /* pos < n unless the wait for the slices' histograms gave up (then the counts of the
          * other slices may be stale and the launch reports it) */
         if (q < q1 && ev[j] < (uint32_t)NMOE_EXPERTS) {
             const uint32_t pos = sl.wc[j][wave][ev[j]] + rk[j];
@@ -524,19 +551,6 @@ __device__ __forceinline__ void nmoe_grouped_xprep(const XT *x, uint16_t *xhi, u
 
 static __constant__ uint64_t nmoe_grouped_exp2_tab[32] = NMOE_EXP2_TAB32;
 
-/* Bounded wait until *cnt reaches target (thread 0); an expired wait sets
- * the status word. */
-__device__ __forceinline__ void nmoe_wait_count(uint32_t *cnt, uint32_t target, uint32_t *sync, uint32_t spin) {
-    uint32_t spins = 0;
-    while ((int32_t)(nmoe_ld_u32_dev(cnt) - target) < 0) {
-        __builtin_amdgcn_s_sleep(1);
-        if (++spins > spin) {
-            __hip_atomic_store((nmoe_g32 *)(sync + NMOE_SYNC_STATUS), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            break;
-        }
-    }
-}
-
 /* The one-launch GEMM's schedule words (zeroed by the preparation launch):
  * done[256], per expert rank, counts the gate/up tiles whose act rows are
  * stored; each adds 1 + 2^(16 + its die). */
@@ -592,9 +606,9 @@ __device__ __forceinline__ void nmoe_wait_tiles(uint32_t *cnt, uint32_t n, uint3
  * entries have been read (they were all written by then, so no block of
  * this launch can read the new value), and tagged words of earlier launches
  * carry earlier epochs, so none is taken for this launch's. */
-template <int BITS, typename XT, bool ROUTED>
+template <int BITS, typename XT, bool ROUTED, bool MULTI>
 __global__ void __launch_bounds__(256) nmoe_grouped_prep_kernel(const uint32_t *idx, int ntok, int k, int nd,
-                                                                uint32_t *counts, uint32_t *perm, uint32_t *offsets,
+                                                                uint64_t *counts, uint32_t *perm, uint32_t *offsets,
                                                                 uint4 *rank, uint32_t *sync, uint32_t spin,
                                                                 const XT *x, uint16_t *xhi, uint16_t *xlo,
                                                                 uint16_t *xs3, const float *logits, uint32_t *idx_out,
@@ -602,8 +616,9 @@ __global__ void __launch_bounds__(256) nmoe_grouped_prep_kernel(const uint32_t *
                                                                 uint64_t *tags, uint64_t *tl) {
     const int b = blockIdx.x;
     nmoe_gtl_begin(tl);
-    /* this launch's epoch of the tagged entries (read at once by every block) */
-    const uint32_t epoch = ROUTED ? nmoe_ld_u32_dev(sync + NMOE_SYNC_PREP_EPOCH) + 1u : 0u;
+    /* this launch's epoch of the tagged entries and histogram words (read
+     * at once by every block) */
+    const uint32_t epoch = ROUTED || MULTI ? nmoe_ld_u32_dev(sync + NMOE_SYNC_PREP_EPOCH) + 1u : 0u;
     /* the one-launch GEMM's tile counts start from 0 (plain stores: the next
      * launch on the stream sees them); rank `skew` (a test of the failure
      * path) from a count no tiles can reach */
@@ -669,33 +684,23 @@ __global__ void __launch_bounds__(256) nmoe_grouped_prep_kernel(const uint32_t *
     __shared__ uint32_t h[NMOE_EXPERTS + 1];
     __shared__ nmoe_scatter_lds s_scat;
     nmoe_dispatch_count<ROUTED>(src, ntok, h, b, nd, ev, s_scat);
-    /* every entry of this slice read (one slice), or of every slice (after
-     * the meeting below): the next launch takes the next epoch */
-    if (ROUTED && nd == 1 && threadIdx.x == 0) nmoe_add_u32_dev(sync + NMOE_SYNC_PREP_EPOCH, 1u);
-    if (nd > 1) {
-        /* publish the histogram with device-coherent stores, completed
-         * (vmcnt 0) before the arrival is counted: no agent-scope release
-         * fence, whose L2 writeback would wait for every dirty line of the
-         * die (the x planes the other blocks are writing) */
-        for (int i = threadIdx.x; i <= NMOE_EXPERTS; i += 256)
-            __hip_atomic_store((nmoe_g32 *)&counts[b * (NMOE_EXPERTS + 1) + i], h[i], __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
-        __builtin_amdgcn_s_waitcnt(0x0F70); /* vmcnt(0) */
-        __syncthreads();
-        if (threadIdx.x == 0) {
-            uint32_t *cnt = sync + NMOE_SYNC_DISPATCH;
-            const uint32_t old = nmoe_add_u32_dev(cnt, (uint32_t)(NMOE_DISPATCH_MAX / nd));
-            const uint32_t target = (old / NMOE_DISPATCH_MAX + 1u) * NMOE_DISPATCH_MAX;
-            nmoe_wait_count(cnt, target, sync, spin);
-            if (ROUTED && b == 0) nmoe_add_u32_dev(sync + NMOE_SYNC_PREP_EPOCH, 1u);
-        }
-        __syncthreads(); /* (the histograms are then read with device-coherent loads) */
-    }
+    /* every entry of the one slice read: the next launch takes the next
+     * epoch (with several slices, dispatch block 0 advances it once every
+     * slice's histogram is in) */
+    if (ROUTED && !MULTI && threadIdx.x == 0) nmoe_add_u32_dev(sync + NMOE_SYNC_PREP_EPOCH, 1u);
+    if constexpr (MULTI)
+        /* this slice's histogram for the other slices, each word tagged with
+         * the launch's epoch (device-coherent stores): a reader takes a word
+         * once it carries the epoch, so nothing waits for these stores and
+         * no arrival is counted */
+        for (int i = threadIdx.x; i < NMOE_EXPERTS; i += 256)
+            __hip_atomic_store((nmoe_g64 *)&counts[b * NMOE_EXPERTS + i], ((uint64_t)epoch << 32) | h[i],
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     /* experts whose gate/up tiles fill one die's first round: 32 CUs a
      * die, two four-wavefront blocks a CU (one of eight) */
     constexpr uint32_t R1 =
         (256u / NMOE_GROUPED_NW) / (uint32_t)(NMOE_INTER / nmoe_gu_rows(sizeof(XT) == 2 ? 1 : 2, NMOE_GROUPED_NW));
-    nmoe_dispatch_scatter<ROUTED>(src, ntok, counts, h, perm, offsets, rank, b, nd, ev, R1, s_scat);
+    nmoe_dispatch_scatter<ROUTED, MULTI>(src, ntok, counts, h, perm, offsets, rank, b, nd, ev, R1, s_scat);
     nmoe_gtl_prep_end(tl, 4);
 }
 
@@ -1051,7 +1056,7 @@ __device__ __forceinline__ void nmoe_gu_tile(const uint8_t *pack, const uint16_t
     constexpr int NB = NT / (16 * NW);          /* column blocks per wavefront and matrix */
     constexpr int NTH = 64 * NW;
     typedef typename nmoe_gu_lds_types<BITS, XPL, NW>::StageU StageU;
-    /* (e, first entry, entries) of a dispatch whose meeting gave up can be
+    /* (e, first entry, entries) of a dispatch whose histogram wait gave up can be
      * anything; the clamps keep every access inside the buffers */
     const uint4 rk = nmoe_rank_entry(rank, es);
     const int e = (int)min(rk.x, (uint32_t)(NMOE_EXPERTS - 1));
@@ -1842,7 +1847,7 @@ int nmoe_pack_stripe(nmoe_hip_ctx *ctx, int layer) {
 extern "C" int nmoe_grouped_init(nmoe_hip_ctx *ctx) {
     const size_t mt = (size_t)ctx->max_tokens, rows = mt * NMOE_MAX_K;
     ctx->grouped_min_tokens = 8;
-    if (hipMalloc((void **)&ctx->g_counts, NMOE_DISPATCH_MAX * (NMOE_EXPERTS + 1) * sizeof(uint32_t)) != hipSuccess ||
+    if (hipMalloc((void **)&ctx->g_counts, NMOE_DISPATCH_MAX * NMOE_EXPERTS * sizeof(uint64_t)) != hipSuccess ||
         hipMalloc((void **)&ctx->g_perm, rows * sizeof(uint32_t)) != hipSuccess ||
         hipMalloc((void **)&ctx->g_offsets, (NMOE_EXPERTS + 1) * sizeof(uint32_t)) != hipSuccess ||
         hipMalloc((void **)&ctx->g_rank, 2 * NMOE_EXPERTS * 4 * sizeof(uint32_t)) != hipSuccess ||
@@ -1858,9 +1863,10 @@ extern "C" int nmoe_grouped_init(nmoe_hip_ctx *ctx) {
         return NMOE_HIP_ENOMEM;
     ctx->grouped_one_launch = ctx->xcd_placed;
     ctx->skew_tiles = -1;
-    /* the dispatch's words start in range: a launch whose slices' meeting
-     * gives up then reads zeros, never uninitialised counts */
-    if (hipMemset(ctx->g_counts, 0, NMOE_DISPATCH_MAX * (NMOE_EXPERTS + 1) * sizeof(uint32_t)) != hipSuccess ||
+    /* the dispatch's words start in range (epoch 0, which no launch takes):
+     * a launch whose wait for the slices' histograms gives up then reads
+     * zeros, never uninitialised counts */
+    if (hipMemset(ctx->g_counts, 0, NMOE_DISPATCH_MAX * NMOE_EXPERTS * sizeof(uint64_t)) != hipSuccess ||
         hipMemset(ctx->g_perm, 0, rows * sizeof(uint32_t)) != hipSuccess ||
         hipMemset(ctx->g_offsets, 0, (NMOE_EXPERTS + 1) * sizeof(uint32_t)) != hipSuccess ||
         hipMemset(ctx->g_rank, 0, 2 * NMOE_EXPERTS * 4 * sizeof(uint32_t)) != hipSuccess ||
@@ -1882,11 +1888,17 @@ extern "C" void nmoe_grouped_free(nmoe_hip_ctx *ctx) {
 extern "C" int nmoe_grouped_dispatch(nmoe_hip_ctx *ctx, const uint32_t *idx, int ntok, int k, uint32_t *perm,
                                      uint32_t *offsets, hipStream_t s) {
     const int nd = nmoe_dispatch_blocks(ntok * k);
-    hipLaunchKernelGGL((nmoe_grouped_prep_kernel<4, uint16_t, false>), dim3(nd), dim3(256), 0, s, idx, ntok, k, nd,
-                       ctx->g_counts, perm, offsets, (uint4 *)ctx->g_rank, ctx->sync, ctx->spin_limit,
-                       (const uint16_t *)NULL, (uint16_t *)NULL, (uint16_t *)NULL, (uint16_t *)NULL,
-                       (const float *)NULL, (uint32_t *)NULL, (float *)NULL, (uint32_t *)NULL, -1, (uint64_t *)NULL,
-                       (uint64_t *)NULL);
+#define NMOE_DISPATCH_LAUNCH(M)                                                                                        \
+    hipLaunchKernelGGL((nmoe_grouped_prep_kernel<4, uint16_t, false, M>), dim3(nd), dim3(256), 0, s, idx, ntok, k, nd, \
+                       ctx->g_counts, perm, offsets, (uint4 *)ctx->g_rank, ctx->sync, ctx->spin_limit,                 \
+                       (const uint16_t *)NULL, (uint16_t *)NULL, (uint16_t *)NULL, (uint16_t *)NULL,                   \
+                       (const float *)NULL, (uint32_t *)NULL, (float *)NULL, (uint32_t *)NULL, -1, (uint64_t *)NULL,    \
+                       (uint64_t *)NULL)
+    if (nd > 1)
+        NMOE_DISPATCH_LAUNCH(true);
+    else
+        NMOE_DISPATCH_LAUNCH(false);
+#undef NMOE_DISPATCH_LAUNCH
     const hipError_t e = hipGetLastError();
     return e == hipSuccess ? NMOE_HIP_OK : nmoe_hip_check(ctx, e, "dispatch launch");
 }
@@ -1914,10 +1926,18 @@ static int nmoe_grouped_run(nmoe_hip_ctx *ctx, const uint8_t *pack, const void *
     if (one) ctx->skew_tiles = -1;
     /* timeline builds: 4 stamps a block of the preparation launch */
     uint64_t *tlp = nmoe_tl_take(ctx, (int)((4 * (size_t)gprep.x + NMOE_TL_SLOT_WORDS - 1) / NMOE_TL_SLOT_WORDS));
-#define NMOE_PREP(XT, R, XLO)                                                                                         \
-    hipLaunchKernelGGL((nmoe_grouped_prep_kernel<BITS, XT, R>), gprep, dim3(256), 0, s, idx, ntok, k, nd, ctx->g_counts, \
-                       ctx->g_perm, ctx->g_offsets, (uint4 *)ctx->g_rank, ctx->sync, ctx->spin_limit, (const XT *)x,  \
-                       ctx->g_xhi, XLO, ctx->g_xs, logits, ri, rw, done, skew, ctx->g_tags, tlp)
+#define NMOE_PREP_M(XT, R, XLO, M)                                                                                      \
+    hipLaunchKernelGGL((nmoe_grouped_prep_kernel<BITS, XT, R, M>), gprep, dim3(256), 0, s, idx, ntok, k, nd,              \
+                       ctx->g_counts, ctx->g_perm, ctx->g_offsets, (uint4 *)ctx->g_rank, ctx->sync, ctx->spin_limit,    \
+                       (const XT *)x, ctx->g_xhi, XLO, ctx->g_xs, logits, ri, rw, done, skew, ctx->g_tags, tlp)
+    /* (one slice: the form without the slices' histogram exchange, and its registers) */
+#define NMOE_PREP(XT, R, XLO)                 \
+    do {                                      \
+        if (nd > 1)                           \
+            NMOE_PREP_M(XT, R, XLO, true);    \
+        else                                  \
+            NMOE_PREP_M(XT, R, XLO, false);   \
+    } while (0)
     if (logits != NULL) {
         if (bf)
             NMOE_PREP(uint16_t, true, (uint16_t *)NULL);
@@ -1930,6 +1950,7 @@ static int nmoe_grouped_run(nmoe_hip_ctx *ctx, const uint8_t *pack, const void *
             NMOE_PREP(float, false, ctx->g_xlo);
     }
 #undef NMOE_PREP
+#undef NMOE_PREP_M
     constexpr int NW = NMOE_GROUPED_NW;
     const dim3 blk(64 * NW);
     const dim3 ggu(lanes * NMOE_EXPERTS * (NMOE_INTER / nmoe_gu_rows(bf ? 1 : 2, NW))),

@@ -48,8 +48,7 @@ struct nmoe_layout<2> {
 #define NMOE_SYNC_STATUS 0     /* set to 1 by a kernel whose bounded wait expired */
 #define NMOE_SYNC_WORDS 8192   /* status + per-block launch epochs of the fused kernel */
 #define NMOE_SYNC_EPOCH(b) (64 + 16 * (b))     /* per-block launch epochs, 64 bytes apart */
-#define NMOE_SYNC_DISPATCH 4352                /* arrival counter of the dispatch blocks */
-#define NMOE_SYNC_PREP_EPOCH 4368              /* launches of the routed preparation so far (its tags' epoch - 1) */
+#define NMOE_SYNC_PREP_EPOCH 4368              /* preparation launches so far (the epoch of their tagged words - 1) */
 #define NMOE_SYNC_BLOCKS 256
 /* The fused launch's exchange words (tagged logits, act and partial y),
  * and with the whole-block form's shared activations and next-norm sums. */
@@ -126,7 +125,7 @@ struct nmoe_hip_ctx {
     int skew_tiles;         /* NMOE_HIP_OPT_SKEW_TILES: rank, or -1 */
     uint32_t *g_done;       /* [256] the one-launch form's gate/up tiles done per expert rank */
     uint64_t *g_tags;       /* [T*8] routed entries of the preparation launch: epoch << 32 | expert */
-    uint32_t *g_counts;     /* [64][257] per-block expert histograms */
+    uint64_t *g_counts;     /* [64][256] per-slice expert histograms, each word epoch << 32 | count */
     uint32_t *g_perm;       /* [T*8] entries grouped by expert */
     uint32_t *g_offsets;    /* [257] */
     uint32_t *g_rank;       /* [2][256][4] the expert order (expert, first entry, entries, entry), then the
