@@ -741,6 +741,35 @@ def test_grouped_on_uploaded_layer_and_reupload(big, nh, bits):
         big.set_grouped_min_tokens(8)
 
 
+def test_grouped_layer_changes_code_width(big, nh):
+    """A layer written as q4, then as q2, then as q4 again: each write of
+    another width allocates the pack and its stripe-major copy anew, and the
+    grouped path reads the copy of the width just written (every token
+    against the oracle)."""
+    rng = np.random.default_rng(830)
+    layer, ntok, k = 54, 20, 8
+    idx = np.zeros((ntok, 8), np.uint32)
+    for t in range(ntok):
+        idx[t, :k] = rng.choice(256, k, replace=False)
+    w = rng.dirichlet(np.ones(k), size=ntok).astype(np.float32)
+    x = rng.standard_normal((ntok, 2048)).astype(np.float32)
+    h = rng.standard_normal((ntok, 2048)).astype(np.float32)
+    d = [big.to_device(a) for a in (x, idx, w, h)]
+    try:
+        big.set_grouped_min_tokens(1)
+        for bits, seed in ((4, 41), (2, 42), (4, 43)):
+            big.synth_layer(layer, bits, seed, SIGMA[bits])
+            out = big.alloc(ntok * 2048 * 4)
+            big._check(big.experts(bits, layer, d[0], nh.F32, ntok, k, d[1], d[2], d[3], out))
+            assert big.device_status() == nh.OK
+            pack = host_pack(bits, seed, layer, idx[:, :k].ravel())
+            want = B.moe_experts(pack, bits, x, k, idx, w, h)
+            assert_close(out.download(np.float32, (ntok, 2048)), want, what=f"layer as q{bits} (seed {seed})")
+            del pack
+    finally:
+        big.set_grouped_min_tokens(8)
+
+
 @pytest.mark.parametrize("bits", [4, 2])
 def test_prefill_2048_sampled(big, nh, bits):
     """C5 shape: 2048 tokens, uniform-random logits -> device top-8 ->
