@@ -291,6 +291,7 @@ __device__ __forceinline__ void nmoe_dispatch_entries(const nmoe_entry_src &s, i
 struct nmoe_scatter_lds {
     uint32_t wc[NMOE_DISPATCH_PRE][4][NMOE_EXPERTS + 1];
     uint32_t bk[64];
+    uint32_t wbk[4][64]; /* each wavefront's experts of each work bucket */
 };
 
 /* D1: h = expert histogram of entry slice b of nd (in LDS). */
@@ -329,10 +330,11 @@ __device__ __forceinline__ uint32_t nmoe_down_entry(uint32_t es, uint32_t nbig, 
 /* Rank of this lane among the wavefront's lanes of the same key e
  * (9 bits: the experts and 256, left out), and their count (a multi-split
  * by ballots). */
+template <int NB = 9>
 __device__ __forceinline__ uint32_t nmoe_multisplit9(uint32_t e, int lane, uint32_t &cnt) {
     uint64_t peers = ~0ull;
 #pragma unroll
-    for (int bit = 0; bit < 9; bit++) {
+    for (int bit = 0; bit < NB; bit++) {
         const uint64_t m = __ballot((e >> bit) & 1u);
         peers &= ((e >> bit) & 1u) ? m : ~m;
     }
@@ -398,15 +400,23 @@ __device__ __forceinline__ void nmoe_dispatch_scatter(const nmoe_entry_src &src,
         if (b == 0 && tid == 0) nmoe_add_u32_dev(src.sync + NMOE_SYNC_PREP_EPOCH, 1u);
     }
     /* the experts by work, most first: bucket = 16-entry row blocks (63 and
-     * more together), a counting sort over the buckets, any order within
-     * one (the GEMM blocks' results do not depend on their order).  The
+     * more together), a counting sort over the buckets, the experts of one
+     * bucket in index order (any order would do: the GEMM blocks' results
+     * do not depend on it).  The
      * GEMM blocks take the experts in this order, so the longest tiles start
      * first and the launch's tail is short.  Entry es runs on die (es + c)
      * mod 8, so each round of eight is dealt back and forth (0..7, then
      * 7..0): dealt the same way every round, the same dies would take the
      * larger expert of every round and finish last. */
     const int bk = 63 - (int)min((total + 15u) / 16u, 63u);
-    if (b == 0) atomicAdd(&sl.bk[bk], 1u);
+    /* (block 0) the expert's place among its wavefront's experts of the same
+     * bucket (a 6-bit multi-split), and each wavefront's count of them */
+    uint32_t brk = 0u;
+    if (b == 0) {
+        uint32_t bcnt;
+        brk = nmoe_multisplit9<6>((uint32_t)bk, lane, bcnt);
+        if (brk == 0u) sl.wbk[wave][bk] = bcnt;
+    }
     /* exclusive scan of total over the 256 experts: an inclusive scan within
      * each wavefront (DPP), then the earlier wavefronts' totals */
     const uint32_t inc = nmoe_wave_incl_scan_u32(total);
@@ -421,7 +431,7 @@ __device__ __forceinline__ void nmoe_dispatch_scatter(const nmoe_entry_src &src,
         rk[j] = 0u;
         if (q0 + 256 * j < q1) { /* (block-uniform) a chunk with entries */
             uint32_t cnt;
-            rk[j] = nmoe_multisplit9(ev[j], lane, cnt);
+            rk[j] = nmoe_multisplit9<>(ev[j], lane, cnt);
             if (rk[j] == 0u) sl.wc[j][wave][ev[j]] = cnt;
         }
     }
@@ -445,7 +455,7 @@ __device__ __forceinline__ void nmoe_dispatch_scatter(const nmoe_entry_src &src,
         offsets[tid] = off;
         if (tid == 255) offsets[NMOE_EXPERTS] = off + total;
         if (tid < 64) { /* exclusive scan of the 64 bucket sizes (one wavefront) */
-            const uint32_t c = sl.bk[tid];
+            const uint32_t c = sl.wbk[0][tid] + sl.wbk[1][tid] + sl.wbk[2][tid] + sl.wbk[3][tid];
             const uint32_t binc = nmoe_wave_incl_scan_u32(c);
             sl.bk[tid] = binc - c;
             static_assert(NMOE_SMALL_PASS == 16, "bucket 62 holds the experts of one small pass");
@@ -466,7 +476,10 @@ __device__ __forceinline__ void nmoe_dispatch_scatter(const nmoe_entry_src &src,
     if (b == 0) {
         /* the order (its fourth word: the entry itself), and the same
          * entries in the down tiles' order after it */
-        const uint32_t pos = atomicAdd(&sl.bk[bk], 1u), round = pos >> 3;
+        uint32_t pos = sl.bk[bk] + brk; /* the bucket's first place, the earlier wavefronts', this one's */
+#pragma unroll
+        for (int w = 0; w < 3; w++) pos += w < wave ? sl.wbk[w][bk] : 0u;
+        const uint32_t round = pos >> 3;
         const uint32_t es = 8u * round + ((round & 1u) ? 7u - (pos & 7u) : (pos & 7u));
         const uint4 ent = make_uint4((uint32_t)tid, off, total, es);
         rank[es] = ent;
@@ -483,7 +496,7 @@ __device__ __forceinline__ void nmoe_dispatch_scatter(const nmoe_entry_src &src,
         const int q = c0 + tid;
         const uint32_t e = q < q1 ? nmoe_entry_expert<ROUTED>(src, q) : (uint32_t)NMOE_EXPERTS;
         uint32_t cnt;
-        const uint32_t r = nmoe_multisplit9(e, lane, cnt);
+        const uint32_t r = nmoe_multisplit9<>(e, lane, cnt);
         if (r == 0u) sl.wc[0][wave][e] = cnt;
         __syncthreads();
         if (q < q1 && e < (uint32_t)NMOE_EXPERTS) {
