@@ -1680,9 +1680,9 @@ __host__ __device__ constexpr int nmoe_ffn_lds(int bits, int xpl, int nw, int ns
     return ns * nmoe_imax(nmoe_gu_stage_max(bits, xpl, nw), nmoe_dn_stage_max(bits, nw, nmoe_ffn_dn_rows(nw))) +
            nmoe_imax(2 * nmoe_gu_rows(xpl, nw) * 64, nmoe_ffn_dn_rows(nw) * 16) + 4 * NMOE_MCHUNK * (1 + nw);
 }
-__host__ __device__ constexpr int nmoe_ffn_stages(int bits, int xpl, int nw) {
-    return nmoe_ffn_lds(bits, xpl, nw, 4) <= (nw == 8 ? 160 : 80) * 1024 - 512 ? 4 : 3;
-}
+/* Three stages: the down tiles' split prologue waits for them (four-wavefront
+ * blocks have no room for a fourth; eight-wavefront ones take three too). */
+__host__ __device__ constexpr int nmoe_ffn_stages(int, int, int) { return 3; }
 
 /* Gate/up and down of the grouped experts in one launch (one pass lane):
  * blocks 0 .. ngu-1 are the gate/up tiles (as nmoe_grouped_gateup_kernel's
