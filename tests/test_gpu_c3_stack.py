@@ -8,9 +8,15 @@ Checked, layer by layer on the GPU's own inputs (teacher-forced):
   - every token's routing at every layer bit-exact with the oracle
     (RMSNorm math.m:34-65, router, softmax/top-k/renormalise math.m:67-153):
     128 x 40 routings;
-  - the first and the last token's 40 layer outputs within max-abs 2e-3 /
-    rel-L2 1e-3 of the oracle's layer (orc_moe_layer_rmsnorm);
+  - every token's 41 hidden states, 40 routings and weights bit for bit
+    against the one-launch-per-layer form (the fused single-layer launch,
+    which the oracle pins on its own);
+  - every token's 40 layer outputs within
+    max-abs 2e-3 / rel-L2 1e-3 of the oracle's layer (orc_moe_layer_rmsnorm);
   - every hidden state finite and the device status clean."""
+import os
+from concurrent.futures import ThreadPoolExecutor
+
 import numpy as np
 import pytest
 
@@ -54,6 +60,20 @@ def test_stack_40_layers_128_tokens():
             IS.append(idx_s.download(np.uint32, (NL, 8)))
             WS.append(w_s.download(np.float32, (NL, 8)))
         assert ctx.device_status() == nh.OK
+        print("[c3] every token again, one launch per layer", flush=True)
+        try:
+            ctx._check(ctx.set_option(nh.OPT_STACK_LOOP, 0))
+            for t in range(NTOK):
+                hs.upload(H0[t])
+                ctx._check(ctx.moe_stack(list(range(NL)), routers, K, 1e-6, hs, idx_s, w_s))
+                np.testing.assert_array_equal(hs.download(np.float32, (NL + 1, 2048)).view(np.uint32),
+                                              HS[t].view(np.uint32), err_msg=f"token {t} hidden states")
+                np.testing.assert_array_equal(idx_s.download(np.uint32, (NL, 8)), IS[t], err_msg=f"token {t}")
+                np.testing.assert_array_equal(w_s.download(np.float32, (NL, 8)).view(np.uint32),
+                                              WS[t].view(np.uint32), err_msg=f"token {t} weights")
+        finally:
+            ctx._check(ctx.set_option(nh.OPT_STACK_LOOP, 1))
+        assert ctx.device_status() == nh.OK
     print("[c3] checking routing of every token at every layer", flush=True)
     x = np.zeros(2048, np.float32)
     o = B.oracle()
@@ -67,8 +87,8 @@ def test_stack_40_layers_128_tokens():
             np.testing.assert_array_equal(IS[t][l], oi, err_msg=f"token {t} layer {l}")
             np.testing.assert_array_equal(WS[t][l].view(np.uint32), ow.view(np.uint32), err_msg=f"token {t} layer {l}")
     esz = B.EXPERT_SIZE[4]
-    for t in (0, NTOK - 1):
-        print(f"[c3] token {t}: 40 layer outputs against the oracle", flush=True)
+
+    def check_token(t):  # the C calls release the interpreter lock
         for l in range(NL):
             pack = np.zeros(256 * esz, np.uint8)
             for e in IS[t][l]:
@@ -76,3 +96,8 @@ def test_stack_40_layers_128_tokens():
             want, oi, ow = _oracle_layer(pack, W[l], HS[t][l])
             np.testing.assert_array_equal(oi, IS[t][l])
             assert_close(HS[t][l + 1], want, what=f"token {t} layer {l}")
+
+    tokens = list(range(NTOK))
+    print(f"[c3] {len(tokens)} tokens: 40 layer outputs each against the oracle", flush=True)
+    with ThreadPoolExecutor(max_workers=min(8, os.cpu_count() or 1)) as ex:
+        list(ex.map(check_token, tokens))

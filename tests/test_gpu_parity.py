@@ -4,6 +4,8 @@ CPU oracle and the reference math.m golden vectors.
 Bars: routing indices, probabilities, dequantised weights and generator
 bytes bit-exact; floating-point outputs within max-abs 2e-3 and relative L2
 1e-3 (tests/conftest.py MAX_ABS / REL_L2)."""
+import os
+
 import numpy as np
 import pytest
 
@@ -26,6 +28,23 @@ def ctx(nh):
     c = nh.Context(0, max_tokens=64)
     yield c
     c.close()
+
+
+def oracle_experts_threaded(pack, bits, x, k, idx, w, h, chunk=64):
+    """The oracle's experts (B.moe_experts) over chunks of tokens on host
+    threads: the C call releases the interpreter lock and keeps its state on
+    its own stack and heap, once the first chunk, run alone, has built the
+    exp table that it fills at first use."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    def part(t0):
+        sl = slice(t0, t0 + chunk)
+        return B.moe_experts(pack, bits, x[sl], k, idx[sl], w[sl], h[sl])
+
+    first = part(0)
+    with ThreadPoolExecutor(max_workers=min(8, os.cpu_count() or 1)) as ex:
+        rest = list(ex.map(part, range(chunk, x.shape[0], chunk)))
+    return np.concatenate([first] + rest)
 
 
 def host_pack(bits, seed, layer, experts):
@@ -771,10 +790,11 @@ def test_grouped_layer_changes_code_width(big, nh):
 
 
 @pytest.mark.parametrize("bits", [4, 2])
-def test_prefill_2048_sampled(big, nh, bits):
+def test_prefill_2048_every_token(big, nh, bits):
     """C5 shape: 2048 tokens, uniform-random logits -> device top-8 ->
-    grouped experts; routing bit-exact for all 2048 tokens, outputs checked
-    against the oracle on a sample of 48 tokens."""
+    grouped experts; routing bit-exact for all 2048 tokens; the outputs of
+    all 2048 tokens against the oracle (on host threads) and against the
+    per-token kernels on the same routing."""
     rng = np.random.default_rng(2048 + bits)
     seed, layer, ntok, k = 33, 50 + bits, 2048, 8
     big.synth_layer(layer, bits, seed, SIGMA[bits])
@@ -792,16 +812,28 @@ def test_prefill_2048_sampled(big, nh, bits):
             out.download(np.float32, (ntok, 2048))
 
     idx, w, full = run_forms(big, run)
-    sample = rng.choice(ntok, 48, replace=False)
     for t in range(ntok):  # every token's routing
         oi, ow, _ = B.route(logits[t], k)
         np.testing.assert_array_equal(idx[t], oi, err_msg=f"t={t}")
         np.testing.assert_array_equal(w[t].view(np.uint32), ow.view(np.uint32), err_msg=f"t={t}")
-    got = full[sample]
-    pack = host_pack(bits, seed, layer, idx[sample, :k].ravel())
-    want = B.moe_experts(pack, bits, x[sample], k, idx[sample], w[sample], h[sample])
     assert big.device_status() == nh.OK
-    assert_close(got, want, what=f"prefill q{bits}")
+    print(f"[prefill] q{bits}: 2048 tokens through the oracle", flush=True)
+    pack = host_pack(bits, seed, layer, idx[:, :k].ravel())
+    want = oracle_experts_threaded(pack, bits, x, k, idx, w, h)
+    del pack
+    for t0 in range(0, ntok, 256):  # every token, in blocks that name the first failing one
+        assert_close(full[t0:t0 + 256], want[t0:t0 + 256], what=f"prefill q{bits} tokens {t0}..{t0 + 255}")
+    print(f"[prefill] q{bits}: 2048 tokens through the per-token kernels", flush=True)
+    d_idx, d_w, out = big.to_device(idx), big.to_device(w), big.alloc(ntok * 2048 * 4)
+    try:
+        big.set_grouped_min_tokens(ntok + 1)
+        big._check(big.experts(bits, layer, d_x, nh.BF16, ntok, k, d_idx, d_w, d_h, out))
+    finally:
+        big.set_grouped_min_tokens(8)
+    assert big.device_status() == nh.OK
+    per_token = out.download(np.float32, (ntok, 2048))
+    for t0 in range(0, ntok, 256):  # every token, in blocks that name the first failing one
+        assert_close(full[t0:t0 + 256], per_token[t0:t0 + 256], what=f"prefill q{bits} tokens {t0}..{t0 + 255}")
 
 
 @pytest.mark.parametrize("bits,ntok,k,xkind,lkind", [
