@@ -1775,15 +1775,17 @@ __global__ void __launch_bounds__(256) nmoe_grouped_combine_rows_kernel(const fl
     out[(size_t)t * NMOE_HIDDEN + r] = nmoe_status_set(status) ? __builtin_nanf("") : o;
 }
 
-__global__ void __launch_bounds__(256) nmoe_grouped_combine_kernel(const float *y, const uint32_t *idx,
-                                                                    const float *w, int k, const float *h_mid,
-                                                                    const float *shared_out,
-                                                                    const float *shared_gate_raw,
-                                                                    const uint32_t *status, float *out) {
-    /* four consecutive rows per thread; all k partial rows are loaded before
-     * the sum (an invalid slot's row was never written: its value is
-     * dropped by the select, never multiplied into the sum) */
-    const int t = blockIdx.y, r = 4 * (blockIdx.x * 256 + threadIdx.x);
+__global__ void __launch_bounds__(64) nmoe_grouped_combine_kernel(const float *y, const uint32_t *idx,
+                                                                   const float *w, int k, const float *h_mid,
+                                                                   const float *shared_out,
+                                                                   const float *shared_gate_raw,
+                                                                   const uint32_t *status, float *out) {
+    /* four consecutive rows per thread, one wavefront a block (eight blocks a
+     * token, so that 64 tokens already spread over every CU); all k partial
+     * rows are loaded before the sum (an invalid slot's row was never
+     * written: its value is dropped by the select, never multiplied into
+     * the sum) */
+    const int t = blockIdx.y, r = 4 * (blockIdx.x * 64 + threadIdx.x);
     float4 yv[NMOE_MAX_K];
 #pragma unroll
     for (int s = 0; s < NMOE_MAX_K; s++)
@@ -2003,7 +2005,7 @@ static int nmoe_grouped_run(nmoe_hip_ctx *ctx, const uint8_t *pack, const void *
     }
     const uint32_t *status = ctx->sync + NMOE_SYNC_STATUS;
     if (nmoe_aligned(h_mid, 16) && nmoe_aligned(out, 16) && (shared_out == NULL || nmoe_aligned(shared_out, 16)))
-        hipLaunchKernelGGL(nmoe_grouped_combine_kernel, dim3(NMOE_HIDDEN / 1024, ntok), dim3(256), 0, s,
+        hipLaunchKernelGGL(nmoe_grouped_combine_kernel, dim3(NMOE_HIDDEN / 256, ntok), dim3(64), 0, s,
                            (const float *)ctx->g_y, idx, w, k, h_mid, shared_out, shared_gate_raw, status, out);
     else
         hipLaunchKernelGGL(nmoe_grouped_combine_rows_kernel, dim3(NMOE_HIDDEN / 256, ntok), dim3(256), 0, s,
